@@ -1,0 +1,281 @@
+"""ctypes bindings of the MI355X decode engine (libchpe.so) and the archive writer
+(libchpe_pack.so), both built in this directory by its Makefile.
+
+The engine API mirrors the reference's C ABI (src/chpe_c_api.zig) plus the additions
+declared in include/chpe.h.  Nothing here computes on the CPU: a missing or unloadable
+libchpe.so raises, it is never replaced by a fallback.
+"""
+import ctypes
+import os
+from pathlib import Path
+
+import numpy as np
+
+PKG_DIR = Path(__file__).resolve().parent
+ENGINE_LIB = PKG_DIR / "libchpe.so"
+PACK_LIB = PKG_DIR / "libchpe_pack.so"
+
+ARCH_3B, ARCH_9B, ARCH_72B = 0, 1, 2
+# archive kinds of chpe_pack_write (include/chpe_pack.h)
+PACK_3B_FP16_RAW, PACK_3B_BF16_RAW, PACK_3B_W4, PACK_3B_W2, PACK_3B_W4_STD, PACK_72B_W4, PACK_72B_W2 = range(7)
+
+# every symbol include/chpe.h declares, in order
+ENGINE_SYMBOLS = [
+    "chpe_init", "chpe_forward_tokens", "chpe_get_last_logits", "chpe_get_vocab_size",
+    "chpe_get_hidden_dim", "chpe_get_num_layers", "chpe_get_last_elapsed_ns",
+    "chpe_get_last_argmax", "chpe_get_last_max_logit", "chpe_get_last_token0_logit",
+    "chpe_get_last_hidden_norm", "chpe_free", "chpe_init_ex", "chpe_decode_step",
+    "chpe_generate", "chpe_last_error", "chpe_get_max_seq_len", "chpe_get_hidden",
+    "chpe_time_steps", "chpe_time_stage", "chpe_stage_bytes", "chpe_step_bytes",
+    "chpe_debug_gemv", "chpe_debug_flat_tile_weights", "chpe_debug_embed_row_cell",
+]
+
+_c_float_p = ctypes.POINTER(ctypes.c_float)
+_c_u32_p = ctypes.POINTER(ctypes.c_uint32)
+_c_u8_p = ctypes.POINTER(ctypes.c_uint8)
+_engine_lib = None
+_pack_lib = None
+
+
+def _fp(a):
+    return a.ctypes.data_as(_c_float_p)
+
+
+def load_engine_lib():
+    """Load libchpe.so (raises OSError when it is not built)."""
+    global _engine_lib
+    if _engine_lib is None:
+        if not ENGINE_LIB.exists():
+            raise OSError(f"{ENGINE_LIB} is not built (run `make -C {PKG_DIR}`)")
+        lib = ctypes.CDLL(str(ENGINE_LIB))
+        V, S, I, U64, F, D = (ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int, ctypes.c_uint64,
+                              ctypes.c_float, ctypes.c_double)
+        sig = {
+            "chpe_init": (V, [ctypes.c_char_p]),
+            "chpe_forward_tokens": (I, [V, _c_u32_p, S, _c_float_p]),
+            "chpe_get_last_logits": (S, [V, _c_float_p, S]),
+            "chpe_get_vocab_size": (S, [V]),
+            "chpe_get_hidden_dim": (S, [V]),
+            "chpe_get_num_layers": (S, [V]),
+            "chpe_get_last_elapsed_ns": (U64, [V]),
+            "chpe_get_last_argmax": (ctypes.c_uint32, [V]),
+            "chpe_get_last_max_logit": (F, [V]),
+            "chpe_get_last_token0_logit": (F, [V]),
+            "chpe_get_last_hidden_norm": (F, [V]),
+            "chpe_free": (None, [V]),
+            "chpe_init_ex": (V, [ctypes.c_char_p, I, S, I]),
+            "chpe_decode_step": (I, [V, ctypes.c_uint32, S, _c_float_p]),
+            "chpe_generate": (I, [V, _c_u32_p, S, S, _c_u32_p]),
+            "chpe_last_error": (ctypes.c_char_p, []),
+            "chpe_get_max_seq_len": (S, [V]),
+            "chpe_get_hidden": (I, [V, _c_float_p]),
+            "chpe_time_steps": (I, [V, S, _c_float_p]),
+            "chpe_time_stage": (I, [V, I, S, S, S, _c_float_p]),
+            "chpe_stage_bytes": (D, [V, I, S]),
+            "chpe_step_bytes": (D, [V, S]),
+            "chpe_debug_gemv": (I, [V, S, I, _c_float_p, _c_float_p]),
+            "chpe_debug_flat_tile_weights": (I, [_c_u8_p, _c_float_p]),
+            "chpe_debug_embed_row_cell": (I, [_c_u8_p, S, ctypes.c_uint32, ctypes.c_uint32, _c_float_p]),
+        }
+        for name, (res, args) in sig.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        _engine_lib = lib
+    return _engine_lib
+
+
+def load_pack_lib():
+    global _pack_lib
+    if _pack_lib is None:
+        if not PACK_LIB.exists():
+            raise OSError(f"{PACK_LIB} is not built (run `make -C {PKG_DIR}`)")
+        lib = ctypes.CDLL(str(PACK_LIB))
+        lib.chpe_pack_size.restype = ctypes.c_uint64
+        lib.chpe_pack_size.argtypes = [ctypes.c_int]
+        lib.chpe_pack_write.restype = ctypes.c_int
+        lib.chpe_pack_write.argtypes = [ctypes.c_char_p, ctypes.c_int, ctypes.c_uint64, ctypes.c_int]
+        lib.chpe_pack_normals.restype = None
+        lib.chpe_pack_normals.argtypes = [ctypes.c_uint64, ctypes.c_uint64, ctypes.c_uint64,
+                                          ctypes.c_uint64, ctypes.c_float, _c_float_p]
+        lib.chpe_pack_cell16.restype = ctypes.c_int
+        lib.chpe_pack_cell16.argtypes = [_c_float_p, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                         ctypes.c_int, ctypes.c_uint32, _c_u8_p]
+        lib.chpe_pack_flat.restype = ctypes.c_int
+        lib.chpe_pack_flat.argtypes = [_c_float_p, ctypes.c_int, ctypes.c_int, ctypes.c_uint32, _c_u8_p]
+        _pack_lib = lib
+    return _pack_lib
+
+
+# ------------------------------------------------------------------ archive writer
+def archive_size(kind):
+    return int(load_pack_lib().chpe_pack_size(kind))
+
+
+def write_archive(path, kind, seed=0, threads=0):
+    rc = load_pack_lib().chpe_pack_write(str(path).encode(), kind, seed, threads)
+    if rc != 0:
+        raise RuntimeError(f"chpe_pack_write({path}, kind={kind}) failed: {rc}")
+    return path
+
+
+def normals(seed, tid, first, n, std=0.02):
+    out = np.empty(n, dtype=np.float32)
+    load_pack_lib().chpe_pack_normals(seed, tid, first, n, std, _fp(out))
+    return out
+
+
+def pack_cell16(w, bits=4, n_outlier_cols=8, layer=0):
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    cell = np.zeros(17408, dtype=np.uint8)
+    rc = load_pack_lib().chpe_pack_cell16(_fp(w), w.shape[0], w.shape[1], bits, n_outlier_cols,
+                                          layer, cell.ctypes.data_as(_c_u8_p))
+    if rc:
+        raise ValueError("chpe_pack_cell16 rejected the shape")
+    return cell
+
+
+def pack_flat(w, bits=4, n_outliers=64, layer=0):
+    w = np.ascontiguousarray(w, dtype=np.float32).reshape(32768)
+    cell = np.zeros(17408, dtype=np.uint8)
+    rc = load_pack_lib().chpe_pack_flat(_fp(w), bits, n_outliers, layer, cell.ctypes.data_as(_c_u8_p))
+    if rc:
+        raise ValueError("chpe_pack_flat rejected the arguments")
+    return cell
+
+
+# ------------------------------------------------------------------ engine
+class EngineError(RuntimeError):
+    pass
+
+
+class Engine:
+    """One engine context (chpe_init / chpe_init_ex)."""
+
+    def __init__(self, path, arch=-1, max_seq_len=2048, kv_f16=False, reference_init=False):
+        self.lib = load_engine_lib()
+        if reference_init:
+            self.ctx = self.lib.chpe_init(str(path).encode())
+        else:
+            self.ctx = self.lib.chpe_init_ex(str(path).encode(), arch, max_seq_len, 1 if kv_f16 else 0)
+        if not self.ctx:
+            raise EngineError(self.lib.chpe_last_error().decode())
+        self.vocab = self.lib.chpe_get_vocab_size(self.ctx)
+        self.hidden_dim = self.lib.chpe_get_hidden_dim(self.ctx)
+        self.num_layers = self.lib.chpe_get_num_layers(self.ctx)
+        self.max_seq_len = self.lib.chpe_get_max_seq_len(self.ctx)
+
+    def close(self):
+        if self.ctx:
+            self.lib.chpe_free(self.ctx)
+            self.ctx = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def _check(self, rc, what):
+        if rc < 0:
+            raise EngineError(f"{what} failed: {rc}")
+        return rc
+
+    def forward_tokens(self, tokens, want_logits=False):
+        toks = np.ascontiguousarray(tokens, dtype=np.uint32)
+        logits = np.empty(self.vocab, dtype=np.float32) if want_logits else None
+        rc = self.lib.chpe_forward_tokens(self.ctx, toks.ctypes.data_as(_c_u32_p), toks.size,
+                                          _fp(logits) if want_logits else None)
+        self._check(rc, "chpe_forward_tokens")
+        return (rc, logits) if want_logits else rc
+
+    def decode_step(self, token, pos, want_logits=True):
+        logits = np.empty(self.vocab, dtype=np.float32) if want_logits else None
+        rc = self.lib.chpe_decode_step(self.ctx, token, pos, _fp(logits) if want_logits else None)
+        self._check(rc, "chpe_decode_step")
+        return (rc, logits) if want_logits else rc
+
+    def generate(self, prompt, n_gen):
+        p = np.ascontiguousarray(prompt, dtype=np.uint32)
+        out = np.empty(n_gen, dtype=np.uint32)
+        rc = self.lib.chpe_generate(self.ctx, p.ctypes.data_as(_c_u32_p), p.size, n_gen,
+                                    out.ctypes.data_as(_c_u32_p))
+        self._check(rc, "chpe_generate")
+        return out
+
+    def logits(self):
+        out = np.empty(self.vocab, dtype=np.float32)
+        if self.lib.chpe_get_last_logits(self.ctx, _fp(out), self.vocab) != self.vocab:
+            raise EngineError("chpe_get_last_logits failed")
+        return out
+
+    def hidden(self):
+        out = np.empty(self.hidden_dim, dtype=np.float32)
+        self._check(self.lib.chpe_get_hidden(self.ctx, _fp(out)), "chpe_get_hidden")
+        return out
+
+    def last(self):
+        L = self.lib
+        return dict(argmax=L.chpe_get_last_argmax(self.ctx), max_logit=L.chpe_get_last_max_logit(self.ctx),
+                    token0_logit=L.chpe_get_last_token0_logit(self.ctx),
+                    hidden_norm=L.chpe_get_last_hidden_norm(self.ctx),
+                    elapsed_ns=L.chpe_get_last_elapsed_ns(self.ctx))
+
+    def debug_gemv(self, layer, which, x, rows):
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        y = np.empty(rows, dtype=np.float32)
+        self._check(self.lib.chpe_debug_gemv(self.ctx, layer, which, _fp(x), _fp(y)), "chpe_debug_gemv")
+        return y
+
+    def time_steps(self, n):
+        ms = ctypes.c_float()
+        self._check(self.lib.chpe_time_steps(self.ctx, n, ctypes.byref(ms)), "chpe_time_steps")
+        return ms.value
+
+    def time_stage(self, stage, layer0, layer1, iters):
+        ms = ctypes.c_float()
+        self._check(self.lib.chpe_time_stage(self.ctx, stage, layer0, layer1, iters, ctypes.byref(ms)),
+                    "chpe_time_stage")
+        return ms.value
+
+    def stage_bytes(self, stage, layer):
+        return self.lib.chpe_stage_bytes(self.ctx, stage, layer)
+
+    def step_bytes(self, pos):
+        return self.lib.chpe_step_bytes(self.ctx, pos)
+
+
+def gpu_flat_tile_weights(cell):
+    cell = np.ascontiguousarray(cell, dtype=np.uint8)
+    out = np.empty(32768, dtype=np.float32)
+    rc = load_engine_lib().chpe_debug_flat_tile_weights(cell.ctypes.data_as(_c_u8_p), _fp(out))
+    if rc:
+        raise EngineError(f"chpe_debug_flat_tile_weights failed: {rc}")
+    return out
+
+
+def gpu_embed_row_cell(region, row, D, init=None):
+    region = np.ascontiguousarray(region, dtype=np.uint8)
+    out = np.array(init, dtype=np.float32) if init is not None else np.zeros(D, dtype=np.float32)
+    rc = load_engine_lib().chpe_debug_embed_row_cell(region.ctypes.data_as(_c_u8_p), region.size, row, D, _fp(out))
+    if rc < 0:
+        raise EngineError(f"chpe_debug_embed_row_cell failed: {rc}")
+    return rc, out
+
+
+def build(jobs=8):
+    """Compile libchpe.so, libchpe_pack.so and the CLIs in place (make)."""
+    import subprocess
+    subprocess.run(["make", "-C", str(PKG_DIR), f"-j{jobs}"], check=True)
+
+
+def default_archive_dir():
+    d = Path(os.environ.get("CHPE_ARCHIVE_DIR", "/tmp/chpe_archives"))
+    d.mkdir(parents=True, exist_ok=True)
+    return d

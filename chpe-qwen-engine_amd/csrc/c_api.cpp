@@ -1,0 +1,259 @@
+// c_api.cpp -- the chpe_* C ABI (libchpe.so).
+//
+// The reference's twelve symbols (src/chpe_c_api.zig:25-143) keep their signatures and
+// sentinel semantics; the context owns the engine (device memory) and nothing else: the
+// archive is mapped and validated (WeightArchive.openPosix + validate,
+// src/weight_archive.zig:152-222), copied to HBM, and unmapped again.
+#include <fcntl.h>
+#include <sys/mman.h>
+#include <sys/stat.h>
+#include <unistd.h>
+
+#include <cstring>
+#include <memory>
+#include <string>
+
+#include "../../include/chpe.h"
+#include "engine.hpp"
+#include "format.hpp"
+
+using namespace chpe;
+
+namespace {
+
+thread_local std::string g_last_error;
+
+struct Context {
+  std::unique_ptr<Engine> engine;
+  ModelArch arch{};
+  uint32_t last_argmax = 0;
+  float last_max_logit = 0.0f, last_token0_logit = 0.0f, last_hidden_norm = 0.0f;
+  uint64_t last_elapsed_ns = 0;
+  hipEvent_t ev0 = nullptr, ev1 = nullptr;
+};
+
+// WeightArchive.validate: src/weight_archive.zig:152-172
+const char* validate(const uint8_t* b, size_t len) {
+  if (len < kHeaderBytes) return "FileTooSmall";
+  ArchiveHeader h;
+  std::memcpy(&h, b, sizeof h);
+  if (h.magic != kArchiveMagic && h.magic != kChpeMagic) return "InvalidMagic";
+  if (h.version != kArchiveVersion) return "UnsupportedVersion";
+  if (h.header_bytes != kHeaderBytes) return "MisalignedHeader";
+  const bool standard = h.record_bytes == kRecordBytes && h.prefetch_bytes == kPrefetchBytes;
+  const bool dense = h.record_bytes == kCellBytes && h.prefetch_bytes == 0;
+  const bool raw = h.record_bytes == kTileCodeBytes && h.prefetch_bytes == 0;
+  if (!standard && !dense && !raw) return "BadGeometry";
+  if (!raw && h.cell_bytes != kCellBytes) return "BadGeometry";
+  if (raw && h.cell_bytes != kTileCodeBytes) return "BadGeometry";
+  if (h.header_bytes + h.record_count * h.record_bytes > len) return "Truncated";
+  return nullptr;
+}
+
+Context* open_ctx(const char* path, int arch, size_t max_seq_len, bool kv_f16) {
+  g_last_error.clear();
+  if (!path) { g_last_error = "null path"; return nullptr; }
+  const int fd = ::open(path, O_RDONLY);
+  if (fd < 0) { g_last_error = std::string("cannot open ") + path; return nullptr; }
+  struct stat st;
+  if (::fstat(fd, &st) != 0 || size_t(st.st_size) < kHeaderBytes) {
+    ::close(fd);
+    g_last_error = "FileTooSmall";
+    return nullptr;
+  }
+  const size_t len = size_t(st.st_size);
+  void* m = ::mmap(nullptr, len, PROT_READ, MAP_PRIVATE, fd, 0);
+  ::close(fd);
+  if (m == MAP_FAILED) { g_last_error = "mmap failed"; return nullptr; }
+  ::madvise(m, len, MADV_SEQUENTIAL);
+  ::madvise(m, len, MADV_WILLNEED);
+  const uint8_t* bytes = static_cast<const uint8_t*>(m);
+  if (const char* v = validate(bytes, len)) {
+    ::munmap(m, len);
+    g_last_error = v;
+    return nullptr;
+  }
+  EngineConfig cfg;
+  cfg.arch_id = arch < 0 ? arch_from_path(path) : arch;
+  cfg.max_seq_len = max_seq_len;
+  cfg.kv_f16 = kv_f16;
+  std::string err;
+  auto engine = Engine::create(bytes, len, cfg, &err);
+  ::munmap(m, len);
+  if (!engine) { g_last_error = err; return nullptr; }
+  auto* ctx = new Context();
+  ctx->arch = engine->arch();
+  ctx->engine = std::move(engine);
+  (void)hipEventCreate(&ctx->ev0);
+  (void)hipEventCreate(&ctx->ev1);
+  return ctx;
+}
+
+void remember(Context* c, const ForwardResult& r) {
+  c->last_argmax = r.argmax_token;
+  c->last_max_logit = r.max_logit;
+  c->last_token0_logit = r.token0_logit;
+  c->last_hidden_norm = r.hidden_norm;
+  c->last_elapsed_ns = r.elapsed_ns;
+}
+
+Context* C(void* p) { return static_cast<Context*>(p); }
+
+}  // namespace
+
+extern "C" {
+
+void* chpe_init(const char* archive_path) { return open_ctx(archive_path, -1, 2048, false); }
+
+void* chpe_init_ex(const char* archive_path, int arch, size_t max_seq_len, int kv_f16) {
+  if (arch > 2) { g_last_error = "unknown architecture"; return nullptr; }
+  return open_ctx(archive_path, arch, max_seq_len, kv_f16 != 0);
+}
+
+const char* chpe_last_error(void) { return g_last_error.c_str(); }
+
+int chpe_forward_tokens(void* ctx, const uint32_t* tokens, size_t n, float* out_logits) {
+  if (!ctx || !tokens || n == 0) return -1;
+  Context* c = C(ctx);
+  ForwardResult r{};
+  const int rc = c->engine->forward_tokens(tokens, n, &r);
+  if (rc) return rc;
+  remember(c, r);
+  if (out_logits && c->engine->copy_logits(out_logits)) return -3;
+  return int(r.argmax_token);
+}
+
+int chpe_decode_step(void* ctx, uint32_t token, size_t pos, float* out_logits) {
+  if (!ctx) return -1;
+  Context* c = C(ctx);
+  ForwardResult r{};
+  const int rc = c->engine->forward(token, pos, &r);
+  if (rc) return rc;
+  remember(c, r);
+  if (out_logits && c->engine->copy_logits(out_logits)) return -3;
+  return int(r.argmax_token);
+}
+
+int chpe_generate(void* ctx, const uint32_t* prompt, size_t n_prompt, size_t n_gen, uint32_t* out_tokens) {
+  if (!ctx || !prompt || n_prompt == 0 || n_gen == 0 || !out_tokens) return -1;
+  Context* c = C(ctx);
+  ForwardResult r{};
+  const int rc = c->engine->generate(prompt, n_prompt, n_gen, out_tokens, &r);
+  if (rc) return rc;
+  remember(c, r);
+  return 0;
+}
+
+size_t chpe_get_last_logits(void* ctx, float* out, size_t max_len) {
+  if (!ctx || !out) return 0;
+  Context* c = C(ctx);
+  const size_t V = c->arch.vocab_size;
+  if (max_len < V) return 0;
+  return c->engine->copy_logits(out) == 0 ? V : 0;
+}
+
+size_t chpe_get_vocab_size(void* ctx) { return ctx ? C(ctx)->arch.vocab_size : 151936; }
+size_t chpe_get_hidden_dim(void* ctx) { return ctx ? C(ctx)->arch.hidden_dim : 2048; }
+size_t chpe_get_num_layers(void* ctx) { return ctx ? C(ctx)->arch.num_layers : 36; }
+uint64_t chpe_get_last_elapsed_ns(void* ctx) { return ctx ? C(ctx)->last_elapsed_ns : 0; }
+uint32_t chpe_get_last_argmax(void* ctx) { return ctx ? C(ctx)->last_argmax : 0; }
+float chpe_get_last_max_logit(void* ctx) { return ctx ? C(ctx)->last_max_logit : 0.0f; }
+float chpe_get_last_token0_logit(void* ctx) { return ctx ? C(ctx)->last_token0_logit : 0.0f; }
+float chpe_get_last_hidden_norm(void* ctx) { return ctx ? C(ctx)->last_hidden_norm : 0.0f; }
+size_t chpe_get_max_seq_len(void* ctx) { return ctx ? C(ctx)->engine->max_seq_len() : 0; }
+
+int chpe_get_hidden(void* ctx, float* out) {
+  if (!ctx || !out) return -1;
+  return C(ctx)->engine->copy_hidden(out);
+}
+
+void chpe_free(void* ctx) {
+  if (!ctx) return;
+  Context* c = C(ctx);
+  c->engine.reset();
+  if (c->ev0) (void)hipEventDestroy(c->ev0);
+  if (c->ev1) (void)hipEventDestroy(c->ev1);
+  delete c;
+}
+
+int chpe_time_steps(void* ctx, size_t n, float* ms) {
+  if (!ctx || !ms) return -1;
+  Context* c = C(ctx);
+  Engine& e = *c->engine;
+  if (hipEventRecord(c->ev0, e.stream()) != hipSuccess) return -3;
+  e.launch_steps(n);
+  if (hipEventRecord(c->ev1, e.stream()) != hipSuccess) return -3;
+  if (hipEventSynchronize(c->ev1) != hipSuccess) return -3;
+  if (hipEventElapsedTime(ms, c->ev0, c->ev1) != hipSuccess) return -3;
+  ForwardResult r{};
+  if (e.read_result(&r) == 0) remember(c, r);
+  return 0;
+}
+
+int chpe_time_stage(void* ctx, int stage, size_t layer0, size_t layer1, size_t iters, float* ms) {
+  if (!ctx || !ms || stage < 0 || stage > 4) return -1;
+  Context* c = C(ctx);
+  Engine& e = *c->engine;
+  if (layer1 > e.arch().num_layers || layer0 >= layer1) return -1;
+  if (hipEventRecord(c->ev0, e.stream()) != hipSuccess) return -3;
+  for (size_t it = 0; it < iters; ++it)
+    for (size_t l = layer0; l < layer1; ++l)
+      if (e.launch_stage(stage, l)) return -1;
+  if (hipEventRecord(c->ev1, e.stream()) != hipSuccess) return -3;
+  if (hipEventSynchronize(c->ev1) != hipSuccess) return -3;
+  return hipEventElapsedTime(ms, c->ev0, c->ev1) == hipSuccess ? 0 : -3;
+}
+
+double chpe_stage_bytes(void* ctx, int stage, size_t layer) {
+  if (!ctx || layer >= C(ctx)->arch.num_layers) return 0.0;
+  return C(ctx)->engine->stage_bytes(stage, layer);
+}
+
+double chpe_step_bytes(void* ctx, size_t pos) { return ctx ? C(ctx)->engine->step_bytes(pos) : 0.0; }
+
+int chpe_debug_gemv(void* ctx, size_t layer, int which, const float* x, float* y) {
+  if (!ctx || !x || !y) return -1;
+  return C(ctx)->engine->debug_gemv(layer, which, x, y);
+}
+
+int chpe_debug_flat_tile_weights(const uint8_t* cell, float* out) {
+  if (!cell || !out) return -1;
+  uint8_t* dc = nullptr;
+  float* dout = nullptr;
+  int rc = -3;
+  if (hipMalloc(&dc, kCellBytes) == hipSuccess && hipMalloc(&dout, kFlatWeights * 4) == hipSuccess &&
+      hipMemcpy(dc, cell, kCellBytes, hipMemcpyHostToDevice) == hipSuccess) {
+    launch_flat_tile_weights(dc, dout, nullptr);
+    if (hipDeviceSynchronize() == hipSuccess &&
+        hipMemcpy(out, dout, kFlatWeights * 4, hipMemcpyDeviceToHost) == hipSuccess)
+      rc = 0;
+  }
+  if (dc) (void)hipFree(dc);
+  if (dout) (void)hipFree(dout);
+  return rc;
+}
+
+int chpe_debug_embed_row_cell(const uint8_t* bytes, size_t len, uint32_t row, uint32_t D, float* out) {
+  if (!bytes || !out || len < kCellBytes || D == 0 || D % 128) return -1;
+  uint8_t* db = nullptr;
+  float* dout = nullptr;
+  int* dw = nullptr;
+  int written = -3;
+  if (hipMalloc(&db, len) == hipSuccess && hipMalloc(&dout, D * 4) == hipSuccess &&
+      hipMalloc(&dw, sizeof(int)) == hipSuccess &&
+      hipMemcpy(db, bytes, len, hipMemcpyHostToDevice) == hipSuccess &&
+      hipMemcpy(dout, out, D * 4, hipMemcpyHostToDevice) == hipSuccess) {
+    launch_embed_row_cell(db, len, row, D, dout, dw, nullptr);
+    int w = 0;
+    if (hipDeviceSynchronize() == hipSuccess &&
+        hipMemcpy(out, dout, D * 4, hipMemcpyDeviceToHost) == hipSuccess &&
+        hipMemcpy(&w, dw, sizeof(int), hipMemcpyDeviceToHost) == hipSuccess)
+      written = w;
+  }
+  if (db) (void)hipFree(db);
+  if (dout) (void)hipFree(dout);
+  if (dw) (void)hipFree(dw);
+  return written;
+}
+
+}  // extern "C"

@@ -1,0 +1,733 @@
+// engine.cpp -- host side of the MI355X decode engine.
+//
+// init() follows CHPEEngine.init (src/chpe_engine.zig:854-974) for format detection, then
+// builds a plan per projection that reproduces gemvLinear's tile walk
+// (src/chpe_engine.zig:1396-1489) on the GPU, extracts norm gains / biases with the
+// reference's fallback rules (:1144-1192), uploads the archive image and captures the whole
+// forwardDecode step (:1663-1803) as one hipGraph.
+#include "engine.hpp"
+
+#include <algorithm>
+#include <chrono>
+#include <cmath>
+#include <cstring>
+#include <map>
+
+#include "format.hpp"
+
+namespace chpe {
+
+namespace {
+
+constexpr size_t kImageShift = 64;       // puts every cell's code area on a 128-byte boundary
+constexpr size_t kImagePad = 1u << 20;   // zero bytes after the archive (bounded over-reads)
+
+uint64_t now_ns() {
+  return uint64_t(std::chrono::duration_cast<std::chrono::nanoseconds>(
+                      std::chrono::steady_clock::now().time_since_epoch())
+                      .count());
+}
+
+template <typename T>
+T rd(const uint8_t* bytes, size_t len, size_t off) {  // little-endian read, zero past the end
+  uint8_t buf[sizeof(T)] = {0};
+  for (size_t i = 0; i < sizeof(T); ++i)
+    if (off + i < len) buf[i] = bytes[off + i];
+  T v;
+  std::memcpy(&v, buf, sizeof(T));
+  return v;
+}
+
+#define HIP_TRY(expr)                                                               \
+  do {                                                                              \
+    hipError_t e_ = (expr);                                                         \
+    if (e_ != hipSuccess) {                                                         \
+      if (err) *err = std::string(#expr) + ": " + hipGetErrorString(e_);            \
+      return false;                                                                 \
+    }                                                                               \
+  } while (0)
+
+}  // namespace
+
+bool arch_preset(int id, ModelArch* a) {
+  switch (id) {
+    case 0: *a = {0, "Qwen2.5-3B", 2048, 11008, 36, 16, 2, 128, 151936, 1000000.0f, 1e-6f}; return true;
+    case 1: *a = {1, "Qwen3.5-9B", 4096, 12288, 32, 16, 4, 256, 248320, 1000000.0f, 1e-6f}; return true;
+    case 2: *a = {2, "Qwen2.5-72B", 8192, 29568, 80, 64, 8, 128, 152064, 1000000.0f, 1e-6f}; return true;
+  }
+  return false;
+}
+
+int arch_from_path(const char* p) {
+  if (std::strstr(p, "9B") || std::strstr(p, "9b") || std::strstr(p, "qwen35")) return 1;
+  if (std::strstr(p, "72B") || std::strstr(p, "72b")) return 2;
+  return 0;
+}
+
+std::unique_ptr<Engine> Engine::create(const uint8_t* bytes, size_t len, const EngineConfig& cfg,
+                                       std::string* err) {
+  std::unique_ptr<Engine> e(new Engine());
+  if (!e->init(bytes, len, cfg, err)) return nullptr;
+  return e;
+}
+
+Engine::~Engine() {
+  if (stream_) (void)hipStreamSynchronize(stream_);
+  if (graph_exec_) (void)hipGraphExecDestroy(graph_exec_);
+  if (graph_) (void)hipGraphDestroy(graph_);
+  for (void* p : allocs_) (void)hipFree(p);
+  if (h_state_) (void)hipHostFree(h_state_);
+  if (h_result_) (void)hipHostFree(h_result_);
+  if (stream_) (void)hipStreamDestroy(stream_);
+}
+
+void* Engine::dev_alloc(size_t bytes) {
+  void* p = nullptr;
+  if (hipMalloc(&p, std::max<size_t>(bytes, 256)) != hipSuccess) return nullptr;
+  allocs_.push_back(p);
+  return p;
+}
+
+float* Engine::upload_vector(const std::vector<float>& v) {
+  float* d = static_cast<float*>(dev_alloc(v.size() * sizeof(float)));
+  if (d) (void)hipMemcpy(d, v.data(), v.size() * sizeof(float), hipMemcpyHostToDevice);
+  return d;
+}
+
+bool Engine::init(const uint8_t* b, size_t len, const EngineConfig& cfg, std::string* err) {
+  cfg_ = cfg;
+  host_bytes_ = b;
+  len_ = len;
+  if (!arch_preset(cfg.arch_id, &arch_)) { *err = "unknown architecture"; return false; }
+  // ---- format detection: CHPEEngine.init, src/chpe_engine.zig:869-918
+  if (len >= 4096) {
+    const uint32_t magic = rd<uint32_t>(b, len, 0);
+    if (magic == kChpeMagic || magic == kArchiveMagic) {
+      archive_valid_ = true;
+      record_count_ = size_t(rd<uint64_t>(b, len, 16));
+      const uint64_t rec_b = rd<uint64_t>(b, len, 32), cell_b = rd<uint64_t>(b, len, 40),
+                     pre_b = rd<uint64_t>(b, len, 48), flags = rd<uint64_t>(b, len, 56);
+      is_dense_ = pre_b == 0 && rec_b == cell_b && rec_b == kCellBytes;
+      is_raw_ = rec_b == kTileCodeBytes;
+      is_raw_fp16_ = is_raw_ && (flags & kFlagRawFp16);
+      if (is_raw_fp16_) {
+        quant_bits_ = 16;
+      } else if (is_raw_) {
+        const size_t gib = size_t(1) << 30;
+        quant_bits_ = (arch_.id == 1 && ((flags & kFlagInt8Hint) || (len < 10 * gib && len > 7 * gib))) ? 8 : 16;
+      } else if (record_count_ > 0 && len >= 4096 + (is_dense_ ? kCellBytes : kRecordBytes)) {
+        quant_bits_ = b[4096 + (is_dense_ ? 0 : kPrefetchBytes) + kPayloadOff + kMetaQuantBits];
+        if (quant_bits_ == 0) quant_bits_ = 2;
+      }
+    }
+  }
+  stride_ = is_raw_ ? kTileCodeBytes : (is_dense_ ? kCellBytes : kRecordBytes);
+  wpt_ = (is_raw_ && quant_bits_ == 16) ? 8192 : (quant_bits_ == 8 ? 16384 : (quant_bits_ == 4 || quant_bits_ == 2 ? 32768 : 8192));
+  map_ = arch_.hidden_dim == 2048 ? (is_raw_ ? MapKind::Qwen3bRaw : MapKind::Qwen3bCell)
+                                  : (arch_.hidden_dim == 8192 ? MapKind::Qwen72b : MapKind::Qwen35_9b);
+  if (!archive_valid_ || record_count_ == 0) {
+    *err = "archive header is not a valid .chpe header (the synthetic-weight fallback of the "
+           "reference engine is not built on the GPU path)";
+    return false;
+  }
+  if (cfg.max_seq_len == 0 || cfg.max_seq_len > (1u << 20)) { *err = "bad max_seq_len"; return false; }
+  const uint32_t chunk = attn_chunk(uint32_t(arch_.head_dim));
+  n_chunks_ = uint32_t((cfg.max_seq_len + chunk - 1) / chunk);
+  if (n_chunks_ > kAttnMaxChunks) {
+    *err = "max_seq_len exceeds the attention kernel's chunk table (" +
+           std::to_string(size_t(kAttnMaxChunks) * chunk) + " positions)";
+    return false;
+  }
+
+  HIP_TRY(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking));
+  // ---- archive image: verbatim, shifted so that code areas are 128-byte aligned
+  const size_t shift = is_raw_ ? 0 : kImageShift;
+  uint8_t* img = static_cast<uint8_t*>(dev_alloc(shift + len + kImagePad));
+  if (!img) { *err = "hipMalloc of the archive image failed"; return false; }
+  d_image_ = img + shift;
+  image_len_ = len + kImagePad;
+  HIP_TRY(hipMemset(img, 0, shift));
+  HIP_TRY(hipMemset(d_image_ + len, 0, kImagePad));
+  const size_t chunk_bytes = size_t(256) << 20;
+  for (size_t off = 0; off < len; off += chunk_bytes)
+    HIP_TRY(hipMemcpy(d_image_ + off, b + off, std::min(chunk_bytes, len - off), hipMemcpyHostToDevice));
+
+  // ---- embedding kind (unpackEmbedRow branches)
+  embed_kind_ = is_raw_fp16_ ? 1 : (is_raw_ ? (quant_bits_ == 8 ? 3 : 2) : 4);
+
+  // ---- per-layer plans
+  const size_t D = arch_.hidden_dim, I = arch_.intermediate_dim,
+               qd = arch_.num_attn_heads * arch_.head_dim, kvd = arch_.num_kv_heads * arch_.head_dim;
+  auto norm = [&](size_t tile) {  // unpackNorm: src/chpe_engine.zig:1144-1170
+    std::vector<float> g(D, 1.0f);
+    if (tile >= record_count_) return g;
+    const size_t off = is_raw_ ? 4096 + tile * kTileCodeBytes
+                               : 4096 + tile * stride_ + (is_dense_ ? 0 : kPrefetchBytes) + kBytecodeHeader;
+    const bool bf = arch_.hidden_dim == 4096 && is_raw_;
+    bool all_zero = true;
+    for (size_t i = 0; i < D; ++i) {
+      g[i] = bf ? bf16_to_f32(rd<uint16_t>(b, len, off + 2 * i)) : rd<float>(b, len, off + 4 * i);
+      if (!std::isfinite(g[i])) { std::fill(g.begin(), g.end(), 1.0f); return g; }
+      if (g[i] != 0.0f) all_zero = false;
+    }
+    if (all_zero) std::fill(g.begin(), g.end(), 1.0f);
+    return g;
+  };
+  layers_.resize(arch_.num_layers);
+  for (size_t l = 0; l < arch_.num_layers; ++l) {
+    const LayerInfo li = layer_info(map_, l);
+    LayerPlan& L = layers_[l];
+    L.gamma_in = upload_vector(norm(li.input_norm));
+    L.gamma_post = upload_vector(norm(li.post_norm));
+    std::string why;
+    auto plan = [&](const char* name, size_t ts, size_t nt, size_t r, size_t c, size_t xl, size_t yl,
+                    bool acc, int64_t bt, ProjPlan* p) {
+      if (plan_projection(ts, nt, r, c, xl, yl, acc, bt, p, &why)) return true;
+      *err = "layer " + std::to_string(l) + " " + name + ": " + why;
+      return false;
+    };
+    if (!plan("q_proj", li.q_proj, li.q_tiles, qd, D, D, qd, false, li.q_bias, &L.q) ||
+        !plan("k_proj", li.k_proj, li.k_tiles, kvd, D, D, kvd, false, li.k_bias, &L.k) ||
+        !plan("v_proj", li.v_proj, li.v_tiles, kvd, D, D, kvd, false, li.v_bias, &L.v) ||
+        !plan("o_proj", li.o_proj, li.o_tiles, D, D, D, D, true, -1, &L.o) ||
+        !plan("gate_proj", li.gate_proj, li.gate_tiles, I, D, D, I, false, -1, &L.gate) ||
+        !plan("up_proj", li.up_proj, li.up_tiles, I, D, D, I, false, -1, &L.up) ||
+        !plan("down_proj", li.down_proj, li.down_tiles, D, I, I, D, true, -1, &L.down))
+      return false;
+    if (L.gate.kind != L.up.kind) { *err = "gate/up weight layouts differ"; return false; }
+  }
+  d_gamma_final_ = upload_vector(norm(final_norm_record(map_)));
+  if (!plan_lm_head(err)) return false;
+
+  // ---- activations, KV cache, RoPE tables, reduction scratch
+  const size_t V = arch_.vocab_size, S = cfg.max_seq_len, hd = arch_.head_dim;
+  d_hidden_ = static_cast<float*>(dev_alloc(D * 4));
+  d_q_ = static_cast<float*>(dev_alloc(qd * 4));
+  d_k_ = static_cast<float*>(dev_alloc(kvd * 4));
+  d_v_ = static_cast<float*>(dev_alloc(kvd * 4));
+  d_attn_ = static_cast<float*>(dev_alloc(std::max(D, qd) * 4));
+  d_mlp_ = static_cast<float*>(dev_alloc(I * 4));
+  d_logits_ = static_cast<float*>(dev_alloc(V * 4));
+  const size_t kv_elem = cfg.kv_f16 ? 2 : 4;
+  const size_t kv_bytes = arch_.num_layers * kvd * S * kv_elem;
+  d_kcache_ = dev_alloc(kv_bytes);
+  d_vcache_ = dev_alloc(kv_bytes);
+  d_part_ml_ = static_cast<float*>(dev_alloc(arch_.num_attn_heads * n_chunks_ * 2 * 4));
+  d_part_acc_ = static_cast<float*>(dev_alloc(arch_.num_attn_heads * n_chunks_ * hd * 4));
+  d_attn_counter_ = static_cast<uint32_t*>(dev_alloc(arch_.num_kv_heads * 4));
+  d_lm_counter_ = static_cast<uint32_t*>(dev_alloc(4));
+  d_partials_ = static_cast<ArgmaxPartial*>(dev_alloc(((V + 15) / 16) * sizeof(ArgmaxPartial)));
+  d_result_ = static_cast<StepResult*>(dev_alloc(sizeof(StepResult)));
+  d_state_ = static_cast<StepState*>(dev_alloc(sizeof(StepState)));
+  d_prompt_ = static_cast<uint32_t*>(dev_alloc(S * 4));
+  d_out_tokens_ = static_cast<uint32_t*>(dev_alloc(S * 4));
+  if (!d_hidden_ || !d_kcache_ || !d_vcache_ || !d_logits_ || !d_part_acc_ || !d_out_tokens_) {
+    *err = "device allocation failed";
+    return false;
+  }
+  HIP_TRY(hipMemset(d_hidden_, 0, D * 4));
+  HIP_TRY(hipMemset(d_kcache_, 0, kv_bytes));
+  HIP_TRY(hipMemset(d_vcache_, 0, kv_bytes));
+  HIP_TRY(hipMemset(d_attn_counter_, 0, arch_.num_kv_heads * 4));
+  HIP_TRY(hipMemset(d_lm_counter_, 0, 4));
+  HIP_TRY(hipMemset(d_result_, 0, sizeof(StepResult)));
+  HIP_TRY(hipMemset(d_state_, 0, sizeof(StepState)));
+  // RoPE angles exactly as applyRope computes them (src/chpe_engine.zig:197-206), in f32
+  std::vector<float> cs(S * (hd / 2)), sn(S * (hd / 2));
+  for (size_t p = 0; p < S; ++p) {
+    const float pos_f = float(p);
+    for (size_t i = 0; i < hd / 2; ++i) {
+      const float freq_exponent = 2.0f * float(i) / float(hd);
+      const float freq = 1.0f / std::pow(arch_.rope_theta, freq_exponent);
+      const float theta = pos_f * freq;
+      cs[p * (hd / 2) + i] = std::cos(theta);
+      sn[p * (hd / 2) + i] = std::sin(theta);
+    }
+  }
+  d_rope_cos_ = upload_vector(cs);
+  d_rope_sin_ = upload_vector(sn);
+  HIP_TRY(hipHostMalloc(reinterpret_cast<void**>(&h_state_), sizeof(StepState), hipHostMallocDefault));
+  HIP_TRY(hipHostMalloc(reinterpret_cast<void**>(&h_result_), sizeof(StepResult), hipHostMallocDefault));
+  HIP_TRY(hipDeviceSynchronize());
+
+  // ---- capture the step
+  HIP_TRY(hipStreamBeginCapture(stream_, hipStreamCaptureModeThreadLocal));
+  record_step(stream_);
+  HIP_TRY(hipStreamEndCapture(stream_, &graph_));
+  HIP_TRY(hipGraphInstantiate(&graph_exec_, graph_, nullptr, nullptr, 0));
+  return true;
+}
+
+bool Engine::plan_projection(size_t tile_start, size_t num_tiles, size_t r_total, size_t c_total,
+                             size_t x_len, size_t y_len, bool accumulate, int64_t bias_tile,
+                             ProjPlan* p, std::string* err) {
+  const uint8_t* b = host_bytes_;
+  const size_t len = len_;
+  (void)accumulate;
+  if (tile_start >= record_count_) {
+    *err = "tensor starts past the end of the archive (synthetic-output fallback)";
+    return false;
+  }
+  const size_t avail = std::min(num_tiles, record_count_ - tile_start);
+  const size_t cell_off = is_dense_ ? 0 : kPrefetchBytes;
+  p->rows = uint32_t(r_total);
+  p->cols = uint32_t(c_total);
+  if (!is_raw_) {
+    auto cell = [&](size_t t) { return 4096 + (tile_start + t) * stride_ + cell_off; };
+    p->base = d_image_ + cell(0);
+    p->stride = uint32_t(stride_);
+    if (c_total > 2048) {  // flat tiles: gemvCellFlat
+      const size_t need = (r_total * c_total + kFlatWeights - 1) / kFlatWeights;
+      if (avail < need) { *err = "flat tensor shorter than its shape"; return false; }
+      if (c_total % 128) { *err = "flat tensor width is not a multiple of 128"; return false; }
+      const uint8_t bits = b[cell(0) + kPayloadOff + kMetaQuantBits];
+      for (size_t t = 0; t < need; ++t) {
+        const size_t pl = cell(t) + kPayloadOff;
+        if (b[pl + kMetaQuantBits] != bits || !(rd<uint64_t>(b, len, pl + kMetaCustomFlags) & kFlagGroup128)) {
+          *err = "flat tiles are not uniformly group-128 " + std::to_string(bits) + "-bit";
+          return false;
+        }
+      }
+      if (bits == 4) p->kind = WeightKind::FlatW4;
+      else if (bits == 2) p->kind = WeightKind::FlatW2;
+      else { *err = "flat tiles of " + std::to_string(bits) + " bits"; return false; }
+      // outliers replace weights (chpe_engine.zig:632-646): per-row (col, w_out - w_code)
+      std::vector<std::vector<std::pair<uint32_t, float>>> by_row;
+      const size_t total = r_total * c_total;
+      for (size_t t = 0; t < need; ++t) {
+        const size_t pl = cell(t) + kPayloadOff, codes = cell(t) + kBytecodeHeader;
+        const uint16_t n = rd<uint16_t>(b, len, pl + kFlatOutlierN);
+        if (n == 0 || n > 64) continue;
+        std::map<uint32_t, float> last;  // offset -> replacement (the last entry wins)
+        for (size_t m = 0; m < n; ++m) {
+          const uint16_t off = rd<uint16_t>(b, len, pl + kFlatOutlierOff + 2 * m);
+          last[off] = f16_to_f32(rd<uint16_t>(b, len, pl + kFlatOutlierW + 2 * m));
+        }
+        for (const auto& [off, w] : last) {
+          const size_t f = t * kFlatWeights + off;
+          if (f >= total) continue;
+          const float s = f16_to_f32(rd<uint16_t>(b, len, pl + kGroupScales + 2 * (off / 128)));
+          float q;
+          if (bits == 4) {
+            q = float((b[codes + off / 2] >> (4 * (off & 1))) & 15) - 8.0f;
+          } else {
+            static const float lut[4] = {0.0f, 1.0f, -2.0f, -1.0f};
+            q = lut[(b[codes + off / 4] >> (2 * (off & 3))) & 3];
+          }
+          if (by_row.empty()) by_row.resize(r_total);
+          by_row[f / c_total].push_back({uint32_t(f % c_total), w - q * s});
+        }
+      }
+      if (!by_row.empty()) {
+        std::vector<uint32_t> ptr(r_total + 1, 0);
+        std::vector<float2> ent;
+        for (size_t r = 0; r < r_total; ++r) {
+          for (const auto& [c, d] : by_row[r]) {
+            float cf;
+            std::memcpy(&cf, &c, 4);
+            ent.push_back(make_float2(cf, d));
+          }
+          ptr[r + 1] = uint32_t(ent.size());
+        }
+        p->corr_ptr = static_cast<uint32_t*>(dev_alloc(ptr.size() * 4));
+        p->corr = static_cast<float2*>(dev_alloc(std::max<size_t>(ent.size(), 1) * sizeof(float2)));
+        if (!p->corr_ptr || !p->corr) { *err = "allocation"; return false; }
+        (void)hipMemcpy(p->corr_ptr, ptr.data(), ptr.size() * 4, hipMemcpyHostToDevice);
+        if (!ent.empty()) (void)hipMemcpy(p->corr, ent.data(), ent.size() * sizeof(float2), hipMemcpyHostToDevice);
+      }
+    } else {  // 16-row polymorphic cells: row bases are a prefix sum of dims.rows
+      size_t row_base = 0, n_cells = 0;
+      for (size_t t = 0; t < avail; ++t) {
+        if (row_base >= r_total) break;
+        const size_t pl = cell(t) + kPayloadOff;
+        const uint32_t rows = rd<uint32_t>(b, len, pl + kDimsRows);
+        if (rows == 0) break;
+        const uint32_t cols = rd<uint32_t>(b, len, pl + kDimsCols);
+        if (rows != 16 || cols != 2048 || b[pl + kMetaQuantBits] != 4 ||
+            !(rd<uint64_t>(b, len, pl + kMetaCustomFlags) & kFlagGroup128)) {
+          *err = "cell " + std::to_string(tile_start + t) +
+                 " is not a 16x2048 group-128 4-bit cell (other polymorphic cells are not built "
+                 "on the GPU path yet)";
+          return false;
+        }
+        row_base += rows;
+        ++n_cells;
+      }
+      if (row_base != r_total || c_total != 2048 || x_len < 2048 || y_len < r_total) {
+        *err = "16-row cells do not cover the tensor exactly";
+        return false;
+      }
+      (void)n_cells;
+      p->kind = WeightKind::Cell16W4;
+    }
+  } else {
+    if (quant_bits_ != 16) { *err = "raw int8 tiles are not built on the GPU path yet"; return false; }
+    if (avail * wpt_ < r_total * c_total || c_total % 8) { *err = "raw tensor shorter than its shape"; return false; }
+    p->kind = WeightKind::Raw16;
+    p->base = d_image_ + 4096 + tile_start * kTileCodeBytes;
+    p->stride = uint32_t(kTileCodeBytes);
+    p->bf16 = is_raw_fp16_ ? 0 : 1;
+  }
+  if (bias_tile >= 0 && size_t(bias_tile) < record_count_) {  // unpackBias: :1172-1192
+    const size_t off = is_raw_ ? 4096 + size_t(bias_tile) * kTileCodeBytes
+                               : 4096 + size_t(bias_tile) * stride_ + cell_off + kBytecodeHeader;
+    std::vector<float> bias(r_total);
+    const bool bf = arch_.hidden_dim == 4096 && is_raw_;
+    for (size_t i = 0; i < r_total; ++i) {
+      bias[i] = bf ? bf16_to_f32(rd<uint16_t>(b, len, off + 2 * i)) : rd<float>(b, len, off + 4 * i);
+      if (!std::isfinite(bias[i])) bias[i] = 0.0f;
+    }
+    p->bias = upload_vector(bias);
+  }
+  return true;
+}
+
+bool Engine::plan_lm_head(std::string* err) {
+  // computeLmHead: src/chpe_engine.zig:1554-1660
+  const size_t D = arch_.hidden_dim, V = arch_.vocab_size;
+  size_t start = 0, tiles = 0;
+  std::string why;
+  if (lm_head_record(D, &start, &tiles) && start < record_count_) {
+    if (!plan_projection(start, tiles, V, D, D, V, false, -1, &lm_head_, &why)) {
+      *err = "lm_head: " + why;
+      return false;
+    }
+    return true;
+  }
+  if (!is_raw_) {  // tied embedding cells, outliers replace (unpackEmbedRowCell)
+    const size_t n_cells = (V + 15) / 16, cell_off = is_dense_ ? 0 : kPrefetchBytes;
+    if (n_cells > record_count_ || D != 2048) { *err = "tied LM head: unsupported shape"; return false; }
+    for (size_t t = 0; t < n_cells; ++t) {
+      const size_t pl = 4096 + t * stride_ + cell_off + kPayloadOff;
+      const uint32_t rows = rd<uint32_t>(host_bytes_, len_, pl + kDimsRows);
+      if ((rows != 16 && rows != 0) || host_bytes_[pl + kMetaQuantBits] != 4 ||
+          !(rd<uint64_t>(host_bytes_, len_, pl + kMetaCustomFlags) & kFlagGroup128)) {
+        *err = "tied LM head: embedding cell " + std::to_string(t) + " is not a 16-row group-128 4-bit cell";
+        return false;
+      }
+    }
+    lm_head_.kind = WeightKind::Cell16W4;
+    lm_head_.base = d_image_ + 4096 + cell_off;
+    lm_head_.stride = uint32_t(stride_);
+    lm_head_.rows = uint32_t(V);
+    lm_head_.cols = uint32_t(D);
+    lm_head_.replace_outliers = 1;
+    return true;
+  }
+  // tied embedding in a raw archive: rows are contiguous 16-bit vectors from record 0
+  const size_t rpt = std::max<size_t>(1, 8192 / D);
+  const size_t need = (V + rpt - 1) / rpt;
+  if (std::min(record_count_, need) < need || D % 8) { *err = "tied raw LM head: archive too short"; return false; }
+  lm_head_.kind = WeightKind::Raw16;
+  lm_head_.base = d_image_ + 4096;
+  lm_head_.stride = uint32_t(kTileCodeBytes);
+  lm_head_.rows = uint32_t(V);
+  lm_head_.cols = uint32_t(D);
+  lm_head_.bf16 = is_raw_fp16_ ? 0 : 1;
+  return true;
+}
+
+void Engine::enqueue_gemv(const ProjPlan* parts[], int n, GemvMode mode, const float* x, uint32_t C,
+                          const float* gamma, float* y_override, hipStream_t st) {
+  GemvArgs a{};
+  a.n_parts = n;
+  a.mode = int(mode);
+  a.C = C;
+  a.rows_per_block = gemv_rows_per_block(parts[0]->kind);
+  a.x = x;
+  a.gamma = gamma;
+  a.eps = arch_.rms_eps;
+  uint32_t blocks = 0;
+  for (int i = 0; i < n; ++i) {
+    const ProjPlan& p = *parts[i];
+    GemvPart& g = a.part[i];
+    g.base = p.base;
+    g.stride = p.stride;
+    g.rows = p.rows;
+    g.bf16 = p.bf16;
+    g.bias = p.bias;
+    g.corr_ptr = p.corr_ptr;
+    g.corr = p.corr;
+    g.replace_outliers = p.replace_outliers;
+    g.block_begin = mode == GemvMode::SwiGlu ? 0 : blocks;
+    const uint32_t nb = (p.rows + a.rows_per_block - 1) / a.rows_per_block;
+    blocks = mode == GemvMode::SwiGlu ? nb : blocks + nb;
+  }
+  if (mode == GemvMode::Logits) {
+    a.partials = d_partials_;
+    a.counter = d_lm_counter_;
+    a.result = d_result_;
+    a.vocab = uint32_t(arch_.vocab_size);
+  }
+  for (int i = 0; i < n; ++i) a.part[i].y = y_override;
+  launch_gemv(parts[0]->kind, a, blocks, st);
+}
+
+void Engine::enqueue_qkv(const LayerPlan& L, hipStream_t st) {
+  // q, k, v in one launch when they share a layout (each part writes its own output + bias)
+  const uint32_t D = uint32_t(arch_.hidden_dim);
+  const ProjPlan* qkv[3] = {&L.q, &L.k, &L.v};
+  float* outs[3] = {d_q_, d_k_, d_v_};
+  if (L.q.kind != L.k.kind || L.k.kind != L.v.kind) {
+    for (int i = 0; i < 3; ++i) {
+      const ProjPlan* one[1] = {qkv[i]};
+      enqueue_gemv(one, 1, GemvMode::Store, d_hidden_, D, L.gamma_in, outs[i], st);
+    }
+    return;
+  }
+  GemvArgs a{};
+  a.n_parts = 3;
+  a.mode = int(GemvMode::Store);
+  a.C = D;
+  a.rows_per_block = gemv_rows_per_block(L.q.kind);
+  a.x = d_hidden_;
+  a.gamma = L.gamma_in;
+  a.eps = arch_.rms_eps;
+  uint32_t blocks = 0;
+  for (int i = 0; i < 3; ++i) {
+    const ProjPlan& p = *qkv[i];
+    GemvPart& g = a.part[i];
+    g.base = p.base; g.stride = p.stride; g.rows = p.rows; g.bf16 = p.bf16; g.bias = p.bias;
+    g.corr_ptr = p.corr_ptr; g.corr = p.corr; g.replace_outliers = p.replace_outliers;
+    g.y = outs[i];
+    g.block_begin = blocks;
+    blocks += (p.rows + a.rows_per_block - 1) / a.rows_per_block;
+  }
+  launch_gemv(L.q.kind, a, blocks, st);
+}
+
+void Engine::record_step(hipStream_t st) {
+  const uint32_t D = uint32_t(arch_.hidden_dim), I = uint32_t(arch_.intermediate_dim);
+  EmbedArgs e{};
+  e.image = d_image_;
+  e.image_len = image_len_;
+  e.state = d_state_;
+  e.hidden = d_hidden_;
+  e.D = D;
+  e.kind = embed_kind_;
+  e.record_count = record_count_;
+  e.stride = stride_;
+  e.code_off = is_raw_ ? 0 : (is_dense_ ? 0 : kPrefetchBytes) + kBytecodeHeader;
+  e.cell_off = is_dense_ ? 0 : kPrefetchBytes;
+  launch_embed(e, st);
+  const size_t kvd = arch_.num_kv_heads * arch_.head_dim, S = cfg_.max_seq_len;
+  const size_t kv_elem = cfg_.kv_f16 ? 2 : 4;
+  for (size_t l = 0; l < arch_.num_layers; ++l) {
+    const LayerPlan& L = layers_[l];
+    enqueue_qkv(L, st);
+    AttnArgs at{};
+    at.state = d_state_;
+    at.q_raw = d_q_;
+    at.k_raw = d_k_;
+    at.v_raw = d_v_;
+    at.k_cache = static_cast<uint8_t*>(d_kcache_) + l * kvd * S * kv_elem;
+    at.v_cache = static_cast<uint8_t*>(d_vcache_) + l * kvd * S * kv_elem;
+    at.rope_cos = d_rope_cos_;
+    at.rope_sin = d_rope_sin_;
+    at.out = d_attn_;
+    at.part_ml = d_part_ml_;
+    at.part_acc = d_part_acc_;
+    at.counter = d_attn_counter_;
+    at.H = uint32_t(arch_.num_attn_heads);
+    at.KV = uint32_t(arch_.num_kv_heads);
+    at.hd = uint32_t(arch_.head_dim);
+    at.max_seq = uint32_t(S);
+    at.n_chunks = n_chunks_;
+    at.kv_f16 = cfg_.kv_f16 ? 1 : 0;
+    at.scale = 1.0f / std::sqrt(float(arch_.head_dim));
+    launch_attention(at, st);
+    const ProjPlan* o[1] = {&L.o};
+    enqueue_gemv(o, 1, GemvMode::Accum, d_attn_, D, nullptr, d_hidden_, st);
+    const ProjPlan* gu[2] = {&L.gate, &L.up};
+    enqueue_gemv(gu, 2, GemvMode::SwiGlu, d_hidden_, D, L.gamma_post, d_mlp_, st);
+    const ProjPlan* dn[1] = {&L.down};
+    enqueue_gemv(dn, 1, GemvMode::Accum, d_mlp_, I, nullptr, d_hidden_, st);
+  }
+  const ProjPlan* lm[1] = {&lm_head_};
+  enqueue_gemv(lm, 1, GemvMode::Logits, d_hidden_, D, d_gamma_final_, d_logits_, st);
+  AdvanceArgs adv{d_state_, d_prompt_, d_result_, d_out_tokens_};
+  launch_advance(adv, st);
+}
+
+int Engine::read_result(ForwardResult* out) const {
+  if (hipMemcpy(h_result_, d_result_, sizeof(StepResult), hipMemcpyDeviceToHost) != hipSuccess) return -3;
+  out->argmax_token = h_result_->argmax;
+  out->max_logit = h_result_->max_logit;
+  out->token0_logit = h_result_->token0_logit;
+  out->hidden_norm = h_result_->hidden_norm;
+  out->all_finite = h_result_->all_finite != 0;
+  return 0;
+}
+
+int Engine::forward(uint32_t token, size_t pos, ForwardResult* out) {
+  if (pos >= cfg_.max_seq_len) return -2;  // the reference reads past its KV cache here
+  const uint64_t t0 = now_ns();
+  *h_state_ = StepState{token, uint32_t(pos), 0, 0};
+  if (hipMemcpyAsync(d_state_, h_state_, sizeof(StepState), hipMemcpyHostToDevice, stream_) != hipSuccess) return -3;
+  if (hipGraphLaunch(graph_exec_, stream_) != hipSuccess) return -3;
+  if (hipMemcpyAsync(h_result_, d_result_, sizeof(StepResult), hipMemcpyDeviceToHost, stream_) != hipSuccess) return -3;
+  if (hipStreamSynchronize(stream_) != hipSuccess) return -3;
+  const uint64_t t1 = now_ns();
+  out->argmax_token = h_result_->argmax;
+  out->max_logit = h_result_->max_logit;
+  out->token0_logit = h_result_->token0_logit;
+  out->hidden_norm = h_result_->hidden_norm;
+  out->all_finite = h_result_->all_finite != 0;
+  out->elapsed_ns = t1 - t0;
+  return 0;
+}
+
+void Engine::launch_steps(size_t n) {
+  for (size_t i = 0; i < n; ++i) (void)hipGraphLaunch(graph_exec_, stream_);
+}
+
+int Engine::sync() { return hipStreamSynchronize(stream_) == hipSuccess ? 0 : -3; }
+
+int Engine::forward_tokens(const uint32_t* toks, size_t n, ForwardResult* out) {
+  if (n == 0 || !toks) return -1;
+  if (n > cfg_.max_seq_len) return -2;
+  if (hipMemcpyAsync(d_prompt_, toks, n * 4, hipMemcpyHostToDevice, stream_) != hipSuccess) return -3;
+  *h_state_ = StepState{toks[0], 0, uint32_t(n), 0};
+  if (hipMemcpyAsync(d_state_, h_state_, sizeof(StepState), hipMemcpyHostToDevice, stream_) != hipSuccess) return -3;
+  launch_steps(n - 1);
+  if (sync()) return -3;
+  const uint64_t t0 = now_ns();
+  launch_steps(1);
+  if (hipMemcpyAsync(h_result_, d_result_, sizeof(StepResult), hipMemcpyDeviceToHost, stream_) != hipSuccess) return -3;
+  if (sync()) return -3;
+  const uint64_t t1 = now_ns();
+  out->argmax_token = h_result_->argmax;
+  out->max_logit = h_result_->max_logit;
+  out->token0_logit = h_result_->token0_logit;
+  out->hidden_norm = h_result_->hidden_norm;
+  out->all_finite = h_result_->all_finite != 0;
+  out->elapsed_ns = t1 - t0;
+  return 0;
+}
+
+int Engine::generate(const uint32_t* prompt, size_t n_prompt, size_t n_gen, uint32_t* out_tokens,
+                     ForwardResult* last) {
+  if (n_prompt == 0 || !prompt || n_gen == 0) return -1;
+  const size_t steps = n_prompt + n_gen - 1;
+  if (steps > cfg_.max_seq_len) return -2;
+  if (hipMemcpyAsync(d_prompt_, prompt, n_prompt * 4, hipMemcpyHostToDevice, stream_) != hipSuccess) return -3;
+  *h_state_ = StepState{prompt[0], 0, uint32_t(n_prompt), 0};
+  if (hipMemcpyAsync(d_state_, h_state_, sizeof(StepState), hipMemcpyHostToDevice, stream_) != hipSuccess) return -3;
+  launch_steps(steps);
+  if (sync()) return -3;
+  if (out_tokens &&
+      hipMemcpy(out_tokens, d_out_tokens_ + (n_prompt - 1), n_gen * 4, hipMemcpyDeviceToHost) != hipSuccess)
+    return -3;
+  if (last && read_result(last)) return -3;
+  return 0;
+}
+
+int Engine::copy_logits(float* out) const {
+  return hipMemcpy(out, d_logits_, arch_.vocab_size * 4, hipMemcpyDeviceToHost) == hipSuccess ? 0 : -3;
+}
+
+int Engine::copy_hidden(float* out) const {
+  return hipMemcpy(out, d_hidden_, arch_.hidden_dim * 4, hipMemcpyDeviceToHost) == hipSuccess ? 0 : -3;
+}
+
+double Engine::proj_bytes(const ProjPlan& p) const {
+  // algorithmic bytes: codes + group scales + outliers (+ bias); no headers or padding
+  const double n = double(p.rows) * p.cols;
+  double bytes = 0.0;
+  switch (p.kind) {
+    case WeightKind::Raw16: bytes = 2.0 * n; break;
+    case WeightKind::Cell16W4: bytes = n / 2 + n / 128 * 2 + double(p.rows / 16) * (16 * 8 * 2 + 8 * 2); break;
+    case WeightKind::FlatW4: bytes = n / 2 + n / 128 * 2 + std::ceil(n / kFlatWeights) * (2 + 64 * 4); break;
+    case WeightKind::FlatW2: bytes = n / 4 + n / 128 * 2 + std::ceil(n / kFlatWeights) * (2 + 64 * 4); break;
+  }
+  if (p.bias) bytes += 4.0 * p.rows;
+  return bytes;
+}
+
+double Engine::stage_bytes(int stage, size_t l) const {
+  const LayerPlan& L = layers_[l];
+  switch (stage) {
+    case 0: return proj_bytes(L.q) + proj_bytes(L.k) + proj_bytes(L.v);
+    case 1: return proj_bytes(L.o);
+    case 2: return proj_bytes(L.gate) + proj_bytes(L.up);
+    case 3: return proj_bytes(L.down);
+    default: return proj_bytes(lm_head_);
+  }
+}
+
+double Engine::step_bytes(size_t pos) const {
+  double bytes = 0.0;
+  const double D = double(arch_.hidden_dim);
+  for (size_t l = 0; l < arch_.num_layers; ++l)
+    bytes += stage_bytes(0, l) + stage_bytes(1, l) + stage_bytes(2, l) + stage_bytes(3, l) + 2 * D * 4;
+  bytes += stage_bytes(4, 0) + D * 4;                        // LM head + final norm
+  bytes += D * (is_raw_ ? 2.0 : 0.5625);                     // embedding row
+  const double kv_row = double(arch_.num_kv_heads * arch_.head_dim) * (cfg_.kv_f16 ? 2 : 4);
+  bytes += double(arch_.num_layers) * 2 * kv_row * (double(pos) + 1);  // K and V read
+  bytes += double(arch_.num_layers) * 2 * kv_row;                      // K and V written
+  return bytes;
+}
+
+int Engine::launch_stage(int stage, size_t l) {
+  if (l >= layers_.size()) return -1;
+  const LayerPlan& L = layers_[l];
+  const uint32_t D = uint32_t(arch_.hidden_dim), I = uint32_t(arch_.intermediate_dim);
+  switch (stage) {
+    case 0:
+      enqueue_qkv(L, stream_);
+      return 0;
+    case 1: {
+      const ProjPlan* o[1] = {&L.o};
+      enqueue_gemv(o, 1, GemvMode::Store, d_attn_, D, nullptr, d_q_, stream_);
+      return 0;
+    }
+    case 2: {
+      const ProjPlan* gu[2] = {&L.gate, &L.up};
+      enqueue_gemv(gu, 2, GemvMode::SwiGlu, d_hidden_, D, L.gamma_post, d_mlp_, stream_);
+      return 0;
+    }
+    case 3: {
+      const ProjPlan* dn[1] = {&L.down};
+      enqueue_gemv(dn, 1, GemvMode::Store, d_mlp_, I, nullptr, d_attn_, stream_);
+      return 0;
+    }
+    case 4: {
+      const ProjPlan* lm[1] = {&lm_head_};
+      enqueue_gemv(lm, 1, GemvMode::Logits, d_hidden_, D, d_gamma_final_, d_logits_, stream_);
+      return 0;
+    }
+  }
+  return -1;
+}
+
+}  // namespace chpe
+
+namespace chpe {
+
+int Engine::debug_gemv(size_t layer, int which, const float* x, float* y) {
+  // which: 0 q, 1 k, 2 v, 3 o, 4 gate, 5 up, 6 down, 7 LM head (logits only)
+  if (which < 7 && layer >= layers_.size()) return -1;
+  const ProjPlan* p = nullptr;
+  if (which == 7) {
+    p = &lm_head_;
+  } else {
+    const LayerPlan& L = layers_[layer];
+    const ProjPlan* all[7] = {&L.q, &L.k, &L.v, &L.o, &L.gate, &L.up, &L.down};
+    if (which < 0 || which > 6) return -1;
+    p = all[which];
+  }
+  const size_t C = p->cols, R = p->rows;
+  float *dx = nullptr, *dy = nullptr;
+  int rc = -3;
+  if (hipMalloc(&dx, C * 4) == hipSuccess && hipMalloc(&dy, R * 4) == hipSuccess &&
+      hipMemcpy(dx, x, C * 4, hipMemcpyHostToDevice) == hipSuccess) {
+    const ProjPlan* one[1] = {p};
+    enqueue_gemv(one, 1, GemvMode::Store, dx, uint32_t(C), nullptr, dy, stream_);
+    if (sync() == 0 && hipMemcpy(y, dy, R * 4, hipMemcpyDeviceToHost) == hipSuccess) rc = 0;
+  }
+  if (dx) (void)hipFree(dx);
+  if (dy) (void)hipFree(dy);
+  return rc;
+}
+
+}  // namespace chpe

@@ -1,0 +1,164 @@
+// engine.hpp -- CHPEEngine for MI355X: the host side of the decode step.
+//
+// Mirrors the reference engine's interface (src/chpe_engine.zig:820-1804):
+//   init(archive bytes, ModelArch, max_seq_len)  -> Engine::create
+//   forwardDecode(token, pos) -> ForwardResult    -> Engine::forward
+//   logits_buf                                    -> Engine::copy_logits
+// The step itself runs on the GPU as one captured hipGraph; the host only writes the
+// (token, pos) state and reads back the result.
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "kernels.hpp"
+#include "tensor_maps.hpp"
+
+namespace chpe {
+
+struct ModelArch {  // src/chpe_engine.zig:96-146
+  int id;           // 0 Qwen2.5-3B, 1 Qwen3.5-9B, 2 Qwen2.5-72B
+  const char* name;
+  size_t hidden_dim, intermediate_dim, num_layers, num_attn_heads, num_kv_heads, head_dim, vocab_size;
+  float rope_theta, rms_eps;
+};
+bool arch_preset(int id, ModelArch* out);
+int arch_from_path(const char* path);  // src/chpe_c_api.zig:29-37
+
+struct ForwardResult {  // src/chpe_engine.zig:803-810
+  uint32_t argmax_token;
+  float max_logit;
+  float token0_logit;
+  uint64_t elapsed_ns;
+  float hidden_norm;
+  bool all_finite;
+};
+
+struct EngineConfig {
+  int arch_id = 0;
+  size_t max_seq_len = 2048;
+  bool kv_f16 = false;  // fp16 KV cache (the reference keeps f32)
+};
+
+// One projection as the GPU computes it (a gemvLinear call of the reference).
+struct ProjPlan {
+  WeightKind kind = WeightKind::Raw16;
+  const uint8_t* base = nullptr;  // device address of the first record
+  uint32_t stride = 0;
+  uint32_t rows = 0, cols = 0;
+  uint32_t bf16 = 0;
+  uint32_t replace_outliers = 0;
+  float* bias = nullptr;               // device, with the reference's non-finite -> 0 rule
+  uint32_t* corr_ptr = nullptr;        // device CSR of flat-tile outlier corrections
+  float2* corr = nullptr;
+};
+
+struct LayerPlan {
+  ProjPlan q, k, v, o, gate, up, down;
+  float* gamma_in = nullptr;    // device, unpackNorm rules applied
+  float* gamma_post = nullptr;
+};
+
+class Engine {
+ public:
+  // `bytes` must stay valid for the engine's lifetime only during create() (the archive is
+  // copied to the GPU).  Returns null and sets *err on failure.
+  static std::unique_ptr<Engine> create(const uint8_t* bytes, size_t len, const EngineConfig& cfg,
+                                        std::string* err);
+  ~Engine();
+  Engine(const Engine&) = delete;
+  Engine& operator=(const Engine&) = delete;
+
+  // forwardDecode(token, pos): one step, synchronous.  Returns 0, or -2 if pos >= max_seq_len.
+  int forward(uint32_t token, size_t pos, ForwardResult* out);
+  // positions 0..n-1 teacher-forced (chpe_forward_tokens); result of the last step
+  int forward_tokens(const uint32_t* tokens, size_t n, ForwardResult* out);
+  // prompt teacher-forced, then n_gen greedy tokens fed back on the device
+  int generate(const uint32_t* prompt, size_t n_prompt, size_t n_gen, uint32_t* out_tokens,
+               ForwardResult* last);
+  // enqueue n graph launches continuing from the current device state (no sync)
+  void launch_steps(size_t n);
+  int sync();
+  int copy_logits(float* out) const;   // vocab_size floats of the last step
+  int copy_hidden(float* out) const;   // hidden_dim floats (the residual stream)
+  int read_result(ForwardResult* out) const;
+
+  const ModelArch& arch() const { return arch_; }
+  size_t max_seq_len() const { return cfg_.max_seq_len; }
+  hipStream_t stream() const { return stream_; }
+  bool archive_valid() const { return archive_valid_; }
+  int quant_bits() const { return quant_bits_; }
+  bool is_raw() const { return is_raw_; }
+  size_t record_count() const { return record_count_; }
+  const LayerPlan& layer(size_t l) const { return layers_[l]; }
+  const ProjPlan& lm_head() const { return lm_head_; }
+  // weight + KV bytes the step reads at position `pos` (the roofline numerator)
+  double step_bytes(size_t pos) const;
+  // re-launch one layer's projection kernel alone (measurement): 0 = qkv, 1 = o,
+  // 2 = gate/up, 3 = down, 4 = LM head
+  int launch_stage(int stage, size_t layer);
+  // bytes one launch of launch_stage(stage, layer) reads from HBM (weights, scales, outliers)
+  double stage_bytes(int stage, size_t layer) const;
+
+ private:
+  Engine() = default;
+  bool init(const uint8_t* bytes, size_t len, const EngineConfig& cfg, std::string* err);
+  bool plan_projection(size_t tile_start, size_t num_tiles, size_t r_total, size_t c_total,
+                       size_t x_len, size_t y_len, bool accumulate, int64_t bias_tile,
+                       ProjPlan* out, std::string* err);
+  bool plan_lm_head(std::string* err);
+  float* upload_vector(const std::vector<float>& v);
+  void* dev_alloc(size_t bytes);
+  void record_step(hipStream_t st);
+  void enqueue_qkv(const LayerPlan& L, hipStream_t st);
+  void enqueue_gemv(const ProjPlan* parts[], int n, GemvMode mode, const float* x, uint32_t C,
+                    const float* gamma, float* y_override, hipStream_t st);
+  double proj_bytes(const ProjPlan& p) const;
+
+ public:
+  // run one projection's GEMV on a caller vector (Store mode, bias included): parity hooks
+  int debug_gemv(size_t layer, int which, const float* x, float* y);
+
+ private:
+
+  // archive
+  const uint8_t* host_bytes_ = nullptr;
+  size_t len_ = 0;
+  bool archive_valid_ = false, is_dense_ = false, is_raw_ = false, is_raw_fp16_ = false;
+  int quant_bits_ = 2;
+  size_t record_count_ = 0, stride_ = 0, wpt_ = 0;
+  MapKind map_ = MapKind::Qwen3bRaw;
+  ModelArch arch_{};
+  EngineConfig cfg_{};
+
+  // device memory
+  std::vector<void*> allocs_;
+  uint8_t* d_image_ = nullptr;  // archive byte 0
+  size_t image_len_ = 0;
+  std::vector<LayerPlan> layers_;
+  ProjPlan lm_head_;
+  float* d_gamma_final_ = nullptr;
+  float *d_hidden_ = nullptr, *d_q_ = nullptr, *d_k_ = nullptr, *d_v_ = nullptr, *d_attn_ = nullptr,
+        *d_mlp_ = nullptr, *d_logits_ = nullptr;
+  void *d_kcache_ = nullptr, *d_vcache_ = nullptr;
+  float *d_rope_cos_ = nullptr, *d_rope_sin_ = nullptr, *d_part_ml_ = nullptr, *d_part_acc_ = nullptr;
+  uint32_t *d_attn_counter_ = nullptr, *d_lm_counter_ = nullptr, *d_prompt_ = nullptr,
+           *d_out_tokens_ = nullptr;
+  ArgmaxPartial* d_partials_ = nullptr;
+  StepResult* d_result_ = nullptr;
+  StepState* d_state_ = nullptr;
+  StepState* h_state_ = nullptr;      // pinned
+  StepResult* h_result_ = nullptr;    // pinned
+  int embed_kind_ = 0;
+  uint32_t n_chunks_ = 0;
+
+  hipStream_t stream_ = nullptr;
+  hipGraph_t graph_ = nullptr;
+  hipGraphExec_t graph_exec_ = nullptr;
+};
+
+}  // namespace chpe

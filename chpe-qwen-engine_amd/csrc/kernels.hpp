@@ -1,0 +1,142 @@
+// kernels.hpp -- argument blocks and launchers of the gfx950 decode kernels.
+//
+// Each kernel is one stage of CHPEEngine.forwardDecode (src/chpe_engine.zig:1663-1803):
+//   embed            unpackEmbedRow                       (:1491-1552, :1288-1394)
+//   gemv_*           gemvLinear / gemvTile* / gemvCellFlat (:1396-1489, :223-729)
+//                    with the RMSNorm that precedes it fused into the prologue
+//                    (rmsNorm :163-193) and the bias / residual / SwiGLU / LM-head argmax
+//                    that follows it fused into the epilogue
+//   attention        RoPE (:195-216) + KV write (:1693-1697) + GQA attention (:1700-1734)
+//   finish           argmax / all_finite / logits[0] / hidden norm (:1775-1803)
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace chpe {
+
+// Weight layouts a GEMV launch can read (selected per tensor by the host plan).
+enum class WeightKind : int {
+  Raw16 = 0,     // raw archive: contiguous row-major fp16 / bf16 matrix (dotSegment)
+  Cell16W4 = 1,  // 16-row cells, 4-bit, GROUP128, rows=16, cols=C (gemvTileW4)
+  FlatW4 = 2,    // flat 32768-weight tiles, 4-bit, GROUP128 (gemvCellFlat)
+  FlatW2 = 3,    // flat tiles, 2-bit, GROUP128
+};
+
+enum class GemvMode : int {
+  Store = 0,   // y = W x (+ bias)
+  Accum = 1,   // y += W x            (o / down projections into the residual stream)
+  SwiGlu = 2,  // y = silu(W0 x) * (W1 x)
+  Logits = 3,  // logits = W x, then the argmax reduction of the whole vocabulary
+};
+
+constexpr int kMaxParts = 3;
+
+struct GemvPart {
+  const uint8_t* base;       // device address of the tensor's first record (cell start / raw codes)
+  uint32_t stride;           // record stride in bytes
+  uint32_t rows;             // output rows (r_total)
+  uint32_t block_begin;      // first block of this part in the launch grid
+  uint32_t bf16;             // Raw16: 1 = bf16, 0 = fp16
+  float* y;                  // output vector
+  const float* bias;         // per-row bias (Store), may be null
+  const uint32_t* corr_ptr;  // FlatW*: per-row outlier corrections (CSR), may be null
+  const float2* corr;        //   (column as float bits, delta)
+  uint32_t replace_outliers; // Cell16W4: outliers replace (embedding / tied LM head) instead of add
+};
+
+struct StepResult {  // ForwardResult, src/chpe_engine.zig:803-810 (elapsed measured on the host)
+  uint32_t argmax;
+  float max_logit;
+  float token0_logit;
+  float hidden_norm;
+  uint32_t all_finite;
+  uint32_t pad[3];
+};
+
+struct ArgmaxPartial {
+  float value;
+  uint32_t index;     // 0xffffffff: no candidate in this block
+  uint32_t nonfinite;
+  uint32_t pad;
+};
+
+struct GemvArgs {
+  GemvPart part[kMaxParts];
+  int n_parts;
+  int mode;
+  uint32_t C;              // columns (length of x)
+  uint32_t rows_per_block; // output rows per block (per part in SwiGlu mode)
+  const float* x;          // input vector (f32)
+  const float* gamma;      // RMSNorm gains: x is normalised in the prologue when non-null
+  float eps;
+  // Logits mode
+  ArgmaxPartial* partials;
+  uint32_t* counter;       // zero between launches; the last block resets it
+  StepResult* result;
+  uint32_t vocab;
+  // hidden-norm output (Logits mode: block 0 writes sqrt(sum x^2) of the raw input)
+};
+
+struct StepState {  // device-resident per-token state read by the captured step
+  uint32_t token;
+  uint32_t pos;
+  uint32_t n_prompt;   // teacher-forced positions (prompt) for device-side advance
+  uint32_t n_steps;    // steps executed so far by generate()
+};
+
+struct EmbedArgs {
+  const uint8_t* image;     // archive image base (device), byte 0 = archive byte 0
+  uint64_t image_len;       // bytes readable at `image` (archive + zero padding)
+  const StepState* state;
+  float* hidden;
+  uint32_t D;
+  int kind;                 // 0 synthetic, 1 raw fp16, 2 raw bf16, 3 raw int8, 4 cell
+  uint64_t record_count;
+  uint64_t stride;          // record stride
+  uint64_t code_off;        // offset of the code area inside a record
+  uint64_t cell_off;        // offset of the cell inside a record
+};
+
+struct AttnArgs {
+  const StepState* state;
+  const float* q_raw;       // [H*hd] projection output (bias included), before RoPE
+  const float* k_raw;       // [KV*hd]
+  const float* v_raw;
+  void* k_cache;            // this layer: [KV][max_seq][hd], f16 or f32
+  void* v_cache;
+  const float* rope_cos;    // [max_seq][hd/2]
+  const float* rope_sin;
+  float* out;               // [H*hd]
+  float* part_ml;           // [H][n_chunks][2] (max, sum)
+  float* part_acc;          // [H][n_chunks][hd]
+  uint32_t* counter;        // [KV], zero between launches
+  uint32_t H, KV, hd, max_seq, n_chunks;
+  uint32_t kv_f16;
+  float scale;              // 1/sqrt(hd)
+};
+
+struct AdvanceArgs {
+  StepState* state;
+  const uint32_t* prompt;   // teacher-forced tokens
+  const StepResult* result;
+  uint32_t* out_tokens;     // argmax of every step, indexed by position
+};
+
+// launchers (kernels.hip); all enqueue on `stream` and never synchronise
+void launch_embed(const EmbedArgs& a, hipStream_t stream);
+void launch_gemv(WeightKind kind, const GemvArgs& a, uint32_t n_blocks, hipStream_t stream);
+void launch_attention(const AttnArgs& a, hipStream_t stream);
+void launch_advance(const AdvanceArgs& a, hipStream_t stream);
+size_t gemv_lds_bytes(WeightKind kind, const GemvArgs& a);
+uint32_t gemv_threads(WeightKind kind, GemvMode mode);
+uint32_t gemv_rows_per_block(WeightKind kind);
+constexpr uint32_t kAttnMaxChunks = 160;  // chunks of 8192/hd positions per attention launch
+inline uint32_t attn_chunk(uint32_t hd) { return 8192u / hd; }
+
+// test hooks: dequantise / unpack exactly as the reference materialises weights
+void launch_flat_tile_weights(const uint8_t* cell, float* out, hipStream_t stream);
+void launch_embed_row_cell(const uint8_t* cell, uint64_t len, uint32_t row, uint32_t D, float* out,
+                           int* written, hipStream_t stream);
+
+}  // namespace chpe

@@ -1,0 +1,99 @@
+/* chpe.h -- C ABI of the MI355X decode engine (libchpe.so).
+ *
+ * The first twelve symbols are the reference's C ABI (src/chpe_c_api.zig:25-143) with the
+ * same signatures, ownership and sentinel-value error behaviour; each one cites the
+ * reference symbol it replaces.  Behaviour kept on purpose:
+ *   - chpe_init guesses the architecture from the path ("9B"/"9b"/"qwen35" -> Qwen3.5-9B,
+ *     "72B"/"72b" -> Qwen2.5-72B, else Qwen2.5-3B) and fixes max_seq_len at 2048;
+ *   - chpe_forward_tokens restarts at position 0 on every call (teacher-forced prompt);
+ *   - getters on a NULL context return the 3B defaults (vocab/hidden/layers) or 0.
+ * One deliberate difference: where the reference reads past its KV cache (more tokens than
+ * max_seq_len), chpe_forward_tokens returns -2.
+ *
+ * Symbols after those twelve are additions; they have no counterpart in the reference.
+ * A context is not re-entrant (one engine state); separate contexts are independent.
+ */
+#ifndef CHPE_H
+#define CHPE_H
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* chpe_c_api.zig:25-48 `chpe_init`: mmap + validate the archive, build the engine.
+ * Returns NULL on any error. */
+void *chpe_init(const char *archive_path);
+
+/* chpe_c_api.zig:50-78 `chpe_forward_tokens`: decode positions 0..num_tokens-1.
+ * Returns the last argmax, -1 if ctx/tokens is NULL or num_tokens == 0, -2 if num_tokens
+ * exceeds the context's max_seq_len, -3 on a device error.  out_logits (optional) receives
+ * vocab_size floats of the last step. */
+int chpe_forward_tokens(void *ctx, const uint32_t *tokens, size_t num_tokens, float *out_logits);
+
+/* chpe_c_api.zig:80-87 `chpe_get_last_logits`: copies vocab_size floats of the last step;
+ * returns vocab_size, or 0 if ctx/out is NULL or max_len < vocab_size. */
+size_t chpe_get_last_logits(void *ctx, float *out_logits, size_t max_len);
+
+size_t chpe_get_vocab_size(void *ctx);   /* chpe_c_api.zig:89-93 */
+size_t chpe_get_hidden_dim(void *ctx);   /* chpe_c_api.zig:95-99 */
+size_t chpe_get_num_layers(void *ctx);   /* chpe_c_api.zig:101-105 */
+uint64_t chpe_get_last_elapsed_ns(void *ctx);   /* chpe_c_api.zig:107-111 */
+uint32_t chpe_get_last_argmax(void *ctx);       /* chpe_c_api.zig:113-117 */
+float chpe_get_last_max_logit(void *ctx);       /* chpe_c_api.zig:119-123 */
+float chpe_get_last_token0_logit(void *ctx);    /* chpe_c_api.zig:125-129 */
+float chpe_get_last_hidden_norm(void *ctx);     /* chpe_c_api.zig:131-135 */
+
+/* chpe_c_api.zig:137-143 `chpe_free`: releases the engine, its device memory and the map. */
+void chpe_free(void *ctx);
+
+/* ---------------- additions (no counterpart in the reference) ---------------- */
+
+/* chpe_init with an explicit architecture (0 = Qwen2.5-3B, 1 = Qwen3.5-9B,
+ * 2 = Qwen2.5-72B, -1 = guess from the path), max_seq_len and KV-cache type
+ * (kv_f16 != 0: fp16 KV cache in HBM; 0: f32 as the reference). */
+void *chpe_init_ex(const char *archive_path, int arch, size_t max_seq_len, int kv_f16);
+
+/* One forwardDecode(token, pos) (src/chpe_engine.zig:1663) on the context's current KV
+ * cache.  Returns the argmax, -1 bad args, -2 pos >= max_seq_len, -3 device error. */
+int chpe_decode_step(void *ctx, uint32_t token, size_t pos, float *out_logits);
+
+/* Teacher-forced prompt (positions 0..n_prompt-1), then n_gen greedy tokens with the argmax
+ * fed back on the device (n_prompt + n_gen - 1 steps).  out_tokens[n_gen].  Returns 0,
+ * -1 bad args, -2 too long for max_seq_len, -3 device error. */
+int chpe_generate(void *ctx, const uint32_t *prompt, size_t n_prompt, size_t n_gen,
+                  uint32_t *out_tokens);
+
+/* Message of the last failed chpe_init / chpe_init_ex on this thread ("" if none). */
+const char *chpe_last_error(void);
+
+size_t chpe_get_max_seq_len(void *ctx);
+/* hidden_dim floats of the residual stream after the last step. */
+int chpe_get_hidden(void *ctx, float *out);
+
+/* Timing: enqueue `n` decode steps that continue from the device state (greedy feedback),
+ * bracketed by HIP events on the engine's stream; *ms = elapsed milliseconds. */
+int chpe_time_steps(void *ctx, size_t n, float *ms);
+/* Launch one projection stage alone (0 q/k/v, 1 o, 2 gate+up, 3 down, 4 LM head) for each
+ * layer in [layer0, layer1), `iters` times, between HIP events; *ms = total. */
+int chpe_time_stage(void *ctx, int stage, size_t layer0, size_t layer1, size_t iters, float *ms);
+/* Algorithmic HBM bytes: of one stage launch for `layer`, and of a whole step at `pos`. */
+double chpe_stage_bytes(void *ctx, int stage, size_t layer);
+double chpe_step_bytes(void *ctx, size_t pos);
+
+/* Parity hooks: one projection's GEMV on a caller vector (which: 0 q, 1 k, 2 v, 3 o,
+ * 4 gate, 5 up, 6 down, 7 LM head), bias included, no norm; y gets the output rows. */
+int chpe_debug_gemv(void *ctx, size_t layer, int which, const float *x, float *y);
+/* Materialised weights of one flat 32768-weight tile (gemvCellFlat's dequantisation),
+ * computed by the GPU from the 17408-byte cell. */
+int chpe_debug_flat_tile_weights(const uint8_t *cell, float *out32768);
+/* unpackEmbedRowCell on the GPU over `len` bytes starting at a cell (rows of wide tensors
+ * read past the cell).  Returns 1 if written, 0 if the row is out of range, <0 on error. */
+int chpe_debug_embed_row_cell(const uint8_t *bytes, size_t len, uint32_t row, uint32_t D,
+                              float *out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif
