@@ -191,7 +191,7 @@ int chpe_time_steps(void* ctx, size_t n, float* ms) {
 }
 
 int chpe_time_stage(void* ctx, int stage, size_t layer0, size_t layer1, size_t iters, float* ms) {
-  if (!ctx || !ms || stage < 0 || stage > 4) return -1;
+  if (!ctx || !ms || stage < 0 || stage > 5) return -1;
   Context* c = C(ctx);
   Engine& e = *c->engine;
   if (layer1 > e.arch().num_layers || layer0 >= layer1) return -1;

@@ -1,0 +1,132 @@
+// device_common.hpp -- device helpers shared by the gfx950 kernels.
+#pragma once
+#include <hip/hip_fp16.h>
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace chpe {
+namespace dev {
+
+constexpr int kWave = 64;
+
+__device__ __forceinline__ float h2f(uint16_t h) { return __half2float(__ushort_as_half(h)); }
+__device__ __forceinline__ float bf2f(uint16_t h) { return __uint_as_float(uint32_t(h) << 16); }
+__device__ __forceinline__ uint16_t ld_u16(const uint8_t* p) { return *reinterpret_cast<const uint16_t*>(p); }
+__device__ __forceinline__ uint4 ld_u128(const uint8_t* p) { return *reinterpret_cast<const uint4*>(p); }
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  return v;
+}
+
+// Reduce N per-lane partials (one per row) over the wave with a reduce-scatter: after the
+// call, lane l holds the total of row l / (64/N) in v[0].  N in {4, 8, 16}.
+template <int N>
+__device__ __forceinline__ float wave_reduce_rows(float (&v)[N], int lane) {
+  int mask = 32;
+#pragma unroll
+  for (int n = N; n > 1; n >>= 1) {
+    const bool up = lane & mask;
+#pragma unroll
+    for (int j = 0; j < n / 2; ++j) {
+      const float keep = up ? v[n / 2 + j] : v[j];
+      const float send = up ? v[j] : v[n / 2 + j];
+      v[j] = keep + __shfl_xor(send, mask);
+    }
+    mask >>= 1;
+  }
+  float s = v[0];
+  for (; mask > 0; mask >>= 1) s += __shfl_xor(s, mask);
+  return s;
+}
+
+// fp16 halves of a 32-bit word, widened (the widening folds into v_fma_mix_f32's op_sel)
+__device__ __forceinline__ float half_lo(uint32_t w) {
+  return float(__builtin_bit_cast(_Float16, static_cast<unsigned short>(w & 0xffffu)));
+}
+__device__ __forceinline__ float half_hi(uint32_t w) {
+  return float(__builtin_bit_cast(_Float16, static_cast<unsigned short>(w >> 16)));
+}
+
+// sum over 32 4-bit codes (byte k: low nibble = column 2k, high nibble = column 2k+1) * x.
+// A nibble masked in place inside a 16-bit half is an fp16 subnormal: bits 0-3 hold n*2^-24,
+// bits 4-7 hold n*2^-20, both exact.  v_fma_mix_f32 widens such a half exactly and fuses the
+// multiply-add with the f32 x, so 8 weights cost 4 masks + 1 shift + 8 fused ops; the two
+// accumulators are rescaled by 2^24 and 2^20 (exact) at the end.
+__device__ __forceinline__ float dot32_w4(uint4 q, const float* x) {
+  const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+  float a = 0.0f, b = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t m0 = w[i] & 0x000F000Fu, m1 = w[i] & 0x00F000F0u, w8 = w[i] >> 8;
+    const uint32_t m2 = w8 & 0x000F000Fu, m3 = w8 & 0x00F000F0u;
+    const float* xi = x + 8 * i;  // columns 8i..8i+7: byte k holds columns 2k, 2k+1
+    a = fmaf(half_lo(m0), xi[0], a);
+    a = fmaf(half_hi(m0), xi[4], a);
+    b = fmaf(half_lo(m1), xi[1], b);
+    b = fmaf(half_hi(m1), xi[5], b);
+    a = fmaf(half_lo(m2), xi[2], a);
+    a = fmaf(half_hi(m2), xi[6], a);
+    b = fmaf(half_lo(m3), xi[3], b);
+    b = fmaf(half_hi(m3), xi[7], b);
+  }
+  return a * 16777216.0f + b * 1048576.0f;
+}
+
+// sum over 64 2-bit codes of (code ^ 2) * x.  The codebook {0:0, 1:+1, 2:-2, 3:-1}
+// (chpe_engine.zig:220) equals (code ^ 2) - 2, so the -2 is applied once per chunk.
+__device__ __forceinline__ float dot64_w2(uint4 q, const float* x) {
+  const uint32_t w[4] = {q.x ^ 0xAAAAAAAAu, q.y ^ 0xAAAAAAAAu, q.z ^ 0xAAAAAAAAu, q.w ^ 0xAAAAAAAAu};
+  float a0 = 0.0f, a1 = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {  // code k of each byte: column 4*byte + k
+      const uint32_t c = (w[i] >> (2 * k)) & 0x03030303u;
+      a0 = fmaf(float(c & 0xffu), x[16 * i + 0 + k], a0);
+      a1 = fmaf(float((c >> 8) & 0xffu), x[16 * i + 4 + k], a1);
+      a0 = fmaf(float((c >> 16) & 0xffu), x[16 * i + 8 + k], a0);
+      a1 = fmaf(float(c >> 24), x[16 * i + 12 + k], a1);
+    }
+  }
+  return a0 + a1;
+}
+
+__device__ __forceinline__ float dot8_f16(uint4 q, const float* x, bool bf16) {
+  const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+  float a = 0.0f, b = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint16_t lo = uint16_t(w[i] & 0xffffu), hi = uint16_t(w[i] >> 16);
+    a = fmaf(bf16 ? bf2f(lo) : h2f(lo), x[2 * i], a);
+    b = fmaf(bf16 ? bf2f(hi) : h2f(hi), x[2 * i + 1], b);
+  }
+  return a + b;
+}
+
+__device__ __forceinline__ float codebook_w2(uint32_t c) {  // chpe_engine.zig:220
+  return c == 0 ? 0.0f : (c == 1 ? 1.0f : (c == 2 ? -2.0f : -1.0f));
+}
+
+// (value, index) order of the reference's argmax scan (chpe_engine.zig:1775-1787): the
+// greatest value, first index among equals; 0xffffffff marks "no candidate".
+__device__ __forceinline__ bool better(float v, uint32_t i, float bv, uint32_t bi) {
+  return i != 0xffffffffu && (bi == 0xffffffffu || v > bv || (v == bv && i < bi));
+}
+
+// Byte reads of the archive image bounded by its length: some reference reads run past the
+// end of a cell into the following records, exactly as here; reads past the image are zero.
+struct Image {
+  const uint8_t* p;
+  uint64_t len;
+  __device__ uint8_t u8(uint64_t off) const { return off < len ? p[off] : 0; }
+  __device__ uint16_t u16(uint64_t off) const { return uint16_t(u8(off) | (u8(off + 1) << 8)); }
+  __device__ uint32_t u32(uint64_t off) const { return u16(off) | (uint32_t(u16(off + 2)) << 16); }
+  __device__ uint64_t u64(uint64_t off) const { return u32(off) | (uint64_t(u32(off + 4)) << 32); }
+  __device__ float f32(uint64_t off) const { return __uint_as_float(u32(off)); }
+};
+
+}  // namespace dev
+}  // namespace chpe

@@ -10,6 +10,7 @@
 #include <algorithm>
 #include <chrono>
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
 #include <map>
 
@@ -214,9 +215,7 @@ bool Engine::init(const uint8_t* b, size_t len, const EngineConfig& cfg, std::st
   d_vcache_ = dev_alloc(kv_bytes);
   d_part_ml_ = static_cast<float*>(dev_alloc(arch_.num_attn_heads * n_chunks_ * 2 * 4));
   d_part_acc_ = static_cast<float*>(dev_alloc(arch_.num_attn_heads * n_chunks_ * hd * 4));
-  d_attn_counter_ = static_cast<uint32_t*>(dev_alloc(arch_.num_kv_heads * 4));
-  d_lm_counter_ = static_cast<uint32_t*>(dev_alloc(4));
-  d_partials_ = static_cast<ArgmaxPartial*>(dev_alloc(((V + 15) / 16) * sizeof(ArgmaxPartial)));
+  d_partials_ = static_cast<ArgmaxPartial*>(dev_alloc(kMaxLogitsBlocks * sizeof(ArgmaxPartial)));
   d_result_ = static_cast<StepResult*>(dev_alloc(sizeof(StepResult)));
   d_state_ = static_cast<StepState*>(dev_alloc(sizeof(StepState)));
   d_prompt_ = static_cast<uint32_t*>(dev_alloc(S * 4));
@@ -228,8 +227,7 @@ bool Engine::init(const uint8_t* b, size_t len, const EngineConfig& cfg, std::st
   HIP_TRY(hipMemset(d_hidden_, 0, D * 4));
   HIP_TRY(hipMemset(d_kcache_, 0, kv_bytes));
   HIP_TRY(hipMemset(d_vcache_, 0, kv_bytes));
-  HIP_TRY(hipMemset(d_attn_counter_, 0, arch_.num_kv_heads * 4));
-  HIP_TRY(hipMemset(d_lm_counter_, 0, 4));
+  HIP_TRY(hipMemset(d_logits_, 0, V * 4));
   HIP_TRY(hipMemset(d_result_, 0, sizeof(StepResult)));
   HIP_TRY(hipMemset(d_state_, 0, sizeof(StepState)));
   // RoPE angles exactly as applyRope computes them (src/chpe_engine.zig:197-206), in f32
@@ -250,12 +248,23 @@ bool Engine::init(const uint8_t* b, size_t len, const EngineConfig& cfg, std::st
   HIP_TRY(hipHostMalloc(reinterpret_cast<void**>(&h_result_), sizeof(StepResult), hipHostMallocDefault));
   HIP_TRY(hipDeviceSynchronize());
 
-  // ---- capture the step
-  HIP_TRY(hipStreamBeginCapture(stream_, hipStreamCaptureModeThreadLocal));
-  record_step(stream_);
-  HIP_TRY(hipStreamEndCapture(stream_, &graph_));
-  HIP_TRY(hipGraphInstantiate(&graph_exec_, graph_, nullptr, nullptr, 0));
+  // ---- capture the step (CHPE_GRAPH=0 launches the same kernels directly on the stream,
+  // which some profilers need)
+  const char* g = std::getenv("CHPE_GRAPH");
+  use_graph_ = !(g && g[0] == '0');
+  if (use_graph_) {
+    HIP_TRY(hipStreamBeginCapture(stream_, hipStreamCaptureModeThreadLocal));
+    record_step(stream_);
+    HIP_TRY(hipStreamEndCapture(stream_, &graph_));
+    HIP_TRY(hipGraphInstantiate(&graph_exec_, graph_, nullptr, nullptr, 0));
+  }
   return true;
+}
+
+int Engine::launch_one() {
+  if (use_graph_) return hipGraphLaunch(graph_exec_, stream_) == hipSuccess ? 0 : -3;
+  record_step(stream_);
+  return hipGetLastError() == hipSuccess ? 0 : -3;
 }
 
 bool Engine::plan_projection(size_t tile_start, size_t num_tiles, size_t r_total, size_t c_total,
@@ -406,6 +415,33 @@ bool Engine::plan_lm_head(std::string* err) {
         return false;
       }
     }
+    // replace-mode outliers (unpackEmbedRowCell :1369-1378): per cell, entry k sets column
+    // col[k] of row n to w_out[n][k]; entries apply in order, so only the last one for a
+    // column counts.  Prepared as additive corrections to the dequantised code.
+    std::vector<CellReplace> repl(n_cells);
+    for (size_t t = 0; t < n_cells; ++t) {
+      const size_t cell = 4096 + t * stride_ + cell_off, pl = cell + kPayloadOff;
+      CellReplace& R = repl[t];
+      for (int k = 0; k < 8; ++k) R.col[k] = rd<uint16_t>(host_bytes_, len_, pl + kRowOutlierCols + 2 * k);
+      for (int k = 0; k < 8; ++k) {
+        bool live = R.col[k] < D;
+        for (int k2 = k + 1; k2 < 8; ++k2) live = live && R.col[k2] != R.col[k];
+        for (int n = 0; n < 16; ++n) {
+          R.delta[n][k] = 0.0f;
+          if (!live) continue;
+          const uint32_t col = R.col[k];
+          const float w = f16_to_f32(rd<uint16_t>(host_bytes_, len_, pl + kRowOutlierW + 2 * (n * 8 + k)));
+          const uint8_t byte = host_bytes_[cell + kBytecodeHeader + n * (D / 2) + col / 2];
+          const float q = float((byte >> (4 * (col & 1))) & 15) - 8.0f;
+          const float s = f16_to_f32(rd<uint16_t>(host_bytes_, len_, pl + kGroupScales + 2 * (n * (D / 128) + col / 128)));
+          R.delta[n][k] = w - q * s;
+        }
+        if (!live) R.col[k] = 0;
+      }
+    }
+    lm_head_.repl = static_cast<CellReplace*>(dev_alloc(n_cells * sizeof(CellReplace)));
+    if (!lm_head_.repl) { *err = "allocation"; return false; }
+    (void)hipMemcpy(lm_head_.repl, repl.data(), n_cells * sizeof(CellReplace), hipMemcpyHostToDevice);
     lm_head_.kind = WeightKind::Cell16W4;
     lm_head_.base = d_image_ + 4096 + cell_off;
     lm_head_.stride = uint32_t(stride_);
@@ -427,40 +463,40 @@ bool Engine::plan_lm_head(std::string* err) {
   return true;
 }
 
-void Engine::enqueue_gemv(const ProjPlan* parts[], int n, GemvMode mode, const float* x, uint32_t C,
-                          const float* gamma, float* y_override, hipStream_t st) {
+uint32_t Engine::enqueue_gemv(const ProjPlan* const* parts, float* const* outs, int n, GemvMode mode,
+                              const float* x, uint32_t C, const float* gamma, hipStream_t st) {
   GemvArgs a{};
   a.n_parts = n;
   a.mode = int(mode);
   a.C = C;
-  a.rows_per_block = gemv_rows_per_block(parts[0]->kind);
   a.x = x;
   a.gamma = gamma;
   a.eps = arch_.rms_eps;
-  uint32_t blocks = 0;
+  uint32_t rows[kMaxParts] = {0, 0, 0}, begin[kMaxParts] = {0, 0, 0};
+  for (int i = 0; i < n; ++i) rows[i] = parts[i]->rows;
+  const GemvLaunch g = gemv_geometry(parts[0]->kind, mode, C, rows, n, &a.n_units, &a.n_panels,
+                                     &a.waves_per_unit, begin);
   for (int i = 0; i < n; ++i) {
     const ProjPlan& p = *parts[i];
-    GemvPart& g = a.part[i];
-    g.base = p.base;
-    g.stride = p.stride;
-    g.rows = p.rows;
-    g.bf16 = p.bf16;
-    g.bias = p.bias;
-    g.corr_ptr = p.corr_ptr;
-    g.corr = p.corr;
-    g.replace_outliers = p.replace_outliers;
-    g.block_begin = mode == GemvMode::SwiGlu ? 0 : blocks;
-    const uint32_t nb = (p.rows + a.rows_per_block - 1) / a.rows_per_block;
-    blocks = mode == GemvMode::SwiGlu ? nb : blocks + nb;
+    GemvPart& gp = a.part[i];
+    gp.base = p.base;
+    gp.stride = p.stride;
+    gp.rows = p.rows;
+    gp.unit_begin = begin[i];
+    gp.bf16 = p.bf16;
+    gp.y = outs[i];
+    gp.bias = p.bias;
+    gp.corr_ptr = p.corr_ptr;
+    gp.corr = p.corr;
+    gp.replace_outliers = p.replace_outliers;
+    gp.repl = p.repl;
   }
   if (mode == GemvMode::Logits) {
     a.partials = d_partials_;
-    a.counter = d_lm_counter_;
     a.result = d_result_;
-    a.vocab = uint32_t(arch_.vocab_size);
   }
-  for (int i = 0; i < n; ++i) a.part[i].y = y_override;
-  launch_gemv(parts[0]->kind, a, blocks, st);
+  launch_gemv(parts[0]->kind, a, g, st);
+  return g.blocks;
 }
 
 void Engine::enqueue_qkv(const LayerPlan& L, hipStream_t st) {
@@ -468,32 +504,36 @@ void Engine::enqueue_qkv(const LayerPlan& L, hipStream_t st) {
   const uint32_t D = uint32_t(arch_.hidden_dim);
   const ProjPlan* qkv[3] = {&L.q, &L.k, &L.v};
   float* outs[3] = {d_q_, d_k_, d_v_};
-  if (L.q.kind != L.k.kind || L.k.kind != L.v.kind) {
-    for (int i = 0; i < 3; ++i) {
-      const ProjPlan* one[1] = {qkv[i]};
-      enqueue_gemv(one, 1, GemvMode::Store, d_hidden_, D, L.gamma_in, outs[i], st);
-    }
-    return;
+  if (L.q.kind == L.k.kind && L.k.kind == L.v.kind) {
+    enqueue_gemv(qkv, outs, 3, GemvMode::Store, d_hidden_, D, L.gamma_in, st);
+  } else {
+    for (int i = 0; i < 3; ++i) enqueue_gemv(&qkv[i], &outs[i], 1, GemvMode::Store, d_hidden_, D, L.gamma_in, st);
   }
-  GemvArgs a{};
-  a.n_parts = 3;
-  a.mode = int(GemvMode::Store);
-  a.C = D;
-  a.rows_per_block = gemv_rows_per_block(L.q.kind);
-  a.x = d_hidden_;
-  a.gamma = L.gamma_in;
-  a.eps = arch_.rms_eps;
-  uint32_t blocks = 0;
-  for (int i = 0; i < 3; ++i) {
-    const ProjPlan& p = *qkv[i];
-    GemvPart& g = a.part[i];
-    g.base = p.base; g.stride = p.stride; g.rows = p.rows; g.bf16 = p.bf16; g.bias = p.bias;
-    g.corr_ptr = p.corr_ptr; g.corr = p.corr; g.replace_outliers = p.replace_outliers;
-    g.y = outs[i];
-    g.block_begin = blocks;
-    blocks += (p.rows + a.rows_per_block - 1) / a.rows_per_block;
-  }
-  launch_gemv(L.q.kind, a, blocks, st);
+}
+
+AttnArgs Engine::attn_args(size_t l) const {
+  const size_t kvd = arch_.num_kv_heads * arch_.head_dim, S = cfg_.max_seq_len;
+  const size_t kv_elem = cfg_.kv_f16 ? 2 : 4;
+  AttnArgs at{};
+  at.state = d_state_;
+  at.q_raw = d_q_;
+  at.k_raw = d_k_;
+  at.v_raw = d_v_;
+  at.k_cache = static_cast<uint8_t*>(d_kcache_) + l * kvd * S * kv_elem;
+  at.v_cache = static_cast<uint8_t*>(d_vcache_) + l * kvd * S * kv_elem;
+  at.rope_cos = d_rope_cos_;
+  at.rope_sin = d_rope_sin_;
+  at.out = d_attn_;
+  at.part_ml = d_part_ml_;
+  at.part_acc = d_part_acc_;
+  at.H = uint32_t(arch_.num_attn_heads);
+  at.KV = uint32_t(arch_.num_kv_heads);
+  at.hd = uint32_t(arch_.head_dim);
+  at.max_seq = uint32_t(S);
+  at.n_chunks = n_chunks_;
+  at.kv_f16 = cfg_.kv_f16 ? 1 : 0;
+  at.scale = 1.0f / std::sqrt(float(arch_.head_dim));
+  return at;
 }
 
 void Engine::record_step(hipStream_t st) {
@@ -507,46 +547,26 @@ void Engine::record_step(hipStream_t st) {
   e.kind = embed_kind_;
   e.record_count = record_count_;
   e.stride = stride_;
-  e.code_off = is_raw_ ? 0 : (is_dense_ ? 0 : kPrefetchBytes) + kBytecodeHeader;
   e.cell_off = is_dense_ ? 0 : kPrefetchBytes;
   launch_embed(e, st);
-  const size_t kvd = arch_.num_kv_heads * arch_.head_dim, S = cfg_.max_seq_len;
-  const size_t kv_elem = cfg_.kv_f16 ? 2 : 4;
   for (size_t l = 0; l < arch_.num_layers; ++l) {
     const LayerPlan& L = layers_[l];
     enqueue_qkv(L, st);
-    AttnArgs at{};
-    at.state = d_state_;
-    at.q_raw = d_q_;
-    at.k_raw = d_k_;
-    at.v_raw = d_v_;
-    at.k_cache = static_cast<uint8_t*>(d_kcache_) + l * kvd * S * kv_elem;
-    at.v_cache = static_cast<uint8_t*>(d_vcache_) + l * kvd * S * kv_elem;
-    at.rope_cos = d_rope_cos_;
-    at.rope_sin = d_rope_sin_;
-    at.out = d_attn_;
-    at.part_ml = d_part_ml_;
-    at.part_acc = d_part_acc_;
-    at.counter = d_attn_counter_;
-    at.H = uint32_t(arch_.num_attn_heads);
-    at.KV = uint32_t(arch_.num_kv_heads);
-    at.hd = uint32_t(arch_.head_dim);
-    at.max_seq = uint32_t(S);
-    at.n_chunks = n_chunks_;
-    at.kv_f16 = cfg_.kv_f16 ? 1 : 0;
-    at.scale = 1.0f / std::sqrt(float(arch_.head_dim));
-    launch_attention(at, st);
+    launch_attention(attn_args(l), st);
     const ProjPlan* o[1] = {&L.o};
-    enqueue_gemv(o, 1, GemvMode::Accum, d_attn_, D, nullptr, d_hidden_, st);
+    float* hid[2] = {d_hidden_, d_hidden_};
+    enqueue_gemv(o, hid, 1, GemvMode::Accum, d_attn_, D, nullptr, st);
     const ProjPlan* gu[2] = {&L.gate, &L.up};
-    enqueue_gemv(gu, 2, GemvMode::SwiGlu, d_hidden_, D, L.gamma_post, d_mlp_, st);
+    float* mlp[2] = {d_mlp_, d_mlp_};
+    enqueue_gemv(gu, mlp, 2, GemvMode::SwiGlu, d_hidden_, D, L.gamma_post, st);
     const ProjPlan* dn[1] = {&L.down};
-    enqueue_gemv(dn, 1, GemvMode::Accum, d_mlp_, I, nullptr, d_hidden_, st);
+    enqueue_gemv(dn, hid, 1, GemvMode::Accum, d_mlp_, I, nullptr, st);
   }
   const ProjPlan* lm[1] = {&lm_head_};
-  enqueue_gemv(lm, 1, GemvMode::Logits, d_hidden_, D, d_gamma_final_, d_logits_, st);
-  AdvanceArgs adv{d_state_, d_prompt_, d_result_, d_out_tokens_};
-  launch_advance(adv, st);
+  float* lg[1] = {d_logits_};
+  const uint32_t n_partials = enqueue_gemv(lm, lg, 1, GemvMode::Logits, d_hidden_, D, d_gamma_final_, st);
+  FinishArgs f{d_state_, d_prompt_, d_partials_, n_partials, d_logits_, d_result_, d_out_tokens_};
+  launch_finish(f, st);
 }
 
 int Engine::read_result(ForwardResult* out) const {
@@ -564,7 +584,7 @@ int Engine::forward(uint32_t token, size_t pos, ForwardResult* out) {
   const uint64_t t0 = now_ns();
   *h_state_ = StepState{token, uint32_t(pos), 0, 0};
   if (hipMemcpyAsync(d_state_, h_state_, sizeof(StepState), hipMemcpyHostToDevice, stream_) != hipSuccess) return -3;
-  if (hipGraphLaunch(graph_exec_, stream_) != hipSuccess) return -3;
+  if (launch_one()) return -3;
   if (hipMemcpyAsync(h_result_, d_result_, sizeof(StepResult), hipMemcpyDeviceToHost, stream_) != hipSuccess) return -3;
   if (hipStreamSynchronize(stream_) != hipSuccess) return -3;
   const uint64_t t1 = now_ns();
@@ -578,7 +598,7 @@ int Engine::forward(uint32_t token, size_t pos, ForwardResult* out) {
 }
 
 void Engine::launch_steps(size_t n) {
-  for (size_t i = 0; i < n; ++i) (void)hipGraphLaunch(graph_exec_, stream_);
+  for (size_t i = 0; i < n; ++i) (void)launch_one();
 }
 
 int Engine::sync() { return hipStreamSynchronize(stream_) == hipSuccess ? 0 : -3; }
@@ -651,7 +671,16 @@ double Engine::stage_bytes(int stage, size_t l) const {
     case 1: return proj_bytes(L.o);
     case 2: return proj_bytes(L.gate) + proj_bytes(L.up);
     case 3: return proj_bytes(L.down);
-    default: return proj_bytes(lm_head_);
+    case 4: return proj_bytes(lm_head_);
+    case 5: {  // K and V rows 0..pos of this layer at the current device position
+      StepState st{};
+      if (hipStreamSynchronize(stream_) != hipSuccess ||
+          hipMemcpy(&st, d_state_, sizeof(st), hipMemcpyDeviceToHost) != hipSuccess)
+        return 0.0;
+      const double kv_row = double(arch_.num_kv_heads * arch_.head_dim) * (cfg_.kv_f16 ? 2 : 4);
+      return 2.0 * kv_row * (double(st.pos) + 1.0);
+    }
+    default: return 0.0;
   }
 }
 
@@ -676,26 +705,33 @@ int Engine::launch_stage(int stage, size_t l) {
     case 0:
       enqueue_qkv(L, stream_);
       return 0;
-    case 1: {
+    case 1: {  // writes a scratch vector, not the residual stream
       const ProjPlan* o[1] = {&L.o};
-      enqueue_gemv(o, 1, GemvMode::Store, d_attn_, D, nullptr, d_q_, stream_);
+      float* y[1] = {d_q_};
+      enqueue_gemv(o, y, 1, GemvMode::Store, d_attn_, D, nullptr, stream_);
       return 0;
     }
     case 2: {
       const ProjPlan* gu[2] = {&L.gate, &L.up};
-      enqueue_gemv(gu, 2, GemvMode::SwiGlu, d_hidden_, D, L.gamma_post, d_mlp_, stream_);
+      float* y[2] = {d_mlp_, d_mlp_};
+      enqueue_gemv(gu, y, 2, GemvMode::SwiGlu, d_hidden_, D, L.gamma_post, stream_);
       return 0;
     }
     case 3: {
       const ProjPlan* dn[1] = {&L.down};
-      enqueue_gemv(dn, 1, GemvMode::Store, d_mlp_, I, nullptr, d_attn_, stream_);
+      float* y[1] = {d_attn_};
+      enqueue_gemv(dn, y, 1, GemvMode::Store, d_mlp_, I, nullptr, stream_);
       return 0;
     }
     case 4: {
       const ProjPlan* lm[1] = {&lm_head_};
-      enqueue_gemv(lm, 1, GemvMode::Logits, d_hidden_, D, d_gamma_final_, d_logits_, stream_);
+      float* y[1] = {d_logits_};
+      enqueue_gemv(lm, y, 1, GemvMode::Logits, d_hidden_, D, d_gamma_final_, stream_);
       return 0;
     }
+    case 5:
+      launch_attention(attn_args(l), stream_);
+      return 0;
   }
   return -1;
 }
@@ -722,7 +758,8 @@ int Engine::debug_gemv(size_t layer, int which, const float* x, float* y) {
   if (hipMalloc(&dx, C * 4) == hipSuccess && hipMalloc(&dy, R * 4) == hipSuccess &&
       hipMemcpy(dx, x, C * 4, hipMemcpyHostToDevice) == hipSuccess) {
     const ProjPlan* one[1] = {p};
-    enqueue_gemv(one, 1, GemvMode::Store, dx, uint32_t(C), nullptr, dy, stream_);
+    float* ys[1] = {dy};
+    enqueue_gemv(one, ys, 1, GemvMode::Store, dx, uint32_t(C), nullptr, stream_);
     if (sync() == 0 && hipMemcpy(y, dy, R * 4, hipMemcpyDeviceToHost) == hipSuccess) rc = 0;
   }
   if (dx) (void)hipFree(dx);

@@ -55,6 +55,7 @@ struct ProjPlan {
   float* bias = nullptr;               // device, with the reference's non-finite -> 0 rule
   uint32_t* corr_ptr = nullptr;        // device CSR of flat-tile outlier corrections
   float2* corr = nullptr;
+  CellReplace* repl = nullptr;         // device, replace-mode outliers of 16-row cells
 };
 
 struct LayerPlan {
@@ -98,8 +99,8 @@ class Engine {
   const ProjPlan& lm_head() const { return lm_head_; }
   // weight + KV bytes the step reads at position `pos` (the roofline numerator)
   double step_bytes(size_t pos) const;
-  // re-launch one layer's projection kernel alone (measurement): 0 = qkv, 1 = o,
-  // 2 = gate/up, 3 = down, 4 = LM head
+  // re-launch one stage of one layer alone (measurement): 0 = qkv, 1 = o, 2 = gate/up,
+  // 3 = down, 4 = LM head, 5 = attention (at the current position)
   int launch_stage(int stage, size_t layer);
   // bytes one launch of launch_stage(stage, layer) reads from HBM (weights, scales, outliers)
   double stage_bytes(int stage, size_t layer) const;
@@ -115,8 +116,10 @@ class Engine {
   void* dev_alloc(size_t bytes);
   void record_step(hipStream_t st);
   void enqueue_qkv(const LayerPlan& L, hipStream_t st);
-  void enqueue_gemv(const ProjPlan* parts[], int n, GemvMode mode, const float* x, uint32_t C,
-                    const float* gamma, float* y_override, hipStream_t st);
+  // one GEMV launch over n parts (outs[i] receives part i); returns the workgroup count
+  uint32_t enqueue_gemv(const ProjPlan* const* parts, float* const* outs, int n, GemvMode mode,
+                        const float* x, uint32_t C, const float* gamma, hipStream_t st);
+  AttnArgs attn_args(size_t layer) const;
   double proj_bytes(const ProjPlan& p) const;
 
  public:
@@ -146,8 +149,7 @@ class Engine {
         *d_mlp_ = nullptr, *d_logits_ = nullptr;
   void *d_kcache_ = nullptr, *d_vcache_ = nullptr;
   float *d_rope_cos_ = nullptr, *d_rope_sin_ = nullptr, *d_part_ml_ = nullptr, *d_part_acc_ = nullptr;
-  uint32_t *d_attn_counter_ = nullptr, *d_lm_counter_ = nullptr, *d_prompt_ = nullptr,
-           *d_out_tokens_ = nullptr;
+  uint32_t *d_prompt_ = nullptr, *d_out_tokens_ = nullptr;
   ArgmaxPartial* d_partials_ = nullptr;
   StepResult* d_result_ = nullptr;
   StepState* d_state_ = nullptr;
@@ -159,6 +161,8 @@ class Engine {
   hipStream_t stream_ = nullptr;
   hipGraph_t graph_ = nullptr;
   hipGraphExec_t graph_exec_ = nullptr;
+  bool use_graph_ = true;
+  int launch_one();
 };
 
 }  // namespace chpe

@@ -1,13 +1,17 @@
 // kernels.hpp -- argument blocks and launchers of the gfx950 decode kernels.
 //
 // Each kernel is one stage of CHPEEngine.forwardDecode (src/chpe_engine.zig:1663-1803):
-//   embed            unpackEmbedRow                       (:1491-1552, :1288-1394)
-//   gemv_*           gemvLinear / gemvTile* / gemvCellFlat (:1396-1489, :223-729)
-//                    with the RMSNorm that precedes it fused into the prologue
-//                    (rmsNorm :163-193) and the bias / residual / SwiGLU / LM-head argmax
-//                    that follows it fused into the epilogue
-//   attention        RoPE (:195-216) + KV write (:1693-1697) + GQA attention (:1700-1734)
-//   finish           argmax / all_finite / logits[0] / hidden norm (:1775-1803)
+//   embed            unpackEmbedRow                        (:1491-1552, :1288-1394)
+//   gemv             gemvLinear / gemvTile* / gemvCellFlat (:1396-1489, :223-729) with the
+//                    RMSNorm before it (rmsNorm :163-193) applied to x as it is loaded, and
+//                    the bias / residual / SwiGLU / LM-head logits after it in the epilogue
+//   attention        RoPE (:195-216) + KV write (:1693-1697) + GQA attention (:1700-1734),
+//                    split over the context, then merged by a second launch
+//   finish           argmax / all_finite / logits[0] (:1775-1803) and the device-side
+//                    advance to the next position
+// No kernel communicates between workgroups inside one launch: cross-workgroup reductions
+// are separate launches, so no device-scope fence (an L2 write-back + invalidate on this
+// multi-die part) is executed anywhere in the step.
 #pragma once
 #include <hip/hip_runtime.h>
 
@@ -15,35 +19,46 @@
 
 namespace chpe {
 
-// Weight layouts a GEMV launch can read (selected per tensor by the host plan).
+// Weight layouts a GEMV launch reads (chosen per tensor by the host plan).
 enum class WeightKind : int {
   Raw16 = 0,     // raw archive: contiguous row-major fp16 / bf16 matrix (dotSegment)
-  Cell16W4 = 1,  // 16-row cells, 4-bit, GROUP128, rows=16, cols=C (gemvTileW4)
+  Cell16W4 = 1,  // 16-row cells, 4-bit, GROUP128, rows=16, cols=2048 (gemvTileW4)
   FlatW4 = 2,    // flat 32768-weight tiles, 4-bit, GROUP128 (gemvCellFlat)
   FlatW2 = 3,    // flat tiles, 2-bit, GROUP128
 };
 
 enum class GemvMode : int {
   Store = 0,   // y = W x (+ bias)
-  Accum = 1,   // y += W x            (o / down projections into the residual stream)
+  Accum = 1,   // y += W x    (o / down projections into the residual stream)
   SwiGlu = 2,  // y = silu(W0 x) * (W1 x)
-  Logits = 3,  // logits = W x, then the argmax reduction of the whole vocabulary
+  Logits = 3,  // logits = W x, plus per-workgroup argmax partials
 };
 
 constexpr int kMaxParts = 3;
+constexpr uint32_t kMaxWavesPerUnit = 8;
 
 struct GemvPart {
-  const uint8_t* base;       // device address of the tensor's first record (cell start / raw codes)
-  uint32_t stride;           // record stride in bytes
-  uint32_t rows;             // output rows (r_total)
-  uint32_t block_begin;      // first block of this part in the launch grid
-  uint32_t bf16;             // Raw16: 1 = bf16, 0 = fp16
-  float* y;                  // output vector
-  const float* bias;         // per-row bias (Store), may be null
-  const uint32_t* corr_ptr;  // FlatW*: per-row outlier corrections (CSR), may be null
-  const float2* corr;        //   (column as float bits, delta)
-  uint32_t replace_outliers; // Cell16W4: outliers replace (embedding / tied LM head) instead of add
+  const uint8_t* base;        // device address of the tensor's first record
+  uint32_t stride;            // record stride in bytes
+  uint32_t rows;              // output rows (r_total)
+  uint32_t unit_begin;        // first work unit of this part
+  uint32_t bf16;              // Raw16: 1 = bf16, 0 = fp16
+  float* y;                   // output vector
+  const float* bias;          // per-row bias (Store), may be null
+  const uint32_t* corr_ptr;   // Flat: per-row outlier corrections (CSR), may be null
+  const float2* corr;         //   (column as float bits, w_out - dequantised code)
+  uint32_t replace_outliers;  // Cell16W4: outliers replace (tied LM head) instead of add
+  const struct CellReplace* repl;  // Cell16W4 replace mode: per-cell corrections (see below)
 };
+
+// Replace-mode outliers of one 16-row cell, prepared at load time: entry k replaces column
+// col[k] of every row, i.e. adds delta[row][k] = w_out - dequantised code.  Entries that do not
+// apply (column out of range, or overridden by a later entry for the same column) have delta 0.
+struct CellReplace {
+  uint16_t col[8];
+  float delta[16][8];
+};
+static_assert(sizeof(CellReplace) == 528, "");
 
 struct StepResult {  // ForwardResult, src/chpe_engine.zig:803-810 (elapsed measured on the host)
   uint32_t argmax;
@@ -56,7 +71,7 @@ struct StepResult {  // ForwardResult, src/chpe_engine.zig:803-810 (elapsed meas
 
 struct ArgmaxPartial {
   float value;
-  uint32_t index;     // 0xffffffff: no candidate in this block
+  uint32_t index;     // 0xffffffff: no candidate
   uint32_t nonfinite;
   uint32_t pad;
 };
@@ -65,24 +80,26 @@ struct GemvArgs {
   GemvPart part[kMaxParts];
   int n_parts;
   int mode;
-  uint32_t C;              // columns (length of x)
-  uint32_t rows_per_block; // output rows per block (per part in SwiGlu mode)
-  const float* x;          // input vector (f32)
-  const float* gamma;      // RMSNorm gains: x is normalised in the prologue when non-null
+  uint32_t C;                // columns (length of x)
+  uint32_t n_units;          // row tiles (SwiGlu: a tile is RU/2 gate rows + RU/2 up rows)
+  uint32_t n_panels;         // column panels of the layout
+  uint32_t waves_per_unit;   // 1, or the K-split width (then one unit per workgroup)
+  const float* x;            // input vector (f32)
+  const float* gamma;        // RMSNorm gains: x is normalised as it is loaded when non-null
   float eps;
-  // Logits mode
-  ArgmaxPartial* partials;
-  uint32_t* counter;       // zero between launches; the last block resets it
-  StepResult* result;
-  uint32_t vocab;
-  // hidden-norm output (Logits mode: block 0 writes sqrt(sum x^2) of the raw input)
+  ArgmaxPartial* partials;   // Logits: one per workgroup
+  StepResult* result;        // Logits: workgroup 0 stores the hidden norm
+};
+
+struct GemvLaunch {  // launch geometry of one GemvArgs
+  uint32_t blocks, threads, ru;
 };
 
 struct StepState {  // device-resident per-token state read by the captured step
   uint32_t token;
   uint32_t pos;
-  uint32_t n_prompt;   // teacher-forced positions (prompt) for device-side advance
-  uint32_t n_steps;    // steps executed so far by generate()
+  uint32_t n_prompt;   // positions teacher-forced from `prompt`
+  uint32_t n_steps;
 };
 
 struct EmbedArgs {
@@ -94,7 +111,6 @@ struct EmbedArgs {
   int kind;                 // 0 synthetic, 1 raw fp16, 2 raw bf16, 3 raw int8, 4 cell
   uint64_t record_count;
   uint64_t stride;          // record stride
-  uint64_t code_off;        // offset of the code area inside a record
   uint64_t cell_off;        // offset of the cell inside a record
 };
 
@@ -108,31 +124,37 @@ struct AttnArgs {
   const float* rope_cos;    // [max_seq][hd/2]
   const float* rope_sin;
   float* out;               // [H*hd]
-  float* part_ml;           // [H][n_chunks][2] (max, sum)
+  float* part_ml;           // [H][n_chunks][2] (chunk max, chunk sum)
   float* part_acc;          // [H][n_chunks][hd]
-  uint32_t* counter;        // [KV], zero between launches
   uint32_t H, KV, hd, max_seq, n_chunks;
   uint32_t kv_f16;
   float scale;              // 1/sqrt(hd)
 };
 
-struct AdvanceArgs {
+struct FinishArgs {
   StepState* state;
   const uint32_t* prompt;   // teacher-forced tokens
-  const StepResult* result;
+  const ArgmaxPartial* partials;
+  uint32_t n_partials;
+  const float* logits;
+  StepResult* result;
   uint32_t* out_tokens;     // argmax of every step, indexed by position
 };
 
-// launchers (kernels.hip); all enqueue on `stream` and never synchronise
+// Launch geometry: work units, panels and the K-split for a GEMV over `rows[n_parts]` rows of
+// C columns; `ru` rows per unit.
+GemvLaunch gemv_geometry(WeightKind kind, GemvMode mode, uint32_t C, const uint32_t* rows,
+                         int n_parts, uint32_t* n_units, uint32_t* n_panels,
+                         uint32_t* waves_per_unit, uint32_t* unit_begin);
+
+// launchers; all enqueue on `stream` and never synchronise
 void launch_embed(const EmbedArgs& a, hipStream_t stream);
-void launch_gemv(WeightKind kind, const GemvArgs& a, uint32_t n_blocks, hipStream_t stream);
+void launch_gemv(WeightKind kind, const GemvArgs& a, const GemvLaunch& g, hipStream_t stream);
 void launch_attention(const AttnArgs& a, hipStream_t stream);
-void launch_advance(const AdvanceArgs& a, hipStream_t stream);
-size_t gemv_lds_bytes(WeightKind kind, const GemvArgs& a);
-uint32_t gemv_threads(WeightKind kind, GemvMode mode);
-uint32_t gemv_rows_per_block(WeightKind kind);
+void launch_finish(const FinishArgs& a, hipStream_t stream);
 constexpr uint32_t kAttnMaxChunks = 160;  // chunks of 8192/hd positions per attention launch
 inline uint32_t attn_chunk(uint32_t hd) { return 8192u / hd; }
+constexpr uint32_t kMaxLogitsBlocks = 1024;
 
 // test hooks: dequantise / unpack exactly as the reference materialises weights
 void launch_flat_tile_weights(const uint8_t* cell, float* out, hipStream_t stream);

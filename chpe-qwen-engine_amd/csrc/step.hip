@@ -1,0 +1,192 @@
+// step.hip -- per-token kernels around the layer stack: embedding lookup, the final argmax
+// reduction with the device-side advance to the next position, and the dequantisation hooks
+// the parity tests use.
+#include "device_common.hpp"
+#include "kernels.hpp"
+
+namespace chpe {
+namespace {
+using namespace dev;
+
+// unpackEmbedRowCell (chpe_engine.zig:1288-1394) for one row of the cell at byte offset
+// `cell` of the image, workgroup-parallel over columns.  Returns false when the row is out
+// of the cell's range (then `out` is left untouched, as in the reference).  Wide rows
+// (D >= 4096) read past the cell into the following records, by byte address as on the CPU.
+__device__ bool unpack_embed_row_cell(const Image& im, uint64_t cell, uint32_t row, uint32_t D,
+                                      float* out) {
+  const uint64_t codes = cell + 64, pl = cell + 16448;
+  const uint8_t qb = im.u8(pl + 20);
+  const bool g128 = (im.u64(pl + 24) & 1u) != 0;
+  const uint32_t ng = D / 128;
+  const int tid = threadIdx.x, nt = blockDim.x;
+  if (qb == 8) {
+    if (row >= 8) return false;
+    for (uint32_t i = tid; i < ng * 128; i += nt) {
+      const float s = h2f(im.u16(pl + 48 + 2 * (row * ng + i / 128)));
+      out[i] = float(int8_t(im.u8(codes + uint64_t(row) * D + i))) * s;
+    }
+    return true;
+  }
+  if (qb == 2) {
+    if (row >= 16) return false;
+    for (uint32_t i = tid; i < ng * 128; i += nt) {
+      const float s = h2f(im.u16(pl + 48 + 2 * (row * ng + i / 128)));
+      const uint32_t b = im.u8(codes + uint64_t(row) * (D / 4) + i / 4);
+      out[i] = codebook_w2((b >> (2 * (i & 3))) & 3u) * s;
+    }
+  } else if (g128 || qb == 4) {
+    if (row >= 16) return false;
+    for (uint32_t i = tid; i < ng * 128; i += nt) {
+      const float s = h2f(im.u16(pl + 48 + 2 * (row * ng + i / 128)));
+      const uint32_t b = im.u8(codes + uint64_t(row) * (D / 2) + i / 2);
+      out[i] = (float((b >> (4 * (i & 1))) & 15u) - 8.0f) * s;
+    }
+  } else {
+    const float scale = im.f32(pl + 32), bias = im.f32(pl + 36);
+    for (uint32_t i = tid; i < (D / 2) * 2; i += nt) {
+      const uint32_t b = im.u8(codes + uint64_t(row) * (D / 2) + i / 2);
+      const float q = float((b >> (4 * (i & 1))) & 15u);
+      out[i] = __fadd_rn(__fmul_rn(q - 8.0f, scale), bias);
+    }
+    return true;
+  }
+  if (g128) {  // outliers replace, in entry order (the last entry for a column wins)
+    __syncthreads();
+    if (tid == 0)
+      for (int k = 0; k < 8; ++k) {
+        const uint32_t col = im.u16(pl + 816 + 2 * k);
+        if (col < D) out[col] = h2f(im.u16(pl + 560 + 2 * (row * 8 + k)));
+      }
+  }
+  return true;
+}
+
+// unpackEmbedRow: chpe_engine.zig:1491-1552
+__global__ void __launch_bounds__(256) k_embed(EmbedArgs a) {
+  const uint32_t tok = a.state->token, D = a.D;
+  const Image im{a.image, a.image_len};
+  const int tid = threadIdx.x, nt = blockDim.x;
+  bool done = false;
+  if (a.kind == 1 || a.kind == 2 || a.kind == 3) {
+    const uint32_t rpt = (a.kind == 3 ? 16384u : 8192u) / D;
+    if (rpt > 0 && tok / rpt < a.record_count) {
+      const uint64_t base = 4096 + uint64_t(tok / rpt) * 16384;
+      const uint32_t row = tok % rpt;
+      for (uint32_t i = tid; i < D; i += nt) {
+        const uint64_t e = uint64_t(row) * D + i;
+        float v;
+        if (a.kind == 1) v = h2f(im.u16(base + 2 * e));
+        else if (a.kind == 2) v = bf2f(im.u16(base + 2 * e));
+        else v = float(int8_t(im.u8(base + e))) * 0.00373708f;
+        a.hidden[i] = v;
+      }
+      done = true;
+    }
+  } else if (a.kind == 4) {
+    const uint32_t tile = tok / 16, row = tok % 16;
+    if (tile < a.record_count) {
+      unpack_embed_row_cell(im, 4096 + uint64_t(tile) * a.stride + a.cell_off, row, D, a.hidden);
+      done = true;  // an out-of-range row keeps the previous hidden state, as on the CPU
+    }
+  }
+  if (!done)
+    for (uint32_t i = tid; i < D; i += nt) a.hidden[i] = 0.05f * float(int((i + tok) % 17u) - 8);
+}
+
+// argmax / all_finite / logits[0] over the LM head's workgroup partials (chpe_engine.zig:
+// 1775-1787), then the next position's (token, pos): the prompt while it lasts, else the argmax.
+__global__ void __launch_bounds__(256) k_finish(FinishArgs a) {
+  float bv = -1e30f;
+  uint32_t bi = 0xffffffffu, nf = 0;
+  for (uint32_t i = threadIdx.x; i < a.n_partials; i += blockDim.x) {
+    const ArgmaxPartial p = a.partials[i];
+    nf |= p.nonfinite;
+    if (better(p.value, p.index, bv, bi)) { bv = p.value; bi = p.index; }
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const float ov = __shfl_xor(bv, o);
+    const uint32_t oi = __shfl_xor(bi, o);
+    nf |= __shfl_xor(nf, o);
+    if (better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
+  }
+  __shared__ float s_v[4];
+  __shared__ uint32_t s_i[4], s_nf[4];
+  const int w = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) { s_v[w] = bv; s_i[w] = bi; s_nf[w] = nf; }
+  __syncthreads();
+  if (threadIdx.x != 0) return;
+  for (int k = 1; k < int(blockDim.x >> 6); ++k) {
+    nf |= s_nf[k];
+    if (better(s_v[k], s_i[k], bv, bi)) { bv = s_v[k]; bi = s_i[k]; }
+  }
+  const uint32_t arg = bi == 0xffffffffu ? 0u : bi;
+  StepResult* r = a.result;
+  r->argmax = arg;
+  r->max_logit = bv;
+  r->token0_logit = a.logits[0];
+  r->all_finite = nf ? 0u : 1u;
+  StepState s = *a.state;
+  if (a.out_tokens) a.out_tokens[s.pos] = arg;
+  const uint32_t next = s.pos + 1;
+  s.token = (a.prompt && next < s.n_prompt) ? a.prompt[next] : arg;
+  s.pos = next;
+  s.n_steps += 1;
+  *a.state = s;
+}
+
+// dequantisation half of gemvCellFlat (chpe_engine.zig:598-699), materialised
+__global__ void k_flat_tile_weights(const uint8_t* cell, float* out) {
+  const Image im{cell, 17408};
+  const uint8_t qb = im.u8(16448 + 20);
+  const bool g128 = (im.u64(16448 + 24) & 1u) != 0;
+  const float scale = im.f32(16448 + 32), bias = im.f32(16448 + 36);
+  for (uint32_t i = threadIdx.x; i < 32768; i += blockDim.x) {
+    float w = 0.0f;
+    if (qb == 4) {
+      const float q = float((im.u8(64 + i / 2) >> (4 * (i & 1))) & 15u) - 8.0f;
+      w = g128 ? q * h2f(im.u16(16448 + 48 + 2 * (i / 128))) : __fadd_rn(__fmul_rn(q, scale), bias);
+    } else if (qb == 2) {
+      const float q = codebook_w2((im.u8(64 + i / 4) >> (2 * (i & 3))) & 3u);
+      w = g128 ? q * h2f(im.u16(16448 + 48 + 2 * (i / 128))) : __fadd_rn(__fmul_rn(q, scale), bias);
+    }
+    out[i] = w;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0 && (qb == 4 || qb == 2)) {
+    const uint32_t n = im.u16(16448 + 560);
+    if (n > 0 && n <= 64)
+      for (uint32_t m = 0; m < n; ++m) {
+        const uint32_t off = im.u16(16448 + 690 + 2 * m);
+        if (off < 32768) out[off] = h2f(im.u16(16448 + 562 + 2 * m));
+      }
+  }
+}
+
+__global__ void k_embed_row_cell(const uint8_t* cell, uint64_t len, uint32_t row, uint32_t D,
+                                 float* out, int* written) {
+  const Image im{cell, len};
+  const bool w = unpack_embed_row_cell(im, 0, row, D, out);
+  if (threadIdx.x == 0) *written = w ? 1 : 0;
+}
+
+}  // namespace
+
+void launch_embed(const EmbedArgs& a, hipStream_t st) {
+  hipLaunchKernelGGL(k_embed, dim3(1), dim3(256), 0, st, a);
+}
+
+void launch_finish(const FinishArgs& a, hipStream_t st) {
+  hipLaunchKernelGGL(k_finish, dim3(1), dim3(256), 0, st, a);
+}
+
+void launch_flat_tile_weights(const uint8_t* cell, float* out, hipStream_t st) {
+  hipLaunchKernelGGL(k_flat_tile_weights, dim3(1), dim3(256), 0, st, cell, out);
+}
+
+void launch_embed_row_cell(const uint8_t* cell, uint64_t len, uint32_t row, uint32_t D, float* out,
+                           int* written, hipStream_t st) {
+  hipLaunchKernelGGL(k_embed_row_cell, dim3(1), dim3(256), 0, st, cell, len, row, D, out, written);
+}
+
+}  // namespace chpe

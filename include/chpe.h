@@ -75,7 +75,7 @@ int chpe_get_hidden(void *ctx, float *out);
 /* Timing: enqueue `n` decode steps that continue from the device state (greedy feedback),
  * bracketed by HIP events on the engine's stream; *ms = elapsed milliseconds. */
 int chpe_time_steps(void *ctx, size_t n, float *ms);
-/* Launch one projection stage alone (0 q/k/v, 1 o, 2 gate+up, 3 down, 4 LM head) for each
+/* Launch one stage alone (0 q/k/v, 1 o, 2 gate+up, 3 down, 4 LM head, 5 attention) for each
  * layer in [layer0, layer1), `iters` times, between HIP events; *ms = total. */
 int chpe_time_stage(void *ctx, int stage, size_t layer0, size_t layer1, size_t iters, float *ms);
 /* Algorithmic HBM bytes: of one stage launch for `layer`, and of a whole step at `pos`. */
