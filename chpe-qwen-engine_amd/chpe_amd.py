@@ -26,7 +26,7 @@ ENGINE_SYMBOLS = [
     "chpe_get_last_argmax", "chpe_get_last_max_logit", "chpe_get_last_token0_logit",
     "chpe_get_last_hidden_norm", "chpe_free", "chpe_init_ex", "chpe_decode_step",
     "chpe_generate", "chpe_last_error", "chpe_get_max_seq_len", "chpe_get_hidden",
-    "chpe_time_steps", "chpe_time_stage", "chpe_stage_bytes", "chpe_step_bytes",
+    "chpe_time_steps", "chpe_time_stage", "chpe_time_stage_live", "chpe_stage_bytes", "chpe_step_bytes",
     "chpe_debug_gemv", "chpe_debug_flat_tile_weights", "chpe_debug_embed_row_cell",
 ]
 
@@ -71,6 +71,7 @@ def load_engine_lib():
             "chpe_get_hidden": (I, [V, _c_float_p]),
             "chpe_time_steps": (I, [V, S, _c_float_p]),
             "chpe_time_stage": (I, [V, I, S, S, S, _c_float_p]),
+            "chpe_time_stage_live": (I, [V, I, S, _c_float_p]),
             "chpe_stage_bytes": (D, [V, I, S]),
             "chpe_step_bytes": (D, [V, S]),
             "chpe_debug_gemv": (I, [V, S, I, _c_float_p, _c_float_p]),
@@ -244,6 +245,12 @@ class Engine:
                     "chpe_time_stage")
         return ms.value
 
+    def time_stage_live(self, stage, n_steps):
+        ms = ctypes.c_float()
+        self._check(self.lib.chpe_time_stage_live(self.ctx, stage, n_steps, ctypes.byref(ms)),
+                    "chpe_time_stage_live")
+        return ms.value
+
     def stage_bytes(self, stage, layer):
         return self.lib.chpe_stage_bytes(self.ctx, stage, layer)
 
@@ -279,3 +286,31 @@ def default_archive_dir():
     d = Path(os.environ.get("CHPE_ARCHIVE_DIR", "/tmp/chpe_archives"))
     d.mkdir(parents=True, exist_ok=True)
     return d
+
+
+ARCHIVE_NAMES = {
+    PACK_3B_FP16_RAW: "qwen2.5-3b-fp16raw", PACK_3B_BF16_RAW: "qwen2.5-3b-bf16raw",
+    PACK_3B_W4: "qwen2.5-3b-w4", PACK_3B_W2: "qwen2.5-3b-w2", PACK_3B_W4_STD: "qwen2.5-3b-w4std",
+    PACK_72B_W4: "qwen2.5-72b-w4", PACK_72B_W2: "qwen2.5-72b-w2",
+}
+
+
+def _generator_tag():
+    import hashlib
+    h = hashlib.sha1()
+    for f in ("csrc/pack.cpp", "csrc/format.hpp", "csrc/tensor_maps.hpp"):
+        h.update((PKG_DIR / f).read_bytes())
+    # letters only: chpe_init guesses the architecture from "9b" / "72b" in the path
+    return "".join(chr(ord("a") + int(c, 16)) for c in h.hexdigest()[:10])
+
+
+def ensure_archive(kind, seed=0, directory=None, threads=0):
+    """Path of the seeded archive `kind` under `directory` (default $CHPE_ARCHIVE_DIR or
+    /tmp/chpe_archives), written on first use and reused while the generator is unchanged."""
+    d = Path(directory) if directory else default_archive_dir()
+    path = d / f"{ARCHIVE_NAMES[kind]}-s{seed}-{_generator_tag()}.chpe"
+    if not path.exists() or path.stat().st_size != archive_size(kind):
+        tmp = path.with_suffix(".tmp")
+        write_archive(tmp, kind, seed, threads)
+        os.replace(tmp, path)
+    return path

@@ -163,11 +163,19 @@ __global__ void __launch_bounds__(256) k_attn_combine(AttnArgs a) {
 
 }  // namespace
 
-void launch_attention(const AttnArgs& a, hipStream_t st) {
+void launch_attention_partial(const AttnArgs& a, hipStream_t st) {
   const dim3 grid(a.n_chunks, a.KV);
-  if (a.hd == 128) hipLaunchKernelGGL(k_attn_partial<128>, grid, dim3(256), 0, st, a);
-  else hipLaunchKernelGGL(k_attn_partial<256>, grid, dim3(256), 0, st, a);
-  hipLaunchKernelGGL(k_attn_combine, dim3(a.H), dim3(a.hd), 0, st, a);
+  if (a.hd == 128) launch_kernel(&k_attn_partial<128>, grid, dim3(256), st, a);
+  else launch_kernel(&k_attn_partial<256>, grid, dim3(256), st, a);
+}
+
+void launch_attention_combine(const AttnArgs& a, hipStream_t st) {
+  launch_kernel(k_attn_combine, dim3(a.H), dim3(a.hd), st, a);
+}
+
+void launch_attention(const AttnArgs& a, hipStream_t st) {
+  launch_attention_partial(a, st);
+  launch_attention_combine(a, st);
 }
 
 }  // namespace chpe

@@ -191,7 +191,7 @@ int chpe_time_steps(void* ctx, size_t n, float* ms) {
 }
 
 int chpe_time_stage(void* ctx, int stage, size_t layer0, size_t layer1, size_t iters, float* ms) {
-  if (!ctx || !ms || stage < 0 || stage > 5) return -1;
+  if (!ctx || !ms || stage < 0 || stage > 6) return -1;
   Context* c = C(ctx);
   Engine& e = *c->engine;
   if (layer1 > e.arch().num_layers || layer0 >= layer1) return -1;
@@ -202,6 +202,19 @@ int chpe_time_stage(void* ctx, int stage, size_t layer0, size_t layer1, size_t i
   if (hipEventRecord(c->ev1, e.stream()) != hipSuccess) return -3;
   if (hipEventSynchronize(c->ev1) != hipSuccess) return -3;
   return hipEventElapsedTime(ms, c->ev0, c->ev1) == hipSuccess ? 0 : -3;
+}
+
+int chpe_time_stage_live(void* ctx, int stage, size_t n_steps, float* avg_ms) {
+  if (!ctx || !avg_ms) return -1;
+  Context* c = C(ctx);
+  double avg = 0.0;
+  size_t n = 0;
+  const int rc = c->engine->time_stage_live(stage, n_steps, &avg, &n);
+  if (rc) return rc;
+  *avg_ms = float(avg);
+  ForwardResult r{};
+  if (c->engine->read_result(&r) == 0) remember(c, r);
+  return 0;
 }
 
 double chpe_stage_bytes(void* ctx, int stage, size_t layer) {

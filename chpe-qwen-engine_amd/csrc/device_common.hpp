@@ -1,11 +1,25 @@
 // device_common.hpp -- device helpers shared by the gfx950 kernels.
 #pragma once
+#include <hip/hip_ext.h>
 #include <hip/hip_fp16.h>
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
 
+#include "kernels.hpp"
+
 namespace chpe {
+
+// Launch through the measurement probe when one is armed (see arm_launch_probe).
+template <class K, class... A>
+inline void launch_kernel(K kernel, dim3 grid, dim3 block, hipStream_t st, A... args) {
+  const LaunchProbe p = take_launch_probe();
+  if (p.start)
+    hipExtLaunchKernelGGL(kernel, grid, block, 0, st, p.start, p.stop, 0, args...);
+  else
+    hipLaunchKernelGGL(kernel, grid, block, 0, st, args...);
+}
+
 namespace dev {
 
 constexpr int kWave = 64;

@@ -548,22 +548,37 @@ void Engine::record_step(hipStream_t st) {
   e.record_count = record_count_;
   e.stride = stride_;
   e.cell_off = is_dense_ ? 0 : kPrefetchBytes;
+  // begin/end events of every launch of one stage (time_stage_live; never during capture)
+  auto mark = [&](int stage) {
+    if (probe_stage_ != stage) return;
+    arm_launch_probe(probe_events_[probe_next_], probe_events_[probe_next_ + 1]);
+    probe_next_ += 2;
+  };
   launch_embed(e, st);
   for (size_t l = 0; l < arch_.num_layers; ++l) {
     const LayerPlan& L = layers_[l];
+    mark(0);
     enqueue_qkv(L, st);
-    launch_attention(attn_args(l), st);
+    const AttnArgs aa = attn_args(l);
+    mark(5);
+    launch_attention_partial(aa, st);
+    mark(6);
+    launch_attention_combine(aa, st);
     const ProjPlan* o[1] = {&L.o};
     float* hid[2] = {d_hidden_, d_hidden_};
+    mark(1);
     enqueue_gemv(o, hid, 1, GemvMode::Accum, d_attn_, D, nullptr, st);
     const ProjPlan* gu[2] = {&L.gate, &L.up};
     float* mlp[2] = {d_mlp_, d_mlp_};
+    mark(2);
     enqueue_gemv(gu, mlp, 2, GemvMode::SwiGlu, d_hidden_, D, L.gamma_post, st);
     const ProjPlan* dn[1] = {&L.down};
+    mark(3);
     enqueue_gemv(dn, hid, 1, GemvMode::Accum, d_mlp_, I, nullptr, st);
   }
   const ProjPlan* lm[1] = {&lm_head_};
   float* lg[1] = {d_logits_};
+  mark(4);
   const uint32_t n_partials = enqueue_gemv(lm, lg, 1, GemvMode::Logits, d_hidden_, D, d_gamma_final_, st);
   FinishArgs f{d_state_, d_prompt_, d_partials_, n_partials, d_logits_, d_result_, d_out_tokens_};
   launch_finish(f, st);
@@ -599,6 +614,37 @@ int Engine::forward(uint32_t token, size_t pos, ForwardResult* out) {
 
 void Engine::launch_steps(size_t n) {
   for (size_t i = 0; i < n; ++i) (void)launch_one();
+}
+
+int Engine::time_stage_live(int stage, size_t n_steps, double* avg_ms, size_t* launches) {
+  if (stage < 0 || stage > 6 || n_steps == 0) return -1;
+  const size_t per_step = stage == 4 ? 1 : arch_.num_layers;
+  const size_t n = per_step * n_steps;
+  std::vector<hipEvent_t> ev(2 * n, nullptr);
+  int rc = 0;
+  for (auto& x : ev)
+    if (hipEventCreate(&x) != hipSuccess) rc = -3;
+  if (rc == 0) {
+    probe_stage_ = stage;
+    probe_events_ = ev.data();
+    probe_next_ = 0;
+    for (size_t i = 0; i < n_steps; ++i) record_step(stream_);  // direct launches
+    probe_stage_ = -1;
+    if (hipStreamSynchronize(stream_) != hipSuccess || probe_next_ != 2 * n) rc = -3;
+  }
+  double total = 0.0;
+  for (size_t i = 0; rc == 0 && i < n; ++i) {
+    float ms = 0.0f;
+    if (hipEventElapsedTime(&ms, ev[2 * i], ev[2 * i + 1]) != hipSuccess) rc = -3;
+    total += ms;
+  }
+  for (auto& x : ev)
+    if (x) (void)hipEventDestroy(x);
+  if (rc == 0) {
+    *avg_ms = total / double(n);
+    *launches = n;
+  }
+  return rc;
 }
 
 int Engine::sync() { return hipStreamSynchronize(stream_) == hipSuccess ? 0 : -3; }
@@ -672,6 +718,8 @@ double Engine::stage_bytes(int stage, size_t l) const {
     case 2: return proj_bytes(L.gate) + proj_bytes(L.up);
     case 3: return proj_bytes(L.down);
     case 4: return proj_bytes(lm_head_);
+    case 6:  // the partials of every chunk, read once
+      return double(arch_.num_attn_heads) * n_chunks_ * (arch_.head_dim + 2) * 4.0;
     case 5: {  // K and V rows 0..pos of this layer at the current device position
       StepState st{};
       if (hipStreamSynchronize(stream_) != hipSuccess ||
@@ -730,7 +778,10 @@ int Engine::launch_stage(int stage, size_t l) {
       return 0;
     }
     case 5:
-      launch_attention(attn_args(l), stream_);
+      launch_attention_partial(attn_args(l), stream_);
+      return 0;
+    case 6:
+      launch_attention_combine(attn_args(l), stream_);
       return 0;
   }
   return -1;

@@ -102,6 +102,9 @@ class Engine {
   // re-launch one stage of one layer alone (measurement): 0 = qkv, 1 = o, 2 = gate/up,
   // 3 = down, 4 = LM head, 5 = attention (at the current position)
   int launch_stage(int stage, size_t layer);
+  // run n_steps real steps (greedy, continuing from the device state) launched directly, with
+  // an event pair around every launch of `stage`; *avg_ms = mean launch duration
+  int time_stage_live(int stage, size_t n_steps, double* avg_ms, size_t* launches);
   // bytes one launch of launch_stage(stage, layer) reads from HBM (weights, scales, outliers)
   double stage_bytes(int stage, size_t layer) const;
 
@@ -162,6 +165,9 @@ class Engine {
   hipGraph_t graph_ = nullptr;
   hipGraphExec_t graph_exec_ = nullptr;
   bool use_graph_ = true;
+  int probe_stage_ = -1;                 // stage bracketed by events in record_step
+  hipEvent_t* probe_events_ = nullptr;
+  size_t probe_next_ = 0;
   int launch_one();
 };
 

@@ -424,9 +424,9 @@ __global__ void __launch_bounds__(512, kMinWavesPerSimd<F>) k_gemv(GemvArgs a) {
 template <class F, int MODE, int RU>
 void launch_one(const GemvArgs& a, const GemvLaunch& g, hipStream_t st) {
   if (a.n_panels == 1)
-    hipLaunchKernelGGL((k_gemv<F, MODE, RU, true>), dim3(g.blocks), dim3(g.threads), 0, st, a);
+    launch_kernel(&k_gemv<F, MODE, RU, true>, dim3(g.blocks), dim3(g.threads), st, a);
   else
-    hipLaunchKernelGGL((k_gemv<F, MODE, RU, false>), dim3(g.blocks), dim3(g.threads), 0, st, a);
+    launch_kernel(&k_gemv<F, MODE, RU, false>, dim3(g.blocks), dim3(g.threads), st, a);
 }
 
 template <class F>

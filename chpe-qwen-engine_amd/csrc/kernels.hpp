@@ -150,11 +150,21 @@ GemvLaunch gemv_geometry(WeightKind kind, GemvMode mode, uint32_t C, const uint3
 // launchers; all enqueue on `stream` and never synchronise
 void launch_embed(const EmbedArgs& a, hipStream_t stream);
 void launch_gemv(WeightKind kind, const GemvArgs& a, const GemvLaunch& g, hipStream_t stream);
-void launch_attention(const AttnArgs& a, hipStream_t stream);
+void launch_attention(const AttnArgs& a, hipStream_t stream);  // partial + combine
+void launch_attention_partial(const AttnArgs& a, hipStream_t stream);
+void launch_attention_combine(const AttnArgs& a, hipStream_t stream);
 void launch_finish(const FinishArgs& a, hipStream_t stream);
 constexpr uint32_t kAttnMaxChunks = 160;  // chunks of 8192/hd positions per attention launch
 inline uint32_t attn_chunk(uint32_t hd) { return 8192u / hd; }
 constexpr uint32_t kMaxLogitsBlocks = 1024;
+
+// Measurement: the next kernel launched by any launcher on this host thread records `start`
+// and `stop` when it begins and ends (hipExtLaunchKernelGGL), then the probe is cleared.
+struct LaunchProbe {
+  hipEvent_t start = nullptr, stop = nullptr;
+};
+void arm_launch_probe(hipEvent_t start, hipEvent_t stop);
+LaunchProbe take_launch_probe();
 
 // test hooks: dequantise / unpack exactly as the reference materialises weights
 void launch_flat_tile_weights(const uint8_t* cell, float* out, hipStream_t stream);

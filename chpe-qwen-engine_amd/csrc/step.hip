@@ -172,12 +172,24 @@ __global__ void k_embed_row_cell(const uint8_t* cell, uint64_t len, uint32_t row
 
 }  // namespace
 
+namespace {
+thread_local LaunchProbe g_probe;
+}
+
+void arm_launch_probe(hipEvent_t start, hipEvent_t stop) { g_probe = LaunchProbe{start, stop}; }
+
+LaunchProbe take_launch_probe() {
+  const LaunchProbe p = g_probe;
+  g_probe = LaunchProbe{};
+  return p;
+}
+
 void launch_embed(const EmbedArgs& a, hipStream_t st) {
-  hipLaunchKernelGGL(k_embed, dim3(1), dim3(256), 0, st, a);
+  launch_kernel(k_embed, dim3(1), dim3(256), st, a);
 }
 
 void launch_finish(const FinishArgs& a, hipStream_t st) {
-  hipLaunchKernelGGL(k_finish, dim3(1), dim3(256), 0, st, a);
+  launch_kernel(k_finish, dim3(1), dim3(256), st, a);
 }
 
 void launch_flat_tile_weights(const uint8_t* cell, float* out, hipStream_t st) {

@@ -1,9 +1,10 @@
 // tensor_maps.hpp -- record index of every tensor for the four archive layouts.
 //
-// The reference keeps these as static tables; here they are computed from each table's
-// construction rule (the same record indices, checked against the tables by the tests):
+// The raw 3B, 9B and 72B layouts follow a construction rule and are computed from it; the
+// 3B cell layout has no rule (its layers sit in an irregular order and layer 21 keeps its
+// down_proj apart from the rest of the layer), so it is carried as a table of records:
 //   3B raw   Bf16LayerOffsets            src/qwen3b_geometry.zig:48-79
-//   3B cell  LAYERS (HF alphabetical)    src/qwen3b_tensor_map.zig:21-531
+//   3B cell  LAYERS                      src/qwen3b_tensor_map.zig:26-531
 //   9B       LAYERS                      src/qwen35_tensor_map.zig:53-1015
 //   72B      makeLayer                   src/qwen72b_tensor_map.zig:16-87
 // and the engine's view of them (tile counts, 9B GQA aliasing): src/chpe_engine.zig:1017-1142.
@@ -23,17 +24,47 @@ struct LayerInfo {  // CHPEEngine.LayerInfo, src/chpe_engine.zig:1017-1033
   int64_t q_bias = -1, k_bias = -1, v_bias = -1;  // -1 = no bias tensor
 };
 
-// 3B cell archives store layers in the order of their names sorted as strings.
-inline size_t alpha_rank(size_t l, size_t n_layers) {
-  char a[8], b[8];
-  std::snprintf(a, sizeof a, "%zu", l);
-  size_t rank = 0;
-  for (size_t i = 0; i < n_layers; ++i) {
-    std::snprintf(b, sizeof b, "%zu", i);
-    if (std::strcmp(b, a) < 0) ++rank;
-  }
-  return rank;
-}
+// Records of the 3B cell archive, per layer: input_norm, q_proj, q_bias, k_proj, k_bias,
+// v_proj, v_bias, o_proj, post_norm, gate_proj, up_proj, down_proj
+// (qwen3b_tensor_map.LAYERS, src/qwen3b_tensor_map.zig:26-531).
+inline constexpr uint32_t kQwen3bCellRecords[36][12] = {
+    {9496, 11708, 11707, 11563, 11562, 11837, 11836, 11579, 11561, 10185, 10873, 9497},  // 0
+    {11853, 14065, 14064, 13920, 13919, 14194, 14193, 13936, 13918, 12542, 13230, 11854},  // 1
+    {37780, 39992, 39991, 39847, 39846, 40121, 40120, 39863, 39845, 38469, 39157, 37781},  // 2
+    {44163, 46375, 46374, 46230, 46229, 46504, 46503, 46246, 46228, 44852, 45540, 44164},  // 3
+    {46520, 48732, 48731, 48587, 48586, 48861, 48860, 48603, 48585, 47209, 47897, 46521},  // 4
+    {48877, 51089, 51088, 50944, 50943, 51218, 51217, 50960, 50942, 49566, 50254, 48878},  // 5
+    {51234, 53446, 53445, 53301, 53300, 53575, 53574, 53317, 53299, 51923, 52611, 51235},  // 6
+    {53591, 55803, 55802, 55658, 55657, 55932, 55931, 55674, 55656, 54280, 54968, 53592},  // 7
+    {55948, 58160, 58159, 58015, 58014, 58289, 58288, 58031, 58013, 56637, 57325, 55949},  // 8
+    {58305, 60517, 60516, 60372, 60371, 60646, 60645, 60388, 60370, 58994, 59682, 58306},  // 9
+    {14210, 16422, 16421, 16277, 16276, 16551, 16550, 16293, 16275, 14899, 15587, 14211},  // 10
+    {16567, 18779, 18778, 18634, 18633, 18908, 18907, 18650, 18632, 17256, 17944, 16568},  // 11
+    {18924, 21136, 21135, 20991, 20990, 21265, 21264, 21007, 20989, 19613, 20301, 18925},  // 12
+    {21281, 23493, 23492, 23348, 23347, 23622, 23621, 23364, 23346, 21970, 22658, 21282},  // 13
+    {23638, 25850, 25849, 25705, 25704, 25979, 25978, 25721, 25703, 24327, 25015, 23639},  // 14
+    {25995, 28207, 28206, 28062, 28061, 28336, 28335, 28078, 28060, 26684, 27372, 25996},  // 15
+    {28352, 30564, 30563, 30419, 30418, 30693, 30692, 30435, 30417, 29041, 29729, 28353},  // 16
+    {30709, 32921, 32920, 32776, 32775, 33050, 33049, 32792, 32774, 31398, 32086, 30710},  // 17
+    {33066, 35278, 35277, 35133, 35132, 35407, 35406, 35149, 35131, 33755, 34443, 33067},  // 18
+    {35423, 37635, 37634, 37490, 37489, 37764, 37763, 37506, 37488, 36112, 36800, 35424},  // 19
+    {40137, 42349, 42348, 42204, 42203, 42478, 42477, 42220, 42202, 40826, 41514, 40138},  // 20
+    {42494, 44018, 44017, 43873, 43872, 44147, 44146, 43889, 43871, 42495, 43183, 60662},  // 21
+    {61350, 63562, 63561, 63417, 63416, 63691, 63690, 63433, 63415, 62039, 62727, 61351},  // 22
+    {63707, 65919, 65918, 65774, 65773, 66048, 66047, 65790, 65772, 64396, 65084, 63708},  // 23
+    {66064, 68276, 68275, 68131, 68130, 68405, 68404, 68147, 68129, 66753, 67441, 66065},  // 24
+    {68421, 70633, 70632, 70488, 70487, 70762, 70761, 70504, 70486, 69110, 69798, 68422},  // 25
+    {70778, 72990, 72989, 72845, 72844, 73119, 73118, 72861, 72843, 71467, 72155, 70779},  // 26
+    {73135, 75347, 75346, 75202, 75201, 75476, 75475, 75218, 75200, 73824, 74512, 73136},  // 27
+    {75492, 77704, 77703, 77559, 77558, 77833, 77832, 77575, 77557, 76181, 76869, 75493},  // 28
+    {77849, 80061, 80060, 79916, 79915, 80190, 80189, 79932, 79914, 78538, 79226, 77850},  // 29
+    {80206, 82418, 82417, 82273, 82272, 82547, 82546, 82289, 82271, 80895, 81583, 80207},  // 30
+    {82563, 84775, 84774, 84630, 84629, 84904, 84903, 84646, 84628, 83252, 83940, 82564},  // 31
+    {84920, 87132, 87131, 86987, 86986, 87261, 87260, 87003, 86985, 85609, 86297, 84921},  // 32
+    {87277, 89489, 89488, 89344, 89343, 89618, 89617, 89360, 89342, 87966, 88654, 87278},  // 33
+    {89634, 91846, 91845, 91701, 91700, 91975, 91974, 91717, 91699, 90323, 91011, 89635},  // 34
+    {91991, 94203, 94202, 94058, 94057, 94332, 94331, 94074, 94056, 92680, 93368, 91992},  // 35
+};
 
 inline bool qwen35_is_full_attn(size_t l) { return l % 4 == 3; }  // layers 3, 7, ..., 31
 
@@ -54,15 +85,12 @@ inline LayerInfo layer_info(MapKind m, size_t l) {
       break;
     }
     case MapKind::Qwen3bCell: {
-      size_t b = 9496 + alpha_rank(l, 36) * 2357;
-      o.input_norm = b;
-      o.down_proj = b + 1; o.gate_proj = b + 689; o.up_proj = b + 1377;
-      o.post_norm = b + 2065;
-      o.k_bias = int64_t(b + 2066); o.k_proj = b + 2067;
-      o.o_proj = b + 2083;
-      o.q_bias = int64_t(b + 2211); o.q_proj = b + 2212;
-      o.v_bias = int64_t(b + 2340); o.v_proj = b + 2341;
-      o.q_tiles = 128; o.k_tiles = 16; o.v_tiles = 16; o.o_tiles = 128;
+      const uint32_t* t = kQwen3bCellRecords[l];
+      o.input_norm = t[0];
+      o.q_proj = t[1]; o.q_bias = t[2]; o.k_proj = t[3]; o.k_bias = t[4];
+      o.v_proj = t[5]; o.v_bias = t[6]; o.o_proj = t[7]; o.post_norm = t[8];
+      o.gate_proj = t[9]; o.up_proj = t[10]; o.down_proj = t[11];
+      o.q_tiles = 128; o.k_tiles = 16; o.v_tiles = 16; o.o_tiles = 128;  // chpe_engine.zig:1061-1082
       o.gate_tiles = 688; o.up_tiles = 688; o.down_tiles = 688;
       break;
     }

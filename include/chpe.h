@@ -75,10 +75,16 @@ int chpe_get_hidden(void *ctx, float *out);
 /* Timing: enqueue `n` decode steps that continue from the device state (greedy feedback),
  * bracketed by HIP events on the engine's stream; *ms = elapsed milliseconds. */
 int chpe_time_steps(void *ctx, size_t n, float *ms);
-/* Launch one stage alone (0 q/k/v, 1 o, 2 gate+up, 3 down, 4 LM head, 5 attention) for each
- * layer in [layer0, layer1), `iters` times, between HIP events; *ms = total. */
+/* Launch one stage alone (0 q/k/v, 1 o, 2 gate+up, 3 down, 4 LM head, 5 attention over the
+ * context chunks, 6 merge of the chunks) for each layer in [layer0, layer1), `iters` times,
+ * between HIP events; *ms = total. */
 int chpe_time_stage(void *ctx, int stage, size_t layer0, size_t layer1, size_t iters, float *ms);
-/* Algorithmic HBM bytes: of one stage launch for `layer`, and of a whole step at `pos`. */
+/* Run n_steps real decode steps (greedy feedback, continuing from the device state), launched
+ * without the graph and with a HIP event pair around every launch of `stage` (numbering as
+ * above); *avg_ms = mean duration of one launch of that stage inside the step. */
+int chpe_time_stage_live(void *ctx, int stage, size_t n_steps, float *avg_ms);
+/* Algorithmic HBM bytes: of one stage launch for `layer` (stage 5: at the current position),
+ * and of a whole step at `pos`. */
 double chpe_stage_bytes(void *ctx, int stage, size_t layer);
 double chpe_step_bytes(void *ctx, size_t pos);
 

@@ -101,6 +101,10 @@ oref_engine *oref_open_bytes(const uint8_t *bytes, size_t len, int arch_id,
                              size_t max_seq_len, int kv_f16, int threads);
 void oref_close(oref_engine *e);
 int oref_forward(oref_engine *e, uint32_t token, size_t pos, oref_result *res);
+/* Timing aid (no reference counterpart): fill K/V cache rows 0..n_pos-1 of every layer with
+ * seeded values in [-1, 1) (fp16-rounded in kv_f16 mode), so that oref_forward can be timed at
+ * position n_pos without decoding a prompt first.  Returns -2 if n_pos > max_seq_len. */
+int oref_prefill_synthetic(oref_engine *e, size_t n_pos, uint64_t seed);
 const float *oref_logits(const oref_engine *e);
 const float *oref_hidden(const oref_engine *e);
 size_t oref_vocab(const oref_engine *e);

@@ -62,6 +62,8 @@ def lib():
         L.oref_unpack_norm.argtypes = [V, S, _fp, S]
         L.oref_unpack_bias.argtypes = [V, S, _fp, S]
         L.oref_unpack_embed_row.argtypes = [V, ctypes.c_uint32, _fp]
+        L.oref_prefill_synthetic.restype = ctypes.c_int
+        L.oref_prefill_synthetic.argtypes = [V, S, ctypes.c_uint64]
         L.oref_generate.restype = ctypes.c_int
         L.oref_generate.argtypes = [V, _u32p, S, S, _u32p, _fp]
         L.oref_validate.restype = ctypes.c_int
@@ -133,6 +135,10 @@ class Oracle:
         if rc:
             raise RuntimeError(f"oref_forward rc={rc}")
         return r
+
+    def prefill_synthetic(self, n_pos, seed=0):
+        if self.L.oref_prefill_synthetic(self.e, n_pos, seed):
+            raise RuntimeError("oref_prefill_synthetic: n_pos > max_seq_len")
 
     def logits(self):
         return np.ctypeslib.as_array(self.L.oref_logits(self.e), shape=(self.vocab,)).copy()
