@@ -35,7 +35,7 @@ sys.path.insert(0, str(ROOT / "chpe-qwen-engine_amd"))
 METRIC = "batch-1 decode tok/s at 1 MI355X; achieved HBM GB/s as % of peak"
 PEAK_HBM_GBS = 8000.0
 V, D, LAYERS, KV_HEADS, HEAD_DIM, Q_HEADS = 151936, 2048, 36, 2, 128, 16
-ATTN_CHUNK = 8192 // HEAD_DIM
+ATTN_CHUNK = 16384 // HEAD_DIM  # positions per attention workgroup
 NS = "chpe::(anonymous namespace)::"
 STAGES = {  # stage id -> (description, kernel name as rocprofv3 prints it, launches per step)
     0: ("q/k/v GEMV (RMSNorm fused)", f"void {NS}k_gemv<{NS}Cell16W4, 0, 8, true>(chpe::GemvArgs)", LAYERS),

@@ -2,12 +2,12 @@
 //
 // Semantics: applyRope (chpe_engine.zig:195-216), KV write at `pos` (:1693-1697) and the
 // per-head attention loop (:1700-1734): scores (q.k_t)*scale, softmax over t <= pos, output
-// sum_t softmax_t * v_t.  The context is split into chunks of 8192/hd positions (flash
-// decoding): k_attn_partial computes, per chunk and query head, the chunk max m, the sum of
-// exp(s - m) and the exp-weighted sum of V; k_attn_combine rescales and merges the chunks.
-// Workgroup (chunk c, kv head g) serves the H/KV query heads that share kv head g, so every
-// K/V row is read from HBM once per step.  The workgroup holding `pos` rotates the new K row,
-// rounds K/V to the cache type, stores them and uses the stored values.
+// sum_t softmax_t * v_t.  The context is split into chunks of attn_chunk(hd) positions
+// (16384/hd: 128 at hd 128): k_attn_chunk computes, per chunk and query head, the chunk max,
+// the sum of exp(s - max) and the exp-weighted sum of the V rows; k_attn_merge rescales and
+// merges the chunks.  Workgroup (chunk, kv head) serves the query heads that share the kv
+// head, so every K/V row is read from HBM once per step.  The workgroup holding `pos` rotates
+// the new K row, rounds K/V to the cache type, stores them and uses the stored values.
 #include "device_common.hpp"
 #include "kernels.hpp"
 
@@ -21,156 +21,290 @@ __device__ __forceinline__ float rope_rot(float x0, float x1, float c, float s, 
   return first ? x0 * c - x1 * s : x0 * s + x1 * c;
 }
 
-template <int HD>
-__global__ void __launch_bounds__(256) k_attn_partial(AttnArgs a) {
-  constexpr int CH = 8192 / HD;  // 64 positions at hd 128, 32 at hd 256
-  constexpr int HALF = HD / 2;
-  constexpr int VEC = 8;         // elements per 16-byte fp16 cache access
+// Cache element access: fp16 or f32 KV cache.
+template <typename T> struct KvElem;
+template <> struct KvElem<__half> {
+  static constexpr int kBytes = 2;
+  __device__ static float get(const uint32_t* w, int i) {
+    return (i & 1) ? half_hi(w[i >> 1]) : half_lo(w[i >> 1]);
+  }
+  __device__ static float round(float x) { return __half2float(__float2half_rn(x)); }
+  __device__ static void put(void* cache, size_t at, float x) {
+    reinterpret_cast<__half*>(cache)[at] = __float2half_rn(x);
+  }
+  __device__ static void set(uint32_t* w, int i, float x) {
+    const uint32_t h = __half_as_ushort(__float2half_rn(x));
+    w[i >> 1] = (i & 1) ? ((w[i >> 1] & 0xffffu) | (h << 16)) : ((w[i >> 1] & 0xffff0000u) | h);
+  }
+};
+template <> struct KvElem<float> {
+  static constexpr int kBytes = 4;
+  __device__ static float get(const uint32_t* w, int i) { return __uint_as_float(w[i]); }
+  __device__ static float round(float x) { return x; }
+  __device__ static void put(void* cache, size_t at, float x) { reinterpret_cast<float*>(cache)[at] = x; }
+  __device__ static void set(uint32_t* w, int i, float x) { w[i] = __float_as_uint(x); }
+};
+
+// One workgroup = 4 waves = one chunk of CH = 4 * PW positions of one kv head, for the GQ
+// query heads that share it.  In a wave, LPP = HD/64 lanes hold one position's K row (64 dims
+// each) for the q.k dots, and every lane holds HD/64 dims of every V row of the wave's PW
+// positions for the weighted sum; all K/V loads of a wave are issued before any arithmetic.
+// The softmax statistics are per wave, merged over the 4 waves in LDS; one partial
+// (max, sum, weighted V sum) per chunk and query head goes to HBM for k_attn_merge.
+template <int HD, int GQ, typename KT>
+__global__ void __launch_bounds__(256) k_attn_chunk(AttnArgs a) {
+  using E = KvElem<KT>;
+  constexpr int NW = 4, LPP = HD / 64, PW = 64 / LPP, CH = NW * PW, HALF = HD / 2;
+  constexpr int KW = 64 * E::kBytes / 4;    // 32-bit words of a lane's 64 K dims
+  constexpr int DPL = HD / 64;              // V dims per lane
+  constexpr int VW = DPL * E::kBytes / 4;   // 32-bit words of a lane's V dims (1, 2 or 4)
+  static_assert(KW % 4 == 0 && VW >= 1, "");
   const uint32_t pos = a.state->pos, ctx = pos + 1;
   const uint32_t c = blockIdx.x, kvh = blockIdx.y;
-  if (c * CH >= ctx) return;
-  const uint32_t t0 = c * CH, nv = min(uint32_t(CH), ctx - t0);
-  const uint32_t G = a.H / a.KV;
-  const int tid = threadIdx.x, nt = blockDim.x;
+  if (c * CH >= ctx) return;  // the whole workgroup
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
 
-  __shared__ float qs[8][HD];
-  __shared__ float ks[CH][HD + 1];
-  __shared__ float vs[CH][HD];
-  __shared__ float ps[8][CH];
-  __shared__ float s_m[8], s_l[8];
+  __shared__ __align__(16) float qs[GQ][LPP][68];  // rotated queries; padding spreads banks
+  __shared__ __align__(16) float ps[NW][PW][GQ];   // exp(s - m) per wave
+  __shared__ __align__(16) float s_acc[NW][GQ][HD];
+  __shared__ float s_ml[NW][GQ][2];
+  __shared__ float s_newk[HD], s_newv[HD];
 
-  const float* cs = a.rope_cos + size_t(pos) * HALF;
-  const float* sn = a.rope_sin + size_t(pos) * HALF;
-  for (uint32_t i = tid; i < G * HD; i += nt) {  // rotated queries of the group
-    const uint32_t g = i / HD, d = i % HD, j = d % HALF;
-    const float* q = a.q_raw + size_t(kvh * G + g) * HD;
-    qs[g][d] = rope_rot(q[j], q[j + HALF], cs[j], sn[j], d < HALF);
+  // 1. the wave's K and V rows straight from HBM
+  const uint32_t tw0 = c * CH + wave * PW;
+  const uint32_t t = tw0 + lane / LPP;
+  const int grp = lane % LPP;
+  const size_t head = size_t(kvh) * a.max_seq * HD;
+  const uint8_t* kc = reinterpret_cast<const uint8_t*>(a.k_cache) + head * E::kBytes;
+  const uint8_t* vc = reinterpret_cast<const uint8_t*>(a.v_cache) + head * E::kBytes;
+  uint32_t kw[KW];
+  if (t < ctx && t != pos) {
+    const uint8_t* src = kc + (size_t(t) * HD + grp * 64) * E::kBytes;
+#pragma unroll
+    for (int i = 0; i < KW / 4; ++i) {
+      const uint4 v = ld_u128(src + 16 * i);
+      kw[4 * i] = v.x; kw[4 * i + 1] = v.y; kw[4 * i + 2] = v.z; kw[4 * i + 3] = v.w;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < KW; ++i) kw[i] = 0u;
   }
-  const size_t head_base = size_t(kvh) * a.max_seq * HD;
-  for (uint32_t i = tid; i < nv * (HD / VEC); i += nt) {
-    const uint32_t t = i / (HD / VEC), d0 = (i % (HD / VEC)) * VEC, tp = t0 + t;
-    const size_t off = head_base + size_t(tp) * HD + d0;
-    float kv[VEC], vv[VEC];
-    if (tp == pos) {  // the new row
-      const float* k = a.k_raw + size_t(kvh) * HD;
-      const float* v = a.v_raw + size_t(kvh) * HD;
+  uint32_t vw[PW][VW];
 #pragma unroll
-      for (int e = 0; e < VEC; ++e) {
-        const uint32_t d = d0 + e, j = d % HALF;
-        kv[e] = rope_rot(k[j], k[j + HALF], cs[j], sn[j], d < HALF);
-        vv[e] = v[d];
-      }
-      if (a.kv_f16) {
-        __half kh[VEC], vh[VEC];
-#pragma unroll
-        for (int e = 0; e < VEC; ++e) {
-          kh[e] = __float2half_rn(kv[e]);
-          vh[e] = __float2half_rn(vv[e]);
-          kv[e] = __half2float(kh[e]);
-          vv[e] = __half2float(vh[e]);
-        }
-        *reinterpret_cast<uint4*>(reinterpret_cast<__half*>(a.k_cache) + off) = *reinterpret_cast<uint4*>(kh);
-        *reinterpret_cast<uint4*>(reinterpret_cast<__half*>(a.v_cache) + off) = *reinterpret_cast<uint4*>(vh);
+  for (int j = 0; j < PW; ++j) {
+    const uint32_t tj = tw0 + j;
+    const uint8_t* src = vc + (size_t(tj) * HD + lane * DPL) * E::kBytes;
+    if (tj < ctx && tj != pos) {
+      if constexpr (VW == 1) {
+        vw[j][0] = *reinterpret_cast<const uint32_t*>(src);
+      } else if constexpr (VW == 2) {
+        const uint2 v = *reinterpret_cast<const uint2*>(src);
+        vw[j][0] = v.x; vw[j][1] = v.y;
       } else {
-        float4* kc = reinterpret_cast<float4*>(reinterpret_cast<float*>(a.k_cache) + off);
-        float4* vc = reinterpret_cast<float4*>(reinterpret_cast<float*>(a.v_cache) + off);
-        kc[0] = make_float4(kv[0], kv[1], kv[2], kv[3]);
-        kc[1] = make_float4(kv[4], kv[5], kv[6], kv[7]);
-        vc[0] = make_float4(vv[0], vv[1], vv[2], vv[3]);
-        vc[1] = make_float4(vv[4], vv[5], vv[6], vv[7]);
-      }
-    } else if (a.kv_f16) {
-      const uint4 kq = *reinterpret_cast<const uint4*>(reinterpret_cast<const __half*>(a.k_cache) + off);
-      const uint4 vq = *reinterpret_cast<const uint4*>(reinterpret_cast<const __half*>(a.v_cache) + off);
-      const uint32_t kw[4] = {kq.x, kq.y, kq.z, kq.w}, vw[4] = {vq.x, vq.y, vq.z, vq.w};
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        kv[2 * e] = h2f(uint16_t(kw[e] & 0xffffu));
-        kv[2 * e + 1] = h2f(uint16_t(kw[e] >> 16));
-        vv[2 * e] = h2f(uint16_t(vw[e] & 0xffffu));
-        vv[2 * e + 1] = h2f(uint16_t(vw[e] >> 16));
+        const uint4 v = ld_u128(src);
+        vw[j][0] = v.x; vw[j][1] = v.y; vw[j][2] = v.z; vw[j][3] = v.w;
       }
     } else {
-      const float4* kc = reinterpret_cast<const float4*>(reinterpret_cast<const float*>(a.k_cache) + off);
-      const float4* vc = reinterpret_cast<const float4*>(reinterpret_cast<const float*>(a.v_cache) + off);
-      const float4 k0 = kc[0], k1 = kc[1], v0 = vc[0], v1 = vc[1];
-      kv[0] = k0.x; kv[1] = k0.y; kv[2] = k0.z; kv[3] = k0.w; kv[4] = k1.x; kv[5] = k1.y; kv[6] = k1.z; kv[7] = k1.w;
-      vv[0] = v0.x; vv[1] = v0.y; vv[2] = v0.z; vv[3] = v0.w; vv[4] = v1.x; vv[5] = v1.y; vv[6] = v1.z; vv[7] = v1.w;
+#pragma unroll
+      for (int i = 0; i < VW; ++i) vw[j][i] = 0u;
+    }
+  }
+
+  // 2. rotated queries (applyRope, chpe_engine.zig:195-216) and, in the workgroup that holds
+  // `pos`, the new K/V row: rotated, rounded to the cache type, stored (:1693-1697)
+  const float* cs = a.rope_cos + size_t(pos) * HALF;
+  const float* sn = a.rope_sin + size_t(pos) * HALF;
+  for (int i = tid; i < GQ * HD; i += 256) {
+    const int g = i / HD, d = i % HD, j = d % HALF;
+    const float* q = a.q_raw + size_t(kvh * GQ + g) * HD;
+    qs[g][d / 64][d % 64] = rope_rot(q[j], q[j + HALF], cs[j], sn[j], d < HALF);
+  }
+  const bool has_new = pos / CH == c;
+  if (has_new && tid < HD) {
+    const int d = tid, j = d % HALF;
+    const float* k = a.k_raw + size_t(kvh) * HD;
+    const float kr = E::round(rope_rot(k[j], k[j + HALF], cs[j], sn[j], d < HALF));
+    const float vr = E::round(a.v_raw[size_t(kvh) * HD + d]);
+    E::put(a.k_cache, head + size_t(pos) * HD + d, kr);
+    E::put(a.v_cache, head + size_t(pos) * HD + d, vr);
+    s_newk[d] = kr;
+    s_newv[d] = vr;
+  }
+  __syncthreads();
+  if (has_new) {
+    if (t == pos) {
+#pragma unroll
+      for (int r = 0; r < 64; ++r) E::set(kw, r, s_newk[grp * 64 + r]);
     }
 #pragma unroll
-    for (int e = 0; e < VEC; ++e) {
-      ks[t][d0 + e] = kv[e];
-      vs[t][d0 + e] = vv[e];
+    for (int j = 0; j < PW; ++j)
+      if (tw0 + j == pos) {
+#pragma unroll
+        for (int dd = 0; dd < DPL; ++dd) E::set(vw[j], dd, s_newv[lane * DPL + dd]);
+      }
+  }
+
+  // 3. scores s = (q . k) * scale over the lane's 64 dims, summed over the LPP lanes
+  float s[GQ];
+#pragma unroll
+  for (int g = 0; g < GQ; ++g) s[g] = 0.0f;
+#pragma unroll
+  for (int r4 = 0; r4 < 16; ++r4) {
+    float kf[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) kf[e] = E::get(kw, 4 * r4 + e);
+#pragma unroll
+    for (int g = 0; g < GQ; ++g) {
+      const float4 q4 = *reinterpret_cast<const float4*>(&qs[g][grp][4 * r4]);
+      s[g] = fmaf(q4.x, kf[0], s[g]);
+      s[g] = fmaf(q4.y, kf[1], s[g]);
+      s[g] = fmaf(q4.z, kf[2], s[g]);
+      s[g] = fmaf(q4.w, kf[3], s[g]);
     }
   }
-  __syncthreads();
-  for (uint32_t i = tid; i < G * CH; i += nt) {  // scores: one (head, position) per thread
-    const uint32_t g = i / CH, t = i % CH;
-    float s = -INFINITY;
-    if (t < nv) {
-      float dot = 0.0f;
-#pragma unroll 8
-      for (int d = 0; d < HD; ++d) dot += qs[g][d] * ks[t][d];
-      s = dot * a.scale;
-    }
-    ps[g][t] = s;
+  const bool valid = t < ctx;
+#pragma unroll
+  for (int g = 0; g < GQ; ++g) {
+#pragma unroll
+    for (int o = 1; o < LPP; o <<= 1) s[g] += __shfl_xor(s[g], o);
+    s[g] = valid ? s[g] * a.scale : -INFINITY;
   }
-  __syncthreads();
-  const int wave = tid >> 6, lane = tid & 63, nw = nt / kWave;
-  for (uint32_t g = wave; g < G; g += nw) {  // chunk-local softmax statistics
-    float m = -INFINITY;
-    for (int t = lane; t < CH; t += kWave) m = fmaxf(m, ps[g][t]);
+
+  // 4. per-wave softmax statistics over the PW positions
+  float m_w[GQ], l_w[GQ];
+#pragma unroll
+  for (int g = 0; g < GQ; ++g) {
+    float m = s[g];
+#pragma unroll
     for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
-    float l = 0.0f;
-    for (int t = lane; t < CH; t += kWave) {
-      const float e = t < int(nv) ? expf(ps[g][t] - m) : 0.0f;
-      ps[g][t] = e;
-      l += e;
-    }
+    const float e = valid ? expf(s[g] - m) : 0.0f;
+    float l = grp == 0 ? e : 0.0f;
     l = wave_sum(l);
-    if (lane == 0) { s_m[g] = m; s_l[g] = l; }
+    if (grp == 0) ps[wave][lane / LPP][g] = e;
+    m_w[g] = m;
+    l_w[g] = l;
   }
   __syncthreads();
+
+  // 5. exp-weighted sum of the V rows over the lane's dims
+  float acc[GQ][DPL];
+#pragma unroll
+  for (int g = 0; g < GQ; ++g)
+#pragma unroll
+    for (int dd = 0; dd < DPL; ++dd) acc[g][dd] = 0.0f;
+#pragma unroll
+  for (int j = 0; j < PW; ++j) {
+    float p[GQ];
+#pragma unroll
+    for (int g4 = 0; g4 < GQ / 4; ++g4) {
+      const float4 v = *reinterpret_cast<const float4*>(&ps[wave][j][4 * g4]);
+      p[4 * g4] = v.x; p[4 * g4 + 1] = v.y; p[4 * g4 + 2] = v.z; p[4 * g4 + 3] = v.w;
+    }
+#pragma unroll
+    for (int dd = 0; dd < DPL; ++dd) {
+      const float v = E::get(vw[j], dd);
+#pragma unroll
+      for (int g = 0; g < GQ; ++g) acc[g][dd] = fmaf(p[g], v, acc[g][dd]);
+    }
+  }
+#pragma unroll
+  for (int g = 0; g < GQ; ++g) {
+#pragma unroll
+    for (int dd = 0; dd < DPL; ++dd) s_acc[wave][g][lane * DPL + dd] = acc[g][dd];
+    if (lane == 0) { s_ml[wave][g][0] = m_w[g]; s_ml[wave][g][1] = l_w[g]; }
+  }
+  __syncthreads();
+
+  // 6. merge the waves; one partial per (query head, chunk)
   const uint32_t nch = a.n_chunks;
-  for (uint32_t i = tid; i < G * HD; i += nt) {
-    const uint32_t g = i / HD, d = i % HD, h = kvh * G + g;
-    float acc = 0.0f;
-    for (uint32_t t = 0; t < nv; ++t) acc += ps[g][t] * vs[t][d];
-    a.part_acc[(size_t(h) * nch + c) * HD + d] = acc;
+  for (int i = tid; i < GQ * HD; i += 256) {
+    const int g = i / HD, d = i % HD;
+    float M = s_ml[0][g][0];
+#pragma unroll
+    for (int w = 1; w < NW; ++w) M = fmaxf(M, s_ml[w][g][0]);
+    float A = 0.0f, L = 0.0f;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+      const float f = s_ml[w][g][1] > 0.0f ? expf(s_ml[w][g][0] - M) : 0.0f;
+      A = fmaf(s_acc[w][g][d], f, A);
+      L = fmaf(s_ml[w][g][1], f, L);
+    }
+    const size_t hc = size_t(kvh * GQ + g) * nch + c;
+    a.part_acc[hc * HD + d] = A;
     if (d == 0) {
-      a.part_ml[(size_t(h) * nch + c) * 2] = s_m[g];
-      a.part_ml[(size_t(h) * nch + c) * 2 + 1] = s_l[g];
+      a.part_ml[hc * 2] = M;
+      a.part_ml[hc * 2 + 1] = L;
     }
   }
 }
 
-// out[h][d] = sum_c acc_c[d] * exp(m_c - M) / sum_c l_c * exp(m_c - M)
-__global__ void __launch_bounds__(256) k_attn_combine(AttnArgs a) {
-  const uint32_t h = blockIdx.x, d = threadIdx.x;
-  if (d >= a.hd) return;
-  const uint32_t ch = 8192u / a.hd, n_act = (a.state->pos + 1 + ch - 1) / ch, nch = a.n_chunks;
+// out[h][d] = sum_c A_c[d] exp(M_c - M) / sum_c L_c exp(M_c - M) over the active chunks
+template <int HD>
+__global__ void __launch_bounds__(512) k_attn_merge(AttnArgs a) {
+  constexpr int NT = 512, P = NT / HD, CH = attn_chunk_of(HD);
+  const uint32_t h = blockIdx.x, n_act = (a.state->pos + CH) / CH, nch = a.n_chunks;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  __shared__ float s_w[kAttnMaxChunks];
+  __shared__ float s_red[NT / 64];
+  __shared__ float s_o[P][HD];
   const float* ml = a.part_ml + size_t(h) * nch * 2;
-  float M = -INFINITY;
-  for (uint32_t j = 0; j < n_act; ++j) M = fmaxf(M, ml[2 * j]);
-  float L = 0.0f, o = 0.0f;
-  for (uint32_t j = 0; j < n_act; ++j) {
-    const float w = expf(ml[2 * j] - M);
-    L += ml[2 * j + 1] * w;
-    o += a.part_acc[(size_t(h) * nch + j) * a.hd + d] * w;
+  float m = -INFINITY;
+  for (uint32_t i = tid; i < n_act; i += NT) m = fmaxf(m, ml[2 * i]);
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+  if (lane == 0) s_red[wave] = m;
+  __syncthreads();
+  float M = s_red[0];
+#pragma unroll
+  for (int w = 1; w < NT / 64; ++w) M = fmaxf(M, s_red[w]);
+  __syncthreads();
+  float l = 0.0f;
+  for (uint32_t i = tid; i < n_act; i += NT) {
+    const float w = expf(ml[2 * i] - M);
+    s_w[i] = w;
+    l = fmaf(ml[2 * i + 1], w, l);
   }
-  a.out[size_t(h) * a.hd + d] = o / L;
+  l = wave_sum(l);
+  if (lane == 0) s_red[wave] = l;
+  __syncthreads();
+  float L = 0.0f;
+#pragma unroll
+  for (int w = 0; w < NT / 64; ++w) L += s_red[w];
+  const int d = tid % HD, part = tid / HD;
+  const float* acc = a.part_acc + size_t(h) * nch * HD + d;
+  float o = 0.0f;
+#pragma unroll 4
+  for (uint32_t j = part; j < n_act; j += P) o = fmaf(acc[size_t(j) * HD], s_w[j], o);
+  s_o[part][d] = o;
+  __syncthreads();
+  if (part == 0) {
+    float sum = s_o[0][d];
+#pragma unroll
+    for (int q = 1; q < P; ++q) sum += s_o[q][d];
+    a.out[size_t(h) * HD + d] = sum / L;
+  }
 }
 
 }  // namespace
 
 void launch_attention_partial(const AttnArgs& a, hipStream_t st) {
-  const dim3 grid(a.n_chunks, a.KV);
-  if (a.hd == 128) launch_kernel(&k_attn_partial<128>, grid, dim3(256), st, a);
-  else launch_kernel(&k_attn_partial<256>, grid, dim3(256), st, a);
+  const dim3 grid(a.n_chunks, a.KV), block(256);
+  const uint32_t gq = a.H / a.KV;
+  if (a.hd == 128 && gq == 8)
+    a.kv_f16 ? launch_kernel(&k_attn_chunk<128, 8, __half>, grid, block, st, a)
+             : launch_kernel(&k_attn_chunk<128, 8, float>, grid, block, st, a);
+  else if (a.hd == 256 && gq == 4)
+    a.kv_f16 ? launch_kernel(&k_attn_chunk<256, 4, __half>, grid, block, st, a)
+             : launch_kernel(&k_attn_chunk<256, 4, float>, grid, block, st, a);
 }
 
 void launch_attention_combine(const AttnArgs& a, hipStream_t st) {
-  launch_kernel(k_attn_combine, dim3(a.H), dim3(a.hd), st, a);
+  if (a.hd == 128) launch_kernel(&k_attn_merge<128>, dim3(a.H), dim3(512), st, a);
+  else launch_kernel(&k_attn_merge<256>, dim3(a.H), dim3(512), st, a);
+}
+
+bool attention_supported(uint32_t H, uint32_t KV, uint32_t hd) {
+  return KV > 0 && H % KV == 0 && ((hd == 128 && H / KV == 8) || (hd == 256 && H / KV == 4));
 }
 
 void launch_attention(const AttnArgs& a, hipStream_t st) {

@@ -132,6 +132,12 @@ bool Engine::init(const uint8_t* b, size_t len, const EngineConfig& cfg, std::st
     return false;
   }
   if (cfg.max_seq_len == 0 || cfg.max_seq_len > (1u << 20)) { *err = "bad max_seq_len"; return false; }
+  if (!attention_supported(uint32_t(arch_.num_attn_heads), uint32_t(arch_.num_kv_heads),
+                           uint32_t(arch_.head_dim))) {
+    *err = "attention kernels are built for head_dim 128 with 8 query heads per kv head and "
+           "head_dim 256 with 4";
+    return false;
+  }
   const uint32_t chunk = attn_chunk(uint32_t(arch_.head_dim));
   n_chunks_ = uint32_t((cfg.max_seq_len + chunk - 1) / chunk);
   if (n_chunks_ > kAttnMaxChunks) {
