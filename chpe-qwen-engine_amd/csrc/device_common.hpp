@@ -10,14 +10,23 @@
 
 namespace chpe {
 
-// Launch through the measurement probe when one is armed (see arm_launch_probe).
+// Launch through the measurement probe when one is armed (see arm_launch_probe), with
+// `lds` bytes of dynamic LDS (above 64 KiB the kernel's limit is raised first).
 template <class K, class... A>
-inline void launch_kernel(K kernel, dim3 grid, dim3 block, hipStream_t st, A... args) {
+inline void launch_kernel_lds(K kernel, dim3 grid, dim3 block, size_t lds, hipStream_t st, A... args) {
+  if (lds > 65536)
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
+                              int(lds));
   const LaunchProbe p = take_launch_probe();
   if (p.start)
-    hipExtLaunchKernelGGL(kernel, grid, block, 0, st, p.start, p.stop, 0, args...);
+    hipExtLaunchKernelGGL(kernel, grid, block, uint32_t(lds), st, p.start, p.stop, 0, args...);
   else
-    hipLaunchKernelGGL(kernel, grid, block, 0, st, args...);
+    hipLaunchKernelGGL(kernel, grid, block, uint32_t(lds), st, args...);
+}
+
+template <class K, class... A>
+inline void launch_kernel(K kernel, dim3 grid, dim3 block, hipStream_t st, A... args) {
+  launch_kernel_lds(kernel, grid, block, 0, st, args...);
 }
 
 namespace dev {
@@ -37,6 +46,8 @@ __device__ __forceinline__ float wave_sum(float v) {
 
 // Reduce N per-lane partials (one per row) over the wave with a reduce-scatter: after the
 // call, lane l holds the total of row l / (64/N) in v[0].  N in {4, 8, 16}.
+// Both halves are summed with their partner lane and the lane keeps the half it serves; the
+// choice is made between the two new sums, so no lane-dependent index into v[] arises.
 template <int N>
 __device__ __forceinline__ float wave_reduce_rows(float (&v)[N], int lane) {
   int mask = 32;
@@ -45,9 +56,9 @@ __device__ __forceinline__ float wave_reduce_rows(float (&v)[N], int lane) {
     const bool up = lane & mask;
 #pragma unroll
     for (int j = 0; j < n / 2; ++j) {
-      const float keep = up ? v[n / 2 + j] : v[j];
-      const float send = up ? v[j] : v[n / 2 + j];
-      v[j] = keep + __shfl_xor(send, mask);
+      const float lo = v[j] + __shfl_xor(v[j], mask);
+      const float hi = v[n / 2 + j] + __shfl_xor(v[n / 2 + j], mask);
+      v[j] = up ? hi : lo;
     }
     mask >>= 1;
   }

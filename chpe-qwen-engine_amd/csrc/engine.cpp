@@ -333,22 +333,25 @@ bool Engine::plan_projection(size_t tile_start, size_t num_tiles, size_t r_total
           by_row[f / c_total].push_back({uint32_t(f % c_total), w - q * s});
         }
       }
-      if (!by_row.empty()) {
-        std::vector<uint32_t> ptr(r_total + 1, 0);
-        std::vector<float2> ent;
-        for (size_t r = 0; r < r_total; ++r) {
-          for (const auto& [c, d] : by_row[r]) {
-            float cf;
-            std::memcpy(&cf, &c, 4);
-            ent.push_back(make_float2(cf, d));
-          }
-          ptr[r + 1] = uint32_t(ent.size());
+      if (!by_row.empty()) {  // fixed stride per row, zero-padded: [r_total][kmax]
+        size_t kmax = 0;
+        for (const auto& row : by_row) kmax = std::max(kmax, row.size());
+        if (kmax > kMaxCorrPerRow) {
+          *err = "a row has more than " + std::to_string(kMaxCorrPerRow) + " flat-tile outliers";
+          return false;
         }
-        p->corr_ptr = static_cast<uint32_t*>(dev_alloc(ptr.size() * 4));
-        p->corr = static_cast<float2*>(dev_alloc(std::max<size_t>(ent.size(), 1) * sizeof(float2)));
-        if (!p->corr_ptr || !p->corr) { *err = "allocation"; return false; }
-        (void)hipMemcpy(p->corr_ptr, ptr.data(), ptr.size() * 4, hipMemcpyHostToDevice);
-        if (!ent.empty()) (void)hipMemcpy(p->corr, ent.data(), ent.size() * sizeof(float2), hipMemcpyHostToDevice);
+        kmax = std::max<size_t>(kmax, 1);
+        std::vector<float2> ent(r_total * kmax, make_float2(0.0f, 0.0f));
+        for (size_t r = 0; r < r_total; ++r)
+          for (size_t k = 0; k < by_row[r].size(); ++k) {
+            float cf;
+            std::memcpy(&cf, &by_row[r][k].first, 4);
+            ent[r * kmax + k] = make_float2(cf, by_row[r][k].second);
+          }
+        p->corr_kmax = uint32_t(kmax);
+        p->corr = static_cast<float2*>(dev_alloc(ent.size() * sizeof(float2)));
+        if (!p->corr) { *err = "allocation"; return false; }
+        (void)hipMemcpy(p->corr, ent.data(), ent.size() * sizeof(float2), hipMemcpyHostToDevice);
       }
     } else {  // 16-row polymorphic cells: row bases are a prefix sum of dims.rows
       size_t row_base = 0, n_cells = 0;
@@ -492,7 +495,7 @@ uint32_t Engine::enqueue_gemv(const ProjPlan* const* parts, float* const* outs, 
     gp.bf16 = p.bf16;
     gp.y = outs[i];
     gp.bias = p.bias;
-    gp.corr_ptr = p.corr_ptr;
+    gp.corr_kmax = p.corr_kmax;
     gp.corr = p.corr;
     gp.replace_outliers = p.replace_outliers;
     gp.repl = p.repl;

@@ -53,8 +53,8 @@ struct ProjPlan {
   uint32_t bf16 = 0;
   uint32_t replace_outliers = 0;
   float* bias = nullptr;               // device, with the reference's non-finite -> 0 rule
-  uint32_t* corr_ptr = nullptr;        // device CSR of flat-tile outlier corrections
-  float2* corr = nullptr;
+  float2* corr = nullptr;              // device [rows][corr_kmax] flat-tile outlier corrections
+  uint32_t corr_kmax = 0;
   CellReplace* repl = nullptr;         // device, replace-mode outliers of 16-row cells
 };
 

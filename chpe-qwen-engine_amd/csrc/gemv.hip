@@ -13,6 +13,7 @@
 // sum((q-8)*x)*scale up to float rounding.  Outliers: added for 16-row cells (gemvTileW4
 // :404-410), replacing for the tied LM head (unpackEmbedRowCell :1369-1378) and for flat tiles
 // (gemvCellFlat :632-646, applied as per-row corrections prepared at load time).
+#include <cstdlib>
 #include <type_traits>
 
 #include "device_common.hpp"
@@ -99,107 +100,168 @@ __device__ __forceinline__ int part_of(const GemvArgs& a, uint32_t unit) {
   return p;
 }
 
-// input element with RMSNorm applied on load: (x * inv) * gamma (rmsNorm :187-191)
-__device__ __forceinline__ float xin(const GemvArgs& a, uint32_t c, float inv) {
-  return a.gamma ? a.x[c] * inv * a.gamma[c] : a.x[c];
-}
+// ---- per-unit terms outside the dense codes, loaded together with the weights -----------
+// 16-row cells: lane k < 8 holds entry k of the cell's outlier list: its column and its
+// weight for each of the unit's rows (added, gemvTileW4 :404-410), or for the tied LM head the
+// prepared (column, w_out - dequantised code) that makes the outlier replace the weight
+// (unpackEmbedRowCell :1369-1378).  Lanes 8.. mirror lanes 0..7 and add nothing.
+template <int RU>
+struct CellExtras {
+  uint32_t colA, colB;  // SwiGlu: A = gate cell, B = up cell
+  float w[RU];
+};
 
-// Per-row terms outside the dense codes, added once per row (by the wave holding panel 0).
-// P0 holds rows i < RU/2 of a SwiGlu unit (gate), P1 the rest (up); otherwise P0 == P1.
-// For 16-row cells the outlier weights/columns load with the codes; x comes from LDS.
-template <class F, int RU, bool kSwi, bool kReplace, bool kCellX>
-__device__ __forceinline__ void apply_extras(const GemvArgs& a, const GemvPart& P0, const GemvPart& P1,
-                                             uint32_t row_base, float (&acc)[RU], int lane, float inv,
-                                             const float* s_x) {
-  if constexpr (std::is_same_v<F, Cell16W4>) {
-    // the unit's rows lie in one cell (two for SwiGlu: the gate cell and the up cell)
-    const int k = lane & 7;  // outlier entry of this lane (lanes 8.. mirror lanes 0..7)
-    uint32_t colA, colB;
-    float w[RU];
-    if constexpr (kReplace) {  // tied LM head: prepared (column, w_out - code) per cell
-      const CellReplace& R = P0.repl[row_base >> 4];
-      colA = colB = R.col[k];
+template <class F, int RU, bool kSwi, bool kReplace>
+__device__ __forceinline__ void load_cell_extras(const GemvPart& P0, const GemvPart& P1, uint32_t row_base,
+                                                 int lane, CellExtras<RU>* e) {
+  const int k = lane & 7;
+  if constexpr (kReplace) {
+    const CellReplace& R = P0.repl[row_base >> 4];
+    e->colA = e->colB = R.col[k];
 #pragma unroll
-      for (int i = 0; i < RU; ++i) w[i] = R.delta[(row_base + uint32_t(i)) & 15][k];
-    } else {  // gemvTileW4: the payload's fp16 outlier weights are added (:309-315)
-      const uint8_t* cA = P0.base + size_t(row_base >> 4) * P0.stride;
-      const uint8_t* cB = P1.base + size_t(row_base >> 4) * P1.stride;
-      colA = ld_u16(cA + 16448 + 816 + 2 * k);
-      colB = kSwi ? ld_u16(cB + 16448 + 816 + 2 * k) : colA;
-#pragma unroll
-      for (int i = 0; i < RU; ++i) {
-        const uint8_t* c = (kSwi && i >= RU / 2) ? cB : cA;
-        const uint32_t n = (row_base + uint32_t(kSwi ? i % (RU / 2) : i)) & 15;
-        w[i] = h2f(ld_u16(c + 16448 + 560 + 2 * (n * 8 + k)));
-      }
-    }
-    // normalised x at the outlier columns: from the LDS mirror of the x chunk when present
-    const float xoA = colA < a.C ? (kCellX ? s_x[colA] : xin(a, colA, inv)) : 0.0f;
-    const float xoB = kSwi ? (colB < a.C ? (kCellX ? s_x[colB] : xin(a, colB, inv)) : 0.0f) : xoA;
-    if (lane < 8) {
-#pragma unroll
-      for (int i = 0; i < RU; ++i) {
-        const GemvPart& P = (kSwi && i >= RU / 2) ? P1 : P0;
-        if (row_base + uint32_t(kSwi ? i % (RU / 2) : i) < P.rows)
-          acc[i] += w[i] * ((kSwi && i >= RU / 2) ? xoB : xoA);
-      }
-    }
-  } else if constexpr (std::is_same_v<F, FlatW4> || std::is_same_v<F, FlatW2>) {
+    for (int i = 0; i < RU; ++i) e->w[i] = R.delta[(row_base + uint32_t(i)) & 15][k];
+  } else {
+    const uint8_t* cA = P0.base + size_t(row_base >> 4) * P0.stride;
+    const uint8_t* cB = P1.base + size_t(row_base >> 4) * P1.stride;
+    e->colA = ld_u16(cA + 16448 + 816 + 2 * k);
+    e->colB = kSwi ? ld_u16(cB + 16448 + 816 + 2 * k) : e->colA;
 #pragma unroll
     for (int i = 0; i < RU; ++i) {
-      const GemvPart& P = (kSwi && i >= RU / 2) ? P1 : P0;
-      const uint32_t r = row_base + uint32_t(kSwi ? i % (RU / 2) : i);
-      if (!P.corr_ptr || r >= P.rows) continue;
-      for (uint32_t j = P.corr_ptr[r] + lane; j < P.corr_ptr[r + 1]; j += kWave) {
-        const float2 c = P.corr[j];
-        acc[i] += c.y * xin(a, __float_as_uint(c.x), inv);
-      }
+      const uint8_t* c = (kSwi && i >= RU / 2) ? cB : cA;
+      const uint32_t n = (row_base + uint32_t(kSwi ? i % (RU / 2) : i)) & 15;
+      e->w[i] = h2f(ld_u16(c + 16448 + 560 + 2 * (n * 8 + k)));
     }
   }
 }
 
-template <int MODE>
-__device__ __forceinline__ void store_row(const GemvPart& P, uint32_t r, float v, float* bv, uint32_t* bi,
-                                          uint32_t* nf) {
-  if (r >= P.rows) return;
-  if constexpr (MODE == int(GemvMode::Store)) {
-    P.y[r] = v + (P.bias ? P.bias[r] : 0.0f);
-  } else if constexpr (MODE == int(GemvMode::Accum)) {
-    P.y[r] = P.y[r] + v;
-  } else if constexpr (MODE == int(GemvMode::Logits)) {
-    P.y[r] = v;
-    if (!isfinite(v)) *nf = 1;
-    if (v > -1e30f && better(v, r, *bv, *bi)) { *bv = v; *bi = r; }
+// Flat tiles: outliers replace weights (gemvCellFlat :632-646), applied as per-row corrections
+// (w_out - dequantised code) * x[col] prepared at load time.  Lane l serves unit row l >> 3 --
+// the row it owns after the reduce-scatter -- and entries (l & 7) + 8 j of that row's list.
+constexpr int kCorrSlots = int(kMaxCorrPerRow) / 8;
+struct FlatExtras {
+  float2 e[kCorrSlots];
+};
+struct NoExtras {};
+
+template <int RU, bool kSwi>
+__device__ __forceinline__ const GemvPart& row_part(const GemvPart& P0, const GemvPart& P1, int i) {
+  return (kSwi && i >= RU / 2) ? P1 : P0;
+}
+template <int RU, bool kSwi>
+__device__ __forceinline__ uint32_t row_of(uint32_t row_base, int i) {
+  return row_base + uint32_t(kSwi ? i % (RU / 2) : i);
+}
+
+template <int RU, bool kSwi>
+__device__ __forceinline__ void load_flat_extras(const GemvPart& P0, const GemvPart& P1, uint32_t row_base,
+                                                 int lane, FlatExtras* f) {
+  const int i = lane >> 3;
+  const GemvPart& P = row_part<RU, kSwi>(P0, P1, i);
+  const uint32_t r = row_of<RU, kSwi>(row_base, i), kmax = P.corr_kmax;
+  const bool ok = P.corr != nullptr && r < P.rows;
+#pragma unroll
+  for (int j = 0; j < kCorrSlots; ++j) {
+    const uint32_t k = uint32_t(lane & 7) + 8u * uint32_t(j);
+    f->e[j] = (ok && k < kmax) ? P.corr[size_t(r) * kmax + k] : make_float2(0.0f, 0.0f);
   }
 }
 
-// x chunk of panel p for this lane: raw values, normalised when `gamma` is set.  Returns
-// sum of squares of the raw values (for the single-panel RMSNorm) in *sq.
+// sum over the lane's entries (x from the workgroup's normalised copy), then over the 8 lanes
+// of its row
+__device__ __forceinline__ float flat_correction(const FlatExtras& f, const float* s_x) {
+  float cs = 0.0f;
+#pragma unroll
+  for (int j = 0; j < kCorrSlots; ++j)
+    if (f.e[j].y != 0.0f) cs = fmaf(f.e[j].y, s_x[__float_as_uint(f.e[j].x)], cs);
+  cs += __shfl_xor(cs, 1);
+  cs += __shfl_xor(cs, 2);
+  cs += __shfl_xor(cs, 4);
+  return cs;
+}
+
+// The workgroup's copy of the input in LDS, normalised (x * inv) * gamma when `gamma` is set
+// (rmsNorm :187-191); *ss = sum of x^2 over the input (also the LM head's hidden norm).
+// Inputs up to 32 floats per thread stay in registers between the two halves of the norm.
+template <bool kNeedSum>
+__device__ __forceinline__ void stage_x(const GemvArgs& a, float* s_x, float* s_red, float* ss, float* inv) {
+  const uint32_t C = a.C, tid = threadIdx.x, nt = blockDim.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  if ((kNeedSum || a.gamma) && C > 32 * nt) {  // wide input: two passes over LDS
+    float q2 = 0.0f;
+    for (uint32_t i = tid * 4; i < C; i += nt * 4) {
+      const float4 t = *reinterpret_cast<const float4*>(a.x + i);
+      *reinterpret_cast<float4*>(s_x + i) = t;
+      q2 = fmaf(t.x, t.x, fmaf(t.y, t.y, fmaf(t.z, t.z, fmaf(t.w, t.w, q2))));
+    }
+    q2 = wave_sum(q2);
+    if (lane == 0) s_red[wave] = q2;
+    __syncthreads();
+    float t = 0.0f;
+    for (uint32_t w = 0; w < nt / kWave; ++w) t += s_red[w];
+    *ss = t;
+    const float iv = a.gamma ? 1.0f / sqrtf(t / float(C) + a.eps) : 1.0f;
+    *inv = iv;
+    if (a.gamma)
+      for (uint32_t i = tid * 4; i < C; i += nt * 4) {
+        const float4 g = *reinterpret_cast<const float4*>(a.gamma + i);
+        float4 v = *reinterpret_cast<float4*>(s_x + i);
+        v.x = v.x * iv * g.x;
+        v.y = v.y * iv * g.y;
+        v.z = v.z * iv * g.z;
+        v.w = v.w * iv * g.w;
+        *reinterpret_cast<float4*>(s_x + i) = v;
+      }
+  } else if (kNeedSum || a.gamma) {
+    float4 xs[8], gs[8];
+    float q2 = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const uint32_t i = (tid + uint32_t(k) * nt) * 4;
+      xs[k] = i < C ? *reinterpret_cast<const float4*>(a.x + i) : make_float4(0.f, 0.f, 0.f, 0.f);
+      gs[k] = (i < C && a.gamma) ? *reinterpret_cast<const float4*>(a.gamma + i) : make_float4(1.f, 1.f, 1.f, 1.f);
+    }
+#pragma unroll
+    for (int k = 0; k < 8; ++k)
+      q2 = fmaf(xs[k].x, xs[k].x, fmaf(xs[k].y, xs[k].y, fmaf(xs[k].z, xs[k].z, fmaf(xs[k].w, xs[k].w, q2))));
+    q2 = wave_sum(q2);
+    if (lane == 0) s_red[wave] = q2;
+    __syncthreads();
+    float t = 0.0f;
+    for (uint32_t w = 0; w < nt / kWave; ++w) t += s_red[w];
+    *ss = t;
+    const float iv = a.gamma ? 1.0f / sqrtf(t / float(C) + a.eps) : 1.0f;
+    *inv = iv;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const uint32_t i = (tid + uint32_t(k) * nt) * 4;
+      if (i < C) {
+        float4 v = xs[k];
+        if (a.gamma) {
+          v.x = v.x * iv * gs[k].x;
+          v.y = v.y * iv * gs[k].y;
+          v.z = v.z * iv * gs[k].z;
+          v.w = v.w * iv * gs[k].w;
+        }
+        *reinterpret_cast<float4*>(s_x + i) = v;
+      }
+    }
+  } else {
+    for (uint32_t i = tid * 4; i < C; i += nt * 4)
+      *reinterpret_cast<float4*>(s_x + i) = *reinterpret_cast<const float4*>(a.x + i);
+  }
+  __syncthreads();
+}
+
+// the lane's input chunk of panel p from LDS, and its sum
 template <class F>
-__device__ __forceinline__ bool load_x(const GemvArgs& a, uint32_t p, int lane, float inv, bool normalise,
-                                       float (&xr)[F::kCols], float* sx, float* sq) {
+__device__ __forceinline__ float lds_chunk(const float* s_x, uint32_t C, uint32_t p, int lane, float (&xr)[F::kCols]) {
   uint32_t c0;
-  const bool v = F::lane_cols(p, lane, a.C, &c0);
-  float s = 0.0f, q2 = 0.0f;
-  if (v) {
-    const float4* x4 = reinterpret_cast<const float4*>(a.x + c0);
+  float s = 0.0f;
+  if (F::lane_cols(p, lane, C, &c0)) {
 #pragma unroll
     for (int k = 0; k < F::kCols / 4; ++k) {
-      const float4 t = x4[k];
+      const float4 t = *reinterpret_cast<const float4*>(s_x + c0 + 4 * k);
       xr[4 * k] = t.x; xr[4 * k + 1] = t.y; xr[4 * k + 2] = t.z; xr[4 * k + 3] = t.w;
-    }
-#pragma unroll
-    for (int k = 0; k < F::kCols; ++k) q2 = fmaf(xr[k], xr[k], q2);
-    if (normalise) {
-      const float4* g4 = reinterpret_cast<const float4*>(a.gamma + c0);
-#pragma unroll
-      for (int k = 0; k < F::kCols / 4; ++k) {
-        const float4 g = g4[k];
-        xr[4 * k] = xr[4 * k] * inv * g.x;
-        xr[4 * k + 1] = xr[4 * k + 1] * inv * g.y;
-        xr[4 * k + 2] = xr[4 * k + 2] * inv * g.z;
-        xr[4 * k + 3] = xr[4 * k + 3] * inv * g.w;
-      }
     }
 #pragma unroll
     for (int k = 0; k < F::kCols; ++k) s += xr[k];
@@ -207,239 +269,288 @@ __device__ __forceinline__ bool load_x(const GemvArgs& a, uint32_t p, int lane, 
 #pragma unroll
     for (int k = 0; k < F::kCols; ++k) xr[k] = 0.0f;
   }
-  *sx = s;
-  *sq = q2;
-  return v;
+  return s;
 }
 
-// occupancy floor per layout: the 16-row-cell kernels need more registers (outlier columns)
-template <class F>
-constexpr int kMinWavesPerSimd = 3;
-template <>
-constexpr int kMinWavesPerSimd<Cell16W4> = 2;
+// Everything one work unit loads: dense codes + group scales of one panel, outlier terms, and
+// the epilogue operand (residual or bias).  Issued before any arithmetic that needs them.
+template <class F, int MODE>
+struct UnitLoads {
+  static constexpr int RU = 8;
+  static constexpr bool kCell = std::is_same_v<F, Cell16W4>;
+  static constexpr bool kFlat = std::is_same_v<F, FlatW4> || std::is_same_v<F, FlatW2>;
+  uint32_t unit, row_base;
+  int pu;
+  uint4 q[RU];
+  float s[RU];
+  std::conditional_t<kCell, CellExtras<RU>, NoExtras> ce;
+  std::conditional_t<kFlat, FlatExtras, NoExtras> fe;
+  float pre;
+};
 
-template <class F, int MODE, int RU, bool SINGLE>
-__global__ void __launch_bounds__(512, kMinWavesPerSimd<F>) k_gemv(GemvArgs a) {
-  constexpr int S = kWave / RU;  // lanes per row after the reduce-scatter
+template <class F, int MODE>
+__device__ __forceinline__ void issue_panel(const GemvArgs& a, const GemvPart& P0, const GemvPart& P1, bool active,
+                                            uint32_t row_base, uint32_t p, int lane, uint4 (&q)[8], float (&s)[8]) {
+  constexpr int RU = 8;
+  constexpr bool kSwi = MODE == int(GemvMode::SwiGlu);
+  uint32_t c0;
+  const bool v = active && F::lane_cols(p, lane, a.C, &c0);
+#pragma unroll
+  for (int i = 0; i < RU; ++i) {
+    const GemvPart& P = row_part<RU, kSwi>(P0, P1, i);
+    const uint32_t r = row_of<RU, kSwi>(row_base, i);
+    if (v && r < P.rows) {
+      F::locate(P, r, p, lane, a.C, &q[i], &s[i]);
+    } else {
+      q[i] = make_uint4(0, 0, 0, 0);
+      s[i] = 0.0f;
+    }
+  }
+}
+
+// extras: the unit's outlier terms (cells), its correction entries (flat: only the wave
+// `with_corr`), and for NW == 1 the epilogue operand of the lane's row
+template <class F, int MODE>
+__device__ __forceinline__ void issue_unit(const GemvArgs& a, uint32_t unit, uint32_t p, int lane, bool with_corr,
+                                           bool with_pre, UnitLoads<F, MODE>* u) {
+  constexpr int RU = 8, S = kWave / RU;
+  constexpr bool kSwi = MODE == int(GemvMode::SwiGlu);
+  constexpr bool kPre = MODE == int(GemvMode::Store) || MODE == int(GemvMode::Accum);
+  const bool active = unit < a.n_units;
+  u->unit = unit;
+  u->pu = kSwi ? 0 : __builtin_amdgcn_readfirstlane(part_of(a, active ? unit : 0u));
+  const GemvPart& P0 = a.part[u->pu];
+  const GemvPart& P1 = a.part[kSwi ? 1 : u->pu];
+  u->row_base = kSwi ? unit * (RU / 2) : (unit - P0.unit_begin) * RU;
+  if constexpr (UnitLoads<F, MODE>::kCell) {
+    if (active) load_cell_extras<F, RU, kSwi, MODE == int(GemvMode::Logits)>(P0, P1, u->row_base, lane, &u->ce);
+  }
+  if constexpr (UnitLoads<F, MODE>::kFlat) {
+    if (active && with_corr) load_flat_extras<RU, kSwi>(P0, P1, u->row_base, lane, &u->fe);
+  }
+  u->pre = 0.0f;
+  if constexpr (kPre) {
+    const uint32_t own = u->row_base + uint32_t(lane / S);
+    if (with_pre && active && (lane % S) == 0 && own < P0.rows)
+      u->pre = MODE == int(GemvMode::Accum) ? P0.y[own] : (P0.bias ? P0.bias[own] : 0.0f);
+  }
+  issue_panel<F, MODE>(a, P0, P1, active, u->row_base, p, lane, u->q, u->s);
+}
+
+// final value v of unit row i (lane-owned): SwiGlu pairs gate row i with up row i + RU/2
+template <int MODE>
+__device__ __forceinline__ void epilogue(const GemvPart& P0, uint32_t r, float v, float u, float pre, float* bv,
+                                         uint32_t* bi, uint32_t* nf) {
+  if (r >= P0.rows) return;
+  if constexpr (MODE == int(GemvMode::SwiGlu)) {
+    P0.y[r] = v / (1.0f + expf(-v)) * u;  // silu(g)*u: :159-161, :1746-1748
+  } else if constexpr (MODE == int(GemvMode::Accum)) {
+    P0.y[r] = pre + v;
+  } else if constexpr (MODE == int(GemvMode::Store)) {
+    P0.y[r] = v + pre;
+  } else {
+    P0.y[r] = v;
+    if (!isfinite(v)) *nf = 1;
+    if (v > -1e30f && better(v, r, *bv, *bi)) { *bv = v; *bi = r; }
+  }
+}
+
+template <int MODE>
+__device__ __forceinline__ void argmax_partial(const GemvArgs& a, float bv, uint32_t bi, uint32_t nf, float ss,
+                                               float* s_bv, uint32_t* s_bi, uint32_t* s_nf) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const float ov = __shfl_xor(bv, o);
+    const uint32_t oi = __shfl_xor(bi, o);
+    nf |= __shfl_xor(nf, o);
+    if (better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
+  }
+  if (lane == 0) { s_bv[wave] = bv; s_bi[wave] = bi; s_nf[wave] = nf; }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int w = 1; w < int(blockDim.x / kWave); ++w) {
+      nf |= s_nf[w];
+      if (better(s_bv[w], s_bi[w], bv, bi)) { bv = s_bv[w]; bi = s_bi[w]; }
+    }
+    a.partials[blockIdx.x] = ArgmaxPartial{bv, bi, nf, 0u};
+    if (blockIdx.x == 0) a.result->hidden_norm = sqrtf(ss);
+  }
+}
+
+// One wave = one unit of RU rows over all columns (NW == 1).  Persistent: the wave strides over
+// units, and issues the next unit's loads before the arithmetic of the current one.
+template <class F, int MODE>
+__global__ void __launch_bounds__(512, 2) k_gemv_rows(GemvArgs a) {
+  constexpr int RU = 8, S = kWave / RU;
   constexpr bool kSwi = MODE == int(GemvMode::SwiGlu);
   constexpr bool kLogits = MODE == int(GemvMode::Logits);
-  constexpr bool kPre = MODE == int(GemvMode::Store) || MODE == int(GemvMode::Accum);
-  constexpr bool kCellX = std::is_same_v<F, Cell16W4> && SINGLE;  // outlier x from the LDS copy
-  __shared__ float s_part[kMaxWavesPerUnit][RU];
-  __shared__ float s_bv[8];
+  constexpr bool kOnePanel = F::kPPW == 1;
+  using U = UnitLoads<F, MODE>;
+  __shared__ __align__(16) float s_x[F::kPanelCols * F::kPPW];
+  __shared__ float s_red[8], s_bv[8];
   __shared__ uint32_t s_bi[8], s_nf[8];
-  __shared__ float s_x[SINGLE ? F::kPanelCols : 1];  // normalised input (single panel)
-  __shared__ float s_red[kMaxWavesPerUnit];
   const int lane = threadIdx.x & 63;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const uint32_t NW = a.waves_per_unit, C = a.C;
-  const uint32_t upb = NW == 1 ? blockDim.x / kWave : 1u;  // units per pass of the workgroup
+  const uint32_t nwv = blockDim.x / kWave, stride = gridDim.x * nwv;
+  uint32_t unit = blockIdx.x * nwv + wave;
 
-  // RMSNorm statistics (sum of x^2 over the input) and, for a single panel, the lane's x
-  // chunk, normalised once and reused for every unit of the wave.  Run after the first
-  // unit's weight loads are issued so that their latency overlaps.
-  float ss = 0.0f, inv = 1.0f, sx0 = 0.0f;
-  float x0[SINGLE ? F::kCols : 1];
-  bool pending = true;
-  auto prologue = [&]() {
-    if constexpr (SINGLE) {
-      // the whole input (C <= one panel) is staged in LDS by the workgroup, normalised once,
-      // then each lane keeps its chunk in registers; the LDS copy also serves the outlier
-      // column lookups
-      const int tid = threadIdx.x, nt = blockDim.x;
-      float q2 = 0.0f;
-      for (uint32_t i = uint32_t(tid) * 4; i < C; i += uint32_t(nt) * 4) {
-        const float4 t = *reinterpret_cast<const float4*>(a.x + i);
-        *reinterpret_cast<float4*>(s_x + i) = t;
-        q2 = fmaf(t.x, t.x, fmaf(t.y, t.y, fmaf(t.z, t.z, fmaf(t.w, t.w, q2))));
-      }
-      if (a.gamma || kLogits) {
-        q2 = wave_sum(q2);
-        if (lane == 0) s_red[wave] = q2;
-        __syncthreads();
-        for (int w = 0; w < nt / kWave; ++w) ss += s_red[w];
-        if (a.gamma) {
-          inv = 1.0f / sqrtf(ss / float(C) + a.eps);
-          for (uint32_t i = uint32_t(tid) * 4; i < C; i += uint32_t(nt) * 4) {
-            const float4 g = *reinterpret_cast<const float4*>(a.gamma + i);
-            float4 t = *reinterpret_cast<float4*>(s_x + i);
-            t.x = t.x * inv * g.x;
-            t.y = t.y * inv * g.y;
-            t.z = t.z * inv * g.z;
-            t.w = t.w * inv * g.w;
-            *reinterpret_cast<float4*>(s_x + i) = t;
-          }
-        }
-      }
-      __syncthreads();
-      uint32_t c0;
-      sx0 = 0.0f;
-      if (F::lane_cols(0, lane, C, &c0)) {
-#pragma unroll
-        for (int k = 0; k < F::kCols / 4; ++k) {
-          const float4 t = *reinterpret_cast<const float4*>(s_x + c0 + 4 * k);
-          x0[4 * k] = t.x; x0[4 * k + 1] = t.y; x0[4 * k + 2] = t.z; x0[4 * k + 3] = t.w;
-        }
-      } else {
-#pragma unroll
-        for (int k = 0; k < F::kCols; ++k) x0[k] = 0.0f;
-      }
-#pragma unroll
-      for (int k = 0; k < F::kCols; ++k) sx0 += x0[k];
-    } else if (a.gamma || kLogits) {
-      for (uint32_t b = uint32_t(lane) * 4; b < C; b += 256 * 8) {  // 8 x 16-byte loads per pass
-        float4 t[8];
-#pragma unroll
-        for (int k = 0; k < 8; ++k) {
-          const uint32_t i = b + uint32_t(k) * 256;
-          t[k] = i < C ? *reinterpret_cast<const float4*>(a.x + i) : make_float4(0.f, 0.f, 0.f, 0.f);
-        }
-#pragma unroll
-        for (int k = 0; k < 8; ++k)
-          ss = fmaf(t[k].x, t[k].x, fmaf(t[k].y, t[k].y, fmaf(t[k].z, t[k].z, fmaf(t[k].w, t[k].w, ss))));
-      }
-      ss = wave_sum(ss);
-      if (a.gamma) inv = 1.0f / sqrtf(ss / float(C) + a.eps);
-    }
-    pending = false;
-  };
-  const uint32_t ppw = (a.n_panels + NW - 1) / NW;
-  const uint32_t p0 = NW == 1 ? 0u : wave * ppw;
-  const uint32_t p1 = NW == 1 ? a.n_panels : min(a.n_panels, p0 + ppw);
+  U cur, nxt;
+  issue_unit<F, MODE>(a, unit, 0, lane, true, true, &cur);
+  float ss = 0.0f, inv = 1.0f;
+  stage_x<kLogits>(a, s_x, s_red, &ss, &inv);
+  float x0[F::kCols];
+  float sx0 = lds_chunk<F>(s_x, a.C, 0, lane, x0);
 
-  float bv = -1e30f;  // Logits: running (max, first index) of the rows this thread owns
+  float bv = -1e30f;
   uint32_t bi = 0xffffffffu, nf = 0;
+  for (; unit < a.n_units; unit += stride) {
+    if constexpr (kOnePanel) {
+      if (unit + stride < a.n_units) issue_unit<F, MODE>(a, unit + stride, 0, lane, true, true, &nxt);
+    }
+    const GemvPart& P0 = a.part[cur.pu];
+    const GemvPart& P1 = a.part[kSwi ? 1 : cur.pu];
+    float acc[RU];
+#pragma unroll
+    for (int i = 0; i < RU; ++i) {
+      const GemvPart& P = row_part<RU, kSwi>(P0, P1, i);
+      acc[i] = (F::dot(cur.q[i], x0, P.bf16 != 0) - F::kOff * sx0) * cur.s[i];
+    }
+    if constexpr (!kOnePanel) {  // further panels (raw tiles): loads of panel p+1 ahead of p's math
+      uint4 qn[RU];
+      float sn[RU];
+      for (uint32_t p = 1; p < a.n_panels; ++p) {
+        issue_panel<F, MODE>(a, P0, P1, true, cur.row_base, p, lane, qn, sn);
+        float xr[F::kCols];
+        const float sx = lds_chunk<F>(s_x, a.C, p, lane, xr);
+#pragma unroll
+        for (int i = 0; i < RU; ++i) {
+          const GemvPart& P = row_part<RU, kSwi>(P0, P1, i);
+          acc[i] += (F::dot(qn[i], xr, P.bf16 != 0) - F::kOff * sx) * sn[i];
+        }
+      }
+    }
+    if constexpr (U::kCell) {  // outlier terms (lanes 0..7)
+      const float xoA = cur.ce.colA < a.C ? s_x[cur.ce.colA] : 0.0f;
+      const float xoB = kSwi ? (cur.ce.colB < a.C ? s_x[cur.ce.colB] : 0.0f) : xoA;
+      if (lane < 8) {
+#pragma unroll
+        for (int i = 0; i < RU; ++i) acc[i] = fmaf(cur.ce.w[i], (kSwi && i >= RU / 2) ? xoB : xoA, acc[i]);
+      }
+    }
+    float tot = wave_reduce_rows<RU>(acc, lane);  // lane l: row l / S of the unit
+    if constexpr (U::kFlat) tot += flat_correction(cur.fe, s_x);
+    const int i = lane / S;
+    const float up = kSwi ? __shfl(tot, (lane + 32) & 63) : 0.0f;  // up row i: 32 lanes above gate row i
+    if ((lane % S) == 0 && (!kSwi || i < RU / 2))
+      epilogue<MODE>(P0, row_of<RU, kSwi>(cur.row_base, i), tot, up, cur.pre, &bv, &bi, &nf);
+    if constexpr (kOnePanel) {
+      cur = nxt;
+    } else if (unit + stride < a.n_units) {
+      issue_unit<F, MODE>(a, unit + stride, 0, lane, true, true, &cur);
+    }
+  }
+  if constexpr (kLogits) argmax_partial<MODE>(a, bv, bi, nf, ss, s_bv, s_bi, s_nf);
+}
 
-  for (uint32_t u0 = blockIdx.x * upb; u0 < a.n_units; u0 += gridDim.x * upb) {
-    const uint32_t unit = __builtin_amdgcn_readfirstlane(u0 + (NW == 1 ? wave : 0u));
-    const bool active = unit < a.n_units;
-    const int pu = kSwi ? 0 : __builtin_amdgcn_readfirstlane(part_of(a, active ? unit : 0u));
-    const GemvPart P0 = a.part[pu];
-    const GemvPart P1 = a.part[kSwi ? 1 : pu];
-    // unit-local row i: SwiGlu = RU/2 rows of part 0 (gate), then the same rows of part 1 (up)
-    const uint32_t row_base = kSwi ? unit * (RU / 2) : (unit - P0.unit_begin) * RU;
-    // the epilogue's other operand (residual or bias), fetched with the weights
+// One workgroup = one unit, its panels split over NW waves (K-split); partial sums meet in LDS
+// in a fixed order.  The input sits in LDS (dynamic, C floats) so that the flat-tile outlier
+// corrections read any column; wave 0 adds them and writes the unit's rows.
+template <class F, int MODE>
+__global__ void __launch_bounds__(512, 2) k_gemv_split(GemvArgs a) {
+  constexpr int RU = 8, S = kWave / RU;
+  constexpr bool kSwi = MODE == int(GemvMode::SwiGlu);
+  constexpr bool kLogits = MODE == int(GemvMode::Logits);
+  using U = UnitLoads<F, MODE>;
+  extern __shared__ __align__(16) float s_x[];  // C floats
+  __shared__ float s_part[kMaxWavesPerUnit][RU];
+  __shared__ float s_red[8], s_bv[8];
+  __shared__ uint32_t s_bi[8], s_nf[8];
+  const int lane = threadIdx.x & 63;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const uint32_t NW = blockDim.x / kWave;
+  const uint32_t ppw = (a.n_panels + NW - 1) / NW;
+  const uint32_t p0 = wave * ppw, p1 = min(a.n_panels, p0 + ppw);
+
+  U cur;
+  uint32_t unit = blockIdx.x;
+  issue_unit<F, MODE>(a, unit, p0, lane, wave == 0, false, &cur);
+  float ss = 0.0f, inv = 1.0f;
+  stage_x<kLogits>(a, s_x, s_red, &ss, &inv);
+
+  float bv = -1e30f;
+  uint32_t bi = 0xffffffffu, nf = 0;
+  for (; unit < a.n_units; unit += gridDim.x) {
+    const GemvPart& P0 = a.part[cur.pu];
+    const GemvPart& P1 = a.part[kSwi ? 1 : cur.pu];
+    // epilogue operand of wave 0's rows, requested now so it overlaps the arithmetic
     float pre = 0.0f;
-    const uint32_t own = row_base + uint32_t(lane / S);
-    if constexpr (kPre) {
-      if (NW == 1 && active && (lane % S) == 0 && own < P0.rows)
+    if constexpr (MODE == int(GemvMode::Store) || MODE == int(GemvMode::Accum)) {
+      const uint32_t own = cur.row_base + uint32_t(lane / S);
+      if (wave == 0 && (lane % S) == 0 && own < P0.rows)
         pre = MODE == int(GemvMode::Accum) ? P0.y[own] : (P0.bias ? P0.bias[own] : 0.0f);
     }
     float acc[RU];
 #pragma unroll
     for (int i = 0; i < RU; ++i) acc[i] = 0.0f;
     for (uint32_t p = p0; p < p1; ++p) {
-      uint32_t c0;
-      const bool v = active && F::lane_cols(p, lane, C, &c0);
-      uint4 q[RU];
-      float s[RU];
+      if (p != p0) issue_panel<F, MODE>(a, P0, P1, true, cur.row_base, p, lane, cur.q, cur.s);
+      float xr[F::kCols];
+      const float sx = lds_chunk<F>(s_x, a.C, p, lane, xr);
 #pragma unroll
-      for (int i = 0; i < RU; ++i) {  // all row loads first: RU 16-byte loads in flight
-        const GemvPart& P = (kSwi && i >= RU / 2) ? P1 : P0;
-        const uint32_t r = row_base + uint32_t(kSwi ? i % (RU / 2) : i);
-        if (v && r < P.rows) {
-          F::locate(P, r, p, lane, C, &q[i], &s[i]);
-        } else {
-          q[i] = make_uint4(0, 0, 0, 0);
-          s[i] = 0.0f;
-        }
-      }
-      if (pending) prologue();
-      if (!active) continue;
-      if constexpr (SINGLE) {
-#pragma unroll
-        for (int i = 0; i < RU; ++i) {
-          const GemvPart& P = (kSwi && i >= RU / 2) ? P1 : P0;
-          acc[i] += (F::dot(q[i], x0, P.bf16 != 0) - F::kOff * sx0) * s[i];
-        }
-      } else {
-        float xr[F::kCols], sx, q2;
-        load_x<F>(a, p, lane, inv, a.gamma != nullptr, xr, &sx, &q2);
-#pragma unroll
-        for (int i = 0; i < RU; ++i) {
-          const GemvPart& P = (kSwi && i >= RU / 2) ? P1 : P0;
-          acc[i] += (F::dot(q[i], xr, P.bf16 != 0) - F::kOff * sx) * s[i];
-        }
+      for (int i = 0; i < RU; ++i) {
+        const GemvPart& P = row_part<RU, kSwi>(P0, P1, i);
+        acc[i] += (F::dot(cur.q[i], xr, P.bf16 != 0) - F::kOff * sx) * cur.s[i];
       }
     }
-    if (pending) prologue();
-    if (active && p0 == 0) apply_extras<F, RU, kSwi, kLogits, kCellX>(a, P0, P1, row_base, acc, lane, inv, s_x);
     const float tot = wave_reduce_rows<RU>(acc, lane);
-    if (NW == 1) {
-      const int i = lane / S;
-      const bool owner = active && (lane % S) == 0;
-      if constexpr (kSwi) {
-        const float u = __shfl(tot, (lane + 32) & 63);  // up row i sits 32 lanes above gate row i
-        if (owner && i < RU / 2 && own < P0.rows)
-          P0.y[own] = tot / (1.0f + expf(-tot)) * u;  // silu(g)*u: :159-161, :1746-1748
-      } else if constexpr (kPre) {
-        if (owner && own < P0.rows) P0.y[own] = MODE == int(GemvMode::Accum) ? pre + tot : tot + pre;
-      } else if (owner) {
-        store_row<MODE>(P0, own, tot, &bv, &bi, &nf);
-      }
-    } else {
-      if (lane % S == 0) s_part[wave][lane / S] = tot;
-      __syncthreads();
-      const int t = threadIdx.x;
-      if (t < RU) {
-        float v = 0.0f;
-        for (uint32_t w = 0; w < NW; ++w) v += s_part[w][t];
-        if constexpr (kSwi) {
-          if (t < RU / 2) {
-            float u = 0.0f;
-            for (uint32_t w = 0; w < NW; ++w) u += s_part[w][t + RU / 2];
-            const uint32_t r = row_base + uint32_t(t);
-            if (r < P0.rows) P0.y[r] = v / (1.0f + expf(-v)) * u;
-          }
-        } else {
-          store_row<MODE>(P0, row_base + uint32_t(t), v, &bv, &bi, &nf);
-        }
-      }
-      __syncthreads();
-    }
-  }
-  if (pending) prologue();
-
-  if constexpr (kLogits) {  // this workgroup's partial of the argmax scan
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-      const float ov = __shfl_xor(bv, o);
-      const uint32_t oi = __shfl_xor(bi, o);
-      nf |= __shfl_xor(nf, o);
-      if (better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
-    }
-    if (lane == 0) { s_bv[wave] = bv; s_bi[wave] = bi; s_nf[wave] = nf; }
+    if (lane % S == 0) s_part[wave][lane / S] = tot;
     __syncthreads();
-    if (threadIdx.x == 0) {
-      for (int w = 1; w < int(blockDim.x / kWave); ++w) {
-        nf |= s_nf[w];
-        if (better(s_bv[w], s_bi[w], bv, bi)) { bv = s_bv[w]; bi = s_bi[w]; }
-      }
-      a.partials[blockIdx.x] = ArgmaxPartial{bv, bi, nf, 0u};
-      if (blockIdx.x == 0) a.result->hidden_norm = sqrtf(ss);
+    if (wave == 0) {
+      const int i = lane / S;
+      float v = 0.0f;
+      for (uint32_t w = 0; w < NW; ++w) v += s_part[w][i];
+      if constexpr (U::kFlat) v += flat_correction(cur.fe, s_x);
+      const float up = kSwi ? __shfl(v, (lane + 32) & 63) : 0.0f;
+      if (unit < a.n_units && (lane % S) == 0 && (!kSwi || i < RU / 2))
+        epilogue<MODE>(P0, row_of<RU, kSwi>(cur.row_base, i), v, up, pre, &bv, &bi, &nf);
     }
+    __syncthreads();
+    if (unit + gridDim.x < a.n_units) issue_unit<F, MODE>(a, unit + gridDim.x, p0, lane, wave == 0, false, &cur);
   }
+  if constexpr (kLogits) argmax_partial<MODE>(a, bv, bi, nf, ss, s_bv, s_bi, s_nf);
 }
 
-template <class F, int MODE, int RU>
+template <class F, int MODE>
 void launch_one(const GemvArgs& a, const GemvLaunch& g, hipStream_t st) {
-  if (a.n_panels == 1)
-    launch_kernel(&k_gemv<F, MODE, RU, true>, dim3(g.blocks), dim3(g.threads), st, a);
+  if (a.waves_per_unit == 1)
+    launch_kernel(&k_gemv_rows<F, MODE>, dim3(g.blocks), dim3(g.threads), st, a);
   else
-    launch_kernel(&k_gemv<F, MODE, RU, false>, dim3(g.blocks), dim3(g.threads), st, a);
+    launch_kernel_lds(&k_gemv_split<F, MODE>, dim3(g.blocks), dim3(g.threads), size_t(a.C) * 4, st, a);
 }
 
 template <class F>
 void launch_layout(const GemvArgs& a, const GemvLaunch& g, hipStream_t st) {
   switch (GemvMode(a.mode)) {
-    case GemvMode::Store: launch_one<F, int(GemvMode::Store), 8>(a, g, st); break;
-    case GemvMode::Accum: launch_one<F, int(GemvMode::Accum), 8>(a, g, st); break;
-    case GemvMode::SwiGlu: launch_one<F, int(GemvMode::SwiGlu), 8>(a, g, st); break;
-    case GemvMode::Logits: launch_one<F, int(GemvMode::Logits), 8>(a, g, st); break;
+    case GemvMode::Store: launch_one<F, int(GemvMode::Store)>(a, g, st); break;
+    case GemvMode::Accum: launch_one<F, int(GemvMode::Accum)>(a, g, st); break;
+    case GemvMode::SwiGlu: launch_one<F, int(GemvMode::SwiGlu)>(a, g, st); break;
+    case GemvMode::Logits: launch_one<F, int(GemvMode::Logits)>(a, g, st); break;
   }
 }
 
 }  // namespace
+
+const GemvTuning& gemv_tuning() {
+  static const GemvTuning t = [] {
+    GemvTuning v;
+    if (const char* e = std::getenv("CHPE_GEMV_ROWS_BLOCKS")) v.rows_blocks = uint32_t(std::strtoul(e, nullptr, 10));
+    if (const char* e = std::getenv("CHPE_GEMV_LOGITS_BLOCKS")) v.logits_blocks = uint32_t(std::strtoul(e, nullptr, 10));
+    if (v.logits_blocks == 0 || v.logits_blocks > kMaxLogitsBlocks) v.logits_blocks = kMaxLogitsBlocks;
+    return v;
+  }();
+  return t;
+}
 
 GemvLaunch gemv_geometry(WeightKind kind, GemvMode mode, uint32_t C, const uint32_t* rows, int n_parts,
                          uint32_t* n_units, uint32_t* n_panels, uint32_t* waves_per_unit,
@@ -469,11 +580,16 @@ GemvLaunch gemv_geometry(WeightKind kind, GemvMode mode, uint32_t C, const uint3
   *n_units = units;
   GemvLaunch g{};
   g.ru = ru;
-  const uint32_t upb = nw == 1 ? 4 : 1;
-  g.threads = nw == 1 ? 256 : nw * 64;
-  g.blocks = (units + upb - 1) / upb;
-  const uint32_t cap = mode == GemvMode::Logits ? kMaxLogitsBlocks : 8192u;
-  if (g.blocks > cap) g.blocks = cap;
+  if (nw == 1) {
+    g.threads = 256;
+    g.blocks = (units + 3) / 4;
+    const uint32_t cap = mode == GemvMode::Logits ? gemv_tuning().logits_blocks : gemv_tuning().rows_blocks;
+    if (cap && g.blocks > cap) g.blocks = cap;  // persistent: the waves stride over the units
+  } else {
+    g.threads = nw * 64;
+    g.blocks = units;
+    if (mode == GemvMode::Logits && g.blocks > kMaxLogitsBlocks) g.blocks = kMaxLogitsBlocks;
+  }
   return g;
 }
 

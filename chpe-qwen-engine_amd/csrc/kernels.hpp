@@ -35,6 +35,7 @@ enum class GemvMode : int {
 };
 
 constexpr int kMaxParts = 3;
+constexpr uint32_t kMaxCorrPerRow = 128;  // flat-tile outliers per output row (two tiles' worth)
 constexpr uint32_t kMaxWavesPerUnit = 8;
 
 struct GemvPart {
@@ -45,8 +46,8 @@ struct GemvPart {
   uint32_t bf16;              // Raw16: 1 = bf16, 0 = fp16
   float* y;                   // output vector
   const float* bias;          // per-row bias (Store), may be null
-  const uint32_t* corr_ptr;   // Flat: per-row outlier corrections (CSR), may be null
-  const float2* corr;         //   (column as float bits, w_out - dequantised code)
+  const float2* corr;         // Flat: outlier corrections [rows][corr_kmax], zero-padded,
+  uint32_t corr_kmax;         //   entry = (column as float bits, w_out - dequantised code)
   uint32_t replace_outliers;  // Cell16W4: outliers replace (tied LM head) instead of add
   const struct CellReplace* repl;  // Cell16W4 replace mode: per-cell corrections (see below)
 };
@@ -141,6 +142,15 @@ struct FinishArgs {
   uint32_t* out_tokens;     // argmax of every step, indexed by position
 };
 
+// Workgroup caps of the one-unit-per-wave GEMV (0 = one unit per wave, no cap); the waves of
+// a capped grid stride over the remaining units.  Defaults, overridable for measurement by
+// CHPE_GEMV_ROWS_BLOCKS / CHPE_GEMV_LOGITS_BLOCKS.
+struct GemvTuning {
+  uint32_t rows_blocks = 0;
+  uint32_t logits_blocks = 2048;
+};
+const GemvTuning& gemv_tuning();
+
 // Launch geometry: work units, panels and the K-split for a GEMV over `rows[n_parts]` rows of
 // C columns; `ru` rows per unit.
 GemvLaunch gemv_geometry(WeightKind kind, GemvMode mode, uint32_t C, const uint32_t* rows,
@@ -159,7 +169,7 @@ __host__ __device__ constexpr uint32_t attn_chunk_of(uint32_t hd) { return 16384
 inline uint32_t attn_chunk(uint32_t hd) { return attn_chunk_of(hd); }
 // (hd, query heads per kv head) pairs the attention kernels are built for
 bool attention_supported(uint32_t H, uint32_t KV, uint32_t hd);
-constexpr uint32_t kMaxLogitsBlocks = 1024;
+constexpr uint32_t kMaxLogitsBlocks = 8192;
 
 // Measurement: the next kernel launched by any launcher on this host thread records `start`
 // and `stop` when it begins and ends (hipExtLaunchKernelGGL), then the probe is cleared.
