@@ -32,12 +32,13 @@ struct Cell16W4 {  // gemvTileW4 over 16x2048 group-128 cells (chpe_engine.zig:3
     return true;
   }
   __device__ static void locate(const GemvPart& P, uint32_t r, uint32_t, int lane, uint32_t, uint4* q,
-                                float* s) {
+                                uint32_t* s) {
     const uint8_t* cell = P.base + size_t(r >> 4) * P.stride;
     const uint32_t n = r & 15;
     *q = ld_u128(cell + 64 + n * 1024 + lane * 16);
-    *s = h2f(ld_u16(cell + 16448 + 48 + 2 * (n * 16 + (lane >> 2))));
+    *s = ld_u16(cell + 16448 + 48 + 2 * (n * 16 + (lane >> 2)));
   }
+  __device__ static float scale(uint32_t s) { return h2f(uint16_t(s)); }
   __device__ static float dot(uint4 q, const float* x, bool) { return dot32_w4(q, x); }
 };
 
@@ -50,13 +51,14 @@ struct FlatW4 {  // gemvCellFlat, 4-bit group-128 (chpe_engine.zig:584-729)
     return g < (C >> 7);
   }
   __device__ static void locate(const GemvPart& P, uint32_t r, uint32_t p, int lane, uint32_t C, uint4* q,
-                                float* s) {
+                                uint32_t* s) {
     const uint64_t G = uint64_t(r) * (C >> 7) + p * 16 + (lane >> 2);
     const uint8_t* cp = P.base + (G >> 8) * P.stride;
     const uint32_t gi = uint32_t(G & 255u);
     *q = ld_u128(cp + 64 + gi * 64 + (lane & 3) * 16);
-    *s = h2f(ld_u16(cp + 16448 + 48 + 2 * gi));
+    *s = ld_u16(cp + 16448 + 48 + 2 * gi);
   }
+  __device__ static float scale(uint32_t s) { return h2f(uint16_t(s)); }
   __device__ static float dot(uint4 q, const float* x, bool) { return dot32_w4(q, x); }
 };
 
@@ -69,13 +71,14 @@ struct FlatW2 {  // gemvCellFlat, 2-bit group-128
     return g < (C >> 7);
   }
   __device__ static void locate(const GemvPart& P, uint32_t r, uint32_t p, int lane, uint32_t C, uint4* q,
-                                float* s) {
+                                uint32_t* s) {
     const uint64_t G = uint64_t(r) * (C >> 7) + p * 32 + (lane >> 1);
     const uint8_t* cp = P.base + (G >> 8) * P.stride;
     const uint32_t gi = uint32_t(G & 255u);
     *q = ld_u128(cp + 64 + gi * 32 + (lane & 1) * 16);
-    *s = h2f(ld_u16(cp + 16448 + 48 + 2 * gi));
+    *s = ld_u16(cp + 16448 + 48 + 2 * gi);
   }
+  __device__ static float scale(uint32_t s) { return h2f(uint16_t(s)); }
   __device__ static float dot(uint4 q, const float* x, bool) { return dot64_w2(q, x); }
 };
 
@@ -87,10 +90,11 @@ struct Raw16 {  // raw fp16 / bf16 tiles read as one row-major matrix (dotSegmen
     return *c0 < C;
   }
   __device__ static void locate(const GemvPart& P, uint32_t r, uint32_t p, int lane, uint32_t C, uint4* q,
-                                float* s) {
+                                uint32_t* s) {
     *q = ld_u128(P.base + (uint64_t(r) * C + p * 512 + lane * 8) * 2);
-    *s = 1.0f;
+    *s = 0;
   }
+  __device__ static float scale(uint32_t) { return 1.0f; }
   __device__ static float dot(uint4 q, const float* x, bool bf16) { return dot8_f16(q, x, bf16); }
 };
 
@@ -101,37 +105,56 @@ __device__ __forceinline__ int part_of(const GemvArgs& a, uint32_t unit) {
 }
 
 // ---- per-unit terms outside the dense codes, loaded together with the weights -----------
-// 16-row cells: lane k < 8 holds entry k of the cell's outlier list: its column and its
-// weight for each of the unit's rows (added, gemvTileW4 :404-410), or for the tied LM head the
-// prepared (column, w_out - dequantised code) that makes the outlier replace the weight
-// (unpackEmbedRowCell :1369-1378).  Lanes 8.. mirror lanes 0..7 and add nothing.
+// 16-row cells: lane i < RU serves unit row i: the 8 outlier columns of the row's cell and the
+// row's 8 outlier weights (added, gemvTileW4 :404-410), or for the tied LM head the prepared
+// (column, w_out - dequantised code) that makes the outlier replace the weight
+// (unpackEmbedRowCell :1369-1378).  Two 16-byte loads (three for the replace table) per lane.
 template <int RU>
 struct CellExtras {
-  uint32_t colA, colB;  // SwiGlu: A = gate cell, B = up cell
-  float w[RU];
+  uint4 cols;     // 8 u16 columns
+  uint4 w0, w1;   // 8 fp16 weights (w0), or 8 f32 replace corrections (w0, w1)
+  bool valid;
 };
 
 template <class F, int RU, bool kSwi, bool kReplace>
 __device__ __forceinline__ void load_cell_extras(const GemvPart& P0, const GemvPart& P1, uint32_t row_base,
                                                  int lane, CellExtras<RU>* e) {
-  const int k = lane & 7;
+  // every lane loads (lanes >= RU and rows past the end read row 0 of the part); the values
+  // are decoded where they are used, so the loads stay in flight together with the codes
+  const int i = lane;
+  const GemvPart& P = (kSwi && i >= RU / 2) ? P1 : P0;
+  const uint32_t r = row_base + uint32_t(kSwi ? i % (RU / 2) : i);
+  e->valid = i < RU && r < P.rows;
+  const uint32_t rr = e->valid ? r : 0u;
   if constexpr (kReplace) {
-    const CellReplace& R = P0.repl[row_base >> 4];
-    e->colA = e->colB = R.col[k];
-#pragma unroll
-    for (int i = 0; i < RU; ++i) e->w[i] = R.delta[(row_base + uint32_t(i)) & 15][k];
+    const CellReplace* R = P.repl + (rr >> 4);
+    e->cols = *reinterpret_cast<const uint4*>(R->col);
+    const uint4* d = reinterpret_cast<const uint4*>(R->delta[rr & 15]);
+    e->w0 = d[0];
+    e->w1 = d[1];
   } else {
-    const uint8_t* cA = P0.base + size_t(row_base >> 4) * P0.stride;
-    const uint8_t* cB = P1.base + size_t(row_base >> 4) * P1.stride;
-    e->colA = ld_u16(cA + 16448 + 816 + 2 * k);
-    e->colB = kSwi ? ld_u16(cB + 16448 + 816 + 2 * k) : e->colA;
-#pragma unroll
-    for (int i = 0; i < RU; ++i) {
-      const uint8_t* c = (kSwi && i >= RU / 2) ? cB : cA;
-      const uint32_t n = (row_base + uint32_t(kSwi ? i % (RU / 2) : i)) & 15;
-      e->w[i] = h2f(ld_u16(c + 16448 + 560 + 2 * (n * 8 + k)));
-    }
+    const uint8_t* cell = P.base + size_t(rr >> 4) * P.stride;
+    e->cols = ld_u128(cell + 16448 + 816);
+    e->w0 = ld_u128(cell + 16448 + 560 + (rr & 15) * 16);
+    e->w1 = e->w0;
   }
+}
+
+// sum_k w[k] * x[col_k] of the lane's row (0 on lanes >= RU)
+template <bool kReplace>
+__device__ __forceinline__ float cell_outlier_sum(const CellExtras<8>& e, const float* s_x, uint32_t C) {
+  const uint32_t cw[4] = {e.cols.x, e.cols.y, e.cols.z, e.cols.w};
+  const uint32_t w0[4] = {e.w0.x, e.w0.y, e.w0.z, e.w0.w}, w1[4] = {e.w1.x, e.w1.y, e.w1.z, e.w1.w};
+  float o = 0.0f;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const uint32_t c = (k & 1) ? (cw[k >> 1] >> 16) : (cw[k >> 1] & 0xffffu);
+    float w;
+    if constexpr (kReplace) w = __uint_as_float(k < 4 ? w0[k] : w1[k - 4]);
+    else w = (k & 1) ? half_hi(w0[k >> 1]) : half_lo(w0[k >> 1]);
+    if (c < C) o = fmaf(w, s_x[c], o);
+  }
+  return e.valid ? o : 0.0f;
 }
 
 // Flat tiles: outliers replace weights (gemvCellFlat :632-646), applied as per-row corrections
@@ -282,7 +305,8 @@ struct UnitLoads {
   uint32_t unit, row_base;
   int pu;
   uint4 q[RU];
-  float s[RU];
+  uint32_t s[RU];  // raw scale bits
+  uint32_t vm;     // bit i: row i of the unit is present
   std::conditional_t<kCell, CellExtras<RU>, NoExtras> ce;
   std::conditional_t<kFlat, FlatExtras, NoExtras> fe;
   float pre;
@@ -290,21 +314,37 @@ struct UnitLoads {
 
 template <class F, int MODE>
 __device__ __forceinline__ void issue_panel(const GemvArgs& a, const GemvPart& P0, const GemvPart& P1, bool active,
-                                            uint32_t row_base, uint32_t p, int lane, uint4 (&q)[8], float (&s)[8]) {
+                                            uint32_t row_base, uint32_t p, int lane, uint4 (&q)[8], uint32_t (&s)[8],
+                                            uint32_t* vm) {
+  // branch-free: absent rows / lanes read row 0 / panel 0 and are masked out in the sum
   constexpr int RU = 8;
   constexpr bool kSwi = MODE == int(GemvMode::SwiGlu);
   uint32_t c0;
-  const bool v = active && F::lane_cols(p, lane, a.C, &c0);
+  const bool lv = active && F::lane_cols(p, lane, a.C, &c0);
+  uint32_t m = 0;
 #pragma unroll
   for (int i = 0; i < RU; ++i) {
     const GemvPart& P = row_part<RU, kSwi>(P0, P1, i);
     const uint32_t r = row_of<RU, kSwi>(row_base, i);
-    if (v && r < P.rows) {
-      F::locate(P, r, p, lane, a.C, &q[i], &s[i]);
-    } else {
-      q[i] = make_uint4(0, 0, 0, 0);
-      s[i] = 0.0f;
-    }
+    const bool ok = lv && r < P.rows;
+    F::locate(P, ok ? r : 0u, ok ? p : 0u, lane, a.C, &q[i], &s[i]);
+    m |= uint32_t(ok) << i;
+  }
+  *vm = m;
+}
+
+// sum of the panel's dense terms into acc
+template <class F, int MODE>
+__device__ __forceinline__ void panel_math(const GemvPart& P0, const GemvPart& P1, const uint4 (&q)[8],
+                                           const uint32_t (&s)[8], uint32_t vm, const float* x, float sx,
+                                           float (&acc)[8]) {
+  constexpr int RU = 8;
+  constexpr bool kSwi = MODE == int(GemvMode::SwiGlu);
+#pragma unroll
+  for (int i = 0; i < RU; ++i) {
+    const GemvPart& P = row_part<RU, kSwi>(P0, P1, i);
+    const float t = (F::dot(q[i], x, P.bf16 != 0) - F::kOff * sx) * F::scale(s[i]);
+    acc[i] += ((vm >> i) & 1u) ? t : 0.0f;
   }
 }
 
@@ -334,7 +374,7 @@ __device__ __forceinline__ void issue_unit(const GemvArgs& a, uint32_t unit, uin
     if (with_pre && active && (lane % S) == 0 && own < P0.rows)
       u->pre = MODE == int(GemvMode::Accum) ? P0.y[own] : (P0.bias ? P0.bias[own] : 0.0f);
   }
-  issue_panel<F, MODE>(a, P0, P1, active, u->row_base, p, lane, u->q, u->s);
+  issue_panel<F, MODE>(a, P0, P1, active, u->row_base, p, lane, u->q, u->s, &u->vm);
 }
 
 // final value v of unit row i (lane-owned): SwiGlu pairs gate row i with up row i + RU/2
@@ -412,33 +452,20 @@ __global__ void __launch_bounds__(512, 2) k_gemv_rows(GemvArgs a) {
     const GemvPart& P1 = a.part[kSwi ? 1 : cur.pu];
     float acc[RU];
 #pragma unroll
-    for (int i = 0; i < RU; ++i) {
-      const GemvPart& P = row_part<RU, kSwi>(P0, P1, i);
-      acc[i] = (F::dot(cur.q[i], x0, P.bf16 != 0) - F::kOff * sx0) * cur.s[i];
-    }
-    if constexpr (!kOnePanel) {  // further panels (raw tiles): loads of panel p+1 ahead of p's math
+    for (int i = 0; i < RU; ++i) acc[i] = 0.0f;
+    panel_math<F, MODE>(P0, P1, cur.q, cur.s, cur.vm, x0, sx0, acc);
+    if constexpr (!kOnePanel) {  // further panels (raw tiles)
       uint4 qn[RU];
-      float sn[RU];
+      uint32_t sn[RU], vn;
       for (uint32_t p = 1; p < a.n_panels; ++p) {
-        issue_panel<F, MODE>(a, P0, P1, true, cur.row_base, p, lane, qn, sn);
+        issue_panel<F, MODE>(a, P0, P1, cur.unit < a.n_units, cur.row_base, p, lane, qn, sn, &vn);
         float xr[F::kCols];
         const float sx = lds_chunk<F>(s_x, a.C, p, lane, xr);
-#pragma unroll
-        for (int i = 0; i < RU; ++i) {
-          const GemvPart& P = row_part<RU, kSwi>(P0, P1, i);
-          acc[i] += (F::dot(qn[i], xr, P.bf16 != 0) - F::kOff * sx) * sn[i];
-        }
-      }
-    }
-    if constexpr (U::kCell) {  // outlier terms (lanes 0..7)
-      const float xoA = cur.ce.colA < a.C ? s_x[cur.ce.colA] : 0.0f;
-      const float xoB = kSwi ? (cur.ce.colB < a.C ? s_x[cur.ce.colB] : 0.0f) : xoA;
-      if (lane < 8) {
-#pragma unroll
-        for (int i = 0; i < RU; ++i) acc[i] = fmaf(cur.ce.w[i], (kSwi && i >= RU / 2) ? xoB : xoA, acc[i]);
+        panel_math<F, MODE>(P0, P1, qn, sn, vn, xr, sx, acc);
       }
     }
     float tot = wave_reduce_rows<RU>(acc, lane);  // lane l: row l / S of the unit
+    if constexpr (U::kCell) tot += __shfl(cell_outlier_sum<kLogits>(cur.ce, s_x, a.C), lane / S);
     if constexpr (U::kFlat) tot += flat_correction(cur.fe, s_x);
     const int i = lane / S;
     const float up = kSwi ? __shfl(tot, (lane + 32) & 63) : 0.0f;  // up row i: 32 lanes above gate row i
@@ -494,14 +521,10 @@ __global__ void __launch_bounds__(512, 2) k_gemv_split(GemvArgs a) {
 #pragma unroll
     for (int i = 0; i < RU; ++i) acc[i] = 0.0f;
     for (uint32_t p = p0; p < p1; ++p) {
-      if (p != p0) issue_panel<F, MODE>(a, P0, P1, true, cur.row_base, p, lane, cur.q, cur.s);
+      if (p != p0) issue_panel<F, MODE>(a, P0, P1, unit < a.n_units, cur.row_base, p, lane, cur.q, cur.s, &cur.vm);
       float xr[F::kCols];
       const float sx = lds_chunk<F>(s_x, a.C, p, lane, xr);
-#pragma unroll
-      for (int i = 0; i < RU; ++i) {
-        const GemvPart& P = row_part<RU, kSwi>(P0, P1, i);
-        acc[i] += (F::dot(cur.q[i], xr, P.bf16 != 0) - F::kOff * sx) * cur.s[i];
-      }
+      panel_math<F, MODE>(P0, P1, cur.q, cur.s, cur.vm, xr, sx, acc);
     }
     const float tot = wave_reduce_rows<RU>(acc, lane);
     if (lane % S == 0) s_part[wave][lane / S] = tot;
