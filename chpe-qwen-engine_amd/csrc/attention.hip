@@ -1,25 +1,19 @@
-// attention.hip -- RoPE + KV append + GQA decode attention over the HBM KV cache.
+// attention.hip -- GQA decode attention over the HBM KV cache.
 //
-// Semantics: applyRope (chpe_engine.zig:195-216), KV write at `pos` (:1693-1697) and the
-// per-head attention loop (:1700-1734): scores (q.k_t)*scale, softmax over t <= pos, output
-// sum_t softmax_t * v_t.  The context is split into chunks of attn_chunk(hd) positions
-// (16384/hd: 128 at hd 128): k_attn_chunk computes, per chunk and query head, the chunk max,
-// the sum of exp(s - max) and the exp-weighted sum of the V rows; k_attn_merge rescales and
-// merges the chunks.  Workgroup (chunk, kv head) serves the query heads that share the kv
-// head, so every K/V row is read from HBM once per step.  The workgroup holding `pos` rotates
-// the new K row, rounds K/V to the cache type, stores them and uses the stored values.
+// Semantics: the per-head attention loop of forwardDecode (chpe_engine.zig:1700-1734): scores
+// (q.k_t)*scale, softmax over t <= pos, output sum_t softmax_t * v_t.  RoPE and the KV append
+// at `pos` (:1688-1697) are done by the q/k/v projection's epilogue (GemvMode::QkvRope), so
+// the queries arrive rotated and cache rows 0..pos are complete.  The context is split into
+// chunks of attn_chunk(hd) positions (16384/hd: 128 at hd 128): k_attn_chunk computes, per
+// chunk and query head, the chunk max, the sum of exp(s - max) and the exp-weighted sum of the
+// V rows; k_attn_merge rescales and merges the chunks.  Workgroup (chunk, kv head) serves the
+// query heads that share the kv head, so every K/V row is read from HBM once per step.
 #include "device_common.hpp"
 #include "kernels.hpp"
 
 namespace chpe {
 namespace {
 using namespace dev;
-
-// x0*cos - x1*sin / x0*sin + x1*cos without contraction, as applyRope (:212-213)
-__device__ __forceinline__ float rope_rot(float x0, float x1, float c, float s, bool first) {
-#pragma clang fp contract(off)
-  return first ? x0 * c - x1 * s : x0 * s + x1 * c;
-}
 
 // Cache element access: fp16 or f32 KV cache.
 template <typename T> struct KvElem;
@@ -28,34 +22,25 @@ template <> struct KvElem<__half> {
   __device__ static float get(const uint32_t* w, int i) {
     return (i & 1) ? half_hi(w[i >> 1]) : half_lo(w[i >> 1]);
   }
-  __device__ static float round(float x) { return __half2float(__float2half_rn(x)); }
-  __device__ static void put(void* cache, size_t at, float x) {
-    reinterpret_cast<__half*>(cache)[at] = __float2half_rn(x);
-  }
-  __device__ static void set(uint32_t* w, int i, float x) {
-    const uint32_t h = __half_as_ushort(__float2half_rn(x));
-    w[i >> 1] = (i & 1) ? ((w[i >> 1] & 0xffffu) | (h << 16)) : ((w[i >> 1] & 0xffff0000u) | h);
-  }
 };
 template <> struct KvElem<float> {
   static constexpr int kBytes = 4;
   __device__ static float get(const uint32_t* w, int i) { return __uint_as_float(w[i]); }
-  __device__ static float round(float x) { return x; }
-  __device__ static void put(void* cache, size_t at, float x) { reinterpret_cast<float*>(cache)[at] = x; }
-  __device__ static void set(uint32_t* w, int i, float x) { w[i] = __float_as_uint(x); }
 };
 
-// One workgroup = 4 waves = one chunk of CH = 4 * PW positions of one kv head, for the GQ
-// query heads that share it.  In a wave, LPP = HD/64 lanes hold one position's K row (64 dims
-// each) for the q.k dots, and every lane holds HD/64 dims of every V row of the wave's PW
-// positions for the weighted sum; all K/V loads of a wave are issued before any arithmetic.
-// The softmax statistics are per wave, merged over the 4 waves in LDS; one partial
-// (max, sum, weighted V sum) per chunk and query head goes to HBM for k_attn_merge.
-template <int HD, int GQ, typename KT>
-__global__ void __launch_bounds__(256) k_attn_chunk(AttnArgs a) {
+// One workgroup = NW waves = one chunk of CH = NW * PW positions of one kv head, for the GQ
+// query heads that share it.  In a wave, LPP lanes hold one position's K row (DK = HD/LPP dims
+// each) for the q.k dots, and every lane holds HD/64 dims of every V row of the wave's
+// PW = 64/LPP positions for the weighted sum; all K/V loads of a wave are issued before any
+// arithmetic.  The softmax statistics are per wave, merged over the NW waves in LDS; one
+// partial (max, sum, weighted V sum) per chunk and query head goes to HBM for k_attn_merge.
+template <int HD, int GQ, typename KT, int LPP, int NW>
+__global__ void __launch_bounds__(NW * 64) k_attn_chunk(AttnArgs a) {
   using E = KvElem<KT>;
-  constexpr int NW = 4, LPP = HD / 64, PW = 64 / LPP, CH = NW * PW, HALF = HD / 2;
-  constexpr int KW = 64 * E::kBytes / 4;    // 32-bit words of a lane's 64 K dims
+  constexpr int PW = 64 / LPP, CH = NW * PW, NT = NW * 64;
+  constexpr int DK = HD / LPP;               // K dims per lane
+  static_assert(CH == int(attn_chunk_of(HD)) && DK % 4 == 0, "");
+  constexpr int KW = DK * E::kBytes / 4;    // 32-bit words of a lane's K dims
   constexpr int DPL = HD / 64;              // V dims per lane
   constexpr int VW = DPL * E::kBytes / 4;   // 32-bit words of a lane's V dims (1, 2 or 4)
   static_assert(KW % 4 == 0 && VW >= 1, "");
@@ -64,13 +49,18 @@ __global__ void __launch_bounds__(256) k_attn_chunk(AttnArgs a) {
   if (c * CH >= ctx) return;  // the whole workgroup
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
 
-  __shared__ __align__(16) float qs[GQ][LPP][68];  // rotated queries; padding spreads banks
+  __shared__ __align__(16) float qs[GQ][LPP][DK + 4];  // rotated queries; padding spreads banks
   __shared__ __align__(16) float ps[NW][PW][GQ];   // exp(s - m) per wave
   __shared__ __align__(16) float s_acc[NW][GQ][HD];
   __shared__ float s_ml[NW][GQ][2];
-  __shared__ float s_newk[HD], s_newv[HD];
 
-  // 1. the wave's K and V rows straight from HBM
+  // 1. the rotated queries of the group, then the wave's K and V rows (row `pos` was appended by
+  // the q/k/v projection); all loads are issued before any value is used, and rows past the
+  // context read row 0 and are masked at use
+  constexpr int QPT = GQ * HD / NT;  // query elements per thread
+  float qv[QPT];
+#pragma unroll
+  for (int k = 0; k < QPT; ++k) qv[k] = a.q[size_t(kvh * GQ) * HD + tid + NT * k];
   const uint32_t tw0 = c * CH + wave * PW;
   const uint32_t t = tw0 + lane / LPP;
   const int grp = lane % LPP;
@@ -78,78 +68,43 @@ __global__ void __launch_bounds__(256) k_attn_chunk(AttnArgs a) {
   const uint8_t* kc = reinterpret_cast<const uint8_t*>(a.k_cache) + head * E::kBytes;
   const uint8_t* vc = reinterpret_cast<const uint8_t*>(a.v_cache) + head * E::kBytes;
   uint32_t kw[KW];
-  if (t < ctx && t != pos) {
-    const uint8_t* src = kc + (size_t(t) * HD + grp * 64) * E::kBytes;
+  {
+    const uint32_t tk = t < ctx ? t : 0u;
+    const uint8_t* src = kc + (size_t(tk) * HD + grp * DK) * E::kBytes;
 #pragma unroll
     for (int i = 0; i < KW / 4; ++i) {
       const uint4 v = ld_u128(src + 16 * i);
       kw[4 * i] = v.x; kw[4 * i + 1] = v.y; kw[4 * i + 2] = v.z; kw[4 * i + 3] = v.w;
     }
-  } else {
-#pragma unroll
-    for (int i = 0; i < KW; ++i) kw[i] = 0u;
   }
   uint32_t vw[PW][VW];
 #pragma unroll
   for (int j = 0; j < PW; ++j) {
-    const uint32_t tj = tw0 + j;
+    const uint32_t tj = tw0 + j < ctx ? tw0 + j : 0u;
     const uint8_t* src = vc + (size_t(tj) * HD + lane * DPL) * E::kBytes;
-    if (tj < ctx && tj != pos) {
-      if constexpr (VW == 1) {
-        vw[j][0] = *reinterpret_cast<const uint32_t*>(src);
-      } else if constexpr (VW == 2) {
-        const uint2 v = *reinterpret_cast<const uint2*>(src);
-        vw[j][0] = v.x; vw[j][1] = v.y;
-      } else {
-        const uint4 v = ld_u128(src);
-        vw[j][0] = v.x; vw[j][1] = v.y; vw[j][2] = v.z; vw[j][3] = v.w;
-      }
+    if constexpr (VW == 1) {
+      vw[j][0] = *reinterpret_cast<const uint32_t*>(src);
+    } else if constexpr (VW == 2) {
+      const uint2 v = *reinterpret_cast<const uint2*>(src);
+      vw[j][0] = v.x; vw[j][1] = v.y;
     } else {
-#pragma unroll
-      for (int i = 0; i < VW; ++i) vw[j][i] = 0u;
+      const uint4 v = ld_u128(src);
+      vw[j][0] = v.x; vw[j][1] = v.y; vw[j][2] = v.z; vw[j][3] = v.w;
     }
   }
-
-  // 2. rotated queries (applyRope, chpe_engine.zig:195-216) and, in the workgroup that holds
-  // `pos`, the new K/V row: rotated, rounded to the cache type, stored (:1693-1697)
-  const float* cs = a.rope_cos + size_t(pos) * HALF;
-  const float* sn = a.rope_sin + size_t(pos) * HALF;
-  for (int i = tid; i < GQ * HD; i += 256) {
-    const int g = i / HD, d = i % HD, j = d % HALF;
-    const float* q = a.q_raw + size_t(kvh * GQ + g) * HD;
-    qs[g][d / 64][d % 64] = rope_rot(q[j], q[j + HALF], cs[j], sn[j], d < HALF);
-  }
-  const bool has_new = pos / CH == c;
-  if (has_new && tid < HD) {
-    const int d = tid, j = d % HALF;
-    const float* k = a.k_raw + size_t(kvh) * HD;
-    const float kr = E::round(rope_rot(k[j], k[j + HALF], cs[j], sn[j], d < HALF));
-    const float vr = E::round(a.v_raw[size_t(kvh) * HD + d]);
-    E::put(a.k_cache, head + size_t(pos) * HD + d, kr);
-    E::put(a.v_cache, head + size_t(pos) * HD + d, vr);
-    s_newk[d] = kr;
-    s_newv[d] = vr;
+#pragma unroll
+  for (int k = 0; k < QPT; ++k) {
+    const int i = tid + NT * k, g = i / HD, d = i % HD;
+    qs[g][d / DK][d % DK] = qv[k];
   }
   __syncthreads();
-  if (has_new) {
-    if (t == pos) {
-#pragma unroll
-      for (int r = 0; r < 64; ++r) E::set(kw, r, s_newk[grp * 64 + r]);
-    }
-#pragma unroll
-    for (int j = 0; j < PW; ++j)
-      if (tw0 + j == pos) {
-#pragma unroll
-        for (int dd = 0; dd < DPL; ++dd) E::set(vw[j], dd, s_newv[lane * DPL + dd]);
-      }
-  }
 
-  // 3. scores s = (q . k) * scale over the lane's 64 dims, summed over the LPP lanes
+  // 3. scores s = (q . k) * scale over the lane's DK dims, summed over the LPP lanes
   float s[GQ];
 #pragma unroll
   for (int g = 0; g < GQ; ++g) s[g] = 0.0f;
 #pragma unroll
-  for (int r4 = 0; r4 < 16; ++r4) {
+  for (int r4 = 0; r4 < DK / 4; ++r4) {
     float kf[4];
 #pragma unroll
     for (int e = 0; e < 4; ++e) kf[e] = E::get(kw, 4 * r4 + e);
@@ -200,9 +155,10 @@ __global__ void __launch_bounds__(256) k_attn_chunk(AttnArgs a) {
       const float4 v = *reinterpret_cast<const float4*>(&ps[wave][j][4 * g4]);
       p[4 * g4] = v.x; p[4 * g4 + 1] = v.y; p[4 * g4 + 2] = v.z; p[4 * g4 + 3] = v.w;
     }
+    const bool vj = tw0 + j < ctx;
 #pragma unroll
     for (int dd = 0; dd < DPL; ++dd) {
-      const float v = E::get(vw[j], dd);
+      const float v = vj ? E::get(vw[j], dd) : 0.0f;
 #pragma unroll
       for (int g = 0; g < GQ; ++g) acc[g][dd] = fmaf(p[g], v, acc[g][dd]);
     }
@@ -217,7 +173,7 @@ __global__ void __launch_bounds__(256) k_attn_chunk(AttnArgs a) {
 
   // 6. merge the waves; one partial per (query head, chunk)
   const uint32_t nch = a.n_chunks;
-  for (int i = tid; i < GQ * HD; i += 256) {
+  for (int i = tid; i < GQ * HD; i += NT) {
     const int g = i / HD, d = i % HD;
     float M = s_ml[0][g][0];
 #pragma unroll
@@ -248,8 +204,19 @@ __global__ void __launch_bounds__(512) k_attn_merge(AttnArgs a) {
   __shared__ float s_red[NT / 64];
   __shared__ float s_o[P][HD];
   const float* ml = a.part_ml + size_t(h) * nch * 2;
-  float m = -INFINITY;
-  for (uint32_t i = tid; i < n_act; i += NT) m = fmaxf(m, ml[2 * i]);
+  const int d = tid % HD, part = tid / HD;
+  const float* acc = a.part_acc + size_t(h) * nch * HD + d;
+  // every load first: the thread's chunk sums, and (one chunk per thread) the chunk statistics
+  constexpr int kPer = int(kAttnMaxChunks) / P;  // chunks per thread at most
+  float av[kPer];
+#pragma unroll
+  for (int k = 0; k < kPer; ++k) {
+    const uint32_t j = uint32_t(part + k * P);
+    av[k] = j < n_act ? acc[size_t(j) * HD] : 0.0f;
+  }
+  const bool mine = uint32_t(tid) < n_act;  // n_act <= kAttnMaxChunks <= NT
+  const float mi = mine ? ml[2 * tid] : -INFINITY, li = mine ? ml[2 * tid + 1] : 0.0f;
+  float m = mi;
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
   if (lane == 0) s_red[wave] = m;
@@ -258,23 +225,20 @@ __global__ void __launch_bounds__(512) k_attn_merge(AttnArgs a) {
 #pragma unroll
   for (int w = 1; w < NT / 64; ++w) M = fmaxf(M, s_red[w]);
   __syncthreads();
-  float l = 0.0f;
-  for (uint32_t i = tid; i < n_act; i += NT) {
-    const float w = expf(ml[2 * i] - M);
-    s_w[i] = w;
-    l = fmaf(ml[2 * i + 1], w, l);
-  }
-  l = wave_sum(l);
+  const float wi = mine ? expf(mi - M) : 0.0f;
+  if (mine) s_w[tid] = wi;
+  const float l = wave_sum(li * wi);
   if (lane == 0) s_red[wave] = l;
   __syncthreads();
   float L = 0.0f;
 #pragma unroll
   for (int w = 0; w < NT / 64; ++w) L += s_red[w];
-  const int d = tid % HD, part = tid / HD;
-  const float* acc = a.part_acc + size_t(h) * nch * HD + d;
   float o = 0.0f;
-#pragma unroll 4
-  for (uint32_t j = part; j < n_act; j += P) o = fmaf(acc[size_t(j) * HD], s_w[j], o);
+#pragma unroll
+  for (int k = 0; k < kPer; ++k) {
+    const uint32_t j = uint32_t(part + k * P);
+    if (j < n_act) o = fmaf(av[k], s_w[j], o);
+  }
   s_o[part][d] = o;
   __syncthreads();
   if (part == 0) {
@@ -288,14 +252,14 @@ __global__ void __launch_bounds__(512) k_attn_merge(AttnArgs a) {
 }  // namespace
 
 void launch_attention_partial(const AttnArgs& a, hipStream_t st) {
-  const dim3 grid(a.n_chunks, a.KV), block(256);
+  const dim3 grid(a.n_chunks, a.KV);
   const uint32_t gq = a.H / a.KV;
-  if (a.hd == 128 && gq == 8)
-    a.kv_f16 ? launch_kernel(&k_attn_chunk<128, 8, __half>, grid, block, st, a)
-             : launch_kernel(&k_attn_chunk<128, 8, float>, grid, block, st, a);
-  else if (a.hd == 256 && gq == 4)
-    a.kv_f16 ? launch_kernel(&k_attn_chunk<256, 4, __half>, grid, block, st, a)
-             : launch_kernel(&k_attn_chunk<256, 4, float>, grid, block, st, a);
+  if (a.hd == 128 && gq == 8)  // 8 waves x 16 positions, 4 lanes per K row
+    a.kv_f16 ? launch_kernel(&k_attn_chunk<128, 8, __half, 4, 8>, grid, dim3(512), st, a)
+             : launch_kernel(&k_attn_chunk<128, 8, float, 4, 8>, grid, dim3(512), st, a);
+  else if (a.hd == 256 && gq == 4)  // 4 waves x 16 positions, 4 lanes per K row
+    a.kv_f16 ? launch_kernel(&k_attn_chunk<256, 4, __half, 4, 4>, grid, dim3(256), st, a)
+             : launch_kernel(&k_attn_chunk<256, 4, float, 4, 4>, grid, dim3(256), st, a);
 }
 
 void launch_attention_combine(const AttnArgs& a, hipStream_t st) {

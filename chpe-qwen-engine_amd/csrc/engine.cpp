@@ -473,8 +473,10 @@ bool Engine::plan_lm_head(std::string* err) {
 }
 
 uint32_t Engine::enqueue_gemv(const ProjPlan* const* parts, float* const* outs, int n, GemvMode mode,
-                              const float* x, uint32_t C, const float* gamma, hipStream_t st) {
+                              const float* x, uint32_t C, const float* gamma, hipStream_t st,
+                              const RopeArgs* rope, const uint32_t* roles) {
   GemvArgs a{};
+  if (rope) a.rope = *rope;
   a.n_parts = n;
   a.mode = int(mode);
   a.C = C;
@@ -499,6 +501,7 @@ uint32_t Engine::enqueue_gemv(const ProjPlan* const* parts, float* const* outs, 
     gp.corr = p.corr;
     gp.replace_outliers = p.replace_outliers;
     gp.repl = p.repl;
+    gp.rope_role = roles ? roles[i] : 0u;
   }
   if (mode == GemvMode::Logits) {
     a.partials = d_partials_;
@@ -508,16 +511,36 @@ uint32_t Engine::enqueue_gemv(const ProjPlan* const* parts, float* const* outs, 
   return g.blocks;
 }
 
-void Engine::enqueue_qkv(const LayerPlan& L, hipStream_t st) {
-  // q, k, v in one launch when they share a layout (each part writes its own output + bias)
+void Engine::enqueue_qkv(size_t l, hipStream_t st) {
+  // q, k, v in one launch when they share a layout: bias, RoPE on q and k, k and v appended to
+  // the layer's KV cache at the step's position, q (rotated) into d_q_
+  const LayerPlan& L = layers_[l];
   const uint32_t D = uint32_t(arch_.hidden_dim);
   const ProjPlan* qkv[3] = {&L.q, &L.k, &L.v};
   float* outs[3] = {d_q_, d_k_, d_v_};
+  const uint32_t roles[3] = {kRoleQ, kRoleK, kRoleV};
+  const RopeArgs rope = rope_args(l);
   if (L.q.kind == L.k.kind && L.k.kind == L.v.kind) {
-    enqueue_gemv(qkv, outs, 3, GemvMode::Store, d_hidden_, D, L.gamma_in, st);
+    enqueue_gemv(qkv, outs, 3, GemvMode::QkvRope, d_hidden_, D, L.gamma_in, st, &rope, roles);
   } else {
-    for (int i = 0; i < 3; ++i) enqueue_gemv(&qkv[i], &outs[i], 1, GemvMode::Store, d_hidden_, D, L.gamma_in, st);
+    for (int i = 0; i < 3; ++i)
+      enqueue_gemv(&qkv[i], &outs[i], 1, GemvMode::QkvRope, d_hidden_, D, L.gamma_in, st, &rope, &roles[i]);
   }
+}
+
+RopeArgs Engine::rope_args(size_t l) const {
+  const size_t kvd = arch_.num_kv_heads * arch_.head_dim, S = cfg_.max_seq_len;
+  const size_t kv_elem = cfg_.kv_f16 ? 2 : 4;
+  RopeArgs r{};
+  r.state = d_state_;
+  r.cos = d_rope_cos_;
+  r.sin = d_rope_sin_;
+  r.k_cache = static_cast<uint8_t*>(d_kcache_) + l * kvd * S * kv_elem;
+  r.v_cache = static_cast<uint8_t*>(d_vcache_) + l * kvd * S * kv_elem;
+  r.head_dim = uint32_t(arch_.head_dim);
+  r.max_seq = uint32_t(S);
+  r.kv_f16 = cfg_.kv_f16 ? 1 : 0;
+  return r;
 }
 
 AttnArgs Engine::attn_args(size_t l) const {
@@ -525,13 +548,9 @@ AttnArgs Engine::attn_args(size_t l) const {
   const size_t kv_elem = cfg_.kv_f16 ? 2 : 4;
   AttnArgs at{};
   at.state = d_state_;
-  at.q_raw = d_q_;
-  at.k_raw = d_k_;
-  at.v_raw = d_v_;
+  at.q = d_q_;
   at.k_cache = static_cast<uint8_t*>(d_kcache_) + l * kvd * S * kv_elem;
   at.v_cache = static_cast<uint8_t*>(d_vcache_) + l * kvd * S * kv_elem;
-  at.rope_cos = d_rope_cos_;
-  at.rope_sin = d_rope_sin_;
   at.out = d_attn_;
   at.part_ml = d_part_ml_;
   at.part_acc = d_part_acc_;
@@ -567,7 +586,7 @@ void Engine::record_step(hipStream_t st) {
   for (size_t l = 0; l < arch_.num_layers; ++l) {
     const LayerPlan& L = layers_[l];
     mark(0);
-    enqueue_qkv(L, st);
+    enqueue_qkv(l, st);
     const AttnArgs aa = attn_args(l);
     mark(5);
     launch_attention_partial(aa, st);
@@ -760,7 +779,7 @@ int Engine::launch_stage(int stage, size_t l) {
   const uint32_t D = uint32_t(arch_.hidden_dim), I = uint32_t(arch_.intermediate_dim);
   switch (stage) {
     case 0:
-      enqueue_qkv(L, stream_);
+      enqueue_qkv(l, stream_);
       return 0;
     case 1: {  // writes a scratch vector, not the residual stream
       const ProjPlan* o[1] = {&L.o};

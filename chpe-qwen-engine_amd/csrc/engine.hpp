@@ -118,10 +118,12 @@ class Engine {
   float* upload_vector(const std::vector<float>& v);
   void* dev_alloc(size_t bytes);
   void record_step(hipStream_t st);
-  void enqueue_qkv(const LayerPlan& L, hipStream_t st);
+  void enqueue_qkv(size_t layer, hipStream_t st);
+  RopeArgs rope_args(size_t layer) const;
   // one GEMV launch over n parts (outs[i] receives part i); returns the workgroup count
   uint32_t enqueue_gemv(const ProjPlan* const* parts, float* const* outs, int n, GemvMode mode,
-                        const float* x, uint32_t C, const float* gamma, hipStream_t st);
+                        const float* x, uint32_t C, const float* gamma, hipStream_t st,
+                        const RopeArgs* rope = nullptr, const uint32_t* roles = nullptr);
   AttnArgs attn_args(size_t layer) const;
   double proj_bytes(const ProjPlan& p) const;
 

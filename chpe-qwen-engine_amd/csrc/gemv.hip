@@ -104,6 +104,20 @@ __device__ __forceinline__ int part_of(const GemvArgs& a, uint32_t unit) {
   return p;
 }
 
+template <int RU, bool kSwi>
+__device__ __forceinline__ const GemvPart& row_part(const GemvPart& P0, const GemvPart& P1, int i) {
+  return (kSwi && i >= RU / 2) ? P1 : P0;
+}
+// Row of unit-local row i.  SwiGlu: rows i and i + RU/2 are the same row of gate and up.
+// QkvRope: rows i and i + RU/2 are the RoPE pair (j, j + head_dim/2) of one head.
+template <int RU, int MODE>
+__device__ __forceinline__ uint32_t row_of(uint32_t row_base, int i, uint32_t half) {
+  if constexpr (MODE == int(GemvMode::SwiGlu)) return row_base + uint32_t(i % (RU / 2));
+  else if constexpr (MODE == int(GemvMode::QkvRope))
+    return row_base + (i < RU / 2 ? uint32_t(i) : half + uint32_t(i - RU / 2));
+  else return row_base + uint32_t(i);
+}
+
 // ---- per-unit terms outside the dense codes, loaded together with the weights -----------
 // 16-row cells: lane i < RU serves unit row i: the 8 outlier columns of the row's cell and the
 // row's 8 outlier weights (added, gemvTileW4 :404-410), or for the tied LM head the prepared
@@ -116,14 +130,16 @@ struct CellExtras {
   bool valid;
 };
 
-template <class F, int RU, bool kSwi, bool kReplace>
+template <class F, int RU, int MODE>
 __device__ __forceinline__ void load_cell_extras(const GemvPart& P0, const GemvPart& P1, uint32_t row_base,
-                                                 int lane, CellExtras<RU>* e) {
+                                                 uint32_t half, int lane, CellExtras<RU>* e) {
   // every lane loads (lanes >= RU and rows past the end read row 0 of the part); the values
   // are decoded where they are used, so the loads stay in flight together with the codes
+  constexpr bool kSwi = MODE == int(GemvMode::SwiGlu);
+  constexpr bool kReplace = MODE == int(GemvMode::Logits);
   const int i = lane;
   const GemvPart& P = (kSwi && i >= RU / 2) ? P1 : P0;
-  const uint32_t r = row_base + uint32_t(kSwi ? i % (RU / 2) : i);
+  const uint32_t r = row_of<RU, MODE>(row_base, i < RU ? i : 0, half);
   e->valid = i < RU && r < P.rows;
   const uint32_t rr = e->valid ? r : 0u;
   if constexpr (kReplace) {
@@ -166,21 +182,13 @@ struct FlatExtras {
 };
 struct NoExtras {};
 
-template <int RU, bool kSwi>
-__device__ __forceinline__ const GemvPart& row_part(const GemvPart& P0, const GemvPart& P1, int i) {
-  return (kSwi && i >= RU / 2) ? P1 : P0;
-}
-template <int RU, bool kSwi>
-__device__ __forceinline__ uint32_t row_of(uint32_t row_base, int i) {
-  return row_base + uint32_t(kSwi ? i % (RU / 2) : i);
-}
-
-template <int RU, bool kSwi>
+template <int RU, int MODE>
 __device__ __forceinline__ void load_flat_extras(const GemvPart& P0, const GemvPart& P1, uint32_t row_base,
-                                                 int lane, FlatExtras* f) {
+                                                 uint32_t half, int lane, FlatExtras* f) {
+  constexpr bool kSwi = MODE == int(GemvMode::SwiGlu);
   const int i = lane >> 3;
   const GemvPart& P = row_part<RU, kSwi>(P0, P1, i);
-  const uint32_t r = row_of<RU, kSwi>(row_base, i), kmax = P.corr_kmax;
+  const uint32_t r = row_of<RU, MODE>(row_base, i, half), kmax = P.corr_kmax;
   const bool ok = P.corr != nullptr && r < P.rows;
 #pragma unroll
   for (int j = 0; j < kCorrSlots; ++j) {
@@ -307,6 +315,7 @@ struct UnitLoads {
   uint4 q[RU];
   uint32_t s[RU];  // raw scale bits
   uint32_t vm;     // bit i: row i of the unit is present
+  float rc, rs;    // QkvRope: cos / sin of the lane's RoPE pair
   std::conditional_t<kCell, CellExtras<RU>, NoExtras> ce;
   std::conditional_t<kFlat, FlatExtras, NoExtras> fe;
   float pre;
@@ -321,11 +330,12 @@ __device__ __forceinline__ void issue_panel(const GemvArgs& a, const GemvPart& P
   constexpr bool kSwi = MODE == int(GemvMode::SwiGlu);
   uint32_t c0;
   const bool lv = active && F::lane_cols(p, lane, a.C, &c0);
+  const uint32_t half = a.rope.head_dim / 2;
   uint32_t m = 0;
 #pragma unroll
   for (int i = 0; i < RU; ++i) {
     const GemvPart& P = row_part<RU, kSwi>(P0, P1, i);
-    const uint32_t r = row_of<RU, kSwi>(row_base, i);
+    const uint32_t r = row_of<RU, MODE>(row_base, i, half);
     const bool ok = lv && r < P.rows;
     F::locate(P, ok ? r : 0u, ok ? p : 0u, lane, a.C, &q[i], &s[i]);
     m |= uint32_t(ok) << i;
@@ -355,26 +365,73 @@ __device__ __forceinline__ void issue_unit(const GemvArgs& a, uint32_t unit, uin
                                            bool with_pre, UnitLoads<F, MODE>* u) {
   constexpr int RU = 8, S = kWave / RU;
   constexpr bool kSwi = MODE == int(GemvMode::SwiGlu);
-  constexpr bool kPre = MODE == int(GemvMode::Store) || MODE == int(GemvMode::Accum);
+  constexpr bool kRope = MODE == int(GemvMode::QkvRope);
+  constexpr bool kPre = MODE == int(GemvMode::Store) || MODE == int(GemvMode::Accum) || kRope;
   const bool active = unit < a.n_units;
+  const uint32_t half = a.rope.head_dim / 2;
   u->unit = unit;
   u->pu = kSwi ? 0 : __builtin_amdgcn_readfirstlane(part_of(a, active ? unit : 0u));
   const GemvPart& P0 = a.part[u->pu];
   const GemvPart& P1 = a.part[kSwi ? 1 : u->pu];
-  u->row_base = kSwi ? unit * (RU / 2) : (unit - P0.unit_begin) * RU;
+  if constexpr (kSwi) {
+    u->row_base = unit * (RU / 2);
+  } else if constexpr (kRope) {  // RU/2 pairs per unit, half/(RU/2) units per head
+    const uint32_t ul = unit - P0.unit_begin, per_head = half / (RU / 2);
+    u->row_base = (ul / per_head) * (2 * half) + (ul % per_head) * (RU / 2);
+  } else {
+    u->row_base = (unit - P0.unit_begin) * RU;
+  }
   if constexpr (UnitLoads<F, MODE>::kCell) {
-    if (active) load_cell_extras<F, RU, kSwi, MODE == int(GemvMode::Logits)>(P0, P1, u->row_base, lane, &u->ce);
+    if (active) load_cell_extras<F, RU, MODE>(P0, P1, u->row_base, half, lane, &u->ce);
   }
   if constexpr (UnitLoads<F, MODE>::kFlat) {
-    if (active && with_corr) load_flat_extras<RU, kSwi>(P0, P1, u->row_base, lane, &u->fe);
+    if (active && with_corr) load_flat_extras<RU, MODE>(P0, P1, u->row_base, half, lane, &u->fe);
   }
+  const uint32_t own = row_of<RU, MODE>(u->row_base, lane / S, half);
   u->pre = 0.0f;
   if constexpr (kPre) {
-    const uint32_t own = u->row_base + uint32_t(lane / S);
     if (with_pre && active && (lane % S) == 0 && own < P0.rows)
       u->pre = MODE == int(GemvMode::Accum) ? P0.y[own] : (P0.bias ? P0.bias[own] : 0.0f);
   }
+  if constexpr (kRope) {  // cos / sin of the pair (j, j + half) served by lane S * i, i < RU/2
+    u->rc = 1.0f;
+    u->rs = 0.0f;
+    if (with_pre && active && (lane % S) == 0 && lane < 32 && P0.rope_role != kRoleV) {
+      const size_t at = size_t(a.rope.state->pos) * half + (own % (2 * half));
+      u->rc = a.rope.cos[at];
+      u->rs = a.rope.sin[at];
+    }
+  }
   issue_panel<F, MODE>(a, P0, P1, active, u->row_base, p, lane, u->q, u->s, &u->vm);
+}
+
+// QkvRope epilogue for the pair (r, r + half) of part P: bias added, then RoPE (q, k) with the
+// reference's arithmetic (x0*cos - x1*sin, x0*sin + x1*cos, :212-213); q into y, k and v into
+// the KV cache at `pos`, rounded to the cache type.
+__device__ __forceinline__ void rope_store(const GemvArgs& a, const GemvPart& P, uint32_t r, float lo, float hi,
+                                           float c, float sn) {
+#pragma clang fp contract(off)
+  const uint32_t half = a.rope.head_dim / 2;
+  float o0 = lo, o1 = hi;
+  if (P.rope_role != kRoleV) {
+    o0 = lo * c - hi * sn;
+    o1 = lo * sn + hi * c;
+  }
+  if (P.rope_role == kRoleQ) {
+    P.y[r] = o0;
+    P.y[r + half] = o1;
+    return;
+  }
+  const uint32_t hd = a.rope.head_dim, head = r / hd, d = r % hd;
+  const size_t at = (size_t(head) * a.rope.max_seq + a.rope.state->pos) * hd + d;
+  void* cache = P.rope_role == kRoleK ? a.rope.k_cache : a.rope.v_cache;
+  if (a.rope.kv_f16) {
+    reinterpret_cast<__half*>(cache)[at] = __float2half_rn(o0);
+    reinterpret_cast<__half*>(cache)[at + half] = __float2half_rn(o1);
+  } else {
+    reinterpret_cast<float*>(cache)[at] = o0;
+    reinterpret_cast<float*>(cache)[at + half] = o1;
+  }
 }
 
 // final value v of unit row i (lane-owned): SwiGlu pairs gate row i with up row i + RU/2
@@ -425,6 +482,7 @@ __global__ void __launch_bounds__(512, 2) k_gemv_rows(GemvArgs a) {
   constexpr int RU = 8, S = kWave / RU;
   constexpr bool kSwi = MODE == int(GemvMode::SwiGlu);
   constexpr bool kLogits = MODE == int(GemvMode::Logits);
+  constexpr bool kRope = MODE == int(GemvMode::QkvRope);
   constexpr bool kOnePanel = F::kPPW == 1;
   using U = UnitLoads<F, MODE>;
   __shared__ __align__(16) float s_x[F::kPanelCols * F::kPPW];
@@ -468,9 +526,16 @@ __global__ void __launch_bounds__(512, 2) k_gemv_rows(GemvArgs a) {
     if constexpr (U::kCell) tot += __shfl(cell_outlier_sum<kLogits>(cur.ce, s_x, a.C), lane / S);
     if constexpr (U::kFlat) tot += flat_correction(cur.fe, s_x);
     const int i = lane / S;
-    const float up = kSwi ? __shfl(tot, (lane + 32) & 63) : 0.0f;  // up row i: 32 lanes above gate row i
-    if ((lane % S) == 0 && (!kSwi || i < RU / 2))
-      epilogue<MODE>(P0, row_of<RU, kSwi>(cur.row_base, i), tot, up, cur.pre, &bv, &bi, &nf);
+    // SwiGlu / QkvRope: the partner of row i < RU/2 sits 32 lanes above it
+    const float up = (kSwi || kRope) ? __shfl(tot, (lane + 32) & 63) : 0.0f;
+    const float up_pre = kRope ? __shfl(cur.pre, (lane + 32) & 63) : 0.0f;
+    if constexpr (kRope) {
+      const uint32_t r = row_of<RU, MODE>(cur.row_base, i, a.rope.head_dim / 2);
+      if ((lane % S) == 0 && i < RU / 2 && cur.unit < a.n_units && r < P0.rows)
+        rope_store(a, P0, r, tot + cur.pre, up + up_pre, cur.rc, cur.rs);
+    } else if ((lane % S) == 0 && (!kSwi || i < RU / 2)) {
+      epilogue<MODE>(P0, row_of<RU, MODE>(cur.row_base, i, 0), tot, up, cur.pre, &bv, &bi, &nf);
+    }
     if constexpr (kOnePanel) {
       cur = nxt;
     } else if (unit + stride < a.n_units) {
@@ -488,6 +553,7 @@ __global__ void __launch_bounds__(512, 2) k_gemv_split(GemvArgs a) {
   constexpr int RU = 8, S = kWave / RU;
   constexpr bool kSwi = MODE == int(GemvMode::SwiGlu);
   constexpr bool kLogits = MODE == int(GemvMode::Logits);
+  constexpr bool kRope = MODE == int(GemvMode::QkvRope);
   using U = UnitLoads<F, MODE>;
   extern __shared__ __align__(16) float s_x[];  // C floats
   __shared__ float s_part[kMaxWavesPerUnit][RU];
@@ -510,12 +576,21 @@ __global__ void __launch_bounds__(512, 2) k_gemv_split(GemvArgs a) {
   for (; unit < a.n_units; unit += gridDim.x) {
     const GemvPart& P0 = a.part[cur.pu];
     const GemvPart& P1 = a.part[kSwi ? 1 : cur.pu];
-    // epilogue operand of wave 0's rows, requested now so it overlaps the arithmetic
-    float pre = 0.0f;
-    if constexpr (MODE == int(GemvMode::Store) || MODE == int(GemvMode::Accum)) {
-      const uint32_t own = cur.row_base + uint32_t(lane / S);
-      if (wave == 0 && (lane % S) == 0 && own < P0.rows)
+    // epilogue operands of wave 0's rows, requested now so they overlap the arithmetic
+    const uint32_t half = a.rope.head_dim / 2;
+    float pre = 0.0f, rc = 1.0f, rs = 0.0f;
+    if constexpr (MODE == int(GemvMode::Store) || MODE == int(GemvMode::Accum) || kRope) {
+      const uint32_t own = row_of<RU, MODE>(cur.row_base, lane / S, half);
+      if (wave == 0 && (lane % S) == 0 && own < P0.rows) {
         pre = MODE == int(GemvMode::Accum) ? P0.y[own] : (P0.bias ? P0.bias[own] : 0.0f);
+        if constexpr (kRope) {
+          if (lane < 32 && P0.rope_role != kRoleV) {
+            const size_t at = size_t(a.rope.state->pos) * half + (own % (2 * half));
+            rc = a.rope.cos[at];
+            rs = a.rope.sin[at];
+          }
+        }
+      }
     }
     float acc[RU];
 #pragma unroll
@@ -534,9 +609,15 @@ __global__ void __launch_bounds__(512, 2) k_gemv_split(GemvArgs a) {
       float v = 0.0f;
       for (uint32_t w = 0; w < NW; ++w) v += s_part[w][i];
       if constexpr (U::kFlat) v += flat_correction(cur.fe, s_x);
-      const float up = kSwi ? __shfl(v, (lane + 32) & 63) : 0.0f;
-      if (unit < a.n_units && (lane % S) == 0 && (!kSwi || i < RU / 2))
-        epilogue<MODE>(P0, row_of<RU, kSwi>(cur.row_base, i), v, up, pre, &bv, &bi, &nf);
+      const float up = (kSwi || kRope) ? __shfl(v, (lane + 32) & 63) : 0.0f;
+      const float up_pre = kRope ? __shfl(pre, (lane + 32) & 63) : 0.0f;
+      if constexpr (kRope) {
+        const uint32_t r = row_of<RU, MODE>(cur.row_base, i, half);
+        if (unit < a.n_units && (lane % S) == 0 && i < RU / 2 && r < P0.rows)
+          rope_store(a, P0, r, v + pre, up + up_pre, rc, rs);
+      } else if (unit < a.n_units && (lane % S) == 0 && (!kSwi || i < RU / 2)) {
+        epilogue<MODE>(P0, row_of<RU, MODE>(cur.row_base, i, 0), v, up, pre, &bv, &bi, &nf);
+      }
     }
     __syncthreads();
     if (unit + gridDim.x < a.n_units) issue_unit<F, MODE>(a, unit + gridDim.x, p0, lane, wave == 0, false, &cur);
@@ -559,6 +640,7 @@ void launch_layout(const GemvArgs& a, const GemvLaunch& g, hipStream_t st) {
     case GemvMode::Accum: launch_one<F, int(GemvMode::Accum)>(a, g, st); break;
     case GemvMode::SwiGlu: launch_one<F, int(GemvMode::SwiGlu)>(a, g, st); break;
     case GemvMode::Logits: launch_one<F, int(GemvMode::Logits)>(a, g, st); break;
+    case GemvMode::QkvRope: launch_one<F, int(GemvMode::QkvRope)>(a, g, st); break;
   }
 }
 

@@ -32,6 +32,20 @@ enum class GemvMode : int {
   Accum = 1,   // y += W x    (o / down projections into the residual stream)
   SwiGlu = 2,  // y = silu(W0 x) * (W1 x)
   Logits = 3,  // logits = W x, plus per-workgroup argmax partials
+  QkvRope = 4, // y = W x + bias, then by part role: q rotated (RoPE) into y; k rotated and v
+               // stored into the KV cache at the step's position (rounded to the cache type)
+};
+
+enum RopeRole : uint32_t { kRoleQ = 0, kRoleK = 1, kRoleV = 2 };
+struct StepState;
+
+struct RopeArgs {            // QkvRope: applyRope (chpe_engine.zig:195-216) + KV append (:1693-1697)
+  const StepState* state;
+  const float* cos;          // [max_seq][head_dim/2]
+  const float* sin;
+  void* k_cache;             // this layer: [KV][max_seq][head_dim], f16 or f32
+  void* v_cache;
+  uint32_t head_dim, max_seq, kv_f16, pad;
 };
 
 constexpr int kMaxParts = 3;
@@ -49,6 +63,7 @@ struct GemvPart {
   const float2* corr;         // Flat: outlier corrections [rows][corr_kmax], zero-padded,
   uint32_t corr_kmax;         //   entry = (column as float bits, w_out - dequantised code)
   uint32_t replace_outliers;  // Cell16W4: outliers replace (tied LM head) instead of add
+  uint32_t rope_role;         // QkvRope: RopeRole of this part
   const struct CellReplace* repl;  // Cell16W4 replace mode: per-cell corrections (see below)
 };
 
@@ -90,6 +105,7 @@ struct GemvArgs {
   float eps;
   ArgmaxPartial* partials;   // Logits: one per workgroup
   StepResult* result;        // Logits: workgroup 0 stores the hidden norm
+  RopeArgs rope;             // QkvRope
 };
 
 struct GemvLaunch {  // launch geometry of one GemvArgs
@@ -117,13 +133,9 @@ struct EmbedArgs {
 
 struct AttnArgs {
   const StepState* state;
-  const float* q_raw;       // [H*hd] projection output (bias included), before RoPE
-  const float* k_raw;       // [KV*hd]
-  const float* v_raw;
-  void* k_cache;            // this layer: [KV][max_seq][hd], f16 or f32
-  void* v_cache;
-  const float* rope_cos;    // [max_seq][hd/2]
-  const float* rope_sin;
+  const float* q;           // [H*hd] rotated queries (the QkvRope GEMV's output)
+  const void* k_cache;      // this layer: [KV][max_seq][hd], f16 or f32, rows 0..pos written
+  const void* v_cache;
   float* out;               // [H*hd]
   float* part_ml;           // [H][n_chunks][2] (chunk max, chunk sum)
   float* part_acc;          // [H][n_chunks][hd]
