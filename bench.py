@@ -38,15 +38,16 @@ V, D, LAYERS, KV_HEADS, HEAD_DIM, Q_HEADS = 151936, 2048, 36, 2, 128, 16
 ATTN_CHUNK = 16384 // HEAD_DIM  # positions per attention workgroup
 NS = "chpe::(anonymous namespace)::"
 STAGES = {  # stage id -> (description, kernel name as rocprofv3 prints it, launches per step)
-    0: ("q/k/v GEMV (RMSNorm fused)", f"void {NS}k_gemv<{NS}Cell16W4, 0, 8, true>(chpe::GemvArgs)", LAYERS),
-    1: ("o GEMV + residual", f"void {NS}k_gemv<{NS}Cell16W4, 1, 8, true>(chpe::GemvArgs)", LAYERS),
-    2: ("gate/up GEMV + SwiGLU (RMSNorm fused)", f"void {NS}k_gemv<{NS}Cell16W4, 2, 8, true>(chpe::GemvArgs)",
-        LAYERS),
-    3: ("down GEMV + residual (flat tiles)", f"void {NS}k_gemv<{NS}FlatW4, 1, 8, false>(chpe::GemvArgs)", LAYERS),
-    4: ("LM head GEMV + argmax partials", f"void {NS}k_gemv<{NS}Cell16W4, 3, 8, true>(chpe::GemvArgs)", 1),
-    5: ("attention over the context chunks", f"void {NS}k_attn_partial<128>(chpe::AttnArgs)", LAYERS),
-    6: ("attention chunk merge", f"{NS}k_attn_combine(chpe::AttnArgs)", LAYERS),
+    0: ("q/k/v GEMV + RoPE + KV append (RMSNorm fused)",
+        f"void {NS}k_gemv_rows<{NS}Cell16W4, 4>(chpe::GemvArgs)", LAYERS),
+    1: ("o GEMV + residual", f"void {NS}k_gemv_rows<{NS}Cell16W4, 1>(chpe::GemvArgs)", LAYERS),
+    2: ("gate/up GEMV + SwiGLU (RMSNorm fused)", f"void {NS}k_gemv_rows<{NS}Cell16W4, 2>(chpe::GemvArgs)", LAYERS),
+    3: ("down GEMV + residual (flat tiles)", f"void {NS}k_gemv_split<{NS}FlatW4, 1>(chpe::GemvArgs)", LAYERS),
+    4: ("LM head GEMV + argmax partials", f"void {NS}k_gemv_rows<{NS}Cell16W4, 3>(chpe::GemvArgs)", 1),
+    5: ("attention over the context chunks", f"void {NS}k_attn_chunk<128, 8, __half, 4, 8>(chpe::AttnArgs)", LAYERS),
+    6: ("attention chunk merge", f"void {NS}k_attn_merge<128>(chpe::AttnArgs)", LAYERS),
 }
+
 
 
 def log(*a):
@@ -92,6 +93,19 @@ def cpu_baseline(archive, prompt_len, budget_s, max_steps):
                       f"(oracle/chpe_oracle.c, {cores} threads, {dt:.1f} s)"}
 
 
+def copy_probe():
+    """A plain copy kernel of known size: 4 x 256 MiB device-to-device."""
+    import torch
+    n = 256 << 20
+    src = torch.ones(n // 4, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(4):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_probe_bytes_per_copy": n, "copies": 4}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -101,7 +115,13 @@ def main():
     ap.add_argument("--live-steps", type=int, default=4, help="decode steps per stage timing")
     ap.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of CPU oracle sample")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="only copy 256 MiB device-to-device 4 times (calibrates rocprofv3 FETCH_SIZE / "
+                         "WRITE_SIZE against known bytes)")
     args = ap.parse_args()
+    if args.copy_probe:
+        copy_probe()
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported (the decode path runs "
               "on a single MI355X; multi-GPU sharding is not built)", file=sys.stderr)

@@ -746,13 +746,16 @@ double Engine::stage_bytes(int stage, size_t l) const {
     case 2: return proj_bytes(L.gate) + proj_bytes(L.up);
     case 3: return proj_bytes(L.down);
     case 4: return proj_bytes(lm_head_);
-    case 6:  // the partials of every chunk, read once
-      return double(arch_.num_attn_heads) * n_chunks_ * (arch_.head_dim + 2) * 4.0;
-    case 5: {  // K and V rows 0..pos of this layer at the current device position
+    case 5:    // K and V rows 0..pos of this layer at the current device position
+    case 6: {  // the partials of the chunks active at that position, read once
       StepState st{};
       if (hipStreamSynchronize(stream_) != hipSuccess ||
           hipMemcpy(&st, d_state_, sizeof(st), hipMemcpyDeviceToHost) != hipSuccess)
         return 0.0;
+      if (stage == 6) {
+        const double chunks = std::ceil((double(st.pos) + 1.0) / attn_chunk(uint32_t(arch_.head_dim)));
+        return double(arch_.num_attn_heads) * chunks * (arch_.head_dim + 2) * 4.0;
+      }
       const double kv_row = double(arch_.num_kv_heads * arch_.head_dim) * (cfg_.kv_f16 ? 2 : 4);
       return 2.0 * kv_row * (double(st.pos) + 1.0);
     }
