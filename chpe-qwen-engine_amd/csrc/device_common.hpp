@@ -35,8 +35,26 @@ constexpr int kWave = 64;
 
 __device__ __forceinline__ float h2f(uint16_t h) { return __half2float(__ushort_as_half(h)); }
 __device__ __forceinline__ float bf2f(uint16_t h) { return __uint_as_float(uint32_t(h) << 16); }
-__device__ __forceinline__ uint16_t ld_u16(const uint8_t* p) { return *reinterpret_cast<const uint16_t*>(p); }
-__device__ __forceinline__ uint4 ld_u128(const uint8_t* p) { return *reinterpret_cast<const uint4*>(p); }
+// Global-memory views.  A load through a generic pointer whose origin the compiler cannot trace
+// to global memory becomes a FLAT load, which counts on both the vector-memory and the LDS
+// counters; while one is outstanding every wait falls back to "all loads done", so the loads of
+// a unit can no longer be consumed as they arrive.  Every device buffer here is global memory.
+template <class T>
+using gptr = const __attribute__((address_space(1))) T*;
+template <class T>
+__device__ __forceinline__ gptr<T> as_global(const T* p) {
+  return (gptr<T>)(p);
+}
+template <class T>
+__device__ __forceinline__ T gld(const T* p) {
+  return *as_global(p);
+}
+__device__ __forceinline__ uint16_t ld_u16(const uint8_t* p) { return gld(reinterpret_cast<const uint16_t*>(p)); }
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint4 ld_u128(const uint8_t* p) {
+  const u32x4_t v = gld(reinterpret_cast<const u32x4_t*>(p));
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
 
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll

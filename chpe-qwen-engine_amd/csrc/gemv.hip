@@ -99,8 +99,9 @@ struct Raw16 {  // raw fp16 / bf16 tiles read as one row-major matrix (dotSegmen
 };
 
 __device__ __forceinline__ int part_of(const GemvArgs& a, uint32_t unit) {
-  int p = 0;
-  while (p + 1 < a.n_parts && unit >= a.part[p + 1].unit_begin) ++p;
+  int p = 0;  // unrolled over the fixed part count: a loop here would precede the weight loads
+#pragma unroll
+  for (int k = 1; k < kMaxParts; ++k) p += (k < int(a.n_parts) && unit >= a.part[k].unit_begin) ? 1 : 0;
   return p;
 }
 
@@ -117,6 +118,35 @@ __device__ __forceinline__ uint32_t row_of(uint32_t row_base, int i, uint32_t ha
     return row_base + (i < RU / 2 ? uint32_t(i) : half + uint32_t(i - RU / 2));
   else return row_base + uint32_t(i);
 }
+
+// A kernel-argument field as a uniform (scalar) value: selecting between two parts' fields per
+// lane must not become a per-lane load from the argument block.
+__device__ __forceinline__ uint32_t uni(uint32_t v) { return __builtin_amdgcn_readfirstlane(v); }
+// (pointers: global memory, kept visible to the compiler through the address-space casts)
+template <class T>
+__device__ __forceinline__ T* uni(T* p) {
+  const uint64_t v = reinterpret_cast<uint64_t>(p);
+  using G = __attribute__((address_space(1))) T*;
+  const G g = reinterpret_cast<G>(uint64_t(uni(uint32_t(v))) | (uint64_t(uni(uint32_t(v >> 32))) << 32));
+  return (T*)(g);
+}
+
+// v if ok, else +0 -- by bit masking, so that no branch separates a load from its use (a branch
+// there makes the compiler wait for every outstanding load)
+__device__ __forceinline__ float keep_if(bool ok, float v) {
+  return __uint_as_float(__float_as_uint(v) & (ok ? 0xffffffffu : 0u));
+}
+__device__ __forceinline__ float4 keep_if(bool ok, float4 v) {
+  return make_float4(keep_if(ok, v.x), keep_if(ok, v.y), keep_if(ok, v.z), keep_if(ok, v.w));
+}
+
+// Position of input column c in the workgroup's LDS copy: 16 bytes of padding after every 32
+// columns, so that lanes reading consecutive 32-column chunks (128 bytes apart) start on
+// different banks and a 16-byte-per-lane read is conflict-free.
+__device__ __forceinline__ uint32_t xs_at(uint32_t c) { return c + ((c >> 5) << 2); }
+// (+4 floats: a slot that absorbs the writes of threads past the input)
+__host__ __device__ constexpr uint32_t xs_floats(uint32_t C) { return C + ((C + 31) >> 5) * 4 + 4; }
+__device__ __forceinline__ uint32_t xs_spare(uint32_t C) { return xs_floats(C) - 4; }
 
 // ---- per-unit terms outside the dense codes, loaded together with the weights -----------
 // 16-row cells: lane i < RU serves unit row i: the 8 outlier columns of the row's cell and the
@@ -138,18 +168,23 @@ __device__ __forceinline__ void load_cell_extras(const GemvPart& P0, const GemvP
   constexpr bool kSwi = MODE == int(GemvMode::SwiGlu);
   constexpr bool kReplace = MODE == int(GemvMode::Logits);
   const int i = lane;
-  const GemvPart& P = (kSwi && i >= RU / 2) ? P1 : P0;
+  // the part's fields are read as uniform values and selected per lane (a per-lane choice of
+  // the part itself would turn them into vector loads that stall the loads issued before)
+  const bool second = kSwi && i >= RU / 2;
+  const uint32_t rows = second ? uni(P1.rows) : uni(P0.rows);
   const uint32_t r = row_of<RU, MODE>(row_base, i < RU ? i : 0, half);
-  e->valid = i < RU && r < P.rows;
+  e->valid = i < RU && r < rows;
   const uint32_t rr = e->valid ? r : 0u;
   if constexpr (kReplace) {
-    const CellReplace* R = P.repl + (rr >> 4);
+    const CellReplace* R = P0.repl + (rr >> 4);
     e->cols = *reinterpret_cast<const uint4*>(R->col);
     const uint4* d = reinterpret_cast<const uint4*>(R->delta[rr & 15]);
     e->w0 = d[0];
     e->w1 = d[1];
   } else {
-    const uint8_t* cell = P.base + size_t(rr >> 4) * P.stride;
+    const uint8_t* base = second ? uni(P1.base) : uni(P0.base);
+    const uint32_t stride = second ? uni(P1.stride) : uni(P0.stride);
+    const uint8_t* cell = base + size_t(rr >> 4) * stride;
     e->cols = ld_u128(cell + 16448 + 816);
     e->w0 = ld_u128(cell + 16448 + 560 + (rr & 15) * 16);
     e->w1 = e->w0;
@@ -168,7 +203,7 @@ __device__ __forceinline__ float cell_outlier_sum(const CellExtras<8>& e, const 
     float w;
     if constexpr (kReplace) w = __uint_as_float(k < 4 ? w0[k] : w1[k - 4]);
     else w = (k & 1) ? half_hi(w0[k >> 1]) : half_lo(w0[k >> 1]);
-    if (c < C) o = fmaf(w, s_x[c], o);
+    if (c < C) o = fmaf(w, s_x[xs_at(c)], o);
   }
   return e.valid ? o : 0.0f;
 }
@@ -184,16 +219,24 @@ struct NoExtras {};
 
 template <int RU, int MODE>
 __device__ __forceinline__ void load_flat_extras(const GemvPart& P0, const GemvPart& P1, uint32_t row_base,
-                                                 uint32_t half, int lane, FlatExtras* f) {
+                                                 uint32_t half, int lane, const float* x_any, FlatExtras* f) {
   constexpr bool kSwi = MODE == int(GemvMode::SwiGlu);
   const int i = lane >> 3;
-  const GemvPart& P = row_part<RU, kSwi>(P0, P1, i);
-  const uint32_t r = row_of<RU, MODE>(row_base, i, half), kmax = P.corr_kmax;
-  const bool ok = P.corr != nullptr && r < P.rows;
+  const bool second = kSwi && i >= RU / 2;  // uniform fields selected per lane (see load_cell_extras)
+  const float2* corr = second ? uni(P1.corr) : uni(P0.corr);
+  const uint32_t kmax = second ? uni(P1.corr_kmax) : uni(P0.corr_kmax);
+  const uint32_t rows = second ? uni(P1.rows) : uni(P0.rows);
+  const uint32_t r = row_of<RU, MODE>(row_base, i, half);
+  const bool ok = corr != nullptr && r < rows;
+  // every slot loads (absent ones: the first entry of a valid table, or of the input vector
+  // when there is no table) and is masked afterwards
+  const float2* src = corr ? corr : reinterpret_cast<const float2*>(x_any);
 #pragma unroll
   for (int j = 0; j < kCorrSlots; ++j) {
     const uint32_t k = uint32_t(lane & 7) + 8u * uint32_t(j);
-    f->e[j] = (ok && k < kmax) ? P.corr[size_t(r) * kmax + k] : make_float2(0.0f, 0.0f);
+    const bool use = ok && k < kmax;
+    const float2 e = src[use ? size_t(r) * kmax + k : 0];
+    f->e[j] = make_float2(e.x, keep_if(use, e.y));
   }
 }
 
@@ -203,7 +246,7 @@ __device__ __forceinline__ float flat_correction(const FlatExtras& f, const floa
   float cs = 0.0f;
 #pragma unroll
   for (int j = 0; j < kCorrSlots; ++j)
-    if (f.e[j].y != 0.0f) cs = fmaf(f.e[j].y, s_x[__float_as_uint(f.e[j].x)], cs);
+    if (f.e[j].y != 0.0f) cs = fmaf(f.e[j].y, s_x[xs_at(__float_as_uint(f.e[j].x))], cs);
   cs += __shfl_xor(cs, 1);
   cs += __shfl_xor(cs, 2);
   cs += __shfl_xor(cs, 4);
@@ -212,75 +255,103 @@ __device__ __forceinline__ float flat_correction(const FlatExtras& f, const floa
 
 // The workgroup's copy of the input in LDS, normalised (x * inv) * gamma when `gamma` is set
 // (rmsNorm :187-191); *ss = sum of x^2 over the input (also the LM head's hidden norm).
-// Inputs up to 32 floats per thread stay in registers between the two halves of the norm.
-template <bool kNeedSum>
-__device__ __forceinline__ void stage_x(const GemvArgs& a, float* s_x, float* s_red, float* ss, float* inv) {
+// Split in two so that the input's loads are issued before the weights' and the staging (its
+// barriers included) overlaps the weights' latency: stage_x_issue loads up to 32 floats per
+// thread into registers, stage_x_finish completes the staging (wider inputs take a two-pass
+// path over LDS in stage_x_finish).
+template <int SL>  // float4 slots per thread
+struct StageRegs {
+  float4 xs[SL], gs[SL];
+};
+
+// branch-free: every slot loads (past the input: its first float4) and is masked when used, so
+// that the wait for these loads does not also wait for the weights issued after them
+template <bool kNorm, int SL>
+__device__ __forceinline__ void stage_x_issue(const GemvArgs& a, StageRegs<SL>* r) {
+  const uint32_t C = a.C, tid = threadIdx.x, nt = blockDim.x;
+#pragma unroll
+  for (int k = 0; k < SL; ++k) {
+    const uint32_t i = (tid + uint32_t(k) * nt) * 4, ic = i < C ? i : 0u;
+    r->xs[k] = *reinterpret_cast<const float4*>(a.x + ic);
+    if constexpr (kNorm) r->gs[k] = *reinterpret_cast<const float4*>(a.gamma + ic);
+  }
+}
+
+// kNorm: RMSNorm with the gains `gamma` (and the sum of squares, also the LM head's hidden norm);
+// kWide: the input may exceed the register slots (then two passes over LDS).  Both are
+// compile-time so that no runtime branch sits between the loads and their use.
+template <bool kNorm, bool kWide, int SL>
+__device__ __forceinline__ void stage_x_finish(const GemvArgs& a, const StageRegs<SL>& r, float* s_x, float* s_red,
+                                               float* ss, float* inv) {
   const uint32_t C = a.C, tid = threadIdx.x, nt = blockDim.x;
   const int lane = tid & 63, wave = tid >> 6;
-  if ((kNeedSum || a.gamma) && C > 32 * nt) {  // wide input: two passes over LDS
+  if constexpr (kWide) {  // two passes over LDS
     float q2 = 0.0f;
     for (uint32_t i = tid * 4; i < C; i += nt * 4) {
       const float4 t = *reinterpret_cast<const float4*>(a.x + i);
-      *reinterpret_cast<float4*>(s_x + i) = t;
+      *reinterpret_cast<float4*>(s_x + xs_at(i)) = t;
       q2 = fmaf(t.x, t.x, fmaf(t.y, t.y, fmaf(t.z, t.z, fmaf(t.w, t.w, q2))));
     }
-    q2 = wave_sum(q2);
-    if (lane == 0) s_red[wave] = q2;
-    __syncthreads();
-    float t = 0.0f;
-    for (uint32_t w = 0; w < nt / kWave; ++w) t += s_red[w];
-    *ss = t;
-    const float iv = a.gamma ? 1.0f / sqrtf(t / float(C) + a.eps) : 1.0f;
-    *inv = iv;
-    if (a.gamma)
+    if constexpr (kNorm) {
+      q2 = wave_sum(q2);
+      if (lane == 0) s_red[wave] = q2;
+      __syncthreads();
+      float t = 0.0f;
+      for (uint32_t w = 0; w < nt / kWave; ++w) t += s_red[w];
+      *ss = t;
+      const float iv = 1.0f / sqrtf(t / float(C) + a.eps);
+      *inv = iv;
       for (uint32_t i = tid * 4; i < C; i += nt * 4) {
         const float4 g = *reinterpret_cast<const float4*>(a.gamma + i);
-        float4 v = *reinterpret_cast<float4*>(s_x + i);
+        float4 v = *reinterpret_cast<float4*>(s_x + xs_at(i));
         v.x = v.x * iv * g.x;
         v.y = v.y * iv * g.y;
         v.z = v.z * iv * g.z;
         v.w = v.w * iv * g.w;
-        *reinterpret_cast<float4*>(s_x + i) = v;
+        *reinterpret_cast<float4*>(s_x + xs_at(i)) = v;
       }
-  } else if (kNeedSum || a.gamma) {
-    float4 xs[8], gs[8];
-    float q2 = 0.0f;
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      const uint32_t i = (tid + uint32_t(k) * nt) * 4;
-      xs[k] = i < C ? *reinterpret_cast<const float4*>(a.x + i) : make_float4(0.f, 0.f, 0.f, 0.f);
-      gs[k] = (i < C && a.gamma) ? *reinterpret_cast<const float4*>(a.gamma + i) : make_float4(1.f, 1.f, 1.f, 1.f);
     }
-#pragma unroll
-    for (int k = 0; k < 8; ++k)
-      q2 = fmaf(xs[k].x, xs[k].x, fmaf(xs[k].y, xs[k].y, fmaf(xs[k].z, xs[k].z, fmaf(xs[k].w, xs[k].w, q2))));
-    q2 = wave_sum(q2);
-    if (lane == 0) s_red[wave] = q2;
     __syncthreads();
-    float t = 0.0f;
-    for (uint32_t w = 0; w < nt / kWave; ++w) t += s_red[w];
-    *ss = t;
-    const float iv = a.gamma ? 1.0f / sqrtf(t / float(C) + a.eps) : 1.0f;
+    return;
+  } else {
+    float iv = 1.0f;
+    if constexpr (kNorm) {
+      float q2 = 0.0f;
+#pragma unroll
+      for (int k = 0; k < SL; ++k) {
+        const float4 t = keep_if((tid + uint32_t(k) * nt) * 4 < C, r.xs[k]);
+        q2 = fmaf(t.x, t.x, fmaf(t.y, t.y, fmaf(t.z, t.z, fmaf(t.w, t.w, q2))));
+      }
+      q2 = wave_sum(q2);
+      if (lane == 0) s_red[wave] = q2;
+      __syncthreads();
+      float t = 0.0f;
+      for (uint32_t w = 0; w < nt / kWave; ++w) t += s_red[w];
+      *ss = t;
+      iv = 1.0f / sqrtf(t / float(C) + a.eps);
+    }
     *inv = iv;
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
+    for (int k = 0; k < SL; ++k) {
       const uint32_t i = (tid + uint32_t(k) * nt) * 4;
-      if (i < C) {
-        float4 v = xs[k];
-        if (a.gamma) {
-          v.x = v.x * iv * gs[k].x;
-          v.y = v.y * iv * gs[k].y;
-          v.z = v.z * iv * gs[k].z;
-          v.w = v.w * iv * gs[k].w;
-        }
-        *reinterpret_cast<float4*>(s_x + i) = v;
+      float4 v = r.xs[k];
+      if constexpr (kNorm) {
+        v.x = v.x * iv * r.gs[k].x;
+        v.y = v.y * iv * r.gs[k].y;
+        v.z = v.z * iv * r.gs[k].z;
+        v.w = v.w * iv * r.gs[k].w;
       }
+      *reinterpret_cast<float4*>(s_x + (i < C ? xs_at(i) : xs_spare(C))) = v;
     }
-  } else {
-    for (uint32_t i = tid * 4; i < C; i += nt * 4)
-      *reinterpret_cast<float4*>(s_x + i) = *reinterpret_cast<const float4*>(a.x + i);
+    __syncthreads();
   }
-  __syncthreads();
+}
+
+template <bool kNorm, int SL = 2>
+__device__ __forceinline__ void stage_x(const GemvArgs& a, float* s_x, float* s_red, float* ss, float* inv) {
+  StageRegs<SL> r;
+  stage_x_issue<kNorm>(a, &r);
+  stage_x_finish<kNorm, false>(a, r, s_x, s_red, ss, inv);
 }
 
 // the lane's input chunk of panel p from LDS, and its sum
@@ -291,7 +362,7 @@ __device__ __forceinline__ float lds_chunk(const float* s_x, uint32_t C, uint32_
   if (F::lane_cols(p, lane, C, &c0)) {
 #pragma unroll
     for (int k = 0; k < F::kCols / 4; ++k) {
-      const float4 t = *reinterpret_cast<const float4*>(s_x + c0 + 4 * k);
+      const float4 t = *reinterpret_cast<const float4*>(s_x + xs_at(c0 + 4 * k));
       xr[4 * k] = t.x; xr[4 * k + 1] = t.y; xr[4 * k + 2] = t.z; xr[4 * k + 3] = t.w;
     }
 #pragma unroll
@@ -315,10 +386,12 @@ struct UnitLoads {
   uint4 q[RU];
   uint32_t s[RU];  // raw scale bits
   uint32_t vm;     // bit i: row i of the unit is present
-  float rc, rs;    // QkvRope: cos / sin of the lane's RoPE pair
+  float rc, rs;    // QkvRope: cos / sin of the lane's RoPE pair (used when rope_ok)
+  bool rope_ok;
   std::conditional_t<kCell, CellExtras<RU>, NoExtras> ce;
   std::conditional_t<kFlat, FlatExtras, NoExtras> fe;
-  float pre;
+  float pre;  // the epilogue operand of the lane's row (used when pre_ok)
+  bool pre_ok;
 };
 
 template <class F, int MODE>
@@ -350,11 +423,14 @@ __device__ __forceinline__ void panel_math(const GemvPart& P0, const GemvPart& P
                                            float (&acc)[8]) {
   constexpr int RU = 8;
   constexpr bool kSwi = MODE == int(GemvMode::SwiGlu);
+  // row by row in load order, so that row i's arithmetic waits only for row i's loads and runs
+  // while the later rows are still arriving (the scheduler would otherwise wait for all of them)
 #pragma unroll
   for (int i = 0; i < RU; ++i) {
     const GemvPart& P = row_part<RU, kSwi>(P0, P1, i);
     const float t = (F::dot(q[i], x, P.bf16 != 0) - F::kOff * sx) * F::scale(s[i]);
     acc[i] += ((vm >> i) & 1u) ? t : 0.0f;
+    __builtin_amdgcn_sched_barrier(0);
   }
 }
 
@@ -385,22 +461,25 @@ __device__ __forceinline__ void issue_unit(const GemvArgs& a, uint32_t unit, uin
     if (active) load_cell_extras<F, RU, MODE>(P0, P1, u->row_base, half, lane, &u->ce);
   }
   if constexpr (UnitLoads<F, MODE>::kFlat) {
-    if (active && with_corr) load_flat_extras<RU, MODE>(P0, P1, u->row_base, half, lane, &u->fe);
+    if (active && with_corr) load_flat_extras<RU, MODE>(P0, P1, u->row_base, half, lane, a.x, &u->fe);
   }
+  // Branch-free like the panel loads: each lane loads at a valid (clamped) address and the
+  // flags say which values count; they are applied where the values are used, after the sums.
   const uint32_t own = row_of<RU, MODE>(u->row_base, lane / S, half);
   u->pre = 0.0f;
+  u->pre_ok = false;
   if constexpr (kPre) {
-    if (with_pre && active && (lane % S) == 0 && own < P0.rows)
-      u->pre = MODE == int(GemvMode::Accum) ? P0.y[own] : (P0.bias ? P0.bias[own] : 0.0f);
+    const float* src = MODE == int(GemvMode::Accum) ? P0.y : P0.bias;
+    const bool ok = with_pre && active && (lane % S) == 0 && own < P0.rows && src != nullptr;
+    u->pre = (src ? src : a.x)[ok ? own : 0u];
+    u->pre_ok = ok;
   }
   if constexpr (kRope) {  // cos / sin of the pair (j, j + half) served by lane S * i, i < RU/2
-    u->rc = 1.0f;
-    u->rs = 0.0f;
-    if (with_pre && active && (lane % S) == 0 && lane < 32 && P0.rope_role != kRoleV) {
-      const size_t at = size_t(a.rope.state->pos) * half + (own % (2 * half));
-      u->rc = a.rope.cos[at];
-      u->rs = a.rope.sin[at];
-    }
+    const bool ok = with_pre && active && (lane % S) == 0 && lane < 32 && P0.rope_role != kRoleV;
+    const size_t at = ok ? size_t(a.rope.state->pos) * half + (own % (2 * half)) : 0u;
+    u->rc = a.rope.cos[at];
+    u->rs = a.rope.sin[at];
+    u->rope_ok = ok;
   }
   issue_panel<F, MODE>(a, P0, P1, active, u->row_base, p, lane, u->q, u->s, &u->vm);
 }
@@ -453,7 +532,7 @@ __device__ __forceinline__ void epilogue(const GemvPart& P0, uint32_t r, float v
 }
 
 template <int MODE>
-__device__ __forceinline__ void argmax_partial(const GemvArgs& a, float bv, uint32_t bi, uint32_t nf, float ss,
+__device__ __forceinline__ void argmax_partial(const GemvArgs& a, float bv, uint32_t bi, uint32_t nf,
                                                float* s_bv, uint32_t* s_bi, uint32_t* s_nf) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
 #pragma unroll
@@ -471,91 +550,155 @@ __device__ __forceinline__ void argmax_partial(const GemvArgs& a, float bv, uint
       if (better(s_bv[w], s_bi[w], bv, bi)) { bv = s_bv[w]; bi = s_bi[w]; }
     }
     a.partials[blockIdx.x] = ArgmaxPartial{bv, bi, nf, 0u};
-    if (blockIdx.x == 0) a.result->hidden_norm = sqrtf(ss);
   }
 }
 
-// One wave = one unit of RU rows over all columns (NW == 1).  Persistent: the wave strides over
-// units, and issues the next unit's loads before the arithmetic of the current one.
+// The arithmetic and the epilogue of one unit of k_gemv_rows (row-by-row, see panel_math).
 template <class F, int MODE>
-__global__ void __launch_bounds__(512, 2) k_gemv_rows(GemvArgs a) {
+__device__ __forceinline__ void rows_unit(const GemvArgs& a, const UnitLoads<F, MODE>& cur, const float* s_x,
+                                          const float (&x0)[F::kCols], float sx0, int lane, float* bv,
+                                          uint32_t* bi, uint32_t* nf) {
   constexpr int RU = 8, S = kWave / RU;
   constexpr bool kSwi = MODE == int(GemvMode::SwiGlu);
   constexpr bool kLogits = MODE == int(GemvMode::Logits);
   constexpr bool kRope = MODE == int(GemvMode::QkvRope);
-  constexpr bool kOnePanel = F::kPPW == 1;
   using U = UnitLoads<F, MODE>;
-  __shared__ __align__(16) float s_x[F::kPanelCols * F::kPPW];
-  __shared__ float s_red[8], s_bv[8];
-  __shared__ uint32_t s_bi[8], s_nf[8];
-  const int lane = threadIdx.x & 63;
-  const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const uint32_t nwv = blockDim.x / kWave, stride = gridDim.x * nwv;
-  uint32_t unit = blockIdx.x * nwv + wave;
-
-  U cur, nxt;
-  issue_unit<F, MODE>(a, unit, 0, lane, true, true, &cur);
-  float ss = 0.0f, inv = 1.0f;
-  stage_x<kLogits>(a, s_x, s_red, &ss, &inv);
-  float x0[F::kCols];
-  float sx0 = lds_chunk<F>(s_x, a.C, 0, lane, x0);
-
-  float bv = -1e30f;
-  uint32_t bi = 0xffffffffu, nf = 0;
-  for (; unit < a.n_units; unit += stride) {
-    if constexpr (kOnePanel) {
-      if (unit + stride < a.n_units) issue_unit<F, MODE>(a, unit + stride, 0, lane, true, true, &nxt);
-    }
-    const GemvPart& P0 = a.part[cur.pu];
-    const GemvPart& P1 = a.part[kSwi ? 1 : cur.pu];
-    float acc[RU];
+  const GemvPart& P0 = a.part[cur.pu];
+  const GemvPart& P1 = a.part[kSwi ? 1 : cur.pu];
+  float acc[RU];
 #pragma unroll
-    for (int i = 0; i < RU; ++i) acc[i] = 0.0f;
-    panel_math<F, MODE>(P0, P1, cur.q, cur.s, cur.vm, x0, sx0, acc);
-    if constexpr (!kOnePanel) {  // further panels (raw tiles)
-      uint4 qn[RU];
-      uint32_t sn[RU], vn;
-      for (uint32_t p = 1; p < a.n_panels; ++p) {
-        issue_panel<F, MODE>(a, P0, P1, cur.unit < a.n_units, cur.row_base, p, lane, qn, sn, &vn);
-        float xr[F::kCols];
-        const float sx = lds_chunk<F>(s_x, a.C, p, lane, xr);
-        panel_math<F, MODE>(P0, P1, qn, sn, vn, xr, sx, acc);
-      }
-    }
-    float tot = wave_reduce_rows<RU>(acc, lane);  // lane l: row l / S of the unit
-    if constexpr (U::kCell) tot += __shfl(cell_outlier_sum<kLogits>(cur.ce, s_x, a.C), lane / S);
-    if constexpr (U::kFlat) tot += flat_correction(cur.fe, s_x);
-    const int i = lane / S;
-    // SwiGlu / QkvRope: the partner of row i < RU/2 sits 32 lanes above it
-    const float up = (kSwi || kRope) ? __shfl(tot, (lane + 32) & 63) : 0.0f;
-    const float up_pre = kRope ? __shfl(cur.pre, (lane + 32) & 63) : 0.0f;
-    if constexpr (kRope) {
-      const uint32_t r = row_of<RU, MODE>(cur.row_base, i, a.rope.head_dim / 2);
-      if ((lane % S) == 0 && i < RU / 2 && cur.unit < a.n_units && r < P0.rows)
-        rope_store(a, P0, r, tot + cur.pre, up + up_pre, cur.rc, cur.rs);
-    } else if ((lane % S) == 0 && (!kSwi || i < RU / 2)) {
-      epilogue<MODE>(P0, row_of<RU, MODE>(cur.row_base, i, 0), tot, up, cur.pre, &bv, &bi, &nf);
-    }
-    if constexpr (kOnePanel) {
-      cur = nxt;
-    } else if (unit + stride < a.n_units) {
-      issue_unit<F, MODE>(a, unit + stride, 0, lane, true, true, &cur);
+  for (int i = 0; i < RU; ++i) acc[i] = 0.0f;
+  panel_math<F, MODE>(P0, P1, cur.q, cur.s, cur.vm, x0, sx0, acc);
+  if constexpr (F::kPPW > 1) {  // further panels (raw tiles)
+    uint4 qn[RU];
+    uint32_t sn[RU], vn;
+    for (uint32_t p = 1; p < a.n_panels; ++p) {
+      issue_panel<F, MODE>(a, P0, P1, cur.unit < a.n_units, cur.row_base, p, lane, qn, sn, &vn);
+      float xr[F::kCols];
+      const float sx = lds_chunk<F>(s_x, a.C, p, lane, xr);
+      panel_math<F, MODE>(P0, P1, qn, sn, vn, xr, sx, acc);
     }
   }
-  if constexpr (kLogits) argmax_partial<MODE>(a, bv, bi, nf, ss, s_bv, s_bi, s_nf);
+  float tot = wave_reduce_rows<RU>(acc, lane);  // lane l: row l / S of the unit
+  if constexpr (U::kCell) tot += __shfl(cell_outlier_sum<kLogits>(cur.ce, s_x, a.C), lane / S);
+  if constexpr (U::kFlat) tot += flat_correction(cur.fe, s_x);
+  const int i = lane / S;
+  // SwiGlu / QkvRope: the partner of row i < RU/2 sits 32 lanes above it
+  const float up = (kSwi || kRope) ? __shfl(tot, (lane + 32) & 63) : 0.0f;
+  const float pre = cur.pre_ok ? cur.pre : 0.0f;
+  const float up_pre = kRope ? __shfl(pre, (lane + 32) & 63) : 0.0f;
+  if constexpr (kRope) {
+    const uint32_t r = row_of<RU, MODE>(cur.row_base, i, a.rope.head_dim / 2);
+    if ((lane % S) == 0 && i < RU / 2 && cur.unit < a.n_units && r < P0.rows)
+      rope_store(a, P0, r, tot + pre, up + up_pre, cur.rope_ok ? cur.rc : 1.0f, cur.rope_ok ? cur.rs : 0.0f);
+  } else if ((lane % S) == 0 && (!kSwi || i < RU / 2) && cur.unit < a.n_units) {
+    epilogue<MODE>(P0, row_of<RU, MODE>(cur.row_base, i, 0), tot, up, pre, bv, bi, nf);
+  }
+}
+
+// Modes whose input is the raw hidden state and which apply the layer's RMS norm while staging.
+template <int MODE>
+constexpr bool kNormOf = MODE == int(GemvMode::SwiGlu) || MODE == int(GemvMode::QkvRope) ||
+                         MODE == int(GemvMode::Logits);
+
+// The staging wave of k_gemv_rows: the whole input (C <= CMAX floats) into the workgroup's LDS
+// copy, RMS-normalised (x * inv) * gamma when kNorm (rmsNorm :187-191); every load is issued
+// before any use and this wave issues no other loads.  Returns the sum of squares (on every
+// lane; also the LM head's hidden norm).
+template <bool kNorm, uint32_t CMAX>
+__device__ __forceinline__ float stage_wave(const GemvArgs& a, float* s_x, int lane) {
+  constexpr int SL = int((CMAX + 255) / 256);  // float4 per lane
+  const uint32_t C = a.C;
+  float4 xs[SL], gs[SL];
+#pragma unroll
+  for (int k = 0; k < SL; ++k) {
+    const uint32_t i = (uint32_t(lane) + 64u * uint32_t(k)) * 4, ic = i < C ? i : 0u;
+    xs[k] = *reinterpret_cast<const float4*>(a.x + ic);
+    if constexpr (kNorm) gs[k] = *reinterpret_cast<const float4*>(a.gamma + ic);
+  }
+  float ss = 0.0f, iv = 1.0f;
+  if constexpr (kNorm) {
+#pragma unroll
+    for (int k = 0; k < SL; ++k) {
+      const float4 t = keep_if((uint32_t(lane) + 64u * uint32_t(k)) * 4 < C, xs[k]);
+      ss = fmaf(t.x, t.x, fmaf(t.y, t.y, fmaf(t.z, t.z, fmaf(t.w, t.w, ss))));
+    }
+    ss = wave_sum(ss);
+    iv = 1.0f / sqrtf(ss / float(C) + a.eps);
+  }
+#pragma unroll
+  for (int k = 0; k < SL; ++k) {
+    const uint32_t i = (uint32_t(lane) + 64u * uint32_t(k)) * 4;
+    float4 v = xs[k];
+    if constexpr (kNorm) {
+      v.x = v.x * iv * gs[k].x;
+      v.y = v.y * iv * gs[k].y;
+      v.z = v.z * iv * gs[k].z;
+      v.w = v.w * iv * gs[k].w;
+    }
+    *reinterpret_cast<float4*>(s_x + (i < C ? xs_at(i) : xs_spare(C))) = v;
+  }
+  return ss;
+}
+
+// One wave = one unit of RU rows over all columns (NW == 1); the workgroup is kRowWaves such
+// waves plus one staging wave that puts the (normalised) input into LDS, so the unit waves'
+// loads are only weights and their arithmetic runs row by row as the rows arrive.  A wave
+// whose grid is capped (the LM head) strides over further units.
+constexpr int kRowWaves = 4;
+template <class F, int MODE>
+__global__ void __launch_bounds__(kWave * (kRowWaves + 1), 2) k_gemv_rows(GemvArgs a) {
+  constexpr bool kLogits = MODE == int(GemvMode::Logits);
+  constexpr bool kNorm = kNormOf<MODE>;
+  using U = UnitLoads<F, MODE>;
+  __shared__ __align__(16) float s_x[xs_floats(F::kPanelCols * F::kPPW)];
+  __shared__ float s_bv[kRowWaves + 1];
+  __shared__ uint32_t s_bi[kRowWaves + 1], s_nf[kRowWaves + 1];
+  const int lane = threadIdx.x & 63;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const uint32_t stride = gridDim.x * kRowWaves;
+  const bool stager = wave == kRowWaves;
+
+  // The two roles are wave-uniform branches that each pass the same barriers (one after the
+  // staging, one more in the LM head's argmax).  Keeping them apart means no value of a unit
+  // wave's loads meets the staging wave's control flow, so nothing that uses those values can be
+  // placed before the barrier (where it would wait for every weight load at once).
+  if (stager) {
+    const float ss = stage_wave<kNorm, F::kPanelCols * F::kPPW>(a, s_x, lane);
+    if (kLogits && blockIdx.x == 0 && lane == 0) a.result->hidden_norm = sqrtf(ss);
+    __syncthreads();
+    if constexpr (kLogits) argmax_partial<MODE>(a, -1e30f, 0xffffffffu, 0u, s_bv, s_bi, s_nf);
+  } else {
+    const uint32_t unit0 = blockIdx.x * kRowWaves + wave;
+    U cur;
+    issue_unit<F, MODE>(a, unit0, 0, lane, true, true, &cur);
+    __syncthreads();
+    float x0[F::kCols];
+    const float sx0 = lds_chunk<F>(s_x, a.C, 0, lane, x0);
+    float bv = -1e30f;
+    uint32_t bi = 0xffffffffu, nf = 0;
+    if (unit0 < a.n_units) rows_unit<F, MODE>(a, cur, s_x, x0, sx0, lane, &bv, &bi, &nf);
+    for (uint32_t unit = unit0 + stride; unit < a.n_units; unit += stride) {
+      U u;
+      issue_unit<F, MODE>(a, unit, 0, lane, true, true, &u);
+      rows_unit<F, MODE>(a, u, s_x, x0, sx0, lane, &bv, &bi, &nf);
+    }
+    if constexpr (kLogits) argmax_partial<MODE>(a, bv, bi, nf, s_bv, s_bi, s_nf);
+  }
 }
 
 // One workgroup = one unit, its panels split over NW waves (K-split); partial sums meet in LDS
 // in a fixed order.  The input sits in LDS (dynamic, C floats) so that the flat-tile outlier
 // corrections read any column; wave 0 adds them and writes the unit's rows.
-template <class F, int MODE>
+template <class F, int MODE, bool kWide>
 __global__ void __launch_bounds__(512, 2) k_gemv_split(GemvArgs a) {
+  constexpr bool kNorm = kNormOf<MODE>;
   constexpr int RU = 8, S = kWave / RU;
   constexpr bool kSwi = MODE == int(GemvMode::SwiGlu);
   constexpr bool kLogits = MODE == int(GemvMode::Logits);
   constexpr bool kRope = MODE == int(GemvMode::QkvRope);
   using U = UnitLoads<F, MODE>;
-  extern __shared__ __align__(16) float s_x[];  // C floats
+  extern __shared__ __align__(16) float s_x[];  // xs_floats(C) floats
   __shared__ float s_part[kMaxWavesPerUnit][RU];
   __shared__ float s_red[8], s_bv[8];
   __shared__ uint32_t s_bi[8], s_nf[8];
@@ -567,9 +710,11 @@ __global__ void __launch_bounds__(512, 2) k_gemv_split(GemvArgs a) {
 
   U cur;
   uint32_t unit = blockIdx.x;
+  StageRegs<8> xr0;
+  if constexpr (!kWide) stage_x_issue<kNorm>(a, &xr0);  // the input first (see k_gemv_rows)
   issue_unit<F, MODE>(a, unit, p0, lane, wave == 0, false, &cur);
   float ss = 0.0f, inv = 1.0f;
-  stage_x<kLogits>(a, s_x, s_red, &ss, &inv);
+  stage_x_finish<kNorm, kWide>(a, xr0, s_x, s_red, &ss, &inv);
 
   float bv = -1e30f;
   uint32_t bi = 0xffffffffu, nf = 0;
@@ -622,15 +767,21 @@ __global__ void __launch_bounds__(512, 2) k_gemv_split(GemvArgs a) {
     __syncthreads();
     if (unit + gridDim.x < a.n_units) issue_unit<F, MODE>(a, unit + gridDim.x, p0, lane, wave == 0, false, &cur);
   }
-  if constexpr (kLogits) argmax_partial<MODE>(a, bv, bi, nf, ss, s_bv, s_bi, s_nf);
+  if constexpr (kLogits) {
+    if (blockIdx.x == 0 && threadIdx.x == 0) a.result->hidden_norm = sqrtf(ss);
+    argmax_partial<MODE>(a, bv, bi, nf, s_bv, s_bi, s_nf);
+  }
 }
 
 template <class F, int MODE>
 void launch_one(const GemvArgs& a, const GemvLaunch& g, hipStream_t st) {
+  const size_t lds = size_t(xs_floats(a.C)) * 4;
   if (a.waves_per_unit == 1)
     launch_kernel(&k_gemv_rows<F, MODE>, dim3(g.blocks), dim3(g.threads), st, a);
+  else if (a.C > 4 * 8 * g.threads)  // more than 8 float4 per thread: staged in two passes
+    launch_kernel_lds(&k_gemv_split<F, MODE, true>, dim3(g.blocks), dim3(g.threads), lds, st, a);
   else
-    launch_kernel_lds(&k_gemv_split<F, MODE>, dim3(g.blocks), dim3(g.threads), size_t(a.C) * 4, st, a);
+    launch_kernel_lds(&k_gemv_split<F, MODE, false>, dim3(g.blocks), dim3(g.threads), lds, st, a);
 }
 
 template <class F>
@@ -686,8 +837,8 @@ GemvLaunch gemv_geometry(WeightKind kind, GemvMode mode, uint32_t C, const uint3
   GemvLaunch g{};
   g.ru = ru;
   if (nw == 1) {
-    g.threads = 256;
-    g.blocks = (units + 3) / 4;
+    g.threads = kWave * (kRowWaves + 1);
+    g.blocks = (units + kRowWaves - 1) / kRowWaves;
     const uint32_t cap = mode == GemvMode::Logits ? gemv_tuning().logits_blocks : gemv_tuning().rows_blocks;
     if (cap && g.blocks > cap) g.blocks = cap;  // persistent: the waves stride over the units
   } else {
