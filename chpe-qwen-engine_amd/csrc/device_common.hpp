@@ -51,6 +51,11 @@ __device__ __forceinline__ T gld(const T* p) {
 }
 __device__ __forceinline__ uint16_t ld_u16(const uint8_t* p) { return gld(reinterpret_cast<const uint16_t*>(p)); }
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ float4 ld_f4(const float* p) {
+  const f32x4_t v = gld(reinterpret_cast<const f32x4_t*>(p));
+  return make_float4(v.x, v.y, v.z, v.w);
+}
 __device__ __forceinline__ uint4 ld_u128(const uint8_t* p) {
   const u32x4_t v = gld(reinterpret_cast<const u32x4_t*>(p));
   return make_uint4(v.x, v.y, v.z, v.w);

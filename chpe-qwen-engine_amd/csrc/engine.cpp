@@ -216,7 +216,8 @@ bool Engine::init(const uint8_t* b, size_t len, const EngineConfig& cfg, std::st
   d_mlp_ = static_cast<float*>(dev_alloc(I * 4));
   d_logits_ = static_cast<float*>(dev_alloc(V * 4));
   const size_t kv_elem = cfg.kv_f16 ? 2 : 4;
-  const size_t kv_bytes = arch_.num_layers * kvd * S * kv_elem;
+  kv_rows_ = (S + 15) / 16 * 16;
+  const size_t kv_bytes = arch_.num_layers * kvd * kv_rows_ * kv_elem;
   d_kcache_ = dev_alloc(kv_bytes);
   d_vcache_ = dev_alloc(kv_bytes);
   d_part_ml_ = static_cast<float*>(dev_alloc(arch_.num_attn_heads * n_chunks_ * 2 * 4));
@@ -529,7 +530,7 @@ void Engine::enqueue_qkv(size_t l, hipStream_t st) {
 }
 
 RopeArgs Engine::rope_args(size_t l) const {
-  const size_t kvd = arch_.num_kv_heads * arch_.head_dim, S = cfg_.max_seq_len;
+  const size_t kvd = arch_.num_kv_heads * arch_.head_dim, S = kv_rows_;
   const size_t kv_elem = cfg_.kv_f16 ? 2 : 4;
   RopeArgs r{};
   r.state = d_state_;
@@ -544,7 +545,7 @@ RopeArgs Engine::rope_args(size_t l) const {
 }
 
 AttnArgs Engine::attn_args(size_t l) const {
-  const size_t kvd = arch_.num_kv_heads * arch_.head_dim, S = cfg_.max_seq_len;
+  const size_t kvd = arch_.num_kv_heads * arch_.head_dim, S = kv_rows_;
   const size_t kv_elem = cfg_.kv_f16 ? 2 : 4;
   AttnArgs at{};
   at.state = d_state_;

@@ -162,6 +162,7 @@ class Engine {
   StepResult* h_result_ = nullptr;    // pinned
   int embed_kind_ = 0;
   uint32_t n_chunks_ = 0;
+  size_t kv_rows_ = 0;  // cache rows per kv head: max_seq_len rounded up to a 16-position tile
 
   hipStream_t stream_ = nullptr;
   hipGraph_t graph_ = nullptr;

@@ -501,10 +501,14 @@ __device__ __forceinline__ void rope_store(const GemvArgs& a, const GemvPart& P,
     P.y[r + half] = o1;
     return;
   }
-  const uint32_t hd = a.rope.head_dim, head = r / hd, d = r % hd;
-  const size_t at = (size_t(head) * a.rope.max_seq + a.rope.state->pos) * hd + d;
+  const uint32_t hd = a.rope.head_dim, head = r / hd, d = r % hd, pos = a.rope.state->pos;
+  const size_t at = (size_t(head) * a.rope.max_seq + pos) * hd + d;
   void* cache = P.rope_role == kRoleK ? a.rope.k_cache : a.rope.v_cache;
-  if (a.rope.kv_f16) {
+  if (a.rope.kv_f16 && P.rope_role == kRoleV) {  // 4-position blocks: [pos/4][dim][pos%4]
+    const size_t blk = (size_t(head) * a.rope.max_seq + (pos & ~3u)) * hd + (pos & 3u);
+    reinterpret_cast<__half*>(cache)[blk + size_t(d) * 4] = __float2half_rn(o0);
+    reinterpret_cast<__half*>(cache)[blk + size_t(d + half) * 4] = __float2half_rn(o1);
+  } else if (a.rope.kv_f16) {
     reinterpret_cast<__half*>(cache)[at] = __float2half_rn(o0);
     reinterpret_cast<__half*>(cache)[at + half] = __float2half_rn(o1);
   } else {

@@ -44,8 +44,8 @@ struct RopeArgs {            // QkvRope: applyRope (chpe_engine.zig:195-216) + K
   const float* cos;          // [max_seq][head_dim/2]
   const float* sin;
   void* k_cache;             // this layer: [KV][max_seq][head_dim], f16 or f32
-  void* v_cache;
-  uint32_t head_dim, max_seq, kv_f16, pad;
+  void* v_cache;             // f32: as k_cache; f16: [KV][max_seq/4][head_dim][4] (4-position blocks)
+  uint32_t head_dim, max_seq, kv_f16, pad;  // max_seq: cache rows per kv head, a multiple of 16
 };
 
 constexpr int kMaxParts = 3;
@@ -135,11 +135,11 @@ struct AttnArgs {
   const StepState* state;
   const float* q;           // [H*hd] rotated queries (the QkvRope GEMV's output)
   const void* k_cache;      // this layer: [KV][max_seq][hd], f16 or f32, rows 0..pos written
-  const void* v_cache;
+  const void* v_cache;      // f32: as k_cache; f16: [KV][max_seq/4][hd][4] (4-position blocks)
   float* out;               // [H*hd]
   float* part_ml;           // [H][n_chunks][2] (chunk max, chunk sum)
   float* part_acc;          // [H][n_chunks][hd]
-  uint32_t H, KV, hd, max_seq, n_chunks;
+  uint32_t H, KV, hd, max_seq, n_chunks;  // max_seq: cache rows per kv head, a multiple of 16
   uint32_t kv_f16;
   float scale;              // 1/sqrt(hd)
 };
