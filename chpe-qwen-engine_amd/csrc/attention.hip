@@ -190,15 +190,17 @@ __global__ void __launch_bounds__(NW * 64) k_attn_chunk(AttnArgs a) {
 }
 
 // fp16 cache: the same chunk partials computed on the matrix cores.  Per tile of 16 positions a
-// wave forms S^T = K . Q^T with v_mfma_f32_16x16x16_f16 (A = K rows, B = the group's queries as
-// an f16 high part plus an f16 low part, so the product keeps ~22 bits of the f32 query), then
-// O = P . V with A = P (the exp-weights, again high + low parts) and B = V.  The accumulator
-// layout of the first product (lane n + 16 G holds positions 4G..4G+3 of head n) is the operand
-// layout P needs in the second, so no data moves between the two.  Dimension order inside an
-// MFMA is free as long as both operands agree: lane group G takes dims [G*HD/4, (G+1)*HD/4) of
-// a K row (one contiguous read), and output column n of N-tile j is dim n*HD/16 + j, so a lane's
-// V operand over all N-tiles is one contiguous read of the 4-position-blocked V cache.  Query
-// heads past GQ (the MFMA has 16 rows) are zero.  Exact fp16 products, f32 accumulation.
+// wave forms S^T = K . Q^T with v_mfma_f32_16x16x16_f16: A = the 16 K rows, B = 16 query
+// columns, of which column h < 8 holds query head h rounded to f16 and column h + 8 the f16
+// remainder q - f16(q); adding the two halves of the result (lanes n and n ^ 8) gives the score
+// with ~22 bits of the f32 query.  O = P . V likewise: A rows h and h + 8 hold the exp-weights
+// of head h as f16 and f16 remainder, B = 16 V columns; rows h and h + 8 of the result are added
+// when the waves are merged.  The accumulator layout of the first product (lane n + 16 G holds
+// positions 4G..4G+3 of column n) is the operand layout P needs in the second, so the weights
+// stay in registers.  Dimension order inside an MFMA is free as long as both operands agree:
+// lane group G takes dims [G*HD/4, (G+1)*HD/4) of a K row (one contiguous read), and output
+// column n of N-tile j is dim n*HD/16 + j, so a lane's V operand over all N-tiles is one
+// contiguous read of the 4-position-blocked V cache.  Exact fp16 products, f32 accumulation.
 typedef _Float16 h4_t __attribute__((ext_vector_type(4)));
 typedef float f4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u2_t __attribute__((ext_vector_type(2)));
@@ -207,13 +209,12 @@ __device__ __forceinline__ h4_t as_h4(uint32_t lo, uint32_t hi) {
   const u2_t w = {lo, hi};
   return __builtin_bit_cast(h4_t, w);
 }
-// v = hi + lo with hi = f16(v), lo = f16(v - hi)
-__device__ __forceinline__ void split4(float a, float b, float c, float d, h4_t* hi, h4_t* lo) {
+// f16(v) (rem false) or the f16 of the remainder v - f16(v) (rem true), for 4 values
+__device__ __forceinline__ h4_t f16_part(float a, float b, float c, float d, bool rem) {
   const h4_t h = {(_Float16)a, (_Float16)b, (_Float16)c, (_Float16)d};
-  const h4_t l = {(_Float16)(a - float(h[0])), (_Float16)(b - float(h[1])), (_Float16)(c - float(h[2])),
+  const h4_t r = {(_Float16)(a - float(h[0])), (_Float16)(b - float(h[1])), (_Float16)(c - float(h[2])),
                   (_Float16)(d - float(h[3]))};
-  *hi = h;
-  *lo = l;
+  return rem ? r : h;
 }
 
 template <int HD, int GQ, int NW, int T>
@@ -222,22 +223,24 @@ __global__ void __launch_bounds__(NW * 64) k_attn_mfma(AttnArgs a) {
   constexpr int KS = HD / 16;  // k-steps of the score product
   constexpr int VD = HD / 16;  // V dims per lane = N-tiles of the output product
   constexpr int CH = NW * T * 16, NT = NW * 64;
-  static_assert(CH == int(attn_chunk_of(HD)) && GQ <= 16 && GQ % 4 == 0, "");
+  static_assert(CH == int(attn_chunk_of(HD)) && GQ <= 8 && NW * GQ <= 64 && (NW & (NW - 1)) == 0, "");
   const uint32_t pos = a.state->pos, ctx = pos + 1;
   const uint32_t c = blockIdx.x, kvh = blockIdx.y;
   if (c * CH >= ctx) return;  // the whole workgroup
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const int G = lane >> 4, n = lane & 15;
+  const int G = lane >> 4, n = lane & 15, h = n & 7;  // h: the query head of column / row n
+  const bool rem = n >= 8;
 
-  __shared__ __align__(16) float s_acc[NW][GQ][HD + 4];
+  __shared__ __align__(16) float s_acc[NW][16][HD + 4];
   __shared__ float s_ml[NW][GQ][2];
+  __shared__ float s_f[GQ][NW];
 
-  // 1. loads, all issued before any use: the lane's query dims (head n), K rows (position n of
+  // 1. loads, all issued before any use: the lane's query dims (head h), K rows (position n of
   // each tile, dims of group G) and V blocks (positions 4G..4G+3 of each tile, dims n*VD..);
   // rows past the context read row 0 / block 0 and are masked at use
   const uint32_t p0 = c * CH + uint32_t(wave) * T * 16;
-  const bool qok = n < GQ;
-  const float* qsrc = a.q + size_t(kvh * GQ + (qok ? n : 0)) * HD + G * KD;
+  const bool qok = h < GQ;
+  const float* qsrc = a.q + size_t(kvh * GQ + (qok ? h : 0)) * HD + G * KD;
   float4 qv[KD / 4];
 #pragma unroll
   for (int i = 0; i < KD / 4; ++i) qv[i] = ld_f4(qsrc + 4 * i);
@@ -256,15 +259,15 @@ __global__ void __launch_bounds__(NW * 64) k_attn_mfma(AttnArgs a) {
     for (int i = 0; i < VD / 2; ++i) vf[t][i] = ld_u128(vs + 16 * i);
   }
 
-  // 2. the queries as f16 high + low operands (zero for heads past the group)
-  h4_t qh[KS], ql[KS];
+  // 2. the query operand (zero for heads past the group)
+  h4_t qb[KS];
 #pragma unroll
   for (int st = 0; st < KS; ++st) {
     const float4 v = qok ? qv[st] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    split4(v.x, v.y, v.z, v.w, &qh[st], &ql[st]);
+    qb[st] = f16_part(v.x, v.y, v.z, v.w, rem);
   }
 
-  // 3. scores of the wave's positions: lane (G, n) gets head n at positions 4G + i of each tile
+  // 3. scores: lane (G, n) gets head h at positions 4G + i of each tile (lanes n and n ^ 8 alike)
   float sc[T][4];
   float m = -INFINITY;
 #pragma unroll
@@ -274,13 +277,13 @@ __global__ void __launch_bounds__(NW * 64) k_attn_mfma(AttnArgs a) {
     for (int st = 0; st < KS; ++st) {
       const uint4 w = kf[t][st / 2];
       const h4_t kk = (st & 1) ? as_h4(w.z, w.w) : as_h4(w.x, w.y);
-      acc = __builtin_amdgcn_mfma_f32_16x16x16f16(kk, qh[st], acc, 0, 0, 0);
-      acc = __builtin_amdgcn_mfma_f32_16x16x16f16(kk, ql[st], acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x16f16(kk, qb[st], acc, 0, 0, 0);
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
+      const float s = acc[i] + __shfl_xor(acc[i], 8);
       const bool ok = p0 + t * 16 + 4 * G + i < ctx;
-      sc[t][i] = ok ? acc[i] * a.scale : -INFINITY;
+      sc[t][i] = ok ? s * a.scale : -INFINITY;
       m = fmaxf(m, sc[t][i]);
     }
   }
@@ -300,52 +303,59 @@ __global__ void __launch_bounds__(NW * 64) k_attn_mfma(AttnArgs a) {
       e[i] = sc[t][i] > -INFINITY ? expf(sc[t][i] - m) : 0.0f;
       l += e[i];
     }
-    h4_t ph, pl;
-    split4(e[0], e[1], e[2], e[3], &ph, &pl);
+    const h4_t pa = f16_part(e[0], e[1], e[2], e[3], rem);
 #pragma unroll
     for (int j = 0; j < VD; ++j) {
       const uint4 w = vf[t][j / 2];
       const h4_t vv = (j & 1) ? as_h4(w.z, w.w) : as_h4(w.x, w.y);
-      o[j] = __builtin_amdgcn_mfma_f32_16x16x16f16(ph, vv, o[j], 0, 0, 0);
-      o[j] = __builtin_amdgcn_mfma_f32_16x16x16f16(pl, vv, o[j], 0, 0, 0);
+      o[j] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa, vv, o[j], 0, 0, 0);
     }
   }
   l += __shfl_xor(l, 16);
   l += __shfl_xor(l, 32);
 
-  // 5. the wave's statistics and sums to LDS (lane (G, n) holds heads 4G + i, dims n*VD + j)
-  if (G == 0 && qok) {
+  // 5. the wave's statistics and sums to LDS (lane (G, n) holds rows 4G + i, dims n*VD + j)
+  if (G == 0 && n < GQ) {
     s_ml[wave][n][0] = m;
     s_ml[wave][n][1] = l;
   }
-  if (4 * G < GQ) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < 4; ++i)
 #pragma unroll
-      for (int j = 0; j < VD; ++j) s_acc[wave][4 * G + i][n * VD + j] = o[j][i];
-  }
+    for (int j = 0; j < VD; j += 4)
+      *reinterpret_cast<float4*>(&s_acc[wave][4 * G + i][n * VD + j]) =
+          make_float4(o[j][i], o[j + 1][i], o[j + 2][i], o[j + 3][i]);
   __syncthreads();
 
-  // 6. merge the waves; one partial per (query head, chunk)
+  // 6. the waves' rescale factors exp(m_w - M) and the chunk statistics (M, L), per head: thread
+  // g*NW + w of the first wave
   const uint32_t nch = a.n_chunks;
-  for (int i = tid; i < GQ * HD; i += NT) {
-    const int g = i / HD, d = i % HD;
-    float M = s_ml[0][g][0];
+  if (tid < NW * GQ) {
+    const int g = tid / NW, w = tid % NW;
+    const float mw = s_ml[w][g][0], lw = s_ml[w][g][1];
+    float M = mw;
 #pragma unroll
-    for (int w = 1; w < NW; ++w) M = fmaxf(M, s_ml[w][g][0]);
-    float A = 0.0f, L = 0.0f;
+    for (int o2 = 1; o2 < NW; o2 <<= 1) M = fmaxf(M, __shfl_xor(M, o2));
+    const float f = lw > 0.0f ? expf(mw - M) : 0.0f;
+    float L = lw * f;
 #pragma unroll
-    for (int w = 0; w < NW; ++w) {
-      const float f = s_ml[w][g][1] > 0.0f ? expf(s_ml[w][g][0] - M) : 0.0f;
-      A = fmaf(s_acc[w][g][d], f, A);
-      L = fmaf(s_ml[w][g][1], f, L);
-    }
-    const size_t hc = size_t(kvh * GQ + g) * nch + c;
-    a.part_acc[hc * HD + d] = A;
-    if (d == 0) {
+    for (int o2 = 1; o2 < NW; o2 <<= 1) L += __shfl_xor(L, o2);
+    s_f[g][w] = f;
+    if (w == 0) {
+      const size_t hc = size_t(kvh * GQ + g) * nch + c;
       a.part_ml[hc * 2] = M;
       a.part_ml[hc * 2 + 1] = L;
     }
+  }
+  __syncthreads();
+
+  // 7. merge the waves (rows h and h + 8 of each wave); one partial per (query head, chunk)
+  for (int i = tid; i < GQ * HD; i += NT) {
+    const int g = i / HD, d = i % HD;
+    float A = 0.0f;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) A = fmaf(s_acc[w][g][d] + s_acc[w][g + 8][d], s_f[g][w], A);
+    a.part_acc[(size_t(kvh * GQ + g) * nch + c) * HD + d] = A;
   }
 }
 
@@ -409,11 +419,11 @@ __global__ void __launch_bounds__(512) k_attn_merge(AttnArgs a) {
 void launch_attention_partial(const AttnArgs& a, hipStream_t st) {
   const dim3 grid(a.n_chunks, a.KV);
   const uint32_t gq = a.H / a.KV;
-  if (a.hd == 128 && gq == 8)  // fp16: 8 waves x 1 tile; f32: 8 waves x 16 positions, 4 lanes per K row
-    a.kv_f16 ? launch_kernel(&k_attn_mfma<128, 8, 8, 1>, grid, dim3(512), st, a)
+  if (a.hd == 128 && gq == 8)  // fp16: 4 waves x 2 tiles; f32: 8 waves x 16 positions, 4 lanes per K row
+    a.kv_f16 ? launch_kernel(&k_attn_mfma<128, 8, 4, 2>, grid, dim3(256), st, a)
              : launch_kernel(&k_attn_chunk<128, 8, float, 4, 8>, grid, dim3(512), st, a);
-  else if (a.hd == 256 && gq == 4)  // fp16: 4 waves x 1 tile; f32: 4 waves x 16 positions
-    a.kv_f16 ? launch_kernel(&k_attn_mfma<256, 4, 4, 1>, grid, dim3(256), st, a)
+  else if (a.hd == 256 && gq == 4)  // fp16: 2 waves x 2 tiles; f32: 4 waves x 16 positions
+    a.kv_f16 ? launch_kernel(&k_attn_mfma<256, 4, 2, 2>, grid, dim3(128), st, a)
              : launch_kernel(&k_attn_chunk<256, 4, float, 4, 4>, grid, dim3(256), st, a);
 }
 
