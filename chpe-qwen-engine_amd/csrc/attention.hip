@@ -359,59 +359,59 @@ __global__ void __launch_bounds__(NW * 64) k_attn_mfma(AttnArgs a) {
   }
 }
 
-// out[h][d] = sum_c A_c[d] exp(M_c - M) / sum_c L_c exp(M_c - M) over the active chunks
+// out[h][d] = sum_c A_c[d] w_c / sum_c L_c w_c, w_c = exp(M_c - M), over the active chunks.  One
+// wave per (head, 64 dims): lane d of dims block y.  The chunk statistics are spread over the
+// lanes (chunk lane + 64 k), the weights go through LDS (w_c = 0 past the active chunks, whose
+// sums are read at chunk 0 and so contribute exactly 0), and every load of a batch of 32
+// chunks is issued before its use.
 template <int HD>
-__global__ void __launch_bounds__(512) k_attn_merge(AttnArgs a) {
-  constexpr int NT = 512, P = NT / HD, CH = attn_chunk_of(HD);
-  const uint32_t h = blockIdx.x, n_act = (a.state->pos + CH) / CH, nch = a.n_chunks;
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  __shared__ float s_w[kAttnMaxChunks];
-  __shared__ float s_red[NT / 64];
-  __shared__ float s_o[P][HD];
+__global__ void __launch_bounds__(64) k_attn_merge(AttnArgs a) {
+  constexpr uint32_t CH = attn_chunk_of(HD), KC = (kAttnMaxChunks + 63) / 64, B = 32;
+  static_assert(kAttnMaxChunks % 4 == 0 && B % 4 == 0, "");
+  __shared__ __align__(16) float s_w[KC * 64];
+  const uint32_t h = blockIdx.x, lane = threadIdx.x, d = blockIdx.y * 64 + lane;
+  const uint32_t n_act = (a.state->pos + CH) / CH, nch = a.n_chunks;
   const float* ml = a.part_ml + size_t(h) * nch * 2;
-  const int d = tid % HD, part = tid / HD;
   const float* acc = a.part_acc + size_t(h) * nch * HD + d;
-  // every load first: the thread's chunk sums, and (one chunk per thread) the chunk statistics
-  constexpr int kPer = int(kAttnMaxChunks) / P;  // chunks per thread at most
-  float av[kPer];
+  float mv[KC], lv[KC], av[B];
 #pragma unroll
-  for (int k = 0; k < kPer; ++k) {
-    const uint32_t j = uint32_t(part + k * P);
-    av[k] = j < n_act ? acc[size_t(j) * HD] : 0.0f;
+  for (uint32_t k = 0; k < KC; ++k) {
+    const uint32_t cc = lane + 64 * k, cl = cc < n_act ? cc : 0u;
+    mv[k] = ml[2 * cl];
+    lv[k] = ml[2 * cl + 1];
   }
-  const bool mine = uint32_t(tid) < n_act;  // n_act <= kAttnMaxChunks <= NT
-  const float mi = mine ? ml[2 * tid] : -INFINITY, li = mine ? ml[2 * tid + 1] : 0.0f;
-  float m = mi;
 #pragma unroll
-  for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
-  if (lane == 0) s_red[wave] = m;
-  __syncthreads();
-  float M = s_red[0];
+  for (uint32_t k = 0; k < B; ++k) av[k] = acc[size_t(k < n_act ? k : 0u) * HD];
+  float M = -INFINITY;
 #pragma unroll
-  for (int w = 1; w < NT / 64; ++w) M = fmaxf(M, s_red[w]);
-  __syncthreads();
-  const float wi = mine ? expf(mi - M) : 0.0f;
-  if (mine) s_w[tid] = wi;
-  const float l = wave_sum(li * wi);
-  if (lane == 0) s_red[wave] = l;
-  __syncthreads();
+  for (uint32_t k = 0; k < KC; ++k) M = fmaxf(M, lane + 64 * k < n_act ? mv[k] : -INFINITY);
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o));
   float L = 0.0f;
 #pragma unroll
-  for (int w = 0; w < NT / 64; ++w) L += s_red[w];
-  float o = 0.0f;
-#pragma unroll
-  for (int k = 0; k < kPer; ++k) {
-    const uint32_t j = uint32_t(part + k * P);
-    if (j < n_act) o = fmaf(av[k], s_w[j], o);
+  for (uint32_t k = 0; k < KC; ++k) {
+    const float w = lane + 64 * k < n_act ? expf(mv[k] - M) : 0.0f;
+    s_w[lane + 64 * k] = w;
+    L = fmaf(lv[k], w, L);
   }
-  s_o[part][d] = o;
+  L = wave_sum(L);
   __syncthreads();
-  if (part == 0) {
-    float sum = s_o[0][d];
+  float o4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (uint32_t c0 = 0; c0 < n_act; c0 += B) {
+    if (c0 > 0) {  // longer contexts: further batches
 #pragma unroll
-    for (int q = 1; q < P; ++q) sum += s_o[q][d];
-    a.out[size_t(h) * HD + d] = sum / L;
+      for (uint32_t k = 0; k < B; ++k) av[k] = acc[size_t(c0 + k < n_act ? c0 + k : 0u) * HD];
+    }
+#pragma unroll
+    for (uint32_t k = 0; k < B; k += 4) {
+      const float4 w4 = *reinterpret_cast<const float4*>(&s_w[c0 + k]);
+      o4[0] = fmaf(av[k], w4.x, o4[0]);
+      o4[1] = fmaf(av[k + 1], w4.y, o4[1]);
+      o4[2] = fmaf(av[k + 2], w4.z, o4[2]);
+      o4[3] = fmaf(av[k + 3], w4.w, o4[3]);
+    }
   }
+  a.out[size_t(h) * HD + d] = ((o4[0] + o4[1]) + (o4[2] + o4[3])) / L;
 }
 
 }  // namespace
@@ -428,8 +428,8 @@ void launch_attention_partial(const AttnArgs& a, hipStream_t st) {
 }
 
 void launch_attention_combine(const AttnArgs& a, hipStream_t st) {
-  if (a.hd == 128) launch_kernel(&k_attn_merge<128>, dim3(a.H), dim3(512), st, a);
-  else launch_kernel(&k_attn_merge<256>, dim3(a.H), dim3(512), st, a);
+  if (a.hd == 128) launch_kernel(&k_attn_merge<128>, dim3(a.H, 2), dim3(64), st, a);
+  else launch_kernel(&k_attn_merge<256>, dim3(a.H, 4), dim3(64), st, a);
 }
 
 bool attention_supported(uint32_t H, uint32_t KV, uint32_t hd) {
