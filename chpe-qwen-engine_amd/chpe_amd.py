@@ -28,6 +28,7 @@ ENGINE_SYMBOLS = [
     "chpe_generate", "chpe_last_error", "chpe_get_max_seq_len", "chpe_get_hidden",
     "chpe_time_steps", "chpe_time_stage", "chpe_time_stage_live", "chpe_stage_bytes", "chpe_step_bytes",
     "chpe_debug_gemv", "chpe_debug_flat_tile_weights", "chpe_debug_embed_row_cell",
+    "chpe_debug_attention",
 ]
 
 _c_float_p = ctypes.POINTER(ctypes.c_float)
@@ -77,6 +78,8 @@ def load_engine_lib():
             "chpe_debug_gemv": (I, [V, S, I, _c_float_p, _c_float_p]),
             "chpe_debug_flat_tile_weights": (I, [_c_u8_p, _c_float_p]),
             "chpe_debug_embed_row_cell": (I, [_c_u8_p, S, ctypes.c_uint32, ctypes.c_uint32, _c_float_p]),
+            "chpe_debug_attention": (I, [ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32, I, ctypes.c_uint32,
+                                         _c_float_p, _c_float_p, _c_float_p, _c_float_p]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(lib, name)
@@ -274,6 +277,21 @@ def gpu_embed_row_cell(region, row, D, init=None):
     if rc < 0:
         raise EngineError(f"chpe_debug_embed_row_cell failed: {rc}")
     return rc, out
+
+
+def gpu_attention(q, k_rows, v_rows, pos, heads, kv_heads, head_dim, kv_f16):
+    """The decode step's attention kernels on caller rows (k_rows / v_rows: [pos+1][kv*hd] f32)."""
+    q = np.ascontiguousarray(q, dtype=np.float32)
+    k = np.ascontiguousarray(k_rows, dtype=np.float32)
+    v = np.ascontiguousarray(v_rows, dtype=np.float32)
+    if q.size != heads * head_dim or k.size != (pos + 1) * kv_heads * head_dim or v.size != k.size:
+        raise ValueError("attention operand sizes do not match the shape")
+    out = np.empty(heads * head_dim, dtype=np.float32)
+    rc = load_engine_lib().chpe_debug_attention(head_dim, heads, kv_heads, int(kv_f16), pos, _fp(q), _fp(k),
+                                                _fp(v), _fp(out))
+    if rc:
+        raise EngineError(f"chpe_debug_attention failed: {rc}")
+    return out
 
 
 def build(jobs=8):

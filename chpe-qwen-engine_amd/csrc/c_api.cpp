@@ -9,9 +9,11 @@
 #include <sys/stat.h>
 #include <unistd.h>
 
+#include <cmath>
 #include <cstring>
 #include <memory>
 #include <string>
+#include <vector>
 
 #include "../../include/chpe.h"
 #include "engine.hpp"
@@ -267,6 +269,72 @@ int chpe_debug_embed_row_cell(const uint8_t* bytes, size_t len, uint32_t row, ui
   if (dout) (void)hipFree(dout);
   if (dw) (void)hipFree(dw);
   return written;
+}
+
+// The decode step's attention kernels on caller data: the caller's f32 rows are laid out as
+// the engine's cache holds them (fp16 rounded to nearest even when kv_f16; V in 4-position
+// blocks for fp16), and the chunk + merge kernels run once.
+int chpe_debug_attention(uint32_t head_dim, uint32_t heads, uint32_t kv_heads, int kv_f16, uint32_t pos,
+                         const float* q, const float* k_rows, const float* v_rows, float* out) {
+  if (!q || !k_rows || !v_rows || !out || !attention_supported(heads, kv_heads, head_dim)) return -1;
+  const uint32_t chunk = attn_chunk_of(head_dim), ctx = pos + 1;
+  const uint32_t n_chunks = (ctx + chunk - 1) / chunk, rows = n_chunks * chunk;  // a multiple of 16
+  if (n_chunks > kAttnMaxChunks) return -1;
+  const size_t hd = head_dim, kvd = size_t(kv_heads) * hd, el = kv_f16 ? 2 : 4;
+  std::vector<uint8_t> kc(size_t(kv_heads) * rows * hd * el, 0), vc(kc.size(), 0);
+  for (size_t t = 0; t < ctx; ++t)
+    for (size_t h = 0; h < kv_heads; ++h)
+      for (size_t d = 0; d < hd; ++d) {
+        const float kv = k_rows[t * kvd + h * hd + d], vv = v_rows[t * kvd + h * hd + d];
+        const size_t ka = (h * rows + t) * hd + d;
+        if (kv_f16) {
+          const size_t va = (h * rows + (t & ~size_t(3))) * hd + d * 4 + (t & 3);
+          reinterpret_cast<uint16_t*>(kc.data())[ka] = f32_to_f16(kv);
+          reinterpret_cast<uint16_t*>(vc.data())[va] = f32_to_f16(vv);
+        } else {
+          reinterpret_cast<float*>(kc.data())[ka] = kv;
+          reinterpret_cast<float*>(vc.data())[ka] = vv;
+        }
+      }
+  const size_t qn = size_t(heads) * hd;
+  void *dk = nullptr, *dv = nullptr;
+  float *dq = nullptr, *dout = nullptr, *dml = nullptr, *dacc = nullptr;
+  StepState* dst = nullptr;
+  StepState st{};
+  st.pos = pos;
+  int rc = -3;
+  if (hipMalloc(&dk, kc.size()) == hipSuccess && hipMalloc(&dv, vc.size()) == hipSuccess &&
+      hipMalloc(&dq, qn * 4) == hipSuccess && hipMalloc(&dout, qn * 4) == hipSuccess &&
+      hipMalloc(&dml, size_t(heads) * n_chunks * 2 * 4) == hipSuccess &&
+      hipMalloc(&dacc, size_t(heads) * n_chunks * hd * 4) == hipSuccess &&
+      hipMalloc(&dst, sizeof(StepState)) == hipSuccess &&
+      hipMemcpy(dk, kc.data(), kc.size(), hipMemcpyHostToDevice) == hipSuccess &&
+      hipMemcpy(dv, vc.data(), vc.size(), hipMemcpyHostToDevice) == hipSuccess &&
+      hipMemcpy(dq, q, qn * 4, hipMemcpyHostToDevice) == hipSuccess &&
+      hipMemcpy(dst, &st, sizeof st, hipMemcpyHostToDevice) == hipSuccess) {
+    AttnArgs a{};
+    a.state = dst;
+    a.q = dq;
+    a.k_cache = dk;
+    a.v_cache = dv;
+    a.out = dout;
+    a.part_ml = dml;
+    a.part_acc = dacc;
+    a.H = heads;
+    a.KV = kv_heads;
+    a.hd = head_dim;
+    a.max_seq = rows;
+    a.n_chunks = n_chunks;
+    a.kv_f16 = kv_f16 ? 1 : 0;
+    a.scale = 1.0f / std::sqrt(float(head_dim));
+    launch_attention(a, nullptr);
+    if (hipDeviceSynchronize() == hipSuccess && hipMemcpy(out, dout, qn * 4, hipMemcpyDeviceToHost) == hipSuccess)
+      rc = 0;
+  }
+  for (void* p : {dk, dv, static_cast<void*>(dq), static_cast<void*>(dout), static_cast<void*>(dml),
+                  static_cast<void*>(dacc), static_cast<void*>(dst)})
+    if (p) (void)hipFree(p);
+  return rc;
 }
 
 }  // extern "C"

@@ -98,6 +98,13 @@ int chpe_debug_flat_tile_weights(const uint8_t *cell, float *out32768);
  * read past the cell).  Returns 1 if written, 0 if the row is out of range, <0 on error. */
 int chpe_debug_embed_row_cell(const uint8_t *bytes, size_t len, uint32_t row, uint32_t D,
                               float *out);
+/* The decode step's attention (chunk + merge kernels) on caller data: q [heads][head_dim]
+ * rotated queries, k_rows / v_rows [pos+1][kv_heads*head_dim] f32 (the layout of the
+ * reference's KVCache rows, src/chpe_engine.zig:755-801); kv_f16 rounds them to fp16 first,
+ * as the fp16 cache holds them.  out [heads][head_dim] (the attention loop :1700-1734).
+ * 0 on success, -1 bad arguments or unsupported shape, -3 device error. */
+int chpe_debug_attention(uint32_t head_dim, uint32_t heads, uint32_t kv_heads, int kv_f16, uint32_t pos,
+                         const float *q, const float *k_rows, const float *v_rows, float *out);
 
 #ifdef __cplusplus
 }

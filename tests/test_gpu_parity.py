@@ -137,6 +137,32 @@ def test_projection_parity(w4, layer):
         assert (np.abs(yg - yo) <= tol).all(), (name, float(np.abs(yg - yo).max()))
 
 
+# (head_dim, query heads, kv heads): the 3B, 9B and 72B attention shapes
+ATTN_SHAPES = [(128, 16, 2), (256, 16, 4), (128, 64, 8)]
+
+
+@pytest.mark.parametrize("kv_f16", [1, 0])
+@pytest.mark.parametrize("hd,H,KV", ATTN_SHAPES)
+def test_attention_kernels_match_oracle(hd, H, KV, kv_f16):
+    """The chunk + merge kernels against the oracle's attention (chpe_engine.zig:1700-1734) on
+    the same rows (fp16-rounded for the fp16 cache): first position, partial and full 16-row
+    tiles, chunk boundaries and a long context.  Tolerance: 2e-5 * max|v| (the matrix-core
+    path keeps ~22 bits of the f32 queries and weights; sums run in another order)."""
+    rng = np.random.default_rng(hd * 1000 + H + kv_f16)
+    chunk = 16384 // hd
+    for pos in (0, 1, 3, 15, 16, 17, chunk - 1, chunk, chunk + 1, 3 * chunk + 5, 1000, 4351):
+        say(f"attention hd={hd} H={H} KV={KV} kv_f16={kv_f16} pos={pos}")
+        q = (rng.standard_normal(H * hd) * 2.0).astype(np.float32)
+        k = rng.standard_normal((pos + 1, KV * hd)).astype(np.float32)
+        v = rng.standard_normal((pos + 1, KV * hd)).astype(np.float32)
+        kr, vr = (k.astype(np.float16).astype(np.float32), v.astype(np.float16).astype(np.float32)) \
+            if kv_f16 else (k, v)
+        ref = orc.attention(q, kr, vr, pos, H, KV, hd)
+        got = ca.gpu_attention(q, k, v, pos, H, KV, hd, kv_f16)
+        err = float(np.max(np.abs(got - ref)))
+        assert err <= 2e-5 * float(np.max(np.abs(vr))), (pos, err)
+
+
 def compare_step(e_logits, o_logits, tag):
     d = np.abs(e_logits.astype(np.float64) - o_logits)
     cos = float(e_logits.astype(np.float64) @ o_logits / np.linalg.norm(e_logits) / np.linalg.norm(o_logits))
