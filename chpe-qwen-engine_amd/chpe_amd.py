@@ -25,7 +25,7 @@ ENGINE_SYMBOLS = [
     "chpe_get_hidden_dim", "chpe_get_num_layers", "chpe_get_last_elapsed_ns",
     "chpe_get_last_argmax", "chpe_get_last_max_logit", "chpe_get_last_token0_logit",
     "chpe_get_last_hidden_norm", "chpe_free", "chpe_init_ex", "chpe_decode_step",
-    "chpe_generate", "chpe_last_error", "chpe_get_max_seq_len", "chpe_get_hidden",
+    "chpe_generate", "chpe_verify", "chpe_last_error", "chpe_get_max_seq_len", "chpe_get_hidden",
     "chpe_time_steps", "chpe_time_stage", "chpe_time_stage_live", "chpe_stage_bytes", "chpe_step_bytes",
     "chpe_debug_gemv", "chpe_debug_flat_tile_weights", "chpe_debug_embed_row_cell",
     "chpe_debug_attention",
@@ -67,6 +67,7 @@ def load_engine_lib():
             "chpe_init_ex": (V, [ctypes.c_char_p, I, S, I]),
             "chpe_decode_step": (I, [V, ctypes.c_uint32, S, _c_float_p]),
             "chpe_generate": (I, [V, _c_u32_p, S, S, _c_u32_p]),
+            "chpe_verify": (I, [V, _c_u32_p, S, S, _c_u32_p]),
             "chpe_last_error": (ctypes.c_char_p, []),
             "chpe_get_max_seq_len": (S, [V]),
             "chpe_get_hidden": (I, [V, _c_float_p]),
@@ -211,6 +212,13 @@ class Engine:
         rc = self.lib.chpe_generate(self.ctx, p.ctypes.data_as(_c_u32_p), p.size, n_gen,
                                     out.ctypes.data_as(_c_u32_p))
         self._check(rc, "chpe_generate")
+        return out
+
+    def verify(self, drafts, pos):
+        d = np.ascontiguousarray(drafts, dtype=np.uint32)
+        out = np.empty(d.size, dtype=np.uint32)
+        rc = self.lib.chpe_verify(self.ctx, d.ctypes.data_as(_c_u32_p), d.size, pos, out.ctypes.data_as(_c_u32_p))
+        self._check(rc, "chpe_verify")
         return out
 
     def logits(self):

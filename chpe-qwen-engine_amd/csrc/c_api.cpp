@@ -146,6 +146,16 @@ int chpe_generate(void* ctx, const uint32_t* prompt, size_t n_prompt, size_t n_g
   return 0;
 }
 
+int chpe_verify(void* ctx, const uint32_t* drafts, size_t m, size_t pos, uint32_t* out_argmax) {
+  if (!ctx || !drafts || m == 0 || !out_argmax) return -1;
+  Context* c = C(ctx);
+  ForwardResult r{};
+  const int rc = c->engine->verify(drafts, m, pos, out_argmax, &r);
+  if (rc) return rc;
+  remember(c, r);
+  return 0;
+}
+
 size_t chpe_get_last_logits(void* ctx, float* out, size_t max_len) {
   if (!ctx || !out) return 0;
   Context* c = C(ctx);

@@ -717,6 +717,24 @@ int Engine::generate(const uint32_t* prompt, size_t n_prompt, size_t n_gen, uint
   return 0;
 }
 
+int Engine::verify(const uint32_t* drafts, size_t m, size_t pos, uint32_t* out_argmax, ForwardResult* last) {
+  if (!drafts || m == 0 || !out_argmax) return -1;
+  if (pos + m > cfg_.max_seq_len) return -2;
+  const uint64_t t0 = now_ns();
+  // the drafts take the prompt slots of their positions, so every step is teacher-forced
+  if (hipMemcpyAsync(d_prompt_ + pos, drafts, m * 4, hipMemcpyHostToDevice, stream_) != hipSuccess) return -3;
+  *h_state_ = StepState{drafts[0], uint32_t(pos), uint32_t(pos + m), 0};
+  if (hipMemcpyAsync(d_state_, h_state_, sizeof(StepState), hipMemcpyHostToDevice, stream_) != hipSuccess) return -3;
+  launch_steps(m);
+  if (sync()) return -3;
+  if (hipMemcpy(out_argmax, d_out_tokens_ + pos, m * 4, hipMemcpyDeviceToHost) != hipSuccess) return -3;
+  if (last) {
+    if (read_result(last)) return -3;
+    last->elapsed_ns = now_ns() - t0;
+  }
+  return 0;
+}
+
 int Engine::copy_logits(float* out) const {
   return hipMemcpy(out, d_logits_, arch_.vocab_size * 4, hipMemcpyDeviceToHost) == hipSuccess ? 0 : -3;
 }

@@ -81,6 +81,9 @@ class Engine {
   // prompt teacher-forced, then n_gen greedy tokens fed back on the device
   int generate(const uint32_t* prompt, size_t n_prompt, size_t n_gen, uint32_t* out_tokens,
                ForwardResult* last);
+  // drafts[0..m) at positions pos..pos+m-1, each step teacher-forced (the KV rows at those
+  // positions are overwritten); out_argmax[i] = argmax after draft i
+  int verify(const uint32_t* drafts, size_t m, size_t pos, uint32_t* out_argmax, ForwardResult* last);
   // enqueue n graph launches continuing from the current device state (no sync)
   void launch_steps(size_t n);
   int sync();

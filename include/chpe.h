@@ -65,6 +65,14 @@ int chpe_decode_step(void *ctx, uint32_t token, size_t pos, float *out_logits);
 int chpe_generate(void *ctx, const uint32_t *prompt, size_t n_prompt, size_t n_gen,
                   uint32_t *out_tokens);
 
+/* Batch-M verify: drafts[0..m) consumed at positions pos..pos+m-1 over the cache built by
+ * earlier calls, out_argmax[i] = the argmax after draft i.  Identical to m sequential
+ * chpe_decode_step(ctx, drafts[i], pos + i) calls (the reference has no verify code; its
+ * equivalent is m forwardDecode calls, src/chpe_engine.zig:1663-1803, whose KV write at pos
+ * overwrites the row, :1693-1697).  last_* report the final step; chpe_get_last_logits gives
+ * its logits.  Returns 0, -1 bad args, -2 pos + m > max_seq_len, -3 device error. */
+int chpe_verify(void *ctx, const uint32_t *drafts, size_t m, size_t pos, uint32_t *out_argmax);
+
 /* Message of the last failed chpe_init / chpe_init_ex on this thread ("" if none). */
 const char *chpe_last_error(void);
 

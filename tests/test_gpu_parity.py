@@ -205,6 +205,33 @@ def test_token_stream_w4(w4):
     assert check_stream(g, r, gaps, "w4") == 32
 
 
+@pytest.mark.parametrize("m", [1, 4, 8])
+def test_verify_equals_sequential_steps(w4, m):
+    """chpe_verify (batch-M verify, no reference code) is defined as m sequential
+    forwardDecode(draft_i, pos + i): same argmaxes and, for the last draft, the same logits
+    bit for bit; for m = 4 the argmaxes also match the oracle's sequential steps."""
+    e, o = w4
+    rng = np.random.default_rng(100 + m)
+    prompt = rng.integers(0, V, 6).astype(np.uint32)
+    drafts = rng.integers(0, V, m).astype(np.uint32)
+    p = int(prompt.size)
+    say(f"verify m={m} at pos {p}")
+    e.forward_tokens(prompt)
+    got = e.verify(drafts, p)
+    last = e.logits()
+    e.forward_tokens(prompt)
+    seq = [e.decode_step(int(d), p + i) for i, d in enumerate(drafts)]
+    assert [int(x) for x in got] == [am for am, _ in seq]
+    assert np.array_equal(bits(last), bits(seq[-1][1]))
+    if m == 4:
+        for pos, tok in enumerate(prompt):
+            o.forward(int(tok), pos)
+        for i, d in enumerate(drafts):
+            r = o.forward(int(d), p + i)
+            compare_step(seq[i][1], o.logits(), f"verify {i}")
+            assert int(got[i]) == r.argmax_token
+
+
 def test_c_abi_semantics(w4_archive):
     """chpe_forward_tokens restarts at position 0 (chpe_c_api.zig:61-63); chpe_init fixes
     max_seq_len 2048 and guesses the 3B architecture from a path without "9B"/"72B"."""
