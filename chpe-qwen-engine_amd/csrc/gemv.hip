@@ -649,7 +649,7 @@ __device__ __forceinline__ float stage_wave(const GemvArgs& a, float* s_x, int l
 // waves plus one staging wave that puts the (normalised) input into LDS, so the unit waves'
 // loads are only weights and their arithmetic runs row by row as the rows arrive.  A wave
 // whose grid is capped (the LM head) strides over further units.
-constexpr int kRowWaves = 4;
+constexpr int kRowWaves = 3;
 template <class F, int MODE>
 __global__ void __launch_bounds__(kWave * (kRowWaves + 1), 2) k_gemv_rows(GemvArgs a) {
   constexpr bool kLogits = MODE == int(GemvMode::Logits);
