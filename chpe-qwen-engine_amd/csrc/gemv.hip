@@ -213,7 +213,8 @@ __device__ __forceinline__ float cell_outlier_sum(const CellExtras<8>& e, const 
 // the row it owns after the reduce-scatter -- and entries (l & 7) + 8 j of that row's list.
 constexpr int kCorrSlots = int(kMaxCorrPerRow) / 8;
 struct FlatExtras {
-  float2 e[kCorrSlots];
+  float2 e[kCorrSlots];  // (column bits, correction) as loaded
+  uint32_t use;          // bit j: slot j is an entry of the row (applied at use, not at load)
 };
 struct NoExtras {};
 
@@ -231,13 +232,15 @@ __device__ __forceinline__ void load_flat_extras(const GemvPart& P0, const GemvP
   // every slot loads (absent ones: the first entry of a valid table, or of the input vector
   // when there is no table) and is masked afterwards
   const float2* src = corr ? corr : reinterpret_cast<const float2*>(x_any);
+  uint32_t m = 0;
 #pragma unroll
   for (int j = 0; j < kCorrSlots; ++j) {
     const uint32_t k = uint32_t(lane & 7) + 8u * uint32_t(j);
     const bool use = ok && k < kmax;
-    const float2 e = src[use ? size_t(r) * kmax + k : 0];
-    f->e[j] = make_float2(e.x, keep_if(use, e.y));
+    f->e[j] = src[use ? size_t(r) * kmax + k : 0];
+    m |= uint32_t(use) << j;
   }
+  f->use = m;
 }
 
 // sum over the lane's entries (x from the workgroup's normalised copy), then over the 8 lanes
@@ -246,7 +249,7 @@ __device__ __forceinline__ float flat_correction(const FlatExtras& f, const floa
   float cs = 0.0f;
 #pragma unroll
   for (int j = 0; j < kCorrSlots; ++j)
-    if (f.e[j].y != 0.0f) cs = fmaf(f.e[j].y, s_x[xs_at(__float_as_uint(f.e[j].x))], cs);
+    if (((f.use >> j) & 1u) && f.e[j].y != 0.0f) cs = fmaf(f.e[j].y, s_x[xs_at(__float_as_uint(f.e[j].x))], cs);
   cs += __shfl_xor(cs, 1);
   cs += __shfl_xor(cs, 2);
   cs += __shfl_xor(cs, 4);
@@ -461,6 +464,7 @@ __device__ __forceinline__ void issue_unit(const GemvArgs& a, uint32_t unit, uin
     if (active) load_cell_extras<F, RU, MODE>(P0, P1, u->row_base, half, lane, &u->ce);
   }
   if constexpr (UnitLoads<F, MODE>::kFlat) {
+    u->fe.use = 0;
     if (active && with_corr) load_flat_extras<RU, MODE>(P0, P1, u->row_base, half, lane, a.x, &u->fe);
   }
   // Branch-free like the panel loads: each lane loads at a valid (clamped) address and the
