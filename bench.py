@@ -42,9 +42,9 @@ STAGES = {  # stage id -> (description, kernel name as rocprofv3 prints it, laun
         f"void {NS}k_gemv_rows<{NS}Cell16W4, 4>(chpe::GemvArgs)", LAYERS),
     1: ("o GEMV + residual", f"void {NS}k_gemv_rows<{NS}Cell16W4, 1>(chpe::GemvArgs)", LAYERS),
     2: ("gate/up GEMV + SwiGLU (RMSNorm fused)", f"void {NS}k_gemv_rows<{NS}Cell16W4, 2>(chpe::GemvArgs)", LAYERS),
-    3: ("down GEMV + residual (flat tiles)", f"void {NS}k_gemv_split<{NS}FlatW4, 1>(chpe::GemvArgs)", LAYERS),
+    3: ("down GEMV + residual (flat tiles)", f"void {NS}k_gemv_split<{NS}FlatW4, 1, false>(chpe::GemvArgs)", LAYERS),
     4: ("LM head GEMV + argmax partials", f"void {NS}k_gemv_rows<{NS}Cell16W4, 3>(chpe::GemvArgs)", 1),
-    5: ("attention over the context chunks", f"void {NS}k_attn_chunk<128, 8, __half, 4, 8>(chpe::AttnArgs)", LAYERS),
+    5: ("attention over the context chunks", f"void {NS}k_attn_mfma<128, 8, 4, 2>(chpe::AttnArgs)", LAYERS),
     6: ("attention chunk merge", f"void {NS}k_attn_merge<128>(chpe::AttnArgs)", LAYERS),
 }
 
