@@ -28,7 +28,7 @@ ENGINE_SYMBOLS = [
     "chpe_generate", "chpe_verify", "chpe_last_error", "chpe_get_max_seq_len", "chpe_get_hidden",
     "chpe_time_steps", "chpe_time_stage", "chpe_time_stage_live", "chpe_stage_bytes", "chpe_step_bytes",
     "chpe_debug_gemv", "chpe_debug_flat_tile_weights", "chpe_debug_embed_row_cell",
-    "chpe_debug_attention",
+    "chpe_debug_attention", "chpe_debug_deltanet_conv", "chpe_debug_deltanet_step",
 ]
 
 _c_float_p = ctypes.POINTER(ctypes.c_float)
@@ -81,6 +81,9 @@ def load_engine_lib():
             "chpe_debug_embed_row_cell": (I, [_c_u8_p, S, ctypes.c_uint32, ctypes.c_uint32, _c_float_p]),
             "chpe_debug_attention": (I, [ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32, I, ctypes.c_uint32,
                                          _c_float_p, _c_float_p, _c_float_p, _c_float_p]),
+            "chpe_debug_deltanet_conv": (I, [ctypes.c_uint32, ctypes.c_uint32, _c_float_p, _c_float_p, _c_float_p,
+                                             _c_float_p]),
+            "chpe_debug_deltanet_step": (I, [ctypes.c_uint32] * 3 + [_c_float_p] * 9 + [F, _c_float_p, _c_float_p]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(lib, name)
@@ -300,6 +303,38 @@ def gpu_attention(q, k_rows, v_rows, pos, heads, kv_heads, head_dim, kv_f16):
     if rc:
         raise EngineError(f"chpe_debug_attention failed: {rc}")
     return out
+
+
+def _f32c(a):
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def gpu_deltanet_conv(x, w, state):
+    """k_dn_conv on caller data; returns (out, new_state)."""
+    x, w, st = _f32c(x), _f32c(w), _f32c(state).copy()
+    ch, taps = w.shape
+    out = np.empty(ch, dtype=np.float32)
+    rc = load_engine_lib().chpe_debug_deltanet_conv(ch, taps, _fp(x), _fp(w), _fp(st), _fp(out))
+    if rc:
+        raise EngineError(f"chpe_debug_deltanet_conv failed: {rc}")
+    return out, st
+
+
+def gpu_deltanet_step(q, k, v, a, b, A_log, dt_bias, state, z=None, norm_w=None, eps=1e-6):
+    """k_dn_step on caller data; returns (out, new_state)."""
+    q, k, v, a, b, A_log, dt_bias = (_f32c(t) for t in (q, k, v, a, b, A_log, dt_bias))
+    st = _f32c(state).copy()
+    nk, hd = q.shape
+    nv = v.shape[0]
+    out = np.empty((nv, hd), dtype=np.float32)
+    zz = _f32c(z) if z is not None else None
+    ww = _f32c(norm_w) if norm_w is not None else None
+    rc = load_engine_lib().chpe_debug_deltanet_step(nv, nk, hd, _fp(q), _fp(k), _fp(v), _fp(a), _fp(b), _fp(A_log),
+                                                    _fp(dt_bias), _fp(zz) if zz is not None else None,
+                                                    _fp(ww) if ww is not None else None, eps, _fp(st), _fp(out))
+    if rc:
+        raise EngineError(f"chpe_debug_deltanet_step failed: {rc}")
+    return out, st
 
 
 def build(jobs=8):

@@ -347,4 +347,75 @@ int chpe_debug_attention(uint32_t head_dim, uint32_t heads, uint32_t kv_heads, i
   return rc;
 }
 
+// One decode step of a gated-DeltaNet layer's recurrent core on caller data (the layers have no
+// reference code; see deltanet.hip for the arithmetic's source).
+int chpe_debug_deltanet_conv(uint32_t channels, uint32_t taps, const float* x, const float* w, float* state,
+                             float* out) {
+  if (!x || !w || !state || !out || channels == 0 || taps < 2 || taps > kDnMaxTaps) return -1;
+  const size_t nx = channels, nw = size_t(channels) * taps, ns = size_t(channels) * (taps - 1);
+  float *dx = nullptr, *dw = nullptr, *ds = nullptr, *dout = nullptr;
+  int rc = -3;
+  if (hipMalloc(&dx, nx * 4) == hipSuccess && hipMalloc(&dw, nw * 4) == hipSuccess &&
+      hipMalloc(&ds, ns * 4) == hipSuccess && hipMalloc(&dout, nx * 4) == hipSuccess &&
+      hipMemcpy(dx, x, nx * 4, hipMemcpyHostToDevice) == hipSuccess &&
+      hipMemcpy(dw, w, nw * 4, hipMemcpyHostToDevice) == hipSuccess &&
+      hipMemcpy(ds, state, ns * 4, hipMemcpyHostToDevice) == hipSuccess) {
+    DnConvArgs a{dx, dw, ds, dout, channels, taps};
+    launch_dn_conv(a, nullptr);
+    if (hipDeviceSynchronize() == hipSuccess && hipMemcpy(out, dout, nx * 4, hipMemcpyDeviceToHost) == hipSuccess &&
+        hipMemcpy(state, ds, ns * 4, hipMemcpyDeviceToHost) == hipSuccess)
+      rc = 0;
+  }
+  for (float* p : {dx, dw, ds, dout})
+    if (p) (void)hipFree(p);
+  return rc;
+}
+
+int chpe_debug_deltanet_step(uint32_t n_v_heads, uint32_t n_k_heads, uint32_t head_dim, const float* q, const float* k,
+                             const float* v, const float* a_in, const float* b_in, const float* A_log,
+                             const float* dt_bias, const float* z, const float* norm_w, float eps, float* state,
+                             float* out) {
+  if (!q || !k || !v || !a_in || !b_in || !A_log || !dt_bias || !state || !out || (norm_w && !z) ||
+      !deltanet_supported(n_v_heads, n_k_heads, head_dim, 4))
+    return -1;
+  const size_t hd = head_dim, nq = n_k_heads * hd, nv = n_v_heads * hd, ns = n_v_heads * hd * hd;
+  const float* src[9] = {q, k, v, a_in, b_in, A_log, dt_bias, z, norm_w};
+  const size_t cnt[9] = {nq, nq, nv, n_v_heads, n_v_heads, n_v_heads, n_v_heads, nv, hd};
+  float* dev[9] = {};
+  float *ds = nullptr, *dout = nullptr;
+  bool ok = hipMalloc(&ds, ns * 4) == hipSuccess && hipMalloc(&dout, nv * 4) == hipSuccess &&
+            hipMemcpy(ds, state, ns * 4, hipMemcpyHostToDevice) == hipSuccess;
+  for (int i = 0; ok && i < 9; ++i)
+    if (src[i])
+      ok = hipMalloc(&dev[i], cnt[i] * 4) == hipSuccess &&
+           hipMemcpy(dev[i], src[i], cnt[i] * 4, hipMemcpyHostToDevice) == hipSuccess;
+  int rc = -3;
+  if (ok) {
+    DnStepArgs a{};
+    a.q = dev[0];
+    a.k = dev[1];
+    a.v = dev[2];
+    a.a = dev[3];
+    a.b = dev[4];
+    a.A_log = dev[5];
+    a.dt_bias = dev[6];
+    a.z = dev[7];
+    a.norm_w = dev[8];
+    a.state = ds;
+    a.out = dout;
+    a.n_v_heads = n_v_heads;
+    a.n_k_heads = n_k_heads;
+    a.eps = eps;
+    launch_dn_step(a, head_dim, nullptr);
+    if (hipDeviceSynchronize() == hipSuccess && hipMemcpy(out, dout, nv * 4, hipMemcpyDeviceToHost) == hipSuccess &&
+        hipMemcpy(state, ds, ns * 4, hipMemcpyDeviceToHost) == hipSuccess)
+      rc = 0;
+  }
+  for (float* p : dev)
+    if (p) (void)hipFree(p);
+  if (ds) (void)hipFree(ds);
+  if (dout) (void)hipFree(dout);
+  return rc;
+}
+
 }  // extern "C"

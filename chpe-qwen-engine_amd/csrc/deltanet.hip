@@ -1,0 +1,162 @@
+// deltanet.hip -- one decode step of a gated-DeltaNet (linear-attention) layer of Qwen3.5.
+//
+// The reference engine has no code for these layers (its README only claims them); the
+// arithmetic follows the published gated delta rule (Yang, Kautz, Hatamizadeh, ICLR 2025)
+// in the form of the library that defines the Qwen3.5 layer (transformers 5.15.0,
+// models/qwen3_5/modeling_qwen3_5.py: causal_conv1d_update :200-217, l2norm :242-245,
+// torch_recurrent_gated_delta_rule :331-380, beta/g :497-499, head repetition :500-502,
+// RMSNormGated :168-184).
+//
+// k_dn_conv: the depthwise causal conv over [state, x] + SiLU, one thread per channel, the
+// state shifted in place.  k_dn_step: one workgroup per value head; the head's 128x128 f32
+// state (64 KiB) is read once and written once: thread (row block rb, column j) holds rows
+// rb*RPB.. of column j in registers, the two column sums (S^T k before the update, S^T q after)
+// meet in LDS in a fixed order, and the gated RMSNorm of the head's output runs in the same
+// launch.  Memory-bound: 2 x 64 KiB of state per head and step.
+#include "device_common.hpp"
+#include "kernels.hpp"
+
+namespace chpe {
+namespace {
+using namespace dev;
+
+__device__ __forceinline__ float silu_f(float x) { return x / (1.0f + expf(-x)); }
+__device__ __forceinline__ float softplus_f(float x) { return x > 20.0f ? x : log1pf(expf(x)); }
+
+__global__ void __launch_bounds__(256) k_dn_conv(DnConvArgs a) {
+  const uint32_t c = blockIdx.x * 256 + threadIdx.x;
+  if (c >= a.channels) return;
+  const uint32_t T = a.taps;
+  const float* w = a.w + size_t(c) * T;
+  float* st = a.state + size_t(c) * (T - 1);
+  float wv[kDnMaxTaps], sv[kDnMaxTaps];
+#pragma unroll
+  for (uint32_t k = 0; k < kDnMaxTaps; ++k) {
+    wv[k] = k + 1 < T ? w[k] : 0.0f;
+    sv[k] = k + 1 < T ? st[k] : 0.0f;
+  }
+  const float x = a.x[c], wl = w[T - 1];
+  float acc = 0.0f;  // oldest tap first, the new input last
+#pragma unroll
+  for (uint32_t k = 0; k < kDnMaxTaps; ++k)
+    if (k + 1 < T) acc += wv[k] * sv[k];
+  acc += wl * x;
+  a.out[c] = silu_f(acc);
+#pragma unroll
+  for (uint32_t k = 0; k + 1 < kDnMaxTaps; ++k)
+    if (k + 2 < T) st[k] = sv[k + 1];
+  st[T - 2] = x;
+}
+
+template <int D>
+__global__ void __launch_bounds__(512) k_dn_step(DnStepArgs a) {
+  constexpr int NT = 512, RB = NT / D, RPB = D / RB;  // row blocks, rows per block
+  static_assert(NT % D == 0 && D % RB == 0 && D % 64 == 0, "");
+  const uint32_t h = blockIdx.x, kh = h / (a.n_v_heads / a.n_k_heads);
+  const int t = threadIdx.x, j = t % D, rb = t / D, lane = t & 63, wave = t >> 6;
+  __shared__ float s_qn[D], s_kn[D];
+  __shared__ float s_part[RB][D];
+  __shared__ float s_red[NT / 64];
+
+  // 1. loads: the thread's state rows, then the head's inputs (all before any use)
+  float* S = a.state + size_t(h) * D * D;
+  float sr[RPB];
+#pragma unroll
+  for (int r = 0; r < RPB; ++r) sr[r] = S[size_t(rb * RPB + r) * D + j];
+  constexpr int PL = D / 64;  // q/k values per lane (every wave normalises both vectors)
+  float qv[PL], kv[PL];
+#pragma unroll
+  for (int m = 0; m < PL; ++m) {
+    qv[m] = a.q[size_t(kh) * D + lane + 64 * m];
+    kv[m] = a.k[size_t(kh) * D + lane + 64 * m];
+  }
+  const float vj = a.v[size_t(h) * D + j];
+  const float beta = 1.0f / (1.0f + expf(-a.b[h]));
+  const float decay = expf(-expf(a.A_log[h]) * softplus_f(a.a[h] + a.dt_bias[h]));
+
+  // 2. l2-normalised q (scaled by 1/sqrt(D)) and k, into LDS
+  float q2 = 0.0f, k2 = 0.0f;
+#pragma unroll
+  for (int m = 0; m < PL; ++m) {
+    q2 += qv[m] * qv[m];
+    k2 += kv[m] * kv[m];
+  }
+  q2 = wave_sum(q2);
+  k2 = wave_sum(k2);
+  const float qi = 1.0f / sqrtf(q2 + 1e-6f), ki = 1.0f / sqrtf(k2 + 1e-6f), scale = 1.0f / sqrtf(float(D));
+  if (wave == 0) {
+#pragma unroll
+    for (int m = 0; m < PL; ++m) {
+      s_qn[lane + 64 * m] = qv[m] * qi * scale;
+      s_kn[lane + 64 * m] = kv[m] * ki;
+    }
+  }
+  __syncthreads();
+
+  // 3. decayed state; kv_mem[j] = sum_i S[i][j] k[i]
+  float p = 0.0f;
+#pragma unroll
+  for (int r = 0; r < RPB; ++r) {
+    sr[r] *= decay;
+    p += sr[r] * s_kn[rb * RPB + r];
+  }
+  s_part[rb][j] = p;
+  __syncthreads();
+  float kvm = 0.0f;
+#pragma unroll
+  for (int b = 0; b < RB; ++b) kvm += s_part[b][j];
+  const float delta = (vj - kvm) * beta;
+  __syncthreads();  // s_part is reused below
+
+  // 4. S += k delta^T, written back; o[j] = sum_i S[i][j] q[i]
+  float o = 0.0f;
+#pragma unroll
+  for (int r = 0; r < RPB; ++r) {
+    sr[r] += s_kn[rb * RPB + r] * delta;
+    S[size_t(rb * RPB + r) * D + j] = sr[r];
+    o += sr[r] * s_qn[rb * RPB + r];
+  }
+  s_part[rb][j] = o;
+  __syncthreads();
+  // threads 0..D-1 (whole waves: rb is uniform per wave) finish the head
+  float oj = 0.0f;
+  if (rb == 0) {
+#pragma unroll
+    for (int b = 0; b < RB; ++b) oj += s_part[b][j];
+  }
+
+  // 5. gated RMSNorm of the head (when given): w * (o * rsqrt(mean o^2 + eps)) * silu(z)
+  if (a.norm_w) {
+    if (rb == 0) {
+      const float s2 = wave_sum(oj * oj);
+      if (lane == 0) s_red[wave] = s2;
+    }
+    __syncthreads();
+    if (rb == 0) {
+      float tot = 0.0f;
+#pragma unroll
+      for (int w = 0; w < D / 64; ++w) tot += s_red[w];
+      const float rr = 1.0f / sqrtf(tot / float(D) + a.eps);
+      oj = a.norm_w[j] * (oj * rr) * silu_f(a.z[size_t(h) * D + j]);
+    }
+  }
+  if (rb == 0) a.out[size_t(h) * D + j] = oj;
+}
+
+}  // namespace
+
+bool deltanet_supported(uint32_t n_v_heads, uint32_t n_k_heads, uint32_t head_dim, uint32_t taps) {
+  return n_k_heads > 0 && n_v_heads % n_k_heads == 0 && (head_dim == 64 || head_dim == 128) && taps >= 2 &&
+         taps <= kDnMaxTaps;
+}
+
+void launch_dn_conv(const DnConvArgs& a, hipStream_t st) {
+  launch_kernel(&k_dn_conv, dim3((a.channels + 255) / 256), dim3(256), st, a);
+}
+
+void launch_dn_step(const DnStepArgs& a, uint32_t head_dim, hipStream_t st) {
+  if (head_dim == 128) launch_kernel(&k_dn_step<128>, dim3(a.n_v_heads), dim3(512), st, a);
+  else launch_kernel(&k_dn_step<64>, dim3(a.n_v_heads), dim3(512), st, a);
+}
+
+}  // namespace chpe

@@ -172,6 +172,31 @@ GemvLaunch gemv_geometry(WeightKind kind, GemvMode mode, uint32_t C, const uint3
 // launchers; all enqueue on `stream` and never synchronise
 void launch_embed(const EmbedArgs& a, hipStream_t stream);
 void launch_gemv(WeightKind kind, const GemvArgs& a, const GemvLaunch& g, hipStream_t stream);
+// Gated-DeltaNet decode step (Qwen3.5 linear-attention layers; deltanet.hip).
+constexpr uint32_t kDnMaxTaps = 8;
+struct DnConvArgs {         // depthwise causal conv update + SiLU
+  const float* x;           // [channels]
+  const float* w;           // [channels][taps]
+  float* state;             // [channels][taps-1], oldest first; shifted in place
+  float* out;               // [channels]
+  uint32_t channels, taps;
+};
+struct DnStepArgs {         // gated delta rule over the value heads (+ gated RMSNorm)
+  const float *q, *k;       // [n_k_heads][head_dim], before the l2 norm
+  const float* v;           // [n_v_heads][head_dim]
+  const float *a, *b;       // [n_v_heads]: the a / b projections
+  const float *A_log, *dt_bias;  // [n_v_heads]
+  const float* z;           // [n_v_heads][head_dim] gate of the norm (used when norm_w)
+  const float* norm_w;      // [head_dim] or null: then out = S^T q
+  float* state;             // [n_v_heads][head_dim][head_dim] f32, updated in place
+  float* out;               // [n_v_heads][head_dim]
+  uint32_t n_v_heads, n_k_heads;
+  float eps;
+};
+bool deltanet_supported(uint32_t n_v_heads, uint32_t n_k_heads, uint32_t head_dim, uint32_t taps);
+void launch_dn_conv(const DnConvArgs& a, hipStream_t stream);
+void launch_dn_step(const DnStepArgs& a, uint32_t head_dim, hipStream_t stream);
+
 void launch_attention(const AttnArgs& a, hipStream_t stream);  // partial + combine
 void launch_attention_partial(const AttnArgs& a, hipStream_t stream);
 void launch_attention_combine(const AttnArgs& a, hipStream_t stream);

@@ -114,6 +114,23 @@ int chpe_debug_embed_row_cell(const uint8_t *bytes, size_t len, uint32_t row, ui
 int chpe_debug_attention(uint32_t head_dim, uint32_t heads, uint32_t kv_heads, int kv_f16, uint32_t pos,
                          const float *q, const float *k_rows, const float *v_rows, float *out);
 
+/* Gated-DeltaNet (Qwen3.5 linear-attention layers) decode-step kernels on caller data.  The
+ * reference has no code for these layers (README claims only); the arithmetic is the gated
+ * delta rule as defined by transformers 5.15.0 models/qwen3_5/modeling_qwen3_5.py.
+ * conv: causal depthwise conv over [state, x] + SiLU (:200-217); w [channels][taps], state
+ * [channels][taps-1] (oldest first), updated in place; out [channels].
+ * step: q, k [n_k_heads][head_dim] before the l2 norm, v [n_v_heads][head_dim], a, b, A_log,
+ * dt_bias [n_v_heads] (:331-380, :497-502); state [n_v_heads][head_dim][head_dim] f32, updated in
+ * place; out [n_v_heads][head_dim] = S^T q, or with norm_w (and z [n_v_heads][head_dim]) the
+ * gated RMSNorm of it (:168-184).  head_dim 64 or 128.  0 on success, -1 bad arguments, -3
+ * device error. */
+int chpe_debug_deltanet_conv(uint32_t channels, uint32_t taps, const float *x, const float *w, float *state,
+                             float *out);
+int chpe_debug_deltanet_step(uint32_t n_v_heads, uint32_t n_k_heads, uint32_t head_dim, const float *q,
+                             const float *k, const float *v, const float *a, const float *b, const float *A_log,
+                             const float *dt_bias, const float *z, const float *norm_w, float eps, float *state,
+                             float *out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -78,6 +78,20 @@ int oref_unpack_embed_row_cell(const uint8_t *cell, size_t row_in_tile, float *o
 void oref_attention(const float *q, const float *k_cache, const float *v_cache, size_t pos,
                     size_t heads, size_t kv_heads, size_t head_dim, float *scores, float *out);
 
+/* ---- gated-DeltaNet decode step (no reference code; deltanet_oracle.c) ----
+ * conv: x [channels], w [channels][taps], state [channels][taps-1] (oldest first, updated),
+ * out [channels] = silu(causal depthwise conv).  step: q, k [n_k_heads][dk] (before the l2
+ * norm), v [n_v_heads][dv], a, b, A_log, dt_bias [n_v_heads], state [n_v_heads][dk][dv]
+ * (updated), out [n_v_heads][dv].  gated rmsnorm: out = w * (x * rsqrt(mean x^2 + eps)) * silu(z)
+ * per head of dv values. */
+void oref_conv1d_update(size_t channels, size_t taps, const float *x, const float *w, float *state,
+                        float *out);
+void oref_gated_delta_step(size_t n_v_heads, size_t n_k_heads, size_t dk, size_t dv, const float *q,
+                           const float *k, const float *v, const float *a, const float *b,
+                           const float *A_log, const float *dt_bias, float *state, float *out);
+void oref_gated_rmsnorm(size_t n, size_t dv, const float *x, const float *z, const float *w, float eps,
+                        float *out);
+
 /* ---- engine (src/chpe_engine.zig:854-1803) ---- */
 typedef struct {
     uint32_t argmax_token;

@@ -80,6 +80,9 @@ def lib():
         L.oref_unpack_embed_row_cell.restype = ctypes.c_int
         L.oref_unpack_embed_row_cell.argtypes = [_u8p, S, _fp, S]
         L.oref_attention.argtypes = [_fp, _fp, _fp, S, S, S, S, _fp, _fp]
+        L.oref_conv1d_update.argtypes = [S, S, _fp, _fp, _fp, _fp]
+        L.oref_gated_delta_step.argtypes = [S, S, S, S, _fp, _fp, _fp, _fp, _fp, _fp, _fp, _fp, _fp]
+        L.oref_gated_rmsnorm.argtypes = [S, S, _fp, _fp, _fp, ctypes.c_float, _fp]
         L.oref_layer_info_for.restype = ctypes.c_int
         L.oref_layer_info_for.argtypes = [ctypes.c_int, S, ctypes.POINTER(LayerInfo)]
         L.oref_final_norm_for.restype = S
@@ -241,6 +244,41 @@ def attention(q, k_cache, v_cache, pos, heads, kv_heads, head_dim):
     out = np.empty(heads * head_dim, dtype=np.float32)
     lib().oref_attention(q.ctypes.data_as(_fp), kc.ctypes.data_as(_fp), vc.ctypes.data_as(_fp), pos,
                          heads, kv_heads, head_dim, scores.ctypes.data_as(_fp), out.ctypes.data_as(_fp))
+    return out
+
+
+def _f32(a):
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def conv1d_update(x, w, state):
+    """One causal depthwise conv step + SiLU; returns (out, new_state)."""
+    x, w, st = _f32(x), _f32(w), _f32(state).copy()
+    ch, taps = w.shape
+    out = np.empty(ch, dtype=np.float32)
+    lib().oref_conv1d_update(ch, taps, x.ctypes.data_as(_fp), w.ctypes.data_as(_fp), st.ctypes.data_as(_fp),
+                             out.ctypes.data_as(_fp))
+    return out, st
+
+
+def gated_delta_step(q, k, v, a, b, A_log, dt_bias, state):
+    """One gated-delta-rule step over all value heads; returns (out, new_state)."""
+    q, k, v, a, b, A_log, dt_bias = (_f32(t) for t in (q, k, v, a, b, A_log, dt_bias))
+    st = _f32(state).copy()
+    nk, dk = q.shape
+    nv, dv = v.shape
+    out = np.empty((nv, dv), dtype=np.float32)
+    lib().oref_gated_delta_step(nv, nk, dk, dv, *(t.ctypes.data_as(_fp) for t in (q, k, v, a, b, A_log, dt_bias)),
+                                st.ctypes.data_as(_fp), out.ctypes.data_as(_fp))
+    return out, st
+
+
+def gated_rmsnorm(x, z, w, eps):
+    x, z, w = _f32(x), _f32(z), _f32(w)
+    n, dv = x.shape
+    out = np.empty_like(x)
+    lib().oref_gated_rmsnorm(n, dv, x.ctypes.data_as(_fp), z.ctypes.data_as(_fp), w.ctypes.data_as(_fp), eps,
+                             out.ctypes.data_as(_fp))
     return out
 
 
