@@ -274,6 +274,73 @@ int Engine::launch_one() {
   return hipGetLastError() == hipSuccess ? 0 : -3;
 }
 
+bool plan_flat_tiles(const uint8_t* cells, size_t len, size_t stride, size_t n_tiles, size_t r_total,
+                     size_t c_total, WeightKind* kind, std::vector<float2>* corr, uint32_t* corr_kmax,
+                     std::string* err) {
+  const uint8_t* b = cells;
+  auto cell = [&](size_t t) { return t * stride; };
+  corr->clear();
+  *corr_kmax = 0;
+  if (n_tiles == 0 || n_tiles * kFlatWeights < r_total * c_total) { *err = "flat tensor shorter than its shape"; return false; }
+  if (c_total % 128) { *err = "flat tensor width is not a multiple of 128"; return false; }
+  const uint8_t bits = rd<uint8_t>(b, len, cell(0) + kPayloadOff + kMetaQuantBits);
+  for (size_t t = 0; t < n_tiles; ++t) {
+    const size_t pl = cell(t) + kPayloadOff;
+    if (rd<uint8_t>(b, len, pl + kMetaQuantBits) != bits ||
+        !(rd<uint64_t>(b, len, pl + kMetaCustomFlags) & kFlagGroup128)) {
+      *err = "flat tiles are not uniformly group-128 " + std::to_string(bits) + "-bit";
+      return false;
+    }
+  }
+  if (bits == 4) *kind = WeightKind::FlatW4;
+  else if (bits == 2) *kind = WeightKind::FlatW2;
+  else { *err = "flat tiles of " + std::to_string(bits) + " bits"; return false; }
+  // outliers replace weights (chpe_engine.zig:632-646): per-row (col, w_out - w_code)
+  std::vector<std::vector<std::pair<uint32_t, float>>> by_row;
+  const size_t total = r_total * c_total;
+  for (size_t t = 0; t < n_tiles; ++t) {
+    const size_t pl = cell(t) + kPayloadOff, codes = cell(t) + kBytecodeHeader;
+    const uint16_t n = rd<uint16_t>(b, len, pl + kFlatOutlierN);
+    if (n == 0 || n > 64) continue;
+    std::map<uint32_t, float> last;  // offset -> replacement (the last entry wins)
+    for (size_t m = 0; m < n; ++m) {
+      const uint16_t off = rd<uint16_t>(b, len, pl + kFlatOutlierOff + 2 * m);
+      last[off] = f16_to_f32(rd<uint16_t>(b, len, pl + kFlatOutlierW + 2 * m));
+    }
+    for (const auto& [off, w] : last) {
+      const size_t f = t * kFlatWeights + off;
+      if (f >= total) continue;
+      const float s = f16_to_f32(rd<uint16_t>(b, len, pl + kGroupScales + 2 * (off / 128)));
+      float q;
+      if (bits == 4) {
+        q = float((rd<uint8_t>(b, len, codes + off / 2) >> (4 * (off & 1))) & 15) - 8.0f;
+      } else {
+        static const float lut[4] = {0.0f, 1.0f, -2.0f, -1.0f};
+        q = lut[(rd<uint8_t>(b, len, codes + off / 4) >> (2 * (off & 3))) & 3];
+      }
+      if (by_row.empty()) by_row.resize(r_total);
+      by_row[f / c_total].push_back({uint32_t(f % c_total), w - q * s});
+    }
+  }
+  if (by_row.empty()) return true;
+  size_t kmax = 0;  // fixed stride per row, zero-padded: [r_total][kmax]
+  for (const auto& row : by_row) kmax = std::max(kmax, row.size());
+  if (kmax > kMaxCorrPerRow) {
+    *err = "a row has more than " + std::to_string(kMaxCorrPerRow) + " flat-tile outliers";
+    return false;
+  }
+  kmax = std::max<size_t>(kmax, 1);
+  corr->assign(r_total * kmax, make_float2(0.0f, 0.0f));
+  for (size_t r = 0; r < r_total; ++r)
+    for (size_t k = 0; k < by_row[r].size(); ++k) {
+      float cf;
+      std::memcpy(&cf, &by_row[r][k].first, 4);
+      (*corr)[r * kmax + k] = make_float2(cf, by_row[r][k].second);
+    }
+  *corr_kmax = uint32_t(kmax);
+  return true;
+}
+
 bool Engine::plan_projection(size_t tile_start, size_t num_tiles, size_t r_total, size_t c_total,
                              size_t x_len, size_t y_len, bool accumulate, int64_t bias_tile,
                              ProjPlan* p, std::string* err) {
@@ -295,61 +362,11 @@ bool Engine::plan_projection(size_t tile_start, size_t num_tiles, size_t r_total
     if (c_total > 2048) {  // flat tiles: gemvCellFlat
       const size_t need = (r_total * c_total + kFlatWeights - 1) / kFlatWeights;
       if (avail < need) { *err = "flat tensor shorter than its shape"; return false; }
-      if (c_total % 128) { *err = "flat tensor width is not a multiple of 128"; return false; }
-      const uint8_t bits = b[cell(0) + kPayloadOff + kMetaQuantBits];
-      for (size_t t = 0; t < need; ++t) {
-        const size_t pl = cell(t) + kPayloadOff;
-        if (b[pl + kMetaQuantBits] != bits || !(rd<uint64_t>(b, len, pl + kMetaCustomFlags) & kFlagGroup128)) {
-          *err = "flat tiles are not uniformly group-128 " + std::to_string(bits) + "-bit";
-          return false;
-        }
-      }
-      if (bits == 4) p->kind = WeightKind::FlatW4;
-      else if (bits == 2) p->kind = WeightKind::FlatW2;
-      else { *err = "flat tiles of " + std::to_string(bits) + " bits"; return false; }
-      // outliers replace weights (chpe_engine.zig:632-646): per-row (col, w_out - w_code)
-      std::vector<std::vector<std::pair<uint32_t, float>>> by_row;
-      const size_t total = r_total * c_total;
-      for (size_t t = 0; t < need; ++t) {
-        const size_t pl = cell(t) + kPayloadOff, codes = cell(t) + kBytecodeHeader;
-        const uint16_t n = rd<uint16_t>(b, len, pl + kFlatOutlierN);
-        if (n == 0 || n > 64) continue;
-        std::map<uint32_t, float> last;  // offset -> replacement (the last entry wins)
-        for (size_t m = 0; m < n; ++m) {
-          const uint16_t off = rd<uint16_t>(b, len, pl + kFlatOutlierOff + 2 * m);
-          last[off] = f16_to_f32(rd<uint16_t>(b, len, pl + kFlatOutlierW + 2 * m));
-        }
-        for (const auto& [off, w] : last) {
-          const size_t f = t * kFlatWeights + off;
-          if (f >= total) continue;
-          const float s = f16_to_f32(rd<uint16_t>(b, len, pl + kGroupScales + 2 * (off / 128)));
-          float q;
-          if (bits == 4) {
-            q = float((b[codes + off / 2] >> (4 * (off & 1))) & 15) - 8.0f;
-          } else {
-            static const float lut[4] = {0.0f, 1.0f, -2.0f, -1.0f};
-            q = lut[(b[codes + off / 4] >> (2 * (off & 3))) & 3];
-          }
-          if (by_row.empty()) by_row.resize(r_total);
-          by_row[f / c_total].push_back({uint32_t(f % c_total), w - q * s});
-        }
-      }
-      if (!by_row.empty()) {  // fixed stride per row, zero-padded: [r_total][kmax]
-        size_t kmax = 0;
-        for (const auto& row : by_row) kmax = std::max(kmax, row.size());
-        if (kmax > kMaxCorrPerRow) {
-          *err = "a row has more than " + std::to_string(kMaxCorrPerRow) + " flat-tile outliers";
-          return false;
-        }
-        kmax = std::max<size_t>(kmax, 1);
-        std::vector<float2> ent(r_total * kmax, make_float2(0.0f, 0.0f));
-        for (size_t r = 0; r < r_total; ++r)
-          for (size_t k = 0; k < by_row[r].size(); ++k) {
-            float cf;
-            std::memcpy(&cf, &by_row[r][k].first, 4);
-            ent[r * kmax + k] = make_float2(cf, by_row[r][k].second);
-          }
-        p->corr_kmax = uint32_t(kmax);
+      std::vector<float2> ent;
+      if (!plan_flat_tiles(b + cell(0), len - cell(0), stride_, need, r_total, c_total, &p->kind, &ent,
+                           &p->corr_kmax, err))
+        return false;
+      if (!ent.empty()) {
         p->corr = static_cast<float2*>(dev_alloc(ent.size() * sizeof(float2)));
         if (!p->corr) { *err = "allocation"; return false; }
         (void)hipMemcpy(p->corr, ent.data(), ent.size() * sizeof(float2), hipMemcpyHostToDevice);

@@ -58,6 +58,16 @@ struct ProjPlan {
   CellReplace* repl = nullptr;         // device, replace-mode outliers of 16-row cells
 };
 
+// A flat-tile tensor (gemvCellFlat, src/chpe_engine.zig:584-729) of r_total x c_total weights in
+// n_tiles cells at cells + t * stride (host bytes, len readable): checks that the tiles are
+// uniformly group-128 4- or 2-bit (*kind), and builds the outlier corrections the GPU adds --
+// outliers replace weights (:632-646), the last entry for an offset wins -- as a zero-padded
+// [r_total][*corr_kmax] table of (column as float bits, w_out - dequantised code); *corr stays
+// empty when no tile has outliers.
+bool plan_flat_tiles(const uint8_t* cells, size_t len, size_t stride, size_t n_tiles, size_t r_total,
+                     size_t c_total, WeightKind* kind, std::vector<float2>* corr, uint32_t* corr_kmax,
+                     std::string* err);
+
 struct LayerPlan {
   ProjPlan q, k, v, o, gate, up, down;
   float* gamma_in = nullptr;    // device, unpackNorm rules applied

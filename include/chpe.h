@@ -102,6 +102,17 @@ int chpe_debug_gemv(void *ctx, size_t layer, int which, const float *x, float *y
 /* Materialised weights of one flat 32768-weight tile (gemvCellFlat's dequantisation),
  * computed by the GPU from the 17408-byte cell. */
 int chpe_debug_flat_tile_weights(const uint8_t *cell, float *out32768);
+/* One flat-tile GEMV (gemvCellFlat, src/chpe_engine.zig:584-729, as gemvLinear drives it for
+ * tensors wider than 2048 columns, :1396-1489) through the decode step's kernels, on a rows x
+ * cols tensor given as n_tiles consecutive 17408-byte cells (group-128 4- or 2-bit; outliers
+ * replace weights).  mode 0: y = W x; 1: y += W x; 2: y = silu(W rmsnorm(x)) * (U rmsnorm(x))
+ * with U in tiles_up; 3: y = W rmsnorm(x) (the LM head's logits) with *out_argmax (first index
+ * of the maximum) and *out_hidden_norm = |x| (both optional).  rmsnorm uses gamma and eps;
+ * gamma is given exactly in modes 2 and 3.  Returns 0, -1 on bad arguments or tiles
+ * (chpe_last_error), -3 on a device error. */
+int chpe_debug_gemv_flat(int mode, uint32_t rows, uint32_t cols, const uint8_t *tiles,
+                         const uint8_t *tiles_up, size_t n_tiles, const float *x, const float *gamma,
+                         float eps, float *y, uint32_t *out_argmax, float *out_hidden_norm);
 /* unpackEmbedRowCell on the GPU over `len` bytes starting at a cell (rows of wide tensors
  * read past the cell).  Returns 1 if written, 0 if the row is out of range, <0 on error. */
 int chpe_debug_embed_row_cell(const uint8_t *bytes, size_t len, uint32_t row, uint32_t D,

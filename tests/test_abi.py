@@ -78,3 +78,29 @@ def test_init_rejects_missing_and_malformed_archives(tmp_path):
     assert L.chpe_last_error() == b"Truncated"
     assert not L.chpe_init_ex(str(small).encode(), 7, 16, 0)
     assert L.chpe_last_error() == b"unknown architecture"
+
+
+def test_flat_gemv_hook_rejects_bad_tiles_before_the_device():
+    """chpe_debug_gemv_flat checks its arguments and plans the tiles on the host first."""
+    w = (np.random.default_rng(1).standard_normal(32768) * 0.02).astype(np.float32)
+    cells = np.stack([ca.pack_flat(w, bits=4), ca.pack_flat(w, bits=4)])
+    x, g = np.ones(4096, np.float32), np.ones(4096, np.float32)
+    bad = [
+        dict(mode="swiglu", rows=16, cols=4096, tiles=cells, x=x, gamma=g),       # no up tiles
+        dict(mode="store", rows=16, cols=4096, tiles=cells, x=x, gamma=g),        # gamma outside 2/3
+        dict(mode="logits", rows=16, cols=4096, tiles=cells, x=x),                # no gamma
+        dict(mode="store", rows=17, cols=4096, tiles=cells, x=x),                 # more rows than tiles
+        dict(mode="store", rows=16, cols=2048, tiles=cells, x=x),                 # not a flat width
+        dict(mode="store", rows=8, cols=4160, tiles=cells, x=x),                  # width % 128
+    ]
+    for kw in bad:
+        with pytest.raises(ca.EngineError):
+            ca.gpu_gemv_flat(**kw)
+    mixed = cells.copy()
+    mixed[1] = ca.pack_flat(w, bits=2)
+    with pytest.raises(ca.EngineError, match="uniformly"):
+        ca.gpu_gemv_flat("store", 16, 4096, mixed, x)
+    three = cells.copy()
+    three[0, 16448 + 20] = 3
+    with pytest.raises(ca.EngineError):
+        ca.gpu_gemv_flat("store", 16, 4096, three, x)
