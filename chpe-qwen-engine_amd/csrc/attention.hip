@@ -116,7 +116,7 @@ __global__ void __launch_bounds__(NW * 64) k_attn_chunk(AttnArgs a) {
 #pragma unroll
   for (int g = 0; g < GQ; ++g) {
 #pragma unroll
-    for (int o = 1; o < LPP; o <<= 1) s[g] += __shfl_xor(s[g], o);
+    for (int o = 1; o < LPP; o <<= 1) s[g] = pair_sum(s[g], o);
     s[g] = valid ? s[g] * a.scale : -INFINITY;
   }
 
@@ -124,9 +124,7 @@ __global__ void __launch_bounds__(NW * 64) k_attn_chunk(AttnArgs a) {
   float m_w[GQ], l_w[GQ];
 #pragma unroll
   for (int g = 0; g < GQ; ++g) {
-    float m = s[g];
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+    const float m = wave_max(s[g]);
     const float e = valid ? expf(s[g] - m) : 0.0f;
     float l = grp == 0 ? e : 0.0f;
     l = wave_sum(l);
@@ -224,9 +222,7 @@ __global__ void __launch_bounds__(NW * 64) k_attn_mfma(AttnArgs a) {
   constexpr int VD = HD / 16;  // V dims per lane = N-tiles of the output product
   constexpr int CH = NW * T * 16, NT = NW * 64;
   static_assert(CH == int(attn_chunk_of(HD)) && GQ <= 8 && NW * GQ <= 64 && (NW & (NW - 1)) == 0, "");
-  const uint32_t pos = a.state->pos, ctx = pos + 1;
   const uint32_t c = blockIdx.x, kvh = blockIdx.y;
-  if (c * CH >= ctx) return;  // the whole workgroup
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int G = lane >> 4, n = lane & 15, h = n & 7;  // h: the query head of column / row n
   const bool rem = n >= 8;
@@ -235,9 +231,9 @@ __global__ void __launch_bounds__(NW * 64) k_attn_mfma(AttnArgs a) {
   __shared__ float s_ml[NW][GQ][2];
   __shared__ float s_f[GQ][NW];
 
-  // 1. loads, all issued before any use: the lane's query dims (head h), K rows (position n of
-  // each tile, dims of group G) and V blocks (positions 4G..4G+3 of each tile, dims n*VD..);
-  // rows past the context read row 0 / block 0 and are masked at use
+  // 1. loads, all issued before any use and before the position is known: the lane's query
+  // dims (head h), K rows (position n of each tile, dims of group G) and V blocks (positions
+  // 4G..4G+3 of each tile, dims n*VD..); rows past the context are masked at use
   const uint32_t p0 = c * CH + uint32_t(wave) * T * 16;
   const bool qok = h < GQ;
   const float* qsrc = a.q + size_t(kvh * GQ + (qok ? h : 0)) * HD + G * KD;
@@ -250,14 +246,19 @@ __global__ void __launch_bounds__(NW * 64) k_attn_mfma(AttnArgs a) {
 #pragma unroll
   for (int t = 0; t < T; ++t) {
     const uint32_t pk = p0 + t * 16 + n;
-    const uint8_t* ks = kc + (size_t(pk < ctx ? pk : 0u) * HD + G * KD) * 2;
+    const uint8_t* ks = kc + (size_t(min(pk, a.max_seq - 1)) * HD + G * KD) * 2;
 #pragma unroll
     for (int i = 0; i < KD / 8; ++i) kf[t][i] = ld_u128(ks + 16 * i);
     const uint32_t pb = p0 + t * 16 + 4 * G;  // first position of the lane's V block
-    const uint8_t* vs = vc + (size_t(pb < ctx ? pb : 0u) * HD + n * VD * 4) * 2;
+    const uint8_t* vs = vc + (size_t(min(pb, a.max_seq - 4)) * HD + n * VD * 4) * 2;
 #pragma unroll
     for (int i = 0; i < VD / 2; ++i) vf[t][i] = ld_u128(vs + 16 * i);
   }
+  // keep every load above this point: the scheduler would otherwise sink the V loads next to
+  // the P.V products, after the softmax
+  __builtin_amdgcn_sched_barrier(0);
+  const uint32_t pos = a.state->pos, ctx = pos + 1;
+  if (c * CH >= ctx) return;  // the whole workgroup; its loads are dropped
 
   // 2. the query operand (zero for heads past the group)
   h4_t qb[KS];
@@ -281,14 +282,13 @@ __global__ void __launch_bounds__(NW * 64) k_attn_mfma(AttnArgs a) {
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const float s = acc[i] + __shfl_xor(acc[i], 8);
+      const float s = pair_sum(acc[i], 8);
       const bool ok = p0 + t * 16 + 4 * G + i < ctx;
       sc[t][i] = ok ? s * a.scale : -INFINITY;
       m = fmaxf(m, sc[t][i]);
     }
   }
-  m = fmaxf(m, __shfl_xor(m, 16));
-  m = fmaxf(m, __shfl_xor(m, 32));
+  m = pair_max(pair_max(m, 16), 32);
 
   // 4. exp-weights and their sum per head; O = P . V
   float l = 0.0f;
@@ -304,15 +304,20 @@ __global__ void __launch_bounds__(NW * 64) k_attn_mfma(AttnArgs a) {
       l += e[i];
     }
     const h4_t pa = f16_part(e[0], e[1], e[2], e[3], rem);
+    // V rows past the context hold stale or zero rows: zeroed, so that 0 * (non-finite) cannot
+    // reach the sums (e = 0 there already)
+    const uint32_t pb = p0 + t * 16 + 4 * G;
+    const uint32_t mlo = (pb < ctx ? 0xffffu : 0u) | (pb + 1 < ctx ? 0xffff0000u : 0u);
+    const uint32_t mhi = (pb + 2 < ctx ? 0xffffu : 0u) | (pb + 3 < ctx ? 0xffff0000u : 0u);
 #pragma unroll
     for (int j = 0; j < VD; ++j) {
-      const uint4 w = vf[t][j / 2];
+      const uint4 w0 = vf[t][j / 2];
+      const uint4 w = make_uint4(w0.x & mlo, w0.y & mhi, w0.z & mlo, w0.w & mhi);
       const h4_t vv = (j & 1) ? as_h4(w.z, w.w) : as_h4(w.x, w.y);
       o[j] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa, vv, o[j], 0, 0, 0);
     }
   }
-  l += __shfl_xor(l, 16);
-  l += __shfl_xor(l, 32);
+  l = pair_sum(pair_sum(l, 16), 32);
 
   // 5. the wave's statistics and sums to LDS (lane (G, n) holds rows 4G + i, dims n*VD + j)
   if (G == 0 && n < GQ) {
@@ -335,11 +340,11 @@ __global__ void __launch_bounds__(NW * 64) k_attn_mfma(AttnArgs a) {
     const float mw = s_ml[w][g][0], lw = s_ml[w][g][1];
     float M = mw;
 #pragma unroll
-    for (int o2 = 1; o2 < NW; o2 <<= 1) M = fmaxf(M, __shfl_xor(M, o2));
+    for (int o2 = 1; o2 < NW; o2 <<= 1) M = pair_max(M, o2);
     const float f = lw > 0.0f ? expf(mw - M) : 0.0f;
     float L = lw * f;
 #pragma unroll
-    for (int o2 = 1; o2 < NW; o2 <<= 1) L += __shfl_xor(L, o2);
+    for (int o2 = 1; o2 < NW; o2 <<= 1) L = pair_sum(L, o2);
     s_f[g][w] = f;
     if (w == 0) {
       const size_t hc = size_t(kvh * GQ + g) * nch + c;
@@ -385,8 +390,7 @@ __global__ void __launch_bounds__(64) k_attn_merge(AttnArgs a) {
   float M = -INFINITY;
 #pragma unroll
   for (uint32_t k = 0; k < KC; ++k) M = fmaxf(M, lane + 64 * k < n_act ? mv[k] : -INFINITY);
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o));
+  M = wave_max(M);
   float L = 0.0f;
 #pragma unroll
   for (uint32_t k = 0; k < KC; ++k) {

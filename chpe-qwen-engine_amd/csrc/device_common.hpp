@@ -61,9 +61,74 @@ __device__ __forceinline__ uint4 ld_u128(const uint8_t* p) {
   return make_uint4(v.x, v.y, v.z, v.w);
 }
 
+// ---- cross-lane exchanges on the vector ALU -------------------------------------------------
+// DPP (quad_perm, row_half_mirror, row_ror) and gfx950's v_permlane16_swap / v_permlane32_swap
+// move values between lanes in a few cycles; ds_bpermute (__shfl_xor) goes through the LDS
+// crossbar and costs an LDS round trip per step of a reduction.  Every lane of the wave must
+// be active.  pair_val(v, M) returns v of lane ^ M (M = 1, 2, 4, 8, 16, 32), so reductions
+// built on it add in the same order as the __shfl_xor butterflies they replace.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u(uint32_t v) {
+  return uint32_t(__builtin_amdgcn_update_dpp(0, int(v), CTRL, 0xF, 0xF, false));
+}
+// quad_perm [1,0,3,2], [2,3,0,1], [3,2,1,0]; row_half_mirror (lane i <-> 7 - i of its 8);
+// row_ror:8 (lane i <-> i ^ 8 of its 16)
+constexpr int kDppXor1 = 0xB1, kDppXor2 = 0x4E, kDppXor3 = 0x1B, kDppHalfMirror = 0x141, kDppRor8 = 0x128;
+
+__device__ __forceinline__ uint32_t pair_u(uint32_t v, int m) {
+  switch (m) {
+    case 1: return dpp_u<kDppXor1>(v);
+    case 2: return dpp_u<kDppXor2>(v);
+    case 4: return dpp_u<kDppHalfMirror>(dpp_u<kDppXor3>(v));  // i ^ 3, then ^ 7
+    case 8: return dpp_u<kDppRor8>(v);
+    case 16: {  // rows 0 <-> 1 and 2 <-> 3 of 16 lanes: [0] = even row's values, [1] = odd row's
+      const auto p = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+      return (__lane_id() & 16) ? p[0] : p[1];
+    }
+    default: {  // 32: the two halves of the wave
+      const auto p = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+      return (__lane_id() & 32) ? p[0] : p[1];
+    }
+  }
+}
+__device__ __forceinline__ float pair_val(float v, int m) { return __uint_as_float(pair_u(__float_as_uint(v), m)); }
+
+// v + (v of the partner across bit m); for m = 16 / 32 the swap yields both halves directly
+__device__ __forceinline__ float pair_sum(float v, int m) {
+  if (m == 16) {
+    const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(p[0]) + __uint_as_float(p[1]);
+  }
+  if (m == 32) {
+    const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(p[0]) + __uint_as_float(p[1]);
+  }
+  return v + pair_val(v, m);
+}
+__device__ __forceinline__ float pair_max(float v, int m) {
+  if (m == 16) {
+    const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(p[0]), __uint_as_float(p[1]));
+  }
+  if (m == 32) {
+    const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(p[0]), __uint_as_float(p[1]));
+  }
+  return fmaxf(v, pair_val(v, m));
+}
+
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  for (int o = 32; o > 0; o >>= 1) v = pair_sum(v, o);
+  return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = pair_max(v, o);
   return v;
 }
 
@@ -79,14 +144,15 @@ __device__ __forceinline__ float wave_reduce_rows(float (&v)[N], int lane) {
     const bool up = lane & mask;
 #pragma unroll
     for (int j = 0; j < n / 2; ++j) {
-      const float lo = v[j] + __shfl_xor(v[j], mask);
-      const float hi = v[n / 2 + j] + __shfl_xor(v[n / 2 + j], mask);
+      const float lo = pair_sum(v[j], mask);
+      const float hi = pair_sum(v[n / 2 + j], mask);
       v[j] = up ? hi : lo;
     }
     mask >>= 1;
   }
   float s = v[0];
-  for (; mask > 0; mask >>= 1) s += __shfl_xor(s, mask);
+#pragma unroll
+  for (; mask > 0; mask >>= 1) s = pair_sum(s, mask);
   return s;
 }
 

@@ -250,9 +250,9 @@ __device__ __forceinline__ float flat_correction(const FlatExtras& f, const floa
 #pragma unroll
   for (int j = 0; j < kCorrSlots; ++j)
     if (((f.use >> j) & 1u) && f.e[j].y != 0.0f) cs = fmaf(f.e[j].y, s_x[xs_at(__float_as_uint(f.e[j].x))], cs);
-  cs += __shfl_xor(cs, 1);
-  cs += __shfl_xor(cs, 2);
-  cs += __shfl_xor(cs, 4);
+  cs = pair_sum(cs, 1);
+  cs = pair_sum(cs, 2);
+  cs = pair_sum(cs, 4);
   return cs;
 }
 
@@ -545,9 +545,9 @@ __device__ __forceinline__ void argmax_partial(const GemvArgs& a, float bv, uint
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) {
-    const float ov = __shfl_xor(bv, o);
-    const uint32_t oi = __shfl_xor(bi, o);
-    nf |= __shfl_xor(nf, o);
+    const float ov = pair_val(bv, o);
+    const uint32_t oi = pair_u(bi, o);
+    nf |= pair_u(nf, o);
     if (better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
   }
   if (lane == 0) { s_bv[wave] = bv; s_bi[wave] = bi; s_nf[wave] = nf; }
@@ -592,9 +592,9 @@ __device__ __forceinline__ void rows_unit(const GemvArgs& a, const UnitLoads<F, 
   if constexpr (U::kFlat) tot += flat_correction(cur.fe, s_x);
   const int i = lane / S;
   // SwiGlu / QkvRope: the partner of row i < RU/2 sits 32 lanes above it
-  const float up = (kSwi || kRope) ? __shfl(tot, (lane + 32) & 63) : 0.0f;
+  const float up = (kSwi || kRope) ? pair_val(tot, 32) : 0.0f;
   const float pre = cur.pre_ok ? cur.pre : 0.0f;
-  const float up_pre = kRope ? __shfl(pre, (lane + 32) & 63) : 0.0f;
+  const float up_pre = kRope ? pair_val(pre, 32) : 0.0f;
   if constexpr (kRope) {
     const uint32_t r = row_of<RU, MODE>(cur.row_base, i, a.rope.head_dim / 2);
     if ((lane % S) == 0 && i < RU / 2 && cur.unit < a.n_units && r < P0.rows)
@@ -762,8 +762,8 @@ __global__ void __launch_bounds__(512, 2) k_gemv_split(GemvArgs a) {
       float v = 0.0f;
       for (uint32_t w = 0; w < NW; ++w) v += s_part[w][i];
       if constexpr (U::kFlat) v += flat_correction(cur.fe, s_x);
-      const float up = (kSwi || kRope) ? __shfl(v, (lane + 32) & 63) : 0.0f;
-      const float up_pre = kRope ? __shfl(pre, (lane + 32) & 63) : 0.0f;
+      const float up = (kSwi || kRope) ? pair_val(v, 32) : 0.0f;
+      const float up_pre = kRope ? pair_val(pre, 32) : 0.0f;
       if constexpr (kRope) {
         const uint32_t r = row_of<RU, MODE>(cur.row_base, i, half);
         if (unit < a.n_units && (lane % S) == 0 && i < RU / 2 && r < P0.rows)

@@ -105,9 +105,9 @@ __global__ void __launch_bounds__(256) k_finish(FinishArgs a) {
   }
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) {
-    const float ov = __shfl_xor(bv, o);
-    const uint32_t oi = __shfl_xor(bi, o);
-    nf |= __shfl_xor(nf, o);
+    const float ov = pair_val(bv, o);
+    const uint32_t oi = pair_u(bi, o);
+    nf |= pair_u(nf, o);
     if (better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
   }
   __shared__ float s_v[4];
