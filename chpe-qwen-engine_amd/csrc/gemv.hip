@@ -13,6 +13,7 @@
 // sum((q-8)*x)*scale up to float rounding.  Outliers: added for 16-row cells (gemvTileW4
 // :404-410), replacing for the tied LM head (unpackEmbedRowCell :1369-1378) and for flat tiles
 // (gemvCellFlat :632-646, applied as per-row corrections prepared at load time).
+#include <cstdio>
 #include <cstdlib>
 #include <type_traits>
 
@@ -140,6 +141,52 @@ __device__ __forceinline__ float4 keep_if(bool ok, float4 v) {
   return make_float4(keep_if(ok, v.x), keep_if(ok, v.y), keep_if(ok, v.z), keep_if(ok, v.w));
 }
 
+// The kernel-argument fields a GEMV reads before its first weight load, requested together:
+// the empty asm consumes them all in scalar registers, so their loads are issued as one batch
+// and waited for once (left to itself the scheduler interleaves them with the address
+// arithmetic, and each later batch costs another round trip before the weights can be
+// addressed).
+template <int MODE>
+__device__ __forceinline__ void args_batch(const GemvArgs& a) {
+  const GemvPart& p0 = a.part[0];
+  if constexpr (MODE == int(GemvMode::QkvRope)) {
+    const GemvPart& p1 = a.part[1];
+    const GemvPart& p2 = a.part[2];
+    asm volatile("" ::"s"(p0.base), "s"(p0.stride), "s"(p0.rows), "s"(p0.unit_begin), "s"(p0.bias), "s"(p0.rope_role),
+                 "s"(p1.base), "s"(p1.stride), "s"(p1.rows), "s"(p1.unit_begin), "s"(p1.bias), "s"(p1.rope_role),
+                 "s"(p2.base), "s"(p2.stride), "s"(p2.rows), "s"(p2.unit_begin), "s"(p2.bias), "s"(p2.rope_role),
+                 "s"(a.x), "s"(a.gamma), "s"(a.C), "s"(a.n_units), "s"(a.n_parts), "s"(a.rope.head_dim));
+  } else if constexpr (MODE == int(GemvMode::SwiGlu)) {
+    const GemvPart& p1 = a.part[1];
+    asm volatile("" ::"s"(p0.base), "s"(p0.stride), "s"(p0.rows), "s"(p0.y), "s"(p0.corr), "s"(p0.corr_kmax),
+                 "s"(p1.base), "s"(p1.stride), "s"(p1.rows), "s"(p1.corr), "s"(p1.corr_kmax), "s"(a.x), "s"(a.gamma),
+                 "s"(a.C), "s"(a.n_units), "s"(a.n_panels));
+  } else if constexpr (MODE == int(GemvMode::Logits)) {
+    asm volatile("" ::"s"(p0.base), "s"(p0.stride), "s"(p0.rows), "s"(p0.y), "s"(p0.corr), "s"(p0.corr_kmax),
+                 "s"(p0.repl), "s"(a.x), "s"(a.gamma), "s"(a.C), "s"(a.n_units), "s"(a.n_panels));
+  } else {
+    asm volatile("" ::"s"(p0.base), "s"(p0.stride), "s"(p0.rows), "s"(p0.unit_begin), "s"(p0.y), "s"(p0.bias),
+                 "s"(p0.corr), "s"(p0.corr_kmax), "s"(a.x), "s"(a.C), "s"(a.n_units), "s"(a.n_panels));
+  }
+}
+
+// The q/k/v launch's part of a unit as a value: every field selected from the three parts'
+// fields (loaded in the one batch above), not loaded again at an address that depends on the
+// unit.  Other modes use part 0 (and part 1 for SwiGlu) at fixed offsets.
+__device__ __forceinline__ GemvPart pick_part(const GemvArgs& a, int pu) {
+  GemvPart p = a.part[0];
+  const GemvPart& b = a.part[1];
+  const GemvPart& c = a.part[2];
+  p.base = pu == 0 ? p.base : (pu == 1 ? b.base : c.base);
+  p.stride = pu == 0 ? p.stride : (pu == 1 ? b.stride : c.stride);
+  p.rows = pu == 0 ? p.rows : (pu == 1 ? b.rows : c.rows);
+  p.unit_begin = pu == 0 ? p.unit_begin : (pu == 1 ? b.unit_begin : c.unit_begin);
+  p.y = pu == 0 ? p.y : (pu == 1 ? b.y : c.y);
+  p.bias = pu == 0 ? p.bias : (pu == 1 ? b.bias : c.bias);
+  p.rope_role = pu == 0 ? p.rope_role : (pu == 1 ? b.rope_role : c.rope_role);
+  return p;
+}
+
 // Position of input column c in the workgroup's LDS copy: 16 bytes of padding after every 32
 // columns, so that lanes reading consecutive 32-column chunks (128 bytes apart) start on
 // different banks and a 16-byte-per-lane read is conflict-free.
@@ -162,7 +209,7 @@ struct CellExtras {
 
 template <class F, int RU, int MODE>
 __device__ __forceinline__ void load_cell_extras(const GemvPart& P0, const GemvPart& P1, uint32_t row_base,
-                                                 uint32_t half, int lane, CellExtras<RU>* e) {
+                                                 uint32_t half, int lane, bool active, CellExtras<RU>* e) {
   // every lane loads (lanes >= RU and rows past the end read row 0 of the part); the values
   // are decoded where they are used, so the loads stay in flight together with the codes
   constexpr bool kSwi = MODE == int(GemvMode::SwiGlu);
@@ -173,7 +220,7 @@ __device__ __forceinline__ void load_cell_extras(const GemvPart& P0, const GemvP
   const bool second = kSwi && i >= RU / 2;
   const uint32_t rows = second ? uni(P1.rows) : uni(P0.rows);
   const uint32_t r = row_of<RU, MODE>(row_base, i < RU ? i : 0, half);
-  e->valid = i < RU && r < rows;
+  e->valid = active && i < RU && r < rows;
   const uint32_t rr = e->valid ? r : 0u;
   if constexpr (kReplace) {
     const CellReplace* R = P0.repl + (rr >> 4);
@@ -220,7 +267,8 @@ struct NoExtras {};
 
 template <int RU, int MODE>
 __device__ __forceinline__ void load_flat_extras(const GemvPart& P0, const GemvPart& P1, uint32_t row_base,
-                                                 uint32_t half, int lane, const float* x_any, FlatExtras* f) {
+                                                 uint32_t half, int lane, bool enable, const float* x_any,
+                                                 FlatExtras* f) {
   constexpr bool kSwi = MODE == int(GemvMode::SwiGlu);
   const int i = lane >> 3;
   const bool second = kSwi && i >= RU / 2;  // uniform fields selected per lane (see load_cell_extras)
@@ -228,7 +276,7 @@ __device__ __forceinline__ void load_flat_extras(const GemvPart& P0, const GemvP
   const uint32_t kmax = second ? uni(P1.corr_kmax) : uni(P0.corr_kmax);
   const uint32_t rows = second ? uni(P1.rows) : uni(P0.rows);
   const uint32_t r = row_of<RU, MODE>(row_base, i, half);
-  const bool ok = corr != nullptr && r < rows;
+  const bool ok = enable && corr != nullptr && r < rows;
   // every slot loads (absent ones: the first entry of a valid table, or of the input vector
   // when there is no table) and is masked afterwards
   const float2* src = corr ? corr : reinterpret_cast<const float2*>(x_any);
@@ -269,9 +317,10 @@ struct StageRegs {
 
 // branch-free: every slot loads (past the input: its first float4) and is masked when used, so
 // that the wait for these loads does not also wait for the weights issued after them
-template <bool kNorm, int SL>
+// NT: the workgroup size when fixed at compile time (0: blockDim.x, an argument load)
+template <bool kNorm, int SL, int NT = 0>
 __device__ __forceinline__ void stage_x_issue(const GemvArgs& a, StageRegs<SL>* r) {
-  const uint32_t C = a.C, tid = threadIdx.x, nt = blockDim.x;
+  const uint32_t C = a.C, tid = threadIdx.x, nt = NT ? uint32_t(NT) : blockDim.x;
 #pragma unroll
   for (int k = 0; k < SL; ++k) {
     const uint32_t i = (tid + uint32_t(k) * nt) * 4, ic = i < C ? i : 0u;
@@ -283,10 +332,10 @@ __device__ __forceinline__ void stage_x_issue(const GemvArgs& a, StageRegs<SL>* 
 // kNorm: RMSNorm with the gains `gamma` (and the sum of squares, also the LM head's hidden norm);
 // kWide: the input may exceed the register slots (then two passes over LDS).  Both are
 // compile-time so that no runtime branch sits between the loads and their use.
-template <bool kNorm, bool kWide, int SL>
+template <bool kNorm, bool kWide, int SL, int NT = 0>
 __device__ __forceinline__ void stage_x_finish(const GemvArgs& a, const StageRegs<SL>& r, float* s_x, float* s_red,
                                                float* ss, float* inv) {
-  const uint32_t C = a.C, tid = threadIdx.x, nt = blockDim.x;
+  const uint32_t C = a.C, tid = threadIdx.x, nt = NT ? uint32_t(NT) : blockDim.x;
   const int lane = tid & 63, wave = tid >> 6;
   if constexpr (kWide) {  // two passes over LDS
     float q2 = 0.0f;
@@ -449,7 +498,11 @@ __device__ __forceinline__ void issue_unit(const GemvArgs& a, uint32_t unit, uin
   const bool active = unit < a.n_units;
   const uint32_t half = a.rope.head_dim / 2;
   u->unit = unit;
-  u->pu = kSwi ? 0 : __builtin_amdgcn_readfirstlane(part_of(a, active ? unit : 0u));
+  // only the q/k/v launch has several parts with units of their own; elsewhere the part is 0 at
+  // compile time, so its fields are kernel-argument loads at fixed offsets, issued together
+  // (a part chosen at run time costs a second dependent round of argument loads before the
+  // first weight load can be addressed)
+  u->pu = kRope ? __builtin_amdgcn_readfirstlane(part_of(a, active ? unit : 0u)) : 0;
   const GemvPart& P0 = a.part[u->pu];
   const GemvPart& P1 = a.part[kSwi ? 1 : u->pu];
   if constexpr (kSwi) {
@@ -460,12 +513,11 @@ __device__ __forceinline__ void issue_unit(const GemvArgs& a, uint32_t unit, uin
   } else {
     u->row_base = (unit - P0.unit_begin) * RU;
   }
-  if constexpr (UnitLoads<F, MODE>::kCell) {
-    if (active) load_cell_extras<F, RU, MODE>(P0, P1, u->row_base, half, lane, &u->ce);
-  }
-  if constexpr (UnitLoads<F, MODE>::kFlat) {
+  // no branch before the loads: a branch would need its condition's argument loads first
+  if constexpr (UnitLoads<F, MODE>::kCell) load_cell_extras<F, RU, MODE>(P0, P1, u->row_base, half, lane, active, &u->ce);
+  if constexpr (UnitLoads<F, MODE>::kFlat) {  // (with_corr is wave-uniform and needs no argument load)
     u->fe.use = 0;
-    if (active && with_corr) load_flat_extras<RU, MODE>(P0, P1, u->row_base, half, lane, a.x, &u->fe);
+    if (with_corr) load_flat_extras<RU, MODE>(P0, P1, u->row_base, half, lane, active, a.x, &u->fe);
   }
   // Branch-free like the panel loads: each lane loads at a valid (clamped) address and the
   // flags say which values count; they are applied where the values are used, after the sums.
@@ -666,6 +718,7 @@ __global__ void __launch_bounds__(kWave * (kRowWaves + 1), 2) k_gemv_rows(GemvAr
   const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const uint32_t stride = gridDim.x * kRowWaves;
   const bool stager = wave == kRowWaves;
+  args_batch<MODE>(a);
 
   // The two roles are wave-uniform branches that each pass the same barriers (one after the
   // staging, one more in the LM head's argmax).  Keeping them apart means no value of a unit
@@ -716,6 +769,7 @@ __global__ void __launch_bounds__(512, 2) k_gemv_split(GemvArgs a) {
   const uint32_t ppw = (a.n_panels + NW - 1) / NW;
   const uint32_t p0 = wave * ppw, p1 = min(a.n_panels, p0 + ppw);
 
+  args_batch<MODE>(a);
   U cur;
   uint32_t unit = blockIdx.x;
   StageRegs<8> xr0;
@@ -781,9 +835,147 @@ __global__ void __launch_bounds__(512, 2) k_gemv_split(GemvArgs a) {
   }
 }
 
+// 16-row cells at 2048 columns (the q/k/v, o and gate/up projections), K-split: one workgroup
+// = one unit of RU = 8 rows, kCellWaves = 4 waves x 512 columns.  Lane (j, c) = (lane / 16,
+// lane % 16) of wave w holds unit rows j and j + 4 at columns 512 w + 32 c .. + 31 (one 16-byte
+// code load and one group scale per row), so a unit's dot products run on four SIMDs at once
+// instead of one.  Row sums meet over the 16 lanes of a row (DPP) and over the waves (LDS, in
+// wave order); wave 0 then holds row i on lanes 8 i .. 8 i + 7, adds the outlier terms and runs
+// the epilogue of the one-unit-per-wave kernel.  Every load is issued before the input staging
+// waits, with no branch in front of them.
+constexpr int kCellWaves = 4;
+template <int MODE>
+__global__ void __launch_bounds__(kWave * kCellWaves) k_gemv_cells(GemvArgs a) {
+  constexpr int RU = 8, S = kWave / RU;
+  constexpr bool kNorm = kNormOf<MODE>;
+  constexpr bool kSwi = MODE == int(GemvMode::SwiGlu);
+  constexpr bool kRope = MODE == int(GemvMode::QkvRope);
+  constexpr bool kPre = MODE == int(GemvMode::Store) || MODE == int(GemvMode::Accum) || kRope;
+  static_assert(MODE != int(GemvMode::Logits), "the LM head stays on k_gemv_rows");
+  __shared__ __align__(16) float s_x[xs_floats(2048)];
+  __shared__ float s_part[kCellWaves][RU];
+  __shared__ float s_red[kCellWaves];
+  const int lane = threadIdx.x & 63, j = lane >> 4, c = lane & 15, i8 = lane >> 3;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  args_batch<MODE>(a);
+  const uint32_t unit = blockIdx.x, half = a.rope.head_dim / 2;
+  const int pu = kRope ? int(__builtin_amdgcn_readfirstlane(part_of(a, unit))) : 0;
+  const GemvPart Pr = kRope ? pick_part(a, pu) : a.part[0];
+  const GemvPart& P0 = kRope ? Pr : a.part[0];
+  const GemvPart& P1 = kSwi ? a.part[1] : P0;
+  uint32_t row_base;
+  if constexpr (kSwi) {
+    row_base = unit * (RU / 2);
+  } else if constexpr (kRope) {  // RU/2 pairs per unit, half/(RU/2) units per head
+    const uint32_t ul = unit - P0.unit_begin, per_head = half / (RU / 2);
+    row_base = (ul / per_head) * (2 * half) + (ul % per_head) * (RU / 2);
+  } else {
+    row_base = (unit - P0.unit_begin) * RU;
+  }
+
+  // 1. the input first (its wait then leaves the later loads in flight), then the codes and
+  // scales of the lane's rows j and j + 4 (rows past the part read a row of it that exists and
+  // count zero): unit rows 0..3 and 4..7 each lie in one cell (their first row is a multiple of 4)
+  StageRegs<2> xr;
+  stage_x_issue<kNorm, 2, kWave * kCellWaves>(a, &xr);
+  const uint32_t rowA = row_of<RU, MODE>(row_base, 0, half), rowB = row_of<RU, MODE>(row_base, RU / 2, half);
+  const bool okA = rowA + j < P0.rows, okB = rowB + j < P1.rows;
+  const uint32_t cA = rowA < P0.rows ? rowA : 0u, cB = rowB < P1.rows ? rowB : 0u;
+  const uint8_t* cellA = P0.base + size_t(cA >> 4) * P0.stride;
+  const uint8_t* cellB = P1.base + size_t(cB >> 4) * P1.stride;
+  const uint32_t nA = (cA & 15u) + (okA ? uint32_t(j) : 0u), nB = (cB & 15u) + (okB ? uint32_t(j) : 0u);
+  const uint32_t boff = wave * 256 + uint32_t(c) * 16, grp = wave * 4 + uint32_t(c >> 2);
+  const uint4 qA = ld_u128(cellA + 64 + nA * 1024 + boff);
+  const uint4 qB = ld_u128(cellB + 64 + nB * 1024 + boff);
+  const uint32_t sA = ld_u16(cellA + 16448 + 48 + 2 * (nA * 16 + grp));
+  const uint32_t sB = ld_u16(cellB + 16448 + 48 + 2 * (nB * 16 + grp));
+  // outlier k = lane % 8 of unit row i8 (gemvTileW4 :404-410: the cell's 8 columns, the row's 8
+  // weights), used by wave 0
+  const bool osecond = kSwi && i8 >= RU / 2;
+  const uint32_t orow = row_of<RU, MODE>(row_base, i8, half);
+  const bool ovalid = orow < (osecond ? P1.rows : P0.rows);
+  const uint32_t orr = ovalid ? orow : 0u;
+  const uint8_t* ocell = (osecond ? P1.base : P0.base) + size_t(orr >> 4) * (osecond ? P1.stride : P0.stride);
+  const uint32_t ocol = ld_u16(ocell + 16448 + 816 + 2 * (lane & 7));
+  const uint32_t ow = ld_u16(ocell + 16448 + 560 + 2 * ((orr & 15u) * 8 + uint32_t(lane & 7)));
+  // epilogue operands of wave 0's rows (lane 8 i serves row i)
+  float pre = 0.0f, rc = 1.0f, rs = 0.0f;
+  bool pre_ok = false, rope_ok = false;
+  if constexpr (kPre) {
+    const float* src = MODE == int(GemvMode::Accum) ? P0.y : P0.bias;
+    pre_ok = (lane % S) == 0 && orow < P0.rows && src != nullptr;
+    pre = (src ? src : a.x)[pre_ok ? orow : 0u];
+  }
+  if constexpr (kRope) {
+    rope_ok = (lane % S) == 0 && lane < 32 && P0.rope_role != kRoleV;
+    const size_t at = rope_ok ? size_t(a.rope.state->pos) * half + (orow % (2 * half)) : 0u;
+    rc = a.rope.cos[at];
+    rs = a.rope.sin[at];
+  }
+
+  // 2. the (normalised) input into LDS
+  float ss = 0.0f, inv = 1.0f;
+  stage_x_finish<kNorm, false, 2, kWave * kCellWaves>(a, xr, s_x, s_red, &ss, &inv);
+
+  // 3. the lane's two 32-column dots, summed over the 16 lanes of each row, then over the waves
+  float xv[32];
+  const uint32_t col0 = wave * 512 + uint32_t(c) * 32;
+  float sx = 0.0f;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const float4 t = *reinterpret_cast<const float4*>(s_x + xs_at(col0 + 4 * k));
+    xv[4 * k] = t.x; xv[4 * k + 1] = t.y; xv[4 * k + 2] = t.z; xv[4 * k + 3] = t.w;
+  }
+#pragma unroll
+  for (int k = 0; k < 32; ++k) sx += xv[k];
+  float tA = (dot32_w4(qA, xv) - Cell16W4::kOff * sx) * Cell16W4::scale(sA);
+  float tB = (dot32_w4(qB, xv) - Cell16W4::kOff * sx) * Cell16W4::scale(sB);
+  tA = okA ? tA : 0.0f;
+  tB = okB ? tB : 0.0f;
+#pragma unroll
+  for (int m = 1; m < 16; m <<= 1) {
+    tA = pair_sum(tA, m);
+    tB = pair_sum(tB, m);
+  }
+  if (c == 0) {
+    s_part[wave][j] = tA;
+    s_part[wave][j + RU / 2] = tB;
+  }
+  __syncthreads();
+  if (wave != 0) return;
+
+  // 4. wave 0: row i8's total and outlier terms on its 8 lanes, then the epilogue
+  float v = 0.0f;
+#pragma unroll
+  for (int w = 0; w < kCellWaves; ++w) v += s_part[w][i8];
+  const float ox = s_x[xs_at(ocol < 2048u ? ocol : 0u)];
+  float o = (ovalid && ocol < 2048u) ? half_lo(ow) * ox : 0.0f;
+  o = pair_sum(o, 1);
+  o = pair_sum(o, 2);
+  o = pair_sum(o, 4);
+  v += o;
+  const float up = (kSwi || kRope) ? pair_val(v, 32) : 0.0f;
+  const float prev = pre_ok ? pre : 0.0f;
+  const float up_pre = kRope ? pair_val(prev, 32) : 0.0f;
+  float bv = -1e30f;
+  uint32_t bi = 0xffffffffu, nf = 0;
+  if constexpr (kRope) {
+    if ((lane % S) == 0 && i8 < RU / 2 && orow < P0.rows)
+      rope_store(a, P0, orow, v + prev, up + up_pre, rope_ok ? rc : 1.0f, rope_ok ? rs : 0.0f);
+  } else if ((lane % S) == 0 && (!kSwi || i8 < RU / 2)) {
+    epilogue<MODE>(P0, row_of<RU, MODE>(row_base, i8, 0), v, up, prev, &bv, &bi, &nf);
+  }
+}
+
 template <class F, int MODE>
 void launch_one(const GemvArgs& a, const GemvLaunch& g, hipStream_t st) {
   const size_t lds = size_t(xs_floats(a.C)) * 4;
+  if constexpr (std::is_same_v<F, Cell16W4> && MODE != int(GemvMode::Logits)) {
+    if (g.cells) {
+      launch_kernel(&k_gemv_cells<MODE>, dim3(g.blocks), dim3(g.threads), st, a);
+      return;
+    }
+  }
   if (a.waves_per_unit == 1)
     launch_kernel(&k_gemv_rows<F, MODE>, dim3(g.blocks), dim3(g.threads), st, a);
   else if (a.C > 4 * 8 * g.threads)  // more than 8 float4 per thread: staged in two passes
@@ -810,6 +1002,7 @@ const GemvTuning& gemv_tuning() {
     GemvTuning v;
     if (const char* e = std::getenv("CHPE_GEMV_ROWS_BLOCKS")) v.rows_blocks = uint32_t(std::strtoul(e, nullptr, 10));
     if (const char* e = std::getenv("CHPE_GEMV_LOGITS_BLOCKS")) v.logits_blocks = uint32_t(std::strtoul(e, nullptr, 10));
+    if (const char* e = std::getenv("CHPE_GEMV_CELLS")) v.cells = uint32_t(std::strtoul(e, nullptr, 10));
     if (v.logits_blocks == 0 || v.logits_blocks > kMaxLogitsBlocks) v.logits_blocks = kMaxLogitsBlocks;
     return v;
   }();
@@ -844,7 +1037,11 @@ GemvLaunch gemv_geometry(WeightKind kind, GemvMode mode, uint32_t C, const uint3
   *n_units = units;
   GemvLaunch g{};
   g.ru = ru;
-  if (nw == 1) {
+  if (kind == WeightKind::Cell16W4 && mode != GemvMode::Logits && C == 2048 && gemv_tuning().cells) {
+    g.cells = 1;  // one unit per workgroup, K-split over kCellWaves waves
+    g.threads = kWave * kCellWaves;
+    g.blocks = units;
+  } else if (nw == 1) {
     g.threads = kWave * (kRowWaves + 1);
     g.blocks = (units + kRowWaves - 1) / kRowWaves;
     const uint32_t cap = mode == GemvMode::Logits ? gemv_tuning().logits_blocks : gemv_tuning().rows_blocks;
@@ -858,6 +1055,11 @@ GemvLaunch gemv_geometry(WeightKind kind, GemvMode mode, uint32_t C, const uint3
 }
 
 void launch_gemv(WeightKind kind, const GemvArgs& a, const GemvLaunch& g, hipStream_t st) {
+  const GemvMode m = GemvMode(a.mode);
+  if (a.n_parts < 1 || a.n_parts > (m == GemvMode::QkvRope ? kMaxParts : m == GemvMode::SwiGlu ? 2 : 1)) {
+    std::fprintf(stderr, "chpe: GEMV launch with %d parts in mode %d is not built\n", a.n_parts, a.mode);
+    return;
+  }
   switch (kind) {
     case WeightKind::Cell16W4: launch_layout<Cell16W4>(a, g, st); break;
     case WeightKind::FlatW4: launch_layout<FlatW4>(a, g, st); break;

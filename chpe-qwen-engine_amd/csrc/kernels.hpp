@@ -94,7 +94,7 @@ struct ArgmaxPartial {
 
 struct GemvArgs {
   GemvPart part[kMaxParts];
-  int n_parts;
+  int n_parts;               // 1; SwiGlu: 2 (gate, up); QkvRope: up to 3 (q, k, v)
   int mode;
   uint32_t C;                // columns (length of x)
   uint32_t n_units;          // row tiles (SwiGlu: a tile is RU/2 gate rows + RU/2 up rows)
@@ -110,6 +110,7 @@ struct GemvArgs {
 
 struct GemvLaunch {  // launch geometry of one GemvArgs
   uint32_t blocks, threads, ru;
+  uint32_t cells;  // 1: the K-split kernel for 16-row cells at 2048 columns (one unit per workgroup)
 };
 
 struct StepState {  // device-resident per-token state read by the captured step
@@ -156,10 +157,11 @@ struct FinishArgs {
 
 // Workgroup caps of the one-unit-per-wave GEMV (0 = one unit per wave, no cap); the waves of
 // a capped grid stride over the remaining units.  Defaults, overridable for measurement by
-// CHPE_GEMV_ROWS_BLOCKS / CHPE_GEMV_LOGITS_BLOCKS.
+// CHPE_GEMV_ROWS_BLOCKS / CHPE_GEMV_LOGITS_BLOCKS / CHPE_GEMV_CELLS.
 struct GemvTuning {
   uint32_t rows_blocks = 0;
   uint32_t logits_blocks = 2048;
+  uint32_t cells = 1;  // CHPE_GEMV_CELLS=0: 16-row cells at 2048 columns on the one-unit-per-wave kernel
 };
 const GemvTuning& gemv_tuning();
 
