@@ -836,15 +836,31 @@ __global__ void __launch_bounds__(512, 2) k_gemv_split(GemvArgs a) {
 }
 
 // 16-row cells at 2048 columns (the q/k/v, o and gate/up projections), K-split: one workgroup
-// = one unit of RU = 8 rows, kCellWaves = 4 waves x 512 columns.  Lane (j, c) = (lane / 16,
-// lane % 16) of wave w holds unit rows j and j + 4 at columns 512 w + 32 c .. + 31 (one 16-byte
-// code load and one group scale per row), so a unit's dot products run on four SIMDs at once
-// instead of one.  Row sums meet over the 16 lanes of a row (DPP) and over the waves (LDS, in
-// wave order); wave 0 then holds row i on lanes 8 i .. 8 i + 7, adds the outlier terms and runs
-// the epilogue of the one-unit-per-wave kernel.  Every load is issued before the input staging
-// waits, with no branch in front of them.
+// = UPW units of RU = 8 rows, kCellWaves = 4 waves x 512 columns.  Lane (j, c) = (lane / 16,
+// lane % 16) of wave w holds rows j and j + 4 of every unit of the workgroup at columns
+// 512 w + 32 c .. + 31 (one 16-byte code load and one group scale per row), so a unit's dot
+// products run on four SIMDs at once instead of one; UPW > 1 shares one staging of the input
+// between units (the gate/up projection has thousands).  Row sums meet over the 16 lanes of a
+// row (DPP) and over the waves (LDS, in wave order); wave u then holds row i of unit u on lanes
+// 8 i .. 8 i + 7, adds the outlier terms and runs the epilogue of the one-unit-per-wave kernel.
+// Every load is issued before the input staging waits, with no branch in front of them.
 constexpr int kCellWaves = 4;
+
+// where unit u's rows start (the unit's part already chosen)
 template <int MODE>
+__device__ __forceinline__ uint32_t cells_row_base(const GemvPart& P0, uint32_t unit, uint32_t half) {
+  constexpr int RU = 8;
+  if constexpr (MODE == int(GemvMode::SwiGlu)) {
+    return unit * (RU / 2);
+  } else if constexpr (MODE == int(GemvMode::QkvRope)) {  // RU/2 pairs per unit, half/(RU/2) units per head
+    const uint32_t ul = unit - P0.unit_begin, per_head = half / (RU / 2);
+    return (ul / per_head) * (2 * half) + (ul % per_head) * (RU / 2);
+  } else {
+    return (unit - P0.unit_begin) * RU;
+  }
+}
+
+template <int MODE, int UPW>
 __global__ void __launch_bounds__(kWave * kCellWaves) k_gemv_cells(GemvArgs a) {
   constexpr int RU = 8, S = kWave / RU;
   constexpr bool kNorm = kNormOf<MODE>;
@@ -852,62 +868,69 @@ __global__ void __launch_bounds__(kWave * kCellWaves) k_gemv_cells(GemvArgs a) {
   constexpr bool kRope = MODE == int(GemvMode::QkvRope);
   constexpr bool kPre = MODE == int(GemvMode::Store) || MODE == int(GemvMode::Accum) || kRope;
   static_assert(MODE != int(GemvMode::Logits), "the LM head stays on k_gemv_rows");
+  static_assert(UPW >= 1 && UPW <= kCellWaves, "one epilogue wave per unit");
   __shared__ __align__(16) float s_x[xs_floats(2048)];
-  __shared__ float s_part[kCellWaves][RU];
+  __shared__ float s_part[kCellWaves][UPW * RU];
   __shared__ float s_red[kCellWaves];
   const int lane = threadIdx.x & 63, j = lane >> 4, c = lane & 15, i8 = lane >> 3;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   args_batch<MODE>(a);
-  const uint32_t unit = blockIdx.x, half = a.rope.head_dim / 2;
-  const int pu = kRope ? int(__builtin_amdgcn_readfirstlane(part_of(a, unit))) : 0;
-  const GemvPart Pr = kRope ? pick_part(a, pu) : a.part[0];
-  const GemvPart& P0 = kRope ? Pr : a.part[0];
-  const GemvPart& P1 = kSwi ? a.part[1] : P0;
-  uint32_t row_base;
-  if constexpr (kSwi) {
-    row_base = unit * (RU / 2);
-  } else if constexpr (kRope) {  // RU/2 pairs per unit, half/(RU/2) units per head
-    const uint32_t ul = unit - P0.unit_begin, per_head = half / (RU / 2);
-    row_base = (ul / per_head) * (2 * half) + (ul % per_head) * (RU / 2);
-  } else {
-    row_base = (unit - P0.unit_begin) * RU;
-  }
+  const uint32_t half = a.rope.head_dim / 2, unit0 = blockIdx.x * UPW;
 
-  // 1. the input first (its wait then leaves the later loads in flight), then the codes and
-  // scales of the lane's rows j and j + 4 (rows past the part read a row of it that exists and
-  // count zero): unit rows 0..3 and 4..7 each lie in one cell (their first row is a multiple of 4)
+  // 1. the input first (its wait then leaves the later loads in flight), then per unit the codes
+  // and scales of the lane's rows j and j + 4 (rows past the part read a row of it that exists
+  // and count zero): unit rows 0..3 and 4..7 each lie in one cell (their first row is a
+  // multiple of 4)
   StageRegs<2> xr;
   stage_x_issue<kNorm, 2, kWave * kCellWaves>(a, &xr);
-  const uint32_t rowA = row_of<RU, MODE>(row_base, 0, half), rowB = row_of<RU, MODE>(row_base, RU / 2, half);
-  const bool okA = rowA + j < P0.rows, okB = rowB + j < P1.rows;
-  const uint32_t cA = rowA < P0.rows ? rowA : 0u, cB = rowB < P1.rows ? rowB : 0u;
-  const uint8_t* cellA = P0.base + size_t(cA >> 4) * P0.stride;
-  const uint8_t* cellB = P1.base + size_t(cB >> 4) * P1.stride;
-  const uint32_t nA = (cA & 15u) + (okA ? uint32_t(j) : 0u), nB = (cB & 15u) + (okB ? uint32_t(j) : 0u);
   const uint32_t boff = wave * 256 + uint32_t(c) * 16, grp = wave * 4 + uint32_t(c >> 2);
-  const uint4 qA = ld_u128(cellA + 64 + nA * 1024 + boff);
-  const uint4 qB = ld_u128(cellB + 64 + nB * 1024 + boff);
-  const uint32_t sA = ld_u16(cellA + 16448 + 48 + 2 * (nA * 16 + grp));
-  const uint32_t sB = ld_u16(cellB + 16448 + 48 + 2 * (nB * 16 + grp));
-  // outlier k = lane % 8 of unit row i8 (gemvTileW4 :404-410: the cell's 8 columns, the row's 8
-  // weights), used by wave 0
+  uint4 qA[UPW], qB[UPW];
+  uint32_t sA[UPW], sB[UPW];
+  bool okA[UPW], okB[UPW];
+#pragma unroll
+  for (int u = 0; u < UPW; ++u) {
+    const uint32_t unit = min(unit0 + u, a.n_units - 1);  // a unit past the end repeats the last, counting zero
+    const bool live = unit0 + u < a.n_units;
+    const GemvPart P0 = kRope ? pick_part(a, int(__builtin_amdgcn_readfirstlane(part_of(a, unit)))) : a.part[0];
+    const GemvPart& P1 = kSwi ? a.part[1] : P0;
+    const uint32_t row_base = cells_row_base<MODE>(P0, unit, half);
+    const uint32_t rowA = row_of<RU, MODE>(row_base, 0, half), rowB = row_of<RU, MODE>(row_base, RU / 2, half);
+    okA[u] = live && rowA + j < P0.rows;
+    okB[u] = live && rowB + j < P1.rows;
+    const uint32_t cA = rowA < P0.rows ? rowA : 0u, cB = rowB < P1.rows ? rowB : 0u;
+    const uint8_t* cellA = P0.base + size_t(cA >> 4) * P0.stride;
+    const uint8_t* cellB = P1.base + size_t(cB >> 4) * P1.stride;
+    const uint32_t nA = (cA & 15u) + (rowA + j < P0.rows ? uint32_t(j) : 0u);
+    const uint32_t nB = (cB & 15u) + (rowB + j < P1.rows ? uint32_t(j) : 0u);
+    qA[u] = ld_u128(cellA + 64 + nA * 1024 + boff);
+    qB[u] = ld_u128(cellB + 64 + nB * 1024 + boff);
+    sA[u] = ld_u16(cellA + 16448 + 48 + 2 * (nA * 16 + grp));
+    sB[u] = ld_u16(cellB + 16448 + 48 + 2 * (nB * 16 + grp));
+  }
+  // the epilogue operands of unit `wave` (when wave < UPW): outlier k = lane % 8 of unit row i8
+  // (gemvTileW4 :404-410: the cell's 8 columns, the row's 8 weights); lane 8 i's residual or
+  // bias and RoPE factors
+  const uint32_t eunit = min(unit0 + (wave < uint32_t(UPW) ? wave : 0u), a.n_units - 1);
+  const bool elive = wave < uint32_t(UPW) && unit0 + wave < a.n_units;
+  const GemvPart E0 = kRope ? pick_part(a, int(__builtin_amdgcn_readfirstlane(part_of(a, eunit)))) : a.part[0];
+  const GemvPart& E1 = kSwi ? a.part[1] : E0;
+  const uint32_t erow_base = cells_row_base<MODE>(E0, eunit, half);
   const bool osecond = kSwi && i8 >= RU / 2;
-  const uint32_t orow = row_of<RU, MODE>(row_base, i8, half);
-  const bool ovalid = orow < (osecond ? P1.rows : P0.rows);
+  const uint32_t orow = row_of<RU, MODE>(erow_base, i8, half);
+  const bool ovalid = elive && orow < (osecond ? E1.rows : E0.rows);
   const uint32_t orr = ovalid ? orow : 0u;
-  const uint8_t* ocell = (osecond ? P1.base : P0.base) + size_t(orr >> 4) * (osecond ? P1.stride : P0.stride);
+  const uint8_t* ocell = (osecond ? E1.base : E0.base) + size_t(orr >> 4) * (osecond ? E1.stride : E0.stride);
   const uint32_t ocol = ld_u16(ocell + 16448 + 816 + 2 * (lane & 7));
   const uint32_t ow = ld_u16(ocell + 16448 + 560 + 2 * ((orr & 15u) * 8 + uint32_t(lane & 7)));
-  // epilogue operands of wave 0's rows (lane 8 i serves row i)
   float pre = 0.0f, rc = 1.0f, rs = 0.0f;
   bool pre_ok = false, rope_ok = false;
   if constexpr (kPre) {
-    const float* src = MODE == int(GemvMode::Accum) ? P0.y : P0.bias;
-    pre_ok = (lane % S) == 0 && orow < P0.rows && src != nullptr;
+    const float* src = MODE == int(GemvMode::Accum) ? E0.y : E0.bias;
+    pre_ok = elive && (lane % S) == 0 && orow < E0.rows && src != nullptr;
     pre = (src ? src : a.x)[pre_ok ? orow : 0u];
   }
   if constexpr (kRope) {
-    rope_ok = (lane % S) == 0 && lane < 32 && P0.rope_role != kRoleV;
+    rope_ok = elive && (lane % S) == 0 && lane < 32 && E0.rope_role != kRoleV;
     const size_t at = rope_ok ? size_t(a.rope.state->pos) * half + (orow % (2 * half)) : 0u;
     rc = a.rope.cos[at];
     rs = a.rope.sin[at];
@@ -917,7 +940,8 @@ __global__ void __launch_bounds__(kWave * kCellWaves) k_gemv_cells(GemvArgs a) {
   float ss = 0.0f, inv = 1.0f;
   stage_x_finish<kNorm, false, 2, kWave * kCellWaves>(a, xr, s_x, s_red, &ss, &inv);
 
-  // 3. the lane's two 32-column dots, summed over the 16 lanes of each row, then over the waves
+  // 3. per unit the lane's two 32-column dots, summed over the 16 lanes of each row, then over
+  // the waves
   float xv[32];
   const uint32_t col0 = wave * 512 + uint32_t(c) * 32;
   float sx = 0.0f;
@@ -928,26 +952,29 @@ __global__ void __launch_bounds__(kWave * kCellWaves) k_gemv_cells(GemvArgs a) {
   }
 #pragma unroll
   for (int k = 0; k < 32; ++k) sx += xv[k];
-  float tA = (dot32_w4(qA, xv) - Cell16W4::kOff * sx) * Cell16W4::scale(sA);
-  float tB = (dot32_w4(qB, xv) - Cell16W4::kOff * sx) * Cell16W4::scale(sB);
-  tA = okA ? tA : 0.0f;
-  tB = okB ? tB : 0.0f;
 #pragma unroll
-  for (int m = 1; m < 16; m <<= 1) {
-    tA = pair_sum(tA, m);
-    tB = pair_sum(tB, m);
-  }
-  if (c == 0) {
-    s_part[wave][j] = tA;
-    s_part[wave][j + RU / 2] = tB;
+  for (int u = 0; u < UPW; ++u) {
+    float tA = (dot32_w4(qA[u], xv) - Cell16W4::kOff * sx) * Cell16W4::scale(sA[u]);
+    float tB = (dot32_w4(qB[u], xv) - Cell16W4::kOff * sx) * Cell16W4::scale(sB[u]);
+    tA = okA[u] ? tA : 0.0f;
+    tB = okB[u] ? tB : 0.0f;
+#pragma unroll
+    for (int m = 1; m < 16; m <<= 1) {
+      tA = pair_sum(tA, m);
+      tB = pair_sum(tB, m);
+    }
+    if (c == 0) {
+      s_part[wave][u * RU + j] = tA;
+      s_part[wave][u * RU + j + RU / 2] = tB;
+    }
   }
   __syncthreads();
-  if (wave != 0) return;
+  if (wave >= uint32_t(UPW)) return;
 
-  // 4. wave 0: row i8's total and outlier terms on its 8 lanes, then the epilogue
+  // 4. wave u: row i8 of unit u with its outlier terms on the row's 8 lanes, then the epilogue
   float v = 0.0f;
 #pragma unroll
-  for (int w = 0; w < kCellWaves; ++w) v += s_part[w][i8];
+  for (int w = 0; w < kCellWaves; ++w) v += s_part[w][wave * RU + i8];
   const float ox = s_x[xs_at(ocol < 2048u ? ocol : 0u)];
   float o = (ovalid && ocol < 2048u) ? half_lo(ow) * ox : 0.0f;
   o = pair_sum(o, 1);
@@ -959,11 +986,12 @@ __global__ void __launch_bounds__(kWave * kCellWaves) k_gemv_cells(GemvArgs a) {
   const float up_pre = kRope ? pair_val(prev, 32) : 0.0f;
   float bv = -1e30f;
   uint32_t bi = 0xffffffffu, nf = 0;
+  if (!elive) return;
   if constexpr (kRope) {
-    if ((lane % S) == 0 && i8 < RU / 2 && orow < P0.rows)
-      rope_store(a, P0, orow, v + prev, up + up_pre, rope_ok ? rc : 1.0f, rope_ok ? rs : 0.0f);
+    if ((lane % S) == 0 && i8 < RU / 2 && orow < E0.rows)
+      rope_store(a, E0, orow, v + prev, up + up_pre, rope_ok ? rc : 1.0f, rope_ok ? rs : 0.0f);
   } else if ((lane % S) == 0 && (!kSwi || i8 < RU / 2)) {
-    epilogue<MODE>(P0, row_of<RU, MODE>(row_base, i8, 0), v, up, prev, &bv, &bi, &nf);
+    epilogue<MODE>(E0, row_of<RU, MODE>(erow_base, i8, 0), v, up, prev, &bv, &bi, &nf);
   }
 }
 
@@ -971,10 +999,9 @@ template <class F, int MODE>
 void launch_one(const GemvArgs& a, const GemvLaunch& g, hipStream_t st) {
   const size_t lds = size_t(xs_floats(a.C)) * 4;
   if constexpr (std::is_same_v<F, Cell16W4> && MODE != int(GemvMode::Logits)) {
-    if (g.cells) {
-      launch_kernel(&k_gemv_cells<MODE>, dim3(g.blocks), dim3(g.threads), st, a);
-      return;
-    }
+    if (g.cells == 1) { launch_kernel(&k_gemv_cells<MODE, 1>, dim3(g.blocks), dim3(g.threads), st, a); return; }
+    if (g.cells == 2) { launch_kernel(&k_gemv_cells<MODE, 2>, dim3(g.blocks), dim3(g.threads), st, a); return; }
+    if (g.cells == 4) { launch_kernel(&k_gemv_cells<MODE, 4>, dim3(g.blocks), dim3(g.threads), st, a); return; }
   }
   if (a.waves_per_unit == 1)
     launch_kernel(&k_gemv_rows<F, MODE>, dim3(g.blocks), dim3(g.threads), st, a);
@@ -1038,9 +1065,13 @@ GemvLaunch gemv_geometry(WeightKind kind, GemvMode mode, uint32_t C, const uint3
   GemvLaunch g{};
   g.ru = ru;
   if (kind == WeightKind::Cell16W4 && mode != GemvMode::Logits && C == 2048 && gemv_tuning().cells) {
-    g.cells = 1;  // one unit per workgroup, K-split over kCellWaves waves
+    // K-split over kCellWaves waves; units per workgroup: 1 for the small projections (more
+    // workgroups, more parallel dot work), up to the tuning cap when there are thousands
+    uint32_t upw = units >= 2048 ? gemv_tuning().cells : 1u;
+    if (upw != 1 && upw != 2 && upw != 4) upw = 1;
+    g.cells = upw;
     g.threads = kWave * kCellWaves;
-    g.blocks = units;
+    g.blocks = (units + upw - 1) / upw;
   } else if (nw == 1) {
     g.threads = kWave * (kRowWaves + 1);
     g.blocks = (units + kRowWaves - 1) / kRowWaves;

@@ -110,7 +110,7 @@ struct GemvArgs {
 
 struct GemvLaunch {  // launch geometry of one GemvArgs
   uint32_t blocks, threads, ru;
-  uint32_t cells;  // 1: the K-split kernel for 16-row cells at 2048 columns (one unit per workgroup)
+  uint32_t cells;  // > 0: the K-split kernel for 16-row cells at 2048 columns, `cells` units per workgroup
 };
 
 struct StepState {  // device-resident per-token state read by the captured step
@@ -161,7 +161,8 @@ struct FinishArgs {
 struct GemvTuning {
   uint32_t rows_blocks = 0;
   uint32_t logits_blocks = 2048;
-  uint32_t cells = 1;  // CHPE_GEMV_CELLS=0: 16-row cells at 2048 columns on the one-unit-per-wave kernel
+  uint32_t cells = 2;  // units per workgroup of the K-split cell kernel when a launch has >= 2048 units
+                       // (1, 2 or 4); CHPE_GEMV_CELLS=0: the one-unit-per-wave kernel instead
 };
 const GemvTuning& gemv_tuning();
 
