@@ -995,6 +995,139 @@ __global__ void __launch_bounds__(kWave * kCellWaves) k_gemv_cells(GemvArgs a) {
   }
 }
 
+// Flat 4-bit tiles (gemvCellFlat: the down projection, and every projection wider than 2048
+// columns), K-split: one workgroup = one unit of RU = 8 rows, kFlatWaves = 8 waves (two per
+// SIMD) striding over panels of 512 columns (4 groups of 128; panel p goes to wave p % 8).
+// Lane (j, c) = (lane / 16, lane % 16) holds unit rows j and j + 4 at columns 512 p + 32 c ..
+// + 31 of each of its wave's panels: one 16-byte code load and one group scale per row and
+// panel, all issued before the input staging waits (up to MAXP panels per wave).  Row sums meet
+// over the 16 lanes (DPP) and the waves (LDS, in wave order); wave 0 adds the row's outlier
+// corrections and runs the epilogue.  The input sits in LDS (dynamic, C floats) for the dots
+// and for the corrections, which read any column.
+constexpr int kFlatWaves = 8;
+template <int MODE, int MAXP, bool kWide>
+__global__ void __launch_bounds__(kWave * kFlatWaves) k_gemv_flat(GemvArgs a) {
+  constexpr int RU = 8, S = kWave / RU, NT = kWave * kFlatWaves;
+  constexpr bool kNorm = kNormOf<MODE>;
+  constexpr bool kSwi = MODE == int(GemvMode::SwiGlu);
+  constexpr bool kRope = MODE == int(GemvMode::QkvRope);
+  constexpr bool kPre = MODE == int(GemvMode::Store) || MODE == int(GemvMode::Accum) || kRope;
+  static_assert(MODE != int(GemvMode::Logits), "the flat LM head stays on k_gemv_split");
+  extern __shared__ __align__(16) float s_x[];  // xs_floats(C) floats
+  __shared__ float s_part[kFlatWaves][RU];
+  __shared__ float s_red[kFlatWaves];
+  const int lane = threadIdx.x & 63, j = lane >> 4, c = lane & 15;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  args_batch<MODE>(a);
+  const uint32_t C = a.C, ng = C >> 7, npan = (ng + 3) / 4, half = a.rope.head_dim / 2, unit = blockIdx.x;
+  const GemvPart P0 = kRope ? pick_part(a, int(__builtin_amdgcn_readfirstlane(part_of(a, unit)))) : a.part[0];
+  const GemvPart& P1 = kSwi ? a.part[1] : P0;
+  const uint32_t row_base = cells_row_base<MODE>(P0, unit, half);
+
+  // 1. the input first, then codes and scales of rows j and j + 4 for each of the wave's panels
+  StageRegs<8> xr;
+  if constexpr (!kWide) stage_x_issue<kNorm, 8, NT>(a, &xr);
+  const uint32_t rowA = row_of<RU, MODE>(row_base, j, half), rowB = row_of<RU, MODE>(row_base, j + RU / 2, half);
+  const bool okA = rowA < P0.rows, okB = rowB < P1.rows;
+  // 32-bit group indices and byte offsets from the part's base (a uniform 64-bit pointer), so
+  // that each load is a scalar base plus one vector offset (the tensors here are < 4 GiB)
+  const uint32_t GA = (okA ? rowA : 0u) * ng, GB = (okB ? rowB : 0u) * ng;
+  const uint8_t* baseA = P0.base;
+  const uint8_t* baseB = P1.base;
+  const uint32_t strA = P0.stride, strB = P1.stride, lo16 = uint32_t(c & 3) * 16;
+  uint4 qa[MAXP], qb[MAXP];
+  uint32_t sa[MAXP], sb[MAXP], gvm = 0;
+#pragma unroll
+  for (int q = 0; q < MAXP; ++q) {
+    const uint32_t p = wave + kFlatWaves * uint32_t(q), g = 4 * p + uint32_t(c >> 2);
+    const bool gv = p < npan && g < ng;
+    gvm |= uint32_t(gv) << q;
+    const uint32_t Ga = GA + (gv ? g : 0u), Gb = GB + (gv ? g : 0u);
+    const uint32_t oa = (Ga >> 8) * strA + (Ga & 255u) * 64, ob = (Gb >> 8) * strB + (Gb & 255u) * 64;
+    const uint32_t sa_off = (Ga >> 8) * strA + 16448 + 48 + 2 * (Ga & 255u);
+    const uint32_t sb_off = (Gb >> 8) * strB + 16448 + 48 + 2 * (Gb & 255u);
+    qa[q] = ld_u128(baseA + (oa + 64 + lo16));
+    qb[q] = ld_u128(baseB + (ob + 64 + lo16));
+    sa[q] = ld_u16(baseA + sa_off);
+    sb[q] = ld_u16(baseB + sb_off);
+  }
+  // wave 0's epilogue operands: the rows' correction entries, lane 8 i's residual / bias / RoPE
+  FlatExtras fe;
+  fe.use = 0;
+  if (wave == 0) load_flat_extras<RU, MODE>(P0, P1, row_base, half, lane, true, a.x, &fe);
+  const int i8 = lane >> 3;
+  const uint32_t orow = row_of<RU, MODE>(row_base, i8, half);
+  float pre = 0.0f, rc = 1.0f, rs = 0.0f;
+  bool pre_ok = false, rope_ok = false;
+  if constexpr (kPre) {
+    const float* src = MODE == int(GemvMode::Accum) ? P0.y : P0.bias;
+    pre_ok = (lane % S) == 0 && orow < P0.rows && src != nullptr;
+    pre = (src ? src : a.x)[pre_ok ? orow : 0u];
+  }
+  if constexpr (kRope) {
+    rope_ok = (lane % S) == 0 && lane < 32 && P0.rope_role != kRoleV;
+    const size_t at = rope_ok ? size_t(a.rope.state->pos) * half + (orow % (2 * half)) : 0u;
+    rc = a.rope.cos[at];
+    rs = a.rope.sin[at];
+  }
+
+  // 2. the (normalised) input into LDS
+  float ss = 0.0f, inv = 1.0f;
+  stage_x_finish<kNorm, kWide, 8, NT>(a, xr, s_x, s_red, &ss, &inv);
+
+  // 3. the dots of the wave's panels, summed over the 16 lanes of each row, then over the waves
+  float accA = 0.0f, accB = 0.0f;
+#pragma unroll
+  for (int q = 0; q < MAXP; ++q) {
+    const uint32_t p = wave + kFlatWaves * uint32_t(q);
+    const bool gv = (gvm >> q) & 1u;
+    const uint32_t col0 = gv ? 512 * p + 32 * uint32_t(c) : 0u;
+    float xv[32];
+    float sx = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const float4 t = *reinterpret_cast<const float4*>(s_x + xs_at(col0 + 4 * k));
+      xv[4 * k] = t.x; xv[4 * k + 1] = t.y; xv[4 * k + 2] = t.z; xv[4 * k + 3] = t.w;
+    }
+#pragma unroll
+    for (int k = 0; k < 32; ++k) sx += xv[k];
+    const float tA = (dot32_w4(qa[q], xv) - FlatW4::kOff * sx) * FlatW4::scale(sa[q]);
+    const float tB = (dot32_w4(qb[q], xv) - FlatW4::kOff * sx) * FlatW4::scale(sb[q]);
+    accA += gv ? tA : 0.0f;
+    accB += gv ? tB : 0.0f;
+  }
+  accA = okA ? accA : 0.0f;
+  accB = okB ? accB : 0.0f;
+#pragma unroll
+  for (int m = 1; m < 16; m <<= 1) {
+    accA = pair_sum(accA, m);
+    accB = pair_sum(accB, m);
+  }
+  if (c == 0) {
+    s_part[wave][j] = accA;
+    s_part[wave][j + RU / 2] = accB;
+  }
+  __syncthreads();
+  if (wave != 0) return;
+
+  // 4. wave 0: row i8 on lanes 8 i8 .. 8 i8 + 7, its corrections, the epilogue
+  float v = 0.0f;
+#pragma unroll
+  for (int w = 0; w < kFlatWaves; ++w) v += s_part[w][i8];
+  v += flat_correction(fe, s_x);
+  const float up = (kSwi || kRope) ? pair_val(v, 32) : 0.0f;
+  const float prev = pre_ok ? pre : 0.0f;
+  const float up_pre = kRope ? pair_val(prev, 32) : 0.0f;
+  float bv = -1e30f;
+  uint32_t bi = 0xffffffffu, nf = 0;
+  if constexpr (kRope) {
+    if ((lane % S) == 0 && i8 < RU / 2 && orow < P0.rows)
+      rope_store(a, P0, orow, v + prev, up + up_pre, rope_ok ? rc : 1.0f, rope_ok ? rs : 0.0f);
+  } else if ((lane % S) == 0 && (!kSwi || i8 < RU / 2)) {
+    epilogue<MODE>(P0, row_of<RU, MODE>(row_base, i8, 0), v, up, prev, &bv, &bi, &nf);
+  }
+}
+
 template <class F, int MODE>
 void launch_one(const GemvArgs& a, const GemvLaunch& g, hipStream_t st) {
   const size_t lds = size_t(xs_floats(a.C)) * 4;
@@ -1002,6 +1135,22 @@ void launch_one(const GemvArgs& a, const GemvLaunch& g, hipStream_t st) {
     if (g.cells == 1) { launch_kernel(&k_gemv_cells<MODE, 1>, dim3(g.blocks), dim3(g.threads), st, a); return; }
     if (g.cells == 2) { launch_kernel(&k_gemv_cells<MODE, 2>, dim3(g.blocks), dim3(g.threads), st, a); return; }
     if (g.cells == 4) { launch_kernel(&k_gemv_cells<MODE, 4>, dim3(g.blocks), dim3(g.threads), st, a); return; }
+  }
+  if constexpr (std::is_same_v<F, FlatW4> && MODE != int(GemvMode::Logits)) {
+    if (g.flat) {
+      const dim3 gr(g.blocks), bl(g.threads);
+      const bool wide = a.C > 8u * 4u * uint32_t(kWave * kFlatWaves);
+      switch (g.flat) {
+        case 1: launch_kernel_lds(&k_gemv_flat<MODE, 1, false>, gr, bl, lds, st, a); return;
+        case 2: launch_kernel_lds(&k_gemv_flat<MODE, 2, false>, gr, bl, lds, st, a); return;
+        case 3: launch_kernel_lds(&k_gemv_flat<MODE, 3, false>, gr, bl, lds, st, a); return;
+        case 4: launch_kernel_lds(&k_gemv_flat<MODE, 4, false>, gr, bl, lds, st, a); return;
+        default:
+          if (wide) launch_kernel_lds(&k_gemv_flat<MODE, 8, true>, gr, bl, lds, st, a);
+          else launch_kernel_lds(&k_gemv_flat<MODE, 8, false>, gr, bl, lds, st, a);
+          return;
+      }
+    }
   }
   if (a.waves_per_unit == 1)
     launch_kernel(&k_gemv_rows<F, MODE>, dim3(g.blocks), dim3(g.threads), st, a);
@@ -1030,6 +1179,7 @@ const GemvTuning& gemv_tuning() {
     if (const char* e = std::getenv("CHPE_GEMV_ROWS_BLOCKS")) v.rows_blocks = uint32_t(std::strtoul(e, nullptr, 10));
     if (const char* e = std::getenv("CHPE_GEMV_LOGITS_BLOCKS")) v.logits_blocks = uint32_t(std::strtoul(e, nullptr, 10));
     if (const char* e = std::getenv("CHPE_GEMV_CELLS")) v.cells = uint32_t(std::strtoul(e, nullptr, 10));
+    if (const char* e = std::getenv("CHPE_GEMV_FLAT")) v.flat = uint32_t(std::strtoul(e, nullptr, 10));
     if (v.logits_blocks == 0 || v.logits_blocks > kMaxLogitsBlocks) v.logits_blocks = kMaxLogitsBlocks;
     return v;
   }();
@@ -1072,6 +1222,13 @@ GemvLaunch gemv_geometry(WeightKind kind, GemvMode mode, uint32_t C, const uint3
     g.cells = upw;
     g.threads = kWave * kCellWaves;
     g.blocks = (units + upw - 1) / upw;
+  } else if (kind == WeightKind::FlatW4 && mode != GemvMode::Logits && C <= 32768 && gemv_tuning().flat &&
+             uint64_t(rows[0]) * C / 2 < (uint64_t(1) << 31) && uint64_t(rows[n_parts - 1]) * C / 2 < (uint64_t(1) << 31)) {
+    // K-split over kFlatWaves waves striding over 512-column panels, one unit per workgroup
+    const uint32_t panels = (C / 128 + 3) / 4, per_wave = (panels + kFlatWaves - 1) / kFlatWaves;
+    g.flat = per_wave <= 4 ? per_wave : 8;
+    g.threads = kWave * kFlatWaves;
+    g.blocks = units;
   } else if (nw == 1) {
     g.threads = kWave * (kRowWaves + 1);
     g.blocks = (units + kRowWaves - 1) / kRowWaves;

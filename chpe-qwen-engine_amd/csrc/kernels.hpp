@@ -111,6 +111,7 @@ struct GemvArgs {
 struct GemvLaunch {  // launch geometry of one GemvArgs
   uint32_t blocks, threads, ru;
   uint32_t cells;  // > 0: the K-split kernel for 16-row cells at 2048 columns, `cells` units per workgroup
+  uint32_t flat;   // > 0: the K-split kernel for flat 4-bit tiles, up to `flat` panels per wave
 };
 
 struct StepState {  // device-resident per-token state read by the captured step
@@ -163,6 +164,7 @@ struct GemvTuning {
   uint32_t logits_blocks = 2048;
   uint32_t cells = 2;  // units per workgroup of the K-split cell kernel when a launch has >= 2048 units
                        // (1, 2 or 4); CHPE_GEMV_CELLS=0: the one-unit-per-wave kernel instead
+  uint32_t flat = 1;   // CHPE_GEMV_FLAT=0: flat 4-bit tiles on the one-workgroup-per-unit K-split by panels
 };
 const GemvTuning& gemv_tuning();
 
