@@ -223,6 +223,8 @@ __global__ void __launch_bounds__(NW * 64) k_attn_mfma(AttnArgs a) {
   constexpr int CH = NW * T * 16, NT = NW * 64;
   static_assert(CH == int(attn_chunk_of(HD)) && GQ <= 8 && NW * GQ <= 64 && (NW & (NW - 1)) == 0, "");
   const uint32_t c = blockIdx.x, kvh = blockIdx.y;
+  // the position is requested first and waited for only after the loads below are issued
+  const uint32_t pos = a.state->pos, ctx = pos + 1;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int G = lane >> 4, n = lane & 15, h = n & 7;  // h: the query head of column / row n
   const bool rem = n >= 8;
@@ -236,10 +238,14 @@ __global__ void __launch_bounds__(NW * 64) k_attn_mfma(AttnArgs a) {
   // 4G..4G+3 of each tile, dims n*VD..); rows past the context are masked at use
   const uint32_t p0 = c * CH + uint32_t(wave) * T * 16;
   const bool qok = h < GQ;
-  const float* qsrc = a.q + size_t(kvh * GQ + (qok ? h : 0)) * HD + G * KD;
-  float4 qv[KD / 4];
+  // the group's queries are read once per workgroup (QF4 float4 per thread) and shared through
+  // LDS: every lane needs 32 of them, and 4 waves reading all their own would quadruple the
+  // workgroup's request traffic
+  constexpr int QN4 = GQ * HD / 4, QF4 = (QN4 + NT - 1) / NT;
+  __shared__ __align__(16) float s_q[GQ * HD];
+  float4 qld[QF4];
 #pragma unroll
-  for (int i = 0; i < KD / 4; ++i) qv[i] = ld_f4(qsrc + 4 * i);
+  for (int k = 0; k < QF4; ++k) qld[k] = ld_f4(a.q + size_t(kvh * GQ) * HD + min(tid + NT * k, QN4 - 1) * 4);
   const uint8_t* kc = reinterpret_cast<const uint8_t*>(a.k_cache) + size_t(kvh) * a.max_seq * HD * 2;
   const uint8_t* vc = reinterpret_cast<const uint8_t*>(a.v_cache) + size_t(kvh) * a.max_seq * HD * 2;
   uint4 kf[T][KD / 8], vf[T][VD / 2];
@@ -257,10 +263,17 @@ __global__ void __launch_bounds__(NW * 64) k_attn_mfma(AttnArgs a) {
   // keep every load above this point: the scheduler would otherwise sink the V loads next to
   // the P.V products, after the softmax
   __builtin_amdgcn_sched_barrier(0);
-  const uint32_t pos = a.state->pos, ctx = pos + 1;
+#pragma unroll
+  for (int k = 0; k < QF4; ++k)
+    if (tid + NT * k < QN4) *reinterpret_cast<float4*>(&s_q[(tid + NT * k) * 4]) = qld[k];
+  __syncthreads();
   if (c * CH >= ctx) return;  // the whole workgroup; its loads are dropped
 
   // 2. the query operand (zero for heads past the group)
+  const float* qsrc = s_q + (qok ? h : 0) * HD + G * KD;
+  float4 qv[KD / 4];
+#pragma unroll
+  for (int i = 0; i < KD / 4; ++i) qv[i] = *reinterpret_cast<const float4*>(qsrc + 4 * i);
   h4_t qb[KS];
 #pragma unroll
   for (int st = 0; st < KS; ++st) {

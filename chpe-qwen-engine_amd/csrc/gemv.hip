@@ -902,10 +902,11 @@ __global__ void __launch_bounds__(kWave * kCellWaves) k_gemv_cells(GemvArgs a) {
     const uint8_t* cellB = P1.base + size_t(cB >> 4) * P1.stride;
     const uint32_t nA = (cA & 15u) + (rowA + j < P0.rows ? uint32_t(j) : 0u);
     const uint32_t nB = (cB & 15u) + (rowB + j < P1.rows ? uint32_t(j) : 0u);
-    qA[u] = ld_u128(cellA + 64 + nA * 1024 + boff);
-    qB[u] = ld_u128(cellB + 64 + nB * 1024 + boff);
-    sA[u] = ld_u16(cellA + 16448 + 48 + 2 * (nA * 16 + grp));
-    sB[u] = ld_u16(cellB + 16448 + 48 + 2 * (nB * 16 + grp));
+    // (a scalar cell base plus one 32-bit vector offset per load)
+    qA[u] = ld_u128(cellA + (64 + nA * 1024 + boff));
+    qB[u] = ld_u128(cellB + (64 + nB * 1024 + boff));
+    sA[u] = ld_u16(cellA + (16448 + 48 + 2 * (nA * 16 + grp)));
+    sB[u] = ld_u16(cellB + (16448 + 48 + 2 * (nB * 16 + grp)));
   }
   // the epilogue operands of unit `wave` (when wave < UPW): outlier k = lane % 8 of unit row i8
   // (gemvTileW4 :404-410: the cell's 8 columns, the row's 8 weights); lane 8 i's residual or
@@ -920,8 +921,8 @@ __global__ void __launch_bounds__(kWave * kCellWaves) k_gemv_cells(GemvArgs a) {
   const bool ovalid = elive && orow < (osecond ? E1.rows : E0.rows);
   const uint32_t orr = ovalid ? orow : 0u;
   const uint8_t* ocell = (osecond ? E1.base : E0.base) + size_t(orr >> 4) * (osecond ? E1.stride : E0.stride);
-  const uint32_t ocol = ld_u16(ocell + 16448 + 816 + 2 * (lane & 7));
-  const uint32_t ow = ld_u16(ocell + 16448 + 560 + 2 * ((orr & 15u) * 8 + uint32_t(lane & 7)));
+  const uint32_t ocol = ld_u16(ocell + (16448 + 816 + 2 * uint32_t(lane & 7)));
+  const uint32_t ow = ld_u16(ocell + (16448 + 560 + 2 * ((orr & 15u) * 8 + uint32_t(lane & 7))));
   float pre = 0.0f, rc = 1.0f, rs = 0.0f;
   bool pre_ok = false, rope_ok = false;
   if constexpr (kPre) {
