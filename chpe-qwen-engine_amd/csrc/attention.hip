@@ -4,7 +4,7 @@
 // (q.k_t)*scale, softmax over t <= pos, output sum_t softmax_t * v_t.  RoPE and the KV append
 // at `pos` (:1688-1697) are done by the q/k/v projection's epilogue (GemvMode::QkvRope), so
 // the queries arrive rotated and cache rows 0..pos are complete.  The context is split into
-// chunks of attn_chunk(hd) positions (16384/hd: 128 at hd 128): the chunk kernel computes, per
+// chunks of attn_chunk(hd) positions (8192/hd: 64 at hd 128): the chunk kernel computes, per
 // chunk and query head, the chunk max, the sum of exp(s - max) and the exp-weighted sum of the
 // V rows (k_attn_mfma on the matrix cores for the fp16 cache, k_attn_chunk on the vector ALUs
 // for the f32 cache); k_attn_merge rescales and merges the chunks.  Workgroup (chunk, kv head)
@@ -382,24 +382,36 @@ __global__ void __launch_bounds__(NW * 64) k_attn_mfma(AttnArgs a) {
 // lanes (chunk lane + 64 k), the weights go through LDS (w_c = 0 past the active chunks, whose
 // sums are read at chunk 0 and so contribute exactly 0), and every load of a batch of 32
 // chunks is issued before its use.
+// The merge: one workgroup of kMergeWaves waves per (query head, 64 output dims).  Wave w sums
+// the chunks w, w + 4, ... (every load issued before the position is known; chunks past the
+// context are masked), the waves' sums meet in LDS in wave order.  Every wave forms the chunk
+// weights exp(m_c - M) itself from the chunk statistics (no barrier before the sums).
+constexpr uint32_t kMergeWaves = 4;
 template <int HD>
-__global__ void __launch_bounds__(64) k_attn_merge(AttnArgs a) {
+__global__ void __launch_bounds__(64 * kMergeWaves) k_attn_merge(AttnArgs a) {
   constexpr uint32_t CH = attn_chunk_of(HD), KC = (kAttnMaxChunks + 63) / 64, B = 32;
-  static_assert(kAttnMaxChunks % 4 == 0 && B % 4 == 0, "");
+  static_assert(kAttnMaxChunks % 4 == 0, "");
   __shared__ __align__(16) float s_w[KC * 64];
-  const uint32_t h = blockIdx.x, lane = threadIdx.x, d = blockIdx.y * 64 + lane;
-  const uint32_t n_act = (a.state->pos + CH) / CH, nch = a.n_chunks;
+  __shared__ float s_o[kMergeWaves][64];
+  const uint32_t h = blockIdx.x, lane = threadIdx.x & 63, d = blockIdx.y * 64 + lane;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const uint32_t pos = a.state->pos, nch = a.n_chunks;
   const float* ml = a.part_ml + size_t(h) * nch * 2;
   const float* acc = a.part_acc + size_t(h) * nch * HD + d;
   float mv[KC], lv[KC], av[B];
 #pragma unroll
   for (uint32_t k = 0; k < KC; ++k) {
-    const uint32_t cc = lane + 64 * k, cl = cc < n_act ? cc : 0u;
+    const uint32_t cc = lane + 64 * k, cl = cc < nch ? cc : 0u;
     mv[k] = ml[2 * cl];
     lv[k] = ml[2 * cl + 1];
   }
 #pragma unroll
-  for (uint32_t k = 0; k < B; ++k) av[k] = acc[size_t(k < n_act ? k : 0u) * HD];
+  for (uint32_t k = 0; k < B; ++k) {
+    const uint32_t cc = wave + kMergeWaves * k;
+    av[k] = acc[size_t(cc < nch ? cc : 0u) * HD];
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  const uint32_t n_act = (pos + CH) / CH;
   float M = -INFINITY;
 #pragma unroll
   for (uint32_t k = 0; k < KC; ++k) M = fmaxf(M, lane + 64 * k < n_act ? mv[k] : -INFINITY);
@@ -407,28 +419,33 @@ __global__ void __launch_bounds__(64) k_attn_merge(AttnArgs a) {
   float L = 0.0f;
 #pragma unroll
   for (uint32_t k = 0; k < KC; ++k) {
-    const float w = lane + 64 * k < n_act ? expf(mv[k] - M) : 0.0f;
-    s_w[lane + 64 * k] = w;
-    L = fmaf(lv[k], w, L);
+    const bool ok = lane + 64 * k < n_act;
+    const float w = ok ? expf(mv[k] - M) : 0.0f;
+    s_w[lane + 64 * k] = w;  // every wave writes the same values
+    L = fmaf(ok ? lv[k] : 0.0f, w, L);
   }
   L = wave_sum(L);
   __syncthreads();
-  float o4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-  for (uint32_t c0 = 0; c0 < n_act; c0 += B) {
+  float o = 0.0f;
+  for (uint32_t c0 = 0; c0 * kMergeWaves < n_act; c0 += B) {
     if (c0 > 0) {  // longer contexts: further batches
 #pragma unroll
-      for (uint32_t k = 0; k < B; ++k) av[k] = acc[size_t(c0 + k < n_act ? c0 + k : 0u) * HD];
+      for (uint32_t k = 0; k < B; ++k) {
+        const uint32_t cc = wave + kMergeWaves * (c0 + k);
+        av[k] = acc[size_t(cc < n_act ? cc : 0u) * HD];
+      }
     }
 #pragma unroll
-    for (uint32_t k = 0; k < B; k += 4) {
-      const float4 w4 = *reinterpret_cast<const float4*>(&s_w[c0 + k]);
-      o4[0] = fmaf(av[k], w4.x, o4[0]);
-      o4[1] = fmaf(av[k + 1], w4.y, o4[1]);
-      o4[2] = fmaf(av[k + 2], w4.z, o4[2]);
-      o4[3] = fmaf(av[k + 3], w4.w, o4[3]);
+    for (uint32_t k = 0; k < B; ++k) {  // branch-free: every weight is read, the unused ones masked
+      const uint32_t cc = wave + kMergeWaves * (c0 + k);
+      const bool ok = cc < n_act;
+      const float wv = s_w[ok ? cc : 0u];
+      o = fmaf(ok ? av[k] : 0.0f, ok ? wv : 0.0f, o);
     }
   }
-  a.out[size_t(h) * HD + d] = ((o4[0] + o4[1]) + (o4[2] + o4[3])) / L;
+  s_o[wave][lane] = o;
+  __syncthreads();
+  if (wave == 0) a.out[size_t(h) * HD + d] = ((s_o[0][lane] + s_o[1][lane]) + (s_o[2][lane] + s_o[3][lane])) / L;
 }
 
 }  // namespace
@@ -436,17 +453,17 @@ __global__ void __launch_bounds__(64) k_attn_merge(AttnArgs a) {
 void launch_attention_partial(const AttnArgs& a, hipStream_t st) {
   const dim3 grid(a.n_chunks, a.KV);
   const uint32_t gq = a.H / a.KV;
-  if (a.hd == 128 && gq == 8)  // fp16: 4 waves x 2 tiles; f32: 8 waves x 16 positions, 4 lanes per K row
-    a.kv_f16 ? launch_kernel(&k_attn_mfma<128, 8, 4, 2>, grid, dim3(256), st, a)
-             : launch_kernel(&k_attn_chunk<128, 8, float, 4, 8>, grid, dim3(512), st, a);
-  else if (a.hd == 256 && gq == 4)  // fp16: 2 waves x 2 tiles; f32: 4 waves x 16 positions
-    a.kv_f16 ? launch_kernel(&k_attn_mfma<256, 4, 2, 2>, grid, dim3(128), st, a)
-             : launch_kernel(&k_attn_chunk<256, 4, float, 4, 4>, grid, dim3(256), st, a);
+  if (a.hd == 128 && gq == 8)  // fp16: 4 waves x 1 tile; f32: 4 waves x 16 positions, 4 lanes per K row
+    a.kv_f16 ? launch_kernel(&k_attn_mfma<128, 8, 4, 1>, grid, dim3(256), st, a)
+             : launch_kernel(&k_attn_chunk<128, 8, float, 4, 4>, grid, dim3(256), st, a);
+  else if (a.hd == 256 && gq == 4)  // fp16: 2 waves x 1 tile; f32: 2 waves x 16 positions
+    a.kv_f16 ? launch_kernel(&k_attn_mfma<256, 4, 2, 1>, grid, dim3(128), st, a)
+             : launch_kernel(&k_attn_chunk<256, 4, float, 4, 2>, grid, dim3(128), st, a);
 }
 
 void launch_attention_combine(const AttnArgs& a, hipStream_t st) {
-  if (a.hd == 128) launch_kernel(&k_attn_merge<128>, dim3(a.H, 2), dim3(64), st, a);
-  else launch_kernel(&k_attn_merge<256>, dim3(a.H, 4), dim3(64), st, a);
+  if (a.hd == 128) launch_kernel(&k_attn_merge<128>, dim3(a.H, 2), dim3(64 * kMergeWaves), st, a);
+  else launch_kernel(&k_attn_merge<256>, dim3(a.H, 4), dim3(64 * kMergeWaves), st, a);
 }
 
 bool attention_supported(uint32_t H, uint32_t KV, uint32_t hd) {

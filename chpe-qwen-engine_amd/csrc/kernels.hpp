@@ -206,8 +206,8 @@ void launch_attention(const AttnArgs& a, hipStream_t stream);  // partial + comb
 void launch_attention_partial(const AttnArgs& a, hipStream_t stream);
 void launch_attention_combine(const AttnArgs& a, hipStream_t stream);
 void launch_finish(const FinishArgs& a, hipStream_t stream);
-constexpr uint32_t kAttnMaxChunks = 160;  // chunks of attn_chunk(hd) positions per launch
-__host__ __device__ constexpr uint32_t attn_chunk_of(uint32_t hd) { return 16384u / hd; }
+constexpr uint32_t kAttnMaxChunks = 320;  // chunks of attn_chunk(hd) positions per launch
+__host__ __device__ constexpr uint32_t attn_chunk_of(uint32_t hd) { return 8192u / hd; }
 inline uint32_t attn_chunk(uint32_t hd) { return attn_chunk_of(hd); }
 // (hd, query heads per kv head) pairs the attention kernels are built for
 bool attention_supported(uint32_t H, uint32_t KV, uint32_t hd);
