@@ -318,9 +318,9 @@ struct StageRegs {
 // branch-free: every slot loads (past the input: its first float4) and is masked when used, so
 // that the wait for these loads does not also wait for the weights issued after them
 // NT: the workgroup size when fixed at compile time (0: blockDim.x, an argument load)
-template <bool kNorm, int SL, int NT = 0>
+template <bool kNorm, int SL, int NT = 0, uint32_t CFIX = 0>
 __device__ __forceinline__ void stage_x_issue(const GemvArgs& a, StageRegs<SL>* r) {
-  const uint32_t C = a.C, tid = threadIdx.x, nt = NT ? uint32_t(NT) : blockDim.x;
+  const uint32_t C = CFIX ? CFIX : a.C, tid = threadIdx.x, nt = NT ? uint32_t(NT) : blockDim.x;
 #pragma unroll
   for (int k = 0; k < SL; ++k) {
     const uint32_t i = (tid + uint32_t(k) * nt) * 4, ic = i < C ? i : 0u;
@@ -332,10 +332,11 @@ __device__ __forceinline__ void stage_x_issue(const GemvArgs& a, StageRegs<SL>* 
 // kNorm: RMSNorm with the gains `gamma` (and the sum of squares, also the LM head's hidden norm);
 // kWide: the input may exceed the register slots (then two passes over LDS).  Both are
 // compile-time so that no runtime branch sits between the loads and their use.
-template <bool kNorm, bool kWide, int SL, int NT = 0>
+// (NT, CFIX: the workgroup size and the input length when fixed at compile time)
+template <bool kNorm, bool kWide, int SL, int NT = 0, uint32_t CFIX = 0>
 __device__ __forceinline__ void stage_x_finish(const GemvArgs& a, const StageRegs<SL>& r, float* s_x, float* s_red,
                                                float* ss, float* inv) {
-  const uint32_t C = a.C, tid = threadIdx.x, nt = NT ? uint32_t(NT) : blockDim.x;
+  const uint32_t C = CFIX ? CFIX : a.C, tid = threadIdx.x, nt = NT ? uint32_t(NT) : blockDim.x;
   const int lane = tid & 63, wave = tid >> 6;
   if constexpr (kWide) {  // two passes over LDS
     float q2 = 0.0f;
@@ -881,12 +882,20 @@ __global__ void __launch_bounds__(kWave * kCellWaves) k_gemv_cells(GemvArgs a) {
   // and scales of the lane's rows j and j + 4 (rows past the part read a row of it that exists
   // and count zero): unit rows 0..3 and 4..7 each lie in one cell (their first row is a
   // multiple of 4)
+  __builtin_assume(threadIdx.x < uint32_t(kWave * kCellWaves));
   StageRegs<2> xr;
-  stage_x_issue<kNorm, 2, kWave * kCellWaves>(a, &xr);
+  stage_x_issue<kNorm, 2, kWave * kCellWaves, 2048>(a, &xr);
   const uint32_t boff = wave * 256 + uint32_t(c) * 16, grp = wave * 4 + uint32_t(c >> 2);
   uint4 qA[UPW], qB[UPW];
   uint32_t sA[UPW], sB[UPW];
   bool okA[UPW], okB[UPW];
+  // per unit, uniform: the two cells, their first rows and row counts, the row base, the part's
+  // epilogue fields (kept for the epilogue wave of the unit)
+  const uint8_t* cellA_[UPW];
+  const uint8_t* cellB_[UPW];
+  uint32_t rowA_[UPW], rowB_[UPW], rowsA_[UPW], rowsB_[UPW], rbase_[UPW];
+  const float* src_[UPW];
+  uint32_t role_[UPW];
 #pragma unroll
   for (int u = 0; u < UPW; ++u) {
     const uint32_t unit = min(unit0 + u, a.n_units - 1);  // a unit past the end repeats the last, counting zero
@@ -902,36 +911,59 @@ __global__ void __launch_bounds__(kWave * kCellWaves) k_gemv_cells(GemvArgs a) {
     const uint8_t* cellB = P1.base + size_t(cB >> 4) * P1.stride;
     const uint32_t nA = (cA & 15u) + (rowA + j < P0.rows ? uint32_t(j) : 0u);
     const uint32_t nB = (cB & 15u) + (rowB + j < P1.rows ? uint32_t(j) : 0u);
-    // (a scalar cell base plus one 32-bit vector offset per load)
+    // (a scalar base plus one 32-bit vector offset per load; uni() keeps the constant in the
+    // scalar base, where the compiler would otherwise fold it into a 64-bit vector address)
+    const uint8_t* scA = uni(cellA + 16448 + 48);
+    const uint8_t* scB = uni(cellB + 16448 + 48);
     qA[u] = ld_u128(cellA + (64 + nA * 1024 + boff));
     qB[u] = ld_u128(cellB + (64 + nB * 1024 + boff));
-    sA[u] = ld_u16(cellA + (16448 + 48 + 2 * (nA * 16 + grp)));
-    sB[u] = ld_u16(cellB + (16448 + 48 + 2 * (nB * 16 + grp)));
+    sA[u] = ld_u16(scA + 2 * (nA * 16 + grp));
+    sB[u] = ld_u16(scB + 2 * (nB * 16 + grp));
+    cellA_[u] = cellA;
+    cellB_[u] = cellB;
+    rowA_[u] = live ? rowA : 0xffffffffu;  // (a unit past the end has no rows)
+    rowB_[u] = live ? rowB : 0xffffffffu;
+    rowsA_[u] = P0.rows;
+    rowsB_[u] = P1.rows;
+    rbase_[u] = row_base;
+    src_[u] = MODE == int(GemvMode::Accum) ? P0.y : P0.bias;
+    role_[u] = P0.rope_role;
   }
-  // the epilogue operands of unit `wave` (when wave < UPW): outlier k = lane % 8 of unit row i8
-  // (gemvTileW4 :404-410: the cell's 8 columns, the row's 8 weights); lane 8 i's residual or
-  // bias and RoPE factors
-  const uint32_t eunit = min(unit0 + (wave < uint32_t(UPW) ? wave : 0u), a.n_units - 1);
+  // the epilogue operands of unit `wave` (when wave < UPW), its uniform values selected above:
+  // outlier k = lane % 8 of unit row i8 (gemvTileW4 :404-410: the cell's 8 columns, the row's 8
+  // weights); lane 8 i's residual or bias and RoPE factors
+  const uint32_t ew = wave < uint32_t(UPW) ? wave : 0u;
+  const uint8_t* eA = cellA_[0];
+  const uint8_t* eB = cellB_[0];
+  uint32_t erA = rowA_[0], erB = rowB_[0], ersA = rowsA_[0], ersB = rowsB_[0], erow_base = rbase_[0], erole = role_[0];
+  const float* esrc = src_[0];
+#pragma unroll
+  for (int u = 1; u < UPW; ++u)
+    if (ew == uint32_t(u)) {
+      eA = cellA_[u]; eB = cellB_[u]; erA = rowA_[u]; erB = rowB_[u]; ersA = rowsA_[u]; ersB = rowsB_[u];
+      erow_base = rbase_[u]; esrc = src_[u]; erole = role_[u];
+    }
   const bool elive = wave < uint32_t(UPW) && unit0 + wave < a.n_units;
-  const GemvPart E0 = kRope ? pick_part(a, int(__builtin_amdgcn_readfirstlane(part_of(a, eunit)))) : a.part[0];
-  const GemvPart& E1 = kSwi ? a.part[1] : E0;
-  const uint32_t erow_base = cells_row_base<MODE>(E0, eunit, half);
-  const bool osecond = kSwi && i8 >= RU / 2;
+  const bool ohalf = i8 >= RU / 2;  // unit rows 4..7: the second cell
   const uint32_t orow = row_of<RU, MODE>(erow_base, i8, half);
-  const bool ovalid = elive && orow < (osecond ? E1.rows : E0.rows);
-  const uint32_t orr = ovalid ? orow : 0u;
-  const uint8_t* ocell = (osecond ? E1.base : E0.base) + size_t(orr >> 4) * (osecond ? E1.stride : E0.stride);
-  const uint32_t ocol = ld_u16(ocell + (16448 + 816 + 2 * uint32_t(lane & 7)));
-  const uint32_t ow = ld_u16(ocell + (16448 + 560 + 2 * ((orr & 15u) * 8 + uint32_t(lane & 7))));
+  const uint32_t ofirst = ohalf ? erB : erA, oi = uint32_t(i8 & 3), k8 = uint32_t(lane & 7);
+  const bool ovalid = elive && ofirst != 0xffffffffu && ofirst + oi < (ohalf ? ersB : ersA);
+  // every lane reads its outlier from both cells through scalar bases and keeps one
+  const uint8_t* oA = uni(eA + 16448);
+  const uint8_t* oB = uni(eB + 16448);
+  const uint32_t onA = erA != 0xffffffffu && erA + oi < ersA ? (erA & 15u) + oi : 0u;
+  const uint32_t onB = erB != 0xffffffffu && erB + oi < ersB ? (erB & 15u) + oi : 0u;
+  const uint32_t colA = ld_u16(oA + (816 + 2 * k8)), colB = ld_u16(oB + (816 + 2 * k8));
+  const uint32_t wA = ld_u16(oA + (560 + 2 * (onA * 8 + k8))), wB = ld_u16(oB + (560 + 2 * (onB * 8 + k8)));
+  const uint32_t ocol = ohalf ? colB : colA, ow = ohalf ? wB : wA;
   float pre = 0.0f, rc = 1.0f, rs = 0.0f;
   bool pre_ok = false, rope_ok = false;
   if constexpr (kPre) {
-    const float* src = MODE == int(GemvMode::Accum) ? E0.y : E0.bias;
-    pre_ok = elive && (lane % S) == 0 && orow < E0.rows && src != nullptr;
-    pre = (src ? src : a.x)[pre_ok ? orow : 0u];
+    pre_ok = elive && (lane % S) == 0 && orow < ersA && esrc != nullptr;
+    pre = (esrc ? esrc : a.x)[pre_ok ? orow : 0u];
   }
   if constexpr (kRope) {
-    rope_ok = elive && (lane % S) == 0 && lane < 32 && E0.rope_role != kRoleV;
+    rope_ok = elive && (lane % S) == 0 && lane < 32 && erole != kRoleV;
     const size_t at = rope_ok ? size_t(a.rope.state->pos) * half + (orow % (2 * half)) : 0u;
     rc = a.rope.cos[at];
     rs = a.rope.sin[at];
@@ -939,7 +971,7 @@ __global__ void __launch_bounds__(kWave * kCellWaves) k_gemv_cells(GemvArgs a) {
 
   // 2. the (normalised) input into LDS
   float ss = 0.0f, inv = 1.0f;
-  stage_x_finish<kNorm, false, 2, kWave * kCellWaves>(a, xr, s_x, s_red, &ss, &inv);
+  stage_x_finish<kNorm, false, 2, kWave * kCellWaves, 2048>(a, xr, s_x, s_red, &ss, &inv);
 
   // 3. per unit the lane's two 32-column dots, summed over the 16 lanes of each row, then over
   // the waves
@@ -988,7 +1020,12 @@ __global__ void __launch_bounds__(kWave * kCellWaves) k_gemv_cells(GemvArgs a) {
   float bv = -1e30f;
   uint32_t bi = 0xffffffffu, nf = 0;
   if (!elive) return;
+  // the epilogue's view of the unit's part (rows, output, KV role; base and stride unused)
+  GemvPart E0 = a.part[0];
+  E0.rows = ersA;
   if constexpr (kRope) {
+    E0.rope_role = erole;
+    E0.y = pick_part(a, int(__builtin_amdgcn_readfirstlane(part_of(a, min(unit0 + ew, a.n_units - 1))))).y;
     if ((lane % S) == 0 && i8 < RU / 2 && orow < E0.rows)
       rope_store(a, E0, orow, v + prev, up + up_pre, rope_ok ? rc : 1.0f, rope_ok ? rs : 0.0f);
   } else if ((lane % S) == 0 && (!kSwi || i8 < RU / 2)) {
