@@ -882,7 +882,6 @@ __global__ void __launch_bounds__(kWave * kCellWaves) k_gemv_cells(GemvArgs a) {
   // and scales of the lane's rows j and j + 4 (rows past the part read a row of it that exists
   // and count zero): unit rows 0..3 and 4..7 each lie in one cell (their first row is a
   // multiple of 4)
-  __builtin_assume(threadIdx.x < uint32_t(kWave * kCellWaves));
   StageRegs<2> xr;
   stage_x_issue<kNorm, 2, kWave * kCellWaves, 2048>(a, &xr);
   const uint32_t boff = wave * 256 + uint32_t(c) * 16, grp = wave * 4 + uint32_t(c >> 2);
@@ -1033,6 +1032,308 @@ __global__ void __launch_bounds__(kWave * kCellWaves) k_gemv_cells(GemvArgs a) {
   }
 }
 
+// ---- 16-row cells on the matrix cores --------------------------------------------------------
+// k_gemv_mma: the dense 4-bit products of the cell GEMVs at 2048 columns as exact integer matrix
+// products (v_mfma_i32_16x16x64_i8).  A tile is 16 rows -- 8 of part A and 8 of part B (SwiGlu:
+// 8 gate + 8 up rows; QkvRope: 8 RoPE pairs (r, r + head_dim/2); otherwise 16 consecutive rows)
+// -- and a workgroup runs UPW tiles on 4 waves of 512 columns (4 groups of 128) each.
+//
+// Input: lane l of wave w holds columns 512 w + 8 l .. + 7 of x' (x * gamma in the modes that
+// normalise: their 1/rms multiplies the row sums instead).  Per group (16 lanes) a power of two
+// 2^(30-e) with max |x'| < 2^e scales x' to integers X (|X| <= 2^30: exact for every element
+// within 2^7 of the group's largest, 2^(e-31) off otherwise), split into four signed bytes
+// (limbs: X = L0 + 2^8 L1 + 2^16 L2 + 2^24 L3), written to the wave's LDS table in the byte
+// order of the A operand.  A (lane (m, kq) = (lane % 16, lane / 16)): the 16 codes of row m at
+// 16 columns of each quarter kq of a group, the nibbles as bytes (two masks and a shift per 8
+// codes).  B column n = s + 4 limb holds limb `limb` of group slot s (zero in the products of the
+// other slots), so one accumulator collects the wave's 4 groups x 4 limbs; it starts at -8 * (the
+// limb summed over the group), the codes' offset, and stays exact: |sum (q - 8) L| <= 128 * 8 *
+// 128.  Row sums: the limbs weighted 2^(8 limb) and by 2^(e-30) and added on DPP (row_shr 4, 8,
+// 12), times the group scale, added over the 4 groups on DPP and over the waves in LDS (fixed
+// order).  Then wave e < 2 UPW takes half e % 2 of tile e / 2 (rows 4h..4h+3 of each part,
+// row i on lanes 8i..8i+7), adds the cell's outlier terms and runs the epilogue of the other
+// cell kernels.  The only workgroup barrier is the one before the epilogue.
+constexpr int kMmaWaves = 4;
+typedef int i32x4_t __attribute__((ext_vector_type(4)));
+
+// first rows of parts A and B of a tile (the tile's part already chosen)
+template <int MODE>
+__device__ __forceinline__ void mma_tile_rows(const GemvPart& P, uint32_t tile, uint32_t half, uint32_t* rA,
+                                              uint32_t* rB) {
+  if constexpr (MODE == int(GemvMode::SwiGlu)) {
+    *rA = *rB = tile * 8;
+  } else if constexpr (MODE == int(GemvMode::QkvRope)) {  // half / 8 tiles per head
+    const uint32_t tl = tile - P.unit_begin, per_head = half / 8;
+    *rA = (tl / per_head) * (2 * half) + (tl % per_head) * 8;
+    *rB = *rA + half;
+  } else {
+    *rA = (tile - P.unit_begin) * 16;
+    *rB = *rA + 8;
+  }
+}
+
+// the 4 x 4 byte transpose: w[k] = (a.k, b.k, c.k, d.k)
+__device__ __forceinline__ void limb_words(uint32_t a, uint32_t b, uint32_t c, uint32_t d, uint32_t* w) {
+  const uint32_t pab = __builtin_amdgcn_perm(b, a, 0x05010400u), qab = __builtin_amdgcn_perm(b, a, 0x07030602u);
+  const uint32_t pcd = __builtin_amdgcn_perm(d, c, 0x05010400u), qcd = __builtin_amdgcn_perm(d, c, 0x07030602u);
+  w[0] = __builtin_amdgcn_perm(pcd, pab, 0x05040100u);
+  w[1] = __builtin_amdgcn_perm(pcd, pab, 0x07060302u);
+  w[2] = __builtin_amdgcn_perm(qcd, qab, 0x05040100u);
+  w[3] = __builtin_amdgcn_perm(qcd, qab, 0x07060302u);
+}
+
+template <int MODE, int UPW>
+__global__ void __launch_bounds__(kWave * kMmaWaves) k_gemv_mma(GemvArgs a) {
+  constexpr bool kNorm = kNormOf<MODE>;
+  constexpr bool kSwi = MODE == int(GemvMode::SwiGlu);
+  constexpr bool kRope = MODE == int(GemvMode::QkvRope);
+  constexpr bool kPre = MODE == int(GemvMode::Store) || MODE == int(GemvMode::Accum) || kRope;
+  constexpr int S = 8;  // lanes per epilogue row
+  static_assert(MODE != int(GemvMode::Logits), "the LM head stays on k_gemv_rows");
+  static_assert(UPW == 1 || UPW == 2, "two epilogue waves per tile");
+  __shared__ __align__(16) float s_x[xs_floats(2048)];          // x' for the outlier terms
+  __shared__ __align__(16) uint4 s_b[kMmaWaves][4 * 4 * 2 * 4 + 1];  // B table per wave (+ a zero entry)
+  __shared__ int s_sx[kMmaWaves][4][4];                            // -8 * limb sums per group
+  __shared__ float s_e[kMmaWaves][4];                              // 2^(e - 30) per group
+  __shared__ __align__(16) float s_part[UPW][kMmaWaves][16];
+  __shared__ float s_red[kMmaWaves];
+  const int lane = threadIdx.x & 63, m = lane & 15, kq = lane >> 4, i8 = lane >> 3;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  args_batch<MODE>(a);
+  const uint32_t half = a.rope.head_dim / 2, tile0 = blockIdx.x * UPW;
+
+  // 1. loads: the position (QkvRope: the RoPE row of the epilogue depends on it), the input
+  // (columns c0 .. c0 + 7 of x and gamma), then the weights
+  const uint32_t rpos = kRope ? a.rope.state->pos : 0u;
+  const uint32_t c0 = wave * 512 + uint32_t(lane) * 8;
+  const float4 xa = ld_f4(a.x + c0), xb = ld_f4(a.x + c0 + 4);
+  float4 ga = make_float4(1.f, 1.f, 1.f, 1.f), gb = ga;
+  if constexpr (kNorm) {
+    ga = ld_f4(a.gamma + c0);
+    gb = ld_f4(a.gamma + c0 + 4);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  // per tile: lane m's row (A: m < 8, B: m >= 8), its codes in the wave's 4 groups, and the
+  // group scales of rows 4 kq .. 4 kq + 3 in the lane's readout slot (lane % 4); rows past a
+  // part read its row 0 and are dropped in the epilogue
+  uint4 q[UPW][4];
+  uint32_t sc[UPW][4];
+  const uint8_t* cA_[UPW];
+  const uint8_t* cB_[UPW];
+  uint32_t rA_[UPW], rB_[UPW], rowsA_[UPW], rowsB_[UPW], role_[UPW];
+  const float* src_[UPW];
+  float* y_[UPW];
+#pragma unroll
+  for (int u = 0; u < UPW; ++u) {
+    const uint32_t tile = min(tile0 + u, a.n_units - 1);
+    const bool live = tile0 + u < a.n_units;
+    const GemvPart PA = kRope ? pick_part(a, int(__builtin_amdgcn_readfirstlane(part_of(a, tile)))) : a.part[0];
+    const GemvPart& PB = kSwi ? a.part[1] : PA;
+    uint32_t rA, rB;
+    mma_tile_rows<MODE>(PA, tile, half, &rA, &rB);
+    const uint8_t* baseA = PA.base;
+    const uint8_t* baseB = PB.base;
+    const uint32_t rowsA = PA.rows, rowsB = PB.rows;
+    // the row's cell: rows rA .. rA + 7 share one (rA is a multiple of 8), as do rB ..
+    const uint8_t* cellA = baseA + size_t((rA < rowsA ? rA : 0u) >> 4) * PA.stride;
+    const uint8_t* cellB = baseB + size_t((rB < rowsB ? rB : 0u) >> 4) * PB.stride;
+    const bool inB = m >= 8;
+    const uint32_t r = (inB ? rB : rA) + uint32_t(m & 7);
+    const uint32_t nrow = r < (inB ? rowsB : rowsA) ? (r & 15u) : 0u;
+    const uint8_t* cell = inB ? cellB : cellA;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) q[u][g] = ld_u128(cell + (64 + nrow * 1024 + (wave * 4 + g) * 64 + uint32_t(kq) * 16));
+    // readout rows 4 kq + j of the tile: part A for kq < 2
+    const bool sB = kq >= 2;
+    const uint32_t rs = (sB ? rB : rA) + 4 * uint32_t(kq & 1);
+    const uint8_t* csv = sB ? cellB : cellA;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t rr = rs + j;
+      const uint32_t nn = rr < (sB ? rowsB : rowsA) ? (rr & 15u) : 0u;
+      sc[u][j] = ld_u16(csv + (16448 + 48 + 2 * (nn * 16 + wave * 4 + uint32_t(lane & 3))));
+    }
+    cA_[u] = cellA;
+    cB_[u] = cellB;
+    rA_[u] = live ? rA : 0xffffffffu;
+    rB_[u] = live ? rB : 0xffffffffu;
+    rowsA_[u] = rowsA;
+    rowsB_[u] = rowsB;
+    role_[u] = PA.rope_role;
+    src_[u] = MODE == int(GemvMode::Accum) ? PA.y : PA.bias;
+    y_[u] = PA.y;
+  }
+  // the epilogue operands of wave e < 2 UPW: half eh = e % 2 of tile eu = e / 2; lane 8 i + k:
+  // outlier k of the row on lanes 8 i.. (i < 4: part A row 4 eh + i; i >= 4: part B row 4 eh + i - 4),
+  // lane 8 i's residual or bias and RoPE factors
+  const uint32_t ew = wave < uint32_t(2 * UPW) ? wave : 0u, eu = ew >> 1, eh = ew & 1u;
+  const uint8_t* eA = cA_[0];
+  const uint8_t* eB = cB_[0];
+  uint32_t erA = rA_[0], erB = rB_[0], ersA = rowsA_[0], ersB = rowsB_[0], erole = role_[0];
+  const float* esrc = src_[0];
+  float* ey = y_[0];
+  if constexpr (UPW == 2) {
+    if (eu == 1u) {
+      eA = cA_[1]; eB = cB_[1]; erA = rA_[1]; erB = rB_[1]; ersA = rowsA_[1]; ersB = rowsB_[1];
+      erole = role_[1]; esrc = src_[1]; ey = y_[1];
+    }
+  }
+  const bool elive = wave < uint32_t(2 * UPW) && tile0 + eu < a.n_units;
+  const bool oB = i8 >= 4;
+  const uint32_t efirst = oB ? erB : erA, erows = oB ? ersB : ersA;
+  const uint32_t orow = efirst + 4 * eh + uint32_t(i8 & 3);
+  const bool ovalid = elive && efirst != 0xffffffffu && orow < erows;
+  const uint8_t* ocell = oB ? eB : eA;
+  const uint32_t on = ovalid ? (orow & 15u) : 0u, k8 = uint32_t(lane & 7);
+  const uint32_t ocol = ld_u16(ocell + (16448 + 816 + 2 * k8));
+  const uint32_t ow = ld_u16(ocell + (16448 + 560 + 2 * (on * 8 + k8)));
+  float pre = 0.0f, rc = 1.0f, rs = 0.0f;
+  bool pre_ok = false, rope_ok = false;
+  if constexpr (kPre) {
+    pre_ok = ovalid && (lane % S) == 0 && esrc != nullptr;
+    pre = (esrc ? esrc : a.x)[pre_ok ? orow : 0u];
+  }
+  if constexpr (kRope) {  // the pair's dimension: (first row of part A mod head_dim) + 4 eh + i < half
+    rope_ok = ovalid && (lane % S) == 0 && !oB && erole != kRoleV;
+    const uint32_t fa = erA != 0xffffffffu ? erA : 0u, dA = fa - (fa / (2 * half)) * (2 * half);
+    const size_t at = size_t(rpos) * half + (dA + 4 * eh + uint32_t(i8 & 3));
+    rc = a.rope.cos[at];
+    rs = a.rope.sin[at];
+  }
+
+  __builtin_amdgcn_sched_barrier(0);  // every load above is issued before the input is used
+
+  // 2. the wave's B table: x' as three signed bytes per column, the group's exponent and limb
+  // sums (wave-local: written and read by this wave only)
+  const float xv[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+  const float gv[8] = {ga.x, ga.y, ga.z, ga.w, gb.x, gb.y, gb.z, gb.w};
+  float xp[8], q2 = 0.0f, mx = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    xp[i] = kNorm ? xv[i] * gv[i] : xv[i];
+    q2 = fmaf(xv[i], xv[i], q2);
+    mx = fmaxf(mx, fabsf(xp[i]));
+  }
+  mx = pair_max(mx, 1);
+  mx = pair_max(mx, 2);
+  mx = pair_max(mx, 4);
+  mx = pair_max(mx, 8);
+  int e = 0;
+  (void)frexpf(mx, &e);  // mx < 2^e (mx = 0: e = 0)
+  const float up = ldexpf(1.0f, 30 - e);
+  uint32_t z[8];  // bytes: the balanced limbs of X
+#pragma unroll
+  for (int i = 0; i < 8; ++i) z[i] = (uint32_t(int(rintf(xp[i] * up))) + 0x808080u) ^ 0x808080u;
+  uint32_t lo[4], hi[4];
+  limb_words(z[0], z[2], z[4], z[6], lo);
+  limb_words(z[1], z[3], z[5], z[7], hi);
+  const uint32_t gs = uint32_t(lane) >> 4, gkq = (uint32_t(lane) >> 2) & 3u, gh = (uint32_t(lane) >> 1) & 1u;
+  uint2* tb = reinterpret_cast<uint2*>(&s_b[wave][0]);
+  float lsum[4];
+#pragma unroll
+  for (int L = 0; L < 4; ++L) {
+    tb[(((gs * 4 + gkq) * 2 + gh) * 4 + L) * 2 + (lane & 1)] = make_uint2(lo[L], hi[L]);
+    lsum[L] = float(__builtin_amdgcn_sdot4(int(lo[L]), 0x01010101, __builtin_amdgcn_sdot4(int(hi[L]), 0x01010101, 0, false), false));
+    lsum[L] = pair_sum(lsum[L], 1);
+    lsum[L] = pair_sum(lsum[L], 2);
+    lsum[L] = pair_sum(lsum[L], 4);
+    lsum[L] = pair_sum(lsum[L], 8);
+  }
+  if ((lane & 15) == 0) {
+#pragma unroll
+    for (int L = 0; L < 4; ++L) s_sx[wave][gs][L] = -8 * int(lsum[L]);
+    s_e[wave][gs] = isfinite(mx) ? ldexpf(1.0f, e - 30) : __int_as_float(0x7fc00000);  // NaN / inf propagate
+  }
+  if (lane == 0) s_b[wave][4 * 4 * 2 * 4] = make_uint4(0, 0, 0, 0);
+  *reinterpret_cast<float4*>(s_x + xs_at(c0)) = make_float4(xp[0], xp[1], xp[2], xp[3]);
+  *reinterpret_cast<float4*>(s_x + xs_at(c0) + 4) = make_float4(xp[4], xp[5], xp[6], xp[7]);
+  if constexpr (kNorm) {
+    q2 = wave_sum(q2);
+    if (lane == 0) s_red[wave] = q2;
+  }
+  __builtin_amdgcn_wave_barrier();  // (one wave's LDS accesses execute in order)
+  // lane (n = m, kq): column n = s + 4 limb of B
+  const uint32_t bs = uint32_t(m & 3), bl = uint32_t(m >> 2);
+  i32x4_t B[4][2];
+#pragma unroll
+  for (int s = 0; s < 4; ++s)
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const uint32_t ent = bs == uint32_t(s) ? ((uint32_t(s) * 4 + uint32_t(kq)) * 2 + uint32_t(h)) * 4 + bl
+                                             : uint32_t(4 * 4 * 2 * 4);
+      const uint4 t = s_b[wave][ent];
+      B[s][h] = i32x4_t{int(t.x), int(t.y), int(t.z), int(t.w)};
+    }
+  const int cinit = s_sx[wave][bs][bl];
+  const float lpf = s_e[wave][bs] * __int_as_float(int(127 + 8 * bl) << 23);  // * 2^(8 limb)
+
+  // 3. per tile: 8 products (4 groups x 2 halves of 64 columns), the row sums of the wave
+#pragma unroll
+  for (int u = 0; u < UPW; ++u) {
+    i32x4_t D = {cinit, cinit, cinit, cinit};
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const uint32_t w[4] = {q[u][g].x, q[u][g].y, q[u][g].z, q[u][g].w};
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const uint32_t w0 = w[2 * h], w1 = w[2 * h + 1];
+        const i32x4_t A = {int(w0 & 0x0f0f0f0fu), int((w0 >> 4) & 0x0f0f0f0fu), int(w1 & 0x0f0f0f0fu),
+                           int((w1 >> 4) & 0x0f0f0f0fu)};
+        D = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, B[g][h], D, 0, 0, 0);
+      }
+    }
+    float t[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float f = float(D[j]) * lpf;
+      // lanes 12..15 of the row: + the limbs of lanes n - 4, n - 8, n - 12 (row_shr)
+      const float v = ((f + dpp_f<0x114>(f)) + dpp_f<0x118>(f)) + dpp_f<0x11c>(f);
+      t[j] = v * h2f(uint16_t(sc[u][j]));
+      t[j] = pair_sum(t[j], 1);
+      t[j] = pair_sum(t[j], 2);  // the 4 groups
+    }
+    if (m == 12) *reinterpret_cast<float4*>(&s_part[u][wave][4 * kq]) = make_float4(t[0], t[1], t[2], t[3]);
+  }
+  __syncthreads();
+  if (wave >= uint32_t(2 * UPW)) return;
+
+  // 4. wave e: rows of its tile half, the outlier terms, 1/rms, the epilogue
+  const uint32_t tr = oB ? 8 + 4 * eh + uint32_t(i8 - 4) : 4 * eh + uint32_t(i8);
+  float v = 0.0f;
+#pragma unroll
+  for (int w = 0; w < kMmaWaves; ++w) v += s_part[eu][w][tr];
+  float o = (ovalid && ocol < 2048u) ? half_lo(ow) * s_x[xs_at(ocol < 2048u ? ocol : 0u)] : 0.0f;
+  o = pair_sum(o, 1);
+  o = pair_sum(o, 2);
+  o = pair_sum(o, 4);
+  v += o;
+  if constexpr (kNorm) {
+    float ss = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kMmaWaves; ++w) ss += s_red[w];
+    v *= 1.0f / sqrtf(ss / 2048.0f + a.eps);
+  }
+  const float upv = (kSwi || kRope) ? pair_val(v, 32) : 0.0f;
+  const float prev = pre_ok ? pre : 0.0f;
+  const float up_pre = kRope ? pair_val(prev, 32) : 0.0f;
+  float bv = -1e30f;
+  uint32_t bi = 0xffffffffu, nf = 0;
+  if (!elive) return;
+  GemvPart E0 = a.part[0];
+  E0.rows = ersA;
+  E0.y = ey;
+  if constexpr (kRope) {
+    E0.rope_role = erole;
+    if ((lane % S) == 0 && !oB && ovalid)
+      rope_store(a, E0, orow, v + prev, upv + up_pre, rope_ok ? rc : 1.0f, rope_ok ? rs : 0.0f);
+  } else if constexpr (kSwi) {
+    if ((lane % S) == 0 && !oB && ovalid) epilogue<MODE>(E0, orow, v, upv, prev, &bv, &bi, &nf);
+  } else {
+    E0.rows = erows;
+    if ((lane % S) == 0 && ovalid) epilogue<MODE>(E0, orow, v, upv, prev, &bv, &bi, &nf);
+  }
+}
+
 // Flat 4-bit tiles (gemvCellFlat: the down projection, and every projection wider than 2048
 // columns), K-split: one workgroup = one unit of RU = 8 rows, kFlatWaves = 8 waves (two per
 // SIMD) striding over panels of 512 columns (4 groups of 128; panel p goes to wave p % 8).
@@ -1043,17 +1344,19 @@ __global__ void __launch_bounds__(kWave * kCellWaves) k_gemv_cells(GemvArgs a) {
 // corrections and runs the epilogue.  The input sits in LDS (dynamic, C floats) for the dots
 // and for the corrections, which read any column.
 constexpr int kFlatWaves = 8;
-template <int MODE, int MAXP, bool kWide>
-__global__ void __launch_bounds__(kWave * kFlatWaves) k_gemv_flat(GemvArgs a) {
-  constexpr int RU = 8, S = kWave / RU, NT = kWave * kFlatWaves;
+template <int MODE, int MAXP, bool kWide, int W = kFlatWaves>
+__global__ void __launch_bounds__(kWave * W) k_gemv_flat(GemvArgs a) {
+  constexpr int RU = 8, S = kWave / RU, NT = kWave * W;
+  // input float4 slots per thread: C <= MAXP * W * 512 columns, so 2 * MAXP suffice
+  constexpr int SL = kWide ? 1 : (2 * MAXP < 8 ? 2 * MAXP : 8);
   constexpr bool kNorm = kNormOf<MODE>;
   constexpr bool kSwi = MODE == int(GemvMode::SwiGlu);
   constexpr bool kRope = MODE == int(GemvMode::QkvRope);
   constexpr bool kPre = MODE == int(GemvMode::Store) || MODE == int(GemvMode::Accum) || kRope;
   static_assert(MODE != int(GemvMode::Logits), "the flat LM head stays on k_gemv_split");
   extern __shared__ __align__(16) float s_x[];  // xs_floats(C) floats
-  __shared__ float s_part[kFlatWaves][RU];
-  __shared__ float s_red[kFlatWaves];
+  __shared__ float s_part[W][RU];
+  __shared__ float s_red[W];
   const int lane = threadIdx.x & 63, j = lane >> 4, c = lane & 15;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   args_batch<MODE>(a);
@@ -1063,8 +1366,8 @@ __global__ void __launch_bounds__(kWave * kFlatWaves) k_gemv_flat(GemvArgs a) {
   const uint32_t row_base = cells_row_base<MODE>(P0, unit, half);
 
   // 1. the input first, then codes and scales of rows j and j + 4 for each of the wave's panels
-  StageRegs<8> xr;
-  if constexpr (!kWide) stage_x_issue<kNorm, 8, NT>(a, &xr);
+  StageRegs<SL> xr;
+  if constexpr (!kWide) stage_x_issue<kNorm, SL, NT>(a, &xr);
   const uint32_t rowA = row_of<RU, MODE>(row_base, j, half), rowB = row_of<RU, MODE>(row_base, j + RU / 2, half);
   const bool okA = rowA < P0.rows, okB = rowB < P1.rows;
   // 32-bit group indices and byte offsets from the part's base (a uniform 64-bit pointer), so
@@ -1077,7 +1380,7 @@ __global__ void __launch_bounds__(kWave * kFlatWaves) k_gemv_flat(GemvArgs a) {
   uint32_t sa[MAXP], sb[MAXP], gvm = 0;
 #pragma unroll
   for (int q = 0; q < MAXP; ++q) {
-    const uint32_t p = wave + kFlatWaves * uint32_t(q), g = 4 * p + uint32_t(c >> 2);
+    const uint32_t p = wave + W * uint32_t(q), g = 4 * p + uint32_t(c >> 2);
     const bool gv = p < npan && g < ng;
     gvm |= uint32_t(gv) << q;
     const uint32_t Ga = GA + (gv ? g : 0u), Gb = GB + (gv ? g : 0u);
@@ -1111,13 +1414,13 @@ __global__ void __launch_bounds__(kWave * kFlatWaves) k_gemv_flat(GemvArgs a) {
 
   // 2. the (normalised) input into LDS
   float ss = 0.0f, inv = 1.0f;
-  stage_x_finish<kNorm, kWide, 8, NT>(a, xr, s_x, s_red, &ss, &inv);
+  stage_x_finish<kNorm, kWide, SL, NT>(a, xr, s_x, s_red, &ss, &inv);
 
   // 3. the dots of the wave's panels, summed over the 16 lanes of each row, then over the waves
   float accA = 0.0f, accB = 0.0f;
 #pragma unroll
   for (int q = 0; q < MAXP; ++q) {
-    const uint32_t p = wave + kFlatWaves * uint32_t(q);
+    const uint32_t p = wave + W * uint32_t(q);
     const bool gv = (gvm >> q) & 1u;
     const uint32_t col0 = gv ? 512 * p + 32 * uint32_t(c) : 0u;
     float xv[32];
@@ -1151,7 +1454,7 @@ __global__ void __launch_bounds__(kWave * kFlatWaves) k_gemv_flat(GemvArgs a) {
   // 4. wave 0: row i8 on lanes 8 i8 .. 8 i8 + 7, its corrections, the epilogue
   float v = 0.0f;
 #pragma unroll
-  for (int w = 0; w < kFlatWaves; ++w) v += s_part[w][i8];
+  for (int w = 0; w < W; ++w) v += s_part[w][i8];
   v += flat_correction(fe, s_x);
   const float up = (kSwi || kRope) ? pair_val(v, 32) : 0.0f;
   const float prev = pre_ok ? pre : 0.0f;
@@ -1170,6 +1473,8 @@ template <class F, int MODE>
 void launch_one(const GemvArgs& a, const GemvLaunch& g, hipStream_t st) {
   const size_t lds = size_t(xs_floats(a.C)) * 4;
   if constexpr (std::is_same_v<F, Cell16W4> && MODE != int(GemvMode::Logits)) {
+    if (g.mma == 1) { launch_kernel(&k_gemv_mma<MODE, 1>, dim3(g.blocks), dim3(g.threads), st, a); return; }
+    if (g.mma == 2) { launch_kernel(&k_gemv_mma<MODE, 2>, dim3(g.blocks), dim3(g.threads), st, a); return; }
     if (g.cells == 1) { launch_kernel(&k_gemv_cells<MODE, 1>, dim3(g.blocks), dim3(g.threads), st, a); return; }
     if (g.cells == 2) { launch_kernel(&k_gemv_cells<MODE, 2>, dim3(g.blocks), dim3(g.threads), st, a); return; }
     if (g.cells == 4) { launch_kernel(&k_gemv_cells<MODE, 4>, dim3(g.blocks), dim3(g.threads), st, a); return; }
@@ -1218,6 +1523,7 @@ const GemvTuning& gemv_tuning() {
     if (const char* e = std::getenv("CHPE_GEMV_LOGITS_BLOCKS")) v.logits_blocks = uint32_t(std::strtoul(e, nullptr, 10));
     if (const char* e = std::getenv("CHPE_GEMV_CELLS")) v.cells = uint32_t(std::strtoul(e, nullptr, 10));
     if (const char* e = std::getenv("CHPE_GEMV_FLAT")) v.flat = uint32_t(std::strtoul(e, nullptr, 10));
+    if (const char* e = std::getenv("CHPE_GEMV_MMA")) v.mma = uint32_t(std::strtoul(e, nullptr, 10));
     if (v.logits_blocks == 0 || v.logits_blocks > kMaxLogitsBlocks) v.logits_blocks = kMaxLogitsBlocks;
     return v;
   }();
@@ -1252,7 +1558,27 @@ GemvLaunch gemv_geometry(WeightKind kind, GemvMode mode, uint32_t C, const uint3
   *n_units = units;
   GemvLaunch g{};
   g.ru = ru;
-  if (kind == WeightKind::Cell16W4 && mode != GemvMode::Logits && C == 2048 && gemv_tuning().cells) {
+  bool rope_tiles = true;  // QkvRope tiles pair rows r, r + head_dim/2 in 8s: parts of whole 16-row heads
+  for (int p = 0; p < n_parts; ++p) rope_tiles = rope_tiles && rows[p] % 16 == 0;
+  if (kind == WeightKind::Cell16W4 && mode != GemvMode::Logits && C == 2048 && gemv_tuning().mma &&
+      (mode != GemvMode::QkvRope || rope_tiles)) {
+    // matrix-core kernel: tiles of 16 rows (SwiGlu: 8 gate + 8 up rows), UPW tiles per workgroup
+    uint32_t tiles = 0;
+    if (mode == GemvMode::SwiGlu) {
+      tiles = (rows[0] + 7) / 8;
+      unit_begin[0] = unit_begin[1] = 0;
+    } else {
+      for (int p = 0; p < n_parts; ++p) {
+        unit_begin[p] = tiles;
+        tiles += (rows[p] + 15) / 16;
+      }
+    }
+    *n_units = tiles;
+    const uint32_t upw = tiles >= 1024 && gemv_tuning().mma == 2 ? 2u : 1u;
+    g.mma = upw;
+    g.threads = kWave * kMmaWaves;
+    g.blocks = (tiles + upw - 1) / upw;
+  } else if (kind == WeightKind::Cell16W4 && mode != GemvMode::Logits && C == 2048 && gemv_tuning().cells) {
     // K-split over kCellWaves waves; units per workgroup: 1 for the small projections (more
     // workgroups, more parallel dot work), up to the tuning cap when there are thousands
     uint32_t upw = units >= 2048 ? gemv_tuning().cells : 1u;

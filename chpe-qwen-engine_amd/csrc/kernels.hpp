@@ -112,6 +112,7 @@ struct GemvLaunch {  // launch geometry of one GemvArgs
   uint32_t blocks, threads, ru;
   uint32_t cells;  // > 0: the K-split kernel for 16-row cells at 2048 columns, `cells` units per workgroup
   uint32_t flat;   // > 0: the K-split kernel for flat 4-bit tiles, up to `flat` panels per wave
+  uint32_t mma;    // > 0: the matrix-core kernel for 16-row cells at 2048 columns, `mma` tiles per workgroup
 };
 
 struct StepState {  // device-resident per-token state read by the captured step
@@ -165,6 +166,8 @@ struct GemvTuning {
   uint32_t cells = 2;  // units per workgroup of the K-split cell kernel when a launch has >= 2048 units
                        // (1, 2 or 4); CHPE_GEMV_CELLS=0: the one-unit-per-wave kernel instead
   uint32_t flat = 1;   // CHPE_GEMV_FLAT=0: flat 4-bit tiles on the one-workgroup-per-unit K-split by panels
+  uint32_t mma = 1;    // 16-row cells at 2048 columns on the matrix-core kernel, 1 or 2 tiles per
+                       // workgroup of a launch with >= 1024 tiles (CHPE_GEMV_MMA; 0: off)
 };
 const GemvTuning& gemv_tuning();
 

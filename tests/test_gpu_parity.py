@@ -259,6 +259,13 @@ def test_c_abi_semantics(w4_archive):
 
 
 def test_kv_f16_matches_oracle_kv_f16(w4_archive):
+    """fp16 KV cache against the oracle's fp16-cache mode.  Every k / v element is rounded to
+    fp16, and an element whose f32 value differs from the oracle's in the last bits (another
+    summation order) can round to the neighbouring fp16 value: a 2^-11 relative step that the
+    following layers carry to the logits.  With the f32 cache the same steps agree to ~2e-5
+    (test_decode_steps_match_oracle); with the fp16 cache the rounding flips leave ~1-3e-3 on
+    logits of magnitude ~4 (measured at these positions: 1.3e-3 for the vector-ALU cell kernel,
+    2.5e-3 for the matrix-core one).  Bounds: max 5e-3, rms 1e-3, cos 0.9999, same argmax."""
     e = ca.Engine(w4_archive, arch=0, max_seq_len=16, kv_f16=True)
     o = orc.Oracle(w4_archive, arch=0, max_seq_len=16, kv_f16=True, threads=16)
     try:
@@ -266,7 +273,10 @@ def test_kv_f16_matches_oracle_kv_f16(w4_archive):
             say(f"kv f16 pos={pos}")
             am, lg = e.decode_step(tok, pos)
             r = o.forward(tok, pos)
-            compare_step(lg, o.logits(), pos)
+            ol = o.logits()
+            d = np.abs(lg.astype(np.float64) - ol)
+            cos = float(lg.astype(np.float64) @ ol / np.linalg.norm(lg) / np.linalg.norm(ol))
+            assert d.max() <= 5e-3 and np.sqrt(np.mean(d * d)) <= 1e-3 and cos >= 0.9999, (pos, float(d.max()), cos)
             assert am == r.argmax_token
     finally:
         e.close()
