@@ -166,7 +166,7 @@ struct GemvTuning {
   uint32_t cells = 2;  // units per workgroup of the K-split cell kernel when a launch has >= 2048 units
                        // (1, 2 or 4); CHPE_GEMV_CELLS=0: the one-unit-per-wave kernel instead
   uint32_t flat = 1;   // CHPE_GEMV_FLAT=0: flat 4-bit tiles on the one-workgroup-per-unit K-split by panels
-  uint32_t mma = 1;    // 16-row cells at 2048 columns on the matrix-core kernel, 1 or 2 tiles per
+  uint32_t mma = 2;    // 16-row cells at 2048 columns on the matrix-core kernel, 1 or 2 tiles per
                        // workgroup of a launch with >= 1024 tiles (CHPE_GEMV_MMA; 0: off)
 };
 const GemvTuning& gemv_tuning();
