@@ -1034,9 +1034,10 @@ __global__ void __launch_bounds__(kWave * kCellWaves) k_gemv_cells(GemvArgs a) {
 
 // ---- 16-row cells on the matrix cores --------------------------------------------------------
 // k_gemv_mma: the dense 4-bit products of the cell GEMVs at 2048 columns as exact integer matrix
-// products (v_mfma_i32_16x16x64_i8).  A tile is 16 rows -- 8 of part A and 8 of part B (SwiGlu:
-// 8 gate + 8 up rows; QkvRope: 8 RoPE pairs (r, r + head_dim/2); otherwise 16 consecutive rows)
-// -- and a workgroup runs UPW tiles on 4 waves of 512 columns (4 groups of 128) each.
+// products (v_mfma_i32_16x16x64_i8).  A tile is 16 rows in two halves of 8 (QkvRope: 8 RoPE
+// pairs (r, r + head_dim/2); otherwise one cell, rows 0..7 and 8..15) and a workgroup runs UPW
+// tiles on 4 waves of 512 columns (4 groups of 128) each; a SwiGlu workgroup takes the gate cell
+// and the up cell of the same 16 rows as its two tiles.
 //
 // Input: lane l of wave w holds columns 512 w + 8 l .. + 7 of x' (x * gamma in the modes that
 // normalise: their 1/rms multiplies the row sums instead).  Per group (16 lanes) a power of two
@@ -1056,13 +1057,12 @@ __global__ void __launch_bounds__(kWave * kCellWaves) k_gemv_cells(GemvArgs a) {
 constexpr int kMmaWaves = 4;
 typedef int i32x4_t __attribute__((ext_vector_type(4)));
 
-// first rows of parts A and B of a tile (the tile's part already chosen)
+// first rows of the two 8-row halves of a tile (the tile's part already chosen; SwiGlu tiles are
+// whole cells of the gate and the up projection, see k_gemv_mma)
 template <int MODE>
 __device__ __forceinline__ void mma_tile_rows(const GemvPart& P, uint32_t tile, uint32_t half, uint32_t* rA,
                                               uint32_t* rB) {
-  if constexpr (MODE == int(GemvMode::SwiGlu)) {
-    *rA = *rB = tile * 8;
-  } else if constexpr (MODE == int(GemvMode::QkvRope)) {  // half / 8 tiles per head
+  if constexpr (MODE == int(GemvMode::QkvRope)) {  // half / 8 tiles per head
     const uint32_t tl = tile - P.unit_begin, per_head = half / 8;
     *rA = (tl / per_head) * (2 * half) + (tl % per_head) * 8;
     *rB = *rA + half;
@@ -1091,6 +1091,7 @@ __global__ void __launch_bounds__(kWave * kMmaWaves) k_gemv_mma(GemvArgs a) {
   constexpr int S = 8;  // lanes per epilogue row
   static_assert(MODE != int(GemvMode::Logits), "the LM head stays on k_gemv_rows");
   static_assert(UPW == 1 || UPW == 2, "two epilogue waves per tile");
+  static_assert(!kSwi || UPW == 2, "a SwiGlu workgroup holds the gate and the up cell");
   __shared__ __align__(16) float s_x[xs_floats(2048)];          // x' for the outlier terms
   __shared__ __align__(16) uint4 s_b[kMmaWaves][4 * 4 * 2 * 4 + 1];  // B table per wave (+ a zero entry)
   __shared__ int s_sx[kMmaWaves][4][4];                            // -8 * limb sums per group
@@ -1113,80 +1114,89 @@ __global__ void __launch_bounds__(kWave * kMmaWaves) k_gemv_mma(GemvArgs a) {
     gb = ld_f4(a.gamma + c0 + 4);
   }
   __builtin_amdgcn_sched_barrier(0);
-  // per tile: lane m's row (A: m < 8, B: m >= 8), its codes in the wave's 4 groups, and the
-  // group scales of rows 4 kq .. 4 kq + 3 in the lane's readout slot (lane % 4); rows past a
-  // part read its row 0 and are dropped in the epilogue
+  // per tile: where its two 8-row halves sit -- part A's cell (a uniform base), the halves'
+  // rows in their cells and the byte distance to the second half's cell -- then lane m's codes
+  // (A half: m < 8) in the wave's 4 groups and the group scales of rows 4 kq .. 4 kq + 3 in the
+  // lane's readout slot (lane % 4).  Every address is that base plus one 32-bit lane offset.
+  // Rows past a part read bytes of its last cell and are dropped in the epilogue.
   uint4 q[UPW][4];
   uint32_t sc[UPW][4];
   const uint8_t* cA_[UPW];
-  const uint8_t* cB_[UPW];
-  uint32_t rA_[UPW], rB_[UPW], rowsA_[UPW], rowsB_[UPW], role_[UPW];
+  uint32_t dB_[UPW], nA_[UPW], nB_[UPW], rA_[UPW], rB_[UPW], rows_[UPW], role_[UPW];
   const float* src_[UPW];
   float* y_[UPW];
 #pragma unroll
   for (int u = 0; u < UPW; ++u) {
-    const uint32_t tile = min(tile0 + u, a.n_units - 1);
-    const bool live = tile0 + u < a.n_units;
-    const GemvPart PA = kRope ? pick_part(a, int(__builtin_amdgcn_readfirstlane(part_of(a, tile)))) : a.part[0];
-    const GemvPart& PB = kSwi ? a.part[1] : PA;
-    uint32_t rA, rB;
-    mma_tile_rows<MODE>(PA, tile, half, &rA, &rB);
-    const uint8_t* baseA = PA.base;
-    const uint8_t* baseB = PB.base;
-    const uint32_t rowsA = PA.rows, rowsB = PB.rows;
-    // the row's cell: rows rA .. rA + 7 share one (rA is a multiple of 8), as do rB ..
-    const uint8_t* cellA = baseA + size_t((rA < rowsA ? rA : 0u) >> 4) * PA.stride;
-    const uint8_t* cellB = baseB + size_t((rB < rowsB ? rB : 0u) >> 4) * PB.stride;
-    const bool inB = m >= 8;
-    const uint32_t r = (inB ? rB : rA) + uint32_t(m & 7);
-    const uint32_t nrow = r < (inB ? rowsB : rowsA) ? (r & 15u) : 0u;
-    const uint8_t* cell = inB ? cellB : cellA;
-#pragma unroll
-    for (int g = 0; g < 4; ++g) q[u][g] = ld_u128(cell + (64 + nrow * 1024 + (wave * 4 + g) * 64 + uint32_t(kq) * 16));
-    // readout rows 4 kq + j of the tile: part A for kq < 2
-    const bool sB = kq >= 2;
-    const uint32_t rs = (sB ? rB : rA) + 4 * uint32_t(kq & 1);
-    const uint8_t* csv = sB ? cellB : cellA;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const uint32_t rr = rs + j;
-      const uint32_t nn = rr < (sB ? rowsB : rowsA) ? (rr & 15u) : 0u;
-      sc[u][j] = ld_u16(csv + (16448 + 48 + 2 * (nn * 16 + wave * 4 + uint32_t(lane & 3))));
+    uint32_t tile, rA, rB;
+    bool live;
+    GemvPart PA;
+    if constexpr (kSwi) {  // workgroup = one unit: the gate cell (u = 0) and the up cell (u = 1)
+      tile = blockIdx.x;
+      live = true;
+      PA = a.part[u];
+      rA = tile * 16;
+      rB = rA + 8;
+    } else {
+      tile = min(tile0 + u, a.n_units - 1);
+      live = tile0 + u < a.n_units;
+      PA = kRope ? pick_part(a, int(__builtin_amdgcn_readfirstlane(part_of(a, tile)))) : a.part[0];
+      mma_tile_rows<MODE>(PA, tile, half, &rA, &rB);
     }
+    const uint32_t rows = PA.rows, ca = rA >> 4, cb = rB < rows ? rB >> 4 : ca;  // (rA < rows)
+    const uint8_t* cellA = PA.base + size_t(ca) * PA.stride;
+    const uint32_t dB = (cb - ca) * PA.stride, nA0 = rA & 15u, nB0 = rB & 15u;
+    const uint32_t vrow = m < 8 ? (nA0 + uint32_t(m)) * 1024u : dB + (nB0 + uint32_t(m - 8)) * 1024u;
+    const uint8_t* cbase = uni(cellA + 64 + wave * 256);
+    const uint32_t vo = vrow + uint32_t(kq) * 16;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) q[u][g] = ld_u128(cbase + (vo + uint32_t(g) * 64));
+    const uint32_t vs = (kq >= 2 ? dB + (nB0 + 4 * uint32_t(kq - 2)) * 32u : (nA0 + 4 * uint32_t(kq)) * 32u) +
+                        2 * (wave * 4 + uint32_t(lane & 3));
+    const uint8_t* sbase = uni(cellA + 16448 + 48);
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) sc[u][jj] = ld_u16(sbase + (vs + uint32_t(jj) * 32));
     cA_[u] = cellA;
-    cB_[u] = cellB;
+    dB_[u] = dB;
+    nA_[u] = nA0;
+    nB_[u] = nB0;
     rA_[u] = live ? rA : 0xffffffffu;
     rB_[u] = live ? rB : 0xffffffffu;
-    rowsA_[u] = rowsA;
-    rowsB_[u] = rowsB;
+    rows_[u] = rows;
     role_[u] = PA.rope_role;
     src_[u] = MODE == int(GemvMode::Accum) ? PA.y : PA.bias;
     y_[u] = PA.y;
   }
-  // the epilogue operands of wave e < 2 UPW: half eh = e % 2 of tile eu = e / 2; lane 8 i + k:
-  // outlier k of the row on lanes 8 i.. (i < 4: part A row 4 eh + i; i >= 4: part B row 4 eh + i - 4),
-  // lane 8 i's residual or bias and RoPE factors
-  const uint32_t ew = wave < uint32_t(2 * UPW) ? wave : 0u, eu = ew >> 1, eh = ew & 1u;
+  // the epilogue operands of wave e < 2 UPW, lane 8 i + k: outlier k of row i's cell
+  // (gemvTileW4 :404-410: the cell's 8 columns, the row's 8 weights), lane 8 i's residual or bias
+  // and RoPE factors.  SwiGlu: wave e < 2 takes rows 8 e + i of the gate and the up cell;
+  // otherwise half eh = e % 2 of tile eu = e / 2 (i < 4: part A row 4 eh + i; i >= 4: part B row
+  // 4 eh + i - 4).
+  const uint32_t ew = wave < uint32_t(kSwi ? 2 : 2 * UPW) ? wave : 0u, eu = kSwi ? 0u : ew >> 1, eh = ew & 1u;
   const uint8_t* eA = cA_[0];
-  const uint8_t* eB = cB_[0];
-  uint32_t erA = rA_[0], erB = rB_[0], ersA = rowsA_[0], ersB = rowsB_[0], erole = role_[0];
+  uint32_t edB = dB_[0], enA = nA_[0], enB = nB_[0], erA = rA_[0], erB = rB_[0], erows = rows_[0], erole = role_[0];
   const float* esrc = src_[0];
   float* ey = y_[0];
-  if constexpr (UPW == 2) {
+  if constexpr (UPW == 2 && !kSwi) {
     if (eu == 1u) {
-      eA = cA_[1]; eB = cB_[1]; erA = rA_[1]; erB = rB_[1]; ersA = rowsA_[1]; ersB = rowsB_[1];
+      eA = cA_[1]; edB = dB_[1]; enA = nA_[1]; enB = nB_[1]; erA = rA_[1]; erB = rB_[1]; erows = rows_[1];
       erole = role_[1]; esrc = src_[1]; ey = y_[1];
     }
   }
-  const bool elive = wave < uint32_t(2 * UPW) && tile0 + eu < a.n_units;
-  const bool oB = i8 >= 4;
-  const uint32_t efirst = oB ? erB : erA, erows = oB ? ersB : ersA;
-  const uint32_t orow = efirst + 4 * eh + uint32_t(i8 & 3);
-  const bool ovalid = elive && efirst != 0xffffffffu && orow < erows;
-  const uint8_t* ocell = oB ? eB : eA;
-  const uint32_t on = ovalid ? (orow & 15u) : 0u, k8 = uint32_t(lane & 7);
-  const uint32_t ocol = ld_u16(ocell + (16448 + 816 + 2 * k8));
-  const uint32_t ow = ld_u16(ocell + (16448 + 560 + 2 * (on * 8 + k8)));
+  const bool elive = wave < uint32_t(kSwi ? 2 : 2 * UPW) && (kSwi || tile0 + eu < a.n_units);
+  const bool oB = !kSwi && i8 >= 4;
+  const uint32_t oi = kSwi ? 8 * eh + uint32_t(i8) : 4 * eh + uint32_t(i8 & 3);
+  const uint32_t orow = (oB ? erB : erA) + oi;
+  const bool ovalid = elive && erA != 0xffffffffu && orow < erows;
+  const uint32_t on = (oB ? enB : enA) + oi, ovo = oB ? edB : 0u, k8 = uint32_t(lane & 7);
+  const uint8_t* obase = uni(eA + 16448);
+  const uint32_t ocol = ld_u16(obase + (ovo + 816 + 2 * k8));
+  const uint32_t ow = ld_u16(obase + (ovo + 560 + 2 * (on * 8 + k8)));
+  uint32_t ocol2 = 0, ow2 = 0;  // SwiGlu: the up cell's outlier of the same row
+  if constexpr (kSwi) {
+    const uint8_t* obase2 = uni(cA_[UPW - 1] + 16448);
+    ocol2 = ld_u16(obase2 + (816 + 2 * k8));
+    ow2 = ld_u16(obase2 + (560 + 2 * (on * 8 + k8)));
+  }
   float pre = 0.0f, rc = 1.0f, rs = 0.0f;
   bool pre_ok = false, rope_ok = false;
   if constexpr (kPre) {
@@ -1295,41 +1305,52 @@ __global__ void __launch_bounds__(kWave * kMmaWaves) k_gemv_mma(GemvArgs a) {
     if (m == 12) *reinterpret_cast<float4*>(&s_part[u][wave][4 * kq]) = make_float4(t[0], t[1], t[2], t[3]);
   }
   __syncthreads();
-  if (wave >= uint32_t(2 * UPW)) return;
+  if (wave >= uint32_t(kSwi ? 2 : 2 * UPW)) return;
 
-  // 4. wave e: rows of its tile half, the outlier terms, 1/rms, the epilogue
-  const uint32_t tr = oB ? 8 + 4 * eh + uint32_t(i8 - 4) : 4 * eh + uint32_t(i8);
-  float v = 0.0f;
+  // 4. wave e: rows of its tile half (SwiGlu: of both cells), the outlier terms, 1/rms, the epilogue
+  const uint32_t tr = kSwi ? oi : (oB ? 8 + 4 * eh + uint32_t(i8 - 4) : 4 * eh + uint32_t(i8));
+  float v = 0.0f, v2 = 0.0f;
 #pragma unroll
-  for (int w = 0; w < kMmaWaves; ++w) v += s_part[eu][w][tr];
+  for (int w = 0; w < kMmaWaves; ++w) {
+    v += s_part[eu][w][tr];
+    if constexpr (kSwi) v2 += s_part[UPW - 1][w][tr];
+  }
   float o = (ovalid && ocol < 2048u) ? half_lo(ow) * s_x[xs_at(ocol < 2048u ? ocol : 0u)] : 0.0f;
   o = pair_sum(o, 1);
   o = pair_sum(o, 2);
   o = pair_sum(o, 4);
   v += o;
+  if constexpr (kSwi) {
+    float o2 = (ovalid && ocol2 < 2048u) ? half_lo(ow2) * s_x[xs_at(ocol2 < 2048u ? ocol2 : 0u)] : 0.0f;
+    o2 = pair_sum(o2, 1);
+    o2 = pair_sum(o2, 2);
+    o2 = pair_sum(o2, 4);
+    v2 += o2;
+  }
   if constexpr (kNorm) {
     float ss = 0.0f;
 #pragma unroll
     for (int w = 0; w < kMmaWaves; ++w) ss += s_red[w];
-    v *= 1.0f / sqrtf(ss / 2048.0f + a.eps);
+    const float inv = 1.0f / sqrtf(ss / 2048.0f + a.eps);
+    v *= inv;
+    v2 *= inv;
   }
-  const float upv = (kSwi || kRope) ? pair_val(v, 32) : 0.0f;
+  const float upv = kSwi ? v2 : (kRope ? pair_val(v, 32) : 0.0f);
   const float prev = pre_ok ? pre : 0.0f;
   const float up_pre = kRope ? pair_val(prev, 32) : 0.0f;
   float bv = -1e30f;
   uint32_t bi = 0xffffffffu, nf = 0;
   if (!elive) return;
   GemvPart E0 = a.part[0];
-  E0.rows = ersA;
+  E0.rows = erows;
   E0.y = ey;
   if constexpr (kRope) {
     E0.rope_role = erole;
     if ((lane % S) == 0 && !oB && ovalid)
       rope_store(a, E0, orow, v + prev, upv + up_pre, rope_ok ? rc : 1.0f, rope_ok ? rs : 0.0f);
   } else if constexpr (kSwi) {
-    if ((lane % S) == 0 && !oB && ovalid) epilogue<MODE>(E0, orow, v, upv, prev, &bv, &bi, &nf);
+    if ((lane % S) == 0 && ovalid) epilogue<MODE>(E0, orow, v, upv, prev, &bv, &bi, &nf);
   } else {
-    E0.rows = erows;
     if ((lane % S) == 0 && ovalid) epilogue<MODE>(E0, orow, v, upv, prev, &bv, &bi, &nf);
   }
 }
@@ -1473,8 +1494,16 @@ template <class F, int MODE>
 void launch_one(const GemvArgs& a, const GemvLaunch& g, hipStream_t st) {
   const size_t lds = size_t(xs_floats(a.C)) * 4;
   if constexpr (std::is_same_v<F, Cell16W4> && MODE != int(GemvMode::Logits)) {
-    if (g.mma == 1) { launch_kernel(&k_gemv_mma<MODE, 1>, dim3(g.blocks), dim3(g.threads), st, a); return; }
-    if (g.mma == 2) { launch_kernel(&k_gemv_mma<MODE, 2>, dim3(g.blocks), dim3(g.threads), st, a); return; }
+    if (g.mma) {
+      if constexpr (MODE == int(GemvMode::SwiGlu)) {
+        launch_kernel(&k_gemv_mma<MODE, 2>, dim3(g.blocks), dim3(g.threads), st, a);
+      } else if (g.mma == 2) {
+        launch_kernel(&k_gemv_mma<MODE, 2>, dim3(g.blocks), dim3(g.threads), st, a);
+      } else {
+        launch_kernel(&k_gemv_mma<MODE, 1>, dim3(g.blocks), dim3(g.threads), st, a);
+      }
+      return;
+    }
     if (g.cells == 1) { launch_kernel(&k_gemv_cells<MODE, 1>, dim3(g.blocks), dim3(g.threads), st, a); return; }
     if (g.cells == 2) { launch_kernel(&k_gemv_cells<MODE, 2>, dim3(g.blocks), dim3(g.threads), st, a); return; }
     if (g.cells == 4) { launch_kernel(&k_gemv_cells<MODE, 4>, dim3(g.blocks), dim3(g.threads), st, a); return; }
@@ -1564,8 +1593,8 @@ GemvLaunch gemv_geometry(WeightKind kind, GemvMode mode, uint32_t C, const uint3
       (mode != GemvMode::QkvRope || rope_tiles)) {
     // matrix-core kernel: tiles of 16 rows (SwiGlu: 8 gate + 8 up rows), UPW tiles per workgroup
     uint32_t tiles = 0;
-    if (mode == GemvMode::SwiGlu) {
-      tiles = (rows[0] + 7) / 8;
+    if (mode == GemvMode::SwiGlu) {  // units of 16 rows: the gate and the up cell in one workgroup
+      tiles = (rows[0] + 15) / 16;
       unit_begin[0] = unit_begin[1] = 0;
     } else {
       for (int p = 0; p < n_parts; ++p) {
@@ -1574,10 +1603,10 @@ GemvLaunch gemv_geometry(WeightKind kind, GemvMode mode, uint32_t C, const uint3
       }
     }
     *n_units = tiles;
-    const uint32_t upw = tiles >= 1024 && gemv_tuning().mma == 2 ? 2u : 1u;
+    const uint32_t upw = mode == GemvMode::SwiGlu || (tiles >= 1024 && gemv_tuning().mma == 2) ? 2u : 1u;
     g.mma = upw;
     g.threads = kWave * kMmaWaves;
-    g.blocks = (tiles + upw - 1) / upw;
+    g.blocks = mode == GemvMode::SwiGlu ? tiles : (tiles + upw - 1) / upw;
   } else if (kind == WeightKind::Cell16W4 && mode != GemvMode::Logits && C == 2048 && gemv_tuning().cells) {
     // K-split over kCellWaves waves; units per workgroup: 1 for the small projections (more
     // workgroups, more parallel dot work), up to the tuning cap when there are thousands
