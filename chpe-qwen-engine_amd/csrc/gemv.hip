@@ -1055,6 +1055,7 @@ __global__ void __launch_bounds__(kWave * kCellWaves) k_gemv_cells(GemvArgs a) {
 // row i on lanes 8i..8i+7), adds the cell's outlier terms and runs the epilogue of the other
 // cell kernels.  The only workgroup barrier is the one before the epilogue.
 constexpr int kMmaWaves = 4;
+constexpr int kMmaTable = 4 * 4 * 2 * 4;  // B table entries per wave: groups x quarters x halves x limbs
 typedef int i32x4_t __attribute__((ext_vector_type(4)));
 
 // first rows of the two 8-row halves of a tile (the tile's part already chosen; SwiGlu tiles are
@@ -1082,6 +1083,114 @@ __device__ __forceinline__ void limb_words(uint32_t a, uint32_t b, uint32_t c, u
   w[3] = __builtin_amdgcn_perm(qcd, qab, 0x07060302u);
 }
 
+// The wave's 512 input columns (lane l: c0 .. c0 + 7; x' = x * gamma when kNorm) as the B
+// operands of k_gemv_mma's products, through the wave's LDS table: the group exponent (max over
+// the group's 16 lanes), the four signed-byte limbs per column in the A operand's byte order,
+// the limb sums (the accumulators' start, -8 * sum) and 2^(e-30); x' also into s_x (for the
+// outliers) and, when kNorm, the wave's sum of x^2 into s_red[wave].  Lane (n, kq) =
+// (lane % 16, lane / 16) gets B[s][h] = limb n / 4 of group slot s = n % 4 (zero for the other
+// slots) for quarter kq and half h, its accumulator start and its readout factor.
+template <bool kNorm>
+__device__ __forceinline__ void mma_stage(const float4& xa, const float4& xb, const float4& ga, const float4& gb,
+                                          uint32_t wave, int lane, uint32_t c0, float* s_x, uint4* s_bw, int* s_sxw,
+                                          float* s_ew, float* s_red, i32x4_t (&B)[4][2], int* cinit, float* lpf) {
+  const int m = lane & 15, kq = lane >> 4;
+  const float xv[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+  const float gv[8] = {ga.x, ga.y, ga.z, ga.w, gb.x, gb.y, gb.z, gb.w};
+  float xp[8], q2 = 0.0f, mx = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    xp[i] = kNorm ? xv[i] * gv[i] : xv[i];
+    q2 = fmaf(xv[i], xv[i], q2);
+    mx = fmaxf(mx, fabsf(xp[i]));
+  }
+  mx = pair_max(mx, 1);
+  mx = pair_max(mx, 2);
+  mx = pair_max(mx, 4);
+  mx = pair_max(mx, 8);
+  int e = 0;
+  (void)frexpf(mx, &e);  // mx < 2^e (mx = 0: e = 0)
+  const float up = ldexpf(1.0f, 30 - e);
+  uint32_t z[8];  // bytes: the balanced limbs of X
+#pragma unroll
+  for (int i = 0; i < 8; ++i) z[i] = (uint32_t(int(xp[i] * up)) + 0x808080u) ^ 0x808080u;  // (toward zero)
+  uint32_t lo[4], hi[4];
+  limb_words(z[0], z[2], z[4], z[6], lo);
+  limb_words(z[1], z[3], z[5], z[7], hi);
+  const uint32_t gs = uint32_t(lane) >> 4, gkq = (uint32_t(lane) >> 2) & 3u, gh = (uint32_t(lane) >> 1) & 1u;
+  uint2* tb = reinterpret_cast<uint2*>(s_bw);
+#pragma unroll
+  for (int L = 0; L < 4; ++L) tb[(((gs * 4 + gkq) * 2 + gh) * 4 + L) * 2 + (lane & 1)] = make_uint2(lo[L], hi[L]);
+  // limb sums over the group: per lane 8 signed bytes (+1024, so that two 16-bit sums share a
+  // word: 16 lanes x 2040 < 2^15), over the 16 lanes on DPP
+  uint32_t lp[2];
+#pragma unroll
+  for (int P = 0; P < 2; ++P) {
+    const int s0 = __builtin_amdgcn_sdot4(int(lo[2 * P]), 0x01010101, __builtin_amdgcn_sdot4(int(hi[2 * P]), 0x01010101, 1024, false), false);
+    const int s1 = __builtin_amdgcn_sdot4(int(lo[2 * P + 1]), 0x01010101, __builtin_amdgcn_sdot4(int(hi[2 * P + 1]), 0x01010101, 1024, false), false);
+    uint32_t w = uint32_t(s0) | (uint32_t(s1) << 16);
+    w += pair_u(w, 1);
+    w += pair_u(w, 2);
+    w += pair_u(w, 4);
+    w += pair_u(w, 8);
+    lp[P] = w;
+  }
+  if ((lane & 15) == 0) {
+#pragma unroll
+    for (int L = 0; L < 4; ++L) s_sxw[gs * 4 + L] = -8 * (int((lp[L >> 1] >> (16 * (L & 1))) & 0xffffu) - 16 * 1024);
+    s_ew[gs] = isfinite(mx) ? ldexpf(1.0f, e - 30) : __int_as_float(0x7fc00000);  // NaN / inf propagate
+  }
+  if (lane == 0) s_bw[kMmaTable] = make_uint4(0, 0, 0, 0);
+  *reinterpret_cast<float4*>(s_x + xs_at(c0)) = make_float4(xp[0], xp[1], xp[2], xp[3]);
+  *reinterpret_cast<float4*>(s_x + xs_at(c0) + 4) = make_float4(xp[4], xp[5], xp[6], xp[7]);
+  if constexpr (kNorm) {
+    q2 = wave_sum(q2);
+    if (lane == 0) s_red[wave] = q2;
+  }
+  __builtin_amdgcn_wave_barrier();  // (one wave's LDS accesses execute in order)
+  const uint32_t bs = uint32_t(m & 3), bl = uint32_t(m >> 2);
+#pragma unroll
+  for (int s = 0; s < 4; ++s)
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const uint32_t ent = bs == uint32_t(s) ? ((uint32_t(s) * 4 + uint32_t(kq)) * 2 + uint32_t(h)) * 4 + bl
+                                             : uint32_t(kMmaTable);
+      const uint4 t = s_bw[ent];
+      B[s][h] = i32x4_t{int(t.x), int(t.y), int(t.z), int(t.w)};
+    }
+  *cinit = s_sxw[bs * 4 + bl];
+  *lpf = s_ew[bs] * __int_as_float(int(127 + 8 * bl) << 23);  // * 2^(8 limb)
+}
+
+// One tile's 8 products (4 groups x 2 halves of 64 columns) and the wave's row sums: the limbs
+// combined on DPP (row_shr 4, 8, 12: lanes 12..15 of each row), times the group scale, summed
+// over the 4 groups (DPP); lane 12 of row kq writes tile rows 4 kq .. 4 kq + 3 to part[].
+__device__ __forceinline__ void mma_tile(const uint4 (&q)[4], const uint32_t (&sc)[4], const i32x4_t (&B)[4][2],
+                                         int cinit, float lpf, int lane, float* part) {
+  i32x4_t D = {cinit, cinit, cinit, cinit};
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const uint32_t w[4] = {q[g].x, q[g].y, q[g].z, q[g].w};
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const uint32_t w0 = w[2 * h], w1 = w[2 * h + 1];
+      const i32x4_t A = {int(w0 & 0x0f0f0f0fu), int((w0 >> 4) & 0x0f0f0f0fu), int(w1 & 0x0f0f0f0fu),
+                         int((w1 >> 4) & 0x0f0f0f0fu)};
+      D = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, B[g][h], D, 0, 0, 0);
+    }
+  }
+  float t[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const float f = float(D[j]) * lpf;
+    const float v = ((f + dpp_f<0x114>(f)) + dpp_f<0x118>(f)) + dpp_f<0x11c>(f);
+    t[j] = v * h2f(uint16_t(sc[j]));
+    t[j] = pair_sum(t[j], 1);
+    t[j] = pair_sum(t[j], 2);
+  }
+  if ((lane & 15) == 12) *reinterpret_cast<float4*>(part + 4 * (lane >> 4)) = make_float4(t[0], t[1], t[2], t[3]);
+}
+
 template <int MODE, int UPW>
 __global__ void __launch_bounds__(kWave * kMmaWaves) k_gemv_mma(GemvArgs a) {
   constexpr bool kNorm = kNormOf<MODE>;
@@ -1093,7 +1202,7 @@ __global__ void __launch_bounds__(kWave * kMmaWaves) k_gemv_mma(GemvArgs a) {
   static_assert(UPW == 1 || UPW == 2, "two epilogue waves per tile");
   static_assert(!kSwi || UPW == 2, "a SwiGlu workgroup holds the gate and the up cell");
   __shared__ __align__(16) float s_x[xs_floats(2048)];          // x' for the outlier terms
-  __shared__ __align__(16) uint4 s_b[kMmaWaves][4 * 4 * 2 * 4 + 1];  // B table per wave (+ a zero entry)
+  __shared__ __align__(16) uint4 s_b[kMmaWaves][kMmaTable + 1];  // B table per wave (+ a zero entry)
   __shared__ int s_sx[kMmaWaves][4][4];                            // -8 * limb sums per group
   __shared__ float s_e[kMmaWaves][4];                              // 2^(e - 30) per group
   __shared__ __align__(16) float s_part[UPW][kMmaWaves][16];
@@ -1213,97 +1322,14 @@ __global__ void __launch_bounds__(kWave * kMmaWaves) k_gemv_mma(GemvArgs a) {
 
   __builtin_amdgcn_sched_barrier(0);  // every load above is issued before the input is used
 
-  // 2. the wave's B table: x' as three signed bytes per column, the group's exponent and limb
-  // sums (wave-local: written and read by this wave only)
-  const float xv[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
-  const float gv[8] = {ga.x, ga.y, ga.z, ga.w, gb.x, gb.y, gb.z, gb.w};
-  float xp[8], q2 = 0.0f, mx = 0.0f;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    xp[i] = kNorm ? xv[i] * gv[i] : xv[i];
-    q2 = fmaf(xv[i], xv[i], q2);
-    mx = fmaxf(mx, fabsf(xp[i]));
-  }
-  mx = pair_max(mx, 1);
-  mx = pair_max(mx, 2);
-  mx = pair_max(mx, 4);
-  mx = pair_max(mx, 8);
-  int e = 0;
-  (void)frexpf(mx, &e);  // mx < 2^e (mx = 0: e = 0)
-  const float up = ldexpf(1.0f, 30 - e);
-  uint32_t z[8];  // bytes: the balanced limbs of X
-#pragma unroll
-  for (int i = 0; i < 8; ++i) z[i] = (uint32_t(int(rintf(xp[i] * up))) + 0x808080u) ^ 0x808080u;
-  uint32_t lo[4], hi[4];
-  limb_words(z[0], z[2], z[4], z[6], lo);
-  limb_words(z[1], z[3], z[5], z[7], hi);
-  const uint32_t gs = uint32_t(lane) >> 4, gkq = (uint32_t(lane) >> 2) & 3u, gh = (uint32_t(lane) >> 1) & 1u;
-  uint2* tb = reinterpret_cast<uint2*>(&s_b[wave][0]);
-  float lsum[4];
-#pragma unroll
-  for (int L = 0; L < 4; ++L) {
-    tb[(((gs * 4 + gkq) * 2 + gh) * 4 + L) * 2 + (lane & 1)] = make_uint2(lo[L], hi[L]);
-    lsum[L] = float(__builtin_amdgcn_sdot4(int(lo[L]), 0x01010101, __builtin_amdgcn_sdot4(int(hi[L]), 0x01010101, 0, false), false));
-    lsum[L] = pair_sum(lsum[L], 1);
-    lsum[L] = pair_sum(lsum[L], 2);
-    lsum[L] = pair_sum(lsum[L], 4);
-    lsum[L] = pair_sum(lsum[L], 8);
-  }
-  if ((lane & 15) == 0) {
-#pragma unroll
-    for (int L = 0; L < 4; ++L) s_sx[wave][gs][L] = -8 * int(lsum[L]);
-    s_e[wave][gs] = isfinite(mx) ? ldexpf(1.0f, e - 30) : __int_as_float(0x7fc00000);  // NaN / inf propagate
-  }
-  if (lane == 0) s_b[wave][4 * 4 * 2 * 4] = make_uint4(0, 0, 0, 0);
-  *reinterpret_cast<float4*>(s_x + xs_at(c0)) = make_float4(xp[0], xp[1], xp[2], xp[3]);
-  *reinterpret_cast<float4*>(s_x + xs_at(c0) + 4) = make_float4(xp[4], xp[5], xp[6], xp[7]);
-  if constexpr (kNorm) {
-    q2 = wave_sum(q2);
-    if (lane == 0) s_red[wave] = q2;
-  }
-  __builtin_amdgcn_wave_barrier();  // (one wave's LDS accesses execute in order)
-  // lane (n = m, kq): column n = s + 4 limb of B
-  const uint32_t bs = uint32_t(m & 3), bl = uint32_t(m >> 2);
+  // 2. the wave's B operands (wave-local LDS table), 3. the products of each tile
   i32x4_t B[4][2];
+  int cinit;
+  float lpf;
+  mma_stage<kNorm>(xa, xb, ga, gb, wave, lane, c0, s_x, &s_b[wave][0], &s_sx[wave][0][0], &s_e[wave][0], s_red, B,
+                   &cinit, &lpf);
 #pragma unroll
-  for (int s = 0; s < 4; ++s)
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const uint32_t ent = bs == uint32_t(s) ? ((uint32_t(s) * 4 + uint32_t(kq)) * 2 + uint32_t(h)) * 4 + bl
-                                             : uint32_t(4 * 4 * 2 * 4);
-      const uint4 t = s_b[wave][ent];
-      B[s][h] = i32x4_t{int(t.x), int(t.y), int(t.z), int(t.w)};
-    }
-  const int cinit = s_sx[wave][bs][bl];
-  const float lpf = s_e[wave][bs] * __int_as_float(int(127 + 8 * bl) << 23);  // * 2^(8 limb)
-
-  // 3. per tile: 8 products (4 groups x 2 halves of 64 columns), the row sums of the wave
-#pragma unroll
-  for (int u = 0; u < UPW; ++u) {
-    i32x4_t D = {cinit, cinit, cinit, cinit};
-#pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      const uint32_t w[4] = {q[u][g].x, q[u][g].y, q[u][g].z, q[u][g].w};
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const uint32_t w0 = w[2 * h], w1 = w[2 * h + 1];
-        const i32x4_t A = {int(w0 & 0x0f0f0f0fu), int((w0 >> 4) & 0x0f0f0f0fu), int(w1 & 0x0f0f0f0fu),
-                           int((w1 >> 4) & 0x0f0f0f0fu)};
-        D = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, B[g][h], D, 0, 0, 0);
-      }
-    }
-    float t[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const float f = float(D[j]) * lpf;
-      // lanes 12..15 of the row: + the limbs of lanes n - 4, n - 8, n - 12 (row_shr)
-      const float v = ((f + dpp_f<0x114>(f)) + dpp_f<0x118>(f)) + dpp_f<0x11c>(f);
-      t[j] = v * h2f(uint16_t(sc[u][j]));
-      t[j] = pair_sum(t[j], 1);
-      t[j] = pair_sum(t[j], 2);  // the 4 groups
-    }
-    if (m == 12) *reinterpret_cast<float4*>(&s_part[u][wave][4 * kq]) = make_float4(t[0], t[1], t[2], t[3]);
-  }
+  for (int u = 0; u < UPW; ++u) mma_tile(q[u], sc[u], B, cinit, lpf, lane, &s_part[u][wave][0]);
   __syncthreads();
   if (wave >= uint32_t(kSwi ? 2 : 2 * UPW)) return;
 
@@ -1353,6 +1379,109 @@ __global__ void __launch_bounds__(kWave * kMmaWaves) k_gemv_mma(GemvArgs a) {
   } else {
     if ((lane % S) == 0 && ovalid) epilogue<MODE>(E0, orow, v, upv, prev, &bv, &bi, &nf);
   }
+}
+
+// The LM head on the matrix cores: a persistent grid whose workgroups stage the final-normed
+// input once (x * gamma; 1/rms multiplies the row sums) and stride over the 16-row cells, one
+// cell per iteration on the 4 waves (the products of k_gemv_mma), the next cell's loads issued
+// before the current cell's products; waves 0 and 1 finish rows 8 w .. 8 w + 7: the outliers
+// replace weights through the prepared table of the tied head (unpackEmbedRowCell :1369-1378)
+// or are added from the cell (untied cells, gemvTileW4 :404-410), then the logit and the
+// workgroup's argmax partial (computeLmHead :1554-1660, argmax :1775-1803).
+struct MmaCellLoads {
+  uint4 q[4];
+  uint32_t sc[4];
+  uint32_t ocol, ow;  // outlier column and fp16 weight (added), or
+  float od;           // the replace table's correction
+};
+
+__global__ void __launch_bounds__(kWave * kMmaWaves) k_gemv_mma_logits(GemvArgs a) {
+  constexpr int MODE = int(GemvMode::Logits);
+  __shared__ __align__(16) float s_x[xs_floats(2048)];
+  __shared__ __align__(16) uint4 s_b[kMmaWaves][kMmaTable + 1];
+  __shared__ int s_sx[kMmaWaves][4][4];
+  __shared__ float s_e[kMmaWaves][4];
+  __shared__ __align__(16) float s_part[2][kMmaWaves][16];
+  __shared__ float s_red[kMmaWaves], s_bv[kMmaWaves];
+  __shared__ uint32_t s_bi[kMmaWaves], s_nf[kMmaWaves];
+  const int lane = threadIdx.x & 63, m = lane & 15, kq = lane >> 4, i8 = lane >> 3;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  args_batch<MODE>(a);
+  const GemvPart& P = a.part[0];
+  const uint32_t n_tiles = a.n_units, step = gridDim.x;
+  const bool repl = P.repl != nullptr;
+  const uint32_t c0 = wave * 512 + uint32_t(lane) * 8;
+  const float4 xa = ld_f4(a.x + c0), xb = ld_f4(a.x + c0 + 4);
+  const float4 ga = ld_f4(a.gamma + c0), gb = ld_f4(a.gamma + c0 + 4);
+  __builtin_amdgcn_sched_barrier(0);
+  const uint32_t tr = 8 * (wave & 1u) + uint32_t(i8), k8 = uint32_t(lane & 7);
+  const uint32_t vo = uint32_t(m) * 1024u + uint32_t(kq) * 16, vs = uint32_t(kq) * 128u + 2 * (wave * 4 + uint32_t(lane & 3));
+  auto issue = [&](uint32_t tile, MmaCellLoads* t) {
+    const uint8_t* cell = P.base + size_t(tile) * P.stride;
+    const uint8_t* cbase = uni(cell + 64 + wave * 256);
+#pragma unroll
+    for (int g = 0; g < 4; ++g) t->q[g] = ld_u128(cbase + (vo + uint32_t(g) * 64));
+    const uint8_t* sbase = uni(cell + 16448 + 48);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) t->sc[j] = ld_u16(sbase + (vs + uint32_t(j) * 32));
+    // branch-free: both kinds are loaded (the replace table's from the cell when there is none)
+    const uint8_t* obase = uni(cell + 16448);
+    const CellReplace* R = uni(P.repl + tile);
+    const uint8_t* cp = repl ? reinterpret_cast<const uint8_t*>(R->col) : obase + 816;
+    const uint8_t* dp = repl ? reinterpret_cast<const uint8_t*>(R->delta[0]) : obase + 560;
+    t->ocol = ld_u16(cp + 2 * k8);
+    t->od = gld(reinterpret_cast<const float*>(dp + 4 * (tr * 8 + k8) * (repl ? 1u : 0u)));
+    t->ow = ld_u16(obase + (560 + 2 * (tr * 8 + k8)));
+  };
+  uint32_t tile = blockIdx.x;  // < n_tiles: the grid is at most the tile count
+  MmaCellLoads L0, L1;
+  issue(tile, &L0);
+  __builtin_amdgcn_sched_barrier(0);
+  i32x4_t B[4][2];
+  int cinit;
+  float lpf;
+  mma_stage<true>(xa, xb, ga, gb, wave, lane, c0, s_x, &s_b[wave][0], &s_sx[wave][0][0], &s_e[wave][0], s_red, B,
+                  &cinit, &lpf);
+  __syncthreads();  // s_x (the outliers' inputs) and s_red complete
+  float ss = 0.0f;
+#pragma unroll
+  for (int w = 0; w < kMmaWaves; ++w) ss += s_red[w];
+  const float inv = 1.0f / sqrtf(ss / 2048.0f + a.eps);
+  float bv = -1e30f;
+  uint32_t bi = 0xffffffffu, nf = 0;
+  // one cell: products, row sums in s_part[buf], then the two epilogue waves (two buffers: a
+  // buffer is written again only after the next barrier, when its readers are done)
+  auto process = [&](uint32_t t, const MmaCellLoads& c, int buf) {
+    mma_tile(c.q, c.sc, B, cinit, lpf, lane, &s_part[buf][wave][0]);
+    __syncthreads();
+    if (wave < 2) {
+      float v = 0.0f;
+#pragma unroll
+      for (int w = 0; w < kMmaWaves; ++w) v += s_part[buf][w][tr];
+      const float xo = s_x[xs_at(c.ocol < 2048u ? c.ocol : 0u)];
+      float o = c.ocol < 2048u ? (repl ? c.od : half_lo(c.ow)) * xo : 0.0f;
+      o = pair_sum(o, 1);
+      o = pair_sum(o, 2);
+      o = pair_sum(o, 4);
+      v = (v + o) * inv;
+      if ((lane & 7) == 0) epilogue<MODE>(P, t * 16 + tr, v, 0.0f, 0.0f, &bv, &bi, &nf);
+    }
+  };
+  // two cells per trip, the loads of the next cell issued before the current one's products (a
+  // clamped repeat past the end); the trip count is the same for every wave of the workgroup
+  while (true) {
+    const uint32_t t1 = tile + step;
+    issue(t1 < n_tiles ? t1 : tile, &L1);
+    process(tile, L0, 0);
+    if (t1 >= n_tiles) break;
+    const uint32_t t2 = t1 + step;
+    issue(t2 < n_tiles ? t2 : t1, &L0);
+    process(t1, L1, 1);
+    if (t2 >= n_tiles) break;
+    tile = t2;
+  }
+  argmax_partial<MODE>(a, bv, bi, nf, s_bv, s_bi, s_nf);
+  if (blockIdx.x == 0 && threadIdx.x == 0) a.result->hidden_norm = sqrtf(ss);
 }
 
 // Flat 4-bit tiles (gemvCellFlat: the down projection, and every projection wider than 2048
@@ -1493,6 +1622,12 @@ __global__ void __launch_bounds__(kWave * W) k_gemv_flat(GemvArgs a) {
 template <class F, int MODE>
 void launch_one(const GemvArgs& a, const GemvLaunch& g, hipStream_t st) {
   const size_t lds = size_t(xs_floats(a.C)) * 4;
+  if constexpr (std::is_same_v<F, Cell16W4> && MODE == int(GemvMode::Logits)) {
+    if (g.mma) {
+      launch_kernel(&k_gemv_mma_logits, dim3(g.blocks), dim3(g.threads), st, a);
+      return;
+    }
+  }
   if constexpr (std::is_same_v<F, Cell16W4> && MODE != int(GemvMode::Logits)) {
     if (g.mma) {
       if constexpr (MODE == int(GemvMode::SwiGlu)) {
@@ -1553,6 +1688,8 @@ const GemvTuning& gemv_tuning() {
     if (const char* e = std::getenv("CHPE_GEMV_CELLS")) v.cells = uint32_t(std::strtoul(e, nullptr, 10));
     if (const char* e = std::getenv("CHPE_GEMV_FLAT")) v.flat = uint32_t(std::strtoul(e, nullptr, 10));
     if (const char* e = std::getenv("CHPE_GEMV_MMA")) v.mma = uint32_t(std::strtoul(e, nullptr, 10));
+    if (const char* e = std::getenv("CHPE_GEMV_MMA_LOGITS_BLOCKS")) v.mma_logits_blocks = uint32_t(std::strtoul(e, nullptr, 10));
+    if (v.mma_logits_blocks == 0 || v.mma_logits_blocks > kMaxLogitsBlocks) v.mma_logits_blocks = kMaxLogitsBlocks;
     if (v.logits_blocks == 0 || v.logits_blocks > kMaxLogitsBlocks) v.logits_blocks = kMaxLogitsBlocks;
     return v;
   }();
@@ -1589,7 +1726,16 @@ GemvLaunch gemv_geometry(WeightKind kind, GemvMode mode, uint32_t C, const uint3
   g.ru = ru;
   bool rope_tiles = true;  // QkvRope tiles pair rows r, r + head_dim/2 in 8s: parts of whole 16-row heads
   for (int p = 0; p < n_parts; ++p) rope_tiles = rope_tiles && rows[p] % 16 == 0;
-  if (kind == WeightKind::Cell16W4 && mode != GemvMode::Logits && C == 2048 && gemv_tuning().mma &&
+  if (kind == WeightKind::Cell16W4 && mode == GemvMode::Logits && C == 2048 && gemv_tuning().mma && n_parts == 1) {
+    // the LM head on the matrix cores: a persistent grid striding over the 16-row cells
+    const uint32_t tiles = (rows[0] + 15) / 16;
+    unit_begin[0] = 0;
+    *n_units = tiles;
+    g.mma = 1;
+    g.threads = kWave * kMmaWaves;
+    const uint32_t cap = gemv_tuning().mma_logits_blocks;
+    g.blocks = tiles < cap ? tiles : cap;
+  } else if (kind == WeightKind::Cell16W4 && mode != GemvMode::Logits && C == 2048 && gemv_tuning().mma &&
       (mode != GemvMode::QkvRope || rope_tiles)) {
     // matrix-core kernel: tiles of 16 rows (SwiGlu: 8 gate + 8 up rows), UPW tiles per workgroup
     uint32_t tiles = 0;

@@ -168,6 +168,7 @@ struct GemvTuning {
   uint32_t flat = 1;   // CHPE_GEMV_FLAT=0: flat 4-bit tiles on the one-workgroup-per-unit K-split by panels
   uint32_t mma = 2;    // 16-row cells at 2048 columns on the matrix-core kernel, 1 or 2 tiles per
                        // workgroup of a launch with >= 1024 tiles (CHPE_GEMV_MMA; 0: off)
+  uint32_t mma_logits_blocks = 512;   // persistent workgroups of the matrix-core LM head (2 per CU)
 };
 const GemvTuning& gemv_tuning();
 
