@@ -209,6 +209,12 @@ bool Engine::init(const uint8_t* b, size_t len, const EngineConfig& cfg, std::st
   // ---- activations, KV cache, RoPE tables, reduction scratch
   const size_t V = arch_.vocab_size, S = cfg.max_seq_len, hd = arch_.head_dim;
   d_hidden_ = static_cast<float*>(dev_alloc(D * 4));
+  d_hidden_out_ = static_cast<float*>(dev_alloc(D * 4));
+  {  // the next token's embedding moves into k_finish when the LM head runs on the matrix-core
+     // kernel (which keeps the step's final hidden state in d_hidden_out_)
+    uint32_t rows[kMaxParts] = {lm_head_.rows, 0, 0}, begin[kMaxParts], nu, np, wpu;
+    embed_fused_ = gemv_geometry(lm_head_.kind, GemvMode::Logits, uint32_t(D), rows, 1, &nu, &np, &wpu, begin).mma != 0;
+  }
   d_q_ = static_cast<float*>(dev_alloc(qd * 4));
   d_k_ = static_cast<float*>(dev_alloc(kvd * 4));
   d_v_ = static_cast<float*>(dev_alloc(kvd * 4));
@@ -524,6 +530,7 @@ uint32_t Engine::enqueue_gemv(const ProjPlan* const* parts, float* const* outs, 
   if (mode == GemvMode::Logits) {
     a.partials = d_partials_;
     a.result = d_result_;
+    a.hidden_out = embed_fused_ ? d_hidden_out_ : nullptr;
   }
   launch_gemv(parts[0]->kind, a, g, st);
   return g.blocks;
@@ -582,25 +589,39 @@ AttnArgs Engine::attn_args(size_t l) const {
   return at;
 }
 
-void Engine::record_step(hipStream_t st) {
-  const uint32_t D = uint32_t(arch_.hidden_dim), I = uint32_t(arch_.intermediate_dim);
+EmbedArgs Engine::embed_args() const {
   EmbedArgs e{};
   e.image = d_image_;
   e.image_len = image_len_;
   e.state = d_state_;
   e.hidden = d_hidden_;
-  e.D = D;
+  e.D = uint32_t(arch_.hidden_dim);
   e.kind = embed_kind_;
   e.record_count = record_count_;
   e.stride = stride_;
   e.cell_off = is_dense_ ? 0 : kPrefetchBytes;
+  return e;
+}
+
+int Engine::set_state(const StepState& s) {
+  *h_state_ = s;
+  if (hipMemcpyAsync(d_state_, h_state_, sizeof(StepState), hipMemcpyHostToDevice, stream_) != hipSuccess) return -3;
+  // the first step's input; with embed_fused_ every step's k_finish embeds the next token
+  if (embed_fused_) launch_embed(embed_args(), stream_);
+  return hipGetLastError() == hipSuccess ? 0 : -3;
+}
+
+// One decode step (forwardDecode :1663-1803) on the device: its input hidden state is already in
+// place (set_state, or the previous step's k_finish).
+void Engine::record_step(hipStream_t st) {
+  const uint32_t D = uint32_t(arch_.hidden_dim), I = uint32_t(arch_.intermediate_dim);
+  if (!embed_fused_) launch_embed(embed_args(), st);
   // begin/end events of every launch of one stage (time_stage_live; never during capture)
   auto mark = [&](int stage) {
     if (probe_stage_ != stage) return;
     arm_launch_probe(probe_events_[probe_next_], probe_events_[probe_next_ + 1]);
     probe_next_ += 2;
   };
-  launch_embed(e, st);
   for (size_t l = 0; l < arch_.num_layers; ++l) {
     const LayerPlan& L = layers_[l];
     mark(0);
@@ -626,7 +647,8 @@ void Engine::record_step(hipStream_t st) {
   float* lg[1] = {d_logits_};
   mark(4);
   const uint32_t n_partials = enqueue_gemv(lm, lg, 1, GemvMode::Logits, d_hidden_, D, d_gamma_final_, st);
-  FinishArgs f{d_state_, d_prompt_, d_partials_, n_partials, d_logits_, d_result_, d_out_tokens_};
+  FinishArgs f{d_state_, d_prompt_, d_partials_, n_partials, d_logits_, d_result_, d_out_tokens_, embed_args(),
+               embed_fused_ ? 1u : 0u};
   launch_finish(f, st);
 }
 
@@ -643,8 +665,7 @@ int Engine::read_result(ForwardResult* out) const {
 int Engine::forward(uint32_t token, size_t pos, ForwardResult* out) {
   if (pos >= cfg_.max_seq_len) return -2;  // the reference reads past its KV cache here
   const uint64_t t0 = now_ns();
-  *h_state_ = StepState{token, uint32_t(pos), 0, 0};
-  if (hipMemcpyAsync(d_state_, h_state_, sizeof(StepState), hipMemcpyHostToDevice, stream_) != hipSuccess) return -3;
+  if (set_state(StepState{token, uint32_t(pos), 0, 0})) return -3;
   if (launch_one()) return -3;
   if (hipMemcpyAsync(h_result_, d_result_, sizeof(StepResult), hipMemcpyDeviceToHost, stream_) != hipSuccess) return -3;
   if (hipStreamSynchronize(stream_) != hipSuccess) return -3;
@@ -699,8 +720,7 @@ int Engine::forward_tokens(const uint32_t* toks, size_t n, ForwardResult* out) {
   if (n == 0 || !toks) return -1;
   if (n > cfg_.max_seq_len) return -2;
   if (hipMemcpyAsync(d_prompt_, toks, n * 4, hipMemcpyHostToDevice, stream_) != hipSuccess) return -3;
-  *h_state_ = StepState{toks[0], 0, uint32_t(n), 0};
-  if (hipMemcpyAsync(d_state_, h_state_, sizeof(StepState), hipMemcpyHostToDevice, stream_) != hipSuccess) return -3;
+  if (set_state(StepState{toks[0], 0, uint32_t(n), 0})) return -3;
   launch_steps(n - 1);
   if (sync()) return -3;
   const uint64_t t0 = now_ns();
@@ -723,8 +743,7 @@ int Engine::generate(const uint32_t* prompt, size_t n_prompt, size_t n_gen, uint
   const size_t steps = n_prompt + n_gen - 1;
   if (steps > cfg_.max_seq_len) return -2;
   if (hipMemcpyAsync(d_prompt_, prompt, n_prompt * 4, hipMemcpyHostToDevice, stream_) != hipSuccess) return -3;
-  *h_state_ = StepState{prompt[0], 0, uint32_t(n_prompt), 0};
-  if (hipMemcpyAsync(d_state_, h_state_, sizeof(StepState), hipMemcpyHostToDevice, stream_) != hipSuccess) return -3;
+  if (set_state(StepState{prompt[0], 0, uint32_t(n_prompt), 0})) return -3;
   launch_steps(steps);
   if (sync()) return -3;
   if (out_tokens &&
@@ -740,8 +759,7 @@ int Engine::verify(const uint32_t* drafts, size_t m, size_t pos, uint32_t* out_a
   const uint64_t t0 = now_ns();
   // the drafts take the prompt slots of their positions, so every step is teacher-forced
   if (hipMemcpyAsync(d_prompt_ + pos, drafts, m * 4, hipMemcpyHostToDevice, stream_) != hipSuccess) return -3;
-  *h_state_ = StepState{drafts[0], uint32_t(pos), uint32_t(pos + m), 0};
-  if (hipMemcpyAsync(d_state_, h_state_, sizeof(StepState), hipMemcpyHostToDevice, stream_) != hipSuccess) return -3;
+  if (set_state(StepState{drafts[0], uint32_t(pos), uint32_t(pos + m), 0})) return -3;
   launch_steps(m);
   if (sync()) return -3;
   if (hipMemcpy(out_argmax, d_out_tokens_ + pos, m * 4, hipMemcpyDeviceToHost) != hipSuccess) return -3;
@@ -757,7 +775,8 @@ int Engine::copy_logits(float* out) const {
 }
 
 int Engine::copy_hidden(float* out) const {
-  return hipMemcpy(out, d_hidden_, arch_.hidden_dim * 4, hipMemcpyDeviceToHost) == hipSuccess ? 0 : -3;
+  const float* h = embed_fused_ ? d_hidden_out_ : d_hidden_;
+  return hipMemcpy(out, h, arch_.hidden_dim * 4, hipMemcpyDeviceToHost) == hipSuccess ? 0 : -3;
 }
 
 double Engine::proj_bytes(const ProjPlan& p) const {

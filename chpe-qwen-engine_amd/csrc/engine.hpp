@@ -131,6 +131,8 @@ class Engine {
   float* upload_vector(const std::vector<float>& v);
   void* dev_alloc(size_t bytes);
   void record_step(hipStream_t st);
+  EmbedArgs embed_args() const;
+  int set_state(const StepState& s);  // host-set (token, pos, ...) and the embedding of its token
   void enqueue_qkv(size_t layer, hipStream_t st);
   RopeArgs rope_args(size_t layer) const;
   // one GEMV launch over n parts (outs[i] receives part i); returns the workgroup count
@@ -181,6 +183,8 @@ class Engine {
   hipGraph_t graph_ = nullptr;
   hipGraphExec_t graph_exec_ = nullptr;
   bool use_graph_ = true;
+  bool embed_fused_ = false;         // k_finish embeds the next token (see init)
+  float* d_hidden_out_ = nullptr;    // the last step's final hidden state when embed_fused_
   int probe_stage_ = -1;                 // stage bracketed by events in record_step
   hipEvent_t* probe_events_ = nullptr;
   size_t probe_next_ = 0;

@@ -1414,6 +1414,10 @@ __global__ void __launch_bounds__(kWave * kMmaWaves) k_gemv_mma_logits(GemvArgs 
   const float4 xa = ld_f4(a.x + c0), xb = ld_f4(a.x + c0 + 4);
   const float4 ga = ld_f4(a.gamma + c0), gb = ld_f4(a.gamma + c0 + 4);
   __builtin_amdgcn_sched_barrier(0);
+  if (a.hidden_out && blockIdx.x == 0) {  // the step's final hidden state, kept for the host
+    *reinterpret_cast<float4*>(a.hidden_out + c0) = xa;
+    *reinterpret_cast<float4*>(a.hidden_out + c0 + 4) = xb;
+  }
   const uint32_t tr = 8 * (wave & 1u) + uint32_t(i8), k8 = uint32_t(lane & 7);
   const uint32_t vo = uint32_t(m) * 1024u + uint32_t(kq) * 16, vs = uint32_t(kq) * 128u + 2 * (wave * 4 + uint32_t(lane & 3));
   auto issue = [&](uint32_t tile, MmaCellLoads* t) {

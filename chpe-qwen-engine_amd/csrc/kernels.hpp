@@ -105,6 +105,7 @@ struct GemvArgs {
   float eps;
   ArgmaxPartial* partials;   // Logits: one per workgroup
   StepResult* result;        // Logits: workgroup 0 stores the hidden norm
+  float* hidden_out;         // Logits (matrix-core kernel): workgroup 0 copies x here when set
   RopeArgs rope;             // QkvRope
 };
 
@@ -155,6 +156,8 @@ struct FinishArgs {
   const float* logits;
   StepResult* result;
   uint32_t* out_tokens;     // argmax of every step, indexed by position
+  EmbedArgs embed;          // embed_next: the next token's row into embed.hidden (the next step's input)
+  uint32_t embed_next;
 };
 
 // Workgroup caps of the one-unit-per-wave GEMV (0 = one unit per wave, no cap); the waves of

@@ -62,8 +62,9 @@ __device__ bool unpack_embed_row_cell(const Image& im, uint64_t cell, uint32_t r
 }
 
 // unpackEmbedRow: chpe_engine.zig:1491-1552
-__global__ void __launch_bounds__(256) k_embed(EmbedArgs a) {
-  const uint32_t tok = a.state->token, D = a.D;
+// The hidden state of token `tok` (unpackEmbedRow / unpackEmbedRowCell), workgroup-parallel.
+__device__ void embed_token(const EmbedArgs& a, uint32_t tok) {
+  const uint32_t D = a.D;
   const Image im{a.image, a.image_len};
   const int tid = threadIdx.x, nt = blockDim.x;
   bool done = false;
@@ -93,6 +94,8 @@ __global__ void __launch_bounds__(256) k_embed(EmbedArgs a) {
     for (uint32_t i = tid; i < D; i += nt) a.hidden[i] = 0.05f * float(int((i + tok) % 17u) - 8);
 }
 
+__global__ void __launch_bounds__(256) k_embed(EmbedArgs a) { embed_token(a, a.state->token); }
+
 // argmax / all_finite / logits[0] over the LM head's workgroup partials (chpe_engine.zig:
 // 1775-1787), then the next position's (token, pos): the prompt while it lasts, else the argmax.
 __global__ void __launch_bounds__(256) k_finish(FinishArgs a) {
@@ -115,7 +118,8 @@ __global__ void __launch_bounds__(256) k_finish(FinishArgs a) {
   const int w = threadIdx.x >> 6;
   if ((threadIdx.x & 63) == 0) { s_v[w] = bv; s_i[w] = bi; s_nf[w] = nf; }
   __syncthreads();
-  if (threadIdx.x != 0) return;
+  __shared__ uint32_t s_next;
+  if (threadIdx.x == 0) {
   for (int k = 1; k < int(blockDim.x >> 6); ++k) {
     nf |= s_nf[k];
     if (better(s_v[k], s_i[k], bv, bi)) { bv = s_v[k]; bi = s_i[k]; }
@@ -133,6 +137,13 @@ __global__ void __launch_bounds__(256) k_finish(FinishArgs a) {
   s.pos = next;
   s.n_steps += 1;
   *a.state = s;
+  s_next = s.token;
+  }
+  // the next step's input: the embedding row of the next token (one launch less per step)
+  if (a.embed_next) {
+    __syncthreads();
+    embed_token(a.embed, s_next);
+  }
 }
 
 // dequantisation half of gemvCellFlat (chpe_engine.zig:598-699), materialised
