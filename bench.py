@@ -42,7 +42,7 @@ STAGES = {  # stage id -> (description, kernel name as rocprofv3 prints it, laun
     1: ("o GEMV + residual", f"void {NS}k_gemv_mma<1, 1>(chpe::GemvArgs)", LAYERS),
     2: ("gate/up GEMV + SwiGLU (RMSNorm fused)", f"void {NS}k_gemv_mma<2, 2>(chpe::GemvArgs)", LAYERS),
     3: ("down GEMV + residual (flat tiles)", f"void {NS}k_gemv_flat<1, 3, false, 8>(chpe::GemvArgs)", LAYERS),
-    4: ("LM head GEMV + argmax partials", f"void {NS}k_gemv_mma_logits(chpe::GemvArgs)", 1),
+    4: ("LM head GEMV + argmax partials", f"{NS}k_gemv_mma_logits(chpe::GemvArgs)", 1),
     5: ("attention over the context chunks", f"void {NS}k_attn_mfma<128, 8, 4, 1>(chpe::AttnArgs)", LAYERS),
     6: ("attention chunk merge", f"void {NS}k_attn_merge<128>(chpe::AttnArgs)", LAYERS),
 }
