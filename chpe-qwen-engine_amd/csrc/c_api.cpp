@@ -358,6 +358,96 @@ int chpe_debug_gemv_flat(int mode, uint32_t rows, uint32_t cols, const uint8_t* 
   return rc;
 }
 
+int chpe_debug_gemv_cells(int mode, uint32_t rows, const uint8_t* cells, const uint8_t* cells_up, size_t n_cells,
+                          const float* x, const float* gamma, float eps, float* y, uint32_t* out_argmax,
+                          float* out_hidden_norm) {
+  g_last_error.clear();
+  constexpr uint32_t cols = 2048;
+  const bool norm = mode == int(GemvMode::SwiGlu) || mode == int(GemvMode::Logits);
+  if (!cells || !x || !y || rows == 0 || mode < 0 || mode > int(GemvMode::Logits) || norm != (gamma != nullptr) ||
+      (mode == int(GemvMode::SwiGlu)) != (cells_up != nullptr))
+    return -1;
+  const size_t need = (size_t(rows) + 15) / 16;
+  if (n_cells < need) { g_last_error = "fewer cells than the rows need"; return -1; }
+  const int n_parts = mode == int(GemvMode::SwiGlu) ? 2 : 1;
+  const uint8_t* src[2] = {cells, cells_up};
+  for (int i = 0; i < n_parts; ++i)
+    for (size_t c = 0; c < need; ++c) {
+      const uint8_t* pl = src[i] + c * kCellBytes + kPayloadOff;
+      uint64_t flags = 0;
+      std::memcpy(&flags, pl + kMetaCustomFlags, 8);
+      if (pl[kMetaQuantBits] != 4 || !(flags & kFlagGroup128)) { g_last_error = "cells are not 4-bit group-128"; return -1; }
+    }
+  constexpr size_t kShift = 64, kPad = size_t(1) << 20;  // as the engine's archive image
+  const size_t img = kShift + need * kCellBytes + kPad;
+  std::vector<void*> mem;
+  auto alloc = [&](size_t bytes) -> void* {
+    void* d = nullptr;
+    if (hipMalloc(&d, bytes) != hipSuccess) return nullptr;
+    mem.push_back(d);
+    return d;
+  };
+  int rc = -3;
+  GemvArgs a{};
+  a.n_parts = n_parts;
+  a.mode = mode;
+  a.C = cols;
+  a.eps = eps;
+  uint32_t prow[kMaxParts] = {rows, rows, 0}, begin[kMaxParts] = {0, 0, 0};
+  const GemvLaunch g = gemv_geometry(WeightKind::Cell16W4, GemvMode(mode), cols, prow, n_parts, &a.n_units,
+                                     &a.n_panels, &a.waves_per_unit, begin);
+  float* dx = static_cast<float*>(alloc(size_t(cols) * 4));
+  float* dy = static_cast<float*>(alloc(size_t(rows) * 4));
+  float* dg = norm ? static_cast<float*>(alloc(size_t(cols) * 4)) : nullptr;
+  bool ok = dx && dy && (!norm || dg) && hipMemcpy(dx, x, size_t(cols) * 4, hipMemcpyHostToDevice) == hipSuccess &&
+            hipMemcpy(dy, y, size_t(rows) * 4, hipMemcpyHostToDevice) == hipSuccess &&
+            (!norm || hipMemcpy(dg, gamma, size_t(cols) * 4, hipMemcpyHostToDevice) == hipSuccess);
+  for (int i = 0; ok && i < n_parts; ++i) {
+    uint8_t* d = static_cast<uint8_t*>(alloc(img));
+    ok = d && hipMemset(d, 0, img) == hipSuccess &&
+         hipMemcpy(d + kShift, src[i], need * kCellBytes, hipMemcpyHostToDevice) == hipSuccess;
+    GemvPart& p = a.part[i];
+    p.base = d + kShift;
+    p.stride = uint32_t(kCellBytes);
+    p.rows = rows;
+    p.unit_begin = begin[i];
+    p.y = dy;
+  }
+  a.x = dx;
+  a.gamma = dg;
+  StepResult* dres = nullptr;
+  StepState* dst = nullptr;
+  if (ok && mode == int(GemvMode::Logits)) {
+    a.partials = static_cast<ArgmaxPartial*>(alloc(size_t(g.blocks) * sizeof(ArgmaxPartial)));
+    dres = static_cast<StepResult*>(alloc(sizeof(StepResult)));
+    dst = static_cast<StepState*>(alloc(sizeof(StepState)));
+    a.result = dres;
+    ok = a.partials && dres && dst && hipMemset(dst, 0, sizeof(StepState)) == hipSuccess;
+  }
+  if (ok) {
+    launch_gemv(WeightKind::Cell16W4, a, g, nullptr);
+    if (mode == int(GemvMode::Logits)) {
+      FinishArgs f{};
+      f.state = dst;
+      f.partials = a.partials;
+      f.n_partials = g.blocks;
+      f.logits = dy;
+      f.result = dres;
+      launch_finish(f, nullptr);
+    }
+    StepResult r{};
+    if (hipDeviceSynchronize() == hipSuccess &&
+        hipMemcpy(y, dy, size_t(rows) * 4, hipMemcpyDeviceToHost) == hipSuccess &&
+        (!dres || hipMemcpy(&r, dres, sizeof r, hipMemcpyDeviceToHost) == hipSuccess)) {
+      if (dres && out_argmax) *out_argmax = r.argmax;
+      if (dres && out_hidden_norm) *out_hidden_norm = r.hidden_norm;
+      rc = 0;
+    }
+  }
+  for (void* p : mem) (void)hipFree(p);
+  return rc;
+}
+
 int chpe_debug_embed_row_cell(const uint8_t* bytes, size_t len, uint32_t row, uint32_t D, float* out) {
   if (!bytes || !out || len < kCellBytes || D == 0 || D % 128) return -1;
   uint8_t* db = nullptr;

@@ -113,6 +113,15 @@ int chpe_debug_flat_tile_weights(const uint8_t *cell, float *out32768);
 int chpe_debug_gemv_flat(int mode, uint32_t rows, uint32_t cols, const uint8_t *tiles,
                          const uint8_t *tiles_up, size_t n_tiles, const float *x, const float *gamma,
                          float eps, float *y, uint32_t *out_argmax, float *out_hidden_norm);
+/* One 16-row-cell GEMV at 2048 columns (gemvTileW4, src/chpe_engine.zig:326-418, per cell of
+ * 16 rows; outliers added) through the decode step's kernels on caller cells: `cells` (and
+ * `cells_up` for mode 2) hold ceil(rows/16) consecutive 17408-byte 4-bit group-128 cells; mode
+ * and the other arguments as for chpe_debug_gemv_flat (x has 2048 floats; mode 3 writes the
+ * logits, the first index of the maximum and the norm of x).  Returns 0, -1 on bad arguments
+ * or cells (chpe_last_error), -3 on a device error. */
+int chpe_debug_gemv_cells(int mode, uint32_t rows, const uint8_t *cells, const uint8_t *cells_up,
+                          size_t n_cells, const float *x, const float *gamma, float eps, float *y,
+                          uint32_t *out_argmax, float *out_hidden_norm);
 /* unpackEmbedRowCell on the GPU over `len` bytes starting at a cell (rows of wide tensors
  * read past the cell).  Returns 1 if written, 0 if the row is out of range, <0 on error. */
 int chpe_debug_embed_row_cell(const uint8_t *bytes, size_t len, uint32_t row, uint32_t D,
