@@ -257,6 +257,7 @@ bool Engine::init(const uint8_t* b, size_t len, const EngineConfig& cfg, std::st
   }
   d_rope_cos_ = upload_vector(cs);
   d_rope_sin_ = upload_vector(sn);
+  d_rope_cur_ = static_cast<float*>(dev_alloc(hd * 4));
   HIP_TRY(hipHostMalloc(reinterpret_cast<void**>(&h_state_), sizeof(StepState), hipHostMallocDefault));
   HIP_TRY(hipHostMalloc(reinterpret_cast<void**>(&h_result_), sizeof(StepResult), hipHostMallocDefault));
   HIP_TRY(hipDeviceSynchronize());
@@ -558,8 +559,8 @@ RopeArgs Engine::rope_args(size_t l) const {
   const size_t kv_elem = cfg_.kv_f16 ? 2 : 4;
   RopeArgs r{};
   r.state = d_state_;
-  r.cos = d_rope_cos_;
-  r.sin = d_rope_sin_;
+  r.cos = d_rope_cur_;
+  r.sin = d_rope_cur_ + arch_.head_dim / 2;
   r.k_cache = static_cast<uint8_t*>(d_kcache_) + l * kvd * S * kv_elem;
   r.v_cache = static_cast<uint8_t*>(d_vcache_) + l * kvd * S * kv_elem;
   r.head_dim = uint32_t(arch_.head_dim);
@@ -600,6 +601,11 @@ EmbedArgs Engine::embed_args() const {
   e.record_count = record_count_;
   e.stride = stride_;
   e.cell_off = is_dense_ ? 0 : kPrefetchBytes;
+  e.rope_cos = d_rope_cos_;
+  e.rope_sin = d_rope_sin_;
+  e.rope_cur = d_rope_cur_;
+  e.rope_half = uint32_t(arch_.head_dim / 2);
+  e.rope_rows = uint32_t(cfg_.max_seq_len);
   return e;
 }
 

@@ -185,6 +185,7 @@ class Engine {
   bool use_graph_ = true;
   bool embed_fused_ = false;         // k_finish embeds the next token (see init)
   float* d_hidden_out_ = nullptr;    // the last step's final hidden state when embed_fused_
+  float* d_rope_cur_ = nullptr;      // the step's cos / sin rows (head_dim floats)
   int probe_stage_ = -1;                 // stage bracketed by events in record_step
   hipEvent_t* probe_events_ = nullptr;
   size_t probe_next_ = 0;

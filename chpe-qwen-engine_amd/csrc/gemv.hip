@@ -533,7 +533,7 @@ __device__ __forceinline__ void issue_unit(const GemvArgs& a, uint32_t unit, uin
   }
   if constexpr (kRope) {  // cos / sin of the pair (j, j + half) served by lane S * i, i < RU/2
     const bool ok = with_pre && active && (lane % S) == 0 && lane < 32 && P0.rope_role != kRoleV;
-    const size_t at = ok ? size_t(a.rope.state->pos) * half + (own % (2 * half)) : 0u;
+    const size_t at = ok ? (own % (2 * half)) : 0u;  // (the step's cos / sin row, staged)
     u->rc = a.rope.cos[at];
     u->rs = a.rope.sin[at];
     u->rope_ok = ok;
@@ -793,7 +793,7 @@ __global__ void __launch_bounds__(512, 2) k_gemv_split(GemvArgs a) {
         pre = MODE == int(GemvMode::Accum) ? P0.y[own] : (P0.bias ? P0.bias[own] : 0.0f);
         if constexpr (kRope) {
           if (lane < 32 && P0.rope_role != kRoleV) {
-            const size_t at = size_t(a.rope.state->pos) * half + (own % (2 * half));
+            const size_t at = own % (2 * half);
             rc = a.rope.cos[at];
             rs = a.rope.sin[at];
           }
@@ -963,7 +963,7 @@ __global__ void __launch_bounds__(kWave * kCellWaves) k_gemv_cells(GemvArgs a) {
   }
   if constexpr (kRope) {
     rope_ok = elive && (lane % S) == 0 && lane < 32 && erole != kRoleV;
-    const size_t at = rope_ok ? size_t(a.rope.state->pos) * half + (orow % (2 * half)) : 0u;
+    const size_t at = rope_ok ? (orow % (2 * half)) : 0u;
     rc = a.rope.cos[at];
     rs = a.rope.sin[at];
   }
@@ -1212,9 +1212,7 @@ __global__ void __launch_bounds__(kWave * kMmaWaves) k_gemv_mma(GemvArgs a) {
   args_batch<MODE>(a);
   const uint32_t half = a.rope.head_dim / 2, tile0 = blockIdx.x * UPW;
 
-  // 1. loads: the position (QkvRope: the RoPE row of the epilogue depends on it), the input
-  // (columns c0 .. c0 + 7 of x and gamma), then the weights
-  const uint32_t rpos = kRope ? a.rope.state->pos : 0u;
+  // 1. loads: the input (columns c0 .. c0 + 7 of x and gamma), then the weights
   const uint32_t c0 = wave * 512 + uint32_t(lane) * 8;
   const float4 xa = ld_f4(a.x + c0), xb = ld_f4(a.x + c0 + 4);
   float4 ga = make_float4(1.f, 1.f, 1.f, 1.f), gb = ga;
@@ -1315,7 +1313,7 @@ __global__ void __launch_bounds__(kWave * kMmaWaves) k_gemv_mma(GemvArgs a) {
   if constexpr (kRope) {  // the pair's dimension: (first row of part A mod head_dim) + 4 eh + i < half
     rope_ok = ovalid && (lane % S) == 0 && !oB && erole != kRoleV;
     const uint32_t fa = erA != 0xffffffffu ? erA : 0u, dA = fa - (fa / (2 * half)) * (2 * half);
-    const size_t at = size_t(rpos) * half + (dA + 4 * eh + uint32_t(i8 & 3));
+    const size_t at = dA + 4 * eh + uint32_t(i8 & 3);
     rc = a.rope.cos[at];
     rs = a.rope.sin[at];
   }
@@ -1561,7 +1559,7 @@ __global__ void __launch_bounds__(kWave * W) k_gemv_flat(GemvArgs a) {
   }
   if constexpr (kRope) {
     rope_ok = (lane % S) == 0 && lane < 32 && P0.rope_role != kRoleV;
-    const size_t at = rope_ok ? size_t(a.rope.state->pos) * half + (orow % (2 * half)) : 0u;
+    const size_t at = rope_ok ? (orow % (2 * half)) : 0u;
     rc = a.rope.cos[at];
     rs = a.rope.sin[at];
   }

@@ -41,8 +41,8 @@ struct StepState;
 
 struct RopeArgs {            // QkvRope: applyRope (chpe_engine.zig:195-216) + KV append (:1693-1697)
   const StepState* state;
-  const float* cos;          // [max_seq][head_dim/2]
-  const float* sin;
+  const float* cos;          // [head_dim/2]: the step's row of the cos table (staged by k_embed /
+  const float* sin;          //   k_finish from the [max_seq][head_dim/2] tables), and of sin
   void* k_cache;             // this layer: [KV][max_seq][head_dim], f16 or f32
   void* v_cache;             // f32: as k_cache; f16: [KV][max_seq/4][head_dim][4] (4-position blocks)
   uint32_t head_dim, max_seq, kv_f16, pad;  // max_seq: cache rows per kv head, a multiple of 16
@@ -133,6 +133,13 @@ struct EmbedArgs {
   uint64_t record_count;
   uint64_t stride;          // record stride
   uint64_t cell_off;        // offset of the cell inside a record
+  // the step's RoPE factors: rows `pos` of the [rope_rows][rope_half] cos / sin tables into
+  // rope_cur[0, rope_half) / [rope_half, 2 rope_half) (so that the q/k/v launch loads them
+  // without waiting for the position)
+  const float* rope_cos;
+  const float* rope_sin;
+  float* rope_cur;
+  uint32_t rope_half, rope_rows;
 };
 
 struct AttnArgs {

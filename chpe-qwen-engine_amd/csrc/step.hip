@@ -63,8 +63,12 @@ __device__ bool unpack_embed_row_cell(const Image& im, uint64_t cell, uint32_t r
 
 // unpackEmbedRow: chpe_engine.zig:1491-1552
 // The hidden state of token `tok` (unpackEmbedRow / unpackEmbedRowCell), workgroup-parallel.
-__device__ void embed_token(const EmbedArgs& a, uint32_t tok) {
+__device__ void embed_token(const EmbedArgs& a, uint32_t tok, uint32_t pos) {
   const uint32_t D = a.D;
+  if (a.rope_cur && pos < a.rope_rows)  // the step's RoPE row (a position past the tables: none)
+    for (uint32_t i = threadIdx.x; i < 2 * a.rope_half; i += blockDim.x)
+      a.rope_cur[i] = i < a.rope_half ? a.rope_cos[size_t(pos) * a.rope_half + i]
+                                      : a.rope_sin[size_t(pos) * a.rope_half + (i - a.rope_half)];
   const Image im{a.image, a.image_len};
   const int tid = threadIdx.x, nt = blockDim.x;
   bool done = false;
@@ -94,7 +98,7 @@ __device__ void embed_token(const EmbedArgs& a, uint32_t tok) {
     for (uint32_t i = tid; i < D; i += nt) a.hidden[i] = 0.05f * float(int((i + tok) % 17u) - 8);
 }
 
-__global__ void __launch_bounds__(256) k_embed(EmbedArgs a) { embed_token(a, a.state->token); }
+__global__ void __launch_bounds__(256) k_embed(EmbedArgs a) { embed_token(a, a.state->token, a.state->pos); }
 
 // argmax / all_finite / logits[0] over the LM head's workgroup partials (chpe_engine.zig:
 // 1775-1787), then the next position's (token, pos): the prompt while it lasts, else the argmax.
@@ -118,7 +122,7 @@ __global__ void __launch_bounds__(256) k_finish(FinishArgs a) {
   const int w = threadIdx.x >> 6;
   if ((threadIdx.x & 63) == 0) { s_v[w] = bv; s_i[w] = bi; s_nf[w] = nf; }
   __syncthreads();
-  __shared__ uint32_t s_next;
+  __shared__ uint32_t s_next, s_next_pos;
   if (threadIdx.x == 0) {
   for (int k = 1; k < int(blockDim.x >> 6); ++k) {
     nf |= s_nf[k];
@@ -138,11 +142,12 @@ __global__ void __launch_bounds__(256) k_finish(FinishArgs a) {
   s.n_steps += 1;
   *a.state = s;
   s_next = s.token;
+  s_next_pos = s.pos;
   }
   // the next step's input: the embedding row of the next token (one launch less per step)
   if (a.embed_next) {
     __syncthreads();
-    embed_token(a.embed, s_next);
+    embed_token(a.embed, s_next, s_next_pos);
   }
 }
 
