@@ -250,7 +250,9 @@ __device__ __forceinline__ float cell_outlier_sum(const CellExtras<8>& e, const 
     float w;
     if constexpr (kReplace) w = __uint_as_float(k < 4 ? w0[k] : w1[k - 4]);
     else w = (k & 1) ? half_hi(w0[k >> 1]) : half_lo(w0[k >> 1]);
-    if (c < C) o = fmaf(w, s_x[xs_at(c)], o);
+    // branch-free: every entry reads LDS (at column 0 when absent), so the reads issue together
+    const float t = fmaf(w, s_x[xs_at(c < C ? c : 0u)], o);
+    o = c < C ? t : o;
   }
   return e.valid ? o : 0.0f;
 }
@@ -296,8 +298,12 @@ __device__ __forceinline__ void load_flat_extras(const GemvPart& P0, const GemvP
 __device__ __forceinline__ float flat_correction(const FlatExtras& f, const float* s_x) {
   float cs = 0.0f;
 #pragma unroll
-  for (int j = 0; j < kCorrSlots; ++j)
-    if (((f.use >> j) & 1u) && f.e[j].y != 0.0f) cs = fmaf(f.e[j].y, s_x[xs_at(__float_as_uint(f.e[j].x))], cs);
+  for (int j = 0; j < kCorrSlots; ++j) {
+    // branch-free: every slot reads LDS (at column 0 when unused), so the reads issue together
+    const bool on = ((f.use >> j) & 1u) && f.e[j].y != 0.0f;
+    const float t = fmaf(f.e[j].y, s_x[xs_at(on ? __float_as_uint(f.e[j].x) : 0u)], cs);
+    cs = on ? t : cs;
+  }
   cs = pair_sum(cs, 1);
   cs = pair_sum(cs, 2);
   cs = pair_sum(cs, 4);
@@ -1491,10 +1497,10 @@ __global__ void __launch_bounds__(kWave * kMmaWaves) k_gemv_mma_logits(GemvArgs 
 // SIMD) striding over panels of 512 columns (4 groups of 128; panel p goes to wave p % 8).
 // Lane (j, c) = (lane / 16, lane % 16) holds unit rows j and j + 4 at columns 512 p + 32 c ..
 // + 31 of each of its wave's panels: one 16-byte code load and one group scale per row and
-// panel, all issued before the input staging waits (up to MAXP panels per wave).  Row sums meet
-// over the 16 lanes (DPP) and the waves (LDS, in wave order); wave 0 adds the row's outlier
-// corrections and runs the epilogue.  The input sits in LDS (dynamic, C floats) for the dots
-// and for the corrections, which read any column.
+// panel, all issued before the input staging waits (up to MAXP panels per wave), then one
+// outlier-correction entry per row and lane.  Row sums meet over the 16 lanes (DPP) and the
+// waves (LDS, in wave order); wave 0 runs the epilogue.  The input sits in LDS (dynamic, C
+// floats) for the dots and for the corrections, which read any column.
 constexpr int kFlatWaves = 8;
 template <int MODE, int MAXP, bool kWide, int W = kFlatWaves>
 __global__ void __launch_bounds__(kWave * W) k_gemv_flat(GemvArgs a) {
@@ -1520,6 +1526,7 @@ __global__ void __launch_bounds__(kWave * W) k_gemv_flat(GemvArgs a) {
   // 1. the input first, then codes and scales of rows j and j + 4 for each of the wave's panels
   StageRegs<SL> xr;
   if constexpr (!kWide) stage_x_issue<kNorm, SL, NT>(a, &xr);
+  __builtin_amdgcn_sched_barrier(0);  // every input load ahead of the code loads
   const uint32_t rowA = row_of<RU, MODE>(row_base, j, half), rowB = row_of<RU, MODE>(row_base, j + RU / 2, half);
   const bool okA = rowA < P0.rows, okB = rowB < P1.rows;
   // 32-bit group indices and byte offsets from the part's base (a uniform 64-bit pointer), so
@@ -1544,10 +1551,28 @@ __global__ void __launch_bounds__(kWave * W) k_gemv_flat(GemvArgs a) {
     sa[q] = ld_u16(baseA + sa_off);
     sb[q] = ld_u16(baseB + sb_off);
   }
-  // wave 0's epilogue operands: the rows' correction entries, lane 8 i's residual / bias / RoPE
-  FlatExtras fe;
-  fe.use = 0;
-  if (wave == 0) load_flat_extras<RU, MODE>(P0, P1, row_base, half, lane, true, a.x, &fe);
+  // the rows' outlier corrections, spread over every wave: lane (j, c) of wave w takes entries
+  // c + 16 (w + W t) of rows j and j + 4, so all waves issue the same loads (the waits stay
+  // exact) and the corrections join the row sums before the lane reduction
+  constexpr int SPL = int(kMaxCorrPerRow + 16 * W - 1) / (16 * W);
+  float2 ca[SPL], cb[SPL];
+  uint32_t cuse = 0;
+  {
+    const float2* corrA = uni(P0.corr);
+    const float2* corrB = uni(P1.corr);
+    const uint32_t kmA = uni(P0.corr_kmax), kmB = uni(P1.corr_kmax);
+    const float2* srcA = corrA ? corrA : reinterpret_cast<const float2*>(a.x);
+    const float2* srcB = corrB ? corrB : reinterpret_cast<const float2*>(a.x);
+#pragma unroll
+    for (int t = 0; t < SPL; ++t) {
+      const uint32_t e = uint32_t(c) + 16u * (wave + uint32_t(W * t));
+      const bool ua = corrA != nullptr && okA && e < kmA, ub = corrB != nullptr && okB && e < kmB;
+      ca[t] = srcA[ua ? size_t(rowA) * kmA + e : 0];
+      cb[t] = srcB[ub ? size_t(rowB) * kmB + e : 0];
+      cuse |= (uint32_t(ua) << (2 * t)) | (uint32_t(ub) << (2 * t + 1));
+    }
+  }
+  // lane 8 i's residual / bias / RoPE operands
   const int i8 = lane >> 3;
   const uint32_t orow = row_of<RU, MODE>(row_base, i8, half);
   float pre = 0.0f, rc = 1.0f, rs = 0.0f;
@@ -1564,7 +1589,8 @@ __global__ void __launch_bounds__(kWave * W) k_gemv_flat(GemvArgs a) {
     rs = a.rope.sin[at];
   }
 
-  // 2. the (normalised) input into LDS
+  // 2. the (normalised) input into LDS, once every load above is issued
+  __builtin_amdgcn_sched_barrier(0);
   float ss = 0.0f, inv = 1.0f;
   stage_x_finish<kNorm, kWide, SL, NT>(a, xr, s_x, s_red, &ss, &inv);
 
@@ -1589,6 +1615,16 @@ __global__ void __launch_bounds__(kWave * W) k_gemv_flat(GemvArgs a) {
     accA += gv ? tA : 0.0f;
     accB += gv ? tB : 0.0f;
   }
+  // corrections (w_out - dequantised code) * x[col], branch-free: unused entries read column 0
+#pragma unroll
+  for (int t = 0; t < SPL; ++t) {
+    const bool ua = ((cuse >> (2 * t)) & 1u) && ca[t].y != 0.0f;
+    const bool ub = ((cuse >> (2 * t + 1)) & 1u) && cb[t].y != 0.0f;
+    const float xa = s_x[xs_at(ua ? __float_as_uint(ca[t].x) : 0u)];
+    const float xb = s_x[xs_at(ub ? __float_as_uint(cb[t].x) : 0u)];
+    accA = ua ? fmaf(ca[t].y, xa, accA) : accA;
+    accB = ub ? fmaf(cb[t].y, xb, accB) : accB;
+  }
   accA = okA ? accA : 0.0f;
   accB = okB ? accB : 0.0f;
 #pragma unroll
@@ -1603,11 +1639,10 @@ __global__ void __launch_bounds__(kWave * W) k_gemv_flat(GemvArgs a) {
   __syncthreads();
   if (wave != 0) return;
 
-  // 4. wave 0: row i8 on lanes 8 i8 .. 8 i8 + 7, its corrections, the epilogue
+  // 4. wave 0: row i8 on lanes 8 i8 .. 8 i8 + 7, the epilogue
   float v = 0.0f;
 #pragma unroll
   for (int w = 0; w < W; ++w) v += s_part[w][i8];
-  v += flat_correction(fe, s_x);
   const float up = (kSwi || kRope) ? pair_val(v, 32) : 0.0f;
   const float prev = pre_ok ? pre : 0.0f;
   const float up_pre = kRope ? pair_val(prev, 32) : 0.0f;
