@@ -12,8 +12,67 @@ using namespace dev;
 // `cell` of the image, workgroup-parallel over columns.  Returns false when the row is out
 // of the cell's range (then `out` is left untouched, as in the reference).  Wide rows
 // (D >= 4096) read past the cell into the following records, by byte address as on the CPU.
+//
+// Fast path for the 4-bit group-128 cells when every byte it reads lies inside the image: the
+// header, the codes (one 32-bit word per 8 columns), the group scales and the 8 outlier entries
+// are all requested before any is used (the step's final kernel waits on this chain once).
+constexpr int kEmbedWords = 4;  // 8-column words per thread (D <= 8 * 4 * blockDim.x)
+__device__ bool unpack_embed_row_cell_fast(const Image& im, uint64_t cell, uint32_t row, uint32_t D,
+                                           float* out, bool* handled) {
+  const uint32_t tid = threadIdx.x, nt = blockDim.x, ng = D / 128;
+  const uint64_t codes = cell + 64, pl = cell + 16448;
+  *handled = false;
+  if (row >= 16 || D % 128 != 0 || D > 8 * uint32_t(kEmbedWords) * nt) return false;
+  if ((reinterpret_cast<uintptr_t>(im.p) & 3u) != 0 || (cell & 3u) != 0) return false;
+  if (cell + 17408 > im.len || codes + uint64_t(row + 1) * (D / 2) > im.len ||
+      pl + 48 + 2 * uint64_t(row + 1) * ng > im.len)
+    return false;
+  const uint8_t* P = im.p;
+  const uint32_t qb = P[pl + 20];
+  const uint32_t flags = *reinterpret_cast<const uint32_t*>(P + pl + 24);
+  uint32_t w[kEmbedWords];
+  uint16_t sv[kEmbedWords];
+#pragma unroll
+  for (int k = 0; k < kEmbedWords; ++k) {
+    const uint32_t i0 = (tid + uint32_t(k) * nt) * 8, ic = i0 < D ? i0 : 0u;
+    w[k] = *reinterpret_cast<const uint32_t*>(P + codes + uint64_t(row) * (D / 2) + ic / 2);
+    sv[k] = *reinterpret_cast<const uint16_t*>(P + pl + 48 + 2 * (uint64_t(row) * ng + ic / 128));
+  }
+  const uint32_t e = tid < 8 ? tid : 0u;
+  const uint32_t ocol = *reinterpret_cast<const uint16_t*>(P + pl + 816 + 2 * e);
+  const uint16_t ow = *reinterpret_cast<const uint16_t*>(P + pl + 560 + 2 * (row * 8 + e));
+  if (qb != 4 || (flags & 1u) == 0) return false;  // (uniform) the generic path decodes the cell
+  *handled = true;
+#pragma unroll
+  for (int k = 0; k < kEmbedWords; ++k) {
+    const uint32_t i0 = (tid + uint32_t(k) * nt) * 8;
+    if (i0 < D) {
+      const float sc = h2f(sv[k]);
+      float v[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v[j] = (float((w[k] >> (4 * j)) & 15u) - 8.0f) * sc;
+      *reinterpret_cast<float4*>(out + i0) = make_float4(v[0], v[1], v[2], v[3]);
+      *reinterpret_cast<float4*>(out + i0 + 4) = make_float4(v[4], v[5], v[6], v[7]);
+    }
+  }
+  // outliers replace, in entry order: an entry overridden by a later one for the same column
+  // is skipped, so the 8 entries store in parallel (after the row's stores: the barrier)
+  __shared__ uint32_t s_oc[8];
+  if (tid < 8) s_oc[tid] = ocol;
+  __syncthreads();
+  if (tid < 8 && ocol < D) {
+    bool later = false;
+    for (uint32_t j = tid + 1; j < 8; ++j) later |= s_oc[j] == ocol;
+    if (!later) out[ocol] = h2f(ow);
+  }
+  return true;
+}
+
 __device__ bool unpack_embed_row_cell(const Image& im, uint64_t cell, uint32_t row, uint32_t D,
                                       float* out) {
+  bool handled = false;
+  const bool ok = unpack_embed_row_cell_fast(im, cell, row, D, out, &handled);
+  if (handled) return ok;
   const uint64_t codes = cell + 64, pl = cell + 16448;
   const uint8_t qb = im.u8(pl + 20);
   const bool g128 = (im.u64(pl + 24) & 1u) != 0;
@@ -63,12 +122,16 @@ __device__ bool unpack_embed_row_cell(const Image& im, uint64_t cell, uint32_t r
 
 // unpackEmbedRow: chpe_engine.zig:1491-1552
 // The hidden state of token `tok` (unpackEmbedRow / unpackEmbedRowCell), workgroup-parallel.
-__device__ void embed_token(const EmbedArgs& a, uint32_t tok, uint32_t pos) {
-  const uint32_t D = a.D;
-  if (a.rope_cur && pos < a.rope_rows)  // the step's RoPE row (a position past the tables: none)
+// the step's RoPE row (cos then sin of position pos; a position past the tables: none)
+__device__ void stage_rope_row(const EmbedArgs& a, uint32_t pos) {
+  if (a.rope_cur && pos < a.rope_rows)
     for (uint32_t i = threadIdx.x; i < 2 * a.rope_half; i += blockDim.x)
       a.rope_cur[i] = i < a.rope_half ? a.rope_cos[size_t(pos) * a.rope_half + i]
                                       : a.rope_sin[size_t(pos) * a.rope_half + (i - a.rope_half)];
+}
+
+__device__ void embed_token(const EmbedArgs& a, uint32_t tok) {
+  const uint32_t D = a.D;
   const Image im{a.image, a.image_len};
   const int tid = threadIdx.x, nt = blockDim.x;
   bool done = false;
@@ -98,11 +161,27 @@ __device__ void embed_token(const EmbedArgs& a, uint32_t tok, uint32_t pos) {
     for (uint32_t i = tid; i < D; i += nt) a.hidden[i] = 0.05f * float(int((i + tok) % 17u) - 8);
 }
 
-__global__ void __launch_bounds__(256) k_embed(EmbedArgs a) { embed_token(a, a.state->token, a.state->pos); }
+__global__ void __launch_bounds__(256) k_embed(EmbedArgs a) {
+  stage_rope_row(a, a.state->pos);
+  embed_token(a, a.state->token);
+}
 
 // argmax / all_finite / logits[0] over the LM head's workgroup partials (chpe_engine.zig:
 // 1775-1787), then the next position's (token, pos): the prompt while it lasts, else the argmax.
 __global__ void __launch_bounds__(256) k_finish(FinishArgs a) {
+  // what does not wait for the argmax first: the state, the next position's RoPE row and its
+  // prompt token (the step's q/k/v launch has read the current row already)
+  const StepState s0 = *a.state;
+  const uint32_t next = s0.pos + 1;
+  const uint32_t ptok = (a.prompt && next < s0.n_prompt) ? a.prompt[next] : 0u;
+  const float logit0 = a.logits[0];
+  const EmbedArgs& e = a.embed;
+  const uint32_t t = threadIdx.x, rn = 2 * e.rope_half;  // one element per thread when it fits
+  const bool rope = a.embed_next && e.rope_cur && next < e.rope_rows;
+  const bool rope_regs = rn <= blockDim.x;
+  float rv = 0.0f;
+  if (rope && rope_regs && t < rn)
+    rv = t < e.rope_half ? e.rope_cos[size_t(next) * e.rope_half + t] : e.rope_sin[size_t(next) * e.rope_half + (t - e.rope_half)];
   float bv = -1e30f;
   uint32_t bi = 0xffffffffu, nf = 0;
   for (uint32_t i = threadIdx.x; i < a.n_partials; i += blockDim.x) {
@@ -117,12 +196,14 @@ __global__ void __launch_bounds__(256) k_finish(FinishArgs a) {
     nf |= pair_u(nf, o);
     if (better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
   }
+  if (rope && rope_regs && t < rn) e.rope_cur[t] = rv;
+  if (rope && !rope_regs) stage_rope_row(e, next);
   __shared__ float s_v[4];
   __shared__ uint32_t s_i[4], s_nf[4];
   const int w = threadIdx.x >> 6;
   if ((threadIdx.x & 63) == 0) { s_v[w] = bv; s_i[w] = bi; s_nf[w] = nf; }
   __syncthreads();
-  __shared__ uint32_t s_next, s_next_pos;
+  __shared__ uint32_t s_next;
   if (threadIdx.x == 0) {
   for (int k = 1; k < int(blockDim.x >> 6); ++k) {
     nf |= s_nf[k];
@@ -132,22 +213,20 @@ __global__ void __launch_bounds__(256) k_finish(FinishArgs a) {
   StepResult* r = a.result;
   r->argmax = arg;
   r->max_logit = bv;
-  r->token0_logit = a.logits[0];
+  r->token0_logit = logit0;
   r->all_finite = nf ? 0u : 1u;
-  StepState s = *a.state;
+  StepState s = s0;
   if (a.out_tokens) a.out_tokens[s.pos] = arg;
-  const uint32_t next = s.pos + 1;
-  s.token = (a.prompt && next < s.n_prompt) ? a.prompt[next] : arg;
+  s.token = (a.prompt && next < s.n_prompt) ? ptok : arg;
   s.pos = next;
   s.n_steps += 1;
   *a.state = s;
   s_next = s.token;
-  s_next_pos = s.pos;
   }
   // the next step's input: the embedding row of the next token (one launch less per step)
   if (a.embed_next) {
     __syncthreads();
-    embed_token(a.embed, s_next, s_next_pos);
+    embed_token(a.embed, s_next);
   }
 }
 

@@ -88,6 +88,17 @@ def test_embed_row_unpack_bit_exact(w4_archive, D_):
         ro, o = orc.embed_row_cell(region, row, D_, init)
         assert rg == ro
         assert np.array_equal(bits(g), bits(o))
+    # outlier entries 1 and 5 on one column (the later one wins), entry 3 past the row
+    cols = region[16448 + 816:16448 + 832].view(np.uint16)
+    cols[1] = cols[5] = 10
+    cols[3] = 65535
+    for row in (0, 9):
+        say(f"embed row cell D={D_} row={row} (repeated / out-of-range outlier columns)")
+        init = np.full(D_, 7.0, np.float32)
+        rg, g = ca.gpu_embed_row_cell(region, row, D_, init)
+        ro, o = orc.embed_row_cell(region, row, D_, init)
+        assert rg == ro
+        assert np.array_equal(bits(g), bits(o))
 
 
 @pytest.mark.parametrize("layer", [0, 21, 35])
