@@ -1524,8 +1524,22 @@ __global__ void __launch_bounds__(kWave * W) k_gemv_flat(GemvArgs a) {
   const uint32_t row_base = cells_row_base<MODE>(P0, unit, half);
 
   // 1. the input first, then codes and scales of rows j and j + 4 for each of the wave's panels
+  // Without the norm (kLocal), a wave stages only its own panels' columns (the only ones its
+  // dots read) and no workgroup barrier precedes the dots; the corrections then read their
+  // input columns from global memory.
+  constexpr bool kLocal = !kNorm && !kWide;
   StageRegs<SL> xr;
-  if constexpr (!kWide) stage_x_issue<kNorm, SL, NT>(a, &xr);
+  float4 xl[MAXP][2];
+  if constexpr (kLocal) {
+#pragma unroll
+    for (int q = 0; q < MAXP; ++q) {
+      const uint32_t col = 512 * (wave + W * uint32_t(q)) + 8 * uint32_t(lane), cl = col < C ? col : 0u;
+      xl[q][0] = ld_f4(a.x + cl);
+      xl[q][1] = ld_f4(a.x + cl + 4);
+    }
+  } else if constexpr (!kWide) {
+    stage_x_issue<kNorm, SL, NT>(a, &xr);
+  }
   __builtin_amdgcn_sched_barrier(0);  // every input load ahead of the code loads
   const uint32_t rowA = row_of<RU, MODE>(row_base, j, half), rowB = row_of<RU, MODE>(row_base, j + RU / 2, half);
   const bool okA = rowA < P0.rows, okB = rowB < P1.rows;
@@ -1592,7 +1606,29 @@ __global__ void __launch_bounds__(kWave * W) k_gemv_flat(GemvArgs a) {
   // 2. the (normalised) input into LDS, once every load above is issued
   __builtin_amdgcn_sched_barrier(0);
   float ss = 0.0f, inv = 1.0f;
-  stage_x_finish<kNorm, kWide, SL, NT>(a, xr, s_x, s_red, &ss, &inv);
+  if constexpr (kLocal) {
+#pragma unroll
+    for (int q = 0; q < MAXP; ++q) {
+      const uint32_t col = 512 * (wave + W * uint32_t(q)) + 8 * uint32_t(lane);
+      if (col < C) {
+        *reinterpret_cast<float4*>(s_x + xs_at(col)) = xl[q][0];
+        *reinterpret_cast<float4*>(s_x + xs_at(col) + 4) = xl[q][1];
+      }
+    }
+    __builtin_amdgcn_wave_barrier();  // (one wave's LDS accesses execute in order)
+  } else {
+    stage_x_finish<kNorm, kWide, SL, NT>(a, xr, s_x, s_red, &ss, &inv);
+  }
+  // the corrections' input columns (kLocal: from global memory, requested before the dots)
+  float xca[SPL], xcb[SPL];
+#pragma unroll
+  for (int t = 0; t < SPL; ++t) {
+    const bool ua = ((cuse >> (2 * t)) & 1u) && ca[t].y != 0.0f;
+    const bool ub = ((cuse >> (2 * t + 1)) & 1u) && cb[t].y != 0.0f;
+    const uint32_t qa = ua ? __float_as_uint(ca[t].x) : 0u, qb = ub ? __float_as_uint(cb[t].x) : 0u;
+    xca[t] = kLocal ? a.x[qa] : s_x[xs_at(qa)];
+    xcb[t] = kLocal ? a.x[qb] : s_x[xs_at(qb)];
+  }
 
   // 3. the dots of the wave's panels, summed over the 16 lanes of each row, then over the waves
   float accA = 0.0f, accB = 0.0f;
@@ -1620,10 +1656,8 @@ __global__ void __launch_bounds__(kWave * W) k_gemv_flat(GemvArgs a) {
   for (int t = 0; t < SPL; ++t) {
     const bool ua = ((cuse >> (2 * t)) & 1u) && ca[t].y != 0.0f;
     const bool ub = ((cuse >> (2 * t + 1)) & 1u) && cb[t].y != 0.0f;
-    const float xa = s_x[xs_at(ua ? __float_as_uint(ca[t].x) : 0u)];
-    const float xb = s_x[xs_at(ub ? __float_as_uint(cb[t].x) : 0u)];
-    accA = ua ? fmaf(ca[t].y, xa, accA) : accA;
-    accB = ub ? fmaf(cb[t].y, xb, accB) : accB;
+    accA = ua ? fmaf(ca[t].y, xca[t], accA) : accA;
+    accB = ub ? fmaf(cb[t].y, xcb[t], accB) : accB;
   }
   accA = okA ? accA : 0.0f;
   accB = okB ? accB : 0.0f;
