@@ -1497,10 +1497,11 @@ __global__ void __launch_bounds__(kWave * kMmaWaves) k_gemv_mma_logits(GemvArgs 
 // SIMD) striding over panels of 512 columns (4 groups of 128; panel p goes to wave p % 8).
 // Lane (j, c) = (lane / 16, lane % 16) holds unit rows j and j + 4 at columns 512 p + 32 c ..
 // + 31 of each of its wave's panels: one 16-byte code load and one group scale per row and
-// panel, all issued before the input staging waits (up to MAXP panels per wave), then one
+// panel, all issued before the input staging waits (up to MAXP panels per wave), after one
 // outlier-correction entry per row and lane.  Row sums meet over the 16 lanes (DPP) and the
 // waves (LDS, in wave order); wave 0 runs the epilogue.  The input sits in LDS (dynamic, C
-// floats) for the dots and for the corrections, which read any column.
+// floats) for the dots and for the corrections, which read any column; without the norm each
+// wave stages only its own panels and the corrections read their columns from global memory.
 constexpr int kFlatWaves = 8;
 template <int MODE, int MAXP, bool kWide, int W = kFlatWaves>
 __global__ void __launch_bounds__(kWave * W) k_gemv_flat(GemvArgs a) {
@@ -1549,22 +1550,6 @@ __global__ void __launch_bounds__(kWave * W) k_gemv_flat(GemvArgs a) {
   const uint8_t* baseA = P0.base;
   const uint8_t* baseB = P1.base;
   const uint32_t strA = P0.stride, strB = P1.stride, lo16 = uint32_t(c & 3) * 16;
-  uint4 qa[MAXP], qb[MAXP];
-  uint32_t sa[MAXP], sb[MAXP], gvm = 0;
-#pragma unroll
-  for (int q = 0; q < MAXP; ++q) {
-    const uint32_t p = wave + W * uint32_t(q), g = 4 * p + uint32_t(c >> 2);
-    const bool gv = p < npan && g < ng;
-    gvm |= uint32_t(gv) << q;
-    const uint32_t Ga = GA + (gv ? g : 0u), Gb = GB + (gv ? g : 0u);
-    const uint32_t oa = (Ga >> 8) * strA + (Ga & 255u) * 64, ob = (Gb >> 8) * strB + (Gb & 255u) * 64;
-    const uint32_t sa_off = (Ga >> 8) * strA + 16448 + 48 + 2 * (Ga & 255u);
-    const uint32_t sb_off = (Gb >> 8) * strB + 16448 + 48 + 2 * (Gb & 255u);
-    qa[q] = ld_u128(baseA + (oa + 64 + lo16));
-    qb[q] = ld_u128(baseB + (ob + 64 + lo16));
-    sa[q] = ld_u16(baseA + sa_off);
-    sb[q] = ld_u16(baseB + sb_off);
-  }
   // the rows' outlier corrections, spread over every wave: lane (j, c) of wave w takes entries
   // c + 16 (w + W t) of rows j and j + 4, so all waves issue the same loads (the waits stay
   // exact) and the corrections join the row sums before the lane reduction
@@ -1585,6 +1570,22 @@ __global__ void __launch_bounds__(kWave * W) k_gemv_flat(GemvArgs a) {
       cb[t] = srcB[ub ? size_t(rowB) * kmB + e : 0];
       cuse |= (uint32_t(ua) << (2 * t)) | (uint32_t(ub) << (2 * t + 1));
     }
+  }
+  uint4 qa[MAXP], qb[MAXP];
+  uint32_t sa[MAXP], sb[MAXP], gvm = 0;
+#pragma unroll
+  for (int q = 0; q < MAXP; ++q) {
+    const uint32_t p = wave + W * uint32_t(q), g = 4 * p + uint32_t(c >> 2);
+    const bool gv = p < npan && g < ng;
+    gvm |= uint32_t(gv) << q;
+    const uint32_t Ga = GA + (gv ? g : 0u), Gb = GB + (gv ? g : 0u);
+    const uint32_t oa = (Ga >> 8) * strA + (Ga & 255u) * 64, ob = (Gb >> 8) * strB + (Gb & 255u) * 64;
+    const uint32_t sa_off = (Ga >> 8) * strA + 16448 + 48 + 2 * (Ga & 255u);
+    const uint32_t sb_off = (Gb >> 8) * strB + 16448 + 48 + 2 * (Gb & 255u);
+    qa[q] = ld_u128(baseA + (oa + 64 + lo16));
+    qb[q] = ld_u128(baseB + (ob + 64 + lo16));
+    sa[q] = ld_u16(baseA + sa_off);
+    sb[q] = ld_u16(baseB + sb_off);
   }
   // lane 8 i's residual / bias / RoPE operands
   const int i8 = lane >> 3;
