@@ -17,7 +17,8 @@ PACK_LIB = PKG_DIR / "libchpe_pack.so"
 
 ARCH_3B, ARCH_9B, ARCH_72B = 0, 1, 2
 # archive kinds of chpe_pack_write (include/chpe_pack.h)
-PACK_3B_FP16_RAW, PACK_3B_BF16_RAW, PACK_3B_W4, PACK_3B_W2, PACK_3B_W4_STD, PACK_72B_W4, PACK_72B_W2 = range(7)
+(PACK_3B_FP16_RAW, PACK_3B_BF16_RAW, PACK_3B_W4, PACK_3B_W2, PACK_3B_W4_STD, PACK_72B_W4, PACK_72B_W2,
+ PACK_9B_W4) = range(8)
 
 # every symbol include/chpe.h declares, in order
 ENGINE_SYMBOLS = [
@@ -107,6 +108,11 @@ def load_pack_lib():
         lib.chpe_pack_size.argtypes = [ctypes.c_int]
         lib.chpe_pack_write.restype = ctypes.c_int
         lib.chpe_pack_write.argtypes = [ctypes.c_char_p, ctypes.c_int, ctypes.c_uint64, ctypes.c_int]
+        lib.chpe_pack_records.restype = ctypes.c_int
+        lib.chpe_pack_records.argtypes = [ctypes.c_int, ctypes.c_uint64, ctypes.c_uint64, ctypes.c_uint64,
+                                          ctypes.c_int, _c_u8_p]
+        lib.chpe_pack_header.restype = ctypes.c_int
+        lib.chpe_pack_header.argtypes = [ctypes.c_int, _c_u8_p]
         lib.chpe_pack_normals.restype = None
         lib.chpe_pack_normals.argtypes = [ctypes.c_uint64, ctypes.c_uint64, ctypes.c_uint64,
                                           ctypes.c_uint64, ctypes.c_float, _c_float_p]
@@ -129,6 +135,23 @@ def write_archive(path, kind, seed=0, threads=0):
     if rc != 0:
         raise RuntimeError(f"chpe_pack_write({path}, kind={kind}) failed: {rc}")
     return path
+
+
+def pack_records(kind, first, count, seed=0, threads=0):
+    """Records [first, first + count) of archive `kind`, as they lie in the file, as a
+    (count, record_bytes) uint8 array."""
+    rb = 16384 if kind in (PACK_3B_FP16_RAW, PACK_3B_BF16_RAW) else (20480 if kind == PACK_3B_W4_STD else 17408)
+    out = np.zeros((count, rb), dtype=np.uint8)
+    if load_pack_lib().chpe_pack_records(kind, seed, first, count, threads, out.ctypes.data_as(_c_u8_p)) != 0:
+        raise ValueError("chpe_pack_records rejected the arguments")
+    return out
+
+
+def pack_header(kind):
+    out = np.zeros(4096, dtype=np.uint8)
+    if load_pack_lib().chpe_pack_header(kind, out.ctypes.data_as(_c_u8_p)) != 0:
+        raise ValueError("chpe_pack_header rejected the kind")
+    return out
 
 
 def normals(seed, tid, first, n, std=0.02):
@@ -397,7 +420,7 @@ def default_archive_dir():
 ARCHIVE_NAMES = {
     PACK_3B_FP16_RAW: "qwen2.5-3b-fp16raw", PACK_3B_BF16_RAW: "qwen2.5-3b-bf16raw",
     PACK_3B_W4: "qwen2.5-3b-w4", PACK_3B_W2: "qwen2.5-3b-w2", PACK_3B_W4_STD: "qwen2.5-3b-w4std",
-    PACK_72B_W4: "qwen2.5-72b-w4", PACK_72B_W2: "qwen2.5-72b-w2",
+    PACK_72B_W4: "qwen2.5-72b-w4", PACK_72B_W2: "qwen2.5-72b-w2", PACK_9B_W4: "qwen3.5-9b-w4",
 }
 
 

@@ -131,6 +131,39 @@ inline LayerInfo layer_info(MapKind m, size_t l) {
   return o;
 }
 
+// Every record index of a Qwen3.5-9B layer (qwen35_tensor_map.LAYERS, the INT8 spans;
+// src/qwen35_tensor_map.zig:7-50 names the fields).  Full-attention layers (3, 7, ..., 31):
+// q (2048 records), k (256), v (256), o (1024), q_norm, k_norm; linear-attention layers:
+// in_proj_qkv (2048), in_proj_z (1024), in_proj_a (8), in_proj_b (8), conv1d (4), a_log,
+// dt_bias, linear_norm, out_proj (1024).  gate / up / down: 3072 records each.
+struct Qwen35Records {
+  bool full_attn;
+  size_t input_norm, post_norm, gate_proj, up_proj, down_proj;
+  size_t q_proj, k_proj, v_proj, o_proj, q_norm, k_norm;                      // full attention
+  size_t in_proj_qkv, in_proj_z, in_proj_a, in_proj_b, conv1d, a_log, dt_bias, linear_norm,
+      out_proj;                                                               // linear attention
+};
+
+inline Qwen35Records qwen35_records(size_t l) {
+  Qwen35Records r{};
+  size_t b = 62080;
+  for (size_t i = 0; i < l; ++i) b += qwen35_is_full_attn(i) ? 12804 : 13337;
+  r.full_attn = qwen35_is_full_attn(l);
+  r.input_norm = b;
+  if (r.full_attn) {
+    r.q_proj = b + 1; r.k_proj = b + 2049; r.v_proj = b + 2305; r.o_proj = b + 2561;
+    r.q_norm = b + 3585; r.k_norm = b + 3586; r.post_norm = b + 3587;
+  } else {
+    r.in_proj_qkv = b + 1; r.in_proj_z = b + 2049; r.in_proj_a = b + 3073; r.in_proj_b = b + 3081;
+    r.conv1d = b + 3089; r.a_log = b + 3093; r.dt_bias = b + 3094; r.linear_norm = b + 3095;
+    r.out_proj = b + 3096; r.post_norm = b + 4120;
+  }
+  r.gate_proj = r.post_norm + 1;
+  r.up_proj = r.gate_proj + 3072;
+  r.down_proj = r.up_proj + 3072;
+  return r;
+}
+
 inline size_t final_norm_record(MapKind m) {
   switch (m) {
     case MapKind::Qwen3bRaw: return 376852;
