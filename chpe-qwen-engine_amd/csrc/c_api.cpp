@@ -48,7 +48,8 @@ const char* validate(const uint8_t* b, size_t len) {
   if (!standard && !dense && !raw) return "BadGeometry";
   if (!raw && h.cell_bytes != kCellBytes) return "BadGeometry";
   if (raw && h.cell_bytes != kTileCodeBytes) return "BadGeometry";
-  if (h.header_bytes + h.record_count * h.record_bytes > len) return "Truncated";
+  // header_bytes + record_count * record_bytes > len, without wrapping in 64 bits
+  if (h.record_count > (len - h.header_bytes) / h.record_bytes) return "Truncated";
   return nullptr;
 }
 
@@ -193,7 +194,7 @@ int chpe_time_steps(void* ctx, size_t n, float* ms) {
   Context* c = C(ctx);
   Engine& e = *c->engine;
   if (hipEventRecord(c->ev0, e.stream()) != hipSuccess) return -3;
-  e.launch_steps(n);
+  if (const int rc = e.launch_steps(n)) return rc;
   if (hipEventRecord(c->ev1, e.stream()) != hipSuccess) return -3;
   if (hipEventSynchronize(c->ev1) != hipSuccess) return -3;
   if (hipEventElapsedTime(ms, c->ev0, c->ev1) != hipSuccess) return -3;
@@ -210,7 +211,7 @@ int chpe_time_stage(void* ctx, int stage, size_t layer0, size_t layer1, size_t i
   if (hipEventRecord(c->ev0, e.stream()) != hipSuccess) return -3;
   for (size_t it = 0; it < iters; ++it)
     for (size_t l = layer0; l < layer1; ++l)
-      if (e.launch_stage(stage, l)) return -1;
+      if (const int rc = e.launch_stage(stage, l)) return rc;
   if (hipEventRecord(c->ev1, e.stream()) != hipSuccess) return -3;
   if (hipEventSynchronize(c->ev1) != hipSuccess) return -3;
   return hipEventElapsedTime(ms, c->ev0, c->ev1) == hipSuccess ? 0 : -3;
@@ -314,6 +315,7 @@ int chpe_debug_gemv_flat(int mode, uint32_t rows, uint32_t cols, const uint8_t* 
     p.base = d + kShift;
     p.stride = uint32_t(kCellBytes);
     p.rows = rows;
+    p.wrows = rows;
     p.unit_begin = begin[i];
     p.y = dy;
     p.corr_kmax = kmax[i];
@@ -410,6 +412,7 @@ int chpe_debug_gemv_cells(int mode, uint32_t rows, const uint8_t* cells, const u
     p.base = d + kShift;
     p.stride = uint32_t(kCellBytes);
     p.rows = rows;
+    p.wrows = rows;
     p.unit_begin = begin[i];
     p.y = dy;
   }

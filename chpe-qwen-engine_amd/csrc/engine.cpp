@@ -276,6 +276,7 @@ bool Engine::init(const uint8_t* b, size_t len, const EngineConfig& cfg, std::st
 }
 
 int Engine::launch_one() {
+  ++h_pos_;  // k_finish advances the device position
   if (use_graph_) return hipGraphLaunch(graph_exec_, stream_) == hipSuccess ? 0 : -3;
   record_step(stream_);
   return hipGetLastError() == hipSuccess ? 0 : -3;
@@ -367,12 +368,28 @@ bool Engine::plan_projection(size_t tile_start, size_t num_tiles, size_t r_total
     p->base = d_image_ + cell(0);
     p->stride = uint32_t(stride_);
     if (c_total > 2048) {  // flat tiles: gemvCellFlat
-      const size_t need = (r_total * c_total + kFlatWeights - 1) / kFlatWeights;
-      if (avail < need) { *err = "flat tensor shorter than its shape"; return false; }
+      // gemvLinear walks the available tiles only (:1423-1429): with fewer tiles than the shape
+      // needs (the 9B map's v <- in_proj_a, one tile, :1119) the rows past them get no
+      // weights (zero in a fresh output, untouched when accumulating)
+      size_t use = (r_total * c_total + kFlatWeights - 1) / kFlatWeights, wrows = r_total;
+      if (avail < use) {
+        const size_t covered = avail * kFlatWeights;
+        if (covered % c_total) {
+          *err = "flat tiles end inside a row (a partial row of a short tensor is not built)";
+          return false;
+        }
+        use = avail;
+        wrows = covered / c_total;
+      }
       std::vector<float2> ent;
-      if (!plan_flat_tiles(b + cell(0), len - cell(0), stride_, need, r_total, c_total, &p->kind, &ent,
+      if (!plan_flat_tiles(b + cell(0), len - cell(0), stride_, use, wrows, c_total, &p->kind, &ent,
                            &p->corr_kmax, err))
         return false;
+      if (wrows < r_total && p->kind != WeightKind::FlatW4) {
+        *err = "a short tensor of 2-bit flat tiles is not built";
+        return false;
+      }
+      p->wrows = uint32_t(wrows);
       if (!ent.empty()) {
         p->corr = static_cast<float2*>(dev_alloc(ent.size() * sizeof(float2)));
         if (!p->corr) { *err = "allocation"; return false; }
@@ -518,6 +535,7 @@ uint32_t Engine::enqueue_gemv(const ProjPlan* const* parts, float* const* outs, 
     gp.base = p.base;
     gp.stride = p.stride;
     gp.rows = p.rows;
+    gp.wrows = p.wrows ? p.wrows : p.rows;
     gp.unit_begin = begin[i];
     gp.bf16 = p.bf16;
     gp.y = outs[i];
@@ -611,6 +629,7 @@ EmbedArgs Engine::embed_args() const {
 
 int Engine::set_state(const StepState& s) {
   *h_state_ = s;
+  h_pos_ = s.pos;
   if (hipMemcpyAsync(d_state_, h_state_, sizeof(StepState), hipMemcpyHostToDevice, stream_) != hipSuccess) return -3;
   // the first step's input; with embed_fused_ every step's k_finish embeds the next token
   if (embed_fused_) launch_embed(embed_args(), stream_);
@@ -685,12 +704,16 @@ int Engine::forward(uint32_t token, size_t pos, ForwardResult* out) {
   return 0;
 }
 
-void Engine::launch_steps(size_t n) {
-  for (size_t i = 0; i < n; ++i) (void)launch_one();
+int Engine::launch_steps(size_t n) {
+  if (h_pos_ + n > cfg_.max_seq_len) return -2;  // a step at max_seq_len would write past the KV cache
+  for (size_t i = 0; i < n; ++i)
+    if (launch_one()) return -3;
+  return 0;
 }
 
 int Engine::time_stage_live(int stage, size_t n_steps, double* avg_ms, size_t* launches) {
   if (stage < 0 || stage > 6 || n_steps == 0) return -1;
+  if (h_pos_ + n_steps > cfg_.max_seq_len) return -2;
   const size_t per_step = stage == 4 ? 1 : arch_.num_layers;
   const size_t n = per_step * n_steps;
   std::vector<hipEvent_t> ev(2 * n, nullptr);
@@ -702,6 +725,7 @@ int Engine::time_stage_live(int stage, size_t n_steps, double* avg_ms, size_t* l
     probe_events_ = ev.data();
     probe_next_ = 0;
     for (size_t i = 0; i < n_steps; ++i) record_step(stream_);  // direct launches
+    h_pos_ += n_steps;
     probe_stage_ = -1;
     if (hipStreamSynchronize(stream_) != hipSuccess || probe_next_ != 2 * n) rc = -3;
   }
@@ -727,10 +751,10 @@ int Engine::forward_tokens(const uint32_t* toks, size_t n, ForwardResult* out) {
   if (n > cfg_.max_seq_len) return -2;
   if (hipMemcpyAsync(d_prompt_, toks, n * 4, hipMemcpyHostToDevice, stream_) != hipSuccess) return -3;
   if (set_state(StepState{toks[0], 0, uint32_t(n), 0})) return -3;
-  launch_steps(n - 1);
+  if (launch_steps(n - 1)) return -3;
   if (sync()) return -3;
   const uint64_t t0 = now_ns();
-  launch_steps(1);
+  if (launch_steps(1)) return -3;
   if (hipMemcpyAsync(h_result_, d_result_, sizeof(StepResult), hipMemcpyDeviceToHost, stream_) != hipSuccess) return -3;
   if (sync()) return -3;
   const uint64_t t1 = now_ns();
@@ -750,7 +774,7 @@ int Engine::generate(const uint32_t* prompt, size_t n_prompt, size_t n_gen, uint
   if (steps > cfg_.max_seq_len) return -2;
   if (hipMemcpyAsync(d_prompt_, prompt, n_prompt * 4, hipMemcpyHostToDevice, stream_) != hipSuccess) return -3;
   if (set_state(StepState{prompt[0], 0, uint32_t(n_prompt), 0})) return -3;
-  launch_steps(steps);
+  if (launch_steps(steps)) return -3;
   if (sync()) return -3;
   if (out_tokens &&
       hipMemcpy(out_tokens, d_out_tokens_ + (n_prompt - 1), n_gen * 4, hipMemcpyDeviceToHost) != hipSuccess)
@@ -766,7 +790,7 @@ int Engine::verify(const uint32_t* drafts, size_t m, size_t pos, uint32_t* out_a
   // the drafts take the prompt slots of their positions, so every step is teacher-forced
   if (hipMemcpyAsync(d_prompt_ + pos, drafts, m * 4, hipMemcpyHostToDevice, stream_) != hipSuccess) return -3;
   if (set_state(StepState{drafts[0], uint32_t(pos), uint32_t(pos + m), 0})) return -3;
-  launch_steps(m);
+  if (launch_steps(m)) return -3;
   if (sync()) return -3;
   if (hipMemcpy(out_argmax, d_out_tokens_ + pos, m * 4, hipMemcpyDeviceToHost) != hipSuccess) return -3;
   if (last) {
@@ -839,6 +863,8 @@ double Engine::step_bytes(size_t pos) const {
 
 int Engine::launch_stage(int stage, size_t l) {
   if (l >= layers_.size()) return -1;
+  // q/k/v appends a KV row and attention reads rows up to the device position
+  if ((stage == 0 || stage == 5 || stage == 6) && h_pos_ >= cfg_.max_seq_len) return -2;
   const LayerPlan& L = layers_[l];
   const uint32_t D = uint32_t(arch_.hidden_dim), I = uint32_t(arch_.intermediate_dim);
   switch (stage) {

@@ -50,6 +50,7 @@ struct ProjPlan {
   const uint8_t* base = nullptr;  // device address of the first record
   uint32_t stride = 0;
   uint32_t rows = 0, cols = 0;
+  uint32_t wrows = 0;                  // rows the tiles cover; 0 = all (see GemvPart::wrows)
   uint32_t bf16 = 0;
   uint32_t replace_outliers = 0;
   float* bias = nullptr;               // device, with the reference's non-finite -> 0 rule
@@ -94,8 +95,9 @@ class Engine {
   // drafts[0..m) at positions pos..pos+m-1, each step teacher-forced (the KV rows at those
   // positions are overwritten); out_argmax[i] = argmax after draft i
   int verify(const uint32_t* drafts, size_t m, size_t pos, uint32_t* out_argmax, ForwardResult* last);
-  // enqueue n graph launches continuing from the current device state (no sync)
-  void launch_steps(size_t n);
+  // enqueue n graph launches continuing from the current device state (no sync); -2 and
+  // nothing enqueued when the steps would pass max_seq_len
+  int launch_steps(size_t n);
   int sync();
   int copy_logits(float* out) const;   // vocab_size floats of the last step
   int copy_hidden(float* out) const;   // hidden_dim floats (the residual stream)
@@ -190,6 +192,7 @@ class Engine {
   hipEvent_t* probe_events_ = nullptr;
   size_t probe_next_ = 0;
   int launch_one();
+  size_t h_pos_ = 0;  // the device position (StepState::pos) as the launches leave it
 };
 
 }  // namespace chpe

@@ -156,6 +156,8 @@ __device__ __forceinline__ void args_batch(const GemvArgs& a) {
                  "s"(p1.base), "s"(p1.stride), "s"(p1.rows), "s"(p1.unit_begin), "s"(p1.bias), "s"(p1.rope_role),
                  "s"(p2.base), "s"(p2.stride), "s"(p2.rows), "s"(p2.unit_begin), "s"(p2.bias), "s"(p2.rope_role),
                  "s"(a.x), "s"(a.gamma), "s"(a.C), "s"(a.n_units), "s"(a.n_parts), "s"(a.rope.head_dim));
+    asm volatile("" ::"s"(p0.corr), "s"(p0.corr_kmax), "s"(p0.wrows), "s"(p1.corr), "s"(p1.corr_kmax), "s"(p1.wrows),
+                 "s"(p2.corr), "s"(p2.corr_kmax), "s"(p2.wrows));
   } else if constexpr (MODE == int(GemvMode::SwiGlu)) {
     const GemvPart& p1 = a.part[1];
     asm volatile("" ::"s"(p0.base), "s"(p0.stride), "s"(p0.rows), "s"(p0.y), "s"(p0.corr), "s"(p0.corr_kmax),
@@ -184,6 +186,9 @@ __device__ __forceinline__ GemvPart pick_part(const GemvArgs& a, int pu) {
   p.y = pu == 0 ? p.y : (pu == 1 ? b.y : c.y);
   p.bias = pu == 0 ? p.bias : (pu == 1 ? b.bias : c.bias);
   p.rope_role = pu == 0 ? p.rope_role : (pu == 1 ? b.rope_role : c.rope_role);
+  p.corr = pu == 0 ? p.corr : (pu == 1 ? b.corr : c.corr);
+  p.corr_kmax = pu == 0 ? p.corr_kmax : (pu == 1 ? b.corr_kmax : c.corr_kmax);
+  p.wrows = pu == 0 ? p.wrows : (pu == 1 ? b.wrows : c.wrows);
   return p;
 }
 
@@ -1543,7 +1548,7 @@ __global__ void __launch_bounds__(kWave * W) k_gemv_flat(GemvArgs a) {
   }
   __builtin_amdgcn_sched_barrier(0);  // every input load ahead of the code loads
   const uint32_t rowA = row_of<RU, MODE>(row_base, j, half), rowB = row_of<RU, MODE>(row_base, j + RU / 2, half);
-  const bool okA = rowA < P0.rows, okB = rowB < P1.rows;
+  const bool okA = rowA < P0.wrows, okB = rowB < P1.wrows;
   // 32-bit group indices and byte offsets from the part's base (a uniform 64-bit pointer), so
   // that each load is a scalar base plus one vector offset (the tensors here are < 4 GiB)
   const uint32_t GA = (okA ? rowA : 0u) * ng, GB = (okB ? rowB : 0u) * ng;
@@ -1686,7 +1691,8 @@ __global__ void __launch_bounds__(kWave * W) k_gemv_flat(GemvArgs a) {
   if constexpr (kRope) {
     if ((lane % S) == 0 && i8 < RU / 2 && orow < P0.rows)
       rope_store(a, P0, orow, v + prev, up + up_pre, rope_ok ? rc : 1.0f, rope_ok ? rs : 0.0f);
-  } else if ((lane % S) == 0 && (!kSwi || i8 < RU / 2)) {
+  } else if ((lane % S) == 0 && (!kSwi || i8 < RU / 2) &&
+             (MODE != int(GemvMode::Accum) || orow < P0.wrows)) {  // Accum: rows past the tiles stay
     epilogue<MODE>(P0, row_of<RU, MODE>(row_base, i8, 0), v, up, prev, &bv, &bi, &nf);
   }
 }

@@ -56,6 +56,10 @@ struct GemvPart {
   const uint8_t* base;        // device address of the tensor's first record
   uint32_t stride;            // record stride in bytes
   uint32_t rows;              // output rows (r_total)
+  uint32_t wrows;             // rows the tiles cover (<= rows; FlatW4 only may have fewer): the
+                              //   rows past it have no weights (gemvLinear computes only the
+                              //   rows its tiles reach), Store / QkvRope give 0 + bias, Accum
+                              //   leaves them untouched
   uint32_t unit_begin;        // first work unit of this part
   uint32_t bf16;              // Raw16: 1 = bf16, 0 = fp16
   float* y;                   // output vector

@@ -1104,6 +1104,13 @@ static void compute_lm_head(oref_engine *e) {
     }
 }
 
+void oref_compute_lm_head(oref_engine *e, const float *xn, float *logits) {
+    /* computeLmHead on a caller's normed hidden state (test hook) */
+    memcpy(e->norm_buf, xn, e->arch.hidden_dim * sizeof(float));
+    compute_lm_head(e);
+    memcpy(logits, e->logits_buf, e->arch.vocab_size * sizeof(float));
+}
+
 static float sumsq_seq(const float *v, size_t n) {
     float s = 0.0f;
     for (size_t i = 0; i < n; i++) s += v[i] * v[i];

@@ -133,6 +133,9 @@ void oref_gemv_linear(oref_engine *e, size_t tile_start, size_t num_tiles, const
 void oref_unpack_norm(oref_engine *e, size_t tile, float *out, size_t n);
 void oref_unpack_bias(oref_engine *e, size_t tile, float *out, size_t n);
 void oref_unpack_embed_row(oref_engine *e, uint32_t token, float *out);
+/* computeLmHead (chpe_engine.zig:1554-1660) on `xn` (hidden_dim floats, already normed):
+ * vocab_size logits into `logits` */
+void oref_compute_lm_head(oref_engine *e, const float *xn, float *logits);
 
 /* Teacher-forced prompt (positions 0..n_prompt-1) then greedy feedback for n_gen
  * tokens.  out_tokens[n_gen]; top2_gap[n_gen] (optional) = max logit - runner-up. */

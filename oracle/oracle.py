@@ -62,6 +62,7 @@ def lib():
         L.oref_unpack_norm.argtypes = [V, S, _fp, S]
         L.oref_unpack_bias.argtypes = [V, S, _fp, S]
         L.oref_unpack_embed_row.argtypes = [V, ctypes.c_uint32, _fp]
+        L.oref_compute_lm_head.argtypes = [V, _fp, _fp]
         L.oref_prefill_synthetic.restype = ctypes.c_int
         L.oref_prefill_synthetic.argtypes = [V, S, ctypes.c_uint64]
         L.oref_generate.restype = ctypes.c_int
@@ -173,6 +174,13 @@ class Oracle:
     def embed_row(self, token):
         out = np.zeros(self.hidden_dim, dtype=np.float32)
         self.L.oref_unpack_embed_row(self.e, token, out.ctypes.data_as(_fp))
+        return out
+
+    def lm_head(self, xn):
+        """computeLmHead on a normed hidden state: the vocab_size logits."""
+        x = np.ascontiguousarray(xn, dtype=np.float32)
+        out = np.empty(self.L.oref_vocab(self.e), dtype=np.float32)
+        self.L.oref_compute_lm_head(self.e, x.ctypes.data_as(_fp), out.ctypes.data_as(_fp))
         return out
 
     def generate(self, prompt, n_gen):
