@@ -4,8 +4,7 @@ The archives are the seeded writer's (include/chpe_pack.h): 72B with 4-bit and 2
 tiles (qwen72b_tensor_map), 9B with 4-bit flat tiles at the INT8 map's indices, decoded the
 way the reference's engine decodes them (the 9B linear-attention layers aliased onto GQA:
 q <- in_proj_qkv, k <- in_proj_z, v <- in_proj_a with one tile, o <- out_proj,
-src/chpe_engine.zig:1107-1131).  Both sides use the fp16 KV cache (the oracle's kv-f16 mode).
-Contexts are short because the oracle reads 37 GB per 72B step on the host.
+src/chpe_engine.zig:1107-1131).  Contexts are short because the oracle reads 37 GB per 72B step on the host.
 
 Bars:
   * greedy token streams (f32 KV cache, as the reference keeps it) identical, a difference
