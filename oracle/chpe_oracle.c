@@ -8,27 +8,46 @@
  * accumulators, ordered `@reduce(.Add)`, fmaf() only where Zig writes `@mulAdd`,
  * separate multiply/add everywhere else (compiled -ffp-contract=off).
  *
- * Pinning (each item is checked by a test in tests/test_oracle.py):
+ * What pins each function (the tests named are the checks; none retypes this file's formulas):
  *   gemvTileW2/W4/W8 ........ closed forms of the reference's own synthetic cells
- *                             (chpe_engine.zig:1814-1891) + float64 brute force on
- *                             random cells (all branches: group/no-group, outliers)
- *   gemvTileF16/F32 ......... float64 brute force (fp16, bf16, f32 cells)
- *   gemvCellFlat ............ float64 brute force of the materialised weights, and the
- *                             weights themselves against an independent numpy unpack
- *   unpackEmbedRowCell ...... independent numpy unpack (q8/q4/q2/no-group, outliers)
- *   rmsNorm ................. KAT qwen_rmsnorm.zig:73-90 + float64 brute force
- *   applyRope ............... KAT qwen_rope.zig:149-162 (+-1e-4), pos-0 identity,
- *                             norm preservation
+ *                             (chpe_engine.zig:1814-1891): test_oracle_kats.py
+ *                             test_gemv_{2,4,8}bit_synthetic_cell, test_gemv_accumulate_adds_to_y;
+ *                             the float64 product of the generator's weights within the
+ *                             quantizer's bound on a whole archive: test_oracle_step.py
+ *                             test_projection_within_quantization_bound
+ *   gemvTileF16/F32 ......... float64 brute force (fp16, bf16, f32 cells; tails, clipping,
+ *                             accumulate): test_oracle_pinning.py
+ *                             test_f16_bf16_f32_cells_are_float64_products
+ *   gemvCellFlat ............ closed-form tiles (group scales, replaced outliers, the 2-bit
+ *                             codebook): test_oracle_kats.py test_flat_tile_*; the down
+ *                             projection within the quantizer's bound (test_oracle_step.py)
+ *   dotSegment / raw gemvLinear / raw unpackEmbedRow / raw tied computeLmHead (fp16, bf16,
+ *   int8 x 0.00373708) ...... float64 products of the generator's weights within the f32
+ *                             summation bound, rows straddling tiles, embedding rows bit for
+ *                             bit: test_oracle_pinning.py test_raw_*
+ *   unpackEmbedRowCell ...... a numpy decode of the q8 / q2 / q4 / per-tile-scale forms
+ *                             (outliers replacing in entry order, rows past the cell):
+ *                             test_oracle_pinning.py test_embed_row_cell_forms_match_numpy_decode;
+ *                             the generator's weights within the quantizer's bound:
+ *                             test_oracle_step.py test_embedding_row_within_quantization_bound
+ *   rmsNorm ................. KAT qwen_rmsnorm.zig:73-90 + float64: test_oracle_kats.py
+ *   applyRope ............... KAT qwen_rope.zig:149-162, pos-0 identity, closed form
  *   silu .................... KAT qwen_mlp.zig:92-111
- *   attention ............... seq-1 pass-through KAT (qwen_attention.zig:144-169),
- *                             seq-2 bounds KAT, float64 softmax brute force
- *   validate ................ the malformed-file KATs of weight_archive.zig:1048-1107
- *   layer maps .............. tests/golden/tensor_maps.json (the reference tables)
- *   forwardDecode ........... mock zero archive KAT (chpe_engine.zig:1893-1933) and a
- *                             float64 numpy re-implementation of one whole step on a
- *                             small seeded archive
- *   Only libm-level ulps of expf/powf/sinf/cosf (Zig's implementations are not
- *   available here) are not pinned bit-for-bit.
+ *   attention ............... seq-1 pass-through KAT (qwen_attention.zig:144-169), float64
+ *                             softmax brute force: test_oracle_kats.py
+ *   validate ................ the malformed-file cases of weight_archive.zig:1048-1078:
+ *                             test_format.py test_validate_reference_error_cases
+ *   layer maps .............. tests/golden/tensor_maps.json (the reference tables):
+ *                             test_format.py test_*_map_*
+ *   forwardDecode ........... the mock zero archive KAT (chpe_engine.zig:1893-1933) with the
+ *                             closed forms of its fallbacks, and two decode steps restated in
+ *                             float64 from forwardDecode on numpy-decoded weights:
+ *                             test_oracle_pinning.py test_mock_zero_archive_known_answer,
+ *                             test_forward_decode_composition_float64
+ *   Gated DeltaNet (deltanet_oracle.c, no reference code): library fixtures, float64 and
+ *                             invariants: test_oracle_deltanet.py
+ *   Not pinned bit for bit: libm-level ulps of expf / powf / sinf / cosf (Zig's
+ *   implementations are not available here); covered by the tolerances above.
  */
 #define _GNU_SOURCE
 #include "chpe_oracle.h"

@@ -114,6 +114,37 @@ def test_raw_tied_lm_head_is_float64_product(raw_prefix):
     assert (np.abs(logits[rows] - ref) <= f32_dot_bound(E, xn.astype(np.float64))).all()
 
 
+def test_raw_int8_dot_segment_and_embedding():
+    """Raw int8 tiles (the 9B int8 archive: flags 0x08, dotSegment :1219-1237): each segment's
+    dot of int8 weights is scaled by the fixed 0.00373708 (the per-tensor scales of the map are
+    never read); embedding rows are int8 * 0.00373708 (:1511-1522).  Rows of 12288 columns
+    straddle the 16384-element tiles."""
+    rng = np.random.default_rng(88)
+    n_tiles, C = 12, 12288
+    tiles = rng.integers(-128, 128, n_tiles * 16384, dtype=np.int8)
+    hdr = np.zeros(4096, np.uint8)
+    hdr[:4] = np.frombuffer(np.uint32(0x45504843).tobytes(), np.uint8)
+    fields = np.array([1, 0], np.uint32)  # version
+    hdr[4:8] = np.frombuffer(fields[:1].tobytes(), np.uint8)
+    hdr[8:64] = np.frombuffer(np.array([4096, n_tiles, n_tiles, 16384, 16384, 0, 0x08], np.uint64).tobytes(), np.uint8)
+    o = orc.Oracle(data=np.concatenate([hdr, tiles.view(np.uint8)]), arch=1, max_seq_len=4, threads=4)
+    try:
+        assert o.info()["is_raw"] == 1 and o.info()["quant_bits"] == 8
+        rows = n_tiles * 16384 // C
+        x = rng.standard_normal(C).astype(np.float32)
+        y = o.gemv_linear(0, n_tiles, x, rows, C).astype(np.float64)
+        w = tiles[:rows * C].astype(np.float64).reshape(rows, C)
+        s = float(np.float32(0.00373708))
+        ref = (w @ x.astype(np.float64)) * s
+        bound = (f32_dot_bound(w, x.astype(np.float64)) + 2 * U * np.abs(w) @ np.abs(x.astype(np.float64))) * s
+        assert (np.abs(y - ref) <= bound + 2 * U * np.abs(ref)).all()
+        for tok in (0, 1, 5, 47):  # 16384 / 4096 = 4 rows per tile
+            want = tiles[tok * 4096:(tok + 1) * 4096].astype(np.float32) * np.float32(0.00373708)
+            assert np.array_equal(o.embed_row(tok), want)
+    finally:
+        o.close()
+
+
 # ------------------------------------------------------------------ 16- and 32-bit cells
 def cell_with(bits, rows, cols, flags, codes):
     cell = np.zeros(CELL, np.uint8)
