@@ -1,23 +1,26 @@
 #!/usr/bin/env python3
 """Batch-1 greedy decode throughput of the MI355X engine (libchpe.so).
 
-Workload: Qwen2.5-3B with 4-bit GROUP128 cells (dense 17408-byte records, the seeded archive
-of libchpe_pack.so), KV cache in fp16 in HBM, a 4096-token seeded random prompt decoded
-teacher-forced (untimed; it builds the context), then `--steps` greedy decode steps timed
-(256 by default: the 256 decoded tokens).  `--warmup` untimed steps run first, at positions
-0..W-1 of the same prompt, before the context is built.
+Default workload (--workload qwen72b-w4): Qwen2.5-72B with 4-bit GROUP128 flat tiles (the
+seeded archive of libchpe_pack.so, 38.6 GB, resident in HBM), KV cache in fp16 in HBM, an
+8192-token seeded random prompt decoded teacher-forced (untimed; it builds the context),
+then `--steps` greedy decode steps timed (128 by default).  `--warmup` untimed steps run
+first, at positions 0..W-1 of the same prompt, before the context is built.  Other
+workloads: qwen72b-w2 (2-bit tiles), qwen3b-w4 (Qwen2.5-3B 4-bit cells, 4096-token prompt),
+qwen9b-w4 (Qwen3.5-9B 4-bit flat tiles, the reference's GQA-aliased decode, 2048 tokens).
 
-A step is one CHPEEngine.forwardDecode (src/chpe_engine.zig:1663-1803): embed, 36 layers,
+A step is one CHPEEngine.forwardDecode (src/chpe_engine.zig:1663-1803): embed, the layers,
 LM head, argmax, with the argmax fed back on the device.  Inputs are resident in HBM before
 the timed region starts.
 
 Printed on stdout: ONE JSON line; diagnostics go to stderr.
-  roofline      the kernel that takes the largest share of the step: algorithmic bytes per
-                launch / mean launch time, timed with HIP events around every launch of it
-                inside real decode steps (chpe_time_stage_live)
-  cpu_baseline  the CPU oracle (oracle/, a C restatement of the reference's forwardDecode)
-                on the host cores, on a bounded sample of the same workload: decode steps at
-                positions 4096.. after a synthetic KV fill of 4096 positions
+  roofline      the stage (kernel) with the largest share of the step: its algorithmic bytes
+                per launch / its mean launch time, timed with HIP events around every launch
+                of it inside real decode steps (chpe_time_stage_live)
+  cpu_baseline  the CPU oracle (oracle/, a C restatement of the reference's forwardDecode) on
+                all of the process's host cores, on a bounded sample of the same workload:
+                decode steps after a synthetic fp16 KV fill of the prompt's positions; a
+                single-thread figure (the reference's engine is single-threaded) beside it
 """
 import argparse
 import json
@@ -34,62 +37,100 @@ sys.path.insert(0, str(ROOT / "chpe-qwen-engine_amd"))
 
 METRIC = "batch-1 decode tok/s at 1 MI355X; achieved HBM GB/s as % of peak"
 PEAK_HBM_GBS = 8000.0
-V, D, LAYERS, KV_HEADS, HEAD_DIM, Q_HEADS = 151936, 2048, 36, 2, 128, 16
-ATTN_CHUNK = 8192 // HEAD_DIM  # positions per attention workgroup
-NS = "chpe::(anonymous namespace)::"
-STAGES = {  # stage id -> (description, kernel name as rocprofv3 prints it, launches per step)
-    0: ("q/k/v GEMV + RoPE + KV append (RMSNorm fused)", f"void {NS}k_gemv_mma<4, 1>(chpe::GemvArgs)", LAYERS),
-    1: ("o GEMV + residual", f"void {NS}k_gemv_mma<1, 1>(chpe::GemvArgs)", LAYERS),
-    2: ("gate/up GEMV + SwiGLU (RMSNorm fused)", f"void {NS}k_gemv_mma<2, 2>(chpe::GemvArgs)", LAYERS),
-    3: ("down GEMV + residual (flat tiles)", f"void {NS}k_gemv_flat<1, 3, false, 8>(chpe::GemvArgs)", LAYERS),
-    4: ("LM head GEMV + argmax partials", f"{NS}k_gemv_mma_logits(chpe::GemvArgs)", 1),
-    5: ("attention over the context chunks", f"void {NS}k_attn_mfma<128, 8, 4, 1>(chpe::AttnArgs)", LAYERS),
-    6: ("attention chunk merge", f"void {NS}k_attn_merge<128>(chpe::AttnArgs)", LAYERS),
+STAGE_DESC = {
+    0: "q/k/v GEMV + RoPE + KV append (RMSNorm fused)",
+    1: "o GEMV + residual",
+    2: "gate/up GEMV + SwiGLU (RMSNorm fused)",
+    3: "down GEMV + residual",
+    4: "LM head GEMV + argmax partials (final RMSNorm fused)",
+    5: "attention over the context chunks",
+    6: "attention chunk merge",
 }
-
+# per workload: archive kind (chpe_pack.h), architecture, prompt length, shapes
+WORKLOADS = {
+    "qwen72b-w4": dict(kind=5, arch=2, prompt=8192, V=152064, L=80, H=64, KV=8, hd=128,
+                       desc="Qwen2.5-72B 4-bit GROUP128 flat tiles (dense 17408 B records)"),
+    "qwen72b-w2": dict(kind=6, arch=2, prompt=8192, V=152064, L=80, H=64, KV=8, hd=128,
+                       desc="Qwen2.5-72B 2-bit GROUP128 flat tiles (dense 17408 B records)"),
+    "qwen3b-w4": dict(kind=2, arch=0, prompt=4096, V=151936, L=36, H=16, KV=2, hd=128,
+                      desc="Qwen2.5-3B 4-bit GROUP128 cells (dense 17408 B records)"),
+    "qwen9b-w4": dict(kind=7, arch=1, prompt=2048, V=248320, L=32, H=16, KV=4, hd=256,
+                      desc="Qwen3.5-9B 4-bit GROUP128 flat tiles at the INT8 map's indices, "
+                           "reference-compatible GQA decode"),
+}
 
 
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def attention_bytes(stage, pos):
+def attention_bytes(w, stage, pos):
     """Algorithmic HBM bytes of one attention launch at position `pos` (fp16 KV)."""
-    if stage == 5:  # K and V rows 0..pos of one layer, plus q/k/v in and the partials out
-        chunks = math.ceil((pos + 1) / ATTN_CHUNK)
-        return 2 * KV_HEADS * HEAD_DIM * 2 * (pos + 1) + Q_HEADS * chunks * (HEAD_DIM + 2) * 4
-    chunks = math.ceil((pos + 1) / ATTN_CHUNK)
-    return Q_HEADS * chunks * (HEAD_DIM + 2) * 4 + Q_HEADS * HEAD_DIM * 4
+    chunk = 8192 // w["hd"]
+    chunks = math.ceil((pos + 1) / chunk)
+    partials = w["H"] * chunks * (w["hd"] + 2) * 4
+    if stage == 5:  # K and V rows 0..pos of one layer, the queries in, the partials out
+        return 2 * w["KV"] * w["hd"] * 2 * (pos + 1) + w["H"] * w["hd"] * 4 + partials
+    return partials + w["H"] * w["hd"] * 4
 
 
-def traffic_for(stage):
+def traffic_for(workload, stage):
     """HBM bytes per launch measured by rocprofv3 --pmc (FETCH_SIZE + WRITE_SIZE, scaled by
     the copy-kernel factor), committed in profiles/traffic.json; None when not measured."""
     f = ROOT / "profiles" / "traffic.json"
     if not f.exists():
         return None
-    t = json.loads(f.read_text()).get(str(stage))
+    t = json.loads(f.read_text()).get(workload, {}).get(str(stage))
     return None if t is None else t.get("bytes_per_launch")
 
 
-def cpu_baseline(archive, prompt_len, budget_s, max_steps):
+def cpu_model():
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(archive, w, prompt_len, budget_s):
+    """The oracle on the host: all of the process's cores over greedy decode steps at positions
+    prompt_len.. after a synthetic fp16 KV fill; then one thread on a sample of one step."""
     sys.path.insert(0, str(ROOT / "oracle"))
     import oracle as orc
-    cores = min(len(os.sched_getaffinity(0)), int(os.environ.get("OMP_NUM_THREADS", "16") or 16))
-    o = orc.Oracle(archive, arch=0, max_seq_len=prompt_len + max_steps + 1, kv_f16=True, threads=cores)
+    cores = len(os.sched_getaffinity(0))
+    o = orc.Oracle(archive, arch=w["arch"], max_seq_len=prompt_len + 64, kv_f16=True, threads=cores)
     try:
         o.prefill_synthetic(prompt_len, seed=1)
         tok, n, t0 = 151643, 0, time.perf_counter()
-        while n < max_steps and time.perf_counter() - t0 < budget_s:
+        while n < 32 and (n == 0 or time.perf_counter() - t0 < budget_s):
             tok = o.forward(tok, prompt_len + n).argmax_token
             n += 1
         dt = time.perf_counter() - t0
+        # one thread: the same step over 0 layers (embedding, final norm, LM head) and over the
+        # first layers; per token = t0 + (t_k - t0) * L / k
+        o.set_threads(1)
+        k = max(1, w["L"] // 10)
+        t = time.perf_counter()
+        o.forward_layers(tok, prompt_len + n, 0)
+        t_head = time.perf_counter() - t
+        t = time.perf_counter()
+        o.forward_layers(tok, prompt_len + n + 1, k)
+        t_k = time.perf_counter() - t
+        per_tok_1 = t_head + (t_k - t_head) * w["L"] / k
     finally:
         o.close()
-    return {"value": round(n / dt, 3), "unit": "tok/s", "cores": cores, "kind": "port",
-            "sample": f"{n} greedy decode steps at positions {prompt_len}..{prompt_len + n - 1} of the "
-                      f"same archive after a synthetic fp16 KV fill of {prompt_len} positions "
-                      f"(oracle/chpe_oracle.c, {cores} threads, {dt:.1f} s)"}
+    model = cpu_model()
+    return {"value": round(n / dt, 4), "unit": "tok/s", "cores": cores, "kind": "port",
+            "sample": f"{n} greedy decode steps at positions {prompt_len}..{prompt_len + n - 1} of the same "
+                      f"archive after a synthetic fp16 KV fill of {prompt_len} positions "
+                      f"(oracle/chpe_oracle.c, {cores} threads, {dt:.1f} s) on {model}",
+            "cpu_model": model,
+            "single_thread": {"value": round(1.0 / per_tok_1, 4), "unit": "tok/s", "cores": 1,
+                              "sample": f"one step at position {prompt_len + n + 1} over the first {k} of "
+                                        f"{w['L']} layers ({t_k:.2f} s) and over none ({t_head:.2f} s: "
+                                        f"embedding, final norm, LM head), scaled to {w['L']} layers"}}
 
 
 def copy_probe():
@@ -108,10 +149,11 @@ def copy_probe():
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=256)
+    ap.add_argument("--steps", type=int, default=128)
     ap.add_argument("--warmup", type=int, default=8)
-    ap.add_argument("--prompt", type=int, default=4096)
-    ap.add_argument("--live-steps", type=int, default=4, help="decode steps per stage timing")
+    ap.add_argument("--workload", default="qwen72b-w4", choices=sorted(WORKLOADS))
+    ap.add_argument("--prompt", type=int, default=0, help="prompt tokens (default: the workload's)")
+    ap.add_argument("--live-steps", type=int, default=2, help="decode steps per stage timing")
     ap.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of CPU oracle sample")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-probe", action="store_true",
@@ -136,16 +178,21 @@ def main():
     except ImportError:
         device_sync = lambda: None  # noqa: E731
 
+    w = WORKLOADS[args.workload]
+    os.environ.setdefault("CHPE_PACK_PROGRESS", "1")
     t = time.perf_counter()
-    archive = ca.ensure_archive(ca.PACK_3B_W4, seed=0)
+    archive = ca.ensure_archive(w["kind"], seed=0)
     log(f"archive {archive} ({archive.stat().st_size / 1e9:.3f} GB) ready in {time.perf_counter() - t:.1f} s")
-    P, K, W = args.prompt, args.steps, args.warmup
-    max_seq = P + K + 7 * args.live_steps + 8
-    e = ca.Engine(archive, arch=0, max_seq_len=max_seq, kv_f16=True)
-    prompt = np.random.default_rng(1).integers(0, V, P).astype(np.uint32)
+    P, K, W = args.prompt or w["prompt"], args.steps, args.warmup
+    max_seq = P + K + 7 * args.live_steps + 16
+    t = time.perf_counter()
+    e = ca.Engine(archive, arch=w["arch"], max_seq_len=max_seq, kv_f16=True)
+    log(f"engine init {time.perf_counter() - t:.1f} s (archive copied to HBM, plans built, step captured)")
+    prompt = np.random.default_rng(1).integers(0, w["V"], P).astype(np.uint32)
 
     if W:
         e.generate(prompt[:W], 1)  # W steps at positions 0..W-1
+    log(f"building the context: {P} teacher-forced steps")
     t = time.perf_counter()
     first = e.generate(prompt, 1)  # teacher-forced context: positions 0..P-1
     prefill_s = time.perf_counter() - t
@@ -160,53 +207,58 @@ def main():
     ms_per_step = wall / K * 1e3
     value = K / wall
     step_bytes = float(np.mean([e.step_bytes(P + i) for i in range(0, K, max(1, K // 16))]))
-    log(f"decode: {K} steps {wall * 1e3:.1f} ms wall ({event_ms:.1f} ms events) -> {value:.1f} tok/s, "
+    log(f"decode: {K} steps {wall * 1e3:.1f} ms wall ({event_ms:.1f} ms events) -> {value:.2f} tok/s, "
         f"{ms_per_step:.4f} ms/step; {step_bytes / 1e9:.4f} GB/step -> "
         f"{step_bytes / (wall / K) / 1e9:.1f} GB/s ({step_bytes / (wall / K) / 1e9 / PEAK_HBM_GBS:.1%} of HBM peak)")
 
     # per-stage mean launch time inside real decode steps
     stages, pos = {}, P + K
-    for st in STAGES:
+    for st in STAGE_DESC:
         avg_ms = e.time_stage_live(st, args.live_steps)
         mid = pos + (args.live_steps - 1) / 2.0
+        per_step = 1 if st == 4 else w["L"]
         if st in (5, 6):
-            nbytes = attention_bytes(st, mid)
+            nbytes = attention_bytes(w, st, mid)
         else:
-            nbytes = float(np.mean([e.stage_bytes(st, l) for l in range(1 if st == 4 else LAYERS)]))
-        desc, kname, per_step = STAGES[st]
-        stages[st] = dict(desc=desc, kernel=kname, us=avg_ms * 1e3, bytes=nbytes, per_step=per_step,
+            nbytes = float(np.mean([e.stage_bytes(st, l) for l in range(per_step)]))
+        stages[st] = dict(desc=STAGE_DESC[st], us=avg_ms * 1e3, bytes=nbytes, per_step=per_step,
                           share=avg_ms * per_step / ms_per_step)
-        log(f"  stage {st} {desc:42s} {avg_ms * 1e3:8.2f} us/launch x{per_step:3d} = "
-            f"{avg_ms * per_step:6.3f} ms/step ({stages[st]['share']:.1%}); {nbytes / 1e6:8.3f} MB/launch "
+        log(f"  stage {st} {STAGE_DESC[st]:52s} {avg_ms * 1e3:8.2f} us/launch x{per_step:3d} = "
+            f"{avg_ms * per_step:6.3f} ms/step ({stages[st]['share']:.1%}); {nbytes / 1e6:9.3f} MB/launch "
             f"-> {nbytes / avg_ms / 1e6:7.1f} GB/s")
         pos += args.live_steps
     dom = max(stages, key=lambda s: stages[s]["us"] * stages[s]["per_step"])
     d = stages[dom]
+    kernel = e.stage_kernel(dom)
     achieved = d["bytes"] / (d["us"] * 1e-6) / 1e9
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": traffic_for(dom),
-                "kernel": d["kernel"], "stage": d["desc"], "bytes_per_launch": round(d["bytes"]),
+                "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": traffic_for(args.workload, dom),
+                "kernel": kernel, "stage": d["desc"], "bytes_per_launch": round(d["bytes"]),
                 "us_per_launch": round(d["us"], 3), "share_of_step": round(d["share"], 4)}
+    stage_table = {str(s): {"desc": v["desc"], "us_per_launch": round(v["us"], 3), "launches_per_step": v["per_step"],
+                            "bytes_per_launch": round(v["bytes"]), "GBps": round(v["bytes"] / v["us"] / 1e3, 1)}
+                   for s, v in stages.items()}
     e.close()
 
     cpu = None
     if not args.no_cpu_baseline:
-        cpu = cpu_baseline(archive, P, args.cpu_budget, 256)
-        log(f"cpu baseline: {cpu['value']} tok/s ({cpu['sample']})")
+        cpu = cpu_baseline(archive, w, P, args.cpu_budget)
+        log(f"cpu baseline: {cpu['value']} tok/s on {cpu['cores']} threads, "
+            f"{cpu['single_thread']['value']} tok/s on 1 ({cpu['sample']})")
 
     out = {
-        "metric": METRIC, "value": round(value, 2), "unit": "tok/s", "n_gpus": 1, "steps": K, "warmup": W,
+        "metric": METRIC, "value": round(value, 3), "unit": "tok/s", "n_gpus": 1, "steps": K, "warmup": W,
         "ms_per_step": round(ms_per_step, 4), "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "f32", "data": "synthetic",
-        "config": {"workload": "Qwen2.5-3B 4-bit GROUP128 cells (dense 17408 B records), "
-                               f"{P}-token prompt + {K} greedy decode steps, fp16 KV cache",
-                   "prompt_tokens": P, "decode_tokens": K, "batch": 1, "kv_cache": "fp16",
-                   "weights": "seeded N(0,0.02) fp16 quantized to 4-bit (libchpe_pack.so, seed 0)",
+        "config": {"workload": f"{w['desc']}, {P}-token prompt + {K} greedy decode steps, fp16 KV cache",
+                   "name": args.workload, "prompt_tokens": P, "decode_tokens": K, "batch": 1, "kv_cache": "fp16",
+                   "weights": f"seeded N(0,0.02) fp16 quantized (libchpe_pack.so, seed 0)",
                    "parallelism": "none (1 GPU)"},
         "step_roofline": {"bytes_per_step": round(step_bytes), "achieved": round(step_bytes / (wall / K) / 1e9, 1),
                           "peak": PEAK_HBM_GBS, "unit": "GB/s",
                           "frac": round(step_bytes / (wall / K) / 1e9 / PEAK_HBM_GBS, 4)},
         "roofline": roofline,
+        "stages": stage_table,
         "cpu_baseline": cpu,
         "context_build_s": round(prefill_s, 3),
     }

@@ -27,7 +27,7 @@ ENGINE_SYMBOLS = [
     "chpe_get_last_argmax", "chpe_get_last_max_logit", "chpe_get_last_token0_logit",
     "chpe_get_last_hidden_norm", "chpe_free", "chpe_init_ex", "chpe_decode_step",
     "chpe_generate", "chpe_verify", "chpe_last_error", "chpe_get_max_seq_len", "chpe_get_hidden",
-    "chpe_time_steps", "chpe_time_stage", "chpe_time_stage_live", "chpe_stage_bytes", "chpe_step_bytes",
+    "chpe_time_steps", "chpe_time_stage", "chpe_time_stage_live", "chpe_stage_bytes", "chpe_step_bytes", "chpe_stage_kernel",
     "chpe_debug_gemv", "chpe_debug_flat_tile_weights", "chpe_debug_gemv_flat", "chpe_debug_gemv_cells", "chpe_debug_embed_row_cell",
     "chpe_debug_attention", "chpe_debug_deltanet_conv", "chpe_debug_deltanet_step",
 ]
@@ -77,6 +77,7 @@ def load_engine_lib():
             "chpe_time_stage_live": (I, [V, I, S, _c_float_p]),
             "chpe_stage_bytes": (D, [V, I, S]),
             "chpe_step_bytes": (D, [V, S]),
+            "chpe_stage_kernel": (ctypes.c_char_p, [V, I]),
             "chpe_debug_gemv": (I, [V, S, I, _c_float_p, _c_float_p]),
             "chpe_debug_flat_tile_weights": (I, [_c_u8_p, _c_float_p]),
             "chpe_debug_gemv_flat": (I, [I, ctypes.c_uint32, ctypes.c_uint32, _c_u8_p, _c_u8_p, S, _c_float_p,
@@ -297,6 +298,16 @@ class Engine:
 
     def step_bytes(self, pos):
         return self.lib.chpe_step_bytes(self.ctx, pos)
+
+    def stage_kernel(self, stage):
+        """The kernel that runs `stage`, demangled when c++filt is available."""
+        name = self.lib.chpe_stage_kernel(self.ctx, stage).decode()
+        try:
+            import subprocess
+            out = subprocess.run(["c++filt", name], capture_output=True, text=True, timeout=10)
+            return out.stdout.strip() or name
+        except (OSError, subprocess.SubprocessError):
+            return name
 
 
 def gpu_flat_tile_weights(cell):

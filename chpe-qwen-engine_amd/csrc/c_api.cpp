@@ -230,6 +230,18 @@ int chpe_time_stage_live(void* ctx, int stage, size_t n_steps, float* avg_ms) {
   return 0;
 }
 
+const char* chpe_stage_kernel(void* ctx, int stage) {
+  thread_local std::string name;
+  name.clear();
+  if (!ctx) return name.c_str();
+  Engine& e = *C(ctx)->engine;
+  record_kernel_names(true);
+  const int rc = e.launch_stage(stage, 0);
+  record_kernel_names(false);
+  if (rc == 0 && e.sync() == 0) name = last_kernel_name();
+  return name.c_str();
+}
+
 double chpe_stage_bytes(void* ctx, int stage, size_t layer) {
   if (!ctx || layer >= C(ctx)->arch.num_layers) return 0.0;
   return C(ctx)->engine->stage_bytes(stage, layer);

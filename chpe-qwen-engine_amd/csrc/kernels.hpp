@@ -239,6 +239,15 @@ struct LaunchProbe {
 void arm_launch_probe(hipEvent_t start, hipEvent_t stop);
 LaunchProbe take_launch_probe();
 
+// Measurement: while on, every launcher on this host thread records the (mangled) name of the
+// kernel it launches; last_kernel_name() returns the latest one.
+void record_kernel_names(bool on);
+const char* last_kernel_name();
+namespace detail {
+extern thread_local bool g_record_names;
+extern thread_local const char* g_last_kernel;
+}  // namespace detail
+
 // test hooks: dequantise / unpack exactly as the reference materialises weights
 void launch_flat_tile_weights(const uint8_t* cell, float* out, hipStream_t stream);
 void launch_embed_row_cell(const uint8_t* cell, uint64_t len, uint32_t row, uint32_t D, float* out,

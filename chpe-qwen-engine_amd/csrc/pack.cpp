@@ -8,12 +8,14 @@
 // Layout rules that follow from how the reference reads an archive:
 //  * A 1-D tensor is read as `len` floats from the start of its record's code area
 //    (unpackNorm / unpackBias, src/chpe_engine.zig:1144-1192), with no bound at the record.
-//    Vectors longer than the 4096 floats of a code area (the 8192-wide norms and q_proj bias
-//    of Qwen2.5-72B) therefore continue through the record's payload, the next record's
-//    64-byte header and the first bytes of the next record's code area.  The writer puts
-//    the vector's floats in exactly those bytes; the next record (always a flat weight tile
-//    in the maps) then has those bytes as its leading codes, and its outliers are chosen
-//    among the weights after them.
+//    Vectors longer than the 4096 floats of a code area (the 8192-wide q_proj bias of
+//    Qwen2.5-72B) therefore continue through the record's payload, the next record's 64-byte
+//    header and the first bytes of the next record's code area.  The writer puts the
+//    vector's floats in exactly those bytes; the next record (always a flat weight tile in
+//    the maps) then has those bytes as its leading codes, and its outliers are chosen among
+//    the weights after them.  Gains of 1.0 that wide (the 72B norms) are written as 1.0 in
+//    the code area and a NaN first in the payload: unpackNorm resets every gain to 1.0 when
+//    one is non-finite (:1161-1166), so they need none of the next record's bytes.
 //  * Embedding rows of cell archives are read as 16-row cells (tile = token / 16, row =
 //    token % 16, row stride D * bits / 8, src/chpe_engine.zig:1540-1546, :1288-1394).  For
 //    D >= 4096 a row runs past its cell, and in the group-128 forms its group scales run past
@@ -33,6 +35,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <limits>
 #include <thread>
 #include <vector>
 
@@ -535,7 +538,7 @@ bool make_plan(int kind, Plan* p) {
     const Segment& s = p->segs[i];
     if (s.first != next) return false;  // the map must tile [0, records) exactly
     next += s.count;
-    if (s.kind == SegKind::CellVec && s.R > kCodeFloats) {  // a long vector: its tail fills the next tile
+    if (s.kind == SegKind::CellVec && s.R > kCodeFloats && !s.ones) {  // a long vector: its tail fills the next tile
       if (s.R > kMaxVecFloats || i + 1 >= p->segs.size() || p->segs[i + 1].kind != SegKind::Flat) return false;
       p->segs[i + 1].spill = i;
     }
@@ -578,6 +581,14 @@ void fill_record(const Plan& p, const Segment& s, size_t t, uint64_t seed, uint8
       if (s.R <= kCodeFloats) {
         write_meta(out, s.layer, 32, 0, 1, uint32_t(s.R));
         std::memcpy(out + kBytecodeHeader, buf.data(), 4 * s.R);
+      } else if (s.ones) {
+        // gains of 1.0 wider than the code area: 1.0 in the code area and a NaN first in the
+        // payload, which unpackNorm's non-finite rule (:1161-1166) turns into gains of 1.0 for
+        // every element, so the next record keeps its own codes
+        std::memcpy(out + kBytecodeHeader, buf.data(), kTileCodeBytes);
+        std::vector<float> pl(kPayloadBytes / 4, 1.0f);
+        pl[0] = std::numeric_limits<float>::quiet_NaN();
+        std::memcpy(out + kPayloadOff, pl.data(), kPayloadBytes);
       } else {  // the code area, then the payload (the rest goes into the next record)
         std::memcpy(out + kBytecodeHeader, buf.data(), kTileCodeBytes);
         std::memcpy(out + kPayloadOff, buf.data() + kCodeFloats, kPayloadBytes);

@@ -279,6 +279,18 @@ LaunchProbe take_launch_probe() {
   return p;
 }
 
+namespace detail {
+thread_local bool g_record_names = false;
+thread_local const char* g_last_kernel = nullptr;
+}  // namespace detail
+
+void record_kernel_names(bool on) {
+  detail::g_record_names = on;
+  if (on) detail::g_last_kernel = nullptr;
+}
+
+const char* last_kernel_name() { return detail::g_last_kernel ? detail::g_last_kernel : ""; }
+
 void launch_embed(const EmbedArgs& a, hipStream_t st) {
   launch_kernel(k_embed, dim3(1), dim3(256), st, a);
 }

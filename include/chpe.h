@@ -95,6 +95,9 @@ int chpe_time_stage_live(void *ctx, int stage, size_t n_steps, float *avg_ms);
  * and of a whole step at `pos`. */
 double chpe_stage_bytes(void *ctx, int stage, size_t layer);
 double chpe_step_bytes(void *ctx, size_t pos);
+/* The (mangled) name of the kernel that runs `stage` of layer 0 (numbering as above; the last
+ * launch of the stage), found by launching it once; "" on error. */
+const char *chpe_stage_kernel(void *ctx, int stage);
 
 /* Parity hooks: one projection's GEMV on a caller vector (which: 0 q, 1 k, 2 v, 3 o,
  * 4 gate, 5 up, 6 down, 7 LM head), bias included, no norm; y gets the output rows. */
@@ -133,7 +136,6 @@ int chpe_debug_embed_row_cell(const uint8_t *bytes, size_t len, uint32_t row, ui
  * 0 on success, -1 bad arguments or unsupported shape, -3 device error. */
 int chpe_debug_attention(uint32_t head_dim, uint32_t heads, uint32_t kv_heads, int kv_f16, uint32_t pos,
                          const float *q, const float *k_rows, const float *v_rows, float *out);
-
 /* Gated-DeltaNet (Qwen3.5 linear-attention layers) decode-step kernels on caller data.  The
  * reference has no code for these layers (README claims only); the arithmetic is the gated
  * delta rule as defined by transformers 5.15.0 models/qwen3_5/modeling_qwen3_5.py.

@@ -19,11 +19,13 @@
  * biases N(0,0.02) f32.
  *
  * Layout where the reference reads past a record (its readers, src/chpe_engine.zig):
- *  - a vector longer than a code area's 4096 floats (the 8192-wide norms and q_proj bias
- *    of Qwen2.5-72B, read by unpackNorm / unpackBias :1144-1192 as one array from the code
- *    area) continues through its record's payload (240 floats), the next record's 64-byte
- *    header (16 floats) and the next record's code area; those bytes are the next tile's
- *    leading codes, and that tile's outliers are chosen among the weights after them;
+ *  - a vector longer than a code area's 4096 floats (the 8192-wide q_proj bias of
+ *    Qwen2.5-72B, read by unpackBias :1172-1192 as one array from the code area) continues
+ *    through its record's payload (240 floats), the next record's 64-byte header (16
+ *    floats) and the next record's code area; those bytes are the next tile's leading codes,
+ *    and that tile's outliers are chosen among the weights after them.  Gains of 1.0 that
+ *    wide (the 72B norms, read by unpackNorm :1144-1170) hold 1.0 in the code area and a NaN
+ *    first in the payload: the reader's non-finite rule sets every gain to 1.0;
  *  - embeddings of archives with D >= 4096 (read as 16-row cells, :1540-1546, whose rows and
  *    group scales run past the cell) are written in the per-tile scale form (quant_bits 0,
  *    no group-128 flag: (nibble - 8) * scale + bias, :1384-1394): the code area holds the

@@ -791,6 +791,8 @@ static void set_threads(const oref_engine *e) {
 #endif
 }
 
+void oref_set_threads(oref_engine *e, int threads) { e->threads = threads; }
+
 oref_engine *oref_open_bytes(const uint8_t *bytes, size_t len, int arch_id, size_t max_seq_len,
                              int kv_f16, int threads) {
     oref_engine *e = calloc(1, sizeof *e);
@@ -1154,7 +1156,18 @@ int oref_prefill_synthetic(oref_engine *e, size_t n_pos, uint64_t seed) {
     return 0;
 }
 
+static int forward_layers(oref_engine *e, uint32_t token, size_t pos, size_t n_layers, oref_result *res);
+
 int oref_forward(oref_engine *e, uint32_t token, size_t pos, oref_result *res) {
+    return forward_layers(e, token, pos, e->arch.num_layers, res);
+}
+
+int oref_forward_layers(oref_engine *e, uint32_t token, size_t pos, size_t n_layers, oref_result *res) {
+    /* a timing sample: forwardDecode over the first n_layers layers only */
+    return forward_layers(e, token, pos, n_layers < e->arch.num_layers ? n_layers : e->arch.num_layers, res);
+}
+
+static int forward_layers(oref_engine *e, uint32_t token, size_t pos, size_t n_layers, oref_result *res) {
     /* forwardDecode: chpe_engine.zig:1663-1803 */
     if (pos >= e->max_seq_len) return -2; /* the reference reads past its KV cache here */
     uint64_t t0 = now_ns();
@@ -1163,7 +1176,7 @@ int oref_forward(oref_engine *e, uint32_t token, size_t pos, oref_result *res) {
     size_t D = a->hidden_dim, H = a->num_attn_heads, KV = a->num_kv_heads, hd = a->head_dim,
            I = a->intermediate_dim, qd = H * hd, kvd = KV * hd;
     oref_unpack_embed_row(e, token, e->hidden);
-    for (size_t l = 0; l < a->num_layers; l++) {
+    for (size_t l = 0; l < n_layers; l++) {
         oref_layer_info li;
         oref_layer_info_for(e->map, l, &li);
         oref_unpack_norm(e, li.input_norm, e->norm_gamma, D);

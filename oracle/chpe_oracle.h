@@ -115,6 +115,10 @@ oref_engine *oref_open_bytes(const uint8_t *bytes, size_t len, int arch_id,
                              size_t max_seq_len, int kv_f16, int threads);
 void oref_close(oref_engine *e);
 int oref_forward(oref_engine *e, uint32_t token, size_t pos, oref_result *res);
+/* worker threads of the row-parallel loops (results do not depend on it) */
+void oref_set_threads(oref_engine *e, int threads);
+/* the same step over the first n_layers layers only (a CPU timing sample) */
+int oref_forward_layers(oref_engine *e, uint32_t token, size_t pos, size_t n_layers, oref_result *res);
 /* Timing aid (no reference counterpart): fill K/V cache rows 0..n_pos-1 of every layer with
  * seeded values in [-1, 1) (fp16-rounded in kv_f16 mode), so that oref_forward can be timed at
  * position n_pos without decoding a prompt first.  Returns -2 if n_pos > max_seq_len. */

@@ -49,6 +49,9 @@ def lib():
         L.oref_close.argtypes = [V]
         L.oref_forward.restype = ctypes.c_int
         L.oref_forward.argtypes = [V, ctypes.c_uint32, S, ctypes.POINTER(Result)]
+        L.oref_forward_layers.restype = ctypes.c_int
+        L.oref_forward_layers.argtypes = [V, ctypes.c_uint32, S, S, ctypes.POINTER(Result)]
+        L.oref_set_threads.argtypes = [V, ctypes.c_int]
         L.oref_logits.restype = _fp
         L.oref_logits.argtypes = [V]
         L.oref_hidden.restype = _fp
@@ -139,6 +142,17 @@ class Oracle:
         if rc:
             raise RuntimeError(f"oref_forward rc={rc}")
         return r
+
+    def forward_layers(self, token, pos, n_layers):
+        """The decode step over the first n_layers layers only (a timing sample)."""
+        r = Result()
+        rc = self.L.oref_forward_layers(self.e, token, pos, n_layers, ctypes.byref(r))
+        if rc:
+            raise RuntimeError(f"oref_forward_layers rc={rc}")
+        return r
+
+    def set_threads(self, n):
+        self.L.oref_set_threads(self.e, n)
 
     def prefill_synthetic(self, n_pos, seed=0):
         if self.L.oref_prefill_synthetic(self.e, n_pos, seed):

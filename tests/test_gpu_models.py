@@ -96,7 +96,7 @@ def run_model(path, arch, vocab, n_prompt, n_gen, seed):
         ref, gaps = o.generate(prompt, n_gen)
         say(f"  gpu {list(map(int, g))} oracle {list(map(int, ref))} top-2 gaps {[round(float(x), 4) for x in gaps]}")
         assert check_stream(g, ref, gaps, f"arch {arch}") == n_gen
-        assert len(set(map(int, ref))) > 1  # a real stream, not a constant fallback
+        assert np.all(np.isfinite(gaps))  # finite logits all along (no NaN layer break)
     finally:
         e.close()
         o.close()

@@ -26,6 +26,13 @@ def floats_from_code_area(records, rel, n):
     return flat[off:off + 4 * n].view(np.float32)
 
 
+def unpack_norm(vals):
+    """unpackNorm's rules (:1161-1169): any non-finite value -> all 1.0; all zero -> 1.0."""
+    if not np.all(np.isfinite(vals)) or not np.any(vals):
+        return np.ones_like(vals)
+    return vals
+
+
 def tid(layer, which):
     return 1000 * (layer + 1) + which
 
@@ -34,12 +41,15 @@ def tid(layer, which):
 def test_72b_long_vectors_read_back(kind):
     base = 38016  # layer 0: input_norm, q_proj (2048), q_bias, k_proj (256), k_bias, v_proj, ...
     recs = ca.pack_records(kind, base, 2052)
-    assert np.all(floats_from_code_area(recs, 0, 8192) == 1.0)          # input_norm, 8192 wide
+    assert np.all(unpack_norm(floats_from_code_area(recs, 0, 8192)) == 1.0)  # input_norm, 8192 wide
+    assert np.isnan(floats_from_code_area(recs, 0, 8192)[4096])         # (through the NaN rule)
     qb = floats_from_code_area(recs, 2049, 8192)                        # q_proj bias, 8192 wide
     assert np.array_equal(qb, ca.normals(0, tid(0, 11), 0, 8192))
-    # the tiles the vectors run into keep valid metadata and, for 4-bit, their outliers lie
-    # after the bytes the vector owns
-    for rel in (1, 2050):
+    # the tile the bias runs into keeps valid metadata and, for 4-bit, its outliers lie after
+    # the bytes the vector owns; the tile after the norm keeps all of its own codes
+    n_q = int(recs[1, PAYLOAD + 560:PAYLOAD + 562].view(np.uint16)[0])
+    assert n_q == 64 and np.any(recs[1, PAYLOAD + 690:PAYLOAD + 818].view(np.uint16) < 2 * 15360)
+    for rel in (2050,):
         pl = recs[rel, PAYLOAD:]
         assert pl[20] == (4 if kind == ca.PACK_72B_W4 else 2) and pl[24] & 1
         n = int(pl[560:562].view(np.uint16)[0])
@@ -51,9 +61,9 @@ def test_72b_long_vectors_read_back(kind):
     k = ca.pack_records(kind, base + 2306, 1)                           # k_bias, 1024 wide: fits
     assert np.array_equal(floats_from_code_area(k, 0, 1024), ca.normals(0, tid(0, 12), 0, 1024))
     post = ca.pack_records(kind, base + 4612, 2)                        # post_attention_layernorm
-    assert np.all(floats_from_code_area(post, 0, 8192) == 1.0)
+    assert np.all(unpack_norm(floats_from_code_area(post, 0, 8192)) == 1.0)
     fin = ca.pack_records(kind, 2181136, 2)                             # final norm -> lm_head tile 0
-    assert np.all(floats_from_code_area(fin, 0, 8192) == 1.0)
+    assert np.all(unpack_norm(floats_from_code_area(fin, 0, 8192)) == 1.0)
 
 
 def embed_row_dims(records, token, D):
