@@ -29,7 +29,7 @@ ENGINE_SYMBOLS = [
     "chpe_generate", "chpe_verify", "chpe_last_error", "chpe_get_max_seq_len", "chpe_get_hidden",
     "chpe_time_steps", "chpe_time_stage", "chpe_time_stage_live", "chpe_stage_bytes", "chpe_step_bytes", "chpe_stage_kernel",
     "chpe_debug_gemv", "chpe_debug_flat_tile_weights", "chpe_debug_gemv_flat", "chpe_debug_gemv_cells", "chpe_debug_embed_row_cell",
-    "chpe_debug_attention", "chpe_debug_deltanet_conv", "chpe_debug_deltanet_step",
+    "chpe_debug_attention", "chpe_attention_noalloc", "chpe_debug_deltanet_conv", "chpe_debug_deltanet_step",
 ]
 
 _c_float_p = ctypes.POINTER(ctypes.c_float)
@@ -87,6 +87,8 @@ def load_engine_lib():
             "chpe_debug_embed_row_cell": (I, [_c_u8_p, S, ctypes.c_uint32, ctypes.c_uint32, _c_float_p]),
             "chpe_debug_attention": (I, [ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32, I, ctypes.c_uint32,
                                          _c_float_p, _c_float_p, _c_float_p, _c_float_p]),
+            "chpe_attention_noalloc": (I, [ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32, I, ctypes.c_uint32,
+                                           ctypes.c_uint32, V, V, V, V, V]),
             "chpe_debug_deltanet_conv": (I, [ctypes.c_uint32, ctypes.c_uint32, _c_float_p, _c_float_p, _c_float_p,
                                              _c_float_p]),
             "chpe_debug_deltanet_step": (I, [ctypes.c_uint32] * 3 + [_c_float_p] * 9 + [F, _c_float_p, _c_float_p]),

@@ -9,6 +9,9 @@
 // V rows (k_attn_mfma on the matrix cores for the fp16 cache, k_attn_chunk on the vector ALUs
 // for the f32 cache); k_attn_merge rescales and merges the chunks.  Workgroup (chunk, kv head)
 // serves the query heads that share the kv head, so every K/V row is read from HBM once per step.
+#include <cmath>
+#include <mutex>
+
 #include "device_common.hpp"
 #include "kernels.hpp"
 
@@ -475,4 +478,75 @@ void launch_attention(const AttnArgs& a, hipStream_t st) {
   launch_attention_combine(a, st);
 }
 
+// ---- the decode attention on caller buffers with no allocation ------------------------------
+// The chunk kernels' partials (max and sum per chunk and query head, and the weighted V rows)
+// and the position they read live in `scratch`, a file-scope device array: each GPU holds its
+// own copy.  Host code never passes the array's name to a kernel (on the host it is a stand-in,
+// not a device address): the device address of each GPU's copy is looked up once, with that
+// device current, and kept in g_scratch_ptr.
+namespace {
+
+__device__ __align__(256) uint8_t scratch[kAttnScratchBytes];
+
+constexpr int kMaxDevices = 64;
+void* g_scratch_ptr[kMaxDevices] = {};
+std::once_flag g_scratch_once[kMaxDevices];
+hipError_t g_scratch_err[kMaxDevices] = {};
+
+__global__ void k_set_position(StepState* st, uint32_t pos) {
+  StepState s{};
+  s.pos = pos;
+  *st = s;
+}
+
+}  // namespace
+
+// device address of this GPU's scratch array (null when the lookup failed)
+static void* scratch_on_current_device() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+  std::call_once(g_scratch_once[dev], [dev] {
+    void* p = nullptr;
+    g_scratch_err[dev] = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (g_scratch_err[dev] == hipSuccess) g_scratch_ptr[dev] = p;
+  });
+  return g_scratch_ptr[dev];
+}
+
 }  // namespace chpe
+
+using namespace chpe;
+
+extern "C" int chpe_attention_noalloc(uint32_t head_dim, uint32_t heads, uint32_t kv_heads, int kv_f16,
+                                      uint32_t pos, uint32_t max_seq, const float* q, const void* k_cache,
+                                      const void* v_cache, float* out, void* stream) {
+  if (!q || !k_cache || !v_cache || !out || !attention_supported(heads, kv_heads, head_dim)) return -1;
+  if (max_seq == 0 || max_seq % 16 != 0 || pos >= max_seq) return -1;
+  const uint32_t chunk = attn_chunk_of(head_dim), n_chunks = (pos + chunk) / chunk;
+  const size_t ml = size_t(heads) * n_chunks * 2 * 4, acc = size_t(heads) * n_chunks * head_dim * 4;
+  // the position, then the two partial arrays, each at a 256-byte boundary
+  const size_t off_ml = 256, off_acc = off_ml + (ml + 255) / 256 * 256;
+  if (n_chunks > kAttnMaxChunks || off_acc + acc > kAttnScratchBytes) return -2;
+  uint8_t* base = static_cast<uint8_t*>(scratch_on_current_device());
+  if (!base) return -3;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  StepState* state = reinterpret_cast<StepState*>(base);
+  hipLaunchKernelGGL(k_set_position, dim3(1), dim3(1), 0, st, state, pos);
+  AttnArgs a{};
+  a.state = state;
+  a.q = q;
+  a.k_cache = k_cache;
+  a.v_cache = v_cache;
+  a.out = out;
+  a.part_ml = reinterpret_cast<float*>(base + off_ml);
+  a.part_acc = reinterpret_cast<float*>(base + off_acc);
+  a.H = heads;
+  a.KV = kv_heads;
+  a.hd = head_dim;
+  a.max_seq = max_seq;
+  a.n_chunks = n_chunks;
+  a.kv_f16 = kv_f16 ? 1 : 0;
+  a.scale = 1.0f / std::sqrt(float(head_dim));
+  launch_attention(a, st);
+  return hipGetLastError() == hipSuccess ? 0 : -3;
+}

@@ -225,6 +225,8 @@ void launch_attention_partial(const AttnArgs& a, hipStream_t stream);
 void launch_attention_combine(const AttnArgs& a, hipStream_t stream);
 void launch_finish(const FinishArgs& a, hipStream_t stream);
 constexpr uint32_t kAttnMaxChunks = 320;  // chunks of attn_chunk(hd) positions per launch
+// device scratch of chpe_attention_noalloc (position + partials), per GPU
+constexpr size_t kAttnScratchBytes = size_t(8) << 20;
 __host__ __device__ constexpr uint32_t attn_chunk_of(uint32_t hd) { return 8192u / hd; }
 inline uint32_t attn_chunk(uint32_t hd) { return attn_chunk_of(hd); }
 // (hd, query heads per kv head) pairs the attention kernels are built for

@@ -136,6 +136,20 @@ int chpe_debug_embed_row_cell(const uint8_t *bytes, size_t len, uint32_t row, ui
  * 0 on success, -1 bad arguments or unsupported shape, -3 device error. */
 int chpe_debug_attention(uint32_t head_dim, uint32_t heads, uint32_t kv_heads, int kv_f16, uint32_t pos,
                          const float *q, const float *k_rows, const float *v_rows, float *out);
+/* No counterpart in the reference.  The decode step's attention (chunk + merge kernels) on
+ * caller device buffers, allocating nothing: for callers that cannot allocate (code under HIP
+ * graph capture, serving loops, harnesses that forbid hipMalloc).  q [heads][head_dim] f32
+ * rotated queries; k_cache [kv_heads][max_seq][head_dim] and v_cache in the engine's cache
+ * layout (f32: as k_cache; kv_f16: fp16, k as above, v [kv_heads][max_seq/4][head_dim][4]),
+ * rows 0..pos written; out [heads][head_dim] f32; all device pointers on the current device.
+ * max_seq: cache rows per kv head, a multiple of 16, > pos.  stream: a hipStream_t (null: the
+ * default stream); the call only enqueues.  The chunk partials live in a per-GPU device array
+ * of 8 MiB (heads * ceil((pos+1)/chunk) * (head_dim + 2) * 4 bytes must fit, chunk = 8192 /
+ * head_dim positions); calls that overlap on one GPU race on it.  Returns 0, -1 bad arguments
+ * or unsupported shape, -2 the partials exceed the scratch, -3 device error. */
+int chpe_attention_noalloc(uint32_t head_dim, uint32_t heads, uint32_t kv_heads, int kv_f16, uint32_t pos,
+                           uint32_t max_seq, const float *q, const void *k_cache, const void *v_cache,
+                           float *out, void *stream);
 /* Gated-DeltaNet (Qwen3.5 linear-attention layers) decode-step kernels on caller data.  The
  * reference has no code for these layers (README claims only); the arithmetic is the gated
  * delta rule as defined by transformers 5.15.0 models/qwen3_5/modeling_qwen3_5.py.
