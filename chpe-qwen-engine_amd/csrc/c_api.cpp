@@ -372,6 +372,105 @@ int chpe_debug_gemv_flat(int mode, uint32_t rows, uint32_t cols, const uint8_t* 
   return rc;
 }
 
+// One GEMV over polymorphic 16-row cells (any width, gemvTilePolymorphic) through the engine's
+// polymorphic path (the raw row sums cell by cell, then the mode's epilogue).
+int chpe_debug_gemv_poly(int mode, uint32_t rows, uint32_t cols, const uint8_t* cells, const uint8_t* cells_up,
+                         size_t n_cells, const float* x, const float* gamma, float eps, float* y, uint32_t* out_argmax,
+                         float* out_hidden_norm) {
+  g_last_error.clear();
+  const bool norm = mode == int(GemvMode::SwiGlu) || mode == int(GemvMode::Logits);
+  if (!cells || !x || !y || rows == 0 || cols == 0 || n_cells == 0 || mode < 0 || mode > int(GemvMode::Logits) ||
+      norm != (gamma != nullptr) || (mode == int(GemvMode::SwiGlu)) != (cells_up != nullptr))
+    return -1;
+  const int n_parts = mode == int(GemvMode::SwiGlu) ? 2 : 1;
+  const uint8_t* src[2] = {cells, cells_up};
+  constexpr size_t kShift = 64, kPad = size_t(1) << 20;  // as the engine's archive image
+  const size_t img = kShift + n_cells * kCellBytes + kPad;
+  std::vector<uint32_t> rb[2];
+  for (int i = 0; i < n_parts; ++i) {
+    bool uniform = false;
+    uint64_t reach = 0;
+    walk_cells(src[i], n_cells * kCellBytes, kCellBytes, n_cells, rows, cols, &rb[i], &uniform, &reach);
+    if (reach > n_cells * kCellBytes + kPad) {
+      g_last_error = "cells read past the end of the given cells";
+      return -1;
+    }
+  }
+  std::vector<void*> mem;
+  auto alloc = [&](size_t bytes) -> void* {
+    void* d = nullptr;
+    if (hipMalloc(&d, bytes) != hipSuccess) return nullptr;
+    mem.push_back(d);
+    return d;
+  };
+  int rc = -3;
+  GemvArgs a{};
+  a.n_parts = n_parts;
+  a.mode = mode;
+  a.C = cols;
+  a.eps = eps;
+  float* dx = static_cast<float*>(alloc(size_t(cols) * 4));
+  float* dxn = static_cast<float*>(alloc(size_t(cols) * 4));
+  float* dy = static_cast<float*>(alloc(size_t(rows) * 4));
+  float* dg = norm ? static_cast<float*>(alloc(size_t(cols) * 4)) : nullptr;
+  PolyRaw raw{};
+  PolyPlan plan[2]{};
+  const PolyPlan* pp[kMaxParts] = {};
+  bool ok = dx && dxn && dy && (!norm || dg) && hipMemcpy(dx, x, size_t(cols) * 4, hipMemcpyHostToDevice) == hipSuccess &&
+            hipMemcpy(dy, y, size_t(rows) * 4, hipMemcpyHostToDevice) == hipSuccess &&
+            (!norm || hipMemcpy(dg, gamma, size_t(cols) * 4, hipMemcpyHostToDevice) == hipSuccess);
+  for (int i = 0; ok && i < n_parts; ++i) {
+    uint8_t* d = static_cast<uint8_t*>(alloc(img));
+    uint32_t* drb = static_cast<uint32_t*>(alloc(rb[i].size() * 4));
+    raw.y[i] = static_cast<float*>(alloc(size_t(rows) * 4));
+    ok = d && drb && raw.y[i] && hipMemset(d, 0, img) == hipSuccess &&
+         hipMemcpy(d + kShift, src[i], n_cells * kCellBytes, hipMemcpyHostToDevice) == hipSuccess &&
+         hipMemcpy(drb, rb[i].data(), rb[i].size() * 4, hipMemcpyHostToDevice) == hipSuccess;
+    plan[i].row_base = drb;
+    plan[i].n_cells = uint32_t(rb[i].size() - 1);
+    pp[i] = &plan[i];
+    GemvPart& p = a.part[i];
+    p.base = d + kShift;
+    p.stride = uint32_t(kCellBytes);
+    p.rows = rows;
+    p.wrows = rows;
+    p.y = dy;
+  }
+  a.x = dx;
+  a.gamma = dg;
+  StepResult* dres = nullptr;
+  StepState* dst = nullptr;
+  if (ok && mode == int(GemvMode::Logits)) {
+    a.partials = static_cast<ArgmaxPartial*>(alloc(size_t(kPolyEpilogueBlocks) * sizeof(ArgmaxPartial)));
+    dres = static_cast<StepResult*>(alloc(sizeof(StepResult)));
+    dst = static_cast<StepState*>(alloc(sizeof(StepState)));
+    a.result = dres;
+    ok = a.partials && dres && dst && hipMemset(dst, 0, sizeof(StepState)) == hipSuccess &&
+         hipMemset(dres, 0, sizeof(StepResult)) == hipSuccess;
+  }
+  if (ok) {
+    const uint32_t n_partials = launch_gemv_poly(a, pp, dxn, raw, nullptr);
+    if (mode == int(GemvMode::Logits)) {
+      FinishArgs f{};
+      f.state = dst;
+      f.partials = a.partials;
+      f.n_partials = n_partials;
+      f.logits = dy;
+      f.result = dres;
+      launch_finish(f, nullptr);
+    }
+    StepResult r{};
+    if (hipDeviceSynchronize() == hipSuccess && hipMemcpy(y, dy, size_t(rows) * 4, hipMemcpyDeviceToHost) == hipSuccess &&
+        (mode != int(GemvMode::Logits) || hipMemcpy(&r, dres, sizeof r, hipMemcpyDeviceToHost) == hipSuccess)) {
+      if (out_argmax) *out_argmax = r.argmax;
+      if (out_hidden_norm) *out_hidden_norm = r.hidden_norm;
+      rc = 0;
+    }
+  }
+  for (void* m : mem) (void)hipFree(m);
+  return rc;
+}
+
 int chpe_debug_gemv_cells(int mode, uint32_t rows, const uint8_t* cells, const uint8_t* cells_up, size_t n_cells,
                           const float* x, const float* gamma, float eps, float* y, uint32_t* out_argmax,
                           float* out_hidden_norm) {

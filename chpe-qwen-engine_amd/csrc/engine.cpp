@@ -349,6 +349,39 @@ bool plan_flat_tiles(const uint8_t* cells, size_t len, size_t stride, size_t n_t
   return true;
 }
 
+void walk_cells(const uint8_t* b, size_t len, size_t stride, size_t n_avail, size_t r_total, size_t c_total,
+                std::vector<uint32_t>* row_base, bool* uniform_w4, uint64_t* extent) {
+  size_t rb = 0;
+  bool uniform = true;
+  unsigned __int128 reach = 0;
+  row_base->clear();
+  for (size_t t = 0; t < n_avail; ++t) {
+    if (rb >= r_total) break;
+    const size_t pl = t * stride + kPayloadOff;
+    const uint32_t rows = rd<uint32_t>(b, len, pl + kDimsRows);
+    if (rows == 0) break;
+    const uint32_t cols = rd<uint32_t>(b, len, pl + kDimsCols);
+    const uint8_t qb = rd<uint8_t>(b, len, pl + kMetaQuantBits);
+    const bool g128 = (rd<uint64_t>(b, len, pl + kMetaCustomFlags) & kFlagGroup128) != 0;
+    uniform = uniform && rows == 16 && cols == c_total && qb == 4 && g128;
+    // the bytes the polymorphic kernel reads for this cell's used rows: codes at the row stride
+    // of its width, group scales past the payload for tall cells
+    const unsigned __int128 used = std::min<size_t>(rows, r_total - rb);
+    const unsigned __int128 row_bytes = qb == 4 ? cols / 2 : qb == 8 ? cols : qb == 16 ? 2ull * cols
+                                        : qb == 32 ? 4ull * cols : cols / 4;
+    unsigned __int128 end = t * stride + kPayloadOff + 1024;  // metadata, row outliers
+    end = std::max(end, t * stride + kBytecodeHeader + used * row_bytes);
+    if (g128 && (qb == 4 || !(qb == 8 || qb == 16 || qb == 32)))
+      end = std::max(end, t * stride + kPayloadOff + kGroupScales + 2 * used * (cols / 128));
+    reach = std::max(reach, end);
+    row_base->push_back(uint32_t(rb));
+    rb += rows;
+  }
+  row_base->push_back(uint32_t(std::min(rb, r_total)));
+  *uniform_w4 = uniform && rb == r_total;
+  if (extent) *extent = reach > ~uint64_t(0) ? ~uint64_t(0) : uint64_t(reach);
+}
+
 bool Engine::plan_projection(size_t tile_start, size_t num_tiles, size_t r_total, size_t c_total,
                              size_t x_len, size_t y_len, bool accumulate, int64_t bias_tile,
                              ProjPlan* p, std::string* err) {
@@ -396,29 +429,31 @@ bool Engine::plan_projection(size_t tile_start, size_t num_tiles, size_t r_total
         (void)hipMemcpy(p->corr, ent.data(), ent.size() * sizeof(float2), hipMemcpyHostToDevice);
       }
     } else {  // 16-row polymorphic cells: row bases are a prefix sum of dims.rows
-      size_t row_base = 0, n_cells = 0;
-      for (size_t t = 0; t < avail; ++t) {
-        if (row_base >= r_total) break;
-        const size_t pl = cell(t) + kPayloadOff;
-        const uint32_t rows = rd<uint32_t>(b, len, pl + kDimsRows);
-        if (rows == 0) break;
-        const uint32_t cols = rd<uint32_t>(b, len, pl + kDimsCols);
-        if (rows != 16 || cols != 2048 || b[pl + kMetaQuantBits] != 4 ||
-            !(rd<uint64_t>(b, len, pl + kMetaCustomFlags) & kFlagGroup128)) {
-          *err = "cell " + std::to_string(tile_start + t) +
-                 " is not a 16x2048 group-128 4-bit cell (other polymorphic cells are not built "
-                 "on the GPU path yet)";
+      std::vector<uint32_t> rb;
+      bool uniform = false;
+      uint64_t reach = 0;
+      walk_cells(b + cell(0), len - cell(0), stride_, avail, r_total, c_total, &rb, &uniform, &reach);
+      if (uniform && c_total == 2048 && x_len >= 2048 && y_len >= r_total) {
+        p->kind = WeightKind::Cell16W4;
+      } else {  // any other mix of widths: the polymorphic kernel, cell by cell
+        if (reach > image_len_ - cell(0)) {  // the device image holds the archive + kImagePad
+          *err = "polymorphic cells read past the end of the archive";
           return false;
         }
-        row_base += rows;
-        ++n_cells;
+        p->kind = WeightKind::Cell16Poly;
+        p->poly.n_cells = uint32_t(rb.size() - 1);
+        uint32_t* d = static_cast<uint32_t*>(dev_alloc(rb.size() * 4));
+        if (!d) { *err = "allocation"; return false; }
+        (void)hipMemcpy(d, rb.data(), rb.size() * 4, hipMemcpyHostToDevice);
+        p->poly.row_base = d;
+        if (!d_xn_) {
+          const size_t n = std::max({arch_.hidden_dim, arch_.intermediate_dim, arch_.vocab_size,
+                                     arch_.num_attn_heads * arch_.head_dim});
+          d_xn_ = static_cast<float*>(dev_alloc(std::max(arch_.hidden_dim, arch_.intermediate_dim) * 4));
+          for (int i = 0; i < kMaxParts; ++i) poly_raw_.y[i] = static_cast<float*>(dev_alloc(n * 4));
+          if (!d_xn_ || !poly_raw_.y[kMaxParts - 1]) { *err = "allocation"; return false; }
+        }
       }
-      if (row_base != r_total || c_total != 2048 || x_len < 2048 || y_len < r_total) {
-        *err = "16-row cells do not cover the tensor exactly";
-        return false;
-      }
-      (void)n_cells;
-      p->kind = WeightKind::Cell16W4;
     }
   } else {
     if (quant_bits_ != 16) { *err = "raw int8 tiles are not built on the GPU path yet"; return false; }
@@ -550,6 +585,11 @@ uint32_t Engine::enqueue_gemv(const ProjPlan* const* parts, float* const* outs, 
     a.partials = d_partials_;
     a.result = d_result_;
     a.hidden_out = embed_fused_ ? d_hidden_out_ : nullptr;
+  }
+  if (parts[0]->kind == WeightKind::Cell16Poly) {
+    const PolyPlan* pp[kMaxParts] = {};
+    for (int i = 0; i < n; ++i) pp[i] = &parts[i]->poly;
+    return launch_gemv_poly(a, pp, d_xn_, poly_raw_, st);
   }
   launch_gemv(parts[0]->kind, a, g, st);
   return g.blocks;
@@ -818,6 +858,7 @@ double Engine::proj_bytes(const ProjPlan& p) const {
     case WeightKind::Cell16W4: bytes = n / 2 + n / 128 * 2 + double(p.rows / 16) * (16 * 8 * 2 + 8 * 2); break;
     case WeightKind::FlatW4: bytes = n / 2 + n / 128 * 2 + std::ceil(n / kFlatWeights) * (2 + 64 * 4); break;
     case WeightKind::FlatW2: bytes = n / 4 + n / 128 * 2 + std::ceil(n / kFlatWeights) * (2 + 64 * 4); break;
+    case WeightKind::Cell16Poly: bytes = double(p.poly.n_cells) * kTileCodeBytes; break;  // the code areas
   }
   if (p.bias) bytes += 4.0 * p.rows;
   return bytes;

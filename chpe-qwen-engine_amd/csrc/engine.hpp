@@ -57,7 +57,15 @@ struct ProjPlan {
   float2* corr = nullptr;              // device [rows][corr_kmax] flat-tile outlier corrections
   uint32_t corr_kmax = 0;
   CellReplace* repl = nullptr;         // device, replace-mode outliers of 16-row cells
+  PolyPlan poly{};                     // Cell16Poly: the cells' row bases
 };
+
+// The cells of a 16-row-cell tensor (c_total <= 2048) as gemvLinear walks them (:1430-1442):
+// row bases are the prefix sums of dims.rows until rows == 0 or r_total is reached.
+// *uniform_w4: every cell is a 16 x c_total group-128 4-bit cell and they cover r_total rows.
+// *extent (when set): the bytes from the first cell's start that the polymorphic kernel reads.
+void walk_cells(const uint8_t* cells, size_t len, size_t stride, size_t n_avail, size_t r_total, size_t c_total,
+                std::vector<uint32_t>* row_base, bool* uniform_w4, uint64_t* extent);
 
 // A flat-tile tensor (gemvCellFlat, src/chpe_engine.zig:584-729) of r_total x c_total weights in
 // n_tiles cells at cells + t * stride (host bytes, len readable): checks that the tiles are
@@ -188,6 +196,8 @@ class Engine {
   bool embed_fused_ = false;         // k_finish embeds the next token (see init)
   float* d_hidden_out_ = nullptr;    // the last step's final hidden state when embed_fused_
   float* d_rope_cur_ = nullptr;      // the step's cos / sin rows (head_dim floats)
+  float* d_xn_ = nullptr;            // polymorphic cells: the RMSNorm'ed input
+  PolyRaw poly_raw_{};               // polymorphic cells: raw row sums per part
   int probe_stage_ = -1;                 // stage bracketed by events in record_step
   hipEvent_t* probe_events_ = nullptr;
   size_t probe_next_ = 0;

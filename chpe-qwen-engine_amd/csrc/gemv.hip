@@ -1756,6 +1756,151 @@ void launch_layout(const GemvArgs& a, const GemvLaunch& g, hipStream_t st) {
   }
 }
 
+// ---- polymorphic 16-row cells of any width (gemvTilePolymorphic, chpe_engine.zig:732-751) ----
+// Tensors whose cells are not all 16 x 2048 group-128 4-bit cells: each cell is dequantised by
+// its own metadata -- 2-bit codebook (:223-323), 4-bit (:326-418), int8 with one scale and
+// bias per row (:421-472), fp16 / bf16 (:475-541), f32 (:544-581), unknown widths as 2-bit
+// (:746-749), group-128 scales or the tile's scale / bias, outliers added for group-128 cells
+// of 16 rows -- into raw row sums; a second launch applies the mode's epilogue.  Rows are the
+// prefix sums of dims.rows the host computed by gemvLinear's walk (:1430-1442).
+
+// x (RMSNorm'ed with gamma when gamma is set: (x * inv_rms) * gamma, rmsNorm :163-193) into out
+// (and |x|, the hidden norm of the LM head's input, into *result when set)
+__global__ void __launch_bounds__(1024) k_rmsnorm(const float* x, const float* gamma, float eps, uint32_t n,
+                                                  float* out, StepResult* result) {
+#pragma clang fp contract(off)
+  __shared__ float s_red[16];
+  float ss = 0.0f;
+  for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) ss += x[i] * x[i];
+#pragma unroll
+  for (int m = 1; m < 64; m <<= 1) ss = pair_sum(ss, m);
+  if ((threadIdx.x & 63) == 0) s_red[threadIdx.x >> 6] = ss;
+  __syncthreads();
+  float tot = 0.0f;
+  for (int w = 0; w < int(blockDim.x / kWave); ++w) tot += s_red[w];
+  const float inv = 1.0f / sqrtf(tot / float(n) + eps);
+  for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) out[i] = (x[i] * inv) * gamma[i];
+  if (result && threadIdx.x == 0) result->hidden_norm = sqrtf(tot);
+}
+
+__device__ __forceinline__ float poly_w2(uint32_t code) {  // CODEBOOK_W2 (:220)
+  return code == 0 ? 0.0f : (code == 1 ? 1.0f : (code == 2 ? -2.0f : -1.0f));
+}
+
+// one workgroup per cell (4 waves, wave w takes rows w, w + 4, ...); block n_cells zeroes the
+// rows past the last cell
+__global__ void __launch_bounds__(256) k_gemv_poly(const uint8_t* base, uint32_t stride, const uint32_t* row_base,
+                                                    uint32_t n_cells, const float* x, uint32_t x_len, float* raw,
+                                                    uint32_t y_len) {
+#pragma clang fp contract(off)
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (blockIdx.x == n_cells) {
+    for (uint32_t r = row_base[n_cells] + threadIdx.x; r < y_len; r += blockDim.x) raw[r] = 0.0f;
+    return;
+  }
+  const uint8_t* cell = base + size_t(blockIdx.x) * stride;
+  const uint8_t* codes = cell + 64;
+  const uint8_t* pl = cell + 16448;
+  const uint32_t qb = pl[20];
+  const bool g128 = (*reinterpret_cast<const uint32_t*>(pl + 24) & 1u) != 0;
+  const float scale = *reinterpret_cast<const float*>(pl + 32), bias = *reinterpret_cast<const float*>(pl + 36);
+  const uint32_t rows = *reinterpret_cast<const uint32_t*>(pl + 40), cols = *reinterpret_cast<const uint32_t*>(pl + 44);
+  const uint32_t rb = row_base[blockIdx.x];
+  if (rb >= y_len) return;
+  const uint32_t max_rows = rows < y_len - rb ? rows : y_len - rb;
+  const uint32_t kind = (qb == 4 || qb == 8 || qb == 16 || qb == 32) ? qb : 2u;
+  const bool outl = g128 && rows == 16 && (kind == 2 || kind == 4);
+  const uint32_t total_g = cols / 128, ng = total_g < x_len / 128 ? total_g : x_len / 128;
+  const uint32_t max_cols = cols < x_len ? cols : x_len;
+  for (uint32_t r = wave; r < max_rows; r += 4) {
+    float acc = 0.0f;
+    if (kind == 4) {
+      const uint8_t* rowb = codes + size_t(r) * (cols / 2);
+      if (g128) {
+        for (uint32_t c = lane; c < ng * 128; c += 64) {
+          const float q = float((rowb[c / 2] >> (4 * (c & 1))) & 15u) - 8.0f;
+          acc += (q * x[c]) * h2f(*reinterpret_cast<const uint16_t*>(pl + 48 + 2 * (r * total_g + c / 128)));
+        }
+      } else {
+        const uint32_t pairs = cols / 2 < x_len / 2 ? cols / 2 : x_len / 2;
+        for (uint32_t c = lane; c < 2 * pairs; c += 64) {
+          const float q = float((rowb[c / 2] >> (4 * (c & 1))) & 15u) - 8.0f;
+          acc += (q * scale + bias) * x[c];
+        }
+      }
+    } else if (kind == 2) {
+      const uint8_t* rowb = codes + size_t(r) * (cols / 4);
+      if (g128) {
+        for (uint32_t c = lane; c < ng * 128; c += 64) {
+          const float q = poly_w2((rowb[c / 4] >> (2 * (c & 3))) & 3u);
+          acc += (q * x[c]) * h2f(*reinterpret_cast<const uint16_t*>(pl + 48 + 2 * (r * total_g + c / 128)));
+        }
+      } else {
+        const uint32_t quads = cols / 4 < x_len / 4 ? cols / 4 : x_len / 4;
+        for (uint32_t c = lane; c < 4 * quads; c += 64) {
+          const float q = poly_w2((rowb[c / 4] >> (2 * (c & 3))) & 3u);
+          acc += (q * scale + bias) * x[c];
+        }
+      }
+    } else if (kind == 8) {
+      const int8_t* rowb = reinterpret_cast<const int8_t*>(codes) + size_t(r) * cols;
+      for (uint32_t c = lane; c < max_cols; c += 64) acc += float(rowb[c]) * x[c];
+    } else if (kind == 16) {
+      const uint16_t* rowb = reinterpret_cast<const uint16_t*>(codes) + size_t(r) * cols;
+      const bool fp16 = (*reinterpret_cast<const uint32_t*>(pl + 24) & 4u) != 0;
+      for (uint32_t c = lane; c < max_cols; c += 64) acc += (fp16 ? h2f(rowb[c]) : bf2f(rowb[c])) * x[c];
+    } else {
+      const float* rowb = reinterpret_cast<const float*>(codes) + size_t(r) * cols;
+      for (uint32_t c = lane; c < max_cols; c += 64) acc += rowb[c] * x[c];
+    }
+#pragma unroll
+    for (int m = 1; m < 64; m <<= 1) acc = pair_sum(acc, m);
+    if (outl) {  // outliers added (:309-315): lane k < 8 takes entry k; their sum joins on lane 0
+      const uint32_t k = uint32_t(lane) & 7u;
+      const uint32_t col = *reinterpret_cast<const uint16_t*>(pl + 816 + 2 * k);
+      float o = (lane < 8 && col < x_len) ? h2f(*reinterpret_cast<const uint16_t*>(pl + 560 + 2 * (r * 8 + k))) * x[col]
+                                          : 0.0f;
+#pragma unroll
+      for (int m = 1; m < 8; m <<= 1) o = pair_sum(o, m);
+      acc += o;
+    }
+    if (kind == 8) acc = acc * scale + bias;  // (:461)
+    if (lane == 0) raw[rb + r] = acc;
+  }
+}
+
+// the mode's epilogue on the raw row sums: grid-stride over rows (QkvRope: over RoPE pairs)
+template <int MODE>
+__global__ void __launch_bounds__(256) k_poly_epilogue(GemvArgs a, PolyRaw raw) {
+#pragma clang fp contract(off)
+  __shared__ float s_bv[4];
+  __shared__ uint32_t s_bi[4], s_nf[4];
+  float bv = -1e30f;
+  uint32_t bi = 0xffffffffu, nf = 0;
+  const uint32_t stride = gridDim.x * blockDim.x;
+  if constexpr (MODE == int(GemvMode::QkvRope)) {
+    const uint32_t half = a.rope.head_dim / 2;
+    for (int p = 0; p < a.n_parts; ++p) {
+      const GemvPart& P = a.part[p];
+      for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < P.rows / 2; i += stride) {
+        const uint32_t r = (i / half) * (2 * half) + i % half, d = i % half;
+        const float lo = raw.y[p][r] + (P.bias ? P.bias[r] : 0.0f);
+        const float hi = raw.y[p][r + half] + (P.bias ? P.bias[r + half] : 0.0f);
+        rope_store(a, P, r, lo, hi, a.rope.cos[d], a.rope.sin[d]);
+      }
+    }
+  } else {
+    const GemvPart& P = a.part[0];
+    for (uint32_t r = blockIdx.x * blockDim.x + threadIdx.x; r < P.rows; r += stride) {
+      const float v = raw.y[0][r];
+      const float u = MODE == int(GemvMode::SwiGlu) ? raw.y[1][r] : 0.0f;
+      const float pre = MODE == int(GemvMode::Accum) ? P.y[r] : (P.bias ? P.bias[r] : 0.0f);
+      epilogue<MODE>(P, r, v, u, pre, &bv, &bi, &nf);
+    }
+  }
+  if constexpr (MODE == int(GemvMode::Logits)) argmax_partial<MODE>(a, bv, bi, nf, s_bv, s_bi, s_nf);
+}
+
 }  // namespace
 
 const GemvTuning& gemv_tuning() {
@@ -1784,6 +1929,7 @@ GemvLaunch gemv_geometry(WeightKind kind, GemvMode mode, uint32_t C, const uint3
     case WeightKind::FlatW4: panel_cols = FlatW4::kPanelCols; ppw = FlatW4::kPPW; break;
     case WeightKind::FlatW2: panel_cols = FlatW2::kPanelCols; ppw = FlatW2::kPPW; break;
     case WeightKind::Raw16: panel_cols = Raw16::kPanelCols; ppw = Raw16::kPPW; break;
+    case WeightKind::Cell16Poly: break;  // launched by launch_gemv_poly
   }
   *n_panels = (C + panel_cols - 1) / panel_cols;
   uint32_t nw = (*n_panels + ppw - 1) / ppw;
@@ -1859,6 +2005,28 @@ GemvLaunch gemv_geometry(WeightKind kind, GemvMode mode, uint32_t C, const uint3
   return g;
 }
 
+uint32_t launch_gemv_poly(const GemvArgs& a, const PolyPlan* const* plans, float* xn, const PolyRaw& raw,
+                          hipStream_t st) {
+  const float* x = a.x;
+  if (a.gamma) {
+    StepResult* res = GemvMode(a.mode) == GemvMode::Logits ? a.result : nullptr;
+    launch_kernel(&k_rmsnorm, dim3(1), dim3(1024), st, a.x, a.gamma, a.eps, a.C, xn, res);
+    x = xn;
+  }
+  for (int p = 0; p < a.n_parts; ++p)
+    launch_kernel(&k_gemv_poly, dim3(plans[p]->n_cells + 1), dim3(256), st, a.part[p].base, a.part[p].stride,
+                  plans[p]->row_base, plans[p]->n_cells, x, a.C, raw.y[p], a.part[p].rows);
+  const uint32_t blocks = kPolyEpilogueBlocks;
+  switch (GemvMode(a.mode)) {
+    case GemvMode::Store: launch_kernel(&k_poly_epilogue<int(GemvMode::Store)>, dim3(blocks), dim3(256), st, a, raw); break;
+    case GemvMode::Accum: launch_kernel(&k_poly_epilogue<int(GemvMode::Accum)>, dim3(blocks), dim3(256), st, a, raw); break;
+    case GemvMode::SwiGlu: launch_kernel(&k_poly_epilogue<int(GemvMode::SwiGlu)>, dim3(blocks), dim3(256), st, a, raw); break;
+    case GemvMode::Logits: launch_kernel(&k_poly_epilogue<int(GemvMode::Logits)>, dim3(blocks), dim3(256), st, a, raw); break;
+    case GemvMode::QkvRope: launch_kernel(&k_poly_epilogue<int(GemvMode::QkvRope)>, dim3(blocks), dim3(256), st, a, raw); break;
+  }
+  return blocks;
+}
+
 void launch_gemv(WeightKind kind, const GemvArgs& a, const GemvLaunch& g, hipStream_t st) {
   const GemvMode m = GemvMode(a.mode);
   if (a.n_parts < 1 || a.n_parts > (m == GemvMode::QkvRope ? kMaxParts : m == GemvMode::SwiGlu ? 2 : 1)) {
@@ -1870,6 +2038,9 @@ void launch_gemv(WeightKind kind, const GemvArgs& a, const GemvLaunch& g, hipStr
     case WeightKind::FlatW4: launch_layout<FlatW4>(a, g, st); break;
     case WeightKind::FlatW2: launch_layout<FlatW2>(a, g, st); break;
     case WeightKind::Raw16: launch_layout<Raw16>(a, g, st); break;
+    case WeightKind::Cell16Poly:
+      std::fprintf(stderr, "chpe: polymorphic cells go through launch_gemv_poly\n");
+      break;
   }
 }
 

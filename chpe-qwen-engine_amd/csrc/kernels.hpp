@@ -25,6 +25,7 @@ enum class WeightKind : int {
   Cell16W4 = 1,  // 16-row cells, 4-bit, GROUP128, rows=16, cols=2048 (gemvTileW4)
   FlatW4 = 2,    // flat 32768-weight tiles, 4-bit, GROUP128 (gemvCellFlat)
   FlatW2 = 3,    // flat tiles, 2-bit, GROUP128
+  Cell16Poly = 4,  // 16-row polymorphic cells of any width (gemvTilePolymorphic), per-cell metadata
 };
 
 enum class GemvMode : int {
@@ -191,6 +192,24 @@ const GemvTuning& gemv_tuning();
 GemvLaunch gemv_geometry(WeightKind kind, GemvMode mode, uint32_t C, const uint32_t* rows,
                          int n_parts, uint32_t* n_units, uint32_t* n_panels,
                          uint32_t* waves_per_unit, uint32_t* unit_begin);
+
+// Polymorphic 16-row cells (any of gemvTilePolymorphic's widths, WeightKind::Cell16Poly): the
+// cells of one tensor and the first output row of each (the prefix sums of dims.rows), with
+// row_base[n_cells] = the rows they cover.
+struct PolyPlan {
+  const uint32_t* row_base;  // device [n_cells + 1]
+  uint32_t n_cells;
+};
+struct PolyRaw {             // raw row sums per part (device, >= the part's rows each)
+  float* y[kMaxParts];
+};
+constexpr uint32_t kPolyEpilogueBlocks = 64;
+// one GEMV over polymorphic cells: the input RMSNorm'ed into xn (when a.gamma is set), the raw
+// row sums of every part, then the mode's epilogue (a.part[*].y, bias, RoPE / KV append,
+// SwiGLU, residual, logits + argmax partials: kPolyEpilogueBlocks of them).  Returns the
+// number of argmax partials.
+uint32_t launch_gemv_poly(const GemvArgs& a, const PolyPlan* const* plans, float* xn, const PolyRaw& raw,
+                          hipStream_t stream);
 
 // launchers; all enqueue on `stream` and never synchronise
 void launch_embed(const EmbedArgs& a, hipStream_t stream);

@@ -125,6 +125,16 @@ int chpe_debug_gemv_flat(int mode, uint32_t rows, uint32_t cols, const uint8_t *
 int chpe_debug_gemv_cells(int mode, uint32_t rows, const uint8_t *cells, const uint8_t *cells_up,
                           size_t n_cells, const float *x, const float *gamma, float eps, float *y,
                           uint32_t *out_argmax, float *out_hidden_norm);
+/* One GEMV over polymorphic 16-row cells of any width (gemvTilePolymorphic,
+ * src/chpe_engine.zig:732-751: 2-bit codebook, 4-bit, int8 with a per-row scale and bias,
+ * fp16 / bf16, f32; group-128 scales or the tile's scale and bias; outliers added to group-128
+ * cells of 16 rows) through the engine's polymorphic path, on n_cells consecutive 17408-byte
+ * cells covering `rows` rows as gemvLinear walks them (row bases = prefix sums of dims.rows);
+ * x has `cols` floats.  Modes and the other arguments as for chpe_debug_gemv_flat.  Returns 0,
+ * -1 on bad arguments, -3 on a device error. */
+int chpe_debug_gemv_poly(int mode, uint32_t rows, uint32_t cols, const uint8_t *cells, const uint8_t *cells_up,
+                         size_t n_cells, const float *x, const float *gamma, float eps, float *y,
+                         uint32_t *out_argmax, float *out_hidden_norm);
 /* unpackEmbedRowCell on the GPU over `len` bytes starting at a cell (rows of wide tensors
  * read past the cell).  Returns 1 if written, 0 if the row is out of range, <0 on error. */
 int chpe_debug_embed_row_cell(const uint8_t *bytes, size_t len, uint32_t row, uint32_t D,

@@ -294,6 +294,30 @@ def test_kv_f16_matches_oracle_kv_f16(w4_archive):
         o.close()
 
 
+def test_token_stream_w4_kv_f16(w4_archive):
+    """C1's own configuration: the 4-bit cell archive with the fp16 KV cache, a greedy stream
+    against the oracle's kv-f16 mode (256-token prompt + 32 generated).  The fp16 cache's
+    rounding flips leave ~1-3e-3 on the logits (test_kv_f16_matches_oracle_kv_f16), so the
+    streams may part only after a step whose top-2 gap in the oracle is below 5e-3."""
+    e = ca.Engine(w4_archive, arch=0, max_seq_len=320, kv_f16=True)
+    o = orc.Oracle(w4_archive, arch=0, max_seq_len=320, kv_f16=True, threads=16)
+    try:
+        prompt = np.random.default_rng(11).integers(0, V, 256).astype(np.uint32)
+        say("token stream 3B W4, fp16 KV: 256 prompt + 32 generated")
+        g = e.generate(prompt, 32)
+        r, gaps = o.generate(prompt, 32)
+        for i, (a, b) in enumerate(zip(g, r)):
+            if a != b:
+                assert gaps[i] < 5e-3, (i, int(a), int(b), float(gaps[i]))
+                break
+        else:
+            i = 32
+        say(f"  identical for {i} of 32 tokens")
+    finally:
+        e.close()
+        o.close()
+
+
 def test_token_stream_fp16_raw(fp16_archive):
     """The reference's CPU configuration: 3B FP16 raw tiles, 32-token prompt + 64 greedy."""
     say("token stream 3B FP16 raw: 32 prompt + 64 generated")
