@@ -1697,6 +1697,261 @@ __global__ void __launch_bounds__(kWave * W) k_gemv_flat(GemvArgs a) {
   }
 }
 
+// ---- flat tiles, input-stationary and pipelined (k_gemv_xs) ---------------------------------
+// gemvCellFlat (:584-729) for every mode, x held in registers: wave w of NW owns the columns
+// w * 64 * F::kCols .. + 64 * F::kCols - 1 (lane l: F::kCols columns from F::kCols * l, one
+// 16-byte code load per row), normalised once per workgroup ((x * inv) * gamma, rmsNorm
+// :187-191) and kept for every unit the workgroup takes.  The grid is persistent: a workgroup
+// strides over units of R rows (SwiGlu: R/2 gate + R/2 up rows; QkvRope: R/2 RoPE pairs) and
+// issues the code, scale, correction and residual loads of its next unit before the arithmetic
+// of the current one, so each wave keeps its own loads in flight while it computes.  Row sums
+// meet over the lanes (reduce-scatter) and the waves (LDS, double-buffered, in wave order);
+// wave 0 runs the epilogue.  Outliers replace weights (:632-646): per-row corrections
+// (w_out - dequantised code) * x[col], spread over all lanes of all waves, with x[col] from the
+// workgroup's LDS copy of the (normalised) input.
+template <int R, int MODE>
+__device__ __forceinline__ uint32_t xs_row_base(const GemvPart& P0, uint32_t unit, uint32_t half) {
+  if constexpr (MODE == int(GemvMode::SwiGlu)) {
+    return unit * (R / 2);
+  } else if constexpr (MODE == int(GemvMode::QkvRope)) {  // R/2 pairs per unit, half/(R/2) units per head
+    const uint32_t ul = unit - P0.unit_begin, per_head = half / (R / 2);
+    return (ul / per_head) * (2 * half) + (ul % per_head) * (R / 2);
+  } else {
+    return (unit - P0.unit_begin) * R;
+  }
+}
+
+template <int R, int SPL>
+struct XsLoads {
+  uint4 q[R];          // codes of row i at the lane's columns
+  uint32_t s[R];       // their group scale
+  float2 ce[SPL];      // correction entries (column bits, w_out - code) of the lane's row
+  uint32_t cuse;       // bit t: ce[t] belongs to the row
+  float pre, pre2;     // lane i: residual / bias of row i (QkvRope: pre2 = bias of the pair's row)
+  float rc, rs;        // lane i < R/2 (QkvRope): cos / sin of the pair
+  uint32_t row_base;   // first row of the unit in its part
+  int pu;              // the unit's part (QkvRope)
+};
+
+template <class F, int MODE, int R, int NW>
+__global__ void __launch_bounds__(kWave * NW) k_gemv_xs(GemvArgs a) {
+  constexpr int KC = F::kCols, CH = kWave * KC;
+  constexpr bool kNorm = kNormOf<MODE>;
+  constexpr bool kSwi = MODE == int(GemvMode::SwiGlu);
+  constexpr bool kRope = MODE == int(GemvMode::QkvRope);
+  constexpr bool kLogits = MODE == int(GemvMode::Logits);
+  constexpr bool kPre = MODE == int(GemvMode::Store) || MODE == int(GemvMode::Accum) || kRope;
+  constexpr int LPR = kWave / R;                                  // lanes per row (corrections)
+  constexpr int SPL = int(kMaxCorrPerRow + LPR * NW - 1) / (LPR * NW);
+  constexpr int NE = (kSwi || kRope) ? R / 2 : R;                 // epilogue lanes
+  static_assert(R == 2 || R == 4 || R == 8, "rows per unit");
+  extern __shared__ __align__(16) float s_x[];                    // C floats: the (normalised) input
+  __shared__ float s_part[2][NW][R];
+  __shared__ float s_red[NW];
+  __shared__ float s_bv[NW];
+  __shared__ uint32_t s_bi[NW], s_nf[NW];
+  const int lane = threadIdx.x & 63;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  args_batch<MODE>(a);
+  const uint32_t C = a.C, ng = C >> 7, half = a.rope.head_dim / 2, n_units = a.n_units, step = gridDim.x;
+  const uint32_t col = wave * CH + uint32_t(KC * lane);
+  const bool okc = col < C;
+  const uint32_t cc = okc ? col : 0u;
+
+  // 1. the lane's input columns (and gains)
+  float xv[KC];
+  float4 gq[kNorm ? KC / 4 : 1];
+#pragma unroll
+  for (int j = 0; j < KC / 4; ++j) {
+    const float4 t = ld_f4(a.x + cc + 4 * j);
+    xv[4 * j] = t.x; xv[4 * j + 1] = t.y; xv[4 * j + 2] = t.z; xv[4 * j + 3] = t.w;
+    if constexpr (kNorm) gq[j] = ld_f4(a.gamma + cc + 4 * j);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  // loads of unit u into L: codes + scales of its R rows, correction entries, residual / bias,
+  // RoPE factors -- every address a uniform base plus a 32-bit lane offset, rows past the part
+  // (or past its tiles) read row 0 and are dropped
+  auto issue = [&](uint32_t u, XsLoads<R, SPL>* L) {
+    const int pu = kRope ? int(__builtin_amdgcn_readfirstlane(part_of(a, u))) : 0;
+    const GemvPart P0 = kRope ? pick_part(a, pu) : a.part[0];
+    const GemvPart& P1 = kSwi ? a.part[1] : P0;
+    const uint32_t rb = xs_row_base<R, MODE>(P0, u, half);
+    L->pu = pu;
+    L->row_base = rb;
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+      const bool second = kSwi && i >= R / 2;
+      const uint32_t r = row_of<R, MODE>(rb, i, half);
+      const uint32_t wr = second ? uni(P1.wrows) : uni(P0.wrows);
+      const uint32_t G = (r < wr ? r : 0u) * ng + (cc >> 7);
+      const uint8_t* base = second ? uni(P1.base) : uni(P0.base);
+      const uint32_t stride = second ? uni(P1.stride) : uni(P0.stride);
+      const uint32_t tile_off = (G >> 8) * stride, gi = G & 255u;
+      L->q[i] = ld_u128(base + (tile_off + 64 + gi * (KC == 32 ? 64u : 32u) + ((cc & 127u) / (KC == 32 ? 2u : 4u))));
+      L->s[i] = ld_u16(base + (tile_off + 16448 + 48 + 2 * gi));
+    }
+    {  // corrections: lane l takes entries (l % LPR) + LPR (w + NW t) of unit row l / LPR
+      const int ci = lane / LPR;
+      const bool second = kSwi && ci >= R / 2;
+      const float2* corr = second ? uni(P1.corr) : uni(P0.corr);
+      const uint32_t kmax = second ? uni(P1.corr_kmax) : uni(P0.corr_kmax);
+      const uint32_t wr = second ? uni(P1.wrows) : uni(P0.wrows);
+      const uint32_t r = row_of<R, MODE>(rb, ci, half);
+      const bool ok = corr != nullptr && r < wr;
+      const float2* src = corr ? corr : reinterpret_cast<const float2*>(a.x);
+      uint32_t m = 0;
+#pragma unroll
+      for (int t = 0; t < SPL; ++t) {
+        const uint32_t e = uint32_t(lane % LPR) + uint32_t(LPR) * (wave + uint32_t(NW * t));
+        const bool use = ok && e < kmax;
+        L->ce[t] = src[use ? size_t(r) * kmax + e : 0];
+        m |= uint32_t(use) << t;
+      }
+      L->cuse = m;
+    }
+    L->pre = 0.0f;
+    L->pre2 = 0.0f;
+    L->rc = 1.0f;
+    L->rs = 0.0f;
+    if constexpr (kPre) {
+      const int i = lane < NE ? lane : 0;
+      const float* src = MODE == int(GemvMode::Accum) ? P0.y : P0.bias;
+      const uint32_t r = row_of<R, MODE>(rb, i, half);
+      const bool ok = lane < NE && r < P0.rows && src != nullptr;
+      L->pre = (src ? src : a.x)[ok ? r : 0u];
+      L->pre = ok ? L->pre : 0.0f;
+      if constexpr (kRope) {
+        const uint32_t r2 = row_of<R, MODE>(rb, i + R / 2, half);
+        const bool ok2 = lane < NE && r2 < P0.rows && src != nullptr;
+        L->pre2 = (src ? src : a.x)[ok2 ? r2 : 0u];
+        L->pre2 = ok2 ? L->pre2 : 0.0f;
+        const bool rope = lane < NE && P0.rope_role != kRoleV;
+        const size_t at = rope ? (r % (2 * half)) : 0u;
+        L->rc = rope ? a.rope.cos[at] : 1.0f;
+        L->rs = rope ? a.rope.sin[at] : 0.0f;
+      }
+    }
+  };
+
+  XsLoads<R, SPL> LA, LB;
+  uint32_t unit = blockIdx.x;  // < n_units: the grid is at most the unit count
+  issue(unit, &LA);
+
+  // 2. the input normalised in registers ((x * inv) * gamma) and copied to LDS for the corrections
+  float ss = 0.0f;
+#pragma unroll
+  for (int j = 0; j < KC; ++j) {
+    xv[j] = okc ? xv[j] : 0.0f;
+    ss = fmaf(xv[j], xv[j], ss);
+  }
+  ss = wave_sum(ss);
+  if (lane == 0) s_red[wave] = ss;
+  __syncthreads();
+  float tot = 0.0f;
+#pragma unroll
+  for (int w = 0; w < NW; ++w) tot += s_red[w];
+  if constexpr (kNorm) {
+    const float inv = 1.0f / sqrtf(tot / float(C) + a.eps);
+#pragma unroll
+    for (int j = 0; j < KC / 4; ++j) {
+      xv[4 * j] = (xv[4 * j] * inv) * gq[j].x;
+      xv[4 * j + 1] = (xv[4 * j + 1] * inv) * gq[j].y;
+      xv[4 * j + 2] = (xv[4 * j + 2] * inv) * gq[j].z;
+      xv[4 * j + 3] = (xv[4 * j + 3] * inv) * gq[j].w;
+    }
+  }
+  if (okc) {
+#pragma unroll
+    for (int j = 0; j < KC / 4; ++j)
+      *reinterpret_cast<float4*>(s_x + col + 4 * j) = make_float4(xv[4 * j], xv[4 * j + 1], xv[4 * j + 2], xv[4 * j + 3]);
+  }
+  float sx = 0.0f;
+#pragma unroll
+  for (int j = 0; j < KC; ++j) sx += xv[j];
+  __syncthreads();  // s_x complete
+
+  float bv = -1e30f;
+  uint32_t bi = 0xffffffffu, nf = 0;
+  auto compute = [&](const XsLoads<R, SPL>& L, int buf) {
+    const GemvPart P0 = kRope ? pick_part(a, L.pu) : a.part[0];
+    const GemvPart& P1 = kSwi ? a.part[1] : P0;
+    const uint32_t rb = L.row_base;
+    float acc[R];
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+      const bool second = kSwi && i >= R / 2;
+      const uint32_t r = row_of<R, MODE>(rb, i, half);
+      const uint32_t wr = second ? uni(P1.wrows) : uni(P0.wrows);
+      const float t = (F::dot(L.q[i], xv, false) - F::kOff * sx) * F::scale(L.s[i]);
+      acc[i] = (okc && r < wr) ? t : 0.0f;
+    }
+    const int ci = lane / LPR;
+#pragma unroll
+    for (int t = 0; t < SPL; ++t) {
+      const bool on = ((L.cuse >> t) & 1u) && L.ce[t].y != 0.0f;
+      const float xc = s_x[on ? __float_as_uint(L.ce[t].x) : 0u];
+      const float d = on ? L.ce[t].y * xc : 0.0f;
+#pragma unroll
+      for (int i = 0; i < R; ++i) acc[i] += ci == i ? d : 0.0f;
+    }
+    const float v = wave_reduce_rows<R>(acc, lane);  // lane l: row l / LPR
+    if ((lane % LPR) == 0) s_part[buf][wave][lane / LPR] = v;
+    __syncthreads();
+    if (wave == 0 && lane < NE) {
+      float y0 = 0.0f, y1 = 0.0f;
+#pragma unroll
+      for (int w = 0; w < NW; ++w) {
+        y0 += s_part[buf][w][lane];
+        if constexpr (kSwi || kRope) y1 += s_part[buf][w][lane + R / 2];
+      }
+      const uint32_t r = row_of<R, MODE>(rb, lane, half);
+      if constexpr (kRope) {
+        if (r < P0.rows) rope_store(a, P0, r, y0 + L.pre, y1 + L.pre2, L.rc, L.rs);
+      } else if (MODE != int(GemvMode::Accum) || r < P0.wrows) {  // Accum: rows past the tiles stay
+        epilogue<MODE>(P0, r, y0, y1, L.pre, &bv, &bi, &nf);
+      }
+    }
+  };
+
+  // 3. the units: the next unit's loads, then the current unit's arithmetic (static buffers)
+  bool last_b = false;
+  while (unit + step < n_units) {
+    issue(unit + step, &LB);
+    compute(LA, 0);
+    unit += step;
+    if (unit + step >= n_units) {
+      last_b = true;
+      break;
+    }
+    issue(unit + step, &LA);
+    compute(LB, 1);
+    unit += step;
+  }
+  if (last_b) compute(LB, 1);
+  else compute(LA, 0);
+  if constexpr (kLogits) {
+    argmax_partial<MODE>(a, bv, bi, nf, s_bv, s_bi, s_nf);
+    if (blockIdx.x == 0 && threadIdx.x == 0) a.result->hidden_norm = sqrtf(tot);
+  }
+}
+
+// the x-stationary kernel's variant for a launch: NW waves of 64 * F::kCols columns
+template <class F, int MODE>
+bool launch_xs(const GemvArgs& a, const GemvLaunch& g, hipStream_t st) {
+  const size_t lds = size_t(a.C) * 4;
+  const dim3 gr(g.blocks), bl(g.threads);
+  const uint32_t nw = g.threads / kWave;
+#define CHPE_XS(Rv, NWv)                                                                         \
+  if (g.xs == Rv && nw == NWv) {                                                                 \
+    launch_kernel_lds(&k_gemv_xs<F, MODE, Rv, NWv>, gr, bl, lds, st, a);                         \
+    return true;                                                                                 \
+  }
+  CHPE_XS(4, 1) CHPE_XS(4, 2) CHPE_XS(4, 4) CHPE_XS(2, 4) CHPE_XS(2, 8) CHPE_XS(4, 8) CHPE_XS(2, 16) CHPE_XS(4, 16)
+#undef CHPE_XS
+  return false;
+}
+
 template <class F, int MODE>
 void launch_one(const GemvArgs& a, const GemvLaunch& g, hipStream_t st) {
   const size_t lds = size_t(xs_floats(a.C)) * 4;
@@ -1720,6 +1975,13 @@ void launch_one(const GemvArgs& a, const GemvLaunch& g, hipStream_t st) {
     if (g.cells == 1) { launch_kernel(&k_gemv_cells<MODE, 1>, dim3(g.blocks), dim3(g.threads), st, a); return; }
     if (g.cells == 2) { launch_kernel(&k_gemv_cells<MODE, 2>, dim3(g.blocks), dim3(g.threads), st, a); return; }
     if (g.cells == 4) { launch_kernel(&k_gemv_cells<MODE, 4>, dim3(g.blocks), dim3(g.threads), st, a); return; }
+  }
+  if constexpr (std::is_same_v<F, FlatW4> || std::is_same_v<F, FlatW2>) {
+    if (g.xs) {
+      if (launch_xs<F, MODE>(a, g, st)) return;
+      std::fprintf(stderr, "chpe: no input-stationary kernel for %u rows x %u waves\n", g.xs, g.threads / kWave);
+      return;
+    }
   }
   if constexpr (std::is_same_v<F, FlatW4> && MODE != int(GemvMode::Logits)) {
     if (g.flat) {
@@ -1912,6 +2174,17 @@ const GemvTuning& gemv_tuning() {
     if (const char* e = std::getenv("CHPE_GEMV_FLAT")) v.flat = uint32_t(std::strtoul(e, nullptr, 10));
     if (const char* e = std::getenv("CHPE_GEMV_MMA")) v.mma = uint32_t(std::strtoul(e, nullptr, 10));
     if (const char* e = std::getenv("CHPE_GEMV_MMA_LOGITS_BLOCKS")) v.mma_logits_blocks = uint32_t(std::strtoul(e, nullptr, 10));
+    if (const char* e = std::getenv("CHPE_GEMV_XS")) v.xs = uint32_t(std::strtoul(e, nullptr, 10));
+    if (const char* e = std::getenv("CHPE_GEMV_XS_MIN_UNITS")) v.xs_min_units = uint32_t(std::strtoul(e, nullptr, 10));
+    if (const char* e = std::getenv("CHPE_GEMV_XS_WPC")) {
+      unsigned w[4] = {v.xs_wpc_small, v.xs_wpc_large, v.xs_wpc_logits, v.xs_wpc_wide};
+      if (std::sscanf(e, "%u,%u,%u,%u", &w[0], &w[1], &w[2], &w[3]) == 4 && w[0] && w[1] && w[2] && w[3]) {
+        v.xs_wpc_small = w[0];
+        v.xs_wpc_large = w[1];
+        v.xs_wpc_logits = w[2];
+        v.xs_wpc_wide = w[3];
+      }
+    }
     if (v.mma_logits_blocks == 0 || v.mma_logits_blocks > kMaxLogitsBlocks) v.mma_logits_blocks = kMaxLogitsBlocks;
     if (v.logits_blocks == 0 || v.logits_blocks > kMaxLogitsBlocks) v.logits_blocks = kMaxLogitsBlocks;
     return v;
@@ -1923,6 +2196,51 @@ GemvLaunch gemv_geometry(WeightKind kind, GemvMode mode, uint32_t C, const uint3
                          uint32_t* n_units, uint32_t* n_panels, uint32_t* waves_per_unit,
                          uint32_t* unit_begin) {
   const uint32_t ru = 8;
+  if ((kind == WeightKind::FlatW4 || kind == WeightKind::FlatW2) && gemv_tuning().xs && C % 128 == 0 &&
+      size_t(C) * 4 <= size_t(150) << 10) {
+    // the input-stationary persistent kernel: waves of 64 * 32 (4-bit) / 64 * 64 (2-bit) columns
+    const uint32_t chunk = kind == WeightKind::FlatW4 ? 2048u : 4096u, need = (C + chunk - 1) / chunk;
+    const uint32_t nw = need <= 1 ? 1u : need <= 2 ? 2u : need <= 4 ? 4u : need <= 8 ? 8u : 16u;
+    const uint32_t R = nw >= 8 ? 2u : 4u;
+    bool ok = need <= 16;
+    // (launches of fewer units at <= 8192 columns -- the 72B q/k/v and o projections -- run
+    // faster on the one-unit-per-workgroup kernels: the persistent grid's start-up is not
+    // amortised over enough units)
+    if (nw < 8 && mode != GemvMode::Logits) {
+      uint32_t u = 0;
+      for (int p = 0; p < (mode == GemvMode::SwiGlu ? 1 : n_parts); ++p)
+        u += mode == GemvMode::SwiGlu ? (rows[p] + R / 2 - 1) / (R / 2) : (rows[p] + R - 1) / R;
+      ok = ok && u >= gemv_tuning().xs_min_units;
+    }
+    if (mode == GemvMode::QkvRope)  // whole units per part (head dims are 128 or 256: whole pairs per unit)
+      for (int p = 0; p < n_parts; ++p) ok = ok && rows[p] % R == 0;
+    if (ok) {
+      uint32_t units = 0;
+      if (mode == GemvMode::SwiGlu) {
+        units = (rows[0] + R / 2 - 1) / (R / 2);
+        unit_begin[0] = unit_begin[1] = 0;
+      } else {
+        for (int p = 0; p < n_parts; ++p) {
+          unit_begin[p] = units;
+          units += (rows[p] + R - 1) / R;
+        }
+      }
+      *n_units = units;
+      *n_panels = need;
+      *waves_per_unit = nw;
+      const GemvTuning& t = gemv_tuning();
+      const uint32_t wpc = nw >= 8 ? t.xs_wpc_wide
+                           : mode == GemvMode::Logits ? t.xs_wpc_logits
+                           : units >= 4096 ? t.xs_wpc_large : t.xs_wpc_small;
+      GemvLaunch g{};
+      g.ru = R;
+      g.xs = R;
+      g.threads = kWave * nw;
+      g.blocks = std::min<uint32_t>(units, 256u * wpc);
+      if (mode == GemvMode::Logits && g.blocks > kMaxLogitsBlocks) g.blocks = kMaxLogitsBlocks;
+      return g;
+    }
+  }
   uint32_t panel_cols = 2048, ppw = 1;
   switch (kind) {
     case WeightKind::Cell16W4: panel_cols = Cell16W4::kPanelCols; ppw = Cell16W4::kPPW; break;

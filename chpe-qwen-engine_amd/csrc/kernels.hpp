@@ -119,6 +119,7 @@ struct GemvLaunch {  // launch geometry of one GemvArgs
   uint32_t cells;  // > 0: the K-split kernel for 16-row cells at 2048 columns, `cells` units per workgroup
   uint32_t flat;   // > 0: the K-split kernel for flat 4-bit tiles, up to `flat` panels per wave
   uint32_t mma;    // > 0: the matrix-core kernel for 16-row cells at 2048 columns, `mma` tiles per workgroup
+  uint32_t xs;     // > 0: the input-stationary persistent kernel for flat tiles, `xs` rows per unit
 };
 
 struct StepState {  // device-resident per-token state read by the captured step
@@ -184,6 +185,11 @@ struct GemvTuning {
   uint32_t mma = 2;    // 16-row cells at 2048 columns on the matrix-core kernel, 1 or 2 tiles per
                        // workgroup of a launch with >= 1024 tiles (CHPE_GEMV_MMA; 0: off)
   uint32_t mma_logits_blocks = 512;   // persistent workgroups of the matrix-core LM head (2 per CU)
+  uint32_t xs = 1;     // flat tiles on the input-stationary persistent kernel (CHPE_GEMV_XS; 0: off)
+  // its persistent workgroups per CU (256 CUs): launches of < 4096 units, of more, the LM head,
+  // and inputs wider than 8192 columns (CHPE_GEMV_XS_WPC=small,large,logits,wide)
+  uint32_t xs_wpc_small = 2, xs_wpc_large = 3, xs_wpc_logits = 6, xs_wpc_wide = 1;
+  uint32_t xs_min_units = 4096;  // below this (at <= 8192 columns, not the LM head): the older kernels
 };
 const GemvTuning& gemv_tuning();
 

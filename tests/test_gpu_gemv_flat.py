@@ -2,9 +2,10 @@
 :1396-1489 for tensors wider than 2048 columns) at the widths of the larger models, through
 chpe_debug_gemv_flat, against the oracle (oracle/chpe_oracle.c: oref_gemv_cell_flat over every
 tile, oref_rmsnorm before it).  The widths pick the kernel variants: 4096 / 8192 / 12288 columns
-split the panels over 2 / 4 / 6 waves, 29568 columns (the 72B down projection) over 8 waves with
-the input staged in two passes, and 2-bit tiles at 4096 columns run the one-wave-per-unit
-kernel.  Row counts are ragged (not multiples of the 8-row unit).
+split the panels over 2 / 4 / 6 waves; launches of 4096 units or more at those widths, every
+LM head and every wider input (the 72B down projection at 29568 columns) run the persistent
+input-stationary kernel (k_gemv_xs), as do the 2-bit tiles.  Row counts are ragged (not
+multiples of the unit).
 
 Tolerance: the GPU sums in another order than the oracle's sequential loop (and as
 sum (q x) - 8 sum x per group, which cancels), so each output is compared within
@@ -62,6 +63,8 @@ CASES = [  # (mode, bits, rows, cols)
     ("logits", 4, 90, 4096),
     ("accum", 4, 20, 29568),
     ("swiglu", 4, 12, 29568),
+    ("swiglu", 4, 8192, 8192),   # 4096 units: the persistent input-stationary kernel
+    ("accum", 4, 16388, 8192),   # (4097 units, the last one partly past the rows)
     ("accum", 2, 40, 8192),
     ("swiglu", 2, 28, 4096),
     ("logits", 2, 70, 4096),
