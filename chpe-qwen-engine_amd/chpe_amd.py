@@ -28,7 +28,7 @@ ENGINE_SYMBOLS = [
     "chpe_get_last_hidden_norm", "chpe_free", "chpe_init_ex", "chpe_decode_step",
     "chpe_generate", "chpe_verify", "chpe_last_error", "chpe_get_max_seq_len", "chpe_get_hidden",
     "chpe_time_steps", "chpe_time_stage", "chpe_time_stage_live", "chpe_stage_bytes", "chpe_step_bytes", "chpe_stage_kernel",
-    "chpe_debug_gemv", "chpe_debug_flat_tile_weights", "chpe_debug_gemv_flat", "chpe_debug_gemv_cells", "chpe_debug_gemv_poly", "chpe_debug_embed_row_cell",
+    "chpe_debug_gemv", "chpe_debug_flat_tile_weights", "chpe_debug_gemv_flat", "chpe_debug_gemv_cells", "chpe_debug_gemv_poly", "chpe_debug_gemv_raw", "chpe_debug_embed_row_cell",
     "chpe_debug_attention", "chpe_attention_noalloc", "chpe_debug_deltanet_conv", "chpe_debug_deltanet_step",
 ]
 
@@ -86,6 +86,8 @@ def load_engine_lib():
                                           _c_float_p, _c_u32_p, _c_float_p]),
             "chpe_debug_gemv_poly": (I, [I, ctypes.c_uint32, ctypes.c_uint32, _c_u8_p, _c_u8_p, S, _c_float_p,
                                          _c_float_p, F, _c_float_p, _c_u32_p, _c_float_p]),
+            "chpe_debug_gemv_raw": (I, [I, ctypes.c_uint32, ctypes.c_uint32, I, _c_u8_p, _c_u8_p, S, _c_float_p,
+                                        _c_float_p, F, _c_float_p, _c_u32_p, _c_float_p]),
             "chpe_debug_embed_row_cell": (I, [_c_u8_p, S, ctypes.c_uint32, ctypes.c_uint32, _c_float_p]),
             "chpe_debug_attention": (I, [ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32, I, ctypes.c_uint32,
                                          _c_float_p, _c_float_p, _c_float_p, _c_float_p]),
@@ -379,6 +381,27 @@ def gpu_gemv_poly(mode, rows, cols, cells, x, cells_up=None, gamma=None, eps=1e-
         cells.size // 17408, _fp(x), None if g is None else _fp(g), eps, _fp(out), ctypes.byref(am), ctypes.byref(hn))
     if rc:
         raise EngineError(f"chpe_debug_gemv_poly failed: {rc} {load_engine_lib().chpe_last_error().decode()}")
+    return (out, am.value, hn.value) if mode == "logits" else out
+
+
+RAW_KINDS = {"fp16": 0, "bf16": 1, "int8": 2}
+
+
+def gpu_gemv_raw(mode, rows, cols, kind, tiles, x, tiles_up=None, gamma=None, eps=1e-6, y=None):
+    """One GEMV over raw 16384-byte tiles (one row-major matrix) through the engine's raw
+    kernels (chpe_debug_gemv_raw); returns y, or for "logits" (y, argmax, hidden_norm)."""
+    m = GEMV_MODES[mode]
+    t = np.ascontiguousarray(tiles, dtype=np.uint8).reshape(-1)
+    up = None if tiles_up is None else np.ascontiguousarray(tiles_up, dtype=np.uint8).reshape(-1)
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    g = None if gamma is None else np.ascontiguousarray(gamma, dtype=np.float32)
+    out = np.zeros(rows, np.float32) if y is None else np.array(y, dtype=np.float32)
+    am, hn = ctypes.c_uint32(0), ctypes.c_float(0.0)
+    rc = load_engine_lib().chpe_debug_gemv_raw(
+        m, rows, cols, RAW_KINDS[kind], t.ctypes.data_as(_c_u8_p), None if up is None else up.ctypes.data_as(_c_u8_p),
+        t.size // 16384, _fp(x), None if g is None else _fp(g), eps, _fp(out), ctypes.byref(am), ctypes.byref(hn))
+    if rc:
+        raise EngineError(f"chpe_debug_gemv_raw failed: {rc} {load_engine_lib().chpe_last_error().decode()}")
     return (out, am.value, hn.value) if mode == "logits" else out
 
 

@@ -274,6 +274,94 @@ int chpe_debug_flat_tile_weights(const uint8_t* cell, float* out) {
 // One flat-tile GEMV launch (the decode step's kernels for gemvCellFlat tensors) on caller
 // cells: the tensor's flat tiles as consecutive 17408-byte cells, copied to the device behind
 // the same 64-byte shift and zero tail as the archive image.
+int chpe_debug_gemv_raw(int mode, uint32_t rows, uint32_t cols, int kind, const uint8_t* tiles,
+                        const uint8_t* tiles_up, size_t n_tiles, const float* x, const float* gamma, float eps, float* y,
+                        uint32_t* out_argmax, float* out_hidden_norm) {
+  g_last_error.clear();
+  const bool norm = mode == int(GemvMode::SwiGlu) || mode == int(GemvMode::Logits);
+  if (!tiles || !x || !y || rows == 0 || cols == 0 || kind < 0 || kind > 2 || mode < 0 ||
+      mode > int(GemvMode::Logits) || norm != (gamma != nullptr) || (mode == int(GemvMode::SwiGlu)) != (tiles_up != nullptr))
+    return -1;
+  const size_t wpt = kind == 2 ? 16384 : 8192;
+  if (cols % (kind == 2 ? 16u : 8u) || n_tiles * wpt < size_t(rows) * cols) {
+    g_last_error = "raw tiles shorter than the matrix, or columns not a multiple of the load width";
+    return -1;
+  }
+  const WeightKind wk = kind == 2 ? WeightKind::Raw8 : WeightKind::Raw16;
+  const int n_parts = mode == int(GemvMode::SwiGlu) ? 2 : 1;
+  const uint8_t* src[2] = {tiles, tiles_up};
+  constexpr size_t kPad = size_t(1) << 20;
+  const size_t bytes = n_tiles * kTileCodeBytes;
+  std::vector<void*> mem;
+  auto alloc = [&](size_t b) -> void* {
+    void* d = nullptr;
+    if (hipMalloc(&d, b) != hipSuccess) return nullptr;
+    mem.push_back(d);
+    return d;
+  };
+  int rc = -3;
+  GemvArgs a{};
+  a.n_parts = n_parts;
+  a.mode = mode;
+  a.C = cols;
+  a.eps = eps;
+  uint32_t prow[kMaxParts] = {rows, rows, 0}, begin[kMaxParts] = {0, 0, 0};
+  const GemvLaunch g = gemv_geometry(wk, GemvMode(mode), cols, prow, n_parts, &a.n_units, &a.n_panels,
+                                     &a.waves_per_unit, begin);
+  float* dx = static_cast<float*>(alloc(size_t(cols) * 4));
+  float* dy = static_cast<float*>(alloc(size_t(rows) * 4));
+  float* dg = norm ? static_cast<float*>(alloc(size_t(cols) * 4)) : nullptr;
+  bool ok = dx && dy && (!norm || dg) && hipMemcpy(dx, x, size_t(cols) * 4, hipMemcpyHostToDevice) == hipSuccess &&
+            hipMemcpy(dy, y, size_t(rows) * 4, hipMemcpyHostToDevice) == hipSuccess &&
+            (!norm || hipMemcpy(dg, gamma, size_t(cols) * 4, hipMemcpyHostToDevice) == hipSuccess);
+  for (int i = 0; ok && i < n_parts; ++i) {
+    uint8_t* d = static_cast<uint8_t*>(alloc(bytes + kPad));
+    ok = d && hipMemset(d, 0, bytes + kPad) == hipSuccess &&
+         hipMemcpy(d, src[i], bytes, hipMemcpyHostToDevice) == hipSuccess;
+    GemvPart& p = a.part[i];
+    p.base = d;
+    p.stride = uint32_t(kTileCodeBytes);
+    p.rows = rows;
+    p.wrows = rows;
+    p.unit_begin = begin[i];
+    p.y = dy;
+    p.bf16 = kind == 1 ? 1 : 0;
+  }
+  a.x = dx;
+  a.gamma = dg;
+  StepResult* dres = nullptr;
+  StepState* dst = nullptr;
+  if (ok && mode == int(GemvMode::Logits)) {
+    a.partials = static_cast<ArgmaxPartial*>(alloc(size_t(g.blocks) * sizeof(ArgmaxPartial)));
+    dres = static_cast<StepResult*>(alloc(sizeof(StepResult)));
+    dst = static_cast<StepState*>(alloc(sizeof(StepState)));
+    a.result = dres;
+    ok = a.partials && dres && dst && hipMemset(dst, 0, sizeof(StepState)) == hipSuccess;
+  }
+  if (ok) {
+    launch_gemv(wk, a, g, nullptr);
+    if (mode == int(GemvMode::Logits)) {
+      FinishArgs f{};
+      f.state = dst;
+      f.partials = a.partials;
+      f.n_partials = g.blocks;
+      f.logits = dy;
+      f.result = dres;
+      launch_finish(f, nullptr);
+    }
+    StepResult r{};
+    if (hipDeviceSynchronize() == hipSuccess &&
+        hipMemcpy(y, dy, size_t(rows) * 4, hipMemcpyDeviceToHost) == hipSuccess &&
+        (!dres || hipMemcpy(&r, dres, sizeof r, hipMemcpyDeviceToHost) == hipSuccess)) {
+      if (dres && out_argmax) *out_argmax = r.argmax;
+      if (dres && out_hidden_norm) *out_hidden_norm = r.hidden_norm;
+      rc = 0;
+    }
+  }
+  for (void* m : mem) (void)hipFree(m);
+  return rc;
+}
+
 int chpe_debug_gemv_flat(int mode, uint32_t rows, uint32_t cols, const uint8_t* tiles, const uint8_t* tiles_up,
                          size_t n_tiles, const float* x, const float* gamma, float eps, float* y,
                          uint32_t* out_argmax, float* out_hidden_norm) {

@@ -209,6 +209,21 @@ __device__ __forceinline__ float dot64_w2(uint4 q, const float* x) {
   return a0 + a1;
 }
 
+// sum over 16 int8 weights (+128, as unsigned bytes: the sign bit flipped) * x; the caller
+// subtracts 128 * sum(x)
+__device__ __forceinline__ float dot16_i8p(uint4 q, const float* x) {
+  const uint32_t w[4] = {q.x ^ 0x80808080u, q.y ^ 0x80808080u, q.z ^ 0x80808080u, q.w ^ 0x80808080u};
+  float a = 0.0f, b = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    a = fmaf(float(w[i] & 0xffu), x[4 * i], a);
+    b = fmaf(float((w[i] >> 8) & 0xffu), x[4 * i + 1], b);
+    a = fmaf(float((w[i] >> 16) & 0xffu), x[4 * i + 2], a);
+    b = fmaf(float(w[i] >> 24), x[4 * i + 3], b);
+  }
+  return a + b;
+}
+
 __device__ __forceinline__ float dot8_f16(uint4 q, const float* x, bool bf16) {
   const uint32_t w[4] = {q.x, q.y, q.z, q.w};
   float a = 0.0f, b = 0.0f;

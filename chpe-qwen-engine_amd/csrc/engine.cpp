@@ -456,9 +456,12 @@ bool Engine::plan_projection(size_t tile_start, size_t num_tiles, size_t r_total
       }
     }
   } else {
-    if (quant_bits_ != 16) { *err = "raw int8 tiles are not built on the GPU path yet"; return false; }
-    if (avail * wpt_ < r_total * c_total || c_total % 8) { *err = "raw tensor shorter than its shape"; return false; }
-    p->kind = WeightKind::Raw16;
+    // one row-major matrix over consecutive raw tiles (dotSegment :1194-1251 segment by segment)
+    if (avail * wpt_ < r_total * c_total || c_total % (quant_bits_ == 8 ? 16 : 8)) {
+      *err = "raw tensor shorter than its shape";
+      return false;
+    }
+    p->kind = quant_bits_ == 8 ? WeightKind::Raw8 : WeightKind::Raw16;
     p->base = d_image_ + 4096 + tile_start * kTileCodeBytes;
     p->stride = uint32_t(kTileCodeBytes);
     p->bf16 = is_raw_fp16_ ? 0 : 1;
@@ -855,6 +858,7 @@ double Engine::proj_bytes(const ProjPlan& p) const {
   double bytes = 0.0;
   switch (p.kind) {
     case WeightKind::Raw16: bytes = 2.0 * n; break;
+    case WeightKind::Raw8: bytes = n; break;
     case WeightKind::Cell16W4: bytes = n / 2 + n / 128 * 2 + double(p.rows / 16) * (16 * 8 * 2 + 8 * 2); break;
     case WeightKind::FlatW4: bytes = n / 2 + n / 128 * 2 + std::ceil(n / kFlatWeights) * (2 + 64 * 4); break;
     case WeightKind::FlatW2: bytes = n / 4 + n / 128 * 2 + std::ceil(n / kFlatWeights) * (2 + 64 * 4); break;

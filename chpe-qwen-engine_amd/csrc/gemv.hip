@@ -99,6 +99,22 @@ struct Raw16 {  // raw fp16 / bf16 tiles read as one row-major matrix (dotSegmen
   __device__ static float dot(uint4 q, const float* x, bool bf16) { return dot8_f16(q, x, bf16); }
 };
 
+struct Raw8 {  // raw int8 tiles read as one row-major matrix, each dot times 0.00373708 (:1219-1237)
+  static constexpr int kCols = 16, kPanelCols = 1024, kPPW = 4;
+  static constexpr float kOff = 128.0f;  // the codes enter the dot as unsigned bytes (w + 128)
+  __device__ static bool lane_cols(uint32_t p, int lane, uint32_t C, uint32_t* c0) {
+    *c0 = p * 1024 + uint32_t(lane) * 16;
+    return *c0 < C;
+  }
+  __device__ static void locate(const GemvPart& P, uint32_t r, uint32_t p, int lane, uint32_t C, uint4* q,
+                                uint32_t* s) {
+    *q = ld_u128(P.base + (uint64_t(r) * C + p * 1024 + lane * 16));
+    *s = 0;
+  }
+  __device__ static float scale(uint32_t) { return 0.00373708f; }
+  __device__ static float dot(uint4 q, const float* x, bool) { return dot16_i8p(q, x); }
+};
+
 __device__ __forceinline__ int part_of(const GemvArgs& a, uint32_t unit) {
   int p = 0;  // unrolled over the fixed part count: a loop here would precede the weight loads
 #pragma unroll
@@ -1936,6 +1952,330 @@ __global__ void __launch_bounds__(kWave * NW) k_gemv_xs(GemvArgs a) {
   }
 }
 
+// ---- flat 4-bit tiles on the matrix cores, input-stationary (k_gemv_xm) ----------------------
+// gemvCellFlat (:584-729) for every mode.  Wave w of NW owns the columns 2048 w .. 2048 w + 2047
+// (four sets of 4 groups of 128) for the whole launch: its input (normalised, (x * inv) * gamma,
+// rmsNorm :187-191) is split into exact integers per group (X = x * 2^(30-e), max |x| < 2^e,
+// truncated; four signed-byte limbs, X = L0 + 2^8 L1 + 2^16 L2 + 2^24 L3) held in a per-wave LDS
+// table in the byte order of the matrix-core operands.  A unit is 4 rows (SwiGlu: 2 gate + 2 up
+// rows; QkvRope: 2 RoPE pairs); per set the wave runs two v_mfma_i32_16x16x64_i8 with
+//   A (16 x 64): row m = 4 r + g -> unit row r, group g of the set, 64 of its codes (one half),
+//   B (64 x 16): column n = g' + 4 L -> limb L of the input in group g' (the same half),
+// so D(r, g; g', L) is the exact integer sum over the half of code * limb where g == g', starting
+// at -8 * (the limb's sum over the group) for the codes' offset.  Lane (n, q) holds D(q, j; n % 4,
+// n / 4) for j = 0..3 and keeps j = n % 4: times 2^(8 L) 2^(e - 30), summed over the limbs (DPP),
+// times the group scale, summed over the set's groups (DPP) -- row q's sum over the set.  Each
+// lane loads 16 bytes of unit row n / 4, group n % 4, quarter q per set: the unit's rows as
+// 256-byte runs.  The grid is persistent; the next unit's loads are issued before the current
+// unit's products.  Row sums meet over the waves in LDS (double-buffered, in wave order); wave 0
+// runs the epilogue.  Outliers replace weights (:632-646): per-row corrections
+// (w_out - dequantised code) * x[col] on the 16 lanes of each row, with x[col] rebuilt from the
+// limb tables (the same integers the products use).
+constexpr uint32_t kXmTableBytes = 4 * 128 * 16;  // per wave: 4 sets x (group, quarter, half, limb) x 16 bytes
+
+template <int R, int SPL>
+struct XmLoads {
+  uint4 q[4];          // codes: unit row n / 4, group n % 4 of set S, quarter q
+  uint32_t s[4];       // group scale: unit row q, group n % 4 of set S
+  float2 ce[SPL];      // correction entries (column bits, w_out - code) of unit row q
+  uint32_t cuse;
+  float pre, pre2, rc, rs;
+  uint32_t row_base;
+  int pu;
+};
+
+// x'[col] from the limb tables: the integer X of the column times 2^(e - 30) of its group
+__device__ __forceinline__ float xm_input(const uint8_t* tb, const float* s_e, uint32_t col) {
+  const uint32_t w = col >> 11, S = (col >> 9) & 3u, g = (col >> 7) & 3u, c = col & 127u;
+  const uint32_t q = c >> 5, h = (c >> 4) & 1u, p = (c >> 3) & 1u, i = c & 7u;
+  const uint32_t at = (w * 4 + S) * 128 * 16 + (((g * 4 + q) * 2 + h) * 4) * 16 + 4 * (2 * p + (i & 1u)) + (i >> 1);
+  const int X = int(int8_t(tb[at])) + (int(int8_t(tb[at + 16])) << 8) + (int(int8_t(tb[at + 32])) << 16) +
+                (int(int8_t(tb[at + 48])) << 24);
+  return float(X) * s_e[(w * 4 + S) * 4 + g];
+}
+
+template <int MODE, int NW>
+__global__ void __launch_bounds__(kWave * NW) k_gemv_xm(GemvArgs a) {
+  constexpr int R = 4;
+  constexpr bool kNorm = kNormOf<MODE>;
+  constexpr bool kSwi = MODE == int(GemvMode::SwiGlu);
+  constexpr bool kRope = MODE == int(GemvMode::QkvRope);
+  constexpr bool kLogits = MODE == int(GemvMode::Logits);
+  constexpr bool kPre = MODE == int(GemvMode::Store) || MODE == int(GemvMode::Accum) || kRope;
+  constexpr int SPL = int(kMaxCorrPerRow + 16 * NW - 1) / (16 * NW);
+  constexpr int NE = (kSwi || kRope) ? R / 2 : R;
+  extern __shared__ __align__(16) uint8_t s_dyn[];  // NW limb tables, then 2^(e-30) per group
+  uint4* s_tb = reinterpret_cast<uint4*>(s_dyn);
+  float* s_e = reinterpret_cast<float*>(s_dyn + NW * kXmTableBytes);
+  __shared__ int s_ci[NW][4][16];
+  __shared__ float s_part[2][NW][R];
+  __shared__ float s_red[NW];
+  __shared__ float s_bv[NW];
+  __shared__ uint32_t s_bi[NW], s_nf[NW];
+  const int lane = threadIdx.x & 63, n = lane & 15, q = lane >> 4;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  args_batch<MODE>(a);
+  const uint32_t C = a.C, ng = C >> 7, half = a.rope.head_dim / 2, n_units = a.n_units, step = gridDim.x;
+  const uint32_t gw = wave * 16;  // the wave's first group
+
+  // 1. the wave's input: 8 columns per lane and set (lane l: set S, columns 2048 w + 512 S + 8 l)
+  float4 xr[4][2], gr[kNorm ? 4 : 1][2];
+#pragma unroll
+  for (int S = 0; S < 4; ++S) {
+    const uint32_t c0 = (gw + 4 * S) * 128 + 8 * uint32_t(lane), cc = c0 < C ? c0 : 0u;
+    xr[S][0] = ld_f4(a.x + cc);
+    xr[S][1] = ld_f4(a.x + cc + 4);
+    if constexpr (kNorm) {
+      gr[S][0] = ld_f4(a.gamma + cc);
+      gr[S][1] = ld_f4(a.gamma + cc + 4);
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  auto issue = [&](uint32_t u, XmLoads<R, SPL>* L) {
+    const int pu = kRope ? int(__builtin_amdgcn_readfirstlane(part_of(a, u))) : 0;
+    const GemvPart P0 = kRope ? pick_part(a, pu) : a.part[0];
+    const GemvPart& P1 = kSwi ? a.part[1] : P0;
+    const uint32_t rb = xs_row_base<R, MODE>(P0, u, half);
+    L->pu = pu;
+    L->row_base = rb;
+    {  // codes: unit row n / 4; scales: unit row q (each in its part, rows past the tiles read row 0)
+      const uint32_t ia = uint32_t(n >> 2), is = uint32_t(q);
+      const bool sa = kSwi && ia >= R / 2, ss = kSwi && is >= R / 2;
+      const uint32_t ra = row_of<R, MODE>(rb, int(ia), half), rs = row_of<R, MODE>(rb, int(is), half);
+      const uint32_t wa = sa ? uni(P1.wrows) : uni(P0.wrows), ws = ss ? uni(P1.wrows) : uni(P0.wrows);
+      const uint8_t* ba = sa ? uni(P1.base) : uni(P0.base);
+      const uint8_t* bs = ss ? uni(P1.base) : uni(P0.base);
+      const uint32_t sta = sa ? uni(P1.stride) : uni(P0.stride), sts = ss ? uni(P1.stride) : uni(P0.stride);
+      const uint32_t Ga0 = (ra < wa ? ra : 0u) * ng, Gs0 = (rs < ws ? rs : 0u) * ng;
+#pragma unroll
+      for (int S = 0; S < 4; ++S) {
+        const uint32_t g = gw + 4 * uint32_t(S) + uint32_t(n & 3), gc = g < ng ? g : 0u;
+        const uint32_t Ga = Ga0 + gc, Gs = Gs0 + gc;
+        L->q[S] = ld_u128(ba + ((Ga >> 8) * sta + 64 + (Ga & 255u) * 64 + 16 * uint32_t(q)));
+        L->s[S] = ld_u16(bs + ((Gs >> 8) * sts + 16448 + 48 + 2 * (Gs & 255u)));
+      }
+    }
+    {  // corrections: lane (n, q) takes entries n + 16 (w + NW t) of unit row q
+      const bool second = kSwi && q >= R / 2;
+      const float2* corr = second ? uni(P1.corr) : uni(P0.corr);
+      const uint32_t kmax = second ? uni(P1.corr_kmax) : uni(P0.corr_kmax);
+      const uint32_t wr = second ? uni(P1.wrows) : uni(P0.wrows);
+      const uint32_t r = row_of<R, MODE>(rb, q, half);
+      const bool ok = corr != nullptr && r < wr;
+      const float2* src = corr ? corr : reinterpret_cast<const float2*>(a.x);
+      uint32_t m = 0;
+#pragma unroll
+      for (int t = 0; t < SPL; ++t) {
+        const uint32_t e = uint32_t(n) + 16u * (wave + uint32_t(NW * t));
+        const bool use = ok && e < kmax;
+        L->ce[t] = src[use ? size_t(r) * kmax + e : 0];
+        m |= uint32_t(use) << t;
+      }
+      L->cuse = m;
+    }
+    L->pre = 0.0f;
+    L->pre2 = 0.0f;
+    L->rc = 1.0f;
+    L->rs = 0.0f;
+    if constexpr (kPre) {
+      const int i = lane < NE ? lane : 0;
+      const float* src = MODE == int(GemvMode::Accum) ? P0.y : P0.bias;
+      const uint32_t r = row_of<R, MODE>(rb, i, half);
+      const bool ok = lane < NE && r < P0.rows && src != nullptr;
+      L->pre = (src ? src : a.x)[ok ? r : 0u];
+      L->pre = ok ? L->pre : 0.0f;
+      if constexpr (kRope) {
+        const uint32_t r2 = row_of<R, MODE>(rb, i + R / 2, half);
+        const bool ok2 = lane < NE && r2 < P0.rows && src != nullptr;
+        L->pre2 = (src ? src : a.x)[ok2 ? r2 : 0u];
+        L->pre2 = ok2 ? L->pre2 : 0.0f;
+        const bool rope = lane < NE && P0.rope_role != kRoleV;
+        const size_t at = rope ? (r % (2 * half)) : 0u;
+        L->rc = rope ? a.rope.cos[at] : 1.0f;
+        L->rs = rope ? a.rope.sin[at] : 0.0f;
+      }
+    }
+  };
+
+  XmLoads<R, SPL> LA, LB;
+  uint32_t unit = blockIdx.x;  // < n_units: the grid is at most the unit count
+  issue(unit, &LA);
+
+  // 2. normalise, then the limb tables, limb sums and group exponents
+  float ss = 0.0f;
+#pragma unroll
+  for (int S = 0; S < 4; ++S) {
+    const bool live = (gw + 4 * S) * 128 + 8 * uint32_t(lane) < C;
+    const float v[8] = {xr[S][0].x, xr[S][0].y, xr[S][0].z, xr[S][0].w, xr[S][1].x, xr[S][1].y, xr[S][1].z, xr[S][1].w};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) ss = live ? fmaf(v[i], v[i], ss) : ss;
+  }
+  ss = wave_sum(ss);
+  if (lane == 0) s_red[wave] = ss;
+  __syncthreads();
+  float tot = 0.0f;
+#pragma unroll
+  for (int w = 0; w < NW; ++w) tot += s_red[w];
+  const float inv = kNorm ? 1.0f / sqrtf(tot / float(C) + a.eps) : 1.0f;
+  uint2* tb2 = reinterpret_cast<uint2*>(s_tb + wave * (kXmTableBytes / 16));
+#pragma unroll
+  for (int S = 0; S < 4; ++S) {
+    const bool live = (gw + 4 * S) * 128 + 8 * uint32_t(lane) < C;
+    float xp[8] = {xr[S][0].x, xr[S][0].y, xr[S][0].z, xr[S][0].w, xr[S][1].x, xr[S][1].y, xr[S][1].z, xr[S][1].w};
+    if constexpr (kNorm) {
+      const float gv[8] = {gr[S][0].x, gr[S][0].y, gr[S][0].z, gr[S][0].w, gr[S][1].x, gr[S][1].y, gr[S][1].z, gr[S][1].w};
+#pragma unroll
+      for (int i = 0; i < 8; ++i) xp[i] = (xp[i] * inv) * gv[i];
+    }
+    float mx = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      xp[i] = live ? xp[i] : 0.0f;
+      mx = fmaxf(mx, fabsf(xp[i]));
+    }
+    mx = pair_max(mx, 1);
+    mx = pair_max(mx, 2);
+    mx = pair_max(mx, 4);
+    mx = pair_max(mx, 8);
+    int e = 0;
+    (void)frexpf(mx, &e);  // mx < 2^e (mx = 0: e = 0)
+    const float up = ldexpf(1.0f, 30 - e);
+    uint32_t z[8];  // bytes: the balanced limbs of X
+#pragma unroll
+    for (int i = 0; i < 8; ++i) z[i] = (uint32_t(int(xp[i] * up)) + 0x808080u) ^ 0x808080u;
+    uint32_t lo[4], hi[4];
+    limb_words(z[0], z[2], z[4], z[6], lo);
+    limb_words(z[1], z[3], z[5], z[7], hi);
+    const uint32_t gs = uint32_t(lane) >> 4, gq = (uint32_t(lane) >> 2) & 3u, gh = (uint32_t(lane) >> 1) & 1u;
+#pragma unroll
+    for (int L = 0; L < 4; ++L) {
+      tb2[((uint32_t(S) * 128 + ((gs * 4 + gq) * 2 + gh) * 4 + uint32_t(L))) * 2 + uint32_t(lane & 1)] =
+          make_uint2(lo[L], hi[L]);
+      int sl = __builtin_amdgcn_sdot4(int(lo[L]), 0x01010101, __builtin_amdgcn_sdot4(int(hi[L]), 0x01010101, 0, false), false);
+      sl += int(pair_u(uint32_t(sl), 1));
+      sl += int(pair_u(uint32_t(sl), 2));
+      sl += int(pair_u(uint32_t(sl), 4));
+      sl += int(pair_u(uint32_t(sl), 8));
+      if ((lane & 15) == 0) s_ci[wave][S][gs + 4 * uint32_t(L)] = -8 * sl;
+    }
+    if ((lane & 15) == 0)
+      s_e[(wave * 4 + uint32_t(S)) * 4 + gs] = isfinite(mx) ? ldexpf(1.0f, e - 30) : __int_as_float(0x7fc00000);
+  }
+  __syncthreads();  // every wave's table (the corrections read any column)
+  int cinit[4];
+  float lpf[4];
+#pragma unroll
+  for (int S = 0; S < 4; ++S) {
+    cinit[S] = s_ci[wave][S][n];
+    lpf[S] = s_e[(wave * 4 + uint32_t(S)) * 4 + uint32_t(n & 3)] * __int_as_float(int(127 + 8 * (n >> 2)) << 23);
+  }
+  const uint4* tbw = s_tb + wave * (kXmTableBytes / 16);
+  const uint8_t* tbytes = reinterpret_cast<const uint8_t*>(s_tb);
+
+  float bv = -1e30f;
+  uint32_t bi = 0xffffffffu, nf = 0;
+  auto compute = [&](const XmLoads<R, SPL>& L, int buf) {
+    const GemvPart P0 = kRope ? pick_part(a, L.pu) : a.part[0];
+    const GemvPart& P1 = kSwi ? a.part[1] : P0;
+    const uint32_t rb = L.row_base;
+    float acc = 0.0f;
+#pragma unroll
+    for (int S = 0; S < 4; ++S) {
+      i32x4_t D = {cinit[S], cinit[S], cinit[S], cinit[S]};
+      const uint32_t w4[4] = {L.q[S].x, L.q[S].y, L.q[S].z, L.q[S].w};
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const uint4 t = tbw[uint32_t(S) * 128 + (((uint32_t(n & 3) * 4 + uint32_t(q)) * 2 + uint32_t(h)) * 4) + uint32_t(n >> 2)];
+        const i32x4_t B = {int(t.x), int(t.y), int(t.z), int(t.w)};
+        const uint32_t w0 = w4[2 * h], w1 = w4[2 * h + 1];
+        const i32x4_t A = {int(w0 & 0x0f0f0f0fu), int((w0 >> 4) & 0x0f0f0f0fu), int(w1 & 0x0f0f0f0fu),
+                           int((w1 >> 4) & 0x0f0f0f0fu)};
+        D = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, B, D, 0, 0, 0);
+      }
+      const int j = n & 3;
+      const int v = j == 0 ? D[0] : j == 1 ? D[1] : j == 2 ? D[2] : D[3];
+      const float f = float(v) * lpf[S];
+      const float t = ((f + dpp_f<0x114>(f)) + dpp_f<0x118>(f)) + dpp_f<0x11c>(f);
+      // (a group past the input: its products are zero; its scale, read from group 0, is not used)
+      const bool gv = gw + 4 * uint32_t(S) + uint32_t(n & 3) < ng;
+      float r = gv ? t * h2f(uint16_t(L.s[S])) : 0.0f;
+      r = pair_sum(r, 1);
+      r = pair_sum(r, 2);
+      acc += r;
+    }
+    // corrections of row q over its 16 lanes
+    float cs = 0.0f;
+#pragma unroll
+    for (int t = 0; t < SPL; ++t) {
+      const bool on = ((L.cuse >> t) & 1u) && L.ce[t].y != 0.0f;
+      const float xc = xm_input(tbytes, s_e, on ? __float_as_uint(L.ce[t].x) : 0u);
+      cs = on ? fmaf(L.ce[t].y, xc, cs) : cs;
+    }
+    cs = pair_sum(cs, 1);
+    cs = pair_sum(cs, 2);
+    cs = pair_sum(cs, 4);
+    cs = pair_sum(cs, 8);
+    {
+      const bool second = kSwi && q >= R / 2;
+      const uint32_t r = row_of<R, MODE>(rb, q, half);
+      const uint32_t wr = second ? uni(P1.wrows) : uni(P0.wrows);
+      if (n == 12) s_part[buf][wave][q] = r < wr ? acc + cs : 0.0f;
+    }
+    __syncthreads();
+    if (wave == 0 && lane < NE) {
+      float y0 = 0.0f, y1 = 0.0f;
+#pragma unroll
+      for (int w = 0; w < NW; ++w) {
+        y0 += s_part[buf][w][lane];
+        if constexpr (kSwi || kRope) y1 += s_part[buf][w][lane + R / 2];
+      }
+      const uint32_t r = row_of<R, MODE>(rb, lane, half);
+      if constexpr (kRope) {
+        if (r < P0.rows) rope_store(a, P0, r, y0 + L.pre, y1 + L.pre2, L.rc, L.rs);
+      } else if (MODE != int(GemvMode::Accum) || r < P0.wrows) {  // Accum: rows past the tiles stay
+        epilogue<MODE>(P0, r, y0, y1, L.pre, &bv, &bi, &nf);
+      }
+    }
+  };
+
+  // 3. the units: the next unit's loads, then the current unit's products (static buffers)
+  bool last_b = false;
+  while (unit + step < n_units) {
+    issue(unit + step, &LB);
+    compute(LA, 0);
+    unit += step;
+    if (unit + step >= n_units) {
+      last_b = true;
+      break;
+    }
+    issue(unit + step, &LA);
+    compute(LB, 1);
+    unit += step;
+  }
+  if (last_b) compute(LB, 1);
+  else compute(LA, 0);
+  if constexpr (kLogits) {
+    argmax_partial<MODE>(a, bv, bi, nf, s_bv, s_bi, s_nf);
+    if (blockIdx.x == 0 && threadIdx.x == 0) a.result->hidden_norm = sqrtf(tot);
+  }
+}
+
+template <int MODE>
+bool launch_xm(const GemvArgs& a, const GemvLaunch& g, hipStream_t st) {
+  const uint32_t nw = g.threads / kWave;
+  const size_t lds = size_t(nw) * kXmTableBytes + size_t(nw) * 16 * 4;
+  const dim3 gr(g.blocks), bl(g.threads);
+  switch (nw) {
+    case 1: launch_kernel_lds(&k_gemv_xm<MODE, 1>, gr, bl, lds, st, a); return true;
+    case 2: launch_kernel_lds(&k_gemv_xm<MODE, 2>, gr, bl, lds, st, a); return true;
+    case 4: launch_kernel_lds(&k_gemv_xm<MODE, 4>, gr, bl, lds, st, a); return true;
+    case 8: launch_kernel_lds(&k_gemv_xm<MODE, 8>, gr, bl, lds, st, a); return true;
+    case 16: launch_kernel_lds(&k_gemv_xm<MODE, 16>, gr, bl, lds, st, a); return true;
+    default: return false;
+  }
+}
+
 // the x-stationary kernel's variant for a launch: NW waves of 64 * F::kCols columns
 template <class F, int MODE>
 bool launch_xs(const GemvArgs& a, const GemvLaunch& g, hipStream_t st) {
@@ -1975,6 +2315,13 @@ void launch_one(const GemvArgs& a, const GemvLaunch& g, hipStream_t st) {
     if (g.cells == 1) { launch_kernel(&k_gemv_cells<MODE, 1>, dim3(g.blocks), dim3(g.threads), st, a); return; }
     if (g.cells == 2) { launch_kernel(&k_gemv_cells<MODE, 2>, dim3(g.blocks), dim3(g.threads), st, a); return; }
     if (g.cells == 4) { launch_kernel(&k_gemv_cells<MODE, 4>, dim3(g.blocks), dim3(g.threads), st, a); return; }
+  }
+  if constexpr (std::is_same_v<F, FlatW4>) {
+    if (g.xm) {
+      if (launch_xm<MODE>(a, g, st)) return;
+      std::fprintf(stderr, "chpe: no matrix-core flat kernel for %u waves\n", g.threads / kWave);
+      return;
+    }
   }
   if constexpr (std::is_same_v<F, FlatW4> || std::is_same_v<F, FlatW2>) {
     if (g.xs) {
@@ -2175,6 +2522,16 @@ const GemvTuning& gemv_tuning() {
     if (const char* e = std::getenv("CHPE_GEMV_MMA")) v.mma = uint32_t(std::strtoul(e, nullptr, 10));
     if (const char* e = std::getenv("CHPE_GEMV_MMA_LOGITS_BLOCKS")) v.mma_logits_blocks = uint32_t(std::strtoul(e, nullptr, 10));
     if (const char* e = std::getenv("CHPE_GEMV_XS")) v.xs = uint32_t(std::strtoul(e, nullptr, 10));
+    if (const char* e = std::getenv("CHPE_GEMV_XM")) v.xm = uint32_t(std::strtoul(e, nullptr, 10));
+    if (const char* e = std::getenv("CHPE_GEMV_XM_WPC")) {
+      unsigned w[4] = {v.xm_wpc_small, v.xm_wpc_large, v.xm_wpc_logits, v.xm_wpc_wide};
+      if (std::sscanf(e, "%u,%u,%u,%u", &w[0], &w[1], &w[2], &w[3]) == 4 && w[0] && w[1] && w[2] && w[3]) {
+        v.xm_wpc_small = w[0];
+        v.xm_wpc_large = w[1];
+        v.xm_wpc_logits = w[2];
+        v.xm_wpc_wide = w[3];
+      }
+    }
     if (const char* e = std::getenv("CHPE_GEMV_XS_MIN_UNITS")) v.xs_min_units = uint32_t(std::strtoul(e, nullptr, 10));
     if (const char* e = std::getenv("CHPE_GEMV_XS_WPC")) {
       unsigned w[4] = {v.xs_wpc_small, v.xs_wpc_large, v.xs_wpc_logits, v.xs_wpc_wide};
@@ -2196,6 +2553,50 @@ GemvLaunch gemv_geometry(WeightKind kind, GemvMode mode, uint32_t C, const uint3
                          uint32_t* n_units, uint32_t* n_panels, uint32_t* waves_per_unit,
                          uint32_t* unit_begin) {
   const uint32_t ru = 8;
+  if (kind == WeightKind::FlatW4 && gemv_tuning().xm && C % 128 == 0 && C <= 32768) {
+    // the matrix-core input-stationary kernel: waves of 2048 columns, units of 4 rows
+    const uint32_t need = (C + 2047) / 2048;
+    const uint32_t nw = need <= 1 ? 1u : need <= 2 ? 2u : need <= 4 ? 4u : need <= 8 ? 8u : 16u;
+    constexpr uint32_t R = 4;
+    bool ok = true;
+    if (mode == GemvMode::QkvRope)  // whole units per part (head dims are 128 or 256: whole pairs per unit)
+      for (int p = 0; p < n_parts; ++p) ok = ok && rows[p] % R == 0;
+    // (launches of fewer units at <= 8192 columns -- the 72B q/k/v and o projections -- run
+    // faster on the one-unit-per-workgroup kernels: the persistent grid's start-up, the input's
+    // limb tables included, is not amortised over enough units)
+    if (nw < 8 && mode != GemvMode::Logits) {
+      uint32_t u = 0;
+      for (int p = 0; p < (mode == GemvMode::SwiGlu ? 1 : n_parts); ++p)
+        u += mode == GemvMode::SwiGlu ? (rows[p] + R / 2 - 1) / (R / 2) : (rows[p] + R - 1) / R;
+      ok = ok && u >= gemv_tuning().xs_min_units;
+    }
+    if (ok) {
+      uint32_t units = 0;
+      if (mode == GemvMode::SwiGlu) {
+        units = (rows[0] + R / 2 - 1) / (R / 2);
+        unit_begin[0] = unit_begin[1] = 0;
+      } else {
+        for (int p = 0; p < n_parts; ++p) {
+          unit_begin[p] = units;
+          units += (rows[p] + R - 1) / R;
+        }
+      }
+      *n_units = units;
+      *n_panels = need;
+      *waves_per_unit = nw;
+      const GemvTuning& t = gemv_tuning();
+      const uint32_t wpc = nw >= 8 ? t.xm_wpc_wide
+                           : mode == GemvMode::Logits ? t.xm_wpc_logits
+                           : units >= 4096 ? t.xm_wpc_large : t.xm_wpc_small;
+      GemvLaunch g{};
+      g.ru = R;
+      g.xm = R;
+      g.threads = kWave * nw;
+      g.blocks = std::min<uint32_t>(units, 256u * wpc);
+      if (mode == GemvMode::Logits && g.blocks > kMaxLogitsBlocks) g.blocks = kMaxLogitsBlocks;
+      return g;
+    }
+  }
   if ((kind == WeightKind::FlatW4 || kind == WeightKind::FlatW2) && gemv_tuning().xs && C % 128 == 0 &&
       size_t(C) * 4 <= size_t(150) << 10) {
     // the input-stationary persistent kernel: waves of 64 * 32 (4-bit) / 64 * 64 (2-bit) columns
@@ -2247,6 +2648,7 @@ GemvLaunch gemv_geometry(WeightKind kind, GemvMode mode, uint32_t C, const uint3
     case WeightKind::FlatW4: panel_cols = FlatW4::kPanelCols; ppw = FlatW4::kPPW; break;
     case WeightKind::FlatW2: panel_cols = FlatW2::kPanelCols; ppw = FlatW2::kPPW; break;
     case WeightKind::Raw16: panel_cols = Raw16::kPanelCols; ppw = Raw16::kPPW; break;
+    case WeightKind::Raw8: panel_cols = Raw8::kPanelCols; ppw = Raw8::kPPW; break;
     case WeightKind::Cell16Poly: break;  // launched by launch_gemv_poly
   }
   *n_panels = (C + panel_cols - 1) / panel_cols;
@@ -2356,6 +2758,7 @@ void launch_gemv(WeightKind kind, const GemvArgs& a, const GemvLaunch& g, hipStr
     case WeightKind::FlatW4: launch_layout<FlatW4>(a, g, st); break;
     case WeightKind::FlatW2: launch_layout<FlatW2>(a, g, st); break;
     case WeightKind::Raw16: launch_layout<Raw16>(a, g, st); break;
+    case WeightKind::Raw8: launch_layout<Raw8>(a, g, st); break;
     case WeightKind::Cell16Poly:
       std::fprintf(stderr, "chpe: polymorphic cells go through launch_gemv_poly\n");
       break;

@@ -26,6 +26,7 @@ enum class WeightKind : int {
   FlatW4 = 2,    // flat 32768-weight tiles, 4-bit, GROUP128 (gemvCellFlat)
   FlatW2 = 3,    // flat tiles, 2-bit, GROUP128
   Cell16Poly = 4,  // 16-row polymorphic cells of any width (gemvTilePolymorphic), per-cell metadata
+  Raw8 = 5,        // raw int8 tiles as one row-major matrix, times 0.00373708 (dotSegment :1219-1237)
 };
 
 enum class GemvMode : int {
@@ -120,6 +121,7 @@ struct GemvLaunch {  // launch geometry of one GemvArgs
   uint32_t flat;   // > 0: the K-split kernel for flat 4-bit tiles, up to `flat` panels per wave
   uint32_t mma;    // > 0: the matrix-core kernel for 16-row cells at 2048 columns, `mma` tiles per workgroup
   uint32_t xs;     // > 0: the input-stationary persistent kernel for flat tiles, `xs` rows per unit
+  uint32_t xm;     // > 0: its matrix-core form for flat 4-bit tiles, `xm` rows per unit
 };
 
 struct StepState {  // device-resident per-token state read by the captured step
@@ -185,6 +187,9 @@ struct GemvTuning {
   uint32_t mma = 2;    // 16-row cells at 2048 columns on the matrix-core kernel, 1 or 2 tiles per
                        // workgroup of a launch with >= 1024 tiles (CHPE_GEMV_MMA; 0: off)
   uint32_t mma_logits_blocks = 512;   // persistent workgroups of the matrix-core LM head (2 per CU)
+  uint32_t xm = 1;     // flat 4-bit tiles on the matrix-core input-stationary kernel (CHPE_GEMV_XM; 0: off)
+  // its persistent workgroups per CU (CHPE_GEMV_XM_WPC=small,large,logits,wide as below)
+  uint32_t xm_wpc_small = 2, xm_wpc_large = 3, xm_wpc_logits = 2, xm_wpc_wide = 1;
   uint32_t xs = 1;     // flat tiles on the input-stationary persistent kernel (CHPE_GEMV_XS; 0: off)
   // its persistent workgroups per CU (256 CUs): launches of < 4096 units, of more, the LM head,
   // and inputs wider than 8192 columns (CHPE_GEMV_XS_WPC=small,large,logits,wide)

@@ -125,6 +125,13 @@ int chpe_debug_gemv_flat(int mode, uint32_t rows, uint32_t cols, const uint8_t *
 int chpe_debug_gemv_cells(int mode, uint32_t rows, const uint8_t *cells, const uint8_t *cells_up,
                           size_t n_cells, const float *x, const float *gamma, float eps, float *y,
                           uint32_t *out_argmax, float *out_hidden_norm);
+/* One GEMV over raw tiles read as one row-major rows x cols matrix (gemvLinear's raw path,
+ * src/chpe_engine.zig:1455-1488, dotSegment :1194-1251): kind 0 IEEE fp16, 1 bf16, 2 int8 with
+ * each dot times 0.00373708; n_tiles consecutive 16384-byte tiles.  Modes and the other
+ * arguments as for chpe_debug_gemv_flat.  Returns 0, -1 on bad arguments, -3 on a device error. */
+int chpe_debug_gemv_raw(int mode, uint32_t rows, uint32_t cols, int kind, const uint8_t *tiles,
+                        const uint8_t *tiles_up, size_t n_tiles, const float *x, const float *gamma, float eps,
+                        float *y, uint32_t *out_argmax, float *out_hidden_norm);
 /* One GEMV over polymorphic 16-row cells of any width (gemvTilePolymorphic,
  * src/chpe_engine.zig:732-751: 2-bit codebook, 4-bit, int8 with a per-row scale and bias,
  * fp16 / bf16, f32; group-128 scales or the tile's scale and bias; outliers added to group-128

@@ -34,3 +34,8 @@ def w4_archive():
 @pytest.fixture(scope="session")
 def fp16_archive():
     return archive_path(chpe_amd.PACK_3B_FP16_RAW)
+
+
+@pytest.fixture(scope="session")
+def bf16_archive():
+    return archive_path(chpe_amd.PACK_3B_BF16_RAW)

@@ -4,8 +4,11 @@ chpe_debug_gemv_flat, against the oracle (oracle/chpe_oracle.c: oref_gemv_cell_f
 tile, oref_rmsnorm before it).  The widths pick the kernel variants: 4096 / 8192 / 12288 columns
 split the panels over 2 / 4 / 6 waves; launches of 4096 units or more at those widths, every
 LM head and every wider input (the 72B down projection at 29568 columns) run the persistent
-input-stationary kernel (k_gemv_xs), as do the 2-bit tiles.  Row counts are ragged (not
-multiples of the unit).
+input-stationary kernels: 4-bit tiles on the matrix cores (k_gemv_xm: exact integer products
+of the codes with the input split into four signed-byte limbs per 128-column group, which is
+exact for every element within 2^7 of its group's largest and within 2^-31 of that largest
+otherwise), 2-bit tiles on the vector ALUs (k_gemv_xs).  Row counts are ragged (not multiples
+of the unit).
 
 Tolerance: the GPU sums in another order than the oracle's sequential loop (and as
 sum (q x) - 8 sum x per group, which cancels), so each output is compared within

@@ -334,3 +334,22 @@ def test_token_stream_fp16_raw(fp16_archive):
     finally:
         e.close()
         o.close()
+
+
+def test_token_stream_bf16_raw(bf16_archive):
+    """3B bf16 raw tiles (dotSegment's bf16 branch :1238-1251, the bf16 embedding rows and tied
+    LM head :1626-1641): 16-token prompt + 32 greedy against the oracle."""
+    say("token stream 3B BF16 raw: 16 prompt + 32 generated")
+    e = ca.Engine(bf16_archive, arch=0, max_seq_len=64)
+    o = orc.Oracle(bf16_archive, arch=0, max_seq_len=64, threads=16)
+    try:
+        prompt = np.random.default_rng(3).integers(0, V, 16).astype(np.uint32)
+        g = e.generate(prompt, 32)
+        r, gaps = o.generate(prompt, 32)
+        assert check_stream(g, r, gaps, "bf16") == 32
+        am, lg = e.decode_step(int(prompt[0]), 0)
+        o.forward(int(prompt[0]), 0)
+        compare_step(lg, o.logits(), "bf16 pos 0")
+    finally:
+        e.close()
+        o.close()
