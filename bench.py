@@ -192,12 +192,16 @@ def main():
 
     if W:
         e.generate(prompt[:W], 1)  # W steps at positions 0..W-1
-    log(f"building the context: {P} teacher-forced steps")
+    block = e.block_ready()
+    log(f"building the context: {P} teacher-forced positions "
+        f"({'block steps of 8 tokens' if block else 'decode steps'})")
     t = time.perf_counter()
-    first = e.generate(prompt, 1)  # teacher-forced context: positions 0..P-1
+    if block:  # positions 0..P-1, every weight read once per 8 tokens; decode continues from P
+        first = [e.prefill(prompt)]
+    else:
+        first = e.generate(prompt, 1)  # teacher-forced context: positions 0..P-1
     prefill_s = time.perf_counter() - t
-    log(f"context: {P} teacher-forced steps in {prefill_s:.2f} s ({prefill_s / P * 1e3:.3f} ms/step), "
-        f"first generated token {int(first[0])}")
+    log(f"context: {P} positions in {prefill_s:.2f} s ({P / prefill_s:.1f} tok/s), first generated token {int(first[0])}")
 
     device_sync()
     t0 = time.perf_counter()
@@ -227,6 +231,20 @@ def main():
             f"{avg_ms * per_step:6.3f} ms/step ({stages[st]['share']:.1%}); {nbytes / 1e6:9.3f} MB/launch "
             f"-> {nbytes / avg_ms / 1e6:7.1f} GB/s")
         pos += args.live_steps
+    # batch-M verify: 8 drafts at positions pos..pos+7 as one block step (or 8 decode steps)
+    verify = None
+    drafts = np.random.default_rng(2).integers(0, w["V"], 8).astype(np.uint32)
+    e.verify(drafts, pos)
+    device_sync()
+    reps = 5
+    t = time.perf_counter()
+    for _ in range(reps):
+        e.verify(drafts, pos)
+    vt = (time.perf_counter() - t) / reps
+    verify = {"m": 8, "ms_per_call": round(vt * 1e3, 3), "positions_per_s": round(8 / vt, 2),
+              "vs_batch1_tok_s": round(8 / vt / value, 3), "block_step": bool(block), "position": int(pos)}
+    log(f"verify: 8 drafts at positions {pos}..{pos + 7} in {vt * 1e3:.2f} ms -> {8 / vt:.1f} positions/s "
+        f"({8 / vt / value:.2f}x the batch-1 decode rate; {'one block step' if block else '8 decode steps'})")
     dom = max(stages, key=lambda s: stages[s]["us"] * stages[s]["per_step"])
     d = stages[dom]
     kernel = e.stage_kernel(dom)
@@ -261,6 +279,9 @@ def main():
         "stages": stage_table,
         "cpu_baseline": cpu,
         "context_build_s": round(prefill_s, 3),
+        "prefill": {"positions": P, "s": round(prefill_s, 3), "tok_s": round(P / prefill_s, 1),
+                    "mode": "block steps of 8 tokens" if block else "decode steps"},
+        "verify": verify,
     }
     print(json.dumps(out), flush=True)
 

@@ -26,7 +26,7 @@ ENGINE_SYMBOLS = [
     "chpe_get_hidden_dim", "chpe_get_num_layers", "chpe_get_last_elapsed_ns",
     "chpe_get_last_argmax", "chpe_get_last_max_logit", "chpe_get_last_token0_logit",
     "chpe_get_last_hidden_norm", "chpe_free", "chpe_init_ex", "chpe_decode_step",
-    "chpe_generate", "chpe_verify", "chpe_last_error", "chpe_get_max_seq_len", "chpe_get_hidden",
+    "chpe_generate", "chpe_verify", "chpe_prefill", "chpe_block_ready", "chpe_last_error", "chpe_get_max_seq_len", "chpe_get_hidden",
     "chpe_time_steps", "chpe_time_stage", "chpe_time_stage_live", "chpe_stage_bytes", "chpe_step_bytes", "chpe_stage_kernel",
     "chpe_debug_gemv", "chpe_debug_flat_tile_weights", "chpe_debug_gemv_flat", "chpe_debug_gemv_cells", "chpe_debug_gemv_poly", "chpe_debug_gemv_raw", "chpe_debug_embed_row_cell",
     "chpe_debug_attention", "chpe_attention_noalloc", "chpe_debug_deltanet_conv", "chpe_debug_deltanet_step",
@@ -68,6 +68,8 @@ def load_engine_lib():
             "chpe_init_ex": (V, [ctypes.c_char_p, I, S, I]),
             "chpe_decode_step": (I, [V, ctypes.c_uint32, S, _c_float_p]),
             "chpe_generate": (I, [V, _c_u32_p, S, S, _c_u32_p]),
+            "chpe_prefill": (I, [V, _c_u32_p, S, _c_float_p]),
+            "chpe_block_ready": (I, [V]),
             "chpe_verify": (I, [V, _c_u32_p, S, S, _c_u32_p]),
             "chpe_last_error": (ctypes.c_char_p, []),
             "chpe_get_max_seq_len": (S, [V]),
@@ -250,6 +252,17 @@ class Engine:
                                     out.ctypes.data_as(_c_u32_p))
         self._check(rc, "chpe_generate")
         return out
+
+    def prefill(self, tokens, want_logits=False):
+        toks = np.ascontiguousarray(tokens, dtype=np.uint32)
+        logits = np.empty(self.vocab, dtype=np.float32) if want_logits else None
+        rc = self.lib.chpe_prefill(self.ctx, toks.ctypes.data_as(_c_u32_p), toks.size,
+                                   _fp(logits) if want_logits else None)
+        self._check(rc, "chpe_prefill")
+        return (rc, logits) if want_logits else rc
+
+    def block_ready(self):
+        return bool(self.lib.chpe_block_ready(self.ctx))
 
     def verify(self, drafts, pos):
         d = np.ascontiguousarray(drafts, dtype=np.uint32)

@@ -32,8 +32,20 @@ template <> struct KvElem<float> {
 // PW = 64/LPP positions for the weighted sum; all K/V loads of a wave are issued before any
 // arithmetic.  The softmax statistics are per wave, merged over the NW waves in LDS; one
 // partial (max, sum, weighted V sum) per chunk and query head goes to HBM for k_attn_merge.
+// query z of a block step (blockIdx.z; 0 in the batch-1 step): its query and output rows, its
+// chunk partials, position pos + z
+__device__ __forceinline__ AttnArgs attn_query(AttnArgs a) {
+  const uint32_t z = blockIdx.z;
+  a.q += size_t(z) * a.H * a.hd;
+  a.out += size_t(z) * a.H * a.hd;
+  a.part_ml += size_t(z) * a.H * a.n_chunks * 2;
+  a.part_acc += size_t(z) * a.H * a.n_chunks * a.hd;
+  return a;
+}
+
 template <int HD, int GQ, typename KT, int LPP, int NW>
-__global__ void __launch_bounds__(NW * 64) k_attn_chunk(AttnArgs a) {
+__global__ void __launch_bounds__(NW * 64) k_attn_chunk(AttnArgs a0) {
+  const AttnArgs a = attn_query(a0);
   using E = KvElem<KT>;
   constexpr int PW = 64 / LPP, CH = NW * PW, NT = NW * 64;
   constexpr int DK = HD / LPP;               // K dims per lane
@@ -42,7 +54,7 @@ __global__ void __launch_bounds__(NW * 64) k_attn_chunk(AttnArgs a) {
   constexpr int DPL = HD / 64;              // V dims per lane
   constexpr int VW = DPL * E::kBytes / 4;   // 32-bit words of a lane's V dims (1, 2 or 4)
   static_assert(KW % 4 == 0 && VW >= 1, "");
-  const uint32_t pos = a.state->pos, ctx = pos + 1;
+  const uint32_t pos = a.state->pos + blockIdx.z, ctx = pos + 1;
   const uint32_t c = blockIdx.x, kvh = blockIdx.y;
   if (c * CH >= ctx) return;  // the whole workgroup
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -219,7 +231,8 @@ __device__ __forceinline__ h4_t f16_part(float a, float b, float c, float d, boo
 }
 
 template <int HD, int GQ, int NW, int T>
-__global__ void __launch_bounds__(NW * 64) k_attn_mfma(AttnArgs a) {
+__global__ void __launch_bounds__(NW * 64) k_attn_mfma(AttnArgs a0) {
+  const AttnArgs a = attn_query(a0);
   constexpr int KD = HD / 4;   // K dims per lane
   constexpr int KS = HD / 16;  // k-steps of the score product
   constexpr int VD = HD / 16;  // V dims per lane = N-tiles of the output product
@@ -227,7 +240,7 @@ __global__ void __launch_bounds__(NW * 64) k_attn_mfma(AttnArgs a) {
   static_assert(CH == int(attn_chunk_of(HD)) && GQ <= 8 && NW * GQ <= 64 && (NW & (NW - 1)) == 0, "");
   const uint32_t c = blockIdx.x, kvh = blockIdx.y;
   // the position is requested first and waited for only after the loads below are issued
-  const uint32_t pos = a.state->pos, ctx = pos + 1;
+  const uint32_t pos = a.state->pos + blockIdx.z, ctx = pos + 1;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int G = lane >> 4, n = lane & 15, h = n & 7;  // h: the query head of column / row n
   const bool rem = n >= 8;
@@ -391,14 +404,15 @@ __global__ void __launch_bounds__(NW * 64) k_attn_mfma(AttnArgs a) {
 // weights exp(m_c - M) itself from the chunk statistics (no barrier before the sums).
 constexpr uint32_t kMergeWaves = 4;
 template <int HD>
-__global__ void __launch_bounds__(64 * kMergeWaves) k_attn_merge(AttnArgs a) {
+__global__ void __launch_bounds__(64 * kMergeWaves) k_attn_merge(AttnArgs a0) {
+  const AttnArgs a = attn_query(a0);
   constexpr uint32_t CH = attn_chunk_of(HD), KC = (kAttnMaxChunks + 63) / 64, B = 32;
   static_assert(kAttnMaxChunks % 4 == 0, "");
   __shared__ __align__(16) float s_w[KC * 64];
   __shared__ float s_o[kMergeWaves][64];
   const uint32_t h = blockIdx.x, lane = threadIdx.x & 63, d = blockIdx.y * 64 + lane;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const uint32_t pos = a.state->pos, nch = a.n_chunks;
+  const uint32_t pos = a.state->pos + blockIdx.z, nch = a.n_chunks;
   const float* ml = a.part_ml + size_t(h) * nch * 2;
   const float* acc = a.part_acc + size_t(h) * nch * HD + d;
   float mv[KC], lv[KC], av[B];
@@ -454,7 +468,7 @@ __global__ void __launch_bounds__(64 * kMergeWaves) k_attn_merge(AttnArgs a) {
 }  // namespace
 
 void launch_attention_partial(const AttnArgs& a, hipStream_t st) {
-  const dim3 grid(a.n_chunks, a.KV);
+  const dim3 grid(a.n_chunks, a.KV, a.nq > 1 ? a.nq : 1);
   const uint32_t gq = a.H / a.KV;
   if (a.hd == 128 && gq == 8)  // fp16: 4 waves x 1 tile; f32: 4 waves x 16 positions, 4 lanes per K row
     a.kv_f16 ? launch_kernel(&k_attn_mfma<128, 8, 4, 1>, grid, dim3(256), st, a)
@@ -465,8 +479,9 @@ void launch_attention_partial(const AttnArgs& a, hipStream_t st) {
 }
 
 void launch_attention_combine(const AttnArgs& a, hipStream_t st) {
-  if (a.hd == 128) launch_kernel(&k_attn_merge<128>, dim3(a.H, 2), dim3(64 * kMergeWaves), st, a);
-  else launch_kernel(&k_attn_merge<256>, dim3(a.H, 4), dim3(64 * kMergeWaves), st, a);
+  const uint32_t nq = a.nq > 1 ? a.nq : 1;
+  if (a.hd == 128) launch_kernel(&k_attn_merge<128>, dim3(a.H, 2, nq), dim3(64 * kMergeWaves), st, a);
+  else launch_kernel(&k_attn_merge<256>, dim3(a.H, 4, nq), dim3(64 * kMergeWaves), st, a);
 }
 
 bool attention_supported(uint32_t H, uint32_t KV, uint32_t hd) {

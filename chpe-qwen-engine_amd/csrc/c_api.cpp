@@ -157,6 +157,19 @@ int chpe_verify(void* ctx, const uint32_t* drafts, size_t m, size_t pos, uint32_
   return 0;
 }
 
+int chpe_prefill(void* ctx, const uint32_t* tokens, size_t num_tokens, float* out_logits) {
+  if (!ctx || !tokens || num_tokens == 0) return -1;
+  Context* c = C(ctx);
+  ForwardResult r{};
+  const int rc = c->engine->prefill(tokens, num_tokens, &r);
+  if (rc) return rc;
+  remember(c, r);
+  if (out_logits && c->engine->copy_logits(out_logits)) return -3;
+  return int(r.argmax_token);
+}
+
+int chpe_block_ready(void* ctx) { return ctx && C(ctx)->engine->block_ready() ? 1 : 0; }
+
 size_t chpe_get_last_logits(void* ctx, float* out, size_t max_len) {
   if (!ctx || !out) return 0;
   Context* c = C(ctx);

@@ -209,6 +209,18 @@ __device__ __forceinline__ float dot64_w2(uint4 q, const float* x) {
   return a0 + a1;
 }
 
+typedef int i32x4_t __attribute__((ext_vector_type(4)));
+
+// the 4 x 4 byte transpose: w[k] = (a.k, b.k, c.k, d.k)
+__device__ __forceinline__ void limb_words(uint32_t a, uint32_t b, uint32_t c, uint32_t d, uint32_t* w) {
+  const uint32_t pab = __builtin_amdgcn_perm(b, a, 0x05010400u), qab = __builtin_amdgcn_perm(b, a, 0x07030602u);
+  const uint32_t pcd = __builtin_amdgcn_perm(d, c, 0x05010400u), qcd = __builtin_amdgcn_perm(d, c, 0x07030602u);
+  w[0] = __builtin_amdgcn_perm(pcd, pab, 0x05040100u);
+  w[1] = __builtin_amdgcn_perm(pcd, pab, 0x07060302u);
+  w[2] = __builtin_amdgcn_perm(qcd, qab, 0x05040100u);
+  w[3] = __builtin_amdgcn_perm(qcd, qab, 0x07060302u);
+}
+
 // sum over 16 int8 weights (+128, as unsigned bytes: the sign bit flipped) * x; the caller
 // subtracts 128 * sum(x)
 __device__ __forceinline__ float dot16_i8p(uint4 q, const float* x) {

@@ -74,11 +74,18 @@ std::unique_ptr<Engine> Engine::create(const uint8_t* bytes, size_t len, const E
 
 Engine::~Engine() {
   if (stream_) (void)hipStreamSynchronize(stream_);
+  for (uint32_t m = 0; m <= kMaxBlock; ++m) {
+    if (bgraph_exec_[m]) (void)hipGraphExecDestroy(bgraph_exec_[m]);
+    if (bgraph_[m]) (void)hipGraphDestroy(bgraph_[m]);
+  }
   if (graph_exec_) (void)hipGraphExecDestroy(graph_exec_);
   if (graph_) (void)hipGraphDestroy(graph_);
   for (void* p : allocs_) (void)hipFree(p);
   if (h_state_) (void)hipHostFree(h_state_);
   if (h_result_) (void)hipHostFree(h_result_);
+  if (h_btok_) (void)hipHostFree(h_btok_);
+  if (h_bout_) (void)hipHostFree(h_bout_);
+  if (h_bstate_) (void)hipHostFree(h_bstate_);
   if (stream_) (void)hipStreamDestroy(stream_);
 }
 
@@ -260,6 +267,14 @@ bool Engine::init(const uint8_t* b, size_t len, const EngineConfig& cfg, std::st
   d_rope_cur_ = static_cast<float*>(dev_alloc(hd * 4));
   HIP_TRY(hipHostMalloc(reinterpret_cast<void**>(&h_state_), sizeof(StepState), hipHostMallocDefault));
   HIP_TRY(hipHostMalloc(reinterpret_cast<void**>(&h_result_), sizeof(StepResult), hipHostMallocDefault));
+  {  // the block step for archives whose projections are all flat 4-bit tiles (CHPE_BLOCK=0: off)
+    const char* bk = std::getenv("CHPE_BLOCK");
+    std::string why;
+    if (!(bk && bk[0] == '0') && !plan_block(&why) && !why.empty()) {
+      *err = "block step: " + why;
+      return false;
+    }
+  }
   HIP_TRY(hipDeviceSynchronize());
 
   // ---- capture the step (CHPE_GRAPH=0 launches the same kernels directly on the stream,
@@ -829,6 +844,13 @@ int Engine::generate(const uint32_t* prompt, size_t n_prompt, size_t n_gen, uint
 int Engine::verify(const uint32_t* drafts, size_t m, size_t pos, uint32_t* out_argmax, ForwardResult* last) {
   if (!drafts || m == 0 || !out_argmax) return -1;
   if (pos + m > cfg_.max_seq_len) return -2;
+  if (block_ok_ && m <= kMaxBlock) {  // every weight read once for the m drafts
+    ForwardResult r{};
+    const int rc = block_forward(drafts, m, pos, out_argmax, &r);
+    if (rc) return rc;
+    if (last) *last = r;
+    return 0;
+  }
   const uint64_t t0 = now_ns();
   // the drafts take the prompt slots of their positions, so every step is teacher-forced
   if (hipMemcpyAsync(d_prompt_ + pos, drafts, m * 4, hipMemcpyHostToDevice, stream_) != hipSuccess) return -3;
@@ -841,6 +863,199 @@ int Engine::verify(const uint32_t* drafts, size_t m, size_t pos, uint32_t* out_a
     last->elapsed_ns = now_ns() - t0;
   }
   return 0;
+}
+
+// ---- the block step ---------------------------------------------------------------------------
+// Returns false with *err empty when the archive has no block step (a projection that is not
+// flat 4-bit tiles), false with *err set on an allocation failure.
+bool Engine::plan_block(std::string* err) {
+  block_ok_ = false;
+  const size_t D = arch_.hidden_dim, I = arch_.intermediate_dim, V = arch_.vocab_size;
+  const size_t qd = arch_.num_attn_heads * arch_.head_dim, kvd = arch_.num_kv_heads * arch_.head_dim;
+  auto flat = [](const ProjPlan& p) { return p.kind == WeightKind::FlatW4; };
+  for (const LayerPlan& L : layers_)
+    if (!flat(L.q) || !flat(L.k) || !flat(L.v) || !flat(L.o) || !flat(L.gate) || !flat(L.up) || !flat(L.down))
+      return false;
+  if (!flat(lm_head_) || D % 128 || I % 128 || qd % 128) return false;
+  auto units = [](size_t rows) { return (rows + 15) / 16; };
+  auto ranges = [](size_t C) { return (C + kBlockRange - 1) / kBlockRange; };
+  size_t part_floats = 0;  // ranges x kMaxBlock x rows_all, the largest GEMV
+  part_floats = std::max(part_floats, ranges(D) * 16 * (units(qd) + 2 * units(kvd)));
+  part_floats = std::max(part_floats, ranges(qd) * 16 * units(D));
+  part_floats = std::max(part_floats, ranges(D) * 16 * 2 * units(I));
+  part_floats = std::max(part_floats, ranges(I) * 16 * units(D));
+  part_floats = std::max(part_floats, ranges(D) * 16 * units(V));
+  part_floats *= kMaxBlock;
+  const size_t Cmax = std::max({D, I, qd}), ngm = Cmax / 128, nq = (kMaxBlock + 3) / 4;
+  const size_t hd = arch_.head_dim, H = arch_.num_attn_heads;
+  auto fa = [&](size_t n) { return static_cast<float*>(dev_alloc(n * 4)); };
+  d_btok_ = static_cast<uint32_t*>(dev_alloc(kMaxBlock * 4));
+  d_bout_ = static_cast<uint32_t*>(dev_alloc(kMaxBlock * 4));
+  d_bstate_ = static_cast<StepState*>(dev_alloc(sizeof(StepState)));
+  d_bx_ = fa(kMaxBlock * D);
+  d_bq_ = fa(kMaxBlock * qd);
+  d_battn_ = fa(kMaxBlock * qd);
+  d_bmlp_ = fa(kMaxBlock * I);
+  d_blog_ = fa(kMaxBlock * V);
+  d_bpartial_ = fa(part_floats);
+  d_bpml_ = fa(kMaxBlock * H * n_chunks_ * 2);
+  d_bpacc_ = fa(kMaxBlock * H * n_chunks_ * hd);
+  btab_.tb = static_cast<uint4*>(dev_alloc(nq * ngm * 128 * sizeof(uint4)));
+  btab_.ci = static_cast<int4*>(dev_alloc(nq * ngm * 4 * sizeof(int4)));
+  btab_.ew = fa(nq * ngm * 4);
+  btab_.xt = fa(Cmax * kMaxBlock);
+  btab_.ss = fa(kMaxBlock);
+  d_bpartials_ = static_cast<ArgmaxPartial*>(dev_alloc(kMaxBlock * 512 * sizeof(ArgmaxPartial)));
+  if (!d_btok_ || !d_bout_ || !d_bstate_ || !d_bx_ || !d_bq_ || !d_battn_ || !d_bmlp_ || !d_blog_ || !d_bpartial_ ||
+      !d_bpml_ || !d_bpacc_ || !btab_.tb || !btab_.ci || !btab_.ew || !btab_.xt || !btab_.ss || !d_bpartials_) {
+    *err = "allocation";
+    return false;
+  }
+  if (hipHostMalloc(reinterpret_cast<void**>(&h_btok_), kMaxBlock * 4, hipHostMallocDefault) != hipSuccess ||
+      hipHostMalloc(reinterpret_cast<void**>(&h_bout_), kMaxBlock * 4, hipHostMallocDefault) != hipSuccess ||
+      hipHostMalloc(reinterpret_cast<void**>(&h_bstate_), sizeof(StepState), hipHostMallocDefault) != hipSuccess) {
+    *err = "pinned allocation";
+    return false;
+  }
+  block_ok_ = true;
+  return true;
+}
+
+uint32_t Engine::enqueue_block_gemv(const ProjPlan* const* parts, float* const* outs, int n, GemvMode mode,
+                                    const float* x, uint32_t C, const float* gamma, uint32_t m, size_t layer,
+                                    hipStream_t st) {
+  BlockGemvArgs b{};
+  b.g.n_parts = n;
+  b.g.mode = int(mode);
+  b.g.C = C;
+  b.g.x = x;
+  b.g.gamma = gamma;
+  b.g.eps = arch_.rms_eps;
+  uint32_t units = 0;
+  const uint32_t roles[3] = {kRoleQ, kRoleK, kRoleV};
+  for (int i = 0; i < n; ++i) {
+    const ProjPlan& p = *parts[i];
+    GemvPart& gp = b.g.part[i];
+    gp.base = p.base;
+    gp.stride = p.stride;
+    gp.rows = p.rows;
+    gp.wrows = p.wrows ? p.wrows : p.rows;
+    gp.unit_begin = units;
+    gp.y = outs[i];
+    gp.bias = p.bias;
+    gp.corr = p.corr;
+    gp.corr_kmax = p.corr_kmax;
+    gp.rope_role = mode == GemvMode::QkvRope ? roles[i] : 0u;
+    units += (p.rows + 15) / 16;
+  }
+  b.t = btab_;
+  b.m = m;
+  b.nq = (m + 3) / 4;
+  b.n_units = units;
+  b.rows_all = 16 * units;
+  b.partial = d_bpartial_;
+  if (mode == GemvMode::QkvRope) {
+    b.g.rope = rope_args(layer);
+    b.state = d_bstate_;
+    b.rope_cos = d_rope_cos_;
+    b.rope_sin = d_rope_sin_;
+    b.rope_rows = uint32_t(cfg_.max_seq_len);
+  }
+  if (mode == GemvMode::Logits) b.partials = d_bpartials_;
+  launch_block_limbs(x, gamma, arch_.rms_eps, C, m, btab_, st);
+  return launch_block_gemv(b, st);
+}
+
+int Engine::block_forward(const uint32_t* tokens, size_t m, size_t pos, uint32_t* out_argmax, ForwardResult* last) {
+  if (!block_ok_ || !tokens || m == 0 || m > kMaxBlock) return -1;
+  if (pos + m > cfg_.max_seq_len) return -2;
+  const uint64_t t0 = now_ns();
+  const uint32_t mm = uint32_t(m);
+  hipStream_t st = stream_;
+  std::memcpy(h_btok_, tokens, m * 4);
+  *h_bstate_ = StepState{tokens[0], uint32_t(pos), 0, 0};
+  if (hipMemcpyAsync(d_btok_, h_btok_, m * 4, hipMemcpyHostToDevice, st) != hipSuccess ||
+      hipMemcpyAsync(d_bstate_, h_bstate_, sizeof(StepState), hipMemcpyHostToDevice, st) != hipSuccess)
+    return -3;
+  if (use_graph_) {  // one captured graph per token count, captured on first use
+    if (!bgraph_exec_[m]) {
+      if (hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal) != hipSuccess) return -3;
+      record_block(mm, st);
+      if (hipStreamEndCapture(st, &bgraph_[m]) != hipSuccess ||
+          hipGraphInstantiate(&bgraph_exec_[m], bgraph_[m], nullptr, nullptr, 0) != hipSuccess)
+        return -3;
+    }
+    if (hipGraphLaunch(bgraph_exec_[m], st) != hipSuccess) return -3;
+  } else {
+    record_block(mm, st);
+  }
+  if (hipMemcpyAsync(h_bout_, d_bout_, m * 4, hipMemcpyDeviceToHost, st) != hipSuccess ||
+      hipMemcpyAsync(h_result_, d_result_, sizeof(StepResult), hipMemcpyDeviceToHost, st) != hipSuccess)
+    return -3;
+  if (hipStreamSynchronize(st) != hipSuccess) return -3;
+  if (out_argmax) std::memcpy(out_argmax, h_bout_, m * 4);
+  if (last) {
+    last->argmax_token = h_result_->argmax;
+    last->max_logit = h_result_->max_logit;
+    last->token0_logit = h_result_->token0_logit;
+    last->hidden_norm = h_result_->hidden_norm;
+    last->all_finite = h_result_->all_finite != 0;
+    last->elapsed_ns = now_ns() - t0;
+  }
+  return 0;
+}
+
+void Engine::record_block(uint32_t mm, hipStream_t st) {
+  const uint32_t D = uint32_t(arch_.hidden_dim), I = uint32_t(arch_.intermediate_dim), V = uint32_t(arch_.vocab_size);
+  const uint32_t qd = uint32_t(arch_.num_attn_heads * arch_.head_dim);
+  launch_block_embed(embed_args(), d_btok_, mm, d_bx_, st);
+  for (size_t l = 0; l < arch_.num_layers; ++l) {
+    const LayerPlan& L = layers_[l];
+    const ProjPlan* qkv[3] = {&L.q, &L.k, &L.v};
+    float* qo[3] = {d_bq_, nullptr, nullptr};
+    enqueue_block_gemv(qkv, qo, 3, GemvMode::QkvRope, d_bx_, D, L.gamma_in, mm, l, st);
+    AttnArgs at = attn_args(l);
+    at.state = d_bstate_;
+    at.q = d_bq_;
+    at.out = d_battn_;
+    at.part_ml = d_bpml_;
+    at.part_acc = d_bpacc_;
+    at.nq = mm;
+    launch_attention(at, st);
+    const ProjPlan* o[1] = {&L.o};
+    float* hid[1] = {d_bx_};
+    enqueue_block_gemv(o, hid, 1, GemvMode::Accum, d_battn_, qd, nullptr, mm, l, st);
+    const ProjPlan* gu[2] = {&L.gate, &L.up};
+    float* mlp[2] = {d_bmlp_, d_bmlp_};
+    enqueue_block_gemv(gu, mlp, 2, GemvMode::SwiGlu, d_bx_, D, L.gamma_post, mm, l, st);
+    const ProjPlan* dn[1] = {&L.down};
+    enqueue_block_gemv(dn, hid, 1, GemvMode::Accum, d_bmlp_, I, nullptr, mm, l, st);
+  }
+  const ProjPlan* lm[1] = {&lm_head_};
+  float* lg[1] = {d_blog_};
+  const uint32_t eb = enqueue_block_gemv(lm, lg, 1, GemvMode::Logits, d_bx_, D, d_gamma_final_, mm, 0, st);
+  launch_block_finish(BlockFinishArgs{d_bpartials_, eb, mm, d_blog_, V, btab_.ss, d_bout_, d_result_}, st);
+  (void)hipMemcpyAsync(d_logits_, d_blog_ + size_t(mm - 1) * V, size_t(V) * 4, hipMemcpyDeviceToDevice, st);
+}
+
+int Engine::prefill(const uint32_t* tokens, size_t n, ForwardResult* out) {
+  if (!tokens || n == 0 || !out) return -1;
+  if (n > cfg_.max_seq_len) return -2;
+  if (!block_ok_) {  // no block step for this archive: sequential steps
+    const int rc = forward_tokens(tokens, n, out);
+    if (rc) return rc;
+    h_pos_ = n;
+    return 0;
+  }
+  uint32_t am[kMaxBlock];
+  for (size_t i = 0; i < n; i += kMaxBlock) {
+    const size_t m = std::min<size_t>(kMaxBlock, n - i);
+    const int rc = block_forward(tokens + i, m, i, am, out);
+    if (rc) return rc;
+  }
+  // continue greedy decoding from here: the last argmax at position n
+  if (n < cfg_.max_seq_len && set_state(StepState{out->argmax_token, uint32_t(n), 0, 0})) return -3;
+  return sync();
 }
 
 int Engine::copy_logits(float* out) const {

@@ -103,6 +103,17 @@ class Engine {
   // drafts[0..m) at positions pos..pos+m-1, each step teacher-forced (the KV rows at those
   // positions are overwritten); out_argmax[i] = argmax after draft i
   int verify(const uint32_t* drafts, size_t m, size_t pos, uint32_t* out_argmax, ForwardResult* last);
+  // the block step: tokens[0..m), m <= kMaxBlock, at positions pos..pos+m-1 through every layer
+  // with each weight read once for all m tokens (flat 4-bit archives: block_ready()), each
+  // token's arithmetic that of forwardDecode; KV rows pos..pos+m-1 are written;
+  // out_argmax[i] = argmax after token i; the last token's logits become copy_logits()'s and
+  // its result *last.  The decode state is not touched.  0, -1 bad arguments or no block step
+  // for this archive, -2 past max_seq_len, -3 device error.
+  int block_forward(const uint32_t* tokens, size_t m, size_t pos, uint32_t* out_argmax, ForwardResult* last);
+  bool block_ready() const { return block_ok_; }
+  // positions 0..n-1 teacher-forced in blocks of kMaxBlock (prefill); result and logits of
+  // the last position; the decode state is left at (argmax of the last, n)
+  int prefill(const uint32_t* tokens, size_t n, ForwardResult* out);
   // enqueue n graph launches continuing from the current device state (no sync); -2 and
   // nothing enqueued when the steps would pass max_seq_len
   int launch_steps(size_t n);
@@ -151,6 +162,11 @@ class Engine {
                         const RopeArgs* rope = nullptr, const uint32_t* roles = nullptr);
   AttnArgs attn_args(size_t layer) const;
   double proj_bytes(const ProjPlan& p) const;
+  bool plan_block(std::string* err);
+  void record_block(uint32_t m, hipStream_t st);  // the block step of m tokens after its inputs
+  uint32_t enqueue_block_gemv(const ProjPlan* const* parts, float* const* outs, int n, GemvMode mode,
+                              const float* x, uint32_t C, const float* gamma, uint32_t m, size_t layer,
+                              hipStream_t st);
 
  public:
   // run one projection's GEMV on a caller vector (Store mode, bias included): parity hooks
@@ -198,6 +214,17 @@ class Engine {
   float* d_rope_cur_ = nullptr;      // the step's cos / sin rows (head_dim floats)
   float* d_xn_ = nullptr;            // polymorphic cells: the RMSNorm'ed input
   PolyRaw poly_raw_{};               // polymorphic cells: raw row sums per part
+
+  // the block step (plan_block): m <= kMaxBlock tokens' activations, operand tables, partials
+  bool block_ok_ = false;
+  uint32_t *d_btok_ = nullptr, *h_btok_ = nullptr, *d_bout_ = nullptr, *h_bout_ = nullptr;
+  StepState *d_bstate_ = nullptr, *h_bstate_ = nullptr;
+  float *d_bx_ = nullptr, *d_bq_ = nullptr, *d_battn_ = nullptr, *d_bmlp_ = nullptr, *d_blog_ = nullptr;
+  float *d_bpartial_ = nullptr, *d_bpml_ = nullptr, *d_bpacc_ = nullptr;
+  BlockTables btab_{};
+  ArgmaxPartial* d_bpartials_ = nullptr;
+  hipGraph_t bgraph_[kMaxBlock + 1] = {};          // captured block steps, by token count
+  hipGraphExec_t bgraph_exec_[kMaxBlock + 1] = {};
   int probe_stage_ = -1;                 // stage bracketed by events in record_step
   hipEvent_t* probe_events_ = nullptr;
   size_t probe_next_ = 0;

@@ -1083,7 +1083,6 @@ __global__ void __launch_bounds__(kWave * kCellWaves) k_gemv_cells(GemvArgs a) {
 // cell kernels.  The only workgroup barrier is the one before the epilogue.
 constexpr int kMmaWaves = 4;
 constexpr int kMmaTable = 4 * 4 * 2 * 4;  // B table entries per wave: groups x quarters x halves x limbs
-typedef int i32x4_t __attribute__((ext_vector_type(4)));
 
 // first rows of the two 8-row halves of a tile (the tile's part already chosen; SwiGlu tiles are
 // whole cells of the gate and the up projection, see k_gemv_mma)
@@ -1100,15 +1099,6 @@ __device__ __forceinline__ void mma_tile_rows(const GemvPart& P, uint32_t tile, 
   }
 }
 
-// the 4 x 4 byte transpose: w[k] = (a.k, b.k, c.k, d.k)
-__device__ __forceinline__ void limb_words(uint32_t a, uint32_t b, uint32_t c, uint32_t d, uint32_t* w) {
-  const uint32_t pab = __builtin_amdgcn_perm(b, a, 0x05010400u), qab = __builtin_amdgcn_perm(b, a, 0x07030602u);
-  const uint32_t pcd = __builtin_amdgcn_perm(d, c, 0x05010400u), qcd = __builtin_amdgcn_perm(d, c, 0x07030602u);
-  w[0] = __builtin_amdgcn_perm(pcd, pab, 0x05040100u);
-  w[1] = __builtin_amdgcn_perm(pcd, pab, 0x07060302u);
-  w[2] = __builtin_amdgcn_perm(qcd, qab, 0x05040100u);
-  w[3] = __builtin_amdgcn_perm(qcd, qab, 0x07060302u);
-}
 
 // The wave's 512 input columns (lane l: c0 .. c0 + 7; x' = x * gamma when kNorm) as the B
 // operands of k_gemv_mma's products, through the wave's LDS table: the group exponent (max over

@@ -161,6 +161,8 @@ struct AttnArgs {
   uint32_t H, KV, hd, max_seq, n_chunks;  // max_seq: cache rows per kv head, a multiple of 16
   uint32_t kv_f16;
   float scale;              // 1/sqrt(hd)
+  uint32_t nq;              // queries of a block step at positions pos .. pos + nq - 1 (rows of q,
+                            // out and the partials follow each other); 0 or 1: one query
 };
 
 struct FinishArgs {
@@ -221,6 +223,55 @@ constexpr uint32_t kPolyEpilogueBlocks = 64;
 // number of argmax partials.
 uint32_t launch_gemv_poly(const GemvArgs& a, const PolyPlan* const* plans, float* xn, const PolyRaw& raw,
                           hipStream_t stream);
+
+// ---- the block step: m <= kMaxBlock tokens at consecutive positions through flat 4-bit tiles,
+// every weight read once for all m tokens (batch-M verify, chunked prefill) ----------------------
+constexpr uint32_t kMaxBlock = 8;
+constexpr uint32_t kBlockRange = 2048;  // input columns per workgroup of the block GEMV
+
+// One GEMV input of m tokens as matrix-core operands (k_block_limbs): per token and 128-column
+// group the input (RMS-normalised when gamma is set) as exact integers X = x * 2^(30-e), max
+// |x| < 2^e, in four signed-byte limbs.  Tokens come in quads T (token 4T + t); nq quads.
+struct BlockTables {
+  uint4* tb;   // [nq][ng][4 kq][2 h][16]: entry lane 4t + L = limb L of token 4T + t, the 16
+               //   columns 32 kq + 16 h .. of the group in the operand byte order
+  int4* ci;    // [nq][ng][4]: -8 * the group's limb sums (limbs 0..3) of token 4T + t
+  float* ew;   // [nq][ng][4]: 2^(e - 30) of token 4T + t in the group
+  float* xt;   // [C][kMaxBlock]: the (normalised) input, token-minor (for the outlier corrections)
+  float* ss;   // [kMaxBlock]: each token's sum of squares of the raw input
+};
+
+struct BlockGemvArgs {
+  GemvArgs g;          // parts, mode, C; g.x = the raw input [m][C], g.gamma; rope: caches and head dim
+  BlockTables t;
+  uint32_t m, nq;
+  uint32_t n_units;    // 16-row units over the parts (unit_begin of part p in units)
+  uint32_t rows_all;   // 16 * n_units: rows of the partial-sum buffer
+  float* partial;      // [ranges][kMaxBlock][rows_all]: raw row sums per column range
+  const StepState* state;   // position of token 0 (QkvRope)
+  const float* rope_cos;    // [rope_rows][head_dim/2] full tables
+  const float* rope_sin;
+  uint32_t rope_rows;
+  ArgmaxPartial* partials;  // Logits: [kMaxBlock][epi_blocks]
+  uint32_t epi_blocks;      // set by launch_block_gemv
+};
+
+struct BlockFinishArgs {
+  const ArgmaxPartial* partials;  // [kMaxBlock][n_partials]
+  uint32_t n_partials, m;
+  const float* logits;            // [m][V]
+  uint32_t V;
+  const float* ss;                // the final-norm input's sums of squares per token
+  uint32_t* out_argmax;           // [m]
+  StepResult* result;             // the last token's result
+};
+
+void launch_block_embed(const EmbedArgs& e, const uint32_t* tokens, uint32_t m, float* X, hipStream_t stream);
+void launch_block_limbs(const float* x, const float* gamma, float eps, uint32_t C, uint32_t m,
+                        const BlockTables& t, hipStream_t stream);
+// the block GEMV (k_gemv_mt) and its epilogue; returns the epilogue's workgroups (Logits partials)
+uint32_t launch_block_gemv(BlockGemvArgs& a, hipStream_t stream);
+void launch_block_finish(const BlockFinishArgs& a, hipStream_t stream);
 
 // launchers; all enqueue on `stream` and never synchronise
 void launch_embed(const EmbedArgs& a, hipStream_t stream);

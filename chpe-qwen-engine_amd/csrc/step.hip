@@ -166,6 +166,13 @@ __global__ void __launch_bounds__(256) k_embed(EmbedArgs a) {
   embed_token(a, a.state->token);
 }
 
+// the block step's inputs: token blockIdx.x's embedding row into X[blockIdx.x]
+__global__ void __launch_bounds__(256) k_block_embed(EmbedArgs a, const uint32_t* tokens, float* X) {
+  EmbedArgs e = a;
+  e.hidden = X + size_t(blockIdx.x) * a.D;
+  embed_token(e, tokens[blockIdx.x]);
+}
+
 // argmax / all_finite / logits[0] over the LM head's workgroup partials (chpe_engine.zig:
 // 1775-1787), then the next position's (token, pos): the prompt while it lasts, else the argmax.
 __global__ void __launch_bounds__(256) k_finish(FinishArgs a) {
@@ -293,6 +300,10 @@ const char* last_kernel_name() { return detail::g_last_kernel ? detail::g_last_k
 
 void launch_embed(const EmbedArgs& a, hipStream_t st) {
   launch_kernel(k_embed, dim3(1), dim3(256), st, a);
+}
+
+void launch_block_embed(const EmbedArgs& e, const uint32_t* tokens, uint32_t m, float* X, hipStream_t st) {
+  launch_kernel(k_block_embed, dim3(m), dim3(256), st, e, tokens, X);
 }
 
 void launch_finish(const FinishArgs& a, hipStream_t st) {

@@ -122,3 +122,70 @@ def test_72b_stream_matches_oracle(a72):
 @pytest.mark.timeout(900)
 def test_9b_compat_stream_matches_oracle(a9):
     run_model(a9, 1, 248320, 8, 6, seed=2)
+
+
+def top2_gap(lg):
+    t = np.sort(lg.astype(np.float64))
+    return float(t[-1] - t[-2])
+
+
+def run_block(path, arch, vocab, seed, oracle_check):
+    """The block step (every weight read once for up to 8 tokens; no reference code, defined as
+    the decode steps it replaces) against the decode step on the same engine: chpe_prefill vs
+    chpe_forward_tokens (the last position's logits, then one decode step on each cache, so the
+    KV rows agree), chpe_verify of 8 drafts vs 8 decode steps (every argmax, the last logits).
+    Bars: 2e-4 * max|logit| with the f32 cache, as for the decode step against the oracle;
+    3e-3 with the fp16 cache, twice the single-step bar: the two paths sum in different orders,
+    so k / v elements near an fp16 rounding boundary round differently, and here 19 cached
+    positions (not 3) carry such flips through 80 layers.  An argmax may differ only where the
+    decode step's top-2 gap is below twice the bar.  oracle_check: the prefill's logits against
+    the oracle's forward as well."""
+    rng = np.random.default_rng(seed)
+    prompt = rng.integers(0, vocab, 11).astype(np.uint32)
+    drafts = rng.integers(0, vocab, 8).astype(np.uint32)
+    n = len(prompt)
+    for kv16, rel in ((False, 2e-4), (True, 3e-3)):
+        e = ca.Engine(path, arch=arch, max_seq_len=64, kv_f16=kv16)
+        try:
+            if not e.block_ready():  # 2-bit tiles: prefill and verify are the decode steps, bit for bit
+                _, lseq = e.forward_tokens(prompt, want_logits=True)
+                _, lblk = e.prefill(prompt, want_logits=True)
+                assert np.array_equal(lseq.view(np.uint32), lblk.view(np.uint32))
+                seq = [e.decode_step(int(d), n + i)[0] for i, d in enumerate(drafts[:4])]
+                assert list(e.verify(drafts[:4], n)) == seq
+                continue
+            say(f"block step arch {arch} kv_f16={kv16}: sequential reference")
+            _, lseq = e.forward_tokens(prompt, want_logits=True)
+            seq = [e.decode_step(int(d), n + i) for i, d in enumerate(drafts)]
+            say("  prefill (blocks of 8 + 3)")
+            _, lblk = e.prefill(prompt, want_logits=True)
+            compare_logits(lblk, lseq, "prefill vs forward_tokens", rel)
+            am, lg = e.decode_step(int(drafts[0]), n)
+            compare_logits(lg, seq[0][1], "decode step after prefill", rel)
+            say("  verify 8 drafts")
+            got = e.verify(drafts, n)
+            for i in range(8):
+                ref_am, ref_lg = seq[i]
+                if got[i] != ref_am:
+                    assert top2_gap(ref_lg) < 2 * rel * float(np.abs(ref_lg).max()), (i, int(got[i]), int(ref_am))
+            compare_logits(e.logits(), seq[7][1], "verify: last draft", rel)
+            if oracle_check and not kv16:
+                o = orc.Oracle(path, arch=arch, max_seq_len=64, kv_f16=False, threads=threads())
+                try:
+                    for pos, tok in enumerate(prompt):
+                        o.forward(int(tok), pos)
+                    compare_logits(lblk, o.logits(), "prefill vs oracle", rel)
+                finally:
+                    o.close()
+        finally:
+            e.close()
+
+
+@pytest.mark.timeout(900)
+def test_72b_block_step_matches_decode_steps(a72):
+    run_block(a72, 2, 152064, seed=5, oracle_check=False)
+
+
+@pytest.mark.timeout(900)
+def test_9b_compat_block_step_matches_decode_steps(a9):
+    run_block(a9, 1, 248320, seed=6, oracle_check=True)
