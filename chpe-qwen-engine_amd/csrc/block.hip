@@ -15,8 +15,11 @@
 //    code * limb over the group, starting at -8 * (the limb's sum) for the codes' offset.  The
 //    lane combines its 4 limbs (2^(8 j)), scales by 2^(e - 30) and by the row's group scale,
 //    and accumulates row n of token q over the range's groups; the raw row sums of each range
-//    go to a partial-sum buffer.  Lane (n, q) loads 16 bytes of row n per group (quarter q), the
-//    next item's loads are issued before the current item's products.
+//    go to a partial-sum buffer.  The B layout reads only 64 bytes of each of 16 rows per load
+//    instruction, which the memory system serves at about half the rate of long runs, so the
+//    codes are loaded 512 contiguous bytes of a row at a time (a stage of 16 rows x 8 groups),
+//    passed through a wave-private LDS slot and read back in the B layout; the next stage's
+//    loads are in flight meanwhile.
 // 3. k_block_epi: per output row the ranges' sums in a fixed order, the flat-tile outlier
 //    corrections ((w_out - dequantised code) * x[col], outliers replace weights :632-646) over
 //    16 lanes, and the batch-1 step's epilogue per token: bias, residual, SwiGLU, RoPE at the
@@ -30,87 +33,104 @@ namespace chpe {
 namespace {
 using namespace dev;
 
+// grid (column chunks of 1024, token slots 4 nq): a workgroup of 128 threads converts 1024
+// columns of one token (8 per thread, 16 threads per 128-column group) into the operand tables:
+// the input, RMS-normalised ((x * inv) * gamma, rmsNorm :187-191) when gamma is set, as
+// X = x * 2^(30-e) with max |x| < 2^e (exact in int32) per 128-column group, in four balanced
+// signed-byte limbs (BlockTables).  The norm's sum of squares comes as the producer's partial
+// sums (ssp), read together with the columns; chunk 0 keeps it (the LM head's hidden norm).
+// Token slots >= m get zero tables.
 template <bool kNorm>
-__global__ void __launch_bounds__(1024) k_block_limbs(const float* X, const float* gamma, float eps, uint32_t C,
-                                                       uint32_t m, BlockTables t) {
-  const uint32_t tok = blockIdx.x, T = tok >> 2, tl = tok & 3u, ng = C >> 7;
+__global__ void __launch_bounds__(128) k_block_limbs(const float* X, const float* gamma, float eps, uint32_t C,
+                                                      uint32_t m, const float* ssp, uint32_t n_ssp, BlockTables t) {
+  const uint32_t tok = blockIdx.y, T = tok >> 2, tl = tok & 3u, ng = C >> 7;
   const bool live = tok < m;
   const float* x = X + size_t(live ? tok : 0u) * C;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  __shared__ float s_red[16];
+  const uint32_t c0 = blockIdx.x * 1024 + 8 * uint32_t(tid);
+  const bool in = c0 < ng * 128;
+  const uint32_t cc = in ? c0 : 0u;
+  // every load first
+  const float4 xa = ld_f4(x + cc), xb = ld_f4(x + cc + 4);
+  float4 ga = make_float4(1.f, 1.f, 1.f, 1.f), gb = ga;
   float ss = 0.0f;
-  for (uint32_t c = uint32_t(tid); c < C; c += 1024) {
-    const float v = x[c];
-    ss = fmaf(v, v, ss);
+  if constexpr (kNorm) {
+    ga = ld_f4(gamma + cc);
+    gb = ld_f4(gamma + cc + 4);
+    if (live) {
+#pragma unroll 4
+      for (uint32_t i = uint32_t(tid); i < n_ssp; i += 128) ss += ssp[size_t(i) * kMaxBlock + tok];
+    }
   }
-  ss = wave_sum(ss);
-  if (lane == 0) s_red[wave] = ss;
-  __syncthreads();
-  float tot = 0.0f;
+  float inv = 1.0f;
+  if constexpr (kNorm) {
+    __shared__ float s_red[2];
+    ss = wave_sum(ss);
+    if (lane == 0) s_red[wave] = ss;
+    __syncthreads();
+    const float tot = s_red[0] + s_red[1];
+    if (blockIdx.x == 0 && tid == 0) t.ss[tok] = live ? tot : 0.0f;
+    inv = 1.0f / sqrtf(tot / float(C) + eps);
+  }
+  float xv[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+  if constexpr (kNorm) {
+    const float gv[8] = {ga.x, ga.y, ga.z, ga.w, gb.x, gb.y, gb.z, gb.w};
 #pragma unroll
-  for (int w = 0; w < 16; ++w) tot += s_red[w];
-  if (tid == 0) t.ss[tok] = live ? tot : 0.0f;
-  const float inv = kNorm ? 1.0f / sqrtf(tot / float(C) + eps) : 1.0f;
+    for (int i = 0; i < 8; ++i) xv[i] = (xv[i] * inv) * gv[i];
+  }
+  float mx = 0.0f;  // (a NaN counts as infinite: the group's scale becomes NaN, as its sum would)
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    xv[i] = (live && in) ? xv[i] : 0.0f;
+    const float ax = fabsf(xv[i]);
+    mx = ax != ax ? __int_as_float(0x7f800000) : fmaxf(mx, ax);
+  }
+  mx = pair_max(mx, 1);
+  mx = pair_max(mx, 2);
+  mx = pair_max(mx, 4);
+  mx = pair_max(mx, 8);
+  int e = 0;
+  (void)frexpf(mx, &e);  // mx < 2^e (mx = 0: e = 0)
+  const float up = ldexpf(1.0f, 30 - e);
+  uint32_t z[8];  // bytes: the balanced limbs of X
+#pragma unroll
+  for (int i = 0; i < 8; ++i) z[i] = (uint32_t(int(xv[i] * up)) + 0x808080u) ^ 0x808080u;
+  uint32_t lo[4], hi[4];
+  limb_words(z[0], z[2], z[4], z[6], lo);
+  limb_words(z[1], z[3], z[5], z[7], hi);
+  const uint32_t g = cc >> 7, c = cc & 127u, kq = c >> 5, h = (c >> 4) & 1u, p = (c >> 3) & 1u;
   uint2* tb2 = reinterpret_cast<uint2*>(t.tb);
-  const uint32_t passes = (ng * 128 + 8 * 1024 - 1) / (8 * 1024);
-  for (uint32_t ps = 0; ps < passes; ++ps) {  // the same trip count on every lane (DPP below)
-    const uint32_t c0 = 8 * (uint32_t(tid) + 1024 * ps);
-    const bool in = c0 < ng * 128;
-    const uint32_t cc = in ? c0 : 0u;
-    const float4 xa = ld_f4(x + cc), xb = ld_f4(x + cc + 4);
-    float xv[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
-    if constexpr (kNorm) {
-      const float4 ga = ld_f4(gamma + cc), gb = ld_f4(gamma + cc + 4);
-      const float gv[8] = {ga.x, ga.y, ga.z, ga.w, gb.x, gb.y, gb.z, gb.w};
+  int sums[4];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) xv[i] = (xv[i] * inv) * gv[i];
-    }
-    float mx = 0.0f;
+  for (int L = 0; L < 4; ++L) {
+    if (in)
+      tb2[((((size_t(T) * ng + g) * 4 + kq) * 2 + h) * 16 + (4 * tl + uint32_t(L))) * 2 + p] = make_uint2(lo[L], hi[L]);
+    int sl = __builtin_amdgcn_sdot4(int(lo[L]), 0x01010101, __builtin_amdgcn_sdot4(int(hi[L]), 0x01010101, 0, false), false);
+    sl += int(pair_u(uint32_t(sl), 1));
+    sl += int(pair_u(uint32_t(sl), 2));
+    sl += int(pair_u(uint32_t(sl), 4));
+    sl += int(pair_u(uint32_t(sl), 8));
+    sums[L] = sl;
+  }
+  if (in && c == 0) {
+    t.ci[(size_t(T) * ng + g) * 4 + tl] = make_int4(-8 * sums[0], -8 * sums[1], -8 * sums[2], -8 * sums[3]);
+    t.ew[(size_t(T) * ng + g) * 4 + tl] = isfinite(mx) ? ldexpf(1.0f, e - 30) : __int_as_float(0x7fc00000);
+  }
+  if (in && live) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      xv[i] = (live && in) ? xv[i] : 0.0f;
-      mx = fmaxf(mx, fabsf(xv[i]));
-    }
-    mx = pair_max(mx, 1);
-    mx = pair_max(mx, 2);
-    mx = pair_max(mx, 4);
-    mx = pair_max(mx, 8);
-    int e = 0;
-    (void)frexpf(mx, &e);  // mx < 2^e (mx = 0: e = 0)
-    const float up = ldexpf(1.0f, 30 - e);
-    uint32_t z[8];  // bytes: the balanced limbs of X
-#pragma unroll
-    for (int i = 0; i < 8; ++i) z[i] = (uint32_t(int(xv[i] * up)) + 0x808080u) ^ 0x808080u;
-    uint32_t lo[4], hi[4];
-    limb_words(z[0], z[2], z[4], z[6], lo);
-    limb_words(z[1], z[3], z[5], z[7], hi);
-    const uint32_t g = cc >> 7, c = cc & 127u, kq = c >> 5, h = (c >> 4) & 1u, p = (c >> 3) & 1u;
-    int sums[4];
-#pragma unroll
-    for (int L = 0; L < 4; ++L) {
-      if (in)
-        tb2[((((size_t(T) * ng + g) * 4 + kq) * 2 + h) * 16 + (4 * tl + uint32_t(L))) * 2 + p] = make_uint2(lo[L], hi[L]);
-      int sl = __builtin_amdgcn_sdot4(int(lo[L]), 0x01010101, __builtin_amdgcn_sdot4(int(hi[L]), 0x01010101, 0, false), false);
-      sl += int(pair_u(uint32_t(sl), 1));
-      sl += int(pair_u(uint32_t(sl), 2));
-      sl += int(pair_u(uint32_t(sl), 4));
-      sl += int(pair_u(uint32_t(sl), 8));
-      sums[L] = sl;
-    }
-    if (in && c == 0) {
-      t.ci[(size_t(T) * ng + g) * 4 + tl] = make_int4(-8 * sums[0], -8 * sums[1], -8 * sums[2], -8 * sums[3]);
-      t.ew[(size_t(T) * ng + g) * 4 + tl] = isfinite(mx) ? ldexpf(1.0f, e - 30) : __int_as_float(0x7fc00000);
-    }
-    if (in) {
-#pragma unroll
-      for (int i = 0; i < 8; ++i) t.xt[size_t(cc + uint32_t(i)) * kMaxBlock + tok] = xv[i];
-    }
+    for (int i = 0; i < 8; ++i) t.xt[size_t(cc + uint32_t(i)) * kMaxBlock + tok] = xv[i];
   }
 }
 
-struct MtItem {
-  uint4 q[4];      // codes of row n, groups 4 S .. 4 S + 3 of the range, quarter q
-  uint32_t s[4];   // their group scales
+// A stage: 16 weight rows x 8 groups of the range (8 KB of codes), loaded 512 contiguous bytes
+// of two rows per instruction (lane l: row 2 i + (l >> 5), group (l & 31) >> 2, quarter l & 3),
+// then written to the wave's LDS slot so that the matrix-core layout (lane (n, q): row n,
+// quarter q of a group) reads it back; rows at kStageRow bytes (16 B of padding: the 16 rows of
+// one read fall on distinct banks).
+constexpr uint32_t kStageRow = 528, kStageBytes = 16 * kStageRow;
+struct MtStage {
+  uint4 v[8];      // codes, in the load layout above
+  uint32_t sc[2];  // group scales: lane l, row 8 i + (l >> 3), group l & 7
 };
 
 template <int NQ, int NW>
@@ -118,11 +138,103 @@ __global__ void __launch_bounds__(kWave * NW) k_gemv_mt(BlockGemvArgs a) {
   __shared__ __align__(16) uint4 s_tb[NQ][16][128];
   __shared__ __align__(16) int4 s_ci[NQ][16][4];
   __shared__ float s_ew[NQ][16][4];
+  __shared__ __align__(16) uint8_t s_w[NW][kStageBytes];
+  __shared__ uint16_t s_sc[NW][16][8];
   const int lane = threadIdx.x & 63, n = lane & 15, q = lane >> 4;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const uint32_t C = a.g.C, ng = C >> 7, range = blockIdx.x, g0 = range * 16;
   const uint32_t ngr = ng - g0 < 16u ? ng - g0 : 16u;
-  // the range's operands (zero past the input)
+  const uint32_t n_units = a.n_units, waves_total = gridDim.y * NW;
+  const uint32_t wid = blockIdx.y * NW + wave;
+  const bool active = wid < n_units;
+  const uint32_t n_stages = active ? 2 * ((n_units - wid + waves_total - 1) / waves_total) : 0u;
+  uint8_t* slot = s_w[wave];
+  // the unit's part: parts hold consecutive unit ranges from part[p].unit_begin
+  auto part_index = [&](uint32_t u) {
+    int p = 0;
+#pragma unroll
+    for (int k = 1; k < kMaxParts; ++k) p += (k < a.g.n_parts && u >= a.g.part[k].unit_begin) ? 1 : 0;
+    return p;
+  };
+  // stage j of this wave: unit wid + (j >> 1) * waves_total, groups 8 (j & 1) .. + 7 of the range
+  // (a stage past the last repeats the last: its lines are cached)
+  auto issue = [&](uint32_t j, MtStage* st) {
+    j = j < n_stages ? j : n_stages - 1;
+    const uint32_t u = wid + (j >> 1) * waves_total, h = j & 1u;
+    const int p = int(__builtin_amdgcn_readfirstlane(part_index(u)));
+    const GemvPart& P = a.g.part[p];
+    const uint8_t* base = P.base;
+    const uint32_t stride = P.stride, wr = P.wrows, r0 = (u - P.unit_begin) * kBlockUnit;
+    const uint32_t gl = 8 * h + ((uint32_t(lane) & 31u) >> 2), gc = gl < ngr ? gl : 0u;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const uint32_t r = r0 + 2 * uint32_t(i) + (uint32_t(lane) >> 5), rr = r < wr ? r : 0u;
+      const uint32_t G = rr * ng + g0 + gc;
+      st->v[i] = ld_u128(base + ((G >> 8) * stride + 64 + (G & 255u) * 64 + 16 * (uint32_t(lane) & 3u)));
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const uint32_t r = r0 + 8 * uint32_t(i) + (uint32_t(lane) >> 3), rr = r < wr ? r : 0u;
+      const uint32_t g = 8 * h + (uint32_t(lane) & 7u), G = rr * ng + g0 + (g < ngr ? g : 0u);
+      st->sc[i] = ld_u16(base + ((G >> 8) * stride + 16448 + 48 + 2 * (G & 255u)));
+    }
+  };
+  // into the wave's slot (LDS operations of one wave complete in order: the previous stage's
+  // reads are done before these writes land)
+  auto stage = [&](const MtStage& st) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      *reinterpret_cast<uint4*>(slot + (2 * i + (lane >> 5)) * kStageRow + 16 * (lane & 31)) = st.v[i];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) s_sc[wave][8 * i + (lane >> 3)][lane & 7] = uint16_t(st.sc[i]);
+  };
+  float acc[NQ];
+#pragma unroll
+  for (int T = 0; T < NQ; ++T) acc[T] = 0.0f;
+  auto compute = [&](uint32_t j) {
+    const uint32_t h = j & 1u;
+#pragma unroll 4
+    for (int k = 0; k < 8; ++k) {
+      const uint32_t gl = 8 * h + uint32_t(k);
+      const bool gv = gl < ngr;
+      const uint32_t gk = gv ? gl : 0u;
+      const uint4 w = *reinterpret_cast<const uint4*>(slot + n * kStageRow + 64 * k + 16 * q);
+      const float sc = gv ? h2f(s_sc[wave][n][k]) : 0.0f;
+      const i32x4_t B0 = {int(w.x & 0x0f0f0f0fu), int((w.x >> 4) & 0x0f0f0f0fu), int(w.y & 0x0f0f0f0fu),
+                          int((w.y >> 4) & 0x0f0f0f0fu)};
+      const i32x4_t B1 = {int(w.z & 0x0f0f0f0fu), int((w.z >> 4) & 0x0f0f0f0fu), int(w.w & 0x0f0f0f0fu),
+                          int((w.w >> 4) & 0x0f0f0f0fu)};
+#pragma unroll
+      for (int T = 0; T < NQ; ++T) {
+        const uint4 t0 = s_tb[T][gk][(uint32_t(q) * 2) * 16 + uint32_t(n)];
+        const uint4 t1 = s_tb[T][gk][(uint32_t(q) * 2 + 1) * 16 + uint32_t(n)];
+        const i32x4_t A0 = {int(t0.x), int(t0.y), int(t0.z), int(t0.w)};
+        const i32x4_t A1 = {int(t1.x), int(t1.y), int(t1.z), int(t1.w)};
+        const int4 c4 = s_ci[T][gk][q];
+        i32x4_t D = {c4.x, c4.y, c4.z, c4.w};
+        D = __builtin_amdgcn_mfma_i32_16x16x64_i8(A0, B0, D, 0, 0, 0);
+        D = __builtin_amdgcn_mfma_i32_16x16x64_i8(A1, B1, D, 0, 0, 0);
+        const float f = ((float(D[0]) + float(D[1]) * 256.0f) + float(D[2]) * 65536.0f) + float(D[3]) * 16777216.0f;
+        acc[T] += gv ? f * s_ew[T][gk][q] * sc : 0.0f;
+      }
+    }
+    if (h == 1u) {  // the unit's second stage: row n of tokens 4 T + q
+      const uint32_t u = wid + (j >> 1) * waves_total;
+      const int p = int(__builtin_amdgcn_readfirstlane(part_index(u)));
+      const GemvPart& P = a.g.part[p];
+      const uint32_t r = (u - P.unit_begin) * kBlockUnit + uint32_t(n), at = P.unit_begin * kBlockUnit + r;
+#pragma unroll
+      for (int T = 0; T < NQ; ++T) {
+        const uint32_t tk = 4 * uint32_t(T) + uint32_t(q);
+        if (tk < a.m) a.partial[(size_t(range) * a.rows_all + at) * kMaxBlock + tk] = r < P.wrows ? acc[T] : 0.0f;
+        acc[T] = 0.0f;
+      }
+    }
+  };
+  // the first stage's loads are in flight while the range's operand tables are staged, the next
+  // stage's while the current stage is staged and multiplied
+  MtStage SA, SB;
+  if (active) issue(0, &SA);
   for (uint32_t i = threadIdx.x; i < uint32_t(NQ) * 16 * 128; i += kWave * NW) {
     const uint32_t T = i >> 11, gl = (i >> 7) & 15u, e = i & 127u;
     s_tb[T][gl][e] = gl < ngr ? a.t.tb[(size_t(T) * ng + g0 + gl) * 128 + e] : make_uint4(0, 0, 0, 0);
@@ -134,92 +246,16 @@ __global__ void __launch_bounds__(kWave * NW) k_gemv_mt(BlockGemvArgs a) {
     s_ew[T][gl][k] = ok ? a.t.ew[(size_t(T) * ng + g0 + gl) * 4 + k] : 0.0f;
   }
   __syncthreads();
-
-  const uint32_t n_units = a.n_units, waves_total = gridDim.y * NW;
-  const uint32_t wid = blockIdx.y * NW + wave;
-  if (wid >= n_units) return;  // (no barrier follows)
-  // the unit's part: parts hold consecutive unit ranges from part[p].unit_begin
-  auto part_index = [&](uint32_t u) {
-    int p = 0;
-#pragma unroll
-    for (int k = 1; k < kMaxParts; ++k) p += (k < a.g.n_parts && u >= a.g.part[k].unit_begin) ? 1 : 0;
-    return p;
-  };
-  auto issue = [&](uint32_t u, uint32_t S, MtItem* it) {
-    const int p = int(__builtin_amdgcn_readfirstlane(part_index(u)));
-    const GemvPart& P = a.g.part[p];
-    const uint8_t* base = P.base;
-    const uint32_t stride = P.stride, wr = P.wrows;
-    const uint32_t r = (u - P.unit_begin) * 16 + uint32_t(n), rr = r < wr ? r : 0u;
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      const uint32_t k = 4 * S + uint32_t(s);
-      const uint32_t G = rr * ng + g0 + (k < ngr ? k : 0u);
-      const uint32_t off = (G >> 8) * stride;
-      it->q[s] = ld_u128(base + (off + 64 + (G & 255u) * 64 + 16 * uint32_t(q)));
-      it->s[s] = ld_u16(base + (off + 16448 + 48 + 2 * (G & 255u)));
-    }
-  };
-  float acc[NQ];
-#pragma unroll
-  for (int T = 0; T < NQ; ++T) acc[T] = 0.0f;
-  auto compute = [&](uint32_t u, uint32_t S, const MtItem& it) {
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      const uint32_t k = 4 * S + uint32_t(s);
-      const bool gv = k < ngr;
-      const uint32_t kk = gv ? k : 0u;
-      const uint32_t w4[4] = {it.q[s].x, it.q[s].y, it.q[s].z, it.q[s].w};
-      const float sc = h2f(uint16_t(it.s[s]));
-#pragma unroll
-      for (int T = 0; T < NQ; ++T) {
-        const int4 c4 = s_ci[T][kk][q];
-        i32x4_t D = {c4.x, c4.y, c4.z, c4.w};
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          const uint4 t = s_tb[T][kk][(uint32_t(q) * 2 + uint32_t(h)) * 16 + uint32_t(n)];
-          const i32x4_t A = {int(t.x), int(t.y), int(t.z), int(t.w)};
-          const uint32_t w0 = w4[2 * h], w1 = w4[2 * h + 1];
-          const i32x4_t B = {int(w0 & 0x0f0f0f0fu), int((w0 >> 4) & 0x0f0f0f0fu), int(w1 & 0x0f0f0f0fu),
-                             int((w1 >> 4) & 0x0f0f0f0fu)};
-          D = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, B, D, 0, 0, 0);
-        }
-        const float f = ((float(D[0]) + float(D[1]) * 256.0f) + float(D[2]) * 65536.0f) + float(D[3]) * 16777216.0f;
-        const float v = f * s_ew[T][kk][q] * sc;
-        acc[T] += gv ? v : 0.0f;
-      }
-    }
-    if (S == 3) {  // the unit's last set: row n of tokens 4 T + q
-      const int p = int(__builtin_amdgcn_readfirstlane(part_index(u)));
-      const GemvPart& P = a.g.part[p];
-      const uint32_t r = (u - P.unit_begin) * 16 + uint32_t(n);
-      const uint32_t at = P.unit_begin * 16 + (u - P.unit_begin) * 16 + uint32_t(n);
-#pragma unroll
-      for (int T = 0; T < NQ; ++T) {
-        const uint32_t tk = 4 * uint32_t(T) + uint32_t(q);
-        if (tk < a.m) a.partial[(size_t(range) * kMaxBlock + tk) * a.rows_all + at] = r < P.wrows ? acc[T] : 0.0f;
-        acc[T] = 0.0f;
-      }
-    }
-  };
-  // items (unit, set of 4 groups); the next item's loads before the current item's products (a
-  // repeat of the last item past the end: its lines are cached)
-  uint32_t u0 = wid, S0 = 0;
-  MtItem IA, IB;
-  issue(u0, S0, &IA);
-  while (true) {
-    const uint32_t u1 = S0 < 3 ? u0 : u0 + waves_total, S1 = S0 < 3 ? S0 + 1 : 0u;
-    const bool v1 = u1 < n_units;
-    issue(v1 ? u1 : u0, v1 ? S1 : S0, &IB);
-    compute(u0, S0, IA);
-    if (!v1) break;
-    const uint32_t u2 = S1 < 3 ? u1 : u1 + waves_total, S2 = S1 < 3 ? S1 + 1 : 0u;
-    const bool v2 = u2 < n_units;
-    issue(v2 ? u2 : u1, v2 ? S2 : S1, &IA);
-    compute(u1, S1, IB);
-    if (!v2) break;
-    u0 = u2;
-    S0 = S2;
+  if (!active) return;  // (no barrier follows)
+  for (uint32_t j = 0;; j += 2) {
+    stage(SA);
+    issue(j + 1, &SB);
+    compute(j);
+    if (j + 1 >= n_stages) break;
+    stage(SB);
+    issue(j + 2, &SA);
+    compute(j + 1);
+    if (j + 2 >= n_stages) break;
   }
 }
 
@@ -244,6 +280,7 @@ __global__ void __launch_bounds__(256) k_block_epi(BlockGemvArgs a) {
   }
   float bv = -1e30f;
   uint32_t bi = 0xffffffffu, nf = 0;
+  float sq = 0.0f;  // Accum: this lane's sum of y^2 over its token's updated rows
   const uint32_t pos0 = kRope ? a.state->pos : 0u;
   for (uint32_t q4 = blockIdx.x * 4 + uint32_t(wave); q4 * 4 < total; q4 += gridDim.x * 4) {
     const uint32_t o = q4 * 4 + uint32_t(i);
@@ -264,6 +301,18 @@ __global__ void __launch_bounds__(256) k_block_epi(BlockGemvArgs a) {
       rows_k[0] = ok ? o : 0u;
       if constexpr (kSwi) rows_k[1] = rows_k[0];
     }
+    // the ranges' raw sums of token t = e0 of each row (requested before the corrections)
+    const uint32_t t = uint32_t(e0);
+    float sum_k[NR];
+#pragma unroll
+    for (int k = 0; k < NR; ++k) {
+      const GemvPart& P = a.g.part[kSwi ? k : p];
+      const uint32_t at = P.unit_begin * kBlockUnit + rows_k[k];
+      float acc_s = 0.0f;
+      if (ok && t < m)
+        for (uint32_t rg = 0; rg < ranges; ++rg) acc_s += a.partial[(size_t(rg) * a.rows_all + at) * kMaxBlock + t];
+      sum_k[k] = acc_s;
+    }
     // corrections of each row, all tokens
     float cor[NR][kMaxBlock];
 #pragma unroll
@@ -275,19 +324,24 @@ __global__ void __launch_bounds__(256) k_block_epi(BlockGemvArgs a) {
 #pragma unroll
       for (int t = 0; t < int(kMaxBlock); ++t) cor[k][t] = 0.0f;
       if (corr != nullptr && ok && r < P.wrows) {
-        for (uint32_t e = uint32_t(e0); e < kmax; e += 16) {
-          const float2 ce = corr[size_t(r) * kmax + e];
-          if (ce.y == 0.0f) continue;
-          const float4* xr = reinterpret_cast<const float4*>(a.t.xt + size_t(__float_as_uint(ce.x)) * kMaxBlock);
-          const float4 xa = xr[0], xb = xr[1];
-          cor[k][0] = fmaf(ce.y, xa.x, cor[k][0]);
-          cor[k][1] = fmaf(ce.y, xa.y, cor[k][1]);
-          cor[k][2] = fmaf(ce.y, xa.z, cor[k][2]);
-          cor[k][3] = fmaf(ce.y, xa.w, cor[k][3]);
-          cor[k][4] = fmaf(ce.y, xb.x, cor[k][4]);
-          cor[k][5] = fmaf(ce.y, xb.y, cor[k][5]);
-          cor[k][6] = fmaf(ce.y, xb.z, cor[k][6]);
-          cor[k][7] = fmaf(ce.y, xb.w, cor[k][7]);
+        // two entries per trip, their loads together (unused slots read entry 0, masked)
+        for (uint32_t e = uint32_t(e0); e < kmax; e += 32) {
+          const bool u1 = e + 16 < kmax;
+          const float2 c0 = corr[size_t(r) * kmax + e];
+          const float2 c1 = corr[size_t(r) * kmax + (u1 ? e + 16 : e)];
+          const float w0 = c0.y, w1 = u1 ? c1.y : 0.0f;
+          const float4* x0 = reinterpret_cast<const float4*>(a.t.xt + size_t(__float_as_uint(c0.x)) * kMaxBlock);
+          const float4* x1 = reinterpret_cast<const float4*>(a.t.xt + size_t(__float_as_uint(c1.x)) * kMaxBlock);
+          const float4 xa = x0[0], xb = x0[1], ya = x1[0], yb = x1[1];
+          const float xs0[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+          const float xs1[8] = {ya.x, ya.y, ya.z, ya.w, yb.x, yb.y, yb.z, yb.w};
+#pragma unroll
+          for (int tt = 0; tt < int(kMaxBlock); ++tt) {  // padding entries (w = 0) are skipped
+            float c = cor[k][tt];
+            c = w0 != 0.0f ? fmaf(w0, xs0[tt], c) : c;
+            c = w1 != 0.0f ? fmaf(w1, xs1[tt], c) : c;
+            cor[k][tt] = c;
+          }
         }
       }
 #pragma unroll
@@ -301,19 +355,14 @@ __global__ void __launch_bounds__(256) k_block_epi(BlockGemvArgs a) {
       }
     }
     // lane (i, t): token t of the output
-    const uint32_t t = uint32_t(e0);
     if (!ok || t >= m) continue;
     float v[NR];
 #pragma unroll
     for (int k = 0; k < NR; ++k) {
-      const GemvPart& P = a.g.part[kSwi ? k : p];
-      const uint32_t at = P.unit_begin * 16 + rows_k[k];
-      float s = 0.0f;
-      for (uint32_t rg = 0; rg < ranges; ++rg) s += a.partial[(size_t(rg) * kMaxBlock + t) * a.rows_all + at];
       float c = cor[k][0];
 #pragma unroll
       for (int tt = 1; tt < int(kMaxBlock); ++tt) c = t == uint32_t(tt) ? cor[k][tt] : c;
-      v[k] = s + c;
+      v[k] = sum_k[k] + c;
     }
     const GemvPart& P0 = a.g.part[kSwi ? 0 : p];
     const uint32_t r = rows_k[0];
@@ -321,7 +370,9 @@ __global__ void __launch_bounds__(256) k_block_epi(BlockGemvArgs a) {
     if constexpr (MODE == int(GemvMode::Store)) {
       y[r] = v[0] + (P0.bias ? P0.bias[r] : 0.0f);
     } else if constexpr (MODE == int(GemvMode::Accum)) {
-      if (r < P0.wrows) y[r] = y[r] + v[0];  // rows past the tiles stay
+      const float yo = y[r], yn = r < P0.wrows ? yo + v[0] : yo;  // rows past the tiles stay
+      if (r < P0.wrows) y[r] = yn;
+      sq = fmaf(yn, yn, sq);
     } else if constexpr (kSwi) {
       y[r] = v[0] / (1.0f + expf(-v[0])) * v[1];  // silu(g)*u: :159-161, :1746-1748
     } else if constexpr (kRope) {
@@ -399,6 +450,21 @@ __global__ void __launch_bounds__(256) k_block_epi(BlockGemvArgs a) {
       a.partials[size_t(tk) * a.epi_blocks + blockIdx.x] = ArgmaxPartial{b, bx, f, 0u};
     }
   }
+  if constexpr (MODE == int(GemvMode::Accum)) {
+    // the workgroup's sums of y^2 per token for the next GEMV's RMS norm (lanes e0 = t of the 4
+    // outputs, then over the waves, in a fixed order)
+    if (a.ssp_out) {
+      float v = pair_sum(sq, 16);
+      v = pair_sum(v, 32);
+      __shared__ float s_sq[4][16];
+      if (lane < 16) s_sq[wave][lane] = v;
+      __syncthreads();
+      if (threadIdx.x < kMaxBlock) {
+        const uint32_t tk = threadIdx.x;
+        a.ssp_out[size_t(blockIdx.x) * kMaxBlock + tk] = (s_sq[0][tk] + s_sq[1][tk]) + (s_sq[2][tk] + s_sq[3][tk]);
+      }
+    }
+  }
 }
 
 __global__ void __launch_bounds__(256) k_block_finish(BlockFinishArgs a) {
@@ -455,18 +521,20 @@ __global__ void __launch_bounds__(256) k_block_finish(BlockFinishArgs a) {
 
 }  // namespace
 
-void launch_block_limbs(const float* x, const float* gamma, float eps, uint32_t C, uint32_t m, const BlockTables& t,
-                        hipStream_t st) {
-  const uint32_t nq = (m + 3) / 4;
-  if (gamma) launch_kernel(&k_block_limbs<true>, dim3(4 * nq), dim3(1024), st, x, gamma, eps, C, m, t);
-  else launch_kernel(&k_block_limbs<false>, dim3(4 * nq), dim3(1024), st, x, gamma, eps, C, m, t);
+void launch_block_limbs(const BlockGemvArgs& a, hipStream_t st) {
+  const dim3 grid((a.g.C + 1023) / 1024, 4 * a.nq);
+  if (a.g.gamma)
+    launch_kernel(&k_block_limbs<true>, grid, dim3(128), st, a.g.x, a.g.gamma, a.g.eps, a.g.C, a.m, a.ssp, a.n_ssp, a.t);
+  else
+    launch_kernel(&k_block_limbs<false>, grid, dim3(128), st, a.g.x, a.g.gamma, a.g.eps, a.g.C, a.m, a.ssp, a.n_ssp, a.t);
 }
 
 uint32_t launch_block_gemv(BlockGemvArgs& a, hipStream_t st) {
   const uint32_t ranges = (a.g.C + kBlockRange - 1) / kBlockRange;
-  // workgroups per range: about 512 workgroups of 8 waves in all (two per CU: the LDS tables)
-  uint32_t per = (512 + ranges - 1) / ranges;
-  const uint32_t need = (a.n_units + 7) / 8;
+  // workgroups per range: about 256 workgroups of 8 waves in all (one per CU: the LDS tables and
+  // stage slots)
+  uint32_t per = (256 + ranges - 1) / ranges;
+  const uint32_t need = (a.n_units + 7) / 8;  // (a wave per unit at least)
   if (per > need) per = need;
   if (per == 0) per = 1;
   const dim3 grid(ranges, per);
@@ -478,8 +546,8 @@ uint32_t launch_block_gemv(BlockGemvArgs& a, hipStream_t st) {
   } else {
     outs = a.g.part[0].rows;
   }
-  uint32_t eb = (outs + 15) / 16;
-  if (eb > 1024) eb = 1024;
+  uint32_t eb = (outs + 15) / 16;  // one pass: 16 outputs per workgroup
+  if (eb > kMaxSsPartials) eb = kMaxSsPartials;  // (Accum leaves a Σy² partial per workgroup)
   if (GemvMode(a.g.mode) == GemvMode::Logits && eb > 512) eb = 512;
   a.epi_blocks = eb;
   switch (GemvMode(a.g.mode)) {

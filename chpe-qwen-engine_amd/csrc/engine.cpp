@@ -844,7 +844,8 @@ int Engine::generate(const uint32_t* prompt, size_t n_prompt, size_t n_gen, uint
 int Engine::verify(const uint32_t* drafts, size_t m, size_t pos, uint32_t* out_argmax, ForwardResult* last) {
   if (!drafts || m == 0 || !out_argmax) return -1;
   if (pos + m > cfg_.max_seq_len) return -2;
-  if (block_ok_ && m <= kMaxBlock) {  // every weight read once for the m drafts
+  if (block_ok_ && m >= 2 && m <= kMaxBlock) {  // every weight read once for the m drafts (one
+                                                  // draft: the batch-1 step's kernels are faster)
     ForwardResult r{};
     const int rc = block_forward(drafts, m, pos, out_argmax, &r);
     if (rc) return rc;
@@ -877,14 +878,14 @@ bool Engine::plan_block(std::string* err) {
     if (!flat(L.q) || !flat(L.k) || !flat(L.v) || !flat(L.o) || !flat(L.gate) || !flat(L.up) || !flat(L.down))
       return false;
   if (!flat(lm_head_) || D % 128 || I % 128 || qd % 128) return false;
-  auto units = [](size_t rows) { return (rows + 15) / 16; };
+  auto units = [](size_t rows) { return (rows + kBlockUnit - 1) / kBlockUnit; };
   auto ranges = [](size_t C) { return (C + kBlockRange - 1) / kBlockRange; };
   size_t part_floats = 0;  // ranges x kMaxBlock x rows_all, the largest GEMV
-  part_floats = std::max(part_floats, ranges(D) * 16 * (units(qd) + 2 * units(kvd)));
-  part_floats = std::max(part_floats, ranges(qd) * 16 * units(D));
-  part_floats = std::max(part_floats, ranges(D) * 16 * 2 * units(I));
-  part_floats = std::max(part_floats, ranges(I) * 16 * units(D));
-  part_floats = std::max(part_floats, ranges(D) * 16 * units(V));
+  part_floats = std::max(part_floats, ranges(D) * kBlockUnit * (units(qd) + 2 * units(kvd)));
+  part_floats = std::max(part_floats, ranges(qd) * kBlockUnit * units(D));
+  part_floats = std::max(part_floats, ranges(D) * kBlockUnit * 2 * units(I));
+  part_floats = std::max(part_floats, ranges(I) * kBlockUnit * units(D));
+  part_floats = std::max(part_floats, ranges(D) * kBlockUnit * units(V));
   part_floats *= kMaxBlock;
   const size_t Cmax = std::max({D, I, qd}), ngm = Cmax / 128, nq = (kMaxBlock + 3) / 4;
   const size_t hd = arch_.head_dim, H = arch_.num_attn_heads;
@@ -900,6 +901,7 @@ bool Engine::plan_block(std::string* err) {
   d_bpartial_ = fa(part_floats);
   d_bpml_ = fa(kMaxBlock * H * n_chunks_ * 2);
   d_bpacc_ = fa(kMaxBlock * H * n_chunks_ * hd);
+  d_bss_ = fa(size_t(kMaxSsPartials) * kMaxBlock);
   btab_.tb = static_cast<uint4*>(dev_alloc(nq * ngm * 128 * sizeof(uint4)));
   btab_.ci = static_cast<int4*>(dev_alloc(nq * ngm * 4 * sizeof(int4)));
   btab_.ew = fa(nq * ngm * 4);
@@ -907,7 +909,8 @@ bool Engine::plan_block(std::string* err) {
   btab_.ss = fa(kMaxBlock);
   d_bpartials_ = static_cast<ArgmaxPartial*>(dev_alloc(kMaxBlock * 512 * sizeof(ArgmaxPartial)));
   if (!d_btok_ || !d_bout_ || !d_bstate_ || !d_bx_ || !d_bq_ || !d_battn_ || !d_bmlp_ || !d_blog_ || !d_bpartial_ ||
-      !d_bpml_ || !d_bpacc_ || !btab_.tb || !btab_.ci || !btab_.ew || !btab_.xt || !btab_.ss || !d_bpartials_) {
+      !d_bpml_ || !d_bpacc_ || !d_bss_ || !btab_.tb || !btab_.ci || !btab_.ew || !btab_.xt || !btab_.ss ||
+      !d_bpartials_) {
     *err = "allocation";
     return false;
   }
@@ -922,8 +925,8 @@ bool Engine::plan_block(std::string* err) {
 }
 
 uint32_t Engine::enqueue_block_gemv(const ProjPlan* const* parts, float* const* outs, int n, GemvMode mode,
-                                    const float* x, uint32_t C, const float* gamma, uint32_t m, size_t layer,
-                                    hipStream_t st) {
+                                    const float* x, uint32_t C, const float* gamma, uint32_t n_ss, uint32_t m,
+                                    size_t layer, hipStream_t st) {
   BlockGemvArgs b{};
   b.g.n_parts = n;
   b.g.mode = int(mode);
@@ -946,13 +949,13 @@ uint32_t Engine::enqueue_block_gemv(const ProjPlan* const* parts, float* const* 
     gp.corr = p.corr;
     gp.corr_kmax = p.corr_kmax;
     gp.rope_role = mode == GemvMode::QkvRope ? roles[i] : 0u;
-    units += (p.rows + 15) / 16;
+    units += (p.rows + kBlockUnit - 1) / kBlockUnit;
   }
   b.t = btab_;
   b.m = m;
   b.nq = (m + 3) / 4;
   b.n_units = units;
-  b.rows_all = 16 * units;
+  b.rows_all = kBlockUnit * units;
   b.partial = d_bpartial_;
   if (mode == GemvMode::QkvRope) {
     b.g.rope = rope_args(layer);
@@ -962,7 +965,10 @@ uint32_t Engine::enqueue_block_gemv(const ProjPlan* const* parts, float* const* 
     b.rope_rows = uint32_t(cfg_.max_seq_len);
   }
   if (mode == GemvMode::Logits) b.partials = d_bpartials_;
-  launch_block_limbs(x, gamma, arch_.rms_eps, C, m, btab_, st);
+  b.ssp = d_bss_;
+  b.n_ssp = n_ss;
+  if (mode == GemvMode::Accum) b.ssp_out = d_bss_;  // (read by this GEMV's kernels: no gamma)
+  launch_block_limbs(b, st);
   return launch_block_gemv(b, st);
 }
 
@@ -1008,12 +1014,13 @@ int Engine::block_forward(const uint32_t* tokens, size_t m, size_t pos, uint32_t
 void Engine::record_block(uint32_t mm, hipStream_t st) {
   const uint32_t D = uint32_t(arch_.hidden_dim), I = uint32_t(arch_.intermediate_dim), V = uint32_t(arch_.vocab_size);
   const uint32_t qd = uint32_t(arch_.num_attn_heads * arch_.head_dim);
-  launch_block_embed(embed_args(), d_btok_, mm, d_bx_, st);
+  launch_block_embed(embed_args(), d_btok_, mm, d_bx_, d_bss_, st);
+  uint32_t n_ss = 1;  // Σx² partials of the hidden rows in d_bss_
   for (size_t l = 0; l < arch_.num_layers; ++l) {
     const LayerPlan& L = layers_[l];
     const ProjPlan* qkv[3] = {&L.q, &L.k, &L.v};
     float* qo[3] = {d_bq_, nullptr, nullptr};
-    enqueue_block_gemv(qkv, qo, 3, GemvMode::QkvRope, d_bx_, D, L.gamma_in, mm, l, st);
+    enqueue_block_gemv(qkv, qo, 3, GemvMode::QkvRope, d_bx_, D, L.gamma_in, n_ss, mm, l, st);
     AttnArgs at = attn_args(l);
     at.state = d_bstate_;
     at.q = d_bq_;
@@ -1024,16 +1031,16 @@ void Engine::record_block(uint32_t mm, hipStream_t st) {
     launch_attention(at, st);
     const ProjPlan* o[1] = {&L.o};
     float* hid[1] = {d_bx_};
-    enqueue_block_gemv(o, hid, 1, GemvMode::Accum, d_battn_, qd, nullptr, mm, l, st);
+    n_ss = enqueue_block_gemv(o, hid, 1, GemvMode::Accum, d_battn_, qd, nullptr, 0, mm, l, st);
     const ProjPlan* gu[2] = {&L.gate, &L.up};
     float* mlp[2] = {d_bmlp_, d_bmlp_};
-    enqueue_block_gemv(gu, mlp, 2, GemvMode::SwiGlu, d_bx_, D, L.gamma_post, mm, l, st);
+    enqueue_block_gemv(gu, mlp, 2, GemvMode::SwiGlu, d_bx_, D, L.gamma_post, n_ss, mm, l, st);
     const ProjPlan* dn[1] = {&L.down};
-    enqueue_block_gemv(dn, hid, 1, GemvMode::Accum, d_bmlp_, I, nullptr, mm, l, st);
+    n_ss = enqueue_block_gemv(dn, hid, 1, GemvMode::Accum, d_bmlp_, I, nullptr, 0, mm, l, st);
   }
   const ProjPlan* lm[1] = {&lm_head_};
   float* lg[1] = {d_blog_};
-  const uint32_t eb = enqueue_block_gemv(lm, lg, 1, GemvMode::Logits, d_bx_, D, d_gamma_final_, mm, 0, st);
+  const uint32_t eb = enqueue_block_gemv(lm, lg, 1, GemvMode::Logits, d_bx_, D, d_gamma_final_, n_ss, mm, 0, st);
   launch_block_finish(BlockFinishArgs{d_bpartials_, eb, mm, d_blog_, V, btab_.ss, d_bout_, d_result_}, st);
   (void)hipMemcpyAsync(d_logits_, d_blog_ + size_t(mm - 1) * V, size_t(V) * 4, hipMemcpyDeviceToDevice, st);
 }

@@ -164,9 +164,11 @@ class Engine {
   double proj_bytes(const ProjPlan& p) const;
   bool plan_block(std::string* err);
   void record_block(uint32_t m, hipStream_t st);  // the block step of m tokens after its inputs
+  // gamma set: the input's Σx² comes as n_ss partials in d_bss_; Accum leaves the updated rows'
+  // partials there and returns their count (as it returns the Logits partials' count)
   uint32_t enqueue_block_gemv(const ProjPlan* const* parts, float* const* outs, int n, GemvMode mode,
-                              const float* x, uint32_t C, const float* gamma, uint32_t m, size_t layer,
-                              hipStream_t st);
+                              const float* x, uint32_t C, const float* gamma, uint32_t n_ss, uint32_t m,
+                              size_t layer, hipStream_t st);
 
  public:
   // run one projection's GEMV on a caller vector (Store mode, bias included): parity hooks
@@ -221,6 +223,7 @@ class Engine {
   StepState *d_bstate_ = nullptr, *h_bstate_ = nullptr;
   float *d_bx_ = nullptr, *d_bq_ = nullptr, *d_battn_ = nullptr, *d_bmlp_ = nullptr, *d_blog_ = nullptr;
   float *d_bpartial_ = nullptr, *d_bpml_ = nullptr, *d_bpacc_ = nullptr;
+  float* d_bss_ = nullptr;  // [kMaxSsPartials][kMaxBlock]: Σx² partials of the hidden rows for the next norm
   BlockTables btab_{};
   ArgmaxPartial* d_bpartials_ = nullptr;
   hipGraph_t bgraph_[kMaxBlock + 1] = {};          // captured block steps, by token count

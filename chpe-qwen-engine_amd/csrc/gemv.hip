@@ -2575,9 +2575,10 @@ GemvLaunch gemv_geometry(WeightKind kind, GemvMode mode, uint32_t C, const uint3
       *n_panels = need;
       *waves_per_unit = nw;
       const GemvTuning& t = gemv_tuning();
-      const uint32_t wpc = nw >= 8 ? t.xm_wpc_wide
-                           : mode == GemvMode::Logits ? t.xm_wpc_logits
-                           : units >= 4096 ? t.xm_wpc_large : t.xm_wpc_small;
+      uint32_t wpc = nw >= 8 ? t.xm_wpc_wide
+                     : mode == GemvMode::Logits ? t.xm_wpc_logits
+                     : units >= 4096 ? t.xm_wpc_large : t.xm_wpc_small;
+      if (nw < 4) wpc *= 4 / nw;  // narrower inputs: as many waves per CU as at 8192 columns
       GemvLaunch g{};
       g.ru = R;
       g.xm = R;

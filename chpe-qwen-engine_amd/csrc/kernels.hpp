@@ -228,6 +228,9 @@ uint32_t launch_gemv_poly(const GemvArgs& a, const PolyPlan* const* plans, float
 // every weight read once for all m tokens (batch-M verify, chunked prefill) ----------------------
 constexpr uint32_t kMaxBlock = 8;
 constexpr uint32_t kBlockRange = 2048;  // input columns per workgroup of the block GEMV
+constexpr uint32_t kBlockUnit = 16;     // weight rows per unit of the block GEMV
+
+constexpr uint32_t kMaxSsPartials = 4096;  // Σx² partials a block kernel may leave for the next GEMV
 
 // One GEMV input of m tokens as matrix-core operands (k_block_limbs): per token and 128-column
 // group the input (RMS-normalised when gamma is set) as exact integers X = x * 2^(30-e), max
@@ -238,16 +241,21 @@ struct BlockTables {
   int4* ci;    // [nq][ng][4]: -8 * the group's limb sums (limbs 0..3) of token 4T + t
   float* ew;   // [nq][ng][4]: 2^(e - 30) of token 4T + t in the group
   float* xt;   // [C][kMaxBlock]: the (normalised) input, token-minor (for the outlier corrections)
-  float* ss;   // [kMaxBlock]: each token's sum of squares of the raw input
+  float* ss;   // [kMaxBlock]: each token's sum of squares of the raw input (norm GEMVs)
 };
 
+// The RMS norm's sum of squares comes as partial sums left by the kernel that wrote the input
+// rows (the embedding, an Accum epilogue): ssp[i][t], i < n_ssp, added in a fixed order.
 struct BlockGemvArgs {
   GemvArgs g;          // parts, mode, C; g.x = the raw input [m][C], g.gamma; rope: caches and head dim
   BlockTables t;
   uint32_t m, nq;
-  uint32_t n_units;    // 16-row units over the parts (unit_begin of part p in units)
-  uint32_t rows_all;   // 16 * n_units: rows of the partial-sum buffer
-  float* partial;      // [ranges][kMaxBlock][rows_all]: raw row sums per column range
+  uint32_t n_units;    // kBlockUnit-row units over the parts (unit_begin of part p in units)
+  uint32_t rows_all;   // kBlockUnit * n_units: rows of the partial-sum buffer
+  float* partial;      // [ranges][rows_all][kMaxBlock]: raw row sums per column range, token-minor
+  const float* ssp;    // [n_ssp][kMaxBlock]: partial sums of x^2 of the input rows (with g.gamma)
+  uint32_t n_ssp;
+  float* ssp_out;      // Accum: [epi_blocks][kMaxBlock] partial sums of y^2 of the updated rows
   const StepState* state;   // position of token 0 (QkvRope)
   const float* rope_cos;    // [rope_rows][head_dim/2] full tables
   const float* rope_sin;
@@ -266,10 +274,12 @@ struct BlockFinishArgs {
   StepResult* result;             // the last token's result
 };
 
-void launch_block_embed(const EmbedArgs& e, const uint32_t* tokens, uint32_t m, float* X, hipStream_t stream);
-void launch_block_limbs(const float* x, const float* gamma, float eps, uint32_t C, uint32_t m,
-                        const BlockTables& t, hipStream_t stream);
-// the block GEMV (k_gemv_mt) and its epilogue; returns the epilogue's workgroups (Logits partials)
+// embeds m tokens into X [m][D] and leaves each row's sum of squares in ssp[0][t]
+void launch_block_embed(const EmbedArgs& e, const uint32_t* tokens, uint32_t m, float* X, float* ssp,
+                        hipStream_t stream);
+// the input's operand tables (k_block_limbs), then the block GEMV (k_gemv_mt) and its epilogue;
+// launch_block_gemv returns the epilogue's workgroups (Logits / Σy² partials)
+void launch_block_limbs(const BlockGemvArgs& a, hipStream_t stream);
 uint32_t launch_block_gemv(BlockGemvArgs& a, hipStream_t stream);
 void launch_block_finish(const BlockFinishArgs& a, hipStream_t stream);
 

@@ -167,10 +167,20 @@ __global__ void __launch_bounds__(256) k_embed(EmbedArgs a) {
 }
 
 // the block step's inputs: token blockIdx.x's embedding row into X[blockIdx.x]
-__global__ void __launch_bounds__(256) k_block_embed(EmbedArgs a, const uint32_t* tokens, float* X) {
+// one workgroup per token; then the row's sum of squares (the first layer's RMS norm)
+__global__ void __launch_bounds__(256) k_block_embed(EmbedArgs a, const uint32_t* tokens, float* X, float* ssp) {
   EmbedArgs e = a;
-  e.hidden = X + size_t(blockIdx.x) * a.D;
+  float* row = X + size_t(blockIdx.x) * a.D;
+  e.hidden = row;
   embed_token(e, tokens[blockIdx.x]);
+  __syncthreads();  // the workgroup's row writes are visible to it
+  float ss = 0.0f;
+  for (uint32_t c = threadIdx.x; c < a.D; c += blockDim.x) ss = fmaf(row[c], row[c], ss);
+  ss = wave_sum(ss);
+  __shared__ float s_ss[4];
+  if ((threadIdx.x & 63) == 0) s_ss[threadIdx.x >> 6] = ss;
+  __syncthreads();
+  if (threadIdx.x == 0) ssp[blockIdx.x] = (s_ss[0] + s_ss[1]) + (s_ss[2] + s_ss[3]);
 }
 
 // argmax / all_finite / logits[0] over the LM head's workgroup partials (chpe_engine.zig:
@@ -302,8 +312,8 @@ void launch_embed(const EmbedArgs& a, hipStream_t st) {
   launch_kernel(k_embed, dim3(1), dim3(256), st, a);
 }
 
-void launch_block_embed(const EmbedArgs& e, const uint32_t* tokens, uint32_t m, float* X, hipStream_t st) {
-  launch_kernel(k_block_embed, dim3(m), dim3(256), st, e, tokens, X);
+void launch_block_embed(const EmbedArgs& e, const uint32_t* tokens, uint32_t m, float* X, float* ssp, hipStream_t st) {
+  launch_kernel(k_block_embed, dim3(m), dim3(256), st, e, tokens, X, ssp);
 }
 
 void launch_finish(const FinishArgs& a, hipStream_t st) {

@@ -70,7 +70,7 @@ int chpe_generate(void *ctx, const uint32_t *prompt, size_t n_prompt, size_t n_g
  * chpe_decode_step(ctx, drafts[i], pos + i) calls (the reference has no verify code; its
  * equivalent is m forwardDecode calls, src/chpe_engine.zig:1663-1803, whose KV write at pos
  * overwrites the row, :1693-1697): on archives of flat 4-bit tiles (chpe_block_ready) and
- * m <= 8 as one block step that reads every weight once for the m drafts, with each draft's
+ * 2 <= m <= 8 as one block step that reads every weight once for the m drafts, with each draft's
  * arithmetic that of the decode step up to the order of the float sums; otherwise m replays of
  * the decode step, bit-identical.  last_* report the final step; chpe_get_last_logits gives
  * its logits.  Returns 0, -1 bad args, -2 pos + m > max_seq_len, -3 device error. */
