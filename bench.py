@@ -48,13 +48,13 @@ STAGE_DESC = {
 }
 # per workload: archive kind (chpe_pack.h), architecture, prompt length, shapes
 WORKLOADS = {
-    "qwen72b-w4": dict(kind=5, arch=2, prompt=8192, V=152064, L=80, H=64, KV=8, hd=128,
+    "qwen72b-w4": dict(kind=5, arch=2, prompt=8192, V=152064, L=80, H=64, KV=8, hd=128, D=8192, I=29568,
                        desc="Qwen2.5-72B 4-bit GROUP128 flat tiles (dense 17408 B records)"),
-    "qwen72b-w2": dict(kind=6, arch=2, prompt=8192, V=152064, L=80, H=64, KV=8, hd=128,
+    "qwen72b-w2": dict(kind=6, arch=2, prompt=8192, V=152064, L=80, H=64, KV=8, hd=128, D=8192, I=29568,
                        desc="Qwen2.5-72B 2-bit GROUP128 flat tiles (dense 17408 B records)"),
-    "qwen3b-w4": dict(kind=2, arch=0, prompt=4096, V=151936, L=36, H=16, KV=2, hd=128,
+    "qwen3b-w4": dict(kind=2, arch=0, prompt=4096, V=151936, L=36, H=16, KV=2, hd=128, D=2048, I=11008,
                       desc="Qwen2.5-3B 4-bit GROUP128 cells (dense 17408 B records)"),
-    "qwen9b-w4": dict(kind=7, arch=1, prompt=2048, V=248320, L=32, H=16, KV=4, hd=256,
+    "qwen9b-w4": dict(kind=7, arch=1, prompt=2048, V=248320, L=32, H=16, KV=4, hd=256, D=4096, I=12288,
                       desc="Qwen3.5-9B 4-bit GROUP128 flat tiles at the INT8 map's indices, "
                            "reference-compatible GQA decode"),
 }
@@ -146,6 +146,28 @@ def copy_probe():
     print(json.dumps({"copy_probe_bytes_per_copy": n, "copies": 4}), flush=True)
 
 
+def gemv_probe(workload):
+    """Only the workload's gate/up GEMV (stage 2: RMSNorm, both projections, SwiGLU) on synthetic
+    flat tiles of its shape, 4 launches through the engine's kernel choice for that shape
+    (chpe_debug_gemv_flat): the rocprofv3 --pmc traffic runs of the dominant kernel."""
+    import chpe_amd as ca
+    w = WORKLOADS[workload]
+    if w["kind"] not in (5, 6, 7):
+        raise SystemExit(f"--gemv-probe: {workload} has no flat-tile gate/up projection")
+    bits = 2 if w["kind"] == 6 else 4
+    D, I = w["D"], w["I"]
+    rng = np.random.default_rng(0)
+    tile = ca.pack_flat((rng.standard_normal(32768) * 0.02).astype(np.float32), bits=bits)
+    n = (I * D + 32767) // 32768
+    gate = np.tile(tile, n)
+    up = gate.copy()
+    x = rng.standard_normal(D).astype(np.float32)
+    g = np.ones(D, np.float32)
+    for _ in range(4):
+        ca.gpu_gemv_flat("swiglu", I, D, gate, x, tiles_up=up, gamma=g)
+    print(json.dumps({"gemv_probe": workload, "rows": I, "cols": D, "bits": bits, "launches": 4}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -159,9 +181,15 @@ def main():
     ap.add_argument("--copy-probe", action="store_true",
                     help="only copy 256 MiB device-to-device 4 times (calibrates rocprofv3 FETCH_SIZE / "
                          "WRITE_SIZE against known bytes)")
+    ap.add_argument("--gemv-probe", action="store_true",
+                    help="only the workload's gate/up GEMV on synthetic tiles of its shape, 4 launches "
+                         "(the rocprofv3 --pmc traffic runs of the dominant kernel)")
     args = ap.parse_args()
     if args.copy_probe:
         copy_probe()
+        return
+    if args.gemv_probe:
+        gemv_probe(args.workload)
         return
     if args.gpus != 1:
         print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported (the decode path runs "
