@@ -2523,6 +2523,7 @@ const GemvTuning& gemv_tuning() {
       }
     }
     if (const char* e = std::getenv("CHPE_GEMV_XS_MIN_UNITS")) v.xs_min_units = uint32_t(std::strtoul(e, nullptr, 10));
+    if (const char* e = std::getenv("CHPE_GEMV_XM_MIN_MB")) v.xm_min_mb = uint32_t(std::strtoul(e, nullptr, 10));
     if (const char* e = std::getenv("CHPE_GEMV_XS_WPC")) {
       unsigned w[4] = {v.xs_wpc_small, v.xs_wpc_large, v.xs_wpc_logits, v.xs_wpc_wide};
       if (std::sscanf(e, "%u,%u,%u,%u", &w[0], &w[1], &w[2], &w[3]) == 4 && w[0] && w[1] && w[2] && w[3]) {
@@ -2539,6 +2540,14 @@ const GemvTuning& gemv_tuning() {
   return t;
 }
 
+// the 4-bit codes of the launch reach the persistent kernels' size threshold (CHPE_GEMV_XM_MIN_MB)
+static bool persistent_pays(const uint32_t* rows, int n_parts, GemvMode mode, uint32_t C) {
+  uint64_t r = 0;
+  for (int p = 0; p < n_parts; ++p) r += rows[p];
+  if (mode == GemvMode::SwiGlu && n_parts == 1) r *= 2;
+  return r * C / 2 >= uint64_t(gemv_tuning().xm_min_mb) << 20;
+}
+
 GemvLaunch gemv_geometry(WeightKind kind, GemvMode mode, uint32_t C, const uint32_t* rows, int n_parts,
                          uint32_t* n_units, uint32_t* n_panels, uint32_t* waves_per_unit,
                          uint32_t* unit_begin) {
@@ -2551,10 +2560,11 @@ GemvLaunch gemv_geometry(WeightKind kind, GemvMode mode, uint32_t C, const uint3
     bool ok = true;
     if (mode == GemvMode::QkvRope)  // whole units per part (head dims are 128 or 256: whole pairs per unit)
       for (int p = 0; p < n_parts; ++p) ok = ok && rows[p] % R == 0;
-    // (launches of fewer units at <= 8192 columns -- the 72B q/k/v and o projections -- run
-    // faster on the one-unit-per-workgroup kernels: the persistent grid's start-up, the input's
-    // limb tables included, is not amortised over enough units)
-    if (nw < 8 && mode != GemvMode::Logits) {
+    // (launches of fewer units -- the 72B q/k/v and o projections, the 3B and 9B down
+    // projections -- run faster on the one-unit-per-workgroup kernels: the persistent grid's
+    // start-up, the input's limb tables included, is not amortised over enough units; a launch
+    // reading many codes in few wide units, the 72B down projection, amortises it all the same)
+    if (mode != GemvMode::Logits && !persistent_pays(rows, n_parts, mode, C)) {
       uint32_t u = 0;
       for (int p = 0; p < (mode == GemvMode::SwiGlu ? 1 : n_parts); ++p)
         u += mode == GemvMode::SwiGlu ? (rows[p] + R / 2 - 1) / (R / 2) : (rows[p] + R - 1) / R;
@@ -2595,10 +2605,8 @@ GemvLaunch gemv_geometry(WeightKind kind, GemvMode mode, uint32_t C, const uint3
     const uint32_t nw = need <= 1 ? 1u : need <= 2 ? 2u : need <= 4 ? 4u : need <= 8 ? 8u : 16u;
     const uint32_t R = nw >= 8 ? 2u : 4u;
     bool ok = need <= 16;
-    // (launches of fewer units at <= 8192 columns -- the 72B q/k/v and o projections -- run
-    // faster on the one-unit-per-workgroup kernels: the persistent grid's start-up is not
-    // amortised over enough units)
-    if (nw < 8 && mode != GemvMode::Logits) {
+    // (launches of fewer units run faster on the one-unit-per-workgroup kernels, as above)
+    if (mode != GemvMode::Logits && !persistent_pays(rows, n_parts, mode, C)) {
       uint32_t u = 0;
       for (int p = 0; p < (mode == GemvMode::SwiGlu ? 1 : n_parts); ++p)
         u += mode == GemvMode::SwiGlu ? (rows[p] + R / 2 - 1) / (R / 2) : (rows[p] + R - 1) / R;

@@ -196,7 +196,8 @@ struct GemvTuning {
   // its persistent workgroups per CU (256 CUs): launches of < 4096 units, of more, the LM head,
   // and inputs wider than 8192 columns (CHPE_GEMV_XS_WPC=small,large,logits,wide)
   uint32_t xs_wpc_small = 2, xs_wpc_large = 3, xs_wpc_logits = 6, xs_wpc_wide = 1;
-  uint32_t xs_min_units = 4096;  // below this (at <= 8192 columns, not the LM head): the older kernels
+  uint32_t xs_min_units = 4096;  // below this (not the LM head): the older kernels, unless the launch
+  uint32_t xm_min_mb = 48;       //   reads at least this many MB of codes (CHPE_GEMV_XM_MIN_MB)
 };
 const GemvTuning& gemv_tuning();
 
