@@ -4,7 +4,7 @@
 // (q.k_t)*scale, softmax over t <= pos, output sum_t softmax_t * v_t.  RoPE and the KV append
 // at `pos` (:1688-1697) are done by the q/k/v projection's epilogue (GemvMode::QkvRope), so
 // the queries arrive rotated and cache rows 0..pos are complete.  The context is split into
-// chunks of attn_chunk(hd) positions (8192/hd: 64 at hd 128): the chunk kernel computes, per
+// chunks of attn_chunk(hd, kv) positions (64 or 128 at hd 128, 32 at hd 256): the chunk kernel computes, per
 // chunk and query head, the chunk max, the sum of exp(s - max) and the exp-weighted sum of the
 // V rows (k_attn_mfma on the matrix cores for the fp16 cache, k_attn_chunk on the vector ALUs
 // for the f32 cache); k_attn_merge rescales and merges the chunks.  Workgroup (chunk, kv head)
@@ -49,7 +49,7 @@ __global__ void __launch_bounds__(NW * 64) k_attn_chunk(AttnArgs a0) {
   using E = KvElem<KT>;
   constexpr int PW = 64 / LPP, CH = NW * PW, NT = NW * 64;
   constexpr int DK = HD / LPP;               // K dims per lane
-  static_assert(CH == int(attn_chunk_of(HD)) && DK % 4 == 0, "");
+  static_assert(DK % 4 == 0, "");
   constexpr int KW = DK * E::kBytes / 4;    // 32-bit words of a lane's K dims
   constexpr int DPL = HD / 64;              // V dims per lane
   constexpr int VW = DPL * E::kBytes / 4;   // 32-bit words of a lane's V dims (1, 2 or 4)
@@ -237,7 +237,7 @@ __global__ void __launch_bounds__(NW * 64) k_attn_mfma(AttnArgs a0) {
   constexpr int KS = HD / 16;  // k-steps of the score product
   constexpr int VD = HD / 16;  // V dims per lane = N-tiles of the output product
   constexpr int CH = NW * T * 16, NT = NW * 64;
-  static_assert(CH == int(attn_chunk_of(HD)) && GQ <= 8 && NW * GQ <= 64 && (NW & (NW - 1)) == 0, "");
+  static_assert(GQ <= 8 && NW * GQ <= 64 && (NW & (NW - 1)) == 0, "");
   const uint32_t c = blockIdx.x, kvh = blockIdx.y;
   // the position is requested first and waited for only after the loads below are issued
   const uint32_t pos = a.state->pos + blockIdx.z, ctx = pos + 1;
@@ -406,7 +406,8 @@ constexpr uint32_t kMergeWaves = 4;
 template <int HD>
 __global__ void __launch_bounds__(64 * kMergeWaves) k_attn_merge(AttnArgs a0) {
   const AttnArgs a = attn_query(a0);
-  constexpr uint32_t CH = attn_chunk_of(HD), KC = (kAttnMaxChunks + 63) / 64, B = 32;
+  constexpr uint32_t KC = (kAttnMaxChunks + 63) / 64, B = 32;
+  const uint32_t CH = a0.chunk;
   static_assert(kAttnMaxChunks % 4 == 0, "");
   __shared__ __align__(16) float s_w[KC * 64];
   __shared__ float s_o[kMergeWaves][64];
@@ -470,7 +471,11 @@ __global__ void __launch_bounds__(64 * kMergeWaves) k_attn_merge(AttnArgs a0) {
 void launch_attention_partial(const AttnArgs& a, hipStream_t st) {
   const dim3 grid(a.n_chunks, a.KV, a.nq > 1 ? a.nq : 1);
   const uint32_t gq = a.H / a.KV;
-  if (a.hd == 128 && gq == 8)  // fp16: 4 waves x 1 tile; f32: 4 waves x 16 positions, 4 lanes per K row
+  // (the chunk size a.chunk = attn_chunk(hd, KV) picks the instance: CH = waves x positions)
+  if (a.hd == 128 && gq == 8 && a.chunk == 128)  // fp16: 4 waves x 2 tiles; f32: 8 waves x 16 positions
+    a.kv_f16 ? launch_kernel(&k_attn_mfma<128, 8, 4, 2>, grid, dim3(256), st, a)
+             : launch_kernel(&k_attn_chunk<128, 8, float, 4, 8>, grid, dim3(512), st, a);
+  else if (a.hd == 128 && gq == 8)  // 64: fp16 4 waves x 1 tile; f32 4 waves x 16 positions, 4 lanes per K row
     a.kv_f16 ? launch_kernel(&k_attn_mfma<128, 8, 4, 1>, grid, dim3(256), st, a)
              : launch_kernel(&k_attn_chunk<128, 8, float, 4, 4>, grid, dim3(256), st, a);
   else if (a.hd == 256 && gq == 4)  // fp16: 2 waves x 1 tile; f32: 2 waves x 16 positions
@@ -537,7 +542,7 @@ extern "C" int chpe_attention_noalloc(uint32_t head_dim, uint32_t heads, uint32_
                                       const void* v_cache, float* out, void* stream) {
   if (!q || !k_cache || !v_cache || !out || !attention_supported(heads, kv_heads, head_dim)) return -1;
   if (max_seq == 0 || max_seq % 16 != 0 || pos >= max_seq) return -1;
-  const uint32_t chunk = attn_chunk_of(head_dim), n_chunks = (pos + chunk) / chunk;
+  const uint32_t chunk = attn_chunk(head_dim, kv_heads), n_chunks = (pos + chunk) / chunk;
   const size_t ml = size_t(heads) * n_chunks * 2 * 4, acc = size_t(heads) * n_chunks * head_dim * 4;
   // the position, then the two partial arrays, each at a 256-byte boundary
   const size_t off_ml = 256, off_acc = off_ml + (ml + 255) / 256 * 256;
@@ -560,6 +565,7 @@ extern "C" int chpe_attention_noalloc(uint32_t head_dim, uint32_t heads, uint32_
   a.hd = head_dim;
   a.max_seq = max_seq;
   a.n_chunks = n_chunks;
+  a.chunk = chunk;
   a.kv_f16 = kv_f16 ? 1 : 0;
   a.scale = 1.0f / std::sqrt(float(head_dim));
   launch_attention(a, st);

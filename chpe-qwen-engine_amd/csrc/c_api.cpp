@@ -692,7 +692,7 @@ int chpe_debug_embed_row_cell(const uint8_t* bytes, size_t len, uint32_t row, ui
 int chpe_debug_attention(uint32_t head_dim, uint32_t heads, uint32_t kv_heads, int kv_f16, uint32_t pos,
                          const float* q, const float* k_rows, const float* v_rows, float* out) {
   if (!q || !k_rows || !v_rows || !out || !attention_supported(heads, kv_heads, head_dim)) return -1;
-  const uint32_t chunk = attn_chunk_of(head_dim), ctx = pos + 1;
+  const uint32_t chunk = attn_chunk(head_dim, kv_heads), ctx = pos + 1;
   const uint32_t n_chunks = (ctx + chunk - 1) / chunk, rows = n_chunks * chunk;  // a multiple of 16
   if (n_chunks > kAttnMaxChunks) return -1;
   const size_t hd = head_dim, kvd = size_t(kv_heads) * hd, el = kv_f16 ? 2 : 4;
@@ -740,6 +740,7 @@ int chpe_debug_attention(uint32_t head_dim, uint32_t heads, uint32_t kv_heads, i
     a.hd = head_dim;
     a.max_seq = rows;
     a.n_chunks = n_chunks;
+    a.chunk = chunk;
     a.kv_f16 = kv_f16 ? 1 : 0;
     a.scale = 1.0f / std::sqrt(float(head_dim));
     launch_attention(a, nullptr);

@@ -145,7 +145,7 @@ bool Engine::init(const uint8_t* b, size_t len, const EngineConfig& cfg, std::st
            "head_dim 256 with 4";
     return false;
   }
-  const uint32_t chunk = attn_chunk(uint32_t(arch_.head_dim));
+  const uint32_t chunk = attn_chunk(uint32_t(arch_.head_dim), uint32_t(arch_.num_kv_heads));
   n_chunks_ = uint32_t((cfg.max_seq_len + chunk - 1) / chunk);
   if (n_chunks_ > kAttnMaxChunks) {
     *err = "max_seq_len exceeds the attention kernel's chunk table (" +
@@ -661,6 +661,7 @@ AttnArgs Engine::attn_args(size_t l) const {
   at.hd = uint32_t(arch_.head_dim);
   at.max_seq = uint32_t(S);
   at.n_chunks = n_chunks_;
+  at.chunk = attn_chunk(at.hd, at.KV);
   at.kv_f16 = cfg_.kv_f16 ? 1 : 0;
   at.scale = 1.0f / std::sqrt(float(arch_.head_dim));
   return at;
@@ -1105,7 +1106,8 @@ double Engine::stage_bytes(int stage, size_t l) const {
           hipMemcpy(&st, d_state_, sizeof(st), hipMemcpyDeviceToHost) != hipSuccess)
         return 0.0;
       if (stage == 6) {
-        const double chunks = std::ceil((double(st.pos) + 1.0) / attn_chunk(uint32_t(arch_.head_dim)));
+        const double chunks =
+            std::ceil((double(st.pos) + 1.0) / attn_chunk(uint32_t(arch_.head_dim), uint32_t(arch_.num_kv_heads)));
         return double(arch_.num_attn_heads) * chunks * (arch_.head_dim + 2) * 4.0;
       }
       const double kv_row = double(arch_.num_kv_heads * arch_.head_dim) * (cfg_.kv_f16 ? 2 : 4);

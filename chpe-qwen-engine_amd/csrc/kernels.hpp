@@ -159,6 +159,7 @@ struct AttnArgs {
   float* part_ml;           // [H][n_chunks][2] (chunk max, chunk sum)
   float* part_acc;          // [H][n_chunks][hd]
   uint32_t H, KV, hd, max_seq, n_chunks;  // max_seq: cache rows per kv head, a multiple of 16
+  uint32_t chunk;           // positions per chunk: attn_chunk(hd, KV)
   uint32_t kv_f16;
   float scale;              // 1/sqrt(hd)
   uint32_t nq;              // queries of a block step at positions pos .. pos + nq - 1 (rows of q,
@@ -319,8 +320,12 @@ void launch_finish(const FinishArgs& a, hipStream_t stream);
 constexpr uint32_t kAttnMaxChunks = 320;  // chunks of attn_chunk(hd) positions per launch
 // device scratch of chpe_attention_noalloc (position + partials), per GPU
 constexpr size_t kAttnScratchBytes = size_t(8) << 20;
-__host__ __device__ constexpr uint32_t attn_chunk_of(uint32_t hd) { return 8192u / hd; }
-inline uint32_t attn_chunk(uint32_t hd) { return attn_chunk_of(hd); }
+// positions per attention chunk: 8192 / head_dim (64 at 128, 32 at 256), 128 at head dim 128
+// with >= 8 kv heads (the 72B model: enough workgroups per launch at half the partials)
+__host__ __device__ constexpr uint32_t attn_chunk_of(uint32_t hd, uint32_t kv) {
+  return hd == 128 && kv >= 8 ? 128u : 8192u / hd;
+}
+inline uint32_t attn_chunk(uint32_t hd, uint32_t kv) { return attn_chunk_of(hd, kv); }
 // (hd, query heads per kv head) pairs the attention kernels are built for
 bool attention_supported(uint32_t H, uint32_t KV, uint32_t hd);
 constexpr uint32_t kMaxLogitsBlocks = 8192;

@@ -174,7 +174,8 @@ int chpe_debug_attention(uint32_t head_dim, uint32_t heads, uint32_t kv_heads, i
  * max_seq: cache rows per kv head, a multiple of 16, > pos.  stream: a hipStream_t (null: the
  * default stream); the call only enqueues.  The chunk partials live in a per-GPU device array
  * of 8 MiB (heads * ceil((pos+1)/chunk) * (head_dim + 2) * 4 bytes must fit, chunk = 8192 /
- * head_dim positions); calls that overlap on one GPU race on it.  Returns 0, -1 bad arguments
+ * head_dim positions, 128 at head_dim 128 with >= 8 kv heads); calls that overlap on one GPU
+ * race on it.  Returns 0, -1 bad arguments
  * or unsupported shape, -2 the partials exceed the scratch, -3 device error. */
 int chpe_attention_noalloc(uint32_t head_dim, uint32_t heads, uint32_t kv_heads, int kv_f16, uint32_t pos,
                            uint32_t max_seq, const float *q, const void *k_cache, const void *v_cache,

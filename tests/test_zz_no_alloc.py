@@ -78,8 +78,9 @@ def test_noalloc_attention_matches_allocating_entry(hd, H, KV, kv_f16):
             assert rc == 0
             got = bufs[3].get(np.float32, H * hd)  # hipMemcpy waits for the default stream
             assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), float(np.abs(got - ref).max())
-            # partials past the 8 MiB scratch (64 heads x 320 chunks x 130 floats): refused, nothing launched
-            assert lib.chpe_attention_noalloc(128, 64, 8, 1, 20479, 20480, dq, dk, dv, dout, None) == -2
+            # partials past the 8 MiB scratch (64 heads x 320 chunks of 128 positions x 130 floats):
+            # refused, nothing launched
+            assert lib.chpe_attention_noalloc(128, 64, 8, 1, 40959, 40960, dq, dk, dv, dout, None) == -2
             # bad arguments: a position past the cache, a null pointer
             assert lib.chpe_attention_noalloc(hd, H, KV, kv_f16, max_seq, max_seq, dq, dk, dv, dout, None) == -1
             assert lib.chpe_attention_noalloc(hd, H, KV, kv_f16, pos, max_seq, None, dk, dv, dout, None) == -1
