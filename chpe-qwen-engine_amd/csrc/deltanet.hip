@@ -8,11 +8,10 @@
 // RMSNormGated :168-184).
 //
 // k_dn_conv: the depthwise causal conv over [state, x] + SiLU, one thread per channel, the
-// state shifted in place.  k_dn_step: one workgroup per value head; the head's 128x128 f32
-// state (64 KiB) is read once and written once: thread (row block rb, column j) holds rows
-// rb*RPB.. of column j in registers, the two column sums (S^T k before the update, S^T q after)
-// meet in LDS in a fixed order, and the gated RMSNorm of the head's output runs in the same
-// launch.  Memory-bound: 2 x 64 KiB of state per head and step.
+// state shifted in place.  k_dn_step: a workgroup per (value head, 16-column block): its slab
+// of the head's 128x128 f32 state is read once and written once (the columns of the update are
+// independent; 32 heads x 8 blocks = 256 workgroups at the 9B shape); k_dn_gnorm: the gated
+// RMSNorm of each head's output.  Memory-bound: 2 x 64 KiB of state per head and step.
 #include "device_common.hpp"
 #include "kernels.hpp"
 
@@ -48,21 +47,28 @@ __global__ void __launch_bounds__(256) k_dn_conv(DnConvArgs a) {
   st[T - 2] = x;
 }
 
-template <int D>
-__global__ void __launch_bounds__(512) k_dn_step(DnStepArgs a) {
-  constexpr int NT = 512, RB = NT / D, RPB = D / RB;  // row blocks, rows per block
-  static_assert(NT % D == 0 && D % RB == 0 && D % 64 == 0, "");
-  const uint32_t h = blockIdx.x, kh = h / (a.n_v_heads / a.n_k_heads);
-  const int t = threadIdx.x, j = t % D, rb = t / D, lane = t & 63, wave = t >> 6;
+// grid (value head, column block of CW columns): the block's D x CW slab of the head's state
+// (rows i, columns c0 + j) is read once and written once; every column of the update is
+// independent (kv_mem[j], delta_j, S[:, j], o[j]), so the head's columns spread over D / CW
+// workgroups.  Thread (row block rb, column j) holds rows rb * RPB .. of column c0 + j; the
+// two column sums (S^T k before the update, S^T q after) meet over the row blocks of a wave
+// (lanes 16 and 32 apart) and over the waves in LDS, in a fixed order.  q and k are
+// l2-normalised by every workgroup of the head (D values each).  Writes o[j] = (S^T q)_j; the
+// gated norm, a reduction over the whole head, is k_dn_gnorm.
+template <int D, int CW>
+__global__ void __launch_bounds__(256) k_dn_step(DnStepArgs a) {
+  constexpr int NT = 256, RB = NT / CW, RPB = D / RB, NWV = NT / 64;
+  static_assert(CW == 16 && NT % CW == 0 && D % RB == 0 && D % 64 == 0, "lanes 16 / 32 apart share a column");
+  const uint32_t h = blockIdx.x, c0 = blockIdx.y * CW, kh = h / (a.n_v_heads / a.n_k_heads);
+  const int t = threadIdx.x, j = t % CW, rb = t / CW, lane = t & 63, wave = t >> 6;
   __shared__ float s_qn[D], s_kn[D];
-  __shared__ float s_part[RB][D];
-  __shared__ float s_red[NT / 64];
+  __shared__ float s_part[NWV][CW];
 
   // 1. loads: the thread's state rows, then the head's inputs (all before any use)
-  float* S = a.state + size_t(h) * D * D;
+  float* S = a.state + size_t(h) * D * D + c0 + j;
   float sr[RPB];
 #pragma unroll
-  for (int r = 0; r < RPB; ++r) sr[r] = S[size_t(rb * RPB + r) * D + j];
+  for (int r = 0; r < RPB; ++r) sr[r] = S[size_t(rb * RPB + r) * D];
   constexpr int PL = D / 64;  // q/k values per lane (every wave normalises both vectors)
   float qv[PL], kv[PL];
 #pragma unroll
@@ -70,7 +76,7 @@ __global__ void __launch_bounds__(512) k_dn_step(DnStepArgs a) {
     qv[m] = a.q[size_t(kh) * D + lane + 64 * m];
     kv[m] = a.k[size_t(kh) * D + lane + 64 * m];
   }
-  const float vj = a.v[size_t(h) * D + j];
+  const float vj = a.v[size_t(h) * D + c0 + j];
   const float beta = 1.0f / (1.0f + expf(-a.b[h]));
   const float decay = expf(-expf(a.A_log[h]) * softplus_f(a.a[h] + a.dt_bias[h]));
 
@@ -93,6 +99,19 @@ __global__ void __launch_bounds__(512) k_dn_step(DnStepArgs a) {
   }
   __syncthreads();
 
+  // the column sum of a per-thread partial: over the wave's 4 row blocks, then the waves
+  auto column_sum = [&](float p) {
+    p = pair_sum(p, 16);
+    p = pair_sum(p, 32);
+    if (lane < CW) s_part[wave][lane] = p;
+    __syncthreads();
+    float v = 0.0f;
+#pragma unroll
+    for (int w = 0; w < NWV; ++w) v += s_part[w][j];
+    __syncthreads();  // s_part is reused by the next sum
+    return v;
+  };
+
   // 3. decayed state; kv_mem[j] = sum_i S[i][j] k[i]
   float p = 0.0f;
 #pragma unroll
@@ -100,47 +119,37 @@ __global__ void __launch_bounds__(512) k_dn_step(DnStepArgs a) {
     sr[r] *= decay;
     p += sr[r] * s_kn[rb * RPB + r];
   }
-  s_part[rb][j] = p;
-  __syncthreads();
-  float kvm = 0.0f;
-#pragma unroll
-  for (int b = 0; b < RB; ++b) kvm += s_part[b][j];
+  const float kvm = column_sum(p);
   const float delta = (vj - kvm) * beta;
-  __syncthreads();  // s_part is reused below
 
   // 4. S += k delta^T, written back; o[j] = sum_i S[i][j] q[i]
   float o = 0.0f;
 #pragma unroll
   for (int r = 0; r < RPB; ++r) {
     sr[r] += s_kn[rb * RPB + r] * delta;
-    S[size_t(rb * RPB + r) * D + j] = sr[r];
+    S[size_t(rb * RPB + r) * D] = sr[r];
     o += sr[r] * s_qn[rb * RPB + r];
   }
-  s_part[rb][j] = o;
-  __syncthreads();
-  // threads 0..D-1 (whole waves: rb is uniform per wave) finish the head
-  float oj = 0.0f;
-  if (rb == 0) {
-#pragma unroll
-    for (int b = 0; b < RB; ++b) oj += s_part[b][j];
-  }
+  o = column_sum(o);
+  if (t < CW) a.out[size_t(h) * D + c0 + j] = o;
+}
 
-  // 5. gated RMSNorm of the head (when given): w * (o * rsqrt(mean o^2 + eps)) * silu(z)
-  if (a.norm_w) {
-    if (rb == 0) {
-      const float s2 = wave_sum(oj * oj);
-      if (lane == 0) s_red[wave] = s2;
-    }
-    __syncthreads();
-    if (rb == 0) {
-      float tot = 0.0f;
+// the gated RMSNorm of each value head's output (one workgroup of D threads per head):
+// w * (o * rsqrt(mean o^2 + eps)) * silu(z)
+template <int D>
+__global__ void __launch_bounds__(D) k_dn_gnorm(DnStepArgs a) {
+  const uint32_t h = blockIdx.x;
+  const int j = threadIdx.x, lane = j & 63, wave = j >> 6;
+  __shared__ float s_red[D / 64];
+  const float o = a.out[size_t(h) * D + j], z = a.z[size_t(h) * D + j], w = a.norm_w[j];
+  const float s2 = wave_sum(o * o);
+  if (lane == 0) s_red[wave] = s2;
+  __syncthreads();
+  float tot = 0.0f;
 #pragma unroll
-      for (int w = 0; w < D / 64; ++w) tot += s_red[w];
-      const float rr = 1.0f / sqrtf(tot / float(D) + a.eps);
-      oj = a.norm_w[j] * (oj * rr) * silu_f(a.z[size_t(h) * D + j]);
-    }
-  }
-  if (rb == 0) a.out[size_t(h) * D + j] = oj;
+  for (int k = 0; k < D / 64; ++k) tot += s_red[k];
+  const float rr = 1.0f / sqrtf(tot / float(D) + a.eps);
+  a.out[size_t(h) * D + j] = w * (o * rr) * silu_f(z);
 }
 
 }  // namespace
@@ -155,8 +164,14 @@ void launch_dn_conv(const DnConvArgs& a, hipStream_t st) {
 }
 
 void launch_dn_step(const DnStepArgs& a, uint32_t head_dim, hipStream_t st) {
-  if (head_dim == 128) launch_kernel(&k_dn_step<128>, dim3(a.n_v_heads), dim3(512), st, a);
-  else launch_kernel(&k_dn_step<64>, dim3(a.n_v_heads), dim3(512), st, a);
+  constexpr uint32_t CW = 16;
+  if (head_dim == 128) {
+    launch_kernel(&k_dn_step<128, CW>, dim3(a.n_v_heads, 128 / CW), dim3(256), st, a);
+    if (a.norm_w) launch_kernel(&k_dn_gnorm<128>, dim3(a.n_v_heads), dim3(128), st, a);
+  } else {
+    launch_kernel(&k_dn_step<64, CW>, dim3(a.n_v_heads, 64 / CW), dim3(256), st, a);
+    if (a.norm_w) launch_kernel(&k_dn_gnorm<64>, dim3(a.n_v_heads), dim3(64), st, a);
+  }
 }
 
 }  // namespace chpe
