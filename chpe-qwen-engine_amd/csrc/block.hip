@@ -531,12 +531,12 @@ void launch_block_limbs(const BlockGemvArgs& a, hipStream_t st) {
 
 uint32_t launch_block_gemv(BlockGemvArgs& a, hipStream_t st) {
   const uint32_t ranges = (a.g.C + kBlockRange - 1) / kBlockRange;
-  // workgroups per range: about 256 workgroups of 8 waves in all (one per CU: the LDS tables and
-  // stage slots)
-  uint32_t per = (256 + ranges - 1) / ranges;
+  // workgroups per range: at most 256 workgroups of 8 waves in all, one round on the 256 CUs (one
+  // workgroup per CU: the LDS tables and stage slots; a 257th workgroup would double the launch)
+  uint32_t per = 256 / ranges;
+  if (per == 0) per = 1;
   const uint32_t need = (a.n_units + 7) / 8;  // (a wave per unit at least)
   if (per > need) per = need;
-  if (per == 0) per = 1;
   const dim3 grid(ranges, per);
   if (a.nq <= 1) launch_kernel(&k_gemv_mt<1, 8>, grid, dim3(512), st, a);
   else launch_kernel(&k_gemv_mt<2, 8>, grid, dim3(512), st, a);
