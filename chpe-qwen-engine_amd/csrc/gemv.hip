@@ -1851,13 +1851,13 @@ __global__ void __launch_bounds__(kWave * NW) k_gemv_xs(GemvArgs a) {
     xv[j] = okc ? xv[j] : 0.0f;
     ss = fmaf(xv[j], xv[j], ss);
   }
-  ss = wave_sum(ss);
-  if (lane == 0) s_red[wave] = ss;
-  __syncthreads();
   float tot = 0.0f;
+  if constexpr (kNorm) {  // (the residual modes skip the sum of squares and its barrier)
+    ss = wave_sum(ss);
+    if (lane == 0) s_red[wave] = ss;
+    __syncthreads();
 #pragma unroll
-  for (int w = 0; w < NW; ++w) tot += s_red[w];
-  if constexpr (kNorm) {
+    for (int w = 0; w < NW; ++w) tot += s_red[w];
     const float inv = 1.0f / sqrtf(tot / float(C) + a.eps);
 #pragma unroll
     for (int j = 0; j < KC / 4; ++j) {
@@ -2092,21 +2092,24 @@ __global__ void __launch_bounds__(kWave * NW) k_gemv_xm(GemvArgs a) {
   uint32_t unit = blockIdx.x;  // < n_units: the grid is at most the unit count
   issue(unit, &LA);
 
-  // 2. normalise, then the limb tables, limb sums and group exponents
-  float ss = 0.0f;
-#pragma unroll
-  for (int S = 0; S < 4; ++S) {
-    const bool live = (gw + 4 * S) * 128 + 8 * uint32_t(lane) < C;
-    const float v[8] = {xr[S][0].x, xr[S][0].y, xr[S][0].z, xr[S][0].w, xr[S][1].x, xr[S][1].y, xr[S][1].z, xr[S][1].w};
-#pragma unroll
-    for (int i = 0; i < 8; ++i) ss = live ? fmaf(v[i], v[i], ss) : ss;
-  }
-  ss = wave_sum(ss);
-  if (lane == 0) s_red[wave] = ss;
-  __syncthreads();
+  // 2. normalise (the norm modes only: the sum of squares and its workgroup barrier cost the
+  // residual launches about 1.4 us), then the limb tables, limb sums and group exponents
   float tot = 0.0f;
+  if constexpr (kNorm) {
+    float ss = 0.0f;
 #pragma unroll
-  for (int w = 0; w < NW; ++w) tot += s_red[w];
+    for (int S = 0; S < 4; ++S) {
+      const bool live = (gw + 4 * S) * 128 + 8 * uint32_t(lane) < C;
+      const float v[8] = {xr[S][0].x, xr[S][0].y, xr[S][0].z, xr[S][0].w, xr[S][1].x, xr[S][1].y, xr[S][1].z, xr[S][1].w};
+#pragma unroll
+      for (int i = 0; i < 8; ++i) ss = live ? fmaf(v[i], v[i], ss) : ss;
+    }
+    ss = wave_sum(ss);
+    if (lane == 0) s_red[wave] = ss;
+    __syncthreads();
+#pragma unroll
+    for (int w = 0; w < NW; ++w) tot += s_red[w];
+  }
   const float inv = kNorm ? 1.0f / sqrtf(tot / float(C) + a.eps) : 1.0f;
   uint2* tb2 = reinterpret_cast<uint2*>(s_tb + wave * (kXmTableBytes / 16));
 #pragma unroll
