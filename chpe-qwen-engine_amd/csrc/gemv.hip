@@ -1564,9 +1564,11 @@ __global__ void __launch_bounds__(kWave * W) k_gemv_flat(GemvArgs a) {
   // the rows' outlier corrections, spread over every wave: lane (j, c) of wave w takes entries
   // c + 16 (w + W t) of rows j and j + 4, so all waves issue the same loads (the waits stay
   // exact) and the corrections join the row sums before the lane reduction
+  // (a wave skips the slots past every row's entries: a uniform test on the tables' row width)
   constexpr int SPL = int(kMaxCorrPerRow + 16 * W - 1) / (16 * W);
   float2 ca[SPL], cb[SPL];
   uint32_t cuse = 0;
+  const uint32_t kmU = max(uni(P0.corr_kmax), uni(P1.corr_kmax));
   {
     const float2* corrA = uni(P0.corr);
     const float2* corrB = uni(P1.corr);
@@ -1575,11 +1577,14 @@ __global__ void __launch_bounds__(kWave * W) k_gemv_flat(GemvArgs a) {
     const float2* srcB = corrB ? corrB : reinterpret_cast<const float2*>(a.x);
 #pragma unroll
     for (int t = 0; t < SPL; ++t) {
-      const uint32_t e = uint32_t(c) + 16u * (wave + uint32_t(W * t));
-      const bool ua = corrA != nullptr && okA && e < kmA, ub = corrB != nullptr && okB && e < kmB;
-      ca[t] = srcA[ua ? size_t(rowA) * kmA + e : 0];
-      cb[t] = srcB[ub ? size_t(rowB) * kmB + e : 0];
-      cuse |= (uint32_t(ua) << (2 * t)) | (uint32_t(ub) << (2 * t + 1));
+      ca[t] = cb[t] = make_float2(0.0f, 0.0f);
+      if (16u * (wave + uint32_t(W * t)) < kmU) {
+        const uint32_t e = uint32_t(c) + 16u * (wave + uint32_t(W * t));
+        const bool ua = corrA != nullptr && okA && e < kmA, ub = corrB != nullptr && okB && e < kmB;
+        ca[t] = srcA[ua ? size_t(rowA) * kmA + e : 0];
+        cb[t] = srcB[ub ? size_t(rowB) * kmB + e : 0];
+        cuse |= (uint32_t(ua) << (2 * t)) | (uint32_t(ub) << (2 * t + 1));
+      }
     }
   }
   uint4 qa[MAXP], qb[MAXP];
@@ -1635,11 +1640,14 @@ __global__ void __launch_bounds__(kWave * W) k_gemv_flat(GemvArgs a) {
   float xca[SPL], xcb[SPL];
 #pragma unroll
   for (int t = 0; t < SPL; ++t) {
-    const bool ua = ((cuse >> (2 * t)) & 1u) && ca[t].y != 0.0f;
-    const bool ub = ((cuse >> (2 * t + 1)) & 1u) && cb[t].y != 0.0f;
-    const uint32_t qa = ua ? __float_as_uint(ca[t].x) : 0u, qb = ub ? __float_as_uint(cb[t].x) : 0u;
-    xca[t] = kLocal ? a.x[qa] : s_x[xs_at(qa)];
-    xcb[t] = kLocal ? a.x[qb] : s_x[xs_at(qb)];
+    xca[t] = xcb[t] = 0.0f;
+    if (16u * (wave + uint32_t(W * t)) < kmU) {
+      const bool ua = ((cuse >> (2 * t)) & 1u) && ca[t].y != 0.0f;
+      const bool ub = ((cuse >> (2 * t + 1)) & 1u) && cb[t].y != 0.0f;
+      const uint32_t qa = ua ? __float_as_uint(ca[t].x) : 0u, qb = ub ? __float_as_uint(cb[t].x) : 0u;
+      xca[t] = kLocal ? a.x[qa] : s_x[xs_at(qa)];
+      xcb[t] = kLocal ? a.x[qb] : s_x[xs_at(qb)];
+    }
   }
 
   // 3. the dots of the wave's panels, summed over the 16 lanes of each row, then over the waves
@@ -2197,18 +2205,25 @@ __global__ void __launch_bounds__(kWave * NW) k_gemv_xm(GemvArgs a) {
       r = pair_sum(r, 2);
       acc += r;
     }
-    // corrections of row q over its 16 lanes
+    // corrections of row q over its 16 lanes.  Slot t of the wave holds entries 16 (w + NW t) ..
+    // + 15 of each row: the wave skips the slots past every row's entries (a uniform test on
+    // the tables' row width), the reduction too when it has none
+    const uint32_t km = kSwi ? max(uni(P0.corr_kmax), uni(P1.corr_kmax)) : uni(P0.corr_kmax);
     float cs = 0.0f;
+    if (16u * wave < km) {
 #pragma unroll
-    for (int t = 0; t < SPL; ++t) {
-      const bool on = ((L.cuse >> t) & 1u) && L.ce[t].y != 0.0f;
-      const float xc = xm_input(tbytes, s_e, on ? __float_as_uint(L.ce[t].x) : 0u);
-      cs = on ? fmaf(L.ce[t].y, xc, cs) : cs;
+      for (int t = 0; t < SPL; ++t) {
+        if (16u * (wave + uint32_t(NW * t)) < km) {
+          const bool on = ((L.cuse >> t) & 1u) && L.ce[t].y != 0.0f;
+          const float xc = xm_input(tbytes, s_e, on ? __float_as_uint(L.ce[t].x) : 0u);
+          cs = on ? fmaf(L.ce[t].y, xc, cs) : cs;
+        }
+      }
+      cs = pair_sum(cs, 1);
+      cs = pair_sum(cs, 2);
+      cs = pair_sum(cs, 4);
+      cs = pair_sum(cs, 8);
     }
-    cs = pair_sum(cs, 1);
-    cs = pair_sum(cs, 2);
-    cs = pair_sum(cs, 4);
-    cs = pair_sum(cs, 8);
     {
       const bool second = kSwi && q >= R / 2;
       const uint32_t r = row_of<R, MODE>(rb, q, half);
