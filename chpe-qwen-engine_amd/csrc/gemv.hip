@@ -2180,7 +2180,23 @@ __global__ void __launch_bounds__(kWave * NW) k_gemv_xm(GemvArgs a) {
     const GemvPart P0 = kRope ? pick_part(a, L.pu) : a.part[0];
     const GemvPart& P1 = kSwi ? a.part[1] : P0;
     const uint32_t rb = L.row_base;
+    // corrections of row q, spread over its 16 lanes (first: their LDS reads overlap the
+    // products).  Slot t of the wave holds entries 16 (w + NW t) .. + 15 of each row: the wave
+    // skips the slots past every row's entries (a uniform test on the tables' row width)
+    const uint32_t km = kSwi ? max(uni(P0.corr_kmax), uni(P1.corr_kmax)) : uni(P0.corr_kmax);
     float acc = 0.0f;
+    if (16u * wave < km) {
+#pragma unroll
+      for (int t = 0; t < SPL; ++t) {
+        if (16u * (wave + uint32_t(NW * t)) < km) {
+          const bool on = ((L.cuse >> t) & 1u) && L.ce[t].y != 0.0f;
+          const float xc = xm_input(tbytes, s_e, on ? __float_as_uint(L.ce[t].x) : 0u);
+          acc = on ? fmaf(L.ce[t].y, xc, acc) : acc;
+        }
+      }
+    }
+    // the products: lane (n, q) adds its limb's share of group n % 4 of each set, times the
+    // group scale; the row's sum over the 16 lanes (limbs, then groups) is taken once at the end
 #pragma unroll
     for (int S = 0; S < 4; ++S) {
       i32x4_t D = {cinit[S], cinit[S], cinit[S], cinit[S]};
@@ -2196,39 +2212,18 @@ __global__ void __launch_bounds__(kWave * NW) k_gemv_xm(GemvArgs a) {
       }
       const int j = n & 3;
       const int v = j == 0 ? D[0] : j == 1 ? D[1] : j == 2 ? D[2] : D[3];
-      const float f = float(v) * lpf[S];
-      const float t = ((f + dpp_f<0x114>(f)) + dpp_f<0x118>(f)) + dpp_f<0x11c>(f);
       // (a group past the input: its products are zero; its scale, read from group 0, is not used)
       const bool gv = gw + 4 * uint32_t(S) + uint32_t(n & 3) < ng;
-      float r = gv ? t * h2f(uint16_t(L.s[S])) : 0.0f;
-      r = pair_sum(r, 1);
-      r = pair_sum(r, 2);
-      acc += r;
+      acc = gv ? fmaf(float(v) * lpf[S], h2f(uint16_t(L.s[S])), acc) : acc;
     }
-    // corrections of row q over its 16 lanes.  Slot t of the wave holds entries 16 (w + NW t) ..
-    // + 15 of each row: the wave skips the slots past every row's entries (a uniform test on
-    // the tables' row width), the reduction too when it has none
-    const uint32_t km = kSwi ? max(uni(P0.corr_kmax), uni(P1.corr_kmax)) : uni(P0.corr_kmax);
-    float cs = 0.0f;
-    if (16u * wave < km) {
-#pragma unroll
-      for (int t = 0; t < SPL; ++t) {
-        if (16u * (wave + uint32_t(NW * t)) < km) {
-          const bool on = ((L.cuse >> t) & 1u) && L.ce[t].y != 0.0f;
-          const float xc = xm_input(tbytes, s_e, on ? __float_as_uint(L.ce[t].x) : 0u);
-          cs = on ? fmaf(L.ce[t].y, xc, cs) : cs;
-        }
-      }
-      cs = pair_sum(cs, 1);
-      cs = pair_sum(cs, 2);
-      cs = pair_sum(cs, 4);
-      cs = pair_sum(cs, 8);
-    }
+    acc = ((acc + dpp_f<0x114>(acc)) + dpp_f<0x118>(acc)) + dpp_f<0x11c>(acc);
+    acc = pair_sum(acc, 1);
+    acc = pair_sum(acc, 2);
     {
       const bool second = kSwi && q >= R / 2;
       const uint32_t r = row_of<R, MODE>(rb, q, half);
       const uint32_t wr = second ? uni(P1.wrows) : uni(P0.wrows);
-      if (n == 12) s_part[buf][wave][q] = r < wr ? acc + cs : 0.0f;
+      if (n == 12) s_part[buf][wave][q] = r < wr ? acc : 0.0f;
     }
     __syncthreads();
     if (wave == 0 && lane < NE) {
