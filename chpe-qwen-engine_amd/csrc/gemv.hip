@@ -1561,14 +1561,16 @@ __global__ void __launch_bounds__(kWave * W) k_gemv_flat(GemvArgs a) {
   const uint8_t* baseA = P0.base;
   const uint8_t* baseB = P1.base;
   const uint32_t strA = P0.stride, strB = P1.stride, lo16 = uint32_t(c & 3) * 16;
-  // the rows' outlier corrections, spread over every wave: lane (j, c) of wave w takes entries
-  // c + 16 (w + W t) of rows j and j + 4, so all waves issue the same loads (the waits stay
-  // exact) and the corrections join the row sums before the lane reduction
-  // (a wave skips the slots past every row's entries: a uniform test on the tables' row width)
+  // the rows' outlier corrections, spread over the waves: lane (j, c) of the wave in slot
+  // position s (wsl below) takes entries c + 16 (s + W t) of rows j and j + 4, and the
+  // corrections join the row sums before the lane reduction (a wave skips the slots past every
+  // row's entries: a uniform test on the tables' row width)
   constexpr int SPL = int(kMaxCorrPerRow + 16 * W - 1) / (16 * W);
   float2 ca[SPL], cb[SPL];
   uint32_t cuse = 0;
   const uint32_t kmU = max(uni(P0.corr_kmax), uni(P1.corr_kmax));
+  // the waves' slot order starts at wave 1: wave 0, which runs the epilogue, takes the last slot
+  const uint32_t wsl = wave == 0 ? uint32_t(W - 1) : wave - 1;
   {
     const float2* corrA = uni(P0.corr);
     const float2* corrB = uni(P1.corr);
@@ -1578,8 +1580,8 @@ __global__ void __launch_bounds__(kWave * W) k_gemv_flat(GemvArgs a) {
 #pragma unroll
     for (int t = 0; t < SPL; ++t) {
       ca[t] = cb[t] = make_float2(0.0f, 0.0f);
-      if (16u * (wave + uint32_t(W * t)) < kmU) {
-        const uint32_t e = uint32_t(c) + 16u * (wave + uint32_t(W * t));
+      if (16u * (wsl + uint32_t(W * t)) < kmU) {
+        const uint32_t e = uint32_t(c) + 16u * (wsl + uint32_t(W * t));
         const bool ua = corrA != nullptr && okA && e < kmA, ub = corrB != nullptr && okB && e < kmB;
         ca[t] = srcA[ua ? size_t(rowA) * kmA + e : 0];
         cb[t] = srcB[ub ? size_t(rowB) * kmB + e : 0];
@@ -1641,7 +1643,7 @@ __global__ void __launch_bounds__(kWave * W) k_gemv_flat(GemvArgs a) {
 #pragma unroll
   for (int t = 0; t < SPL; ++t) {
     xca[t] = xcb[t] = 0.0f;
-    if (16u * (wave + uint32_t(W * t)) < kmU) {
+    if (16u * (wsl + uint32_t(W * t)) < kmU) {
       const bool ua = ((cuse >> (2 * t)) & 1u) && ca[t].y != 0.0f;
       const bool ub = ((cuse >> (2 * t + 1)) & 1u) && cb[t].y != 0.0f;
       const uint32_t qa = ua ? __float_as_uint(ca[t].x) : 0u, qb = ub ? __float_as_uint(cb[t].x) : 0u;
@@ -2015,6 +2017,8 @@ __global__ void __launch_bounds__(kWave * NW) k_gemv_xm(GemvArgs a) {
   args_batch<MODE>(a);
   const uint32_t C = a.C, ng = C >> 7, half = a.rope.head_dim / 2, n_units = a.n_units, step = gridDim.x;
   const uint32_t gw = wave * 16;  // the wave's first group
+  // correction slots in wave order from wave 1: wave 0, which runs the epilogue, takes the last
+  const uint32_t wsl = wave == 0 ? uint32_t(NW - 1) : wave - 1;
 
   // 1. the wave's input: 8 columns per lane and set (lane l: set S, columns 2048 w + 512 S + 8 l)
   float4 xr[4][2], gr[kNorm ? 4 : 1][2];
@@ -2054,7 +2058,7 @@ __global__ void __launch_bounds__(kWave * NW) k_gemv_xm(GemvArgs a) {
         L->s[S] = ld_u16(bs + ((Gs >> 8) * sts + 16448 + 48 + 2 * (Gs & 255u)));
       }
     }
-    {  // corrections: lane (n, q) takes entries n + 16 (w + NW t) of unit row q
+    {  // corrections: lane (n, q) takes entries n + 16 (s + NW t) of unit row q (s = wsl)
       const bool second = kSwi && q >= R / 2;
       const float2* corr = second ? uni(P1.corr) : uni(P0.corr);
       const uint32_t kmax = second ? uni(P1.corr_kmax) : uni(P0.corr_kmax);
@@ -2065,7 +2069,7 @@ __global__ void __launch_bounds__(kWave * NW) k_gemv_xm(GemvArgs a) {
       uint32_t m = 0;
 #pragma unroll
       for (int t = 0; t < SPL; ++t) {
-        const uint32_t e = uint32_t(n) + 16u * (wave + uint32_t(NW * t));
+        const uint32_t e = uint32_t(n) + 16u * (wsl + uint32_t(NW * t));
         const bool use = ok && e < kmax;
         L->ce[t] = src[use ? size_t(r) * kmax + e : 0];
         m |= uint32_t(use) << t;
@@ -2181,14 +2185,14 @@ __global__ void __launch_bounds__(kWave * NW) k_gemv_xm(GemvArgs a) {
     const GemvPart& P1 = kSwi ? a.part[1] : P0;
     const uint32_t rb = L.row_base;
     // corrections of row q, spread over its 16 lanes (first: their LDS reads overlap the
-    // products).  Slot t of the wave holds entries 16 (w + NW t) .. + 15 of each row: the wave
-    // skips the slots past every row's entries (a uniform test on the tables' row width)
+    // products).  Slot t of the wave holds entries 16 (wsl + NW t) .. + 15 of each row: the
+    // wave skips the slots past every row's entries (a uniform test on the tables' row width)
     const uint32_t km = kSwi ? max(uni(P0.corr_kmax), uni(P1.corr_kmax)) : uni(P0.corr_kmax);
     float acc = 0.0f;
-    if (16u * wave < km) {
+    if (16u * wsl < km) {
 #pragma unroll
       for (int t = 0; t < SPL; ++t) {
-        if (16u * (wave + uint32_t(NW * t)) < km) {
+        if (16u * (wsl + uint32_t(NW * t)) < km) {
           const bool on = ((L.cuse >> t) & 1u) && L.ce[t].y != 0.0f;
           const float xc = xm_input(tbytes, s_e, on ? __float_as_uint(L.ce[t].x) : 0u);
           acc = on ? fmaf(L.ce[t].y, xc, acc) : acc;
