@@ -449,6 +449,14 @@ int chpe_debug_gemv_flat(int mode, uint32_t rows, uint32_t cols, const uint8_t* 
     a.result = dres;
     ok = a.partials && dres && dst && hipMemset(dst, 0, sizeof(StepState)) == hipSuccess;
   }
+  if (ok) {  // the permuted code copy where the engine builds one
+    const size_t xb = xm_layout_bytes(kind[0], a, g);
+    if (xb) {
+      uint8_t* dxc = static_cast<uint8_t*>(alloc(xb));
+      ok = dxc && build_xm_layout(a, g, dxc, nullptr);
+      a.part[0].xcodes = dxc;
+    }
+  }
   if (ok) {
     launch_gemv(kind[0], a, g, nullptr);
     if (mode == int(GemvMode::Logits)) {

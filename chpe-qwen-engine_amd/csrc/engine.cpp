@@ -275,6 +275,7 @@ bool Engine::init(const uint8_t* b, size_t len, const EngineConfig& cfg, std::st
       return false;
     }
   }
+  build_xm_layouts();  // the gate/up and LM head codes in the matrix-core kernel's load order
   HIP_TRY(hipDeviceSynchronize());
 
   // ---- capture the step (CHPE_GRAPH=0 launches the same kernels directly on the stream,
@@ -571,6 +572,21 @@ uint32_t Engine::enqueue_gemv(const ProjPlan* const* parts, float* const* outs, 
                               const float* x, uint32_t C, const float* gamma, hipStream_t st,
                               const RopeArgs* rope, const uint32_t* roles) {
   GemvArgs a{};
+  const GemvLaunch g = gemv_args(parts, outs, n, mode, x, C, gamma, rope, roles, &a);
+  if (parts[0]->kind == WeightKind::Cell16Poly) {
+    const PolyPlan* pp[kMaxParts] = {};
+    for (int i = 0; i < n; ++i) pp[i] = &parts[i]->poly;
+    return launch_gemv_poly(a, pp, d_xn_, poly_raw_, st);
+  }
+  launch_gemv(parts[0]->kind, a, g, st);
+  return g.blocks;
+}
+
+GemvLaunch Engine::gemv_args(const ProjPlan* const* parts, float* const* outs, int n, GemvMode mode, const float* x,
+                             uint32_t C, const float* gamma, const RopeArgs* rope, const uint32_t* roles,
+                             GemvArgs* out) const {
+  GemvArgs& a = *out;
+  a = GemvArgs{};
   if (rope) a.rope = *rope;
   a.n_parts = n;
   a.mode = int(mode);
@@ -598,19 +614,39 @@ uint32_t Engine::enqueue_gemv(const ProjPlan* const* parts, float* const* outs, 
     gp.replace_outliers = p.replace_outliers;
     gp.repl = p.repl;
     gp.rope_role = roles ? roles[i] : 0u;
+    gp.xcodes = i == 0 ? p.xcodes : nullptr;
   }
   if (mode == GemvMode::Logits) {
     a.partials = d_partials_;
     a.result = d_result_;
     a.hidden_out = embed_fused_ ? d_hidden_out_ : nullptr;
   }
-  if (parts[0]->kind == WeightKind::Cell16Poly) {
-    const PolyPlan* pp[kMaxParts] = {};
-    for (int i = 0; i < n; ++i) pp[i] = &parts[i]->poly;
-    return launch_gemv_poly(a, pp, d_xn_, poly_raw_, st);
+  return g;
+}
+
+void Engine::build_xm_layout_of(ProjPlan* const* parts, int n, GemvMode mode, uint32_t C) {
+  GemvArgs a{};
+  float* outs[kMaxParts] = {d_mlp_, d_mlp_, d_mlp_};
+  const GemvLaunch g = gemv_args(parts, outs, n, mode, d_hidden_, C, nullptr, nullptr, nullptr, &a);
+  const size_t bytes = xm_layout_bytes(parts[0]->kind, a, g);
+  if (bytes == 0) return;
+  void* d = nullptr;
+  if (hipMalloc(&d, bytes) != hipSuccess) {  // (no copy: the launch reads the records)
+    (void)hipGetLastError();
+    return;
   }
-  launch_gemv(parts[0]->kind, a, g, st);
-  return g.blocks;
+  allocs_.push_back(d);
+  if (build_xm_layout(a, g, static_cast<uint8_t*>(d), stream_)) parts[0]->xcodes = static_cast<uint8_t*>(d);
+}
+
+void Engine::build_xm_layouts() {
+  const uint32_t D = uint32_t(arch_.hidden_dim);
+  for (LayerPlan& L : layers_) {
+    ProjPlan* gu[2] = {&L.gate, &L.up};
+    if (L.gate.kind == L.up.kind && L.gate.rows) build_xm_layout_of(gu, 2, GemvMode::SwiGlu, D);
+  }
+  ProjPlan* lm[1] = {&lm_head_};
+  if (lm_head_.rows) build_xm_layout_of(lm, 1, GemvMode::Logits, D);
 }
 
 void Engine::enqueue_qkv(size_t l, hipStream_t st) {

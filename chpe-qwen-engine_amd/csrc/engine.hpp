@@ -57,6 +57,9 @@ struct ProjPlan {
   float2* corr = nullptr;              // device [rows][corr_kmax] flat-tile outlier corrections
   uint32_t corr_kmax = 0;
   CellReplace* repl = nullptr;         // device, replace-mode outliers of 16-row cells
+  uint8_t* xcodes = nullptr;           // device, the decode launch's codes in the persistent
+                                       //   matrix-core kernel's load order (see xm_layout_bytes);
+                                       //   set on the launch's first part
   PolyPlan poly{};                     // Cell16Poly: the cells' row bases
 };
 
@@ -160,6 +163,12 @@ class Engine {
   uint32_t enqueue_gemv(const ProjPlan* const* parts, float* const* outs, int n, GemvMode mode,
                         const float* x, uint32_t C, const float* gamma, hipStream_t st,
                         const RopeArgs* rope = nullptr, const uint32_t* roles = nullptr);
+  // the launch arguments and geometry of enqueue_gemv's launch
+  GemvLaunch gemv_args(const ProjPlan* const* parts, float* const* outs, int n, GemvMode mode, const float* x,
+                       uint32_t C, const float* gamma, const RopeArgs* rope, const uint32_t* roles, GemvArgs* a) const;
+  // the permuted code copies of the decode launches that read them (gate/up, the LM head)
+  void build_xm_layouts();
+  void build_xm_layout_of(ProjPlan* const* parts, int n, GemvMode mode, uint32_t C);
   AttnArgs attn_args(size_t layer) const;
   double proj_bytes(const ProjPlan& p) const;
   bool plan_block(std::string* err);

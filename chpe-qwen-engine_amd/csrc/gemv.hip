@@ -204,6 +204,7 @@ __device__ __forceinline__ GemvPart pick_part(const GemvArgs& a, int pu) {
   p.rope_role = pu == 0 ? p.rope_role : (pu == 1 ? b.rope_role : c.rope_role);
   p.corr = pu == 0 ? p.corr : (pu == 1 ? b.corr : c.corr);
   p.corr_kmax = pu == 0 ? p.corr_kmax : (pu == 1 ? b.corr_kmax : c.corr_kmax);
+  p.xcodes = pu == 0 ? p.xcodes : (pu == 1 ? b.xcodes : c.xcodes);
   p.wrows = pu == 0 ? p.wrows : (pu == 1 ? b.wrows : c.wrows);
   return p;
 }
@@ -1994,6 +1995,27 @@ __device__ __forceinline__ float xm_input(const uint8_t* tb, const float* s_e, u
   return float(X) * s_e[(w * 4 + S) * 4 + g];
 }
 
+// The 16 code bytes lane (n, q) of wave w reads for set S of the unit at row base rb: unit row
+// n / 4 (SwiGlu: rows 2 and 3 from the up part), group 16 w + 4 S + n % 4, quarter q, in the
+// records (rows past the tiles and groups past the input read row 0 / group 0; their products
+// are not used).  The launch's permuted copy (GemvPart::xcodes) holds the same bytes at
+// u * xm_unit_bytes(NW) + ((w * 4 + S) * 64 + lane) * 16: each load instruction of a wave then
+// reads 1 KB of contiguous memory instead of four 256-byte runs.
+template <int R, int MODE>
+__device__ __forceinline__ const uint8_t* xm_code_at(const GemvPart& P0, const GemvPart& P1, uint32_t rb,
+                                                     uint32_t half, uint32_t ng, uint32_t gw, int S, int n, int q) {
+  constexpr bool kSwi = MODE == int(GemvMode::SwiGlu);
+  const uint32_t ia = uint32_t(n >> 2);
+  const bool sa = kSwi && ia >= R / 2;
+  const uint32_t ra = row_of<R, MODE>(rb, int(ia), half);
+  const uint32_t wa = sa ? uni(P1.wrows) : uni(P0.wrows);
+  const uint8_t* ba = sa ? uni(P1.base) : uni(P0.base);
+  const uint32_t sta = sa ? uni(P1.stride) : uni(P0.stride);
+  const uint32_t g = gw + 4 * uint32_t(S) + uint32_t(n & 3), gc = g < ng ? g : 0u;
+  const uint32_t Ga = (ra < wa ? ra : 0u) * ng + gc;
+  return ba + ((Ga >> 8) * sta + 64 + (Ga & 255u) * 64 + 16 * uint32_t(q));
+}
+
 template <int MODE, int NW>
 __global__ void __launch_bounds__(kWave * NW) k_gemv_xm(GemvArgs a) {
   constexpr int R = 4;
@@ -2041,20 +2063,23 @@ __global__ void __launch_bounds__(kWave * NW) k_gemv_xm(GemvArgs a) {
     const uint32_t rb = xs_row_base<R, MODE>(P0, u, half);
     L->pu = pu;
     L->row_base = rb;
-    {  // codes: unit row n / 4; scales: unit row q (each in its part, rows past the tiles read row 0)
-      const uint32_t ia = uint32_t(n >> 2), is = uint32_t(q);
-      const bool sa = kSwi && ia >= R / 2, ss = kSwi && is >= R / 2;
-      const uint32_t ra = row_of<R, MODE>(rb, int(ia), half), rs = row_of<R, MODE>(rb, int(is), half);
-      const uint32_t wa = sa ? uni(P1.wrows) : uni(P0.wrows), ws = ss ? uni(P1.wrows) : uni(P0.wrows);
-      const uint8_t* ba = sa ? uni(P1.base) : uni(P0.base);
+    {  // codes (xm_code_at, or the permuted copy); scales: unit row q (each in its part, rows
+       // past the tiles read row 0)
+      const uint32_t is = uint32_t(q);
+      const bool ss = kSwi && is >= R / 2;
+      const uint32_t rs = row_of<R, MODE>(rb, int(is), half);
+      const uint32_t ws = ss ? uni(P1.wrows) : uni(P0.wrows);
       const uint8_t* bs = ss ? uni(P1.base) : uni(P0.base);
-      const uint32_t sta = sa ? uni(P1.stride) : uni(P0.stride), sts = ss ? uni(P1.stride) : uni(P0.stride);
-      const uint32_t Ga0 = (ra < wa ? ra : 0u) * ng, Gs0 = (rs < ws ? rs : 0u) * ng;
+      const uint32_t sts = ss ? uni(P1.stride) : uni(P0.stride);
+      const uint32_t Gs0 = (rs < ws ? rs : 0u) * ng;
+      const uint8_t* xc = uni(P0.xcodes);
 #pragma unroll
       for (int S = 0; S < 4; ++S) {
         const uint32_t g = gw + 4 * uint32_t(S) + uint32_t(n & 3), gc = g < ng ? g : 0u;
-        const uint32_t Ga = Ga0 + gc, Gs = Gs0 + gc;
-        L->q[S] = ld_u128(ba + ((Ga >> 8) * sta + 64 + (Ga & 255u) * 64 + 16 * uint32_t(q)));
+        const uint32_t Gs = Gs0 + gc;
+        const uint8_t* src = xc ? xc + (u * (NW * 4096u) + ((wave * 4 + uint32_t(S)) * 64 + uint32_t(lane)) * 16)
+                                : xm_code_at<R, MODE>(P0, P1, rb, half, ng, gw, S, n, q);
+        L->q[S] = ld_u128(src);
         L->s[S] = ld_u16(bs + ((Gs >> 8) * sts + 16448 + 48 + 2 * (Gs & 255u)));
       }
     }
@@ -2279,6 +2304,38 @@ bool launch_xm(const GemvArgs& a, const GemvLaunch& g, hipStream_t st) {
     case 4: launch_kernel_lds(&k_gemv_xm<MODE, 4>, gr, bl, lds, st, a); return true;
     case 8: launch_kernel_lds(&k_gemv_xm<MODE, 8>, gr, bl, lds, st, a); return true;
     case 16: launch_kernel_lds(&k_gemv_xm<MODE, 16>, gr, bl, lds, st, a); return true;
+    default: return false;
+  }
+}
+
+// The permuted copy of a launch's codes for k_gemv_xm: thread (w, lane) of workgroup u copies
+// the 16 bytes of each set S that the kernel's lane reads for unit u (xm_code_at) to
+// dst + u * NW * 4096 + ((w * 4 + S) * 64 + lane) * 16.
+template <int MODE, int NW>
+__global__ void __launch_bounds__(kWave * NW) k_xm_layout(GemvArgs a, uint8_t* dst) {
+  constexpr int R = 4;
+  const int lane = threadIdx.x & 63, n = lane & 15, q = lane >> 4;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), u = blockIdx.x;
+  const uint32_t ng = a.C >> 7, half = a.rope.head_dim / 2, gw = wave * 16;
+  const GemvPart P0 = a.part[0];
+  const GemvPart& P1 = MODE == int(GemvMode::SwiGlu) ? a.part[1] : P0;
+  const uint32_t rb = xs_row_base<R, MODE>(P0, u, half);
+#pragma unroll
+  for (int S = 0; S < 4; ++S) {
+    const uint4 v = ld_u128(xm_code_at<R, MODE>(P0, P1, rb, half, ng, gw, S, n, q));
+    *reinterpret_cast<uint4*>(dst + (size_t(u) * (NW * 4096u) + ((wave * 4 + uint32_t(S)) * 64 + uint32_t(lane)) * 16)) = v;
+  }
+}
+
+template <int MODE>
+bool launch_xm_layout(const GemvArgs& a, const GemvLaunch& g, uint8_t* dst, hipStream_t st) {
+  const dim3 gr(a.n_units), bl(g.threads);
+  switch (g.threads / kWave) {
+    case 1: launch_kernel(&k_xm_layout<MODE, 1>, gr, bl, st, a, dst); return true;
+    case 2: launch_kernel(&k_xm_layout<MODE, 2>, gr, bl, st, a, dst); return true;
+    case 4: launch_kernel(&k_xm_layout<MODE, 4>, gr, bl, st, a, dst); return true;
+    case 8: launch_kernel(&k_xm_layout<MODE, 8>, gr, bl, st, a, dst); return true;
+    case 16: launch_kernel(&k_xm_layout<MODE, 16>, gr, bl, st, a, dst); return true;
     default: return false;
   }
 }
@@ -2539,6 +2596,9 @@ const GemvTuning& gemv_tuning() {
         v.xm_wpc_wide = w[3];
       }
     }
+    if (const char* e = std::getenv("CHPE_XM_LAYOUT")) v.xm_layout = e[0] == '0' ? 0u : 1u;
+    if (const char* e = std::getenv("CHPE_GEMV_XM_WPC_GATEUP")) v.xm_wpc_gateup = uint32_t(std::strtoul(e, nullptr, 10));
+    if (v.xm_wpc_gateup == 0) v.xm_wpc_gateup = 1;
     if (const char* e = std::getenv("CHPE_GEMV_XS_MIN_UNITS")) v.xs_min_units = uint32_t(std::strtoul(e, nullptr, 10));
     if (const char* e = std::getenv("CHPE_GEMV_XM_MIN_MB")) v.xm_min_mb = uint32_t(std::strtoul(e, nullptr, 10));
     if (const char* e = std::getenv("CHPE_GEMV_XS_WPC")) {
@@ -2604,7 +2664,9 @@ GemvLaunch gemv_geometry(WeightKind kind, GemvMode mode, uint32_t C, const uint3
       const GemvTuning& t = gemv_tuning();
       uint32_t wpc = nw >= 8 ? t.xm_wpc_wide
                      : mode == GemvMode::Logits ? t.xm_wpc_logits
-                     : units >= 4096 ? t.xm_wpc_large : t.xm_wpc_small;
+                     : units >= 4096 ? (mode == GemvMode::SwiGlu && nw == 4 && t.xm_layout ? t.xm_wpc_gateup
+                                                                                            : t.xm_wpc_large)
+                     : t.xm_wpc_small;
       if (nw < 4) wpc *= 4 / nw;  // narrower inputs: as many waves per CU as at 8192 columns
       GemvLaunch g{};
       g.ru = R;
@@ -2761,6 +2823,24 @@ uint32_t launch_gemv_poly(const GemvArgs& a, const PolyPlan* const* plans, float
     case GemvMode::QkvRope: launch_kernel(&k_poly_epilogue<int(GemvMode::QkvRope)>, dim3(blocks), dim3(256), st, a, raw); break;
   }
   return blocks;
+}
+
+size_t xm_layout_bytes(WeightKind kind, const GemvArgs& a, const GemvLaunch& g) {
+  const GemvMode m = GemvMode(a.mode);
+  const uint32_t nw = g.threads / kWave;
+  if (!gemv_tuning().xm_layout || kind != WeightKind::FlatW4 || !g.xm ||
+      (m != GemvMode::SwiGlu && m != GemvMode::Logits) || a.C != nw * 2048u)
+    return 0;
+  const size_t bytes = size_t(a.n_units) * nw * 4096u;
+  return bytes < (size_t(1) << 32) ? bytes : 0;
+}
+
+bool build_xm_layout(const GemvArgs& a, const GemvLaunch& g, uint8_t* dst, hipStream_t st) {
+  switch (GemvMode(a.mode)) {
+    case GemvMode::SwiGlu: return launch_xm_layout<int(GemvMode::SwiGlu)>(a, g, dst, st);
+    case GemvMode::Logits: return launch_xm_layout<int(GemvMode::Logits)>(a, g, dst, st);
+    default: return false;
+  }
 }
 
 void launch_gemv(WeightKind kind, const GemvArgs& a, const GemvLaunch& g, hipStream_t st) {

@@ -71,6 +71,8 @@ struct GemvPart {
   uint32_t replace_outliers;  // Cell16W4: outliers replace (tied LM head) instead of add
   uint32_t rope_role;         // QkvRope: RopeRole of this part
   const struct CellReplace* repl;  // Cell16W4 replace mode: per-cell corrections (see below)
+  const uint8_t* xcodes;      // FlatW4 on the persistent matrix-core kernel (part 0): the launch's
+                              //   codes in that kernel's load order, or null (read from the records)
 };
 
 // Replace-mode outliers of one 16-row cell, prepared at load time: entry k replaces column
@@ -193,6 +195,12 @@ struct GemvTuning {
   uint32_t xm = 1;     // flat 4-bit tiles on the matrix-core input-stationary kernel (CHPE_GEMV_XM; 0: off)
   // its persistent workgroups per CU (CHPE_GEMV_XM_WPC=small,large,logits,wide as below)
   uint32_t xm_wpc_small = 2, xm_wpc_large = 3, xm_wpc_logits = 2, xm_wpc_wide = 1;
+  // the permuted code copies of the gate/up and LM head launches (xm_layout_bytes;
+  // CHPE_XM_LAYOUT=0: the kernel reads the records), and the persistent workgroups per CU of the
+  // gate/up launches of 4096 units or more at 4 waves (8192 columns) that read such a copy
+  // (CHPE_GEMV_XM_WPC_GATEUP; without the copy: xm_wpc_large)
+  uint32_t xm_layout = 1;
+  uint32_t xm_wpc_gateup = 2;
   uint32_t xs = 1;     // flat tiles on the input-stationary persistent kernel (CHPE_GEMV_XS; 0: off)
   // its persistent workgroups per CU (256 CUs): launches of < 4096 units, of more, the LM head,
   // and inputs wider than 8192 columns (CHPE_GEMV_XS_WPC=small,large,logits,wide)
@@ -288,6 +296,12 @@ void launch_block_finish(const BlockFinishArgs& a, hipStream_t stream);
 // launchers; all enqueue on `stream` and never synchronise
 void launch_embed(const EmbedArgs& a, hipStream_t stream);
 void launch_gemv(WeightKind kind, const GemvArgs& a, const GemvLaunch& g, hipStream_t stream);
+// The permuted copy of a launch's 4-bit codes for the persistent matrix-core kernel
+// (GemvPart::xcodes): its size in bytes, or 0 where it is not built (another kernel, another
+// mode than SwiGlu / Logits, an input that leaves a wave's columns partly empty, 4 GiB or more);
+// build_xm_layout enqueues the copy into dst (that many bytes).
+size_t xm_layout_bytes(WeightKind kind, const GemvArgs& a, const GemvLaunch& g);
+bool build_xm_layout(const GemvArgs& a, const GemvLaunch& g, uint8_t* dst, hipStream_t stream);
 // Gated-DeltaNet decode step (Qwen3.5 linear-attention layers; deltanet.hip).
 constexpr uint32_t kDnMaxTaps = 8;
 struct DnConvArgs {         // depthwise causal conv update + SiLU
