@@ -2303,6 +2303,7 @@ bool launch_xm(const GemvArgs& a, const GemvLaunch& g, hipStream_t st) {
     case 2: launch_kernel_lds(&k_gemv_xm<MODE, 2>, gr, bl, lds, st, a); return true;
     case 4: launch_kernel_lds(&k_gemv_xm<MODE, 4>, gr, bl, lds, st, a); return true;
     case 8: launch_kernel_lds(&k_gemv_xm<MODE, 8>, gr, bl, lds, st, a); return true;
+    case 15: launch_kernel_lds(&k_gemv_xm<MODE, 15>, gr, bl, lds, st, a); return true;
     case 16: launch_kernel_lds(&k_gemv_xm<MODE, 16>, gr, bl, lds, st, a); return true;
     default: return false;
   }
@@ -2632,7 +2633,9 @@ GemvLaunch gemv_geometry(WeightKind kind, GemvMode mode, uint32_t C, const uint3
   if (kind == WeightKind::FlatW4 && gemv_tuning().xm && C % 128 == 0 && C <= 32768) {
     // the matrix-core input-stationary kernel: waves of 2048 columns, units of 4 rows
     const uint32_t need = (C + 2047) / 2048;
-    const uint32_t nw = need <= 1 ? 1u : need <= 2 ? 2u : need <= 4 ? 4u : need <= 8 ? 8u : 16u;
+    // (15 columns of waves exactly: the 72B down projection's 29568 columns; a 16th wave would
+    // hold no group and still join every unit's barrier)
+    const uint32_t nw = need <= 1 ? 1u : need <= 2 ? 2u : need <= 4 ? 4u : need <= 8 ? 8u : need == 15 ? 15u : 16u;
     constexpr uint32_t R = 4;
     bool ok = true;
     if (mode == GemvMode::QkvRope)  // whole units per part (head dims are 128 or 256: whole pairs per unit)
