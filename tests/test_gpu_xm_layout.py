@@ -1,0 +1,85 @@
+"""The permuted code copy of the matrix-core flat GEMV (k_xm_layout; gemvCellFlat,
+src/chpe_engine.zig:584-729).  The engine writes the gate/up and LM head codes once more in the
+kernel's load order, and the kernel then reads each lane's 16 bytes from the copy instead of
+the records.  The copy holds the same bytes for the same lanes, so the outputs must be bit for
+bit those of the records path: each case runs here (copy) and in a child process started with
+CHPE_XM_LAYOUT=0 (records, read once per process), on the same inputs.  Both are also checked
+against the oracle by test_gpu_gemv_flat.py."""
+import os
+import subprocess
+import sys
+import tempfile
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+import chpe_amd as ca
+
+pytestmark = pytest.mark.gpu
+
+ROOT = Path(__file__).resolve().parents[1]
+TILE = 32768
+
+CHILD = r"""
+import sys
+import numpy as np
+sys.path.insert(0, sys.argv[1])
+import chpe_amd as ca
+d = np.load(sys.argv[2])
+mode = str(d["mode"])
+up = d["up"] if d["up"].size else None
+g = d["gamma"] if d["gamma"].size else None
+r = ca.gpu_gemv_flat(mode, int(d["rows"]), int(d["cols"]), d["cells"], d["x"], tiles_up=up, gamma=g, eps=1e-6)
+y = r[0] if mode == "logits" else r
+extra = np.array([r[1], np.float32(r[2]).view(np.uint32)] if mode == "logits" else [], np.uint32)
+np.save(sys.argv[3], np.concatenate([y.view(np.uint32), extra]))
+"""
+
+
+def say(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def make_tiles(rng, rows, cols):
+    n = rows * cols
+    w = (rng.standard_normal(n) * 0.02).astype(np.float32)
+    hot = rng.choice(n, size=max(1, n // 2000), replace=False)
+    w[hot] = (rng.standard_normal(hot.size) * 0.5).astype(np.float32)
+    n_tiles = (n + TILE - 1) // TILE
+    w = np.concatenate([w, np.zeros(n_tiles * TILE - n, np.float32)])
+    return np.stack([ca.pack_flat(w[t * TILE:(t + 1) * TILE], bits=4, n_outliers=64) for t in range(n_tiles)])
+
+
+CASES = [  # (mode, rows, cols): every one on the matrix-core kernel with the copy
+    ("swiglu", 8192, 8192),   # 4096 units at 4 waves, 2 workgroups per CU
+    ("logits", 300, 8192),
+    ("logits", 90, 4096),     # 2 waves
+]
+
+
+@pytest.mark.parametrize("mode,rows,cols", CASES)
+def test_permuted_codes_match_records(mode, rows, cols):
+    rng = np.random.default_rng(rows + cols)
+    say(f"xm layout mode={mode} rows={rows} cols={cols}")
+    cells = make_tiles(rng, rows, cols)
+    up = make_tiles(rng, rows, cols) if mode == "swiglu" else None
+    x = rng.standard_normal(cols).astype(np.float32)
+    gamma = (rng.standard_normal(cols) * 0.2 + 1.0).astype(np.float32)
+    r = ca.gpu_gemv_flat(mode, rows, cols, cells, x, tiles_up=up, gamma=gamma, eps=1e-6)
+    y = r[0] if mode == "logits" else r
+    got = np.concatenate([y.view(np.uint32),
+                          np.array([r[1], np.float32(r[2]).view(np.uint32)] if mode == "logits" else [], np.uint32)])
+    with tempfile.TemporaryDirectory() as td:
+        inp, out = os.path.join(td, "in.npz"), os.path.join(td, "out.npy")
+        np.savez(inp, mode=np.array(mode), rows=np.array(rows), cols=np.array(cols), cells=cells, x=x,
+                 up=up if up is not None else np.zeros(0, np.uint8), gamma=gamma)
+        env = dict(os.environ, CHPE_XM_LAYOUT="0")
+        say("  records path in a child process")
+        subprocess.run([sys.executable, "-c", CHILD, str(ROOT / "chpe-qwen-engine_amd"), inp, out], env=env,
+                       check=True, timeout=300)
+        want = np.load(out)
+    assert got.shape == want.shape
+    bad = np.flatnonzero(got != want)
+    assert bad.size == 0, f"{bad.size} outputs differ, first at {int(bad[0])}"
