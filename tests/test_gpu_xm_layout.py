@@ -75,7 +75,8 @@ def test_permuted_codes_match_records(mode, rows, cols):
         inp, out = os.path.join(td, "in.npz"), os.path.join(td, "out.npy")
         np.savez(inp, mode=np.array(mode), rows=np.array(rows), cols=np.array(cols), cells=cells, x=x,
                  up=up if up is not None else np.zeros(0, np.uint8), gamma=gamma)
-        env = dict(os.environ, CHPE_XM_LAYOUT="0")
+        # (2 workgroups per CU as with the copy, so that the launches differ in the code source only)
+        env = dict(os.environ, CHPE_XM_LAYOUT="0", CHPE_GEMV_XM_WPC="2,2,2,1")
         say("  records path in a child process")
         subprocess.run([sys.executable, "-c", CHILD, str(ROOT / "chpe-qwen-engine_amd"), inp, out], env=env,
                        check=True, timeout=300)
