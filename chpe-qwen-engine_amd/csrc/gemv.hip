@@ -1964,14 +1964,16 @@ __global__ void __launch_bounds__(kWave * NW) k_gemv_xs(GemvArgs a) {
 //   B (64 x 16): column n = g' + 4 L -> limb L of the input in group g' (the same half),
 // so D(r, g; g', L) is the exact integer sum over the half of code * limb where g == g', starting
 // at -8 * (the limb's sum over the group) for the codes' offset.  Lane (n, q) holds D(q, j; n % 4,
-// n / 4) for j = 0..3 and keeps j = n % 4: times 2^(8 L) 2^(e - 30), summed over the limbs (DPP),
-// times the group scale, summed over the set's groups (DPP) -- row q's sum over the set.  Each
-// lane loads 16 bytes of unit row n / 4, group n % 4, quarter q per set: the unit's rows as
-// 256-byte runs.  The grid is persistent; the next unit's loads are issued before the current
+// n / 4) for j = 0..3 and keeps j = n % 4, times 2^(8 L) 2^(e - 30) and the group scale; it adds
+// these over the four sets (and its share of row q's corrections), and row q's sum over its 16
+// lanes (the limbs, then the groups; DPP) is taken once per unit.  Each lane loads 16 bytes of unit row n / 4, group n % 4, quarter q per set: the unit's rows as
+// 256-byte runs in the records, or 1 KB contiguous per load from the launch's permuted copy
+// (xm_code_at).  The grid is persistent; the next unit's loads are issued before the current
 // unit's products.  Row sums meet over the waves in LDS (double-buffered, in wave order); wave 0
 // runs the epilogue.  Outliers replace weights (:632-646): per-row corrections
 // (w_out - dequantised code) * x[col] on the 16 lanes of each row, with x[col] rebuilt from the
-// limb tables (the same integers the products use).
+// limb tables (the same integers the products use).  The residual modes skip the input's sum of
+// squares.
 constexpr uint32_t kXmTableBytes = 4 * 128 * 16;  // per wave: 4 sets x (group, quarter, half, limb) x 16 bytes
 
 template <int R, int SPL>
@@ -1999,8 +2001,8 @@ __device__ __forceinline__ float xm_input(const uint8_t* tb, const float* s_e, u
 // n / 4 (SwiGlu: rows 2 and 3 from the up part), group 16 w + 4 S + n % 4, quarter q, in the
 // records (rows past the tiles and groups past the input read row 0 / group 0; their products
 // are not used).  The launch's permuted copy (GemvPart::xcodes) holds the same bytes at
-// u * xm_unit_bytes(NW) + ((w * 4 + S) * 64 + lane) * 16: each load instruction of a wave then
-// reads 1 KB of contiguous memory instead of four 256-byte runs.
+// u * NW * 4096 + ((w * 4 + S) * 64 + lane) * 16: each load instruction of a wave then reads
+// 1 KB of contiguous memory instead of four 256-byte runs.
 template <int R, int MODE>
 __device__ __forceinline__ const uint8_t* xm_code_at(const GemvPart& P0, const GemvPart& P1, uint32_t rb,
                                                      uint32_t half, uint32_t ng, uint32_t gw, int S, int n, int q) {
