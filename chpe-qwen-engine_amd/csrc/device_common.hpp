@@ -57,6 +57,11 @@ __device__ __forceinline__ float4 ld_f4(const float* p) {
   const f32x4_t v = gld(reinterpret_cast<const f32x4_t*>(p));
   return make_float4(v.x, v.y, v.z, v.w);
 }
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint2 ld_u64(const uint8_t* p) {
+  const u32x2_t v = gld(reinterpret_cast<const u32x2_t*>(p));
+  return make_uint2(v.x, v.y);
+}
 __device__ __forceinline__ uint4 ld_u128(const uint8_t* p) {
   const u32x4_t v = gld(reinterpret_cast<const u32x4_t*>(p));
   return make_uint4(v.x, v.y, v.z, v.w);

@@ -1987,11 +1987,16 @@ struct XmLoads {
   int pu;
 };
 
-// x'[col] from the limb tables: the integer X of the column times 2^(e - 30) of its group
+// x'[col] from the limb tables: the integer X of the column times 2^(e - 30) of its group.
+// Within a 16-column block's 16 bytes per limb, 4-bit tables hold the columns in the order
+// {0,2,4,6}, {1,3,5,7}, {8,10,12,14}, {9,11,13,15} (the nibbles of the codes), 2-bit tables in
+// the order {0,4,8,12}, {1,5,9,13}, {2,6,10,14}, {3,7,11,15} (the 2-bit fields).
+template <int BITS = 4>
 __device__ __forceinline__ float xm_input(const uint8_t* tb, const float* s_e, uint32_t col) {
   const uint32_t w = col >> 11, S = (col >> 9) & 3u, g = (col >> 7) & 3u, c = col & 127u;
-  const uint32_t q = c >> 5, h = (c >> 4) & 1u, p = (c >> 3) & 1u, i = c & 7u;
-  const uint32_t at = (w * 4 + S) * 128 * 16 + (((g * 4 + q) * 2 + h) * 4) * 16 + 4 * (2 * p + (i & 1u)) + (i >> 1);
+  const uint32_t q = c >> 5, h = (c >> 4) & 1u, p = (c >> 3) & 1u, i = c & 7u, c16 = c & 15u;
+  const uint32_t in16 = BITS == 2 ? 4 * (c16 & 3u) + (c16 >> 2) : 4 * (2 * p + (i & 1u)) + (i >> 1);
+  const uint32_t at = (w * 4 + S) * 128 * 16 + (((g * 4 + q) * 2 + h) * 4) * 16 + in16;
   const int X = int(int8_t(tb[at])) + (int(int8_t(tb[at + 16])) << 8) + (int(int8_t(tb[at + 32])) << 16) +
                 (int(int8_t(tb[at + 48])) << 24);
   return float(X) * s_e[(w * 4 + S) * 4 + g];
@@ -2003,7 +2008,7 @@ __device__ __forceinline__ float xm_input(const uint8_t* tb, const float* s_e, u
 // are not used).  The launch's permuted copy (GemvPart::xcodes) holds the same bytes at
 // u * NW * 4096 + ((w * 4 + S) * 64 + lane) * 16: each load instruction of a wave then reads
 // 1 KB of contiguous memory instead of four 256-byte runs.
-template <int R, int MODE>
+template <int R, int MODE, int BITS = 4>
 __device__ __forceinline__ const uint8_t* xm_code_at(const GemvPart& P0, const GemvPart& P1, uint32_t rb,
                                                      uint32_t half, uint32_t ng, uint32_t gw, int S, int n, int q) {
   constexpr bool kSwi = MODE == int(GemvMode::SwiGlu);
@@ -2015,12 +2020,19 @@ __device__ __forceinline__ const uint8_t* xm_code_at(const GemvPart& P0, const G
   const uint32_t sta = sa ? uni(P1.stride) : uni(P0.stride);
   const uint32_t g = gw + 4 * uint32_t(S) + uint32_t(n & 3), gc = g < ng ? g : 0u;
   const uint32_t Ga = (ra < wa ? ra : 0u) * ng + gc;
+  if constexpr (BITS == 2)  // 32 bytes per group: quarter q is 8 bytes (the same 32 columns)
+    return ba + ((Ga >> 8) * sta + 64 + (Ga & 255u) * 32 + 8 * uint32_t(q));
   return ba + ((Ga >> 8) * sta + 64 + (Ga & 255u) * 64 + 16 * uint32_t(q));
 }
 
-template <int MODE, int NW>
+// BITS = 2: 2-bit flat tiles.  Their codebook {0, +1, -2, -1} is the 2-bit two's complement, so
+// (code ^ 2) - 2 is the weight: the products take code ^ 2 (0..3) as the A operand and start at
+// -2 * (the limb's sum over the group).  A lane reads 8 bytes per set (the same 32 columns of its
+// group quarter); the B tables hold the 2-bit field order (xm_input).
+template <int MODE, int NW, int BITS = 4>
 __global__ void __launch_bounds__(kWave * NW) k_gemv_xm(GemvArgs a) {
   constexpr int R = 4;
+  static_assert(BITS == 4 || BITS == 2, "4- or 2-bit flat tiles");
   constexpr bool kNorm = kNormOf<MODE>;
   constexpr bool kSwi = MODE == int(GemvMode::SwiGlu);
   constexpr bool kRope = MODE == int(GemvMode::QkvRope);
@@ -2079,9 +2091,14 @@ __global__ void __launch_bounds__(kWave * NW) k_gemv_xm(GemvArgs a) {
       for (int S = 0; S < 4; ++S) {
         const uint32_t g = gw + 4 * uint32_t(S) + uint32_t(n & 3), gc = g < ng ? g : 0u;
         const uint32_t Gs = Gs0 + gc;
-        const uint8_t* src = xc ? xc + (u * (NW * 4096u) + ((wave * 4 + uint32_t(S)) * 64 + uint32_t(lane)) * 16)
-                                : xm_code_at<R, MODE>(P0, P1, rb, half, ng, gw, S, n, q);
-        L->q[S] = ld_u128(src);
+        if constexpr (BITS == 2) {
+          const uint2 v = ld_u64(xm_code_at<R, MODE, 2>(P0, P1, rb, half, ng, gw, S, n, q));
+          L->q[S] = make_uint4(v.x, v.y, 0u, 0u);
+        } else {
+          const uint8_t* src = xc ? xc + (u * (NW * 4096u) + ((wave * 4 + uint32_t(S)) * 64 + uint32_t(lane)) * 16)
+                                  : xm_code_at<R, MODE>(P0, P1, rb, half, ng, gw, S, n, q);
+          L->q[S] = ld_u128(src);
+        }
         L->s[S] = ld_u16(bs + ((Gs >> 8) * sts + 16448 + 48 + 2 * (Gs & 255u)));
       }
     }
@@ -2177,8 +2194,24 @@ __global__ void __launch_bounds__(kWave * NW) k_gemv_xm(GemvArgs a) {
 #pragma unroll
     for (int i = 0; i < 8; ++i) z[i] = (uint32_t(int(xp[i] * up)) + 0x808080u) ^ 0x808080u;
     uint32_t lo[4], hi[4];
-    limb_words(z[0], z[2], z[4], z[6], lo);
-    limb_words(z[1], z[3], z[5], z[7], hi);
+    if constexpr (BITS == 2) {
+      // lanes 2k, 2k + 1 hold columns 0..7 and 8..15 of a 16-column block; the 2-bit order wants
+      // {0,4,8,12}, {1,5,9,13} in the even lane and {2,6,10,14}, {3,7,11,15} in the odd one:
+      // each sends the four its neighbour needs
+      const bool odd = (lane & 1) != 0;
+      const uint32_t r0 = pair_u(odd ? z[0] : z[2], 1), r1 = pair_u(odd ? z[1] : z[3], 1);
+      const uint32_t r2 = pair_u(odd ? z[4] : z[6], 1), r3 = pair_u(odd ? z[5] : z[7], 1);
+      if (odd) {  // columns 2, 6, 10, 14 and 3, 7, 11, 15
+        limb_words(r0, r2, z[2], z[6], lo);
+        limb_words(r1, r3, z[3], z[7], hi);
+      } else {    // columns 0, 4, 8, 12 and 1, 5, 9, 13
+        limb_words(z[0], z[4], r0, r2, lo);
+        limb_words(z[1], z[5], r1, r3, hi);
+      }
+    } else {
+      limb_words(z[0], z[2], z[4], z[6], lo);
+      limb_words(z[1], z[3], z[5], z[7], hi);
+    }
     const uint32_t gs = uint32_t(lane) >> 4, gq = (uint32_t(lane) >> 2) & 3u, gh = (uint32_t(lane) >> 1) & 1u;
 #pragma unroll
     for (int L = 0; L < 4; ++L) {
@@ -2189,7 +2222,7 @@ __global__ void __launch_bounds__(kWave * NW) k_gemv_xm(GemvArgs a) {
       sl += int(pair_u(uint32_t(sl), 2));
       sl += int(pair_u(uint32_t(sl), 4));
       sl += int(pair_u(uint32_t(sl), 8));
-      if ((lane & 15) == 0) s_ci[wave][S][gs + 4 * uint32_t(L)] = -8 * sl;
+      if ((lane & 15) == 0) s_ci[wave][S][gs + 4 * uint32_t(L)] = (BITS == 2 ? -2 : -8) * sl;
     }
     if ((lane & 15) == 0)
       s_e[(wave * 4 + uint32_t(S)) * 4 + gs] = isfinite(mx) ? ldexpf(1.0f, e - 30) : __int_as_float(0x7fc00000);
@@ -2221,7 +2254,7 @@ __global__ void __launch_bounds__(kWave * NW) k_gemv_xm(GemvArgs a) {
       for (int t = 0; t < SPL; ++t) {
         if (16u * (wsl + uint32_t(NW * t)) < km) {
           const bool on = ((L.cuse >> t) & 1u) && L.ce[t].y != 0.0f;
-          const float xc = xm_input(tbytes, s_e, on ? __float_as_uint(L.ce[t].x) : 0u);
+          const float xc = xm_input<BITS>(tbytes, s_e, on ? __float_as_uint(L.ce[t].x) : 0u);
           acc = on ? fmaf(L.ce[t].y, xc, acc) : acc;
         }
       }
@@ -2236,9 +2269,16 @@ __global__ void __launch_bounds__(kWave * NW) k_gemv_xm(GemvArgs a) {
       for (int h = 0; h < 2; ++h) {
         const uint4 t = tbw[uint32_t(S) * 128 + (((uint32_t(n & 3) * 4 + uint32_t(q)) * 2 + uint32_t(h)) * 4) + uint32_t(n >> 2)];
         const i32x4_t B = {int(t.x), int(t.y), int(t.z), int(t.w)};
-        const uint32_t w0 = w4[2 * h], w1 = w4[2 * h + 1];
-        const i32x4_t A = {int(w0 & 0x0f0f0f0fu), int((w0 >> 4) & 0x0f0f0f0fu), int(w1 & 0x0f0f0f0fu),
-                           int((w1 >> 4) & 0x0f0f0f0fu)};
+        i32x4_t A;
+        if constexpr (BITS == 2) {  // 16 codes in 4 bytes: field k of each byte, code ^ 2
+          const uint32_t w = w4[h] ^ 0xAAAAAAAAu;
+          A = i32x4_t{int(w & 0x03030303u), int((w >> 2) & 0x03030303u), int((w >> 4) & 0x03030303u),
+                      int((w >> 6) & 0x03030303u)};
+        } else {
+          const uint32_t w0 = w4[2 * h], w1 = w4[2 * h + 1];
+          A = i32x4_t{int(w0 & 0x0f0f0f0fu), int((w0 >> 4) & 0x0f0f0f0fu), int(w1 & 0x0f0f0f0fu),
+                      int((w1 >> 4) & 0x0f0f0f0fu)};
+        }
         D = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, B, D, 0, 0, 0);
       }
       const int j = n & 3;
@@ -2295,18 +2335,18 @@ __global__ void __launch_bounds__(kWave * NW) k_gemv_xm(GemvArgs a) {
   }
 }
 
-template <int MODE>
+template <int MODE, int BITS = 4>
 bool launch_xm(const GemvArgs& a, const GemvLaunch& g, hipStream_t st) {
   const uint32_t nw = g.threads / kWave;
   const size_t lds = size_t(nw) * kXmTableBytes + size_t(nw) * 16 * 4;
   const dim3 gr(g.blocks), bl(g.threads);
   switch (nw) {
-    case 1: launch_kernel_lds(&k_gemv_xm<MODE, 1>, gr, bl, lds, st, a); return true;
-    case 2: launch_kernel_lds(&k_gemv_xm<MODE, 2>, gr, bl, lds, st, a); return true;
-    case 4: launch_kernel_lds(&k_gemv_xm<MODE, 4>, gr, bl, lds, st, a); return true;
-    case 8: launch_kernel_lds(&k_gemv_xm<MODE, 8>, gr, bl, lds, st, a); return true;
-    case 15: launch_kernel_lds(&k_gemv_xm<MODE, 15>, gr, bl, lds, st, a); return true;
-    case 16: launch_kernel_lds(&k_gemv_xm<MODE, 16>, gr, bl, lds, st, a); return true;
+    case 1: launch_kernel_lds(&k_gemv_xm<MODE, 1, BITS>, gr, bl, lds, st, a); return true;
+    case 2: launch_kernel_lds(&k_gemv_xm<MODE, 2, BITS>, gr, bl, lds, st, a); return true;
+    case 4: launch_kernel_lds(&k_gemv_xm<MODE, 4, BITS>, gr, bl, lds, st, a); return true;
+    case 8: launch_kernel_lds(&k_gemv_xm<MODE, 8, BITS>, gr, bl, lds, st, a); return true;
+    case 15: launch_kernel_lds(&k_gemv_xm<MODE, 15, BITS>, gr, bl, lds, st, a); return true;
+    case 16: launch_kernel_lds(&k_gemv_xm<MODE, 16, BITS>, gr, bl, lds, st, a); return true;
     default: return false;
   }
 }
@@ -2383,9 +2423,9 @@ void launch_one(const GemvArgs& a, const GemvLaunch& g, hipStream_t st) {
     if (g.cells == 2) { launch_kernel(&k_gemv_cells<MODE, 2>, dim3(g.blocks), dim3(g.threads), st, a); return; }
     if (g.cells == 4) { launch_kernel(&k_gemv_cells<MODE, 4>, dim3(g.blocks), dim3(g.threads), st, a); return; }
   }
-  if constexpr (std::is_same_v<F, FlatW4>) {
+  if constexpr (std::is_same_v<F, FlatW4> || std::is_same_v<F, FlatW2>) {
     if (g.xm) {
-      if (launch_xm<MODE>(a, g, st)) return;
+      if (launch_xm<MODE, std::is_same_v<F, FlatW2> ? 2 : 4>(a, g, st)) return;
       std::fprintf(stderr, "chpe: no matrix-core flat kernel for %u waves\n", g.threads / kWave);
       return;
     }
@@ -2600,6 +2640,7 @@ const GemvTuning& gemv_tuning() {
       }
     }
     if (const char* e = std::getenv("CHPE_XM_LAYOUT")) v.xm_layout = e[0] == '0' ? 0u : 1u;
+    if (const char* e = std::getenv("CHPE_GEMV_XM2")) v.xm2 = e[0] == '0' ? 0u : 1u;
     if (const char* e = std::getenv("CHPE_GEMV_XM_WPC_GATEUP")) v.xm_wpc_gateup = uint32_t(std::strtoul(e, nullptr, 10));
     if (v.xm_wpc_gateup == 0) v.xm_wpc_gateup = 1;
     if (const char* e = std::getenv("CHPE_GEMV_XS_MIN_UNITS")) v.xs_min_units = uint32_t(std::strtoul(e, nullptr, 10));
@@ -2632,7 +2673,8 @@ GemvLaunch gemv_geometry(WeightKind kind, GemvMode mode, uint32_t C, const uint3
                          uint32_t* n_units, uint32_t* n_panels, uint32_t* waves_per_unit,
                          uint32_t* unit_begin) {
   const uint32_t ru = 8;
-  if (kind == WeightKind::FlatW4 && gemv_tuning().xm && C % 128 == 0 && C <= 32768) {
+  if (((kind == WeightKind::FlatW4 && gemv_tuning().xm) || (kind == WeightKind::FlatW2 && gemv_tuning().xm2)) &&
+      C % 128 == 0 && C <= 32768) {
     // the matrix-core input-stationary kernel: waves of 2048 columns, units of 4 rows
     const uint32_t need = (C + 2047) / 2048;
     // (15 columns of waves exactly: the 72B down projection's 29568 columns; a 16th wave would
@@ -2646,7 +2688,9 @@ GemvLaunch gemv_geometry(WeightKind kind, GemvMode mode, uint32_t C, const uint3
     // projections -- run faster on the one-unit-per-workgroup kernels: the persistent grid's
     // start-up, the input's limb tables included, is not amortised over enough units; a launch
     // reading many codes in few wide units, the 72B down projection, amortises it all the same)
-    if (mode != GemvMode::Logits && !persistent_pays(rows, n_parts, mode, C)) {
+    // (2-bit tiles take the matrix-core kernel at every size: the vector-ALU kernels are
+    // bound by their arithmetic there)
+    if (kind == WeightKind::FlatW4 && mode != GemvMode::Logits && !persistent_pays(rows, n_parts, mode, C)) {
       uint32_t u = 0;
       for (int p = 0; p < (mode == GemvMode::SwiGlu ? 1 : n_parts); ++p)
         u += mode == GemvMode::SwiGlu ? (rows[p] + R / 2 - 1) / (R / 2) : (rows[p] + R - 1) / R;
@@ -2669,8 +2713,9 @@ GemvLaunch gemv_geometry(WeightKind kind, GemvMode mode, uint32_t C, const uint3
       const GemvTuning& t = gemv_tuning();
       uint32_t wpc = nw >= 8 ? t.xm_wpc_wide
                      : mode == GemvMode::Logits ? t.xm_wpc_logits
-                     : units >= 4096 ? (mode == GemvMode::SwiGlu && nw == 4 && t.xm_layout ? t.xm_wpc_gateup
-                                                                                            : t.xm_wpc_large)
+                     : units >= 4096 ? (mode == GemvMode::SwiGlu && nw == 4 && t.xm_layout && kind == WeightKind::FlatW4
+                                            ? t.xm_wpc_gateup
+                                            : t.xm_wpc_large)
                      : t.xm_wpc_small;
       if (nw < 4) wpc *= 4 / nw;  // narrower inputs: as many waves per CU as at 8192 columns
       GemvLaunch g{};

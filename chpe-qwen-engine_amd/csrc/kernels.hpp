@@ -193,6 +193,7 @@ struct GemvTuning {
                        // workgroup of a launch with >= 1024 tiles (CHPE_GEMV_MMA; 0: off)
   uint32_t mma_logits_blocks = 512;   // persistent workgroups of the matrix-core LM head (2 per CU)
   uint32_t xm = 1;     // flat 4-bit tiles on the matrix-core input-stationary kernel (CHPE_GEMV_XM; 0: off)
+  uint32_t xm2 = 1;    // flat 2-bit tiles on it (CHPE_GEMV_XM2; 0: the vector-ALU kernels)
   // its persistent workgroups per CU (CHPE_GEMV_XM_WPC=small,large,logits,wide as below)
   uint32_t xm_wpc_small = 2, xm_wpc_large = 3, xm_wpc_logits = 2, xm_wpc_wide = 1;
   // the permuted code copies of the gate/up and LM head launches (xm_layout_bytes;
