@@ -453,7 +453,7 @@ int chpe_debug_gemv_flat(int mode, uint32_t rows, uint32_t cols, const uint8_t* 
     const size_t xb = xm_layout_bytes(kind[0], a, g);
     if (xb) {
       uint8_t* dxc = static_cast<uint8_t*>(alloc(xb));
-      ok = dxc && build_xm_layout(a, g, dxc, nullptr);
+      ok = dxc && build_xm_layout(kind[0], a, g, dxc, nullptr);
       a.part[0].xcodes = dxc;
     }
   }

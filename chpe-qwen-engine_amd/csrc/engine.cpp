@@ -636,7 +636,7 @@ void Engine::build_xm_layout_of(ProjPlan* const* parts, int n, GemvMode mode, ui
     return;
   }
   allocs_.push_back(d);
-  if (build_xm_layout(a, g, static_cast<uint8_t*>(d), stream_)) parts[0]->xcodes = static_cast<uint8_t*>(d);
+  if (build_xm_layout(parts[0]->kind, a, g, static_cast<uint8_t*>(d), stream_)) parts[0]->xcodes = static_cast<uint8_t*>(d);
 }
 
 void Engine::build_xm_layouts() {

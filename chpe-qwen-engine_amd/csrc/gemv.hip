@@ -2029,10 +2029,14 @@ __device__ __forceinline__ const uint8_t* xm_code_at(const GemvPart& P0, const G
 // (code ^ 2) - 2 is the weight: the products take code ^ 2 (0..3) as the A operand and start at
 // -2 * (the limb's sum over the group).  A lane reads 8 bytes per set (the same 32 columns of its
 // group quarter); the B tables hold the 2-bit field order (xm_input).
-template <int MODE, int NW, int BITS = 4>
+// kXc (2-bit): the codes come from the launch's permuted copy, two sets per 16-byte load (a
+// compile-time choice: the two forms issue different numbers of loads, and a runtime branch
+// between them would leave every later wait counting the larger number)
+template <int MODE, int NW, int BITS = 4, bool kXc = false>
 __global__ void __launch_bounds__(kWave * NW) k_gemv_xm(GemvArgs a) {
   constexpr int R = 4;
   static_assert(BITS == 4 || BITS == 2, "4- or 2-bit flat tiles");
+  static_assert(!kXc || BITS == 2, "the 4-bit copy is read through the same loads as the records");
   constexpr bool kNorm = kNormOf<MODE>;
   constexpr bool kSwi = MODE == int(GemvMode::SwiGlu);
   constexpr bool kRope = MODE == int(GemvMode::QkvRope);
@@ -2091,7 +2095,13 @@ __global__ void __launch_bounds__(kWave * NW) k_gemv_xm(GemvArgs a) {
       for (int S = 0; S < 4; ++S) {
         const uint32_t g = gw + 4 * uint32_t(S) + uint32_t(n & 3), gc = g < ng ? g : 0u;
         const uint32_t Gs = Gs0 + gc;
-        if constexpr (BITS == 2) {
+        if constexpr (BITS == 2 && kXc) {  // sets S and S + 1 in one 16-byte load (the permuted copy)
+          if ((S & 1) == 0) {
+            const uint4 v = ld_u128(xc + (u * (NW * 2048u) + ((wave * 2 + uint32_t(S / 2)) * 64 + uint32_t(lane)) * 16));
+            L->q[S] = make_uint4(v.x, v.y, 0u, 0u);
+            L->q[S + 1] = make_uint4(v.z, v.w, 0u, 0u);
+          }
+        } else if constexpr (BITS == 2) {
           const uint2 v = ld_u64(xm_code_at<R, MODE, 2>(P0, P1, rb, half, ng, gw, S, n, q));
           L->q[S] = make_uint4(v.x, v.y, 0u, 0u);
         } else {
@@ -2335,26 +2345,30 @@ __global__ void __launch_bounds__(kWave * NW) k_gemv_xm(GemvArgs a) {
   }
 }
 
-template <int MODE, int BITS = 4>
+template <int MODE, int BITS = 4, bool kXc = false>
 bool launch_xm(const GemvArgs& a, const GemvLaunch& g, hipStream_t st) {
+  if constexpr (BITS == 2 && !kXc &&
+                (MODE == int(GemvMode::SwiGlu) || MODE == int(GemvMode::Logits)))  // (the modes with a copy)
+    if (a.part[0].xcodes) return launch_xm<MODE, 2, true>(a, g, st);
   const uint32_t nw = g.threads / kWave;
   const size_t lds = size_t(nw) * kXmTableBytes + size_t(nw) * 16 * 4;
   const dim3 gr(g.blocks), bl(g.threads);
   switch (nw) {
-    case 1: launch_kernel_lds(&k_gemv_xm<MODE, 1, BITS>, gr, bl, lds, st, a); return true;
-    case 2: launch_kernel_lds(&k_gemv_xm<MODE, 2, BITS>, gr, bl, lds, st, a); return true;
-    case 4: launch_kernel_lds(&k_gemv_xm<MODE, 4, BITS>, gr, bl, lds, st, a); return true;
-    case 8: launch_kernel_lds(&k_gemv_xm<MODE, 8, BITS>, gr, bl, lds, st, a); return true;
-    case 15: launch_kernel_lds(&k_gemv_xm<MODE, 15, BITS>, gr, bl, lds, st, a); return true;
-    case 16: launch_kernel_lds(&k_gemv_xm<MODE, 16, BITS>, gr, bl, lds, st, a); return true;
+    case 1: launch_kernel_lds(&k_gemv_xm<MODE, 1, BITS, kXc>, gr, bl, lds, st, a); return true;
+    case 2: launch_kernel_lds(&k_gemv_xm<MODE, 2, BITS, kXc>, gr, bl, lds, st, a); return true;
+    case 4: launch_kernel_lds(&k_gemv_xm<MODE, 4, BITS, kXc>, gr, bl, lds, st, a); return true;
+    case 8: launch_kernel_lds(&k_gemv_xm<MODE, 8, BITS, kXc>, gr, bl, lds, st, a); return true;
+    case 15: launch_kernel_lds(&k_gemv_xm<MODE, 15, BITS, kXc>, gr, bl, lds, st, a); return true;
+    case 16: launch_kernel_lds(&k_gemv_xm<MODE, 16, BITS, kXc>, gr, bl, lds, st, a); return true;
     default: return false;
   }
 }
 
 // The permuted copy of a launch's codes for k_gemv_xm: thread (w, lane) of workgroup u copies
-// the 16 bytes of each set S that the kernel's lane reads for unit u (xm_code_at) to
-// dst + u * NW * 4096 + ((w * 4 + S) * 64 + lane) * 16.
-template <int MODE, int NW>
+// what the kernel's lane reads for unit u (xm_code_at).  4-bit: the 16 bytes of set S to
+// dst + u * NW * 4096 + ((w * 4 + S) * 64 + lane) * 16.  2-bit: the 8 bytes of sets 2 p and
+// 2 p + 1 side by side to dst + u * NW * 2048 + ((w * 2 + p) * 64 + lane) * 16.
+template <int MODE, int NW, int BITS = 4>
 __global__ void __launch_bounds__(kWave * NW) k_xm_layout(GemvArgs a, uint8_t* dst) {
   constexpr int R = 4;
   const int lane = threadIdx.x & 63, n = lane & 15, q = lane >> 4;
@@ -2363,22 +2377,32 @@ __global__ void __launch_bounds__(kWave * NW) k_xm_layout(GemvArgs a, uint8_t* d
   const GemvPart P0 = a.part[0];
   const GemvPart& P1 = MODE == int(GemvMode::SwiGlu) ? a.part[1] : P0;
   const uint32_t rb = xs_row_base<R, MODE>(P0, u, half);
+  if constexpr (BITS == 2) {
 #pragma unroll
-  for (int S = 0; S < 4; ++S) {
-    const uint4 v = ld_u128(xm_code_at<R, MODE>(P0, P1, rb, half, ng, gw, S, n, q));
-    *reinterpret_cast<uint4*>(dst + (size_t(u) * (NW * 4096u) + ((wave * 4 + uint32_t(S)) * 64 + uint32_t(lane)) * 16)) = v;
+    for (int p = 0; p < 2; ++p) {
+      const uint2 v0 = ld_u64(xm_code_at<R, MODE, 2>(P0, P1, rb, half, ng, gw, 2 * p, n, q));
+      const uint2 v1 = ld_u64(xm_code_at<R, MODE, 2>(P0, P1, rb, half, ng, gw, 2 * p + 1, n, q));
+      *reinterpret_cast<uint4*>(dst + (size_t(u) * (NW * 2048u) + ((wave * 2 + uint32_t(p)) * 64 + uint32_t(lane)) * 16)) =
+          make_uint4(v0.x, v0.y, v1.x, v1.y);
+    }
+  } else {
+#pragma unroll
+    for (int S = 0; S < 4; ++S) {
+      const uint4 v = ld_u128(xm_code_at<R, MODE>(P0, P1, rb, half, ng, gw, S, n, q));
+      *reinterpret_cast<uint4*>(dst + (size_t(u) * (NW * 4096u) + ((wave * 4 + uint32_t(S)) * 64 + uint32_t(lane)) * 16)) = v;
+    }
   }
 }
 
-template <int MODE>
+template <int MODE, int BITS>
 bool launch_xm_layout(const GemvArgs& a, const GemvLaunch& g, uint8_t* dst, hipStream_t st) {
   const dim3 gr(a.n_units), bl(g.threads);
   switch (g.threads / kWave) {
-    case 1: launch_kernel(&k_xm_layout<MODE, 1>, gr, bl, st, a, dst); return true;
-    case 2: launch_kernel(&k_xm_layout<MODE, 2>, gr, bl, st, a, dst); return true;
-    case 4: launch_kernel(&k_xm_layout<MODE, 4>, gr, bl, st, a, dst); return true;
-    case 8: launch_kernel(&k_xm_layout<MODE, 8>, gr, bl, st, a, dst); return true;
-    case 16: launch_kernel(&k_xm_layout<MODE, 16>, gr, bl, st, a, dst); return true;
+    case 1: launch_kernel(&k_xm_layout<MODE, 1, BITS>, gr, bl, st, a, dst); return true;
+    case 2: launch_kernel(&k_xm_layout<MODE, 2, BITS>, gr, bl, st, a, dst); return true;
+    case 4: launch_kernel(&k_xm_layout<MODE, 4, BITS>, gr, bl, st, a, dst); return true;
+    case 8: launch_kernel(&k_xm_layout<MODE, 8, BITS>, gr, bl, st, a, dst); return true;
+    case 16: launch_kernel(&k_xm_layout<MODE, 16, BITS>, gr, bl, st, a, dst); return true;
     default: return false;
   }
 }
@@ -2714,7 +2738,7 @@ GemvLaunch gemv_geometry(WeightKind kind, GemvMode mode, uint32_t C, const uint3
       uint32_t wpc = nw >= 8 ? t.xm_wpc_wide
                      : mode == GemvMode::Logits ? t.xm_wpc_logits
                      : units >= 4096 ? (mode == GemvMode::SwiGlu && nw == 4 && t.xm_layout && kind == WeightKind::FlatW4
-                                            ? t.xm_wpc_gateup
+                                            ? t.xm_wpc_gateup  // (2-bit gate/up: 3 per CU measured faster)
                                             : t.xm_wpc_large)
                      : t.xm_wpc_small;
       if (nw < 4) wpc *= 4 / nw;  // narrower inputs: as many waves per CU as at 8192 columns
@@ -2878,17 +2902,22 @@ uint32_t launch_gemv_poly(const GemvArgs& a, const PolyPlan* const* plans, float
 size_t xm_layout_bytes(WeightKind kind, const GemvArgs& a, const GemvLaunch& g) {
   const GemvMode m = GemvMode(a.mode);
   const uint32_t nw = g.threads / kWave;
-  if (!gemv_tuning().xm_layout || kind != WeightKind::FlatW4 || !g.xm ||
+  if (!gemv_tuning().xm_layout || (kind != WeightKind::FlatW4 && kind != WeightKind::FlatW2) || !g.xm ||
       (m != GemvMode::SwiGlu && m != GemvMode::Logits) || a.C != nw * 2048u)
     return 0;
-  const size_t bytes = size_t(a.n_units) * nw * 4096u;
+  const size_t bytes = size_t(a.n_units) * nw * (kind == WeightKind::FlatW2 ? 2048u : 4096u);
   return bytes < (size_t(1) << 32) ? bytes : 0;
 }
 
-bool build_xm_layout(const GemvArgs& a, const GemvLaunch& g, uint8_t* dst, hipStream_t st) {
+bool build_xm_layout(WeightKind kind, const GemvArgs& a, const GemvLaunch& g, uint8_t* dst, hipStream_t st) {
+  const bool w2 = kind == WeightKind::FlatW2;
   switch (GemvMode(a.mode)) {
-    case GemvMode::SwiGlu: return launch_xm_layout<int(GemvMode::SwiGlu)>(a, g, dst, st);
-    case GemvMode::Logits: return launch_xm_layout<int(GemvMode::Logits)>(a, g, dst, st);
+    case GemvMode::SwiGlu:
+      return w2 ? launch_xm_layout<int(GemvMode::SwiGlu), 2>(a, g, dst, st)
+                : launch_xm_layout<int(GemvMode::SwiGlu), 4>(a, g, dst, st);
+    case GemvMode::Logits:
+      return w2 ? launch_xm_layout<int(GemvMode::Logits), 2>(a, g, dst, st)
+                : launch_xm_layout<int(GemvMode::Logits), 4>(a, g, dst, st);
     default: return false;
   }
 }

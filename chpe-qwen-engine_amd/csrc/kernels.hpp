@@ -71,7 +71,7 @@ struct GemvPart {
   uint32_t replace_outliers;  // Cell16W4: outliers replace (tied LM head) instead of add
   uint32_t rope_role;         // QkvRope: RopeRole of this part
   const struct CellReplace* repl;  // Cell16W4 replace mode: per-cell corrections (see below)
-  const uint8_t* xcodes;      // FlatW4 on the persistent matrix-core kernel (part 0): the launch's
+  const uint8_t* xcodes;      // Flat tiles on the persistent matrix-core kernel (part 0): the launch's
                               //   codes in that kernel's load order, or null (read from the records)
 };
 
@@ -198,8 +198,8 @@ struct GemvTuning {
   uint32_t xm_wpc_small = 2, xm_wpc_large = 3, xm_wpc_logits = 2, xm_wpc_wide = 1;
   // the permuted code copies of the gate/up and LM head launches (xm_layout_bytes;
   // CHPE_XM_LAYOUT=0: the kernel reads the records), and the persistent workgroups per CU of the
-  // gate/up launches of 4096 units or more at 4 waves (8192 columns) that read such a copy
-  // (CHPE_GEMV_XM_WPC_GATEUP; without the copy: xm_wpc_large)
+  // 4-bit gate/up launches of 4096 units or more at 4 waves (8192 columns) that read such a
+  // copy (CHPE_GEMV_XM_WPC_GATEUP; without the copy, and for 2-bit tiles: xm_wpc_large)
   uint32_t xm_layout = 1;
   uint32_t xm_wpc_gateup = 2;
   uint32_t xs = 1;     // flat tiles on the input-stationary persistent kernel (CHPE_GEMV_XS; 0: off)
@@ -297,12 +297,12 @@ void launch_block_finish(const BlockFinishArgs& a, hipStream_t stream);
 // launchers; all enqueue on `stream` and never synchronise
 void launch_embed(const EmbedArgs& a, hipStream_t stream);
 void launch_gemv(WeightKind kind, const GemvArgs& a, const GemvLaunch& g, hipStream_t stream);
-// The permuted copy of a launch's 4-bit codes for the persistent matrix-core kernel
+// The permuted copy of a launch's 4- or 2-bit codes for the persistent matrix-core kernel
 // (GemvPart::xcodes): its size in bytes, or 0 where it is not built (another kernel, another
 // mode than SwiGlu / Logits, an input that leaves a wave's columns partly empty, 4 GiB or more);
 // build_xm_layout enqueues the copy into dst (that many bytes).
 size_t xm_layout_bytes(WeightKind kind, const GemvArgs& a, const GemvLaunch& g);
-bool build_xm_layout(const GemvArgs& a, const GemvLaunch& g, uint8_t* dst, hipStream_t stream);
+bool build_xm_layout(WeightKind kind, const GemvArgs& a, const GemvLaunch& g, uint8_t* dst, hipStream_t stream);
 // Gated-DeltaNet decode step (Qwen3.5 linear-attention layers; deltanet.hip).
 constexpr uint32_t kDnMaxTaps = 8;
 struct DnConvArgs {         // depthwise causal conv update + SiLU

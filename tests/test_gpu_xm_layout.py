@@ -1,7 +1,7 @@
 """The permuted code copy of the matrix-core flat GEMV (k_xm_layout; gemvCellFlat,
 src/chpe_engine.zig:584-729).  The engine writes the gate/up and LM head codes once more in the
-kernel's load order, and the kernel then reads each lane's 16 bytes from the copy instead of
-the records.  The copy holds the same bytes for the same lanes, so the outputs must be bit for
+kernel's load order, and the kernel then reads each lane's bytes from the copy instead of the
+records (4-bit: 16 bytes per set; 2-bit: the 8 bytes of two sets in one 16-byte load).  The copy holds the same bytes for the same lanes, so the outputs must be bit for
 bit those of the records path: each case runs here (copy) and in a child process started with
 CHPE_XM_LAYOUT=0 (records, read once per process), on the same inputs.  Both are also checked
 against the oracle by test_gpu_gemv_flat.py."""
@@ -42,29 +42,31 @@ def say(msg):
     sys.stdout.flush()
 
 
-def make_tiles(rng, rows, cols):
+def make_tiles(rng, rows, cols, bits=4):
     n = rows * cols
     w = (rng.standard_normal(n) * 0.02).astype(np.float32)
     hot = rng.choice(n, size=max(1, n // 2000), replace=False)
     w[hot] = (rng.standard_normal(hot.size) * 0.5).astype(np.float32)
     n_tiles = (n + TILE - 1) // TILE
     w = np.concatenate([w, np.zeros(n_tiles * TILE - n, np.float32)])
-    return np.stack([ca.pack_flat(w[t * TILE:(t + 1) * TILE], bits=4, n_outliers=64) for t in range(n_tiles)])
+    return np.stack([ca.pack_flat(w[t * TILE:(t + 1) * TILE], bits=bits, n_outliers=64) for t in range(n_tiles)])
 
 
-CASES = [  # (mode, rows, cols): every one on the matrix-core kernel with the copy
-    ("swiglu", 8192, 8192),   # 4096 units at 4 waves, 2 workgroups per CU
-    ("logits", 300, 8192),
-    ("logits", 90, 4096),     # 2 waves
+CASES = [  # (mode, bits, rows, cols): every one on the matrix-core kernel with the copy
+    ("swiglu", 4, 8192, 8192),   # 4096 units at 4 waves, 2 workgroups per CU
+    ("logits", 4, 300, 8192),
+    ("logits", 4, 90, 4096),     # 2 waves
+    ("swiglu", 2, 8192, 8192),   # 2-bit: two sets per 16-byte load
+    ("logits", 2, 130, 4096),
 ]
 
 
-@pytest.mark.parametrize("mode,rows,cols", CASES)
-def test_permuted_codes_match_records(mode, rows, cols):
-    rng = np.random.default_rng(rows + cols)
-    say(f"xm layout mode={mode} rows={rows} cols={cols}")
-    cells = make_tiles(rng, rows, cols)
-    up = make_tiles(rng, rows, cols) if mode == "swiglu" else None
+@pytest.mark.parametrize("mode,bits,rows,cols", CASES)
+def test_permuted_codes_match_records(mode, bits, rows, cols):
+    rng = np.random.default_rng(rows + cols + bits)
+    say(f"xm layout mode={mode} bits={bits} rows={rows} cols={cols}")
+    cells = make_tiles(rng, rows, cols, bits)
+    up = make_tiles(rng, rows, cols, bits) if mode == "swiglu" else None
     x = rng.standard_normal(cols).astype(np.float32)
     gamma = (rng.standard_normal(cols) * 0.2 + 1.0).astype(np.float32)
     r = ca.gpu_gemv_flat(mode, rows, cols, cells, x, tiles_up=up, gamma=gamma, eps=1e-6)
