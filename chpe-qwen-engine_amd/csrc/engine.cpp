@@ -614,7 +614,7 @@ GemvLaunch Engine::gemv_args(const ProjPlan* const* parts, float* const* outs, i
     gp.replace_outliers = p.replace_outliers;
     gp.repl = p.repl;
     gp.rope_role = roles ? roles[i] : 0u;
-    gp.xcodes = i == 0 ? p.xcodes : nullptr;
+    gp.xcodes = i == 0 && mode == p.xcodes_mode && n == p.xcodes_parts ? p.xcodes : nullptr;
   }
   if (mode == GemvMode::Logits) {
     a.partials = d_partials_;
@@ -636,7 +636,11 @@ void Engine::build_xm_layout_of(ProjPlan* const* parts, int n, GemvMode mode, ui
     return;
   }
   allocs_.push_back(d);
-  if (build_xm_layout(parts[0]->kind, a, g, static_cast<uint8_t*>(d), stream_)) parts[0]->xcodes = static_cast<uint8_t*>(d);
+  if (build_xm_layout(parts[0]->kind, a, g, static_cast<uint8_t*>(d), stream_)) {
+    parts[0]->xcodes = static_cast<uint8_t*>(d);
+    parts[0]->xcodes_mode = mode;
+    parts[0]->xcodes_parts = n;
+  }
 }
 
 void Engine::build_xm_layouts() {

@@ -59,7 +59,10 @@ struct ProjPlan {
   CellReplace* repl = nullptr;         // device, replace-mode outliers of 16-row cells
   uint8_t* xcodes = nullptr;           // device, the decode launch's codes in the persistent
                                        //   matrix-core kernel's load order (see xm_layout_bytes);
-                                       //   set on the launch's first part
+                                       //   set on the launch's first part, and passed only to
+                                       //   launches of the mode and part count it was built for
+  GemvMode xcodes_mode = GemvMode::Store;
+  int xcodes_parts = 0;
   PolyPlan poly{};                     // Cell16Poly: the cells' row bases
 };
 
