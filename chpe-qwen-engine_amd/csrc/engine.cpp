@@ -624,10 +624,11 @@ GemvLaunch Engine::gemv_args(const ProjPlan* const* parts, float* const* outs, i
   return g;
 }
 
-void Engine::build_xm_layout_of(ProjPlan* const* parts, int n, GemvMode mode, uint32_t C) {
+void Engine::build_xm_layout_of(ProjPlan* const* parts, int n, GemvMode mode, uint32_t C, const RopeArgs* rope,
+                                const uint32_t* roles) {
   GemvArgs a{};
   float* outs[kMaxParts] = {d_mlp_, d_mlp_, d_mlp_};
-  const GemvLaunch g = gemv_args(parts, outs, n, mode, d_hidden_, C, nullptr, nullptr, nullptr, &a);
+  const GemvLaunch g = gemv_args(parts, outs, n, mode, d_hidden_, C, nullptr, rope, roles, &a);
   const size_t bytes = xm_layout_bytes(parts[0]->kind, a, g);
   if (bytes == 0) return;
   void* d = nullptr;
@@ -645,9 +646,21 @@ void Engine::build_xm_layout_of(ProjPlan* const* parts, int n, GemvMode mode, ui
 
 void Engine::build_xm_layouts() {
   const uint32_t D = uint32_t(arch_.hidden_dim);
-  for (LayerPlan& L : layers_) {
+  for (size_t l = 0; l < layers_.size(); ++l) {
+    LayerPlan& L = layers_[l];
     ProjPlan* gu[2] = {&L.gate, &L.up};
     if (L.gate.kind == L.up.kind && L.gate.rows) build_xm_layout_of(gu, 2, GemvMode::SwiGlu, D);
+    // (2-bit tiles: the q/k/v, o and down launches too; xm_layout_bytes decides)
+    ProjPlan* o[1] = {&L.o};
+    if (L.o.rows) build_xm_layout_of(o, 1, GemvMode::Accum, D);  // (the launch's input length)
+    ProjPlan* dn[1] = {&L.down};
+    if (L.down.rows) build_xm_layout_of(dn, 1, GemvMode::Accum, uint32_t(arch_.intermediate_dim));
+    if (L.q.kind == L.k.kind && L.k.kind == L.v.kind && L.q.rows) {  // one q/k/v launch (enqueue_qkv)
+      ProjPlan* qkv[3] = {&L.q, &L.k, &L.v};
+      const uint32_t roles[3] = {kRoleQ, kRoleK, kRoleV};
+      const RopeArgs rope = rope_args(l);
+      build_xm_layout_of(qkv, 3, GemvMode::QkvRope, D, &rope, roles);
+    }
   }
   ProjPlan* lm[1] = {&lm_head_};
   if (lm_head_.rows) build_xm_layout_of(lm, 1, GemvMode::Logits, D);

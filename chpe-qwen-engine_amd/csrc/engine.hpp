@@ -171,7 +171,8 @@ class Engine {
                        uint32_t C, const float* gamma, const RopeArgs* rope, const uint32_t* roles, GemvArgs* a) const;
   // the permuted code copies of the decode launches that read them (gate/up, the LM head)
   void build_xm_layouts();
-  void build_xm_layout_of(ProjPlan* const* parts, int n, GemvMode mode, uint32_t C);
+  void build_xm_layout_of(ProjPlan* const* parts, int n, GemvMode mode, uint32_t C, const RopeArgs* rope = nullptr,
+                          const uint32_t* roles = nullptr);
   AttnArgs attn_args(size_t layer) const;
   double proj_bytes(const ProjPlan& p) const;
   bool plan_block(std::string* err);

@@ -2097,7 +2097,8 @@ __global__ void __launch_bounds__(kWave * NW) k_gemv_xm(GemvArgs a) {
         const uint32_t Gs = Gs0 + gc;
         if constexpr (BITS == 2 && kXc) {  // sets S and S + 1 in one 16-byte load (the permuted copy)
           if ((S & 1) == 0) {
-            const uint4 v = ld_u128(xc + (u * (NW * 2048u) + ((wave * 2 + uint32_t(S / 2)) * 64 + uint32_t(lane)) * 16));
+            const uint4 v = ld_u128(uni(a.part[0].xcodes) +
+                                    (u * (NW * 2048u) + ((wave * 2 + uint32_t(S / 2)) * 64 + uint32_t(lane)) * 16));
             L->q[S] = make_uint4(v.x, v.y, 0u, 0u);
             L->q[S + 1] = make_uint4(v.z, v.w, 0u, 0u);
           }
@@ -2347,8 +2348,7 @@ __global__ void __launch_bounds__(kWave * NW) k_gemv_xm(GemvArgs a) {
 
 template <int MODE, int BITS = 4, bool kXc = false>
 bool launch_xm(const GemvArgs& a, const GemvLaunch& g, hipStream_t st) {
-  if constexpr (BITS == 2 && !kXc &&
-                (MODE == int(GemvMode::SwiGlu) || MODE == int(GemvMode::Logits)))  // (the modes with a copy)
+  if constexpr (BITS == 2 && !kXc)
     if (a.part[0].xcodes) return launch_xm<MODE, 2, true>(a, g, st);
   const uint32_t nw = g.threads / kWave;
   const size_t lds = size_t(nw) * kXmTableBytes + size_t(nw) * 16 * 4;
@@ -2374,7 +2374,9 @@ __global__ void __launch_bounds__(kWave * NW) k_xm_layout(GemvArgs a, uint8_t* d
   const int lane = threadIdx.x & 63, n = lane & 15, q = lane >> 4;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), u = blockIdx.x;
   const uint32_t ng = a.C >> 7, half = a.rope.head_dim / 2, gw = wave * 16;
-  const GemvPart P0 = a.part[0];
+  args_batch<MODE>(a);
+  const GemvPart P0 = MODE == int(GemvMode::QkvRope) ? pick_part(a, int(__builtin_amdgcn_readfirstlane(part_of(a, u))))
+                                                      : a.part[0];
   const GemvPart& P1 = MODE == int(GemvMode::SwiGlu) ? a.part[1] : P0;
   const uint32_t rb = xs_row_base<R, MODE>(P0, u, half);
   if constexpr (BITS == 2) {
@@ -2402,6 +2404,7 @@ bool launch_xm_layout(const GemvArgs& a, const GemvLaunch& g, uint8_t* dst, hipS
     case 2: launch_kernel(&k_xm_layout<MODE, 2, BITS>, gr, bl, st, a, dst); return true;
     case 4: launch_kernel(&k_xm_layout<MODE, 4, BITS>, gr, bl, st, a, dst); return true;
     case 8: launch_kernel(&k_xm_layout<MODE, 8, BITS>, gr, bl, st, a, dst); return true;
+    case 15: launch_kernel(&k_xm_layout<MODE, 15, BITS>, gr, bl, st, a, dst); return true;
     case 16: launch_kernel(&k_xm_layout<MODE, 16, BITS>, gr, bl, st, a, dst); return true;
     default: return false;
   }
@@ -2902,9 +2905,11 @@ uint32_t launch_gemv_poly(const GemvArgs& a, const PolyPlan* const* plans, float
 size_t xm_layout_bytes(WeightKind kind, const GemvArgs& a, const GemvLaunch& g) {
   const GemvMode m = GemvMode(a.mode);
   const uint32_t nw = g.threads / kWave;
-  if (!gemv_tuning().xm_layout || (kind != WeightKind::FlatW4 && kind != WeightKind::FlatW2) || !g.xm ||
-      (m != GemvMode::SwiGlu && m != GemvMode::Logits) || a.C != nw * 2048u)
-    return 0;
+  if (!gemv_tuning().xm_layout || (kind != WeightKind::FlatW4 && kind != WeightKind::FlatW2) || !g.xm) return 0;
+  if (kind == WeightKind::FlatW4 && ((m != GemvMode::SwiGlu && m != GemvMode::Logits) || a.C != nw * 2048u)) return 0;
+  // 2-bit: every mode of the decode step; the last wave's columns may be partly empty (the copy
+  // then holds group 0 there, as the records path reads)
+  if (kind == WeightKind::FlatW2 && (m == GemvMode::Store || a.C > nw * 2048u || a.C <= (nw - 1) * 2048u)) return 0;
   const size_t bytes = size_t(a.n_units) * nw * (kind == WeightKind::FlatW2 ? 2048u : 4096u);
   return bytes < (size_t(1) << 32) ? bytes : 0;
 }
@@ -2918,6 +2923,8 @@ bool build_xm_layout(WeightKind kind, const GemvArgs& a, const GemvLaunch& g, ui
     case GemvMode::Logits:
       return w2 ? launch_xm_layout<int(GemvMode::Logits), 2>(a, g, dst, st)
                 : launch_xm_layout<int(GemvMode::Logits), 4>(a, g, dst, st);
+    case GemvMode::Accum: return w2 && launch_xm_layout<int(GemvMode::Accum), 2>(a, g, dst, st);
+    case GemvMode::QkvRope: return w2 && launch_xm_layout<int(GemvMode::QkvRope), 2>(a, g, dst, st);
     default: return false;
   }
 }
