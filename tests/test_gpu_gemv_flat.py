@@ -7,7 +7,8 @@ LM head and every wider input (the 72B down projection at 29568 columns) run the
 input-stationary kernels: 4-bit tiles on the matrix cores (k_gemv_xm: exact integer products
 of the codes with the input split into four signed-byte limbs per 128-column group, which is
 exact for every element within 2^7 of its group's largest and within 2^-31 of that largest
-otherwise), 2-bit tiles on the vector ALUs (k_gemv_xs).  The SwiGLU and LM head launches of
+otherwise).  2-bit tiles take that kernel at every size (code ^ 2 as the operand, the 2-bit
+field order in the limb tables).  The SwiGLU and LM head launches of
 that kernel at 4096 and 8192 columns read their codes from the permuted copy the engine builds
 for them (k_xm_layout: the same bytes in the kernel's load order).  Row counts are ragged (not
 multiples of the unit).
