@@ -195,7 +195,9 @@ struct GemvTuning {
   uint32_t xm = 1;     // flat 4-bit tiles on the matrix-core input-stationary kernel (CHPE_GEMV_XM; 0: off)
   uint32_t xm2 = 1;    // flat 2-bit tiles on it (CHPE_GEMV_XM2; 0: the vector-ALU kernels)
   // its persistent workgroups per CU (CHPE_GEMV_XM_WPC=small,large,logits,wide as below)
-  uint32_t xm_wpc_small = 2, xm_wpc_large = 3, xm_wpc_logits = 2, xm_wpc_wide = 1;
+  // (small: launches of < 4096 units; in these models only 2-bit ones, whose q/k/v and o ran
+  // 0.5 us faster at 3 than at 2)
+  uint32_t xm_wpc_small = 3, xm_wpc_large = 3, xm_wpc_logits = 2, xm_wpc_wide = 1;
   // the permuted code copies of the gate/up and LM head launches (xm_layout_bytes;
   // CHPE_XM_LAYOUT=0: the kernel reads the records), and the persistent workgroups per CU of the
   // 4-bit gate/up launches of 4096 units or more at 4 waves (8192 columns) that read such a
