@@ -412,3 +412,28 @@ def test_forward_decode_composition_float64(w4_archive):
             assert np.argmax(ref) == rows.size - 1 or ref[-1] >= ref.max() - 1e-3
     finally:
         o.close()
+
+
+@pytest.mark.parametrize("bits", [4, 2])
+def test_flat_code_value_identities(bits):
+    """The matrix-core flat GEMV takes each code as an unsigned operand and a constant offset:
+    4-bit value = code - 8 (low nibble = even column), 2-bit value = (code ^ 2) - 2 (the
+    codebook {0, +1, -2, -1} of gemvCellFlat, src/chpe_engine.zig:584-729, is the 2-bit two's
+    complement; field k of byte b = column 4 b + k).  Checked bit for bit against the oracle's
+    own decode of a packed tile (oref_flat_tile_weights), every weight of the tile."""
+    rng = np.random.default_rng(17 + bits)
+    w = (rng.standard_normal(32768) * 0.02).astype(np.float32)
+    cell = ca.pack_flat(w, bits=bits, n_outliers=0)
+    got = orc.flat_tile_weights(cell)
+    scale = cell[16448 + 48:16448 + 48 + 512].view(np.float16).astype(np.float32)
+    o = np.arange(32768)
+    if bits == 4:
+        b = cell[64 + o // 2]
+        code = (b >> (4 * (o & 1))) & 15
+        val = code.astype(np.float32) - 8.0
+    else:
+        b = cell[64 + o // 4]
+        code = (b >> (2 * (o & 3))) & 3
+        val = (code ^ 2).astype(np.float32) - 2.0
+    want = (val * scale[o // 128]).astype(np.float32)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
