@@ -26,7 +26,7 @@ ENGINE_SYMBOLS = [
     "chpe_get_hidden_dim", "chpe_get_num_layers", "chpe_get_last_elapsed_ns",
     "chpe_get_last_argmax", "chpe_get_last_max_logit", "chpe_get_last_token0_logit",
     "chpe_get_last_hidden_norm", "chpe_free", "chpe_init_ex", "chpe_decode_step",
-    "chpe_generate", "chpe_verify", "chpe_prefill", "chpe_block_ready", "chpe_last_error", "chpe_get_max_seq_len", "chpe_get_hidden",
+    "chpe_generate", "chpe_verify", "chpe_prefill", "chpe_block_ready", "chpe_last_error", "chpe_build_id", "chpe_get_max_seq_len", "chpe_get_hidden",
     "chpe_time_steps", "chpe_time_stage", "chpe_time_stage_live", "chpe_stage_bytes", "chpe_step_bytes", "chpe_stage_kernel",
     "chpe_debug_gemv", "chpe_debug_flat_tile_weights", "chpe_debug_gemv_flat", "chpe_debug_gemv_cells", "chpe_debug_gemv_poly", "chpe_debug_gemv_raw", "chpe_debug_embed_row_cell",
     "chpe_debug_attention", "chpe_attention_noalloc", "chpe_debug_deltanet_conv", "chpe_debug_deltanet_step",
@@ -43,13 +43,32 @@ def _fp(a):
     return a.ctypes.data_as(_c_float_p)
 
 
+def source_hash():
+    """The hash libchpe.so carries of the sources it was built from (chpe_build_id): the
+    Makefile's LIBSRC list, in its order, through SHA-256, first 16 hex digits."""
+    import hashlib
+    src = PKG_DIR / "csrc"
+    files = sorted(list(src.glob("*.hip")) + list(src.glob("*.hpp")), key=lambda p: f"csrc/{p.name}")
+    files += [src / "engine.cpp", src / "c_api.cpp", PKG_DIR.parent / "include" / "chpe.h", PKG_DIR / "Makefile"]
+    h = hashlib.sha256()
+    for f in files:
+        h.update(f.read_bytes())
+    return h.hexdigest()[:16]
+
+
 def load_engine_lib():
-    """Load libchpe.so (raises OSError when it is not built)."""
+    """Load libchpe.so (raises OSError when it is not built, or was built from other sources
+    than the ones beside it)."""
     global _engine_lib
     if _engine_lib is None:
         if not ENGINE_LIB.exists():
             raise OSError(f"{ENGINE_LIB} is not built (run `make -C {PKG_DIR}`)")
         lib = ctypes.CDLL(str(ENGINE_LIB))
+        lib.chpe_build_id.restype = ctypes.c_char_p
+        built, here = lib.chpe_build_id().decode(), source_hash()
+        if built != here:
+            raise OSError(f"{ENGINE_LIB} was built from other sources (build id {built}, sources {here}): "
+                          f"run `make -C {PKG_DIR}`")
         V, S, I, U64, F, D = (ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int, ctypes.c_uint64,
                               ctypes.c_float, ctypes.c_double)
         sig = {
@@ -72,6 +91,7 @@ def load_engine_lib():
             "chpe_block_ready": (I, [V]),
             "chpe_verify": (I, [V, _c_u32_p, S, S, _c_u32_p]),
             "chpe_last_error": (ctypes.c_char_p, []),
+            "chpe_build_id": (ctypes.c_char_p, []),
             "chpe_get_max_seq_len": (S, [V]),
             "chpe_get_hidden": (I, [V, _c_float_p]),
             "chpe_time_steps": (I, [V, S, _c_float_p]),

@@ -39,10 +39,12 @@ using namespace dev;
 // X = x * 2^(30-e) with max |x| < 2^e (exact in int32) per 128-column group, in four balanced
 // signed-byte limbs (BlockTables).  The norm's sum of squares comes as the producer's partial
 // sums (ssp), read together with the columns; chunk 0 keeps it (the LM head's hidden norm).
-// Token slots >= m get zero tables.
+// Token slots >= m get zero tables.  A q/k/v launch (chk, as RopeArgs::brk_check) also makes
+// forwardDecode's break test (StepState::broken) on each token's input and records it in brk[token].
 template <bool kNorm>
 __global__ void __launch_bounds__(128) k_block_limbs(const float* X, const float* gamma, float eps, uint32_t C,
-                                                      uint32_t m, const float* ssp, uint32_t n_ssp, BlockTables t) {
+                                                      uint32_t m, const float* ssp, uint32_t n_ssp, BlockTables t,
+                                                      uint32_t* brk, uint32_t chk) {
   const uint32_t tok = blockIdx.y, T = tok >> 2, tl = tok & 3u, ng = C >> 7;
   const bool live = tok < m;
   const float* x = X + size_t(live ? tok : 0u) * C;
@@ -69,7 +71,10 @@ __global__ void __launch_bounds__(128) k_block_limbs(const float* X, const float
     if (lane == 0) s_red[wave] = ss;
     __syncthreads();
     const float tot = s_red[0] + s_red[1];
-    if (blockIdx.x == 0 && tid == 0) t.ss[tok] = live ? tot : 0.0f;
+    if (blockIdx.x == 0 && tid == 0) {
+      t.ss[tok] = live ? tot : 0.0f;
+      if (live && ((chk == 1u && !isfinite(tot)) || (chk == 2u && !isfinite(x[0])))) brk[tok] = 1u;
+    }
     inv = 1.0f / sqrtf(tot / float(C) + eps);
   }
   float xv[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
@@ -282,6 +287,8 @@ __global__ void __launch_bounds__(256) k_block_epi(BlockGemvArgs a) {
   uint32_t bi = 0xffffffffu, nf = 0;
   float sq = 0.0f;  // Accum: this lane's sum of y^2 over its token's updated rows
   const uint32_t pos0 = kRope ? a.state->pos : 0u;
+  // token e0's break (k_block_limbs): no KV append, the residual stays
+  const bool brk = (kRope || MODE == int(GemvMode::Accum)) && uint32_t(e0) < m && a.brk[e0] != 0u;
   for (uint32_t q4 = blockIdx.x * 4 + uint32_t(wave); q4 * 4 < total; q4 += gridDim.x * 4) {
     const uint32_t o = q4 * 4 + uint32_t(i);
     const bool ok = o < total;
@@ -370,8 +377,9 @@ __global__ void __launch_bounds__(256) k_block_epi(BlockGemvArgs a) {
     if constexpr (MODE == int(GemvMode::Store)) {
       y[r] = v[0] + (P0.bias ? P0.bias[r] : 0.0f);
     } else if constexpr (MODE == int(GemvMode::Accum)) {
-      const float yo = y[r], yn = r < P0.wrows ? yo + v[0] : yo;  // rows past the tiles stay
-      if (r < P0.wrows) y[r] = yn;
+      const bool upd = r < P0.wrows && !brk;  // rows past the tiles stay
+      const float yo = y[r], yn = upd ? yo + v[0] : yo;
+      if (upd) y[r] = yn;
       sq = fmaf(yn, yn, sq);
     } else if constexpr (kSwi) {
       y[r] = v[0] / (1.0f + expf(-v[0])) * v[1];  // silu(g)*u: :159-161, :1746-1748
@@ -389,7 +397,7 @@ __global__ void __launch_bounds__(256) k_block_epi(BlockGemvArgs a) {
       if (P0.rope_role == kRoleQ) {
         y[r] = o0;
         y[r + half] = o1;
-      } else {
+      } else if (!brk) {
         const uint32_t hd = a.g.rope.head_dim, head = r / hd;
         void* cache = P0.rope_role == kRoleK ? a.g.rope.k_cache : a.g.rope.v_cache;
         if (a.g.rope.kv_f16 && P0.rope_role == kRoleV) {  // 4-position blocks: [pos/4][dim][pos%4]
@@ -523,10 +531,13 @@ __global__ void __launch_bounds__(256) k_block_finish(BlockFinishArgs a) {
 
 void launch_block_limbs(const BlockGemvArgs& a, hipStream_t st) {
   const dim3 grid((a.g.C + 1023) / 1024, 4 * a.nq);
+  const uint32_t chk = GemvMode(a.g.mode) == GemvMode::QkvRope ? a.g.rope.brk_check : 0u;
   if (a.g.gamma)
-    launch_kernel(&k_block_limbs<true>, grid, dim3(128), st, a.g.x, a.g.gamma, a.g.eps, a.g.C, a.m, a.ssp, a.n_ssp, a.t);
+    launch_kernel(&k_block_limbs<true>, grid, dim3(128), st, a.g.x, a.g.gamma, a.g.eps, a.g.C, a.m, a.ssp, a.n_ssp, a.t,
+                  a.brk, chk);
   else
-    launch_kernel(&k_block_limbs<false>, grid, dim3(128), st, a.g.x, a.g.gamma, a.g.eps, a.g.C, a.m, a.ssp, a.n_ssp, a.t);
+    launch_kernel(&k_block_limbs<false>, grid, dim3(128), st, a.g.x, a.g.gamma, a.g.eps, a.g.C, a.m, a.ssp, a.n_ssp, a.t,
+                  a.brk, 0u);
 }
 
 uint32_t launch_block_gemv(BlockGemvArgs& a, hipStream_t st) {

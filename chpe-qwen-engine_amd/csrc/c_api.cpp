@@ -18,6 +18,7 @@
 #include "../../include/chpe.h"
 #include "engine.hpp"
 #include "format.hpp"
+#include "src_hash.h"  // CHPE_SRC_HASH: the Makefile's hash of the library's sources
 
 using namespace chpe;
 
@@ -114,6 +115,8 @@ void* chpe_init_ex(const char* archive_path, int arch, size_t max_seq_len, int k
 }
 
 const char* chpe_last_error(void) { return g_last_error.c_str(); }
+
+const char* chpe_build_id(void) { return CHPE_SRC_HASH; }
 
 int chpe_forward_tokens(void* ctx, const uint32_t* tokens, size_t n, float* out_logits) {
   if (!ctx || !tokens || n == 0) return -1;
@@ -519,7 +522,7 @@ int chpe_debug_gemv_poly(int mode, uint32_t rows, uint32_t cols, const uint8_t* 
   a.C = cols;
   a.eps = eps;
   float* dx = static_cast<float*>(alloc(size_t(cols) * 4));
-  float* dxn = static_cast<float*>(alloc(size_t(cols) * 4));
+  float* dxn = static_cast<float*>(alloc((size_t(cols) + 1) * 4));
   float* dy = static_cast<float*>(alloc(size_t(rows) * 4));
   float* dg = norm ? static_cast<float*>(alloc(size_t(cols) * 4)) : nullptr;
   PolyRaw raw{};

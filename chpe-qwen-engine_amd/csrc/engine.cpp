@@ -465,7 +465,7 @@ bool Engine::plan_projection(size_t tile_start, size_t num_tiles, size_t r_total
         if (!d_xn_) {
           const size_t n = std::max({arch_.hidden_dim, arch_.intermediate_dim, arch_.vocab_size,
                                      arch_.num_attn_heads * arch_.head_dim});
-          d_xn_ = static_cast<float*>(dev_alloc(std::max(arch_.hidden_dim, arch_.intermediate_dim) * 4));
+          d_xn_ = static_cast<float*>(dev_alloc((std::max(arch_.hidden_dim, arch_.intermediate_dim) + 1) * 4));
           for (int i = 0; i < kMaxParts; ++i) poly_raw_.y[i] = static_cast<float*>(dev_alloc(n * 4));
           if (!d_xn_ || !poly_raw_.y[kMaxParts - 1]) { *err = "allocation"; return false; }
         }
@@ -588,6 +588,7 @@ GemvLaunch Engine::gemv_args(const ProjPlan* const* parts, float* const* outs, i
   GemvArgs& a = *out;
   a = GemvArgs{};
   if (rope) a.rope = *rope;
+  else a.rope.state = d_state_;  // (the residual launches read StepState::broken)
   a.n_parts = n;
   a.mode = int(mode);
   a.C = C;
@@ -695,6 +696,11 @@ RopeArgs Engine::rope_args(size_t l) const {
   r.head_dim = uint32_t(arch_.head_dim);
   r.max_seq = uint32_t(S);
   r.kv_f16 = cfg_.kv_f16 ? 1 : 0;
+  // the break test on the hidden state layer l - 1 left (forwardDecode :1753-1764): the sum of
+  // squares after layers 0-2 and 8-16, otherwise hidden[0] (whose non-finite value makes the sum
+  // non-finite too)
+  const size_t prev = l - 1;
+  r.brk_check = l == 0 ? 0u : ((prev < 3 || (prev >= 8 && prev <= 16)) ? 1u : 2u);
   return r;
 }
 
@@ -904,6 +910,8 @@ int Engine::verify(const uint32_t* drafts, size_t m, size_t pos, uint32_t* out_a
     const int rc = block_forward(drafts, m, pos, out_argmax, &r);
     if (rc) return rc;
     if (last) *last = r;
+    // the decode state the sequential path leaves: the last argmax at position pos + m
+    if (set_state(StepState{r.argmax_token, uint32_t(pos + m), 0, 0}) || sync()) return -3;
     return 0;
   }
   const uint64_t t0 = now_ns();
@@ -931,7 +939,9 @@ bool Engine::plan_block(std::string* err) {
   for (const LayerPlan& L : layers_)
     if (!flat(L.q) || !flat(L.k) || !flat(L.v) || !flat(L.o) || !flat(L.gate) || !flat(L.up) || !flat(L.down))
       return false;
-  if (!flat(lm_head_) || D % 128 || I % 128 || qd % 128) return false;
+  // (the o projection reads the attention output of qd columns as hidden_dim columns, as the
+  // reference's gemvLinear call does, :1737: the two must agree)
+  if (!flat(lm_head_) || D % 128 || I % 128 || qd % 128 || qd != D) return false;
   auto units = [](size_t rows) { return (rows + kBlockUnit - 1) / kBlockUnit; };
   auto ranges = [](size_t C) { return (C + kBlockRange - 1) / kBlockRange; };
   size_t part_floats = 0;  // ranges x kMaxBlock x rows_all, the largest GEMV
@@ -947,6 +957,7 @@ bool Engine::plan_block(std::string* err) {
   d_btok_ = static_cast<uint32_t*>(dev_alloc(kMaxBlock * 4));
   d_bout_ = static_cast<uint32_t*>(dev_alloc(kMaxBlock * 4));
   d_bstate_ = static_cast<StepState*>(dev_alloc(sizeof(StepState)));
+  d_bbrk_ = static_cast<uint32_t*>(dev_alloc(kMaxBlock * 4));
   d_bx_ = fa(kMaxBlock * D);
   d_bq_ = fa(kMaxBlock * qd);
   d_battn_ = fa(kMaxBlock * qd);
@@ -962,7 +973,7 @@ bool Engine::plan_block(std::string* err) {
   btab_.xt = fa(Cmax * kMaxBlock);
   btab_.ss = fa(kMaxBlock);
   d_bpartials_ = static_cast<ArgmaxPartial*>(dev_alloc(kMaxBlock * 512 * sizeof(ArgmaxPartial)));
-  if (!d_btok_ || !d_bout_ || !d_bstate_ || !d_bx_ || !d_bq_ || !d_battn_ || !d_bmlp_ || !d_blog_ || !d_bpartial_ ||
+  if (!d_btok_ || !d_bout_ || !d_bstate_ || !d_bbrk_ || !d_bx_ || !d_bq_ || !d_battn_ || !d_bmlp_ || !d_blog_ || !d_bpartial_ ||
       !d_bpml_ || !d_bpacc_ || !d_bss_ || !btab_.tb || !btab_.ci || !btab_.ew || !btab_.xt || !btab_.ss ||
       !d_bpartials_) {
     *err = "allocation";
@@ -1011,6 +1022,7 @@ uint32_t Engine::enqueue_block_gemv(const ProjPlan* const* parts, float* const* 
   b.n_units = units;
   b.rows_all = kBlockUnit * units;
   b.partial = d_bpartial_;
+  b.brk = d_bbrk_;
   if (mode == GemvMode::QkvRope) {
     b.g.rope = rope_args(layer);
     b.state = d_bstate_;
@@ -1068,7 +1080,7 @@ int Engine::block_forward(const uint32_t* tokens, size_t m, size_t pos, uint32_t
 void Engine::record_block(uint32_t mm, hipStream_t st) {
   const uint32_t D = uint32_t(arch_.hidden_dim), I = uint32_t(arch_.intermediate_dim), V = uint32_t(arch_.vocab_size);
   const uint32_t qd = uint32_t(arch_.num_attn_heads * arch_.head_dim);
-  launch_block_embed(embed_args(), d_btok_, mm, d_bx_, d_bss_, st);
+  launch_block_embed(embed_args(), d_btok_, mm, d_bx_, d_bss_, d_bbrk_, st);
   uint32_t n_ss = 1;  // Σx² partials of the hidden rows in d_bss_
   for (size_t l = 0; l < arch_.num_layers; ++l) {
     const LayerPlan& L = layers_[l];
@@ -1115,7 +1127,7 @@ int Engine::prefill(const uint32_t* tokens, size_t n, ForwardResult* out) {
     if (rc) return rc;
   }
   // continue greedy decoding from here: the last argmax at position n
-  if (n < cfg_.max_seq_len && set_state(StepState{out->argmax_token, uint32_t(n), 0, 0})) return -3;
+  if (set_state(StepState{out->argmax_token, uint32_t(n), 0, 0})) return -3;
   return sync();
 }
 

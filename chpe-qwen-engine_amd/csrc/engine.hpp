@@ -114,7 +114,8 @@ class Engine {
   // token's arithmetic that of forwardDecode; KV rows pos..pos+m-1 are written;
   // out_argmax[i] = argmax after token i; the last token's logits become copy_logits()'s and
   // its result *last.  The decode state is not touched.  0, -1 bad arguments or no block step
-  // for this archive, -2 past max_seq_len, -3 device error.
+  // for this archive, -2 past max_seq_len, -3 device error.  (verify() and prefill() then leave
+  // the decode state where the sequential steps would: the last argmax at pos + m.)
   int block_forward(const uint32_t* tokens, size_t m, size_t pos, uint32_t* out_argmax, ForwardResult* last);
   bool block_ready() const { return block_ok_; }
   // positions 0..n-1 teacher-forced in blocks of kMaxBlock (prefill); result and logits of
@@ -234,6 +235,7 @@ class Engine {
   bool block_ok_ = false;
   uint32_t *d_btok_ = nullptr, *h_btok_ = nullptr, *d_bout_ = nullptr, *h_bout_ = nullptr;
   StepState *d_bstate_ = nullptr, *h_bstate_ = nullptr;
+  uint32_t* d_bbrk_ = nullptr;  // [kMaxBlock] per-token break flags of the block step
   float *d_bx_ = nullptr, *d_bq_ = nullptr, *d_battn_ = nullptr, *d_bmlp_ = nullptr, *d_blog_ = nullptr;
   float *d_bpartial_ = nullptr, *d_bpml_ = nullptr, *d_bpacc_ = nullptr;
   float* d_bss_ = nullptr;  // [kMaxSsPartials][kMaxBlock]: Σx² partials of the hidden rows for the next norm

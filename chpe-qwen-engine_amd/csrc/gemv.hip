@@ -569,11 +569,47 @@ __device__ __forceinline__ void issue_unit(const GemvArgs& a, uint32_t unit, uin
   issue_panel<F, MODE>(a, P0, P1, active, u->row_base, p, lane, u->q, u->s, &u->vm);
 }
 
+// forwardDecode's non-finite break (StepState::broken), as the q/k/v and residual launches see
+// it: loaded at the launch's start, whether an earlier launch of the step broke and (q/k/v) the
+// input's first element.
+struct BreakIn {
+  uint32_t was;
+  float x0;
+};
+template <int MODE>
+__device__ __forceinline__ BreakIn break_in(const GemvArgs& a) {
+  BreakIn b{0u, 0.0f};
+  if constexpr (MODE == int(GemvMode::QkvRope) || MODE == int(GemvMode::Accum)) {
+    // (global-address-space loads of uniform addresses, issued before any store of the kernel:
+    // scalar loads, kept out of the vector registers)
+    if (a.rope.state) b.was = gld(&a.rope.state->broken);
+    if constexpr (MODE == int(GemvMode::QkvRope)) b.x0 = gld(a.x);
+  }
+  return b;
+}
+// Whether the launch leaves the KV cache (q/k/v) or the residual stream (o, down) alone.  The
+// q/k/v launch tests its input (ss_bad: the input's sum of squares is not finite; the first
+// element, RopeArgs::brk_check) and records a new break.  Every workgroup reaches the same
+// answer from the same input; thread 0 of workgroup 0 stores it, so every thread of a q/k/v
+// launch calls this outside lane-dependent branches.
+template <int MODE>
+__device__ __forceinline__ bool break_now(const GemvArgs& a, const BreakIn& b, bool ss_bad) {
+  if constexpr (MODE == int(GemvMode::QkvRope)) {
+    const uint32_t chk = a.rope.brk_check;
+    // (uniform: kept in scalar registers)
+    const bool now = __builtin_amdgcn_readfirstlane(((chk == 1u && ss_bad) || (chk == 2u && !isfinite(b.x0))) ? 1 : 0) != 0;
+    if (now && b.was == 0u && blockIdx.x == 0 && threadIdx.x == 0) a.rope.state->broken = 1u;
+    return now || b.was != 0u;
+  } else {
+    return b.was != 0u;
+  }
+}
+
 // QkvRope epilogue for the pair (r, r + half) of part P: bias added, then RoPE (q, k) with the
 // reference's arithmetic (x0*cos - x1*sin, x0*sin + x1*cos, :212-213); q into y, k and v into
-// the KV cache at `pos`, rounded to the cache type.
+// the KV cache at `pos`, rounded to the cache type (not after a break: brk).
 __device__ __forceinline__ void rope_store(const GemvArgs& a, const GemvPart& P, uint32_t r, float lo, float hi,
-                                           float c, float sn) {
+                                           float c, float sn, bool brk) {
 #pragma clang fp contract(off)
   const uint32_t half = a.rope.head_dim / 2;
   float o0 = lo, o1 = hi;
@@ -586,6 +622,7 @@ __device__ __forceinline__ void rope_store(const GemvArgs& a, const GemvPart& P,
     P.y[r + half] = o1;
     return;
   }
+  if (brk) return;
   const uint32_t hd = a.rope.head_dim, head = r / hd, d = r % hd, pos = a.rope.state->pos;
   const size_t at = (size_t(head) * a.rope.max_seq + pos) * hd + d;
   void* cache = P.rope_role == kRoleK ? a.rope.k_cache : a.rope.v_cache;
@@ -602,15 +639,16 @@ __device__ __forceinline__ void rope_store(const GemvArgs& a, const GemvPart& P,
   }
 }
 
-// final value v of unit row i (lane-owned): SwiGlu pairs gate row i with up row i + RU/2
+// final value v of unit row i (lane-owned): SwiGlu pairs gate row i with up row i + RU/2; the
+// residual (Accum) stays as it is after a break (brk)
 template <int MODE>
 __device__ __forceinline__ void epilogue(const GemvPart& P0, uint32_t r, float v, float u, float pre, float* bv,
-                                         uint32_t* bi, uint32_t* nf) {
+                                         uint32_t* bi, uint32_t* nf, bool brk = false) {
   if (r >= P0.rows) return;
   if constexpr (MODE == int(GemvMode::SwiGlu)) {
     P0.y[r] = v / (1.0f + expf(-v)) * u;  // silu(g)*u: :159-161, :1746-1748
   } else if constexpr (MODE == int(GemvMode::Accum)) {
-    P0.y[r] = pre + v;
+    if (!brk) P0.y[r] = pre + v;
   } else if constexpr (MODE == int(GemvMode::Store)) {
     P0.y[r] = v + pre;
   } else {
@@ -646,7 +684,7 @@ __device__ __forceinline__ void argmax_partial(const GemvArgs& a, float bv, uint
 template <class F, int MODE>
 __device__ __forceinline__ void rows_unit(const GemvArgs& a, const UnitLoads<F, MODE>& cur, const float* s_x,
                                           const float (&x0)[F::kCols], float sx0, int lane, float* bv,
-                                          uint32_t* bi, uint32_t* nf) {
+                                          uint32_t* bi, uint32_t* nf, bool brk) {
   constexpr int RU = 8, S = kWave / RU;
   constexpr bool kSwi = MODE == int(GemvMode::SwiGlu);
   constexpr bool kLogits = MODE == int(GemvMode::Logits);
@@ -679,9 +717,9 @@ __device__ __forceinline__ void rows_unit(const GemvArgs& a, const UnitLoads<F, 
   if constexpr (kRope) {
     const uint32_t r = row_of<RU, MODE>(cur.row_base, i, a.rope.head_dim / 2);
     if ((lane % S) == 0 && i < RU / 2 && cur.unit < a.n_units && r < P0.rows)
-      rope_store(a, P0, r, tot + pre, up + up_pre, cur.rope_ok ? cur.rc : 1.0f, cur.rope_ok ? cur.rs : 0.0f);
+      rope_store(a, P0, r, tot + pre, up + up_pre, cur.rope_ok ? cur.rc : 1.0f, cur.rope_ok ? cur.rs : 0.0f, brk);
   } else if ((lane % S) == 0 && (!kSwi || i < RU / 2) && cur.unit < a.n_units) {
-    epilogue<MODE>(P0, row_of<RU, MODE>(cur.row_base, i, 0), tot, up, pre, bv, bi, nf);
+    epilogue<MODE>(P0, row_of<RU, MODE>(cur.row_base, i, 0), tot, up, pre, bv, bi, nf, brk);
   }
 }
 
@@ -743,10 +781,13 @@ __global__ void __launch_bounds__(kWave * (kRowWaves + 1), 2) k_gemv_rows(GemvAr
   __shared__ __align__(16) float s_x[xs_floats(F::kPanelCols * F::kPPW)];
   __shared__ float s_bv[kRowWaves + 1];
   __shared__ uint32_t s_bi[kRowWaves + 1], s_nf[kRowWaves + 1];
+  __shared__ uint32_t s_bad;  // QkvRope: the input's sum of squares is not finite
   const int lane = threadIdx.x & 63;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const uint32_t stride = gridDim.x * kRowWaves;
   const bool stager = wave == kRowWaves;
+  constexpr bool kRope = MODE == int(GemvMode::QkvRope);
+  const BreakIn bin = break_in<MODE>(a);  // (before any store or asm: scalar loads)
   args_batch<MODE>(a);
 
   // The two roles are wave-uniform branches that each pass the same barriers (one after the
@@ -756,6 +797,7 @@ __global__ void __launch_bounds__(kWave * (kRowWaves + 1), 2) k_gemv_rows(GemvAr
   if (stager) {
     const float ss = stage_wave<kNorm, F::kPanelCols * F::kPPW>(a, s_x, lane);
     if (kLogits && blockIdx.x == 0 && lane == 0) a.result->hidden_norm = sqrtf(ss);
+    if (kRope && lane == 0) s_bad = isfinite(ss) ? 0u : 1u;
     __syncthreads();
     if constexpr (kLogits) argmax_partial<MODE>(a, -1e30f, 0xffffffffu, 0u, s_bv, s_bi, s_nf);
   } else {
@@ -763,15 +805,16 @@ __global__ void __launch_bounds__(kWave * (kRowWaves + 1), 2) k_gemv_rows(GemvAr
     U cur;
     issue_unit<F, MODE>(a, unit0, 0, lane, true, true, &cur);
     __syncthreads();
+    const bool brk = break_now<MODE>(a, bin, kRope && s_bad != 0u);
     float x0[F::kCols];
     const float sx0 = lds_chunk<F>(s_x, a.C, 0, lane, x0);
     float bv = -1e30f;
     uint32_t bi = 0xffffffffu, nf = 0;
-    if (unit0 < a.n_units) rows_unit<F, MODE>(a, cur, s_x, x0, sx0, lane, &bv, &bi, &nf);
+    if (unit0 < a.n_units) rows_unit<F, MODE>(a, cur, s_x, x0, sx0, lane, &bv, &bi, &nf, brk);
     for (uint32_t unit = unit0 + stride; unit < a.n_units; unit += stride) {
       U u;
       issue_unit<F, MODE>(a, unit, 0, lane, true, true, &u);
-      rows_unit<F, MODE>(a, u, s_x, x0, sx0, lane, &bv, &bi, &nf);
+      rows_unit<F, MODE>(a, u, s_x, x0, sx0, lane, &bv, &bi, &nf, brk);
     }
     if constexpr (kLogits) argmax_partial<MODE>(a, bv, bi, nf, s_bv, s_bi, s_nf);
   }
@@ -798,6 +841,7 @@ __global__ void __launch_bounds__(512, 2) k_gemv_split(GemvArgs a) {
   const uint32_t ppw = (a.n_panels + NW - 1) / NW;
   const uint32_t p0 = wave * ppw, p1 = min(a.n_panels, p0 + ppw);
 
+  const BreakIn bin = break_in<MODE>(a);  // (before any store or asm: scalar loads)
   args_batch<MODE>(a);
   U cur;
   uint32_t unit = blockIdx.x;
@@ -806,6 +850,7 @@ __global__ void __launch_bounds__(512, 2) k_gemv_split(GemvArgs a) {
   issue_unit<F, MODE>(a, unit, p0, lane, wave == 0, false, &cur);
   float ss = 0.0f, inv = 1.0f;
   stage_x_finish<kNorm, kWide>(a, xr0, s_x, s_red, &ss, &inv);
+  const bool brk = break_now<MODE>(a, bin, !isfinite(ss));
 
   float bv = -1e30f;
   uint32_t bi = 0xffffffffu, nf = 0;
@@ -850,9 +895,9 @@ __global__ void __launch_bounds__(512, 2) k_gemv_split(GemvArgs a) {
       if constexpr (kRope) {
         const uint32_t r = row_of<RU, MODE>(cur.row_base, i, half);
         if (unit < a.n_units && (lane % S) == 0 && i < RU / 2 && r < P0.rows)
-          rope_store(a, P0, r, v + pre, up + up_pre, rc, rs);
+          rope_store(a, P0, r, v + pre, up + up_pre, rc, rs, brk);
       } else if (unit < a.n_units && (lane % S) == 0 && (!kSwi || i < RU / 2)) {
-        epilogue<MODE>(P0, row_of<RU, MODE>(cur.row_base, i, 0), v, up, pre, &bv, &bi, &nf);
+        epilogue<MODE>(P0, row_of<RU, MODE>(cur.row_base, i, 0), v, up, pre, &bv, &bi, &nf, brk);
       }
     }
     __syncthreads();
@@ -903,6 +948,7 @@ __global__ void __launch_bounds__(kWave * kCellWaves) k_gemv_cells(GemvArgs a) {
   __shared__ float s_red[kCellWaves];
   const int lane = threadIdx.x & 63, j = lane >> 4, c = lane & 15, i8 = lane >> 3;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const BreakIn bin = break_in<MODE>(a);  // (before any store or asm: scalar loads)
   args_batch<MODE>(a);
   const uint32_t half = a.rope.head_dim / 2, unit0 = blockIdx.x * UPW;
 
@@ -999,6 +1045,7 @@ __global__ void __launch_bounds__(kWave * kCellWaves) k_gemv_cells(GemvArgs a) {
   // 2. the (normalised) input into LDS
   float ss = 0.0f, inv = 1.0f;
   stage_x_finish<kNorm, false, 2, kWave * kCellWaves, 2048>(a, xr, s_x, s_red, &ss, &inv);
+  const bool brk = break_now<MODE>(a, bin, !isfinite(ss));
 
   // 3. per unit the lane's two 32-column dots, summed over the 16 lanes of each row, then over
   // the waves
@@ -1054,9 +1101,9 @@ __global__ void __launch_bounds__(kWave * kCellWaves) k_gemv_cells(GemvArgs a) {
     E0.rope_role = erole;
     E0.y = pick_part(a, int(__builtin_amdgcn_readfirstlane(part_of(a, min(unit0 + ew, a.n_units - 1))))).y;
     if ((lane % S) == 0 && i8 < RU / 2 && orow < E0.rows)
-      rope_store(a, E0, orow, v + prev, up + up_pre, rope_ok ? rc : 1.0f, rope_ok ? rs : 0.0f);
+      rope_store(a, E0, orow, v + prev, up + up_pre, rope_ok ? rc : 1.0f, rope_ok ? rs : 0.0f, brk);
   } else if ((lane % S) == 0 && (!kSwi || i8 < RU / 2)) {
-    epilogue<MODE>(E0, row_of<RU, MODE>(erow_base, i8, 0), v, up, prev, &bv, &bi, &nf);
+    epilogue<MODE>(E0, row_of<RU, MODE>(erow_base, i8, 0), v, up, prev, &bv, &bi, &nf, brk);
   }
 }
 
@@ -1120,7 +1167,8 @@ __device__ __forceinline__ void mma_stage(const float4& xa, const float4& xb, co
   for (int i = 0; i < 8; ++i) {
     xp[i] = kNorm ? xv[i] * gv[i] : xv[i];
     q2 = fmaf(xv[i], xv[i], q2);
-    mx = fmaxf(mx, fabsf(xp[i]));
+    const float ax = fabsf(xp[i]);  // (a NaN counts as infinite: the group's factor becomes NaN)
+    mx = ax != ax ? __int_as_float(0x7f800000) : fmaxf(mx, ax);
   }
   mx = pair_max(mx, 1);
   mx = pair_max(mx, 2);
@@ -1227,6 +1275,7 @@ __global__ void __launch_bounds__(kWave * kMmaWaves) k_gemv_mma(GemvArgs a) {
   __shared__ float s_red[kMmaWaves];
   const int lane = threadIdx.x & 63, m = lane & 15, kq = lane >> 4, i8 = lane >> 3;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const BreakIn bin = break_in<MODE>(a);  // (before any store or asm: scalar loads)
   args_batch<MODE>(a);
   const uint32_t half = a.rope.head_dim / 2, tile0 = blockIdx.x * UPW;
 
@@ -1369,14 +1418,15 @@ __global__ void __launch_bounds__(kWave * kMmaWaves) k_gemv_mma(GemvArgs a) {
     o2 = pair_sum(o2, 4);
     v2 += o2;
   }
+  float ss = 0.0f;
   if constexpr (kNorm) {
-    float ss = 0.0f;
 #pragma unroll
     for (int w = 0; w < kMmaWaves; ++w) ss += s_red[w];
     const float inv = 1.0f / sqrtf(ss / 2048.0f + a.eps);
     v *= inv;
     v2 *= inv;
   }
+  const bool brk = break_now<MODE>(a, bin, !isfinite(ss));
   const float upv = kSwi ? v2 : (kRope ? pair_val(v, 32) : 0.0f);
   const float prev = pre_ok ? pre : 0.0f;
   const float up_pre = kRope ? pair_val(prev, 32) : 0.0f;
@@ -1389,11 +1439,11 @@ __global__ void __launch_bounds__(kWave * kMmaWaves) k_gemv_mma(GemvArgs a) {
   if constexpr (kRope) {
     E0.rope_role = erole;
     if ((lane % S) == 0 && !oB && ovalid)
-      rope_store(a, E0, orow, v + prev, upv + up_pre, rope_ok ? rc : 1.0f, rope_ok ? rs : 0.0f);
+      rope_store(a, E0, orow, v + prev, upv + up_pre, rope_ok ? rc : 1.0f, rope_ok ? rs : 0.0f, brk);
   } else if constexpr (kSwi) {
     if ((lane % S) == 0 && ovalid) epilogue<MODE>(E0, orow, v, upv, prev, &bv, &bi, &nf);
   } else {
-    if ((lane % S) == 0 && ovalid) epilogue<MODE>(E0, orow, v, upv, prev, &bv, &bi, &nf);
+    if ((lane % S) == 0 && ovalid) epilogue<MODE>(E0, orow, v, upv, prev, &bv, &bi, &nf, brk);
   }
 }
 
@@ -1530,6 +1580,7 @@ __global__ void __launch_bounds__(kWave * W) k_gemv_flat(GemvArgs a) {
   __shared__ float s_red[W];
   const int lane = threadIdx.x & 63, j = lane >> 4, c = lane & 15;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const BreakIn bin = break_in<MODE>(a);  // (before any store or asm: scalar loads)
   args_batch<MODE>(a);
   const uint32_t C = a.C, ng = C >> 7, npan = (ng + 3) / 4, half = a.rope.head_dim / 2, unit = blockIdx.x;
   const GemvPart P0 = kRope ? pick_part(a, int(__builtin_amdgcn_readfirstlane(part_of(a, unit)))) : a.part[0];
@@ -1639,6 +1690,7 @@ __global__ void __launch_bounds__(kWave * W) k_gemv_flat(GemvArgs a) {
   } else {
     stage_x_finish<kNorm, kWide, SL, NT>(a, xr, s_x, s_red, &ss, &inv);
   }
+  const bool brk = break_now<MODE>(a, bin, !isfinite(ss));
   // the corrections' input columns (kLocal: from global memory, requested before the dots)
   float xca[SPL], xcb[SPL];
 #pragma unroll
@@ -1707,10 +1759,10 @@ __global__ void __launch_bounds__(kWave * W) k_gemv_flat(GemvArgs a) {
   uint32_t bi = 0xffffffffu, nf = 0;
   if constexpr (kRope) {
     if ((lane % S) == 0 && i8 < RU / 2 && orow < P0.rows)
-      rope_store(a, P0, orow, v + prev, up + up_pre, rope_ok ? rc : 1.0f, rope_ok ? rs : 0.0f);
+      rope_store(a, P0, orow, v + prev, up + up_pre, rope_ok ? rc : 1.0f, rope_ok ? rs : 0.0f, brk);
   } else if ((lane % S) == 0 && (!kSwi || i8 < RU / 2) &&
              (MODE != int(GemvMode::Accum) || orow < P0.wrows)) {  // Accum: rows past the tiles stay
-    epilogue<MODE>(P0, row_of<RU, MODE>(row_base, i8, 0), v, up, prev, &bv, &bi, &nf);
+    epilogue<MODE>(P0, row_of<RU, MODE>(row_base, i8, 0), v, up, prev, &bv, &bi, &nf, brk);
   }
 }
 
@@ -1769,6 +1821,7 @@ __global__ void __launch_bounds__(kWave * NW) k_gemv_xs(GemvArgs a) {
   __shared__ uint32_t s_bi[NW], s_nf[NW];
   const int lane = threadIdx.x & 63;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const BreakIn bin = break_in<MODE>(a);  // (before any store or asm: scalar loads)
   args_batch<MODE>(a);
   const uint32_t C = a.C, ng = C >> 7, half = a.rope.head_dim / 2, n_units = a.n_units, step = gridDim.x;
   const uint32_t col = wave * CH + uint32_t(KC * lane);
@@ -1886,6 +1939,7 @@ __global__ void __launch_bounds__(kWave * NW) k_gemv_xs(GemvArgs a) {
   float sx = 0.0f;
 #pragma unroll
   for (int j = 0; j < KC; ++j) sx += xv[j];
+  const bool brk = break_now<MODE>(a, bin, !isfinite(tot));
   __syncthreads();  // s_x complete
 
   float bv = -1e30f;
@@ -1924,9 +1978,9 @@ __global__ void __launch_bounds__(kWave * NW) k_gemv_xs(GemvArgs a) {
       }
       const uint32_t r = row_of<R, MODE>(rb, lane, half);
       if constexpr (kRope) {
-        if (r < P0.rows) rope_store(a, P0, r, y0 + L.pre, y1 + L.pre2, L.rc, L.rs);
+        if (r < P0.rows) rope_store(a, P0, r, y0 + L.pre, y1 + L.pre2, L.rc, L.rs, brk);
       } else if (MODE != int(GemvMode::Accum) || r < P0.wrows) {  // Accum: rows past the tiles stay
-        epilogue<MODE>(P0, r, y0, y1, L.pre, &bv, &bi, &nf);
+        epilogue<MODE>(P0, r, y0, y1, L.pre, &bv, &bi, &nf, brk);
       }
     }
   };
@@ -2054,6 +2108,7 @@ __global__ void __launch_bounds__(kWave * NW) k_gemv_xm(GemvArgs a) {
   __shared__ uint32_t s_bi[NW], s_nf[NW];
   const int lane = threadIdx.x & 63, n = lane & 15, q = lane >> 4;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const BreakIn bin = break_in<MODE>(a);  // (before any store or asm: scalar loads)
   args_batch<MODE>(a);
   const uint32_t C = a.C, ng = C >> 7, half = a.rope.head_dim / 2, n_units = a.n_units, step = gridDim.x;
   const uint32_t gw = wave * 16;  // the wave's first group
@@ -2188,11 +2243,12 @@ __global__ void __launch_bounds__(kWave * NW) k_gemv_xm(GemvArgs a) {
 #pragma unroll
       for (int i = 0; i < 8; ++i) xp[i] = (xp[i] * inv) * gv[i];
     }
-    float mx = 0.0f;
+    float mx = 0.0f;  // (a NaN counts as infinite: the group's factor becomes NaN, as its sum would)
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       xp[i] = live ? xp[i] : 0.0f;
-      mx = fmaxf(mx, fabsf(xp[i]));
+      const float ax = fabsf(xp[i]);
+      mx = ax != ax ? __int_as_float(0x7f800000) : fmaxf(mx, ax);
     }
     mx = pair_max(mx, 1);
     mx = pair_max(mx, 2);
@@ -2238,6 +2294,7 @@ __global__ void __launch_bounds__(kWave * NW) k_gemv_xm(GemvArgs a) {
     if ((lane & 15) == 0)
       s_e[(wave * 4 + uint32_t(S)) * 4 + gs] = isfinite(mx) ? ldexpf(1.0f, e - 30) : __int_as_float(0x7fc00000);
   }
+  const bool brk = break_now<MODE>(a, bin, !isfinite(tot));
   __syncthreads();  // every wave's table (the corrections read any column)
   int cinit[4];
   float lpf[4];
@@ -2317,9 +2374,9 @@ __global__ void __launch_bounds__(kWave * NW) k_gemv_xm(GemvArgs a) {
       }
       const uint32_t r = row_of<R, MODE>(rb, lane, half);
       if constexpr (kRope) {
-        if (r < P0.rows) rope_store(a, P0, r, y0 + L.pre, y1 + L.pre2, L.rc, L.rs);
+        if (r < P0.rows) rope_store(a, P0, r, y0 + L.pre, y1 + L.pre2, L.rc, L.rs, brk);
       } else if (MODE != int(GemvMode::Accum) || r < P0.wrows) {  // Accum: rows past the tiles stay
-        epilogue<MODE>(P0, r, y0, y1, L.pre, &bv, &bi, &nf);
+        epilogue<MODE>(P0, r, y0, y1, L.pre, &bv, &bi, &nf, brk);
       }
     }
   };
@@ -2508,7 +2565,8 @@ void launch_layout(const GemvArgs& a, const GemvLaunch& g, hipStream_t st) {
 // prefix sums of dims.rows the host computed by gemvLinear's walk (:1430-1442).
 
 // x (RMSNorm'ed with gamma when gamma is set: (x * inv_rms) * gamma, rmsNorm :163-193) into out
-// (and |x|, the hidden norm of the LM head's input, into *result when set)
+// and its sum of squares into out[n] (and |x|, the hidden norm of the LM head's input, into
+// *result when set)
 __global__ void __launch_bounds__(1024) k_rmsnorm(const float* x, const float* gamma, float eps, uint32_t n,
                                                   float* out, StepResult* result) {
 #pragma clang fp contract(off)
@@ -2523,6 +2581,7 @@ __global__ void __launch_bounds__(1024) k_rmsnorm(const float* x, const float* g
   for (int w = 0; w < int(blockDim.x / kWave); ++w) tot += s_red[w];
   const float inv = 1.0f / sqrtf(tot / float(n) + eps);
   for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) out[i] = (x[i] * inv) * gamma[i];
+  if (threadIdx.x == 0) out[n] = tot;
   if (result && threadIdx.x == 0) result->hidden_norm = sqrtf(tot);
 }
 
@@ -2612,15 +2671,17 @@ __global__ void __launch_bounds__(256) k_gemv_poly(const uint8_t* base, uint32_t
   }
 }
 
-// the mode's epilogue on the raw row sums: grid-stride over rows (QkvRope: over RoPE pairs)
+// the mode's epilogue on the raw row sums: grid-stride over rows (QkvRope: over RoPE pairs);
+// ss: the normalised input's sum of squares (k_rmsnorm), or null
 template <int MODE>
-__global__ void __launch_bounds__(256) k_poly_epilogue(GemvArgs a, PolyRaw raw) {
+__global__ void __launch_bounds__(256) k_poly_epilogue(GemvArgs a, PolyRaw raw, const float* ss) {
 #pragma clang fp contract(off)
   __shared__ float s_bv[4];
   __shared__ uint32_t s_bi[4], s_nf[4];
   float bv = -1e30f;
   uint32_t bi = 0xffffffffu, nf = 0;
   const uint32_t stride = gridDim.x * blockDim.x;
+  const bool brk = break_now<MODE>(a, break_in<MODE>(a), ss != nullptr && !isfinite(*ss));
   if constexpr (MODE == int(GemvMode::QkvRope)) {
     const uint32_t half = a.rope.head_dim / 2;
     for (int p = 0; p < a.n_parts; ++p) {
@@ -2629,7 +2690,7 @@ __global__ void __launch_bounds__(256) k_poly_epilogue(GemvArgs a, PolyRaw raw) 
         const uint32_t r = (i / half) * (2 * half) + i % half, d = i % half;
         const float lo = raw.y[p][r] + (P.bias ? P.bias[r] : 0.0f);
         const float hi = raw.y[p][r + half] + (P.bias ? P.bias[r + half] : 0.0f);
-        rope_store(a, P, r, lo, hi, a.rope.cos[d], a.rope.sin[d]);
+        rope_store(a, P, r, lo, hi, a.rope.cos[d], a.rope.sin[d], brk);
       }
     }
   } else {
@@ -2638,7 +2699,7 @@ __global__ void __launch_bounds__(256) k_poly_epilogue(GemvArgs a, PolyRaw raw) 
       const float v = raw.y[0][r];
       const float u = MODE == int(GemvMode::SwiGlu) ? raw.y[1][r] : 0.0f;
       const float pre = MODE == int(GemvMode::Accum) ? P.y[r] : (P.bias ? P.bias[r] : 0.0f);
-      epilogue<MODE>(P, r, v, u, pre, &bv, &bi, &nf);
+      epilogue<MODE>(P, r, v, u, pre, &bv, &bi, &nf, brk);
     }
   }
   if constexpr (MODE == int(GemvMode::Logits)) argmax_partial<MODE>(a, bv, bi, nf, s_bv, s_bi, s_nf);
@@ -2883,21 +2944,23 @@ GemvLaunch gemv_geometry(WeightKind kind, GemvMode mode, uint32_t C, const uint3
 uint32_t launch_gemv_poly(const GemvArgs& a, const PolyPlan* const* plans, float* xn, const PolyRaw& raw,
                           hipStream_t st) {
   const float* x = a.x;
+  const float* ss = nullptr;
   if (a.gamma) {
     StepResult* res = GemvMode(a.mode) == GemvMode::Logits ? a.result : nullptr;
     launch_kernel(&k_rmsnorm, dim3(1), dim3(1024), st, a.x, a.gamma, a.eps, a.C, xn, res);
     x = xn;
+    ss = xn + a.C;
   }
   for (int p = 0; p < a.n_parts; ++p)
     launch_kernel(&k_gemv_poly, dim3(plans[p]->n_cells + 1), dim3(256), st, a.part[p].base, a.part[p].stride,
                   plans[p]->row_base, plans[p]->n_cells, x, a.C, raw.y[p], a.part[p].rows);
   const uint32_t blocks = kPolyEpilogueBlocks;
   switch (GemvMode(a.mode)) {
-    case GemvMode::Store: launch_kernel(&k_poly_epilogue<int(GemvMode::Store)>, dim3(blocks), dim3(256), st, a, raw); break;
-    case GemvMode::Accum: launch_kernel(&k_poly_epilogue<int(GemvMode::Accum)>, dim3(blocks), dim3(256), st, a, raw); break;
-    case GemvMode::SwiGlu: launch_kernel(&k_poly_epilogue<int(GemvMode::SwiGlu)>, dim3(blocks), dim3(256), st, a, raw); break;
-    case GemvMode::Logits: launch_kernel(&k_poly_epilogue<int(GemvMode::Logits)>, dim3(blocks), dim3(256), st, a, raw); break;
-    case GemvMode::QkvRope: launch_kernel(&k_poly_epilogue<int(GemvMode::QkvRope)>, dim3(blocks), dim3(256), st, a, raw); break;
+    case GemvMode::Store: launch_kernel(&k_poly_epilogue<int(GemvMode::Store)>, dim3(blocks), dim3(256), st, a, raw, ss); break;
+    case GemvMode::Accum: launch_kernel(&k_poly_epilogue<int(GemvMode::Accum)>, dim3(blocks), dim3(256), st, a, raw, ss); break;
+    case GemvMode::SwiGlu: launch_kernel(&k_poly_epilogue<int(GemvMode::SwiGlu)>, dim3(blocks), dim3(256), st, a, raw, ss); break;
+    case GemvMode::Logits: launch_kernel(&k_poly_epilogue<int(GemvMode::Logits)>, dim3(blocks), dim3(256), st, a, raw, ss); break;
+    case GemvMode::QkvRope: launch_kernel(&k_poly_epilogue<int(GemvMode::QkvRope)>, dim3(blocks), dim3(256), st, a, raw, ss); break;
   }
   return blocks;
 }

@@ -42,12 +42,15 @@ enum RopeRole : uint32_t { kRoleQ = 0, kRoleK = 1, kRoleV = 2 };
 struct StepState;
 
 struct RopeArgs {            // QkvRope: applyRope (chpe_engine.zig:195-216) + KV append (:1693-1697)
-  const StepState* state;
+  StepState* state;          // (also set for the residual launches: StepState::broken)
   const float* cos;          // [head_dim/2]: the step's row of the cos table (staged by k_embed /
   const float* sin;          //   k_finish from the [max_seq][head_dim/2] tables), and of sin
   void* k_cache;             // this layer: [KV][max_seq][head_dim], f16 or f32
   void* v_cache;             // f32: as k_cache; f16: [KV][max_seq/4][head_dim][4] (4-position blocks)
-  uint32_t head_dim, max_seq, kv_f16, pad;  // max_seq: cache rows per kv head, a multiple of 16
+  uint32_t head_dim, max_seq, kv_f16;  // max_seq: cache rows per kv head, a multiple of 16
+  uint32_t brk_check;        // the break test this launch makes on its input (see StepState::broken):
+                             //   0 none (layer 0), 1 the sum of squares (after layers 0-2 and 8-16),
+                             //   2 the first element (after the other layers)
 };
 
 constexpr int kMaxParts = 3;
@@ -131,6 +134,14 @@ struct StepState {  // device-resident per-token state read by the captured step
   uint32_t pos;
   uint32_t n_prompt;   // positions teacher-forced from `prompt`
   uint32_t n_steps;
+  // forwardDecode's non-finite break (chpe_engine.zig:1753-1764): after layer l the reference
+  // leaves the layer loop when the hidden state's sum of squares is not finite, a test it makes
+  // after layers 0-2 and 8-16 and whenever hidden[0] is not finite; the final norm and the LM
+  // head then see the hidden state of the break.  The q/k/v launch of layer l + 1 makes the test
+  // on its input (RopeArgs::brk_check) and sets `broken`; from then on the step's launches write
+  // neither the KV cache nor the residual stream.  k_finish clears it for the next step.
+  uint32_t broken = 0;
+  uint32_t pad[3] = {0, 0, 0};
 };
 
 struct EmbedArgs {
@@ -230,7 +241,8 @@ struct PolyRaw {             // raw row sums per part (device, >= the part's row
   float* y[kMaxParts];
 };
 constexpr uint32_t kPolyEpilogueBlocks = 64;
-// one GEMV over polymorphic cells: the input RMSNorm'ed into xn (when a.gamma is set), the raw
+// one GEMV over polymorphic cells: the input RMSNorm'ed into xn (when a.gamma is set; xn holds
+// C + 1 floats, the last one the input's sum of squares), the raw
 // row sums of every part, then the mode's epilogue (a.part[*].y, bias, RoPE / KV append,
 // SwiGLU, residual, logits + argmax partials: kPolyEpilogueBlocks of them).  Returns the
 // number of argmax partials.
@@ -275,6 +287,7 @@ struct BlockGemvArgs {
   uint32_t rope_rows;
   ArgmaxPartial* partials;  // Logits: [kMaxBlock][epi_blocks]
   uint32_t epi_blocks;      // set by launch_block_gemv
+  uint32_t* brk;            // [kMaxBlock]: token t broke (StepState::broken), cleared by the block's embedding
 };
 
 struct BlockFinishArgs {
@@ -287,9 +300,9 @@ struct BlockFinishArgs {
   StepResult* result;             // the last token's result
 };
 
-// embeds m tokens into X [m][D] and leaves each row's sum of squares in ssp[0][t]
+// embeds m tokens into X [m][D], leaves each row's sum of squares in ssp[0][t] and clears brk[t]
 void launch_block_embed(const EmbedArgs& e, const uint32_t* tokens, uint32_t m, float* X, float* ssp,
-                        hipStream_t stream);
+                        uint32_t* brk, hipStream_t stream);
 // the input's operand tables (k_block_limbs), then the block GEMV (k_gemv_mt) and its epilogue;
 // launch_block_gemv returns the epilogue's workgroups (Logits / Σy² partials)
 void launch_block_limbs(const BlockGemvArgs& a, hipStream_t stream);

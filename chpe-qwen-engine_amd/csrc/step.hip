@@ -168,8 +168,10 @@ __global__ void __launch_bounds__(256) k_embed(EmbedArgs a) {
 
 // the block step's inputs: token blockIdx.x's embedding row into X[blockIdx.x]
 // one workgroup per token; then the row's sum of squares (the first layer's RMS norm)
-__global__ void __launch_bounds__(256) k_block_embed(EmbedArgs a, const uint32_t* tokens, float* X, float* ssp) {
+__global__ void __launch_bounds__(256) k_block_embed(EmbedArgs a, const uint32_t* tokens, float* X, float* ssp,
+                                                     uint32_t* brk) {
   EmbedArgs e = a;
+  if (threadIdx.x == 0) brk[blockIdx.x] = 0u;
   float* row = X + size_t(blockIdx.x) * a.D;
   e.hidden = row;
   embed_token(e, tokens[blockIdx.x]);
@@ -237,6 +239,7 @@ __global__ void __launch_bounds__(256) k_finish(FinishArgs a) {
   s.token = (a.prompt && next < s.n_prompt) ? ptok : arg;
   s.pos = next;
   s.n_steps += 1;
+  s.broken = 0u;
   *a.state = s;
   s_next = s.token;
   }
@@ -312,8 +315,9 @@ void launch_embed(const EmbedArgs& a, hipStream_t st) {
   launch_kernel(k_embed, dim3(1), dim3(256), st, a);
 }
 
-void launch_block_embed(const EmbedArgs& e, const uint32_t* tokens, uint32_t m, float* X, float* ssp, hipStream_t st) {
-  launch_kernel(k_block_embed, dim3(m), dim3(256), st, e, tokens, X, ssp);
+void launch_block_embed(const EmbedArgs& e, const uint32_t* tokens, uint32_t m, float* X, float* ssp, uint32_t* brk,
+                        hipStream_t st) {
+  launch_kernel(k_block_embed, dim3(m), dim3(256), st, e, tokens, X, ssp, brk);
 }
 
 void launch_finish(const FinishArgs& a, hipStream_t st) {

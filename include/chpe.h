@@ -87,6 +87,9 @@ int chpe_block_ready(void *ctx);
 
 /* Message of the last failed chpe_init / chpe_init_ex on this thread ("" if none). */
 const char *chpe_last_error(void);
+/* The first 16 hex digits of the SHA-256 of the sources this library was built from (the
+ * Makefile's LIBSRC list), so that a caller can tell a library built from other sources. */
+const char *chpe_build_id(void);
 
 size_t chpe_get_max_seq_len(void *ctx);
 /* hidden_dim floats of the residual stream after the last step. */

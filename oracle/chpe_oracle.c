@@ -19,8 +19,10 @@
  *                             accumulate): test_oracle_pinning.py
  *                             test_f16_bf16_f32_cells_are_float64_products
  *   gemvCellFlat ............ closed-form tiles (group scales, replaced outliers, the 2-bit
- *                             codebook): test_oracle_kats.py test_flat_tile_*; the down
- *                             projection within the quantizer's bound (test_oracle_step.py)
+ *                             codebook, the no-group scale + bias forms of both widths with
+ *                             the product and the sum rounded separately): test_oracle_kats.py
+ *                             test_flat_tile_*; the down projection within the quantizer's
+ *                             bound (test_oracle_step.py)
  *   dotSegment / raw gemvLinear / raw unpackEmbedRow / raw tied computeLmHead (fp16, bf16,
  *   int8 x 0.00373708) ...... float64 products of the generator's weights within the f32
  *                             summation bound, rows straddling tiles, embedding rows bit for
@@ -30,6 +32,10 @@
  *                             test_oracle_pinning.py test_embed_row_cell_forms_match_numpy_decode;
  *                             the generator's weights within the quantizer's bound:
  *                             test_oracle_step.py test_embedding_row_within_quantization_bound
+ *   f16 / bf16 widening, f32 -> f16 rounding (the fp16 KV cache) ...... numpy's float16 over
+ *                             all 65536 codes and over every f32 of the f16 exponent range:
+ *                             test_oracle_kats.py test_f16_widening_exhaustive,
+ *                             test_f32_to_f16_matches_numpy
  *   rmsNorm ................. KAT qwen_rmsnorm.zig:73-90 + float64: test_oracle_kats.py
  *   applyRope ............... KAT qwen_rope.zig:149-162, pos-0 identity, closed form
  *   silu .................... KAT qwen_mlp.zig:92-111
@@ -114,7 +120,9 @@ float oref_bf16_to_f32(uint16_t h) {
     return f;
 }
 
-/* f32 -> f16 round-to-nearest-even (used for the fp16-KV variant only). */
+/* f32 -> f16 round-to-nearest-even (used for the fp16-KV variant only; the reference keeps an
+ * f32 cache).  Pinned against numpy's float16 conversion over every f32 whose exponent reaches
+ * the f16 range, both signs (test_oracle_kats.py test_f32_to_f16_matches_numpy). */
 static uint16_t f32_to_f16(float f) {
     uint32_t x;
     memcpy(&x, &f, 4);
@@ -133,6 +141,14 @@ static uint16_t f32_to_f16(float f) {
     uint32_t half = ((uint32_t)e << 10) | (man >> 13), rem = man & 0x1fffu;
     if (rem > 0x1000u || (rem == 0x1000u && (half & 1u))) half++;
     return (uint16_t)(sign | half);
+}
+
+void oref_f32_to_f16_n(const float *x, uint16_t *out, size_t n) {
+    for (size_t i = 0; i < n; i++) out[i] = f32_to_f16(x[i]);
+}
+
+void oref_f16_to_f32_n(const uint16_t *h, float *out, size_t n) {
+    for (size_t i = 0; i < n; i++) out[i] = oref_f16_to_f32(h[i]);
 }
 
 static uint64_t now_ns(void) { /* nowNs: src/chpe_engine.zig:812-816 */
@@ -711,6 +727,7 @@ struct oref_engine {
     uint8_t quant_bits;
     size_t record_count, stride, wpt, max_seq_len;
     int kv_f16, threads;
+    int no_break;  /* test only: skip forwardDecode's non-finite break (a planted deviation) */
     float *hidden, *norm_buf, *norm_gamma, *bias_buf, *q_buf, *k_buf, *v_buf, *attn_out, *gate_buf,
         *up_buf, *mlp_buf, *scores_buf, *logits_buf, *k_cache, *v_cache;
 };
@@ -792,6 +809,10 @@ static void set_threads(const oref_engine *e) {
 }
 
 void oref_set_threads(oref_engine *e, int threads) { e->threads = threads; }
+
+/* Test only: with on == 0 the layer loop never breaks (:1763 removed) -- the deviation a test
+ * plants to show that its comparison tells the break from its absence. */
+void oref_set_break(oref_engine *e, int on) { e->no_break = on ? 0 : 1; }
 
 oref_engine *oref_open_bytes(const uint8_t *bytes, size_t len, int arch_id, size_t max_seq_len,
                              int kv_f16, int threads) {
@@ -1203,7 +1224,7 @@ static int forward_layers(oref_engine *e, uint32_t token, size_t pos, size_t n_l
         oref_gemv_linear(e, li.down_proj, li.down_tiles, e->mlp_buf, I, e->hidden, D, D, I, 1, -1);
         /* debug-norm block (:1753-1764): only its non-finite break changes results */
         if (l < 3 || (l >= 8 && l <= 16) || !isfinite(e->hidden[0]))
-            if (!isfinite(sumsq_seq(e->hidden, D))) break;
+            if (!isfinite(sumsq_seq(e->hidden, D)) && !e->no_break) break;
     }
     oref_unpack_norm(e, oref_final_norm_for(e->map), e->norm_gamma, D);
     oref_rmsnorm(e->hidden, e->norm_gamma, e->norm_buf, D, a->rms_eps);

@@ -61,6 +61,9 @@ float oref_silu(float z);
 void oref_rmsnorm(const float *x, const float *gamma, float *y, size_t n, float eps);
 void oref_apply_rope(float *vec, size_t pos, size_t num_heads, size_t head_dim, float theta);
 float oref_f16_to_f32(uint16_t h);
+/* element-wise: f32 -> f16 round-to-nearest-even (the fp16 KV cache), f16 -> f32 */
+void oref_f32_to_f16_n(const float *x, uint16_t *out, size_t n);
+void oref_f16_to_f32_n(const uint16_t *h, float *out, size_t n);
 float oref_bf16_to_f32(uint16_t h);
 
 /* ---- cell kernels on one 17408-byte cell (src/chpe_engine.zig:223-751, 1288-1394) ---- */
@@ -117,6 +120,7 @@ void oref_close(oref_engine *e);
 int oref_forward(oref_engine *e, uint32_t token, size_t pos, oref_result *res);
 /* worker threads of the row-parallel loops (results do not depend on it) */
 void oref_set_threads(oref_engine *e, int threads);
+void oref_set_break(oref_engine *e, int on);  /* test only: 0 removes the non-finite break */
 /* the same step over the first n_layers layers only (a CPU timing sample) */
 int oref_forward_layers(oref_engine *e, uint32_t token, size_t pos, size_t n_layers, oref_result *res);
 /* Timing aid (no reference counterpart): fill K/V cache rows 0..n_pos-1 of every layer with

@@ -52,6 +52,7 @@ def lib():
         L.oref_forward_layers.restype = ctypes.c_int
         L.oref_forward_layers.argtypes = [V, ctypes.c_uint32, S, S, ctypes.POINTER(Result)]
         L.oref_set_threads.argtypes = [V, ctypes.c_int]
+        L.oref_set_break.argtypes = [V, ctypes.c_int]
         L.oref_logits.restype = _fp
         L.oref_logits.argtypes = [V]
         L.oref_hidden.restype = _fp
@@ -78,6 +79,9 @@ def lib():
         L.oref_apply_rope.argtypes = [_fp, S, S, S, ctypes.c_float]
         L.oref_f16_to_f32.restype = ctypes.c_float
         L.oref_f16_to_f32.argtypes = [ctypes.c_uint16]
+        _u16p = ctypes.POINTER(ctypes.c_uint16)
+        L.oref_f32_to_f16_n.argtypes = [_fp, _u16p, S]
+        L.oref_f16_to_f32_n.argtypes = [_u16p, _fp, S]
         L.oref_gemv_tile_polymorphic.argtypes = [_u8p, _fp, S, _fp, S, S, ctypes.c_int]
         L.oref_flat_tile_weights.argtypes = [_u8p, S, _fp]
         L.oref_gemv_cell_flat.argtypes = [_u8p, S, S, S, S, _fp, _fp]
@@ -153,6 +157,11 @@ class Oracle:
 
     def set_threads(self, n):
         self.L.oref_set_threads(self.e, n)
+
+    def set_break(self, on):
+        """Test only: set_break(False) removes forwardDecode's non-finite break (:1763), a
+        planted deviation that shows a comparison can tell the break from its absence."""
+        self.L.oref_set_break(self.e, 1 if on else 0)
 
     def prefill_synthetic(self, n_pos, seed=0):
         if self.L.oref_prefill_synthetic(self.e, n_pos, seed):
@@ -311,3 +320,19 @@ def validate(data):
 
 def f16_to_f32(h):
     return lib().oref_f16_to_f32(h)
+
+
+def f16_to_f32_array(h):
+    """The oracle's f16 -> f32 widening of every element of a uint16 array."""
+    h = np.ascontiguousarray(h, dtype=np.uint16)
+    out = np.empty(h.size, dtype=np.float32)
+    lib().oref_f16_to_f32_n(h.ctypes.data_as(ctypes.POINTER(ctypes.c_uint16)), out.ctypes.data_as(_fp), h.size)
+    return out
+
+
+def f32_to_f16_array(x):
+    """The oracle's f32 -> f16 rounding (its fp16 KV cache) of every element, as uint16 codes."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty(x.size, dtype=np.uint16)
+    lib().oref_f32_to_f16_n(x.ctypes.data_as(_fp), out.ctypes.data_as(ctypes.POINTER(ctypes.c_uint16)), x.size)
+    return out

@@ -84,13 +84,25 @@ def run_model(path, arch, vocab, n_prompt, n_gen, seed):
     e = ca.Engine(path, arch=arch, max_seq_len=64, kv_f16=False)
     o = orc.Oracle(path, arch=arch, max_seq_len=64, kv_f16=False, threads=threads())
     try:
+        steps = []
         for pos in range(2):
             say(f"f32 KV step pos={pos} token={int(prompt[pos])}")
             am, lg = e.decode_step(int(prompt[pos]), pos)
             r = o.forward(int(prompt[pos]), pos)
-            compare_logits(lg, o.logits(), f"pos {pos}", 2e-4)
+            ol = o.logits()
+            compare_logits(lg, ol, f"pos {pos}", 2e-4)
             assert am == r.argmax_token and r.all_finite
             assert e.last()["hidden_norm"] == pytest.approx(r.hidden_norm, rel=1e-4)
+            steps.append((lg.astype(np.float64), ol.astype(np.float64)))
+        # the steps' dependence on their input: the change of the logits from one teacher-forced
+        # token to the next is the oracle's within the two steps' bars, and it is large against
+        # them -- a step that ignored its token (or the context) fails this even where the
+        # argmax does not move (the 2-bit model's greedy stream repeats one token)
+        (g0, o0), (g1, o1) = steps
+        bar = 2 * 2e-4 * float(max(np.abs(o0).max(), np.abs(o1).max()))
+        dd, dref = float(np.abs((g1 - g0) - (o1 - o0)).max()), float(np.abs(o1 - o0).max())
+        say(f"  logit change pos 0 -> 1: max {dref:.4f}, gpu vs oracle {dd:.2e} (bar {bar:.2e})")
+        assert dd <= bar and dref >= 20 * bar
         say(f"stream (f32 KV): {n_prompt} prompt + {n_gen} generated")
         g = e.generate(prompt, n_gen)
         ref, gaps = o.generate(prompt, n_gen)
@@ -175,17 +187,84 @@ def run_block(path, arch, vocab, seed, oracle_check):
                     for pos, tok in enumerate(prompt):
                         o.forward(int(tok), pos)
                     compare_logits(lblk, o.logits(), "prefill vs oracle", rel)
+                    # verify of 4 drafts (the batch-4 configuration) against the oracle's
+                    # sequential steps: every argmax, the last draft's logits
+                    e.prefill(prompt)
+                    say("  verify 4 drafts vs the oracle")
+                    got4 = e.verify(drafts[:4], n)
+                    lv4 = e.logits()
+                    for i in range(4):
+                        r = o.forward(int(drafts[i]), n + i)
+                        if int(got4[i]) != r.argmax_token:
+                            ol = o.logits()
+                            assert top2_gap(ol) < 2 * rel * float(np.abs(ol).max()), (i, int(got4[i]), r.argmax_token)
+                    compare_logits(lv4, o.logits(), "verify 4: last draft vs oracle", rel)
+                    # the device state continues where the sequential steps would leave it:
+                    # the last draft's argmax at position n + 4 (one step launched from it)
+                    e.time_steps(1)
+                    o.forward(int(got4[3]), n + 4)
+                    compare_logits(e.logits(), o.logits(), "step continuing after verify 4 vs oracle", rel)
                 finally:
                     o.close()
         finally:
             e.close()
 
 
-@pytest.mark.timeout(900)
+@pytest.mark.timeout(1200)
 def test_72b_block_step_matches_decode_steps(a72):
-    run_block(a72, 2, 152064, seed=5, oracle_check=False)
+    run_block(a72, 2, 152064, seed=5, oracle_check=True)
 
 
 @pytest.mark.timeout(900)
 def test_9b_compat_block_step_matches_decode_steps(a9):
     run_block(a9, 1, 248320, seed=6, oracle_check=True)
+
+
+@pytest.mark.timeout(900)
+def test_9b_break_in_block_and_decode_steps(a9):
+    """forwardDecode's non-finite break (src/chpe_engine.zig:1753-1764) in the block step (per
+    token) and in the decode step: layer 1's down projection with its first group scale set to
+    +inf (row 0, columns 0..127) makes hidden[0] infinite after layer 1 at every position, so the
+    reference leaves the layer loop there; its hidden norm is +inf, its logits NaN (argmax 0,
+    all_finite false), and layers 2-31 write no KV rows.  Without the break (the oracle's
+    set_break(False), a planted deviation) the hidden norm turns NaN."""
+    import tempfile
+    li = orc.layer_info(2, 1)
+    off = 4096 + li["down_proj"] * 17408 + 64 + 16384 + 48
+    data = np.fromfile(a9, dtype=np.uint8)
+    data[off:off + 2] = np.frombuffer(np.uint16(0x7c00).tobytes(), np.uint8)
+    fd, path = tempfile.mkstemp(suffix=".chpe", prefix="qwen3.5-9b-mod-", dir=os.path.dirname(str(a9)))
+    os.close(fd)
+    data.tofile(path)
+    prompt = np.random.default_rng(8).integers(0, 248320, 11).astype(np.uint32)
+    try:
+        e = ca.Engine(path, arch=1, max_seq_len=64, kv_f16=False)
+        o = orc.Oracle(data=data, arch=1, max_seq_len=64, threads=threads())
+        nb = orc.Oracle(data=data, arch=1, max_seq_len=64, threads=threads())
+        nb.set_break(False)
+        try:
+            assert e.block_ready()
+            say("9B break: prefill of 11 positions (blocks of 8 + 3)")
+            am, lg = e.prefill(prompt, want_logits=True)
+            for pos, tok in enumerate(prompt):
+                r = o.forward(int(tok), pos)
+                rn = nb.forward(int(tok), pos)
+            last = e.last()
+            say(f"  gpu argmax {am} hidden_norm {last['hidden_norm']} | oracle {r.argmax_token} {r.hidden_norm} "
+                f"| without the break {rn.hidden_norm}")
+            assert am == r.argmax_token == 0 and not r.all_finite and np.isnan(lg).all()
+            assert np.isinf(last["hidden_norm"]) and np.isinf(r.hidden_norm) and np.isnan(rn.hidden_norm)
+            for i in range(2):
+                pos = len(prompt) + i
+                am, lg = e.decode_step(int(prompt[i]), pos)
+                r = o.forward(int(prompt[i]), pos)
+                last = e.last()
+                say(f"  decode pos {pos}: gpu argmax {am} hidden_norm {last['hidden_norm']} | oracle {r.argmax_token} {r.hidden_norm}")
+                assert am == r.argmax_token and np.isnan(lg).all() and not r.all_finite
+                assert np.isinf(last["hidden_norm"]) and np.isinf(r.hidden_norm)
+        finally:
+            e.close()
+            o.close()
+            nb.close()
+    finally:
+        os.unlink(path)

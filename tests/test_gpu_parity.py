@@ -161,7 +161,10 @@ def test_attention_kernels_match_oracle(hd, H, KV, kv_f16):
     path keeps ~22 bits of the f32 queries and weights; sums run in another order)."""
     rng = np.random.default_rng(hd * 1000 + H + kv_f16)
     chunk = 16384 // hd
-    for pos in (0, 1, 3, 15, 16, 17, chunk - 1, chunk, chunk + 1, 3 * chunk + 5, 1000, 4351):
+    # the contexts the configs decode at: 3B 4096 + 256 and 72B 8192 + 128 (head dim 128),
+    # 9B 2048 + 256 (head dim 256)
+    far = (8191, 8192, 8320) if hd == 128 else (2304, 2312)
+    for pos in (0, 1, 3, 15, 16, 17, chunk - 1, chunk, chunk + 1, 3 * chunk + 5, 1000, 4351) + far:
         say(f"attention hd={hd} H={H} KV={KV} kv_f16={kv_f16} pos={pos}")
         q = (rng.standard_normal(H * hd) * 2.0).astype(np.float32)
         k = rng.standard_normal((pos + 1, KV * hd)).astype(np.float32)

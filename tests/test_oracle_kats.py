@@ -95,6 +95,59 @@ def test_flat_tile_2bit_codebook():
     assert np.array_equal(w, np.tile(np.array([0.0, 0.5, -1.0, -0.5], np.float32), 8192))
 
 
+def _no_group_tile(bits, scale, bias):
+    cell = np.zeros(17408, dtype=np.uint8)
+    cell[PAYLOAD + 20] = bits                   # quant_bits, custom_flags 0: no GROUP128
+    cell[PAYLOAD + 32:PAYLOAD + 36] = np.frombuffer(np.float32(scale).tobytes(), np.uint8)
+    cell[PAYLOAD + 36:PAYLOAD + 40] = np.frombuffer(np.float32(bias).tobytes(), np.uint8)
+    n = 16384 if bits == 4 else 8192
+    cell[64:64 + n] = (np.arange(n) * 37 + 11).astype(np.uint8)   # every code value occurs
+    return cell
+
+
+@pytest.mark.parametrize("bits", [4, 2])
+def test_flat_tile_no_group_scale_bias(bits):
+    # gemvCellFlat without GROUP128 (chpe_engine.zig:619-630 for 4 bits, :666-677 for 2): every
+    # weight is value * dims.scale + dims.bias over the tile's wpt weights, the product and the
+    # sum rounded separately.  Exact case: scale 0.5, bias 0.25 (every result representable).
+    # Rounding case: scale 0.1, bias 0.3 -- the expected value is two float32 roundings (numpy's
+    # float32 multiply, then add); for 4-bit codes a fused multiply-add differs from it on some
+    # codes, which the assert below also checks, so a contracted restatement fails.
+    n = 16384 if bits == 4 else 8192
+    codes = (np.arange(n) * 37 + 11).astype(np.uint8)
+    if bits == 4:
+        val = np.stack([(codes & 15).astype(np.float32) - 8, (codes >> 4).astype(np.float32) - 8], 1).reshape(-1)
+    else:
+        book = np.array([0.0, 1.0, -2.0, -1.0], np.float32)   # CODEBOOK_W2 (:220)
+        val = np.stack([book[(codes >> (2 * s)) & 3] for s in range(4)], 1).reshape(-1)
+    w = orc.flat_tile_weights(_no_group_tile(bits, 0.5, 0.25))
+    assert np.array_equal(w, val * np.float32(0.5) + np.float32(0.25))
+    s, b = np.float32(0.1), np.float32(0.3)
+    w = orc.flat_tile_weights(_no_group_tile(bits, s, b))
+    expect = (val * s).astype(np.float32) + b
+    assert np.array_equal(w, expect)
+    if bits == 4:  # (the 2-bit values +-1, -2 make every product exact: nothing to contract)
+        fused = (val.astype(np.float64) * np.float64(s) + np.float64(b)).astype(np.float32)
+        assert not np.array_equal(expect, fused)
+    # outliers still replace (:632-646), the last entry of an offset counting
+    cell = _no_group_tile(bits, 0.5, 0.25)
+    offs = np.array([7, 7, 30000], np.uint16)
+    vals = np.array([1.5, -3.0, 2.0], np.float16)
+    cell[PAYLOAD + 560:PAYLOAD + 562] = np.frombuffer(np.uint16(3).tobytes(), np.uint8)
+    cell[PAYLOAD + 562:PAYLOAD + 568] = np.frombuffer(vals.tobytes(), np.uint8)
+    cell[PAYLOAD + 690:PAYLOAD + 696] = np.frombuffer(offs.tobytes(), np.uint8)
+    w = orc.flat_tile_weights(cell)
+    expect = val * np.float32(0.5) + np.float32(0.25)
+    expect[7], expect[30000] = -3.0, 2.0
+    assert np.array_equal(w, expect)
+    # and the tile's dot onto rows: a 256 x 128 tensor (one tile) against x = e_c picks column c
+    for c in (0, 77, 127):
+        x = np.zeros(128, np.float32)
+        x[c] = 1.0
+        y = orc.gemv_cell_flat(cell, 0, 256, 128, x, np.zeros(256, np.float32))
+        assert np.array_equal(y, expect.reshape(256, 128)[:, c])
+
+
 # ---------------------------------------------------------------- RoPE / SiLU / RMSNorm
 def test_rope_known_answer():
     # src/qwen_rope.zig:149-162: x[i] = (i+1)*0.1, pos 1, theta 1e6, head_dim 128
@@ -178,12 +231,46 @@ def test_attention_float64_brute_force(pos):
         assert (out[h] <= vv.max(axis=0) + 1e-5).all() and (out[h] >= vv.min(axis=0) - 1e-5).all()
 
 
-# ---------------------------------------------------------------- fp16 widening
+# ---------------------------------------------------------------- fp16 widening and rounding
 def test_f16_widening_exhaustive():
+    # every one of the 65536 codes against numpy's float16 -> float32 (exact by definition):
+    # finite values and infinities bit for bit, NaN codes as NaN
     h = np.arange(65536, dtype=np.uint32).astype(np.uint16)
     ref = h.view(np.float16).astype(np.float32)
-    got = np.array([orc.f16_to_f32(int(v)) for v in h[::97]], np.float32)
-    r = ref[::97]
-    fin = np.isfinite(r)
-    assert np.array_equal(got[fin], r[fin])
-    assert np.array_equal(np.isnan(got), np.isnan(r))
+    got = orc.f16_to_f32_array(h)
+    nan = np.isnan(ref)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), ref[~nan].view(np.uint32))
+    # the scalar entry point agrees with the array one
+    for v in range(0, 65536, 251):
+        g = orc.f16_to_f32(v)
+        assert g == got[v] or (np.isnan(g) and np.isnan(got[v]))
+
+
+def test_f32_to_f16_matches_numpy():
+    # The fp16 KV cache's rounding (round to nearest, ties to even) against numpy's float16
+    # conversion, an independent implementation of IEEE 754 binary16 rounding.  Every f32 bit
+    # pattern whose exponent lies in [2^-26, 2^16] -- both signs, all 2^23 mantissas of each
+    # exponent -- which holds every rounding boundary that matters: the subnormal range and its
+    # edge at 2^-25 (half the smallest subnormal), the ties between subnormals, the normal/
+    # subnormal switch at 2^-14, ties to even across every binade, and overflow to infinity at
+    # 65520 (the tie between 65504 and 2^16).  Below that range everything rounds to signed
+    # zero and above it to infinity (random samples of both), plus infinities and NaN.
+    mant = np.arange(1 << 23, dtype=np.uint32)
+    for e in range(127 - 26, 127 + 16 + 1):
+        for sign in (0, 1):
+            bits = (np.uint32(sign << 31) | np.uint32(e << 23) | mant).view(np.float32)
+            got = orc.f32_to_f16_array(bits)
+            ref = bits.astype(np.float16).view(np.uint16)
+            assert np.array_equal(got, ref), (e, sign, int(np.argmax(got != ref)))
+    rng = np.random.default_rng(0)
+    low = (rng.integers(0, 127 - 26, 100000).astype(np.uint32) << 23) | rng.integers(0, 1 << 23, 100000).astype(np.uint32)
+    high = (rng.integers(127 + 17, 255, 100000).astype(np.uint32) << 23) | rng.integers(0, 1 << 23, 100000).astype(np.uint32)
+    for bits in (low, high, low | np.uint32(1 << 31), high | np.uint32(1 << 31)):
+        x = bits.view(np.float32)
+        assert np.array_equal(orc.f32_to_f16_array(x), x.astype(np.float16).view(np.uint16))
+    special = np.array([np.inf, -np.inf, 0.0, -0.0, 65504.0, 65519.996, 65520.0, 2.0 ** -24, 2.0 ** -25,
+                        2.0 ** -25 * (1 + 2.0 ** -23), 2.0 ** -26], np.float32)
+    assert np.array_equal(orc.f32_to_f16_array(special), special.astype(np.float16).view(np.uint16))
+    nan = orc.f32_to_f16_array(np.array([np.nan, -np.nan], np.float32)).view(np.float16)
+    assert np.isnan(nan).all()
