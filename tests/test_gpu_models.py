@@ -223,16 +223,17 @@ def test_9b_compat_block_step_matches_decode_steps(a9):
 @pytest.mark.timeout(900)
 def test_9b_break_in_block_and_decode_steps(a9):
     """forwardDecode's non-finite break (src/chpe_engine.zig:1753-1764) in the block step (per
-    token) and in the decode step: layer 1's down projection with its first group scale set to
-    +inf (row 0, columns 0..127) makes hidden[0] infinite after layer 1 at every position, so the
-    reference leaves the layer loop there; its hidden norm is +inf, its logits NaN (argmax 0,
-    all_finite false), and layers 2-31 write no KV rows.  Without the break (the oracle's
-    set_break(False), a planted deviation) the hidden norm turns NaN."""
+    token) and in the decode step: layer 1's down projection with one outlier weight set to +inf
+    (outliers replace weights, :632-646) makes a hidden row infinite after layer 1 at every
+    position, so the reference leaves the layer loop there; its hidden norm is +inf, its logits
+    NaN (argmax 0, all_finite false), and layers 2-31 write no KV rows.  Without the break (the
+    oracle's set_break(False), a planted deviation) the hidden norm turns NaN."""
     import tempfile
+    from test_gpu_nonfinite import inf_outlier_edit
     li = orc.layer_info(2, 1)
-    off = 4096 + li["down_proj"] * 17408 + 64 + 16384 + 48
+    off, b = inf_outlier_edit(a9, li["down_proj"], li["down_tiles"])
     data = np.fromfile(a9, dtype=np.uint8)
-    data[off:off + 2] = np.frombuffer(np.uint16(0x7c00).tobytes(), np.uint8)
+    data[off:off + 2] = np.frombuffer(b, np.uint8)
     fd, path = tempfile.mkstemp(suffix=".chpe", prefix="qwen3.5-9b-mod-", dir=os.path.dirname(str(a9)))
     os.close(fd)
     data.tofile(path)

@@ -13,9 +13,12 @@
    leaves the layer loop when the hidden state's sum of squares is not finite (tested after
    layers 0-2 and 8-16, and after any layer whose hidden[0] is not finite); the final norm and
    the LM head then see the hidden state of the break, and the later layers write no KV rows.
-   * Infinite weight: one f16 group scale of layer 1's down projection set to +inf makes
-     hidden[0] infinite at every step.  With the break, the hidden state keeps that infinity and
-     hidden_norm is +inf; without it the next layer's norm turns it into NaN everywhere.
+   * Infinite weight: one outlier weight of layer 1's down projection set to +inf (flat-tile
+     outliers replace the dequantised weight, :632-646) makes one hidden row infinite at every
+     step.  With the break, the hidden state keeps that infinity and hidden_norm is +inf;
+     without it the next layer's norm turns it into NaN everywhere.  (An infinite group scale
+     would not do: the reference multiplies every code value by it, and a zero code gives
+     0 * inf = NaN, where the GPU scales the group's integer sum and gets +-inf.)
    * Overflow without a non-finite element: one token's bf16 embedding row set to 1e20 (a
      bf16 archive) gives a finite hidden state whose sum of squares overflows, so the step
      breaks after layer 0; its logits are 0 and layers 1-35 keep zero KV rows at its position,
@@ -137,6 +140,25 @@ def _modified_copy(src, edits):
     return path, data
 
 
+def inf_outlier_edit(path, rec0, n_tiles):
+    """(file offset, bytes) that set one outlier weight of the first flat tile from record rec0
+    on that has outliers to +inf: an entry whose offset no later entry overrides."""
+    P = 64 + 16384
+    with open(path, "rb") as f:
+        for t in range(n_tiles):
+            base = 4096 + (rec0 + t) * 17408
+            f.seek(base + P + 560)
+            pay = f.read(272)
+            n = int(np.frombuffer(pay[:2], np.uint16)[0])
+            if not 0 < n <= 64:
+                continue
+            offs = np.frombuffer(pay[130:130 + 2 * n], np.uint16)
+            for m in range(n - 1, -1, -1):
+                if offs[m] not in offs[m + 1:]:
+                    return base + P + 562 + 2 * m, np.uint16(0x7c00).tobytes()
+    raise AssertionError("no flat tile with outliers")
+
+
 def _step_result(e, tok, pos):
     am, lg = e.decode_step(tok, pos)
     return am, lg, e.last()
@@ -166,12 +188,10 @@ def _same_result(am, lg, last, r, ol, tag, apart=()):
 
 
 def test_break_on_infinite_weight(w4_archive):
-    # layer 1's down projection: its first flat tile's group 0 (row 0, columns 0..127) scaled by
-    # +inf, so hidden[0] is infinite after layer 1 at every step
-    li = orc.layer_info(1, 1)  # map 1: the 3B cell map
-    rec = li["down_proj"]
-    off = 4096 + rec * 17408 + 64 + 16384 + 48
-    path, data = _modified_copy(w4_archive, [(off, np.uint16(0x7c00).tobytes())])
+    # layer 1's down projection: one outlier weight = +inf, so a hidden row is infinite after
+    # layer 1 at every step (map 1: the 3B cell map)
+    li = orc.layer_info(1, 1)
+    path, data = _modified_copy(w4_archive, [inf_outlier_edit(w4_archive, li["down_proj"], li["down_tiles"])])
     try:
         e = ca.Engine(path, arch=0, max_seq_len=16, kv_f16=False)
         o = orc.Oracle(data=data, arch=0, max_seq_len=16, threads=16)
