@@ -383,24 +383,27 @@ int chpe_debug_gemv_flat(int mode, uint32_t rows, uint32_t cols, const uint8_t* 
                          uint32_t* out_argmax, float* out_hidden_norm) {
   g_last_error.clear();
   const bool norm = mode == int(GemvMode::SwiGlu) || mode == int(GemvMode::Logits);
-  if (!tiles || !x || !y || rows == 0 || cols <= 2048 || mode < 0 || mode > int(GemvMode::Logits) ||
+  if (!tiles || !x || !y || rows == 0 || cols <= 2048 || n_tiles == 0 || mode < 0 || mode > int(GemvMode::Logits) ||
       norm != (gamma != nullptr) || (mode == int(GemvMode::SwiGlu)) != (tiles_up != nullptr))
     return -1;
-  const size_t need = (size_t(rows) * cols + kFlatWeights - 1) / kFlatWeights;
-  if (n_tiles < need) { g_last_error = "fewer tiles than the shape needs"; return -1; }
   const int n_parts = mode == int(GemvMode::SwiGlu) ? 2 : 1;
   const uint8_t* src[2] = {tiles, tiles_up};
-  WeightKind kind[2] = {WeightKind::FlatW4, WeightKind::FlatW4};
-  std::vector<float2> corr[2];
-  uint32_t kmax[2] = {0, 0};
-  for (int i = 0; i < n_parts; ++i)
-    if (!plan_flat_tiles(src[i], need * kCellBytes, kCellBytes, need, rows, cols, &kind[i], &corr[i], &kmax[i],
-                         &g_last_error))
-      return -1;
-  if (n_parts == 2 && kind[1] != kind[0]) { g_last_error = "gate and up tiles differ in width"; return -1; }
+  // the engine's plan: the uniform kernels, or tile by tile (FlatPoly) for any other tensor
+  FlatPlan fp[2];
+  for (int i = 0; i < n_parts; ++i) plan_flat(src[i], n_tiles * kCellBytes, kCellBytes, n_tiles, rows, cols, &fp[i]);
+  if (n_parts == 2 && fp[1].kind != fp[0].kind)  // (gate and up share a launch)
+    for (int i = 0; i < 2; ++i) {
+      fp[i].kind = WeightKind::FlatPoly;
+      fp[i].corr.clear();
+      fp[i].corr_kmax = 0;
+      fp[i].wrows = rows;
+    }
+  const WeightKind kind = fp[0].kind;
+  const bool poly = kind == WeightKind::FlatPoly;
+  const size_t used = std::max(fp[0].n_tiles, fp[n_parts - 1].n_tiles);
 
   constexpr size_t kShift = 64, kPad = size_t(1) << 20;  // as the engine's archive image
-  const size_t img = kShift + need * kCellBytes + kPad;
+  const size_t img = kShift + used * kCellBytes + kPad;
   std::vector<void*> mem;
   auto alloc = [&](size_t bytes) -> void* {
     void* d = nullptr;
@@ -415,7 +418,7 @@ int chpe_debug_gemv_flat(int mode, uint32_t rows, uint32_t cols, const uint8_t* 
   a.C = cols;
   a.eps = eps;
   uint32_t prow[kMaxParts] = {rows, rows, 0}, begin[kMaxParts] = {0, 0, 0};
-  const GemvLaunch g = gemv_geometry(kind[0], GemvMode(mode), cols, prow, n_parts, &a.n_units, &a.n_panels,
+  const GemvLaunch g = gemv_geometry(kind, GemvMode(mode), cols, prow, n_parts, &a.n_units, &a.n_panels,
                                      &a.waves_per_unit, begin);
   float* dx = static_cast<float*>(alloc(size_t(cols) * 4));
   float* dy = static_cast<float*>(alloc(size_t(rows) * 4));
@@ -426,18 +429,18 @@ int chpe_debug_gemv_flat(int mode, uint32_t rows, uint32_t cols, const uint8_t* 
   for (int i = 0; ok && i < n_parts; ++i) {
     uint8_t* d = static_cast<uint8_t*>(alloc(img));
     ok = d && hipMemset(d, 0, img) == hipSuccess &&
-         hipMemcpy(d + kShift, src[i], need * kCellBytes, hipMemcpyHostToDevice) == hipSuccess;
+         hipMemcpy(d + kShift, src[i], fp[i].n_tiles * kCellBytes, hipMemcpyHostToDevice) == hipSuccess;
     GemvPart& p = a.part[i];
     p.base = d + kShift;
     p.stride = uint32_t(kCellBytes);
     p.rows = rows;
-    p.wrows = rows;
+    p.wrows = fp[i].wrows;
     p.unit_begin = begin[i];
     p.y = dy;
-    p.corr_kmax = kmax[i];
-    if (ok && !corr[i].empty()) {
-      float2* dc = static_cast<float2*>(alloc(corr[i].size() * sizeof(float2)));
-      ok = dc && hipMemcpy(dc, corr[i].data(), corr[i].size() * sizeof(float2), hipMemcpyHostToDevice) == hipSuccess;
+    p.corr_kmax = fp[i].corr_kmax;
+    if (ok && !fp[i].corr.empty()) {
+      float2* dc = static_cast<float2*>(alloc(fp[i].corr.size() * sizeof(float2)));
+      ok = dc && hipMemcpy(dc, fp[i].corr.data(), fp[i].corr.size() * sizeof(float2), hipMemcpyHostToDevice) == hipSuccess;
       p.corr = dc;
     }
   }
@@ -445,28 +448,39 @@ int chpe_debug_gemv_flat(int mode, uint32_t rows, uint32_t cols, const uint8_t* 
   a.gamma = dg;
   StepResult* dres = nullptr;
   StepState* dst = nullptr;
+  const uint32_t n_partials = poly ? kPolyEpilogueBlocks : g.blocks;
   if (ok && mode == int(GemvMode::Logits)) {
-    a.partials = static_cast<ArgmaxPartial*>(alloc(size_t(g.blocks) * sizeof(ArgmaxPartial)));
+    a.partials = static_cast<ArgmaxPartial*>(alloc(size_t(n_partials) * sizeof(ArgmaxPartial)));
     dres = static_cast<StepResult*>(alloc(sizeof(StepResult)));
     dst = static_cast<StepState*>(alloc(sizeof(StepState)));
     a.result = dres;
     ok = a.partials && dres && dst && hipMemset(dst, 0, sizeof(StepState)) == hipSuccess;
   }
-  if (ok) {  // the permuted code copy where the engine builds one
-    const size_t xb = xm_layout_bytes(kind[0], a, g);
+  if (ok && !poly) {  // the permuted code copy where the engine builds one
+    const size_t xb = xm_layout_bytes(kind, a, g);
     if (xb) {
       uint8_t* dxc = static_cast<uint8_t*>(alloc(xb));
-      ok = dxc && build_xm_layout(kind[0], a, g, dxc, nullptr);
+      ok = dxc && build_xm_layout(kind, a, g, dxc, nullptr);
       a.part[0].xcodes = dxc;
     }
   }
+  if (ok && poly) {
+    float* xn = static_cast<float*>(alloc((size_t(cols) + 1) * 4));
+    float* part = static_cast<float*>(alloc(flat_poly_part_floats(uint32_t(used), cols) * 4));
+    PolyRaw raw{};
+    for (int i = 0; i < kMaxParts; ++i) raw.y[i] = i < n_parts ? static_cast<float*>(alloc(size_t(rows) * 4)) : nullptr;
+    ok = xn && part && raw.y[n_parts - 1];
+    const uint32_t nt[kMaxParts] = {fp[0].n_tiles, fp[n_parts - 1].n_tiles, 0};
+    if (ok) launch_gemv_flat_poly(a, nt, xn, raw, part, nullptr);
+  } else if (ok) {
+    launch_gemv(kind, a, g, nullptr);
+  }
   if (ok) {
-    launch_gemv(kind[0], a, g, nullptr);
     if (mode == int(GemvMode::Logits)) {
       FinishArgs f{};
       f.state = dst;
       f.partials = a.partials;
-      f.n_partials = g.blocks;
+      f.n_partials = n_partials;
       f.logits = dy;
       f.result = dres;
       launch_finish(f, nullptr);

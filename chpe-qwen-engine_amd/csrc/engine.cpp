@@ -208,7 +208,17 @@ bool Engine::init(const uint8_t* b, size_t len, const EngineConfig& cfg, std::st
         !plan("up_proj", li.up_proj, li.up_tiles, I, D, D, I, false, -1, &L.up) ||
         !plan("down_proj", li.down_proj, li.down_tiles, D, I, I, D, true, -1, &L.down))
       return false;
-    if (L.gate.kind != L.up.kind) { *err = "gate/up weight layouts differ"; return false; }
+    if (L.gate.kind != L.up.kind) {  // one SwiGLU launch: flat tensors of two forms run tile by tile
+      auto flat = [](WeightKind k) { return k == WeightKind::FlatW4 || k == WeightKind::FlatW2 || k == WeightKind::FlatPoly; };
+      if (!flat(L.gate.kind) || !flat(L.up.kind)) { *err = "gate/up weight layouts differ"; return false; }
+      for (ProjPlan* q : {&L.gate, &L.up}) {
+        q->kind = WeightKind::FlatPoly;
+        q->corr = nullptr;
+        q->corr_kmax = 0;
+        q->wrows = 0;
+        if (!ensure_poly_buffers(q->poly.n_cells, q->cols)) { *err = "allocation"; return false; }
+      }
+    }
   }
   d_gamma_final_ = upload_vector(norm(final_norm_record(map_)));
   if (!plan_lm_head(err)) return false;
@@ -365,6 +375,30 @@ bool plan_flat_tiles(const uint8_t* cells, size_t len, size_t stride, size_t n_t
   return true;
 }
 
+void plan_flat(const uint8_t* cells, size_t len, size_t stride, size_t n_avail, size_t r_total, size_t c_total,
+               FlatPlan* out) {
+  const size_t need = (r_total * c_total + kFlatWeights - 1) / kFlatWeights;
+  const size_t use = std::min(n_avail, need);  // (tiles past the shape add nothing, :702)
+  const size_t covered = use * kFlatWeights;
+  const size_t wrows = use < need ? covered / c_total : r_total;
+  std::string why;
+  out->corr.clear();
+  out->n_tiles = uint32_t(use);
+  out->wrows = uint32_t(wrows);
+  out->corr_kmax = 0;
+  // the uniform kernels: whole rows of uniformly group-128 4- or 2-bit tiles (a short tensor:
+  // 4-bit only), at most kMaxCorrPerRow outliers per row
+  const bool whole_rows = use == need || covered % c_total == 0;
+  if (use > 0 && whole_rows &&
+      plan_flat_tiles(cells, len, stride, use, wrows, c_total, &out->kind, &out->corr, &out->corr_kmax, &why) &&
+      (wrows == r_total || out->kind == WeightKind::FlatW4))
+    return;
+  out->kind = WeightKind::FlatPoly;
+  out->corr.clear();
+  out->corr_kmax = 0;
+  out->wrows = uint32_t(r_total);
+}
+
 void walk_cells(const uint8_t* b, size_t len, size_t stride, size_t n_avail, size_t r_total, size_t c_total,
                 std::vector<uint32_t>* row_base, bool* uniform_w4, uint64_t* extent) {
   size_t rb = 0;
@@ -420,29 +454,20 @@ bool Engine::plan_projection(size_t tile_start, size_t num_tiles, size_t r_total
       // gemvLinear walks the available tiles only (:1423-1429): with fewer tiles than the shape
       // needs (the 9B map's v <- in_proj_a, one tile, :1119) the rows past them get no
       // weights (zero in a fresh output, untouched when accumulating)
-      size_t use = (r_total * c_total + kFlatWeights - 1) / kFlatWeights, wrows = r_total;
-      if (avail < use) {
-        const size_t covered = avail * kFlatWeights;
-        if (covered % c_total) {
-          *err = "flat tiles end inside a row (a partial row of a short tensor is not built)";
-          return false;
-        }
-        use = avail;
-        wrows = covered / c_total;
-      }
-      std::vector<float2> ent;
-      if (!plan_flat_tiles(b + cell(0), len - cell(0), stride_, use, wrows, c_total, &p->kind, &ent,
-                           &p->corr_kmax, err))
-        return false;
-      if (wrows < r_total && p->kind != WeightKind::FlatW4) {
-        *err = "a short tensor of 2-bit flat tiles is not built";
-        return false;
-      }
-      p->wrows = uint32_t(wrows);
-      if (!ent.empty()) {
-        p->corr = static_cast<float2*>(dev_alloc(ent.size() * sizeof(float2)));
+      FlatPlan fp;
+      plan_flat(b + cell(0), len - cell(0), stride_, avail, r_total, c_total, &fp);
+      p->kind = fp.kind;
+      p->wrows = fp.wrows;
+      p->corr_kmax = fp.corr_kmax;
+      if (!fp.corr.empty()) {
+        p->corr = static_cast<float2*>(dev_alloc(fp.corr.size() * sizeof(float2)));
         if (!p->corr) { *err = "allocation"; return false; }
-        (void)hipMemcpy(p->corr, ent.data(), ent.size() * sizeof(float2), hipMemcpyHostToDevice);
+        (void)hipMemcpy(p->corr, fp.corr.data(), fp.corr.size() * sizeof(float2), hipMemcpyHostToDevice);
+      }
+      p->poly.n_cells = fp.n_tiles;
+      if (fp.kind == WeightKind::FlatPoly && !ensure_poly_buffers(fp.n_tiles, uint32_t(c_total))) {
+        *err = "allocation";
+        return false;
       }
     } else {  // 16-row polymorphic cells: row bases are a prefix sum of dims.rows
       std::vector<uint32_t> rb;
@@ -462,13 +487,7 @@ bool Engine::plan_projection(size_t tile_start, size_t num_tiles, size_t r_total
         if (!d) { *err = "allocation"; return false; }
         (void)hipMemcpy(d, rb.data(), rb.size() * 4, hipMemcpyHostToDevice);
         p->poly.row_base = d;
-        if (!d_xn_) {
-          const size_t n = std::max({arch_.hidden_dim, arch_.intermediate_dim, arch_.vocab_size,
-                                     arch_.num_attn_heads * arch_.head_dim});
-          d_xn_ = static_cast<float*>(dev_alloc((std::max(arch_.hidden_dim, arch_.intermediate_dim) + 1) * 4));
-          for (int i = 0; i < kMaxParts; ++i) poly_raw_.y[i] = static_cast<float*>(dev_alloc(n * 4));
-          if (!d_xn_ || !poly_raw_.y[kMaxParts - 1]) { *err = "allocation"; return false; }
-        }
+        if (!ensure_poly_buffers(0, 0)) { *err = "allocation"; return false; }
       }
     }
   } else {
@@ -492,6 +511,23 @@ bool Engine::plan_projection(size_t tile_start, size_t num_tiles, size_t r_total
       if (!std::isfinite(bias[i])) bias[i] = 0.0f;
     }
     p->bias = upload_vector(bias);
+  }
+  return true;
+}
+
+bool Engine::ensure_poly_buffers(uint32_t flat_tiles, uint32_t C) {
+  if (!d_xn_) {
+    const size_t n = std::max({arch_.hidden_dim, arch_.intermediate_dim, arch_.vocab_size,
+                               arch_.num_attn_heads * arch_.head_dim});
+    d_xn_ = static_cast<float*>(dev_alloc((std::max(arch_.hidden_dim, arch_.intermediate_dim) + 1) * 4));
+    for (int i = 0; i < kMaxParts; ++i) poly_raw_.y[i] = static_cast<float*>(dev_alloc(n * 4));
+    if (!d_xn_ || !poly_raw_.y[kMaxParts - 1]) return false;
+  }
+  const size_t need = flat_tiles ? flat_poly_part_floats(flat_tiles, C) : 0;
+  if (need > flat_part_floats_) {  // the row-segment sums of the largest FlatPoly tensor
+    flat_part_ = static_cast<float*>(dev_alloc(need * 4));
+    if (!flat_part_) return false;
+    flat_part_floats_ = need;
   }
   return true;
 }
@@ -577,6 +613,11 @@ uint32_t Engine::enqueue_gemv(const ProjPlan* const* parts, float* const* outs, 
     const PolyPlan* pp[kMaxParts] = {};
     for (int i = 0; i < n; ++i) pp[i] = &parts[i]->poly;
     return launch_gemv_poly(a, pp, d_xn_, poly_raw_, st);
+  }
+  if (parts[0]->kind == WeightKind::FlatPoly) {
+    uint32_t nt[kMaxParts] = {0, 0, 0};
+    for (int i = 0; i < n; ++i) nt[i] = parts[i]->poly.n_cells;
+    return launch_gemv_flat_poly(a, nt, d_xn_, poly_raw_, flat_part_, st);
   }
   launch_gemv(parts[0]->kind, a, g, st);
   return g.blocks;
@@ -1151,6 +1192,7 @@ double Engine::proj_bytes(const ProjPlan& p) const {
     case WeightKind::FlatW4: bytes = n / 2 + n / 128 * 2 + std::ceil(n / kFlatWeights) * (2 + 64 * 4); break;
     case WeightKind::FlatW2: bytes = n / 4 + n / 128 * 2 + std::ceil(n / kFlatWeights) * (2 + 64 * 4); break;
     case WeightKind::Cell16Poly: bytes = double(p.poly.n_cells) * kTileCodeBytes; break;  // the code areas
+    case WeightKind::FlatPoly: bytes = double(p.poly.n_cells) * kTileCodeBytes; break;    // (at most)
   }
   if (p.bias) bytes += 4.0 * p.rows;
   return bytes;

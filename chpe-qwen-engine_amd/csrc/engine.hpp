@@ -63,7 +63,7 @@ struct ProjPlan {
                                        //   launches of the mode and part count it was built for
   GemvMode xcodes_mode = GemvMode::Store;
   int xcodes_parts = 0;
-  PolyPlan poly{};                     // Cell16Poly: the cells' row bases
+  PolyPlan poly{};                     // Cell16Poly: the cells' row bases; FlatPoly: n_cells = the tiles
 };
 
 // The cells of a 16-row-cell tensor (c_total <= 2048) as gemvLinear walks them (:1430-1442):
@@ -82,6 +82,19 @@ void walk_cells(const uint8_t* cells, size_t len, size_t stride, size_t n_avail,
 bool plan_flat_tiles(const uint8_t* cells, size_t len, size_t stride, size_t n_tiles, size_t r_total,
                      size_t c_total, WeightKind* kind, std::vector<float2>* corr, uint32_t* corr_kmax,
                      std::string* err);
+
+// How a flat-tile tensor of r_total x c_total weights over n_avail available tiles runs: on the
+// uniform kernels (kind FlatW4 / FlatW2, wrows rows covered, the correction table) when the
+// tiles are uniformly group-128 4- or 2-bit, cover whole rows (a short tensor: 4-bit only) and
+// keep to kMaxCorrPerRow outliers per row; otherwise kind FlatPoly over n_tiles tiles (any tile
+// form gemvCellFlat decodes, partial rows).
+struct FlatPlan {
+  WeightKind kind = WeightKind::FlatPoly;
+  uint32_t n_tiles = 0, wrows = 0, corr_kmax = 0;
+  std::vector<float2> corr;
+};
+void plan_flat(const uint8_t* cells, size_t len, size_t stride, size_t n_avail, size_t r_total, size_t c_total,
+               FlatPlan* out);
 
 struct LayerPlan {
   ProjPlan q, k, v, o, gate, up, down;
@@ -156,6 +169,9 @@ class Engine {
                        size_t x_len, size_t y_len, bool accumulate, int64_t bias_tile,
                        ProjPlan* out, std::string* err);
   bool plan_lm_head(std::string* err);
+  // the polymorphic paths' buffers (normalised input, raw row sums), and the FlatPoly row-segment
+  // sums for a tensor of flat_tiles tiles of C columns
+  bool ensure_poly_buffers(uint32_t flat_tiles, uint32_t C);
   float* upload_vector(const std::vector<float>& v);
   void* dev_alloc(size_t bytes);
   void record_step(hipStream_t st);
@@ -230,6 +246,8 @@ class Engine {
   float* d_rope_cur_ = nullptr;      // the step's cos / sin rows (head_dim floats)
   float* d_xn_ = nullptr;            // polymorphic cells: the RMSNorm'ed input
   PolyRaw poly_raw_{};               // polymorphic cells: raw row sums per part
+  float* flat_part_ = nullptr;       // FlatPoly: row-segment sums per tile
+  size_t flat_part_floats_ = 0;
 
   // the block step (plan_block): m <= kMaxBlock tokens' activations, operand tables, partials
   bool block_ok_ = false;

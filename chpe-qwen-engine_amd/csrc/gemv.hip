@@ -2671,6 +2671,79 @@ __global__ void __launch_bounds__(256) k_gemv_poly(const uint8_t* base, uint32_t
   }
 }
 
+// ---- flat tiles of any form gemvCellFlat decodes (src/chpe_engine.zig:584-729) ---------------
+// Tensors the uniform flat kernels do not take -- tiles without GROUP128 (each weight
+// value * dims.scale + dims.bias), widths other than 2 and 4 bits (all weights zero), a mix of
+// forms, tiles that end inside a row of a short tensor, rows whose width is not a multiple of
+// 128, more outliers per row than the correction table holds -- run here.  One workgroup per
+// tile materialises its 32768 weights in LDS as the reference does (the product and the sum
+// rounded separately, outliers replacing in entry order), then dots each row segment of the tile
+// with x into part[tile][segment]; k_flat_poly_rows adds each row's segments in tile order.
+constexpr uint32_t kFlatPolyThreads = 512;
+__host__ __device__ constexpr uint32_t flat_poly_segments(uint32_t C) { return 32768u / C + 2u; }
+
+__global__ void __launch_bounds__(kFlatPolyThreads) k_flat_poly(const uint8_t* base, uint32_t stride, uint32_t R,
+                                                                uint32_t C, const float* x, float* part) {
+#pragma clang fp contract(off)
+  extern __shared__ __align__(16) float s_w[];  // the tile's 32768 weights
+  const uint32_t t = blockIdx.x, tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+  const uint8_t* cell = base + size_t(t) * stride;
+  const uint8_t* codes = cell + 64;
+  const uint8_t* pl = cell + 16448;
+  const uint32_t qb = pl[20];
+  const bool g128 = (*reinterpret_cast<const uint32_t*>(pl + 24) & 1u) != 0;
+  const float scale = *reinterpret_cast<const float*>(pl + 32), bias = *reinterpret_cast<const float*>(pl + 36);
+  const uint16_t* gs = reinterpret_cast<const uint16_t*>(pl + 48);
+  for (uint32_t k = tid; k < 32768u; k += blockDim.x) {
+    float w = 0.0f;  // (other widths: zero, :694-696)
+    if (qb == 4 || qb == 2) {
+      const float q = qb == 4 ? float((codes[k / 2] >> (4 * (k & 1))) & 15u) - 8.0f
+                              : poly_w2((codes[k / 4] >> (2 * (k & 3))) & 3u);
+      w = g128 ? q * h2f(gs[k / 128]) : q * scale + bias;  // :607-630, :654-677
+    }
+    s_w[k] = w;
+  }
+  __syncthreads();
+  if (tid == 0 && (qb == 4 || qb == 2)) {  // outliers replace, in entry order (:632-646, :680-693)
+    const uint32_t n = *reinterpret_cast<const uint16_t*>(pl + 560);
+    if (n > 0 && n <= 64)
+      for (uint32_t m = 0; m < n; ++m) {
+        const uint32_t off = *reinterpret_cast<const uint16_t*>(pl + 690 + 2 * m);
+        if (off < 32768u) s_w[off] = h2f(*reinterpret_cast<const uint16_t*>(pl + 562 + 2 * m));
+      }
+  }
+  __syncthreads();
+  // the segments (:698-727): row r_first + s of the tile, wave w takes segments w, w + 8, ..
+  const uint64_t f0 = uint64_t(t) * 32768u;
+  const uint64_t r_first = f0 / C;
+  if (r_first >= R) return;
+  const uint64_t r_last = min(uint64_t(R) - 1, (f0 + 32767u) / C);
+  const uint32_t n_seg = uint32_t(r_last - r_first + 1), ps = flat_poly_segments(C);
+  for (uint32_t sg = wave; sg < n_seg; sg += blockDim.x / 64) {
+    const uint64_t r = r_first + sg, rs = r * C;
+    const uint32_t j0 = uint32_t((rs > f0 ? rs : f0) - f0), j1 = uint32_t(min(f0 + 32768u, rs + C) - f0);
+    const float* xs = x + (f0 + j0 - rs);
+    float acc = 0.0f;
+    for (uint32_t j = j0 + lane; j < j1; j += 64) acc = fmaf(s_w[j], xs[j - j0], acc);
+#pragma unroll
+    for (int m = 1; m < 64; m <<= 1) acc = pair_sum(acc, m);
+    if (lane == 0) part[size_t(t) * ps + sg] = acc;
+  }
+}
+
+// raw[r] = the row's segments in tile order (y[r] += dot, :719); rows past the tiles: 0
+__global__ void __launch_bounds__(256) k_flat_poly_rows(const float* part, uint32_t n_tiles, uint32_t R, uint32_t C,
+                                                        float* raw) {
+#pragma clang fp contract(off)
+  const uint32_t ps = flat_poly_segments(C);
+  for (uint32_t r = blockIdx.x * blockDim.x + threadIdx.x; r < R; r += gridDim.x * blockDim.x) {
+    const uint64_t a = uint64_t(r) * C, b = a + C - 1;
+    float v = 0.0f;
+    for (uint64_t t = a / 32768u; t <= b / 32768u && t < n_tiles; ++t) v += part[t * ps + (r - (t * 32768u) / C)];
+    raw[r] = v;
+  }
+}
+
 // the mode's epilogue on the raw row sums: grid-stride over rows (QkvRope: over RoPE pairs);
 // ss: the normalised input's sum of squares (k_rmsnorm), or null
 template <int MODE>
@@ -2866,6 +2939,7 @@ GemvLaunch gemv_geometry(WeightKind kind, GemvMode mode, uint32_t C, const uint3
     case WeightKind::Raw16: panel_cols = Raw16::kPanelCols; ppw = Raw16::kPPW; break;
     case WeightKind::Raw8: panel_cols = Raw8::kPanelCols; ppw = Raw8::kPPW; break;
     case WeightKind::Cell16Poly: break;  // launched by launch_gemv_poly
+    case WeightKind::FlatPoly: break;    // launched by launch_gemv_flat_poly
   }
   *n_panels = (C + panel_cols - 1) / panel_cols;
   uint32_t nw = (*n_panels + ppw - 1) / ppw;
@@ -2941,6 +3015,36 @@ GemvLaunch gemv_geometry(WeightKind kind, GemvMode mode, uint32_t C, const uint3
   return g;
 }
 
+size_t flat_poly_part_floats(uint32_t n_tiles, uint32_t C) { return size_t(n_tiles) * flat_poly_segments(C); }
+
+uint32_t launch_gemv_flat_poly(const GemvArgs& a, const uint32_t* n_tiles, float* xn, const PolyRaw& raw,
+                               float* part, hipStream_t st) {
+  const float* x = a.x;
+  const float* ss = nullptr;
+  if (a.gamma) {
+    StepResult* res = GemvMode(a.mode) == GemvMode::Logits ? a.result : nullptr;
+    launch_kernel(&k_rmsnorm, dim3(1), dim3(1024), st, a.x, a.gamma, a.eps, a.C, xn, res);
+    x = xn;
+    ss = xn + a.C;
+  }
+  for (int p = 0; p < a.n_parts; ++p) {
+    if (n_tiles[p])
+      launch_kernel_lds(&k_flat_poly, dim3(n_tiles[p]), dim3(kFlatPolyThreads), size_t(32768) * 4, st, a.part[p].base,
+                        a.part[p].stride, a.part[p].rows, a.C, x, part);
+    launch_kernel(&k_flat_poly_rows, dim3((a.part[p].rows + 255) / 256), dim3(256), st, part, n_tiles[p],
+                  a.part[p].rows, a.C, raw.y[p]);
+  }
+  const uint32_t blocks = kPolyEpilogueBlocks;
+  switch (GemvMode(a.mode)) {
+    case GemvMode::Store: launch_kernel(&k_poly_epilogue<int(GemvMode::Store)>, dim3(blocks), dim3(256), st, a, raw, ss); break;
+    case GemvMode::Accum: launch_kernel(&k_poly_epilogue<int(GemvMode::Accum)>, dim3(blocks), dim3(256), st, a, raw, ss); break;
+    case GemvMode::SwiGlu: launch_kernel(&k_poly_epilogue<int(GemvMode::SwiGlu)>, dim3(blocks), dim3(256), st, a, raw, ss); break;
+    case GemvMode::Logits: launch_kernel(&k_poly_epilogue<int(GemvMode::Logits)>, dim3(blocks), dim3(256), st, a, raw, ss); break;
+    case GemvMode::QkvRope: launch_kernel(&k_poly_epilogue<int(GemvMode::QkvRope)>, dim3(blocks), dim3(256), st, a, raw, ss); break;
+  }
+  return blocks;
+}
+
 uint32_t launch_gemv_poly(const GemvArgs& a, const PolyPlan* const* plans, float* xn, const PolyRaw& raw,
                           hipStream_t st) {
   const float* x = a.x;
@@ -3005,7 +3109,8 @@ void launch_gemv(WeightKind kind, const GemvArgs& a, const GemvLaunch& g, hipStr
     case WeightKind::Raw16: launch_layout<Raw16>(a, g, st); break;
     case WeightKind::Raw8: launch_layout<Raw8>(a, g, st); break;
     case WeightKind::Cell16Poly:
-      std::fprintf(stderr, "chpe: polymorphic cells go through launch_gemv_poly\n");
+    case WeightKind::FlatPoly:
+      std::fprintf(stderr, "chpe: polymorphic cells and tiles go through launch_gemv_poly / launch_gemv_flat_poly\n");
       break;
   }
 }

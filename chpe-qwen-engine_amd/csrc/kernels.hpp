@@ -27,6 +27,7 @@ enum class WeightKind : int {
   FlatW2 = 3,    // flat tiles, 2-bit, GROUP128
   Cell16Poly = 4,  // 16-row polymorphic cells of any width (gemvTilePolymorphic), per-cell metadata
   Raw8 = 5,        // raw int8 tiles as one row-major matrix, times 0.00373708 (dotSegment :1219-1237)
+  FlatPoly = 6,    // flat tiles of any form gemvCellFlat decodes, tile by tile (launch_gemv_flat_poly)
 };
 
 enum class GemvMode : int {
@@ -248,6 +249,15 @@ constexpr uint32_t kPolyEpilogueBlocks = 64;
 // number of argmax partials.
 uint32_t launch_gemv_poly(const GemvArgs& a, const PolyPlan* const* plans, float* xn, const PolyRaw& raw,
                           hipStream_t stream);
+
+// Flat tiles of any form (WeightKind::FlatPoly): part p walks n_tiles[p] tiles from its base
+// (gemvLinear's available tiles, :1423-1429) over a.part[p].rows x a.C weights; the input
+// RMSNorm'ed into xn (C + 1 floats) when a.gamma is set; `part` holds
+// flat_poly_part_floats(max n_tiles, C) floats of row-segment sums; then the raw row sums of
+// every part and the mode's epilogue as launch_gemv_poly.  Returns the argmax partials' count.
+size_t flat_poly_part_floats(uint32_t n_tiles, uint32_t C);
+uint32_t launch_gemv_flat_poly(const GemvArgs& a, const uint32_t* n_tiles, float* xn, const PolyRaw& raw,
+                               float* part, hipStream_t stream);
 
 // ---- the block step: m <= kMaxBlock tokens at consecutive positions through flat 4-bit tiles,
 // every weight read once for all m tokens (batch-M verify, chunked prefill) ----------------------

@@ -122,8 +122,10 @@ int chpe_debug_gemv(void *ctx, size_t layer, int which, const float *x, float *y
 int chpe_debug_flat_tile_weights(const uint8_t *cell, float *out32768);
 /* One flat-tile GEMV (gemvCellFlat, src/chpe_engine.zig:584-729, as gemvLinear drives it for
  * tensors wider than 2048 columns, :1396-1489) through the decode step's kernels, on a rows x
- * cols tensor given as n_tiles consecutive 17408-byte cells (group-128 4- or 2-bit; outliers
- * replace weights).  mode 0: y = W x; 1: y += W x; 2: y = silu(W rmsnorm(x)) * (U rmsnorm(x))
+ * cols tensor given as n_tiles consecutive 17408-byte cells, planned as the engine plans a
+ * tensor: uniformly group-128 4- or 2-bit tiles on the uniform kernels, any other tile form,
+ * a mix of forms or fewer tiles than the shape needs (a short tensor) tile by tile; outliers
+ * replace weights.  mode 0: y = W x; 1: y += W x; 2: y = silu(W rmsnorm(x)) * (U rmsnorm(x))
  * with U in tiles_up; 3: y = W rmsnorm(x) (the LM head's logits) with *out_argmax (first index
  * of the maximum) and *out_hidden_norm = |x| (both optional).  rmsnorm uses gamma and eps;
  * gamma is given exactly in modes 2 and 3.  Returns 0, -1 on bad arguments or tiles

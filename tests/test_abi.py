@@ -80,8 +80,10 @@ def test_init_rejects_missing_and_malformed_archives(tmp_path):
     assert L.chpe_last_error() == b"unknown architecture"
 
 
-def test_flat_gemv_hook_rejects_bad_tiles_before_the_device():
-    """chpe_debug_gemv_flat checks its arguments and plans the tiles on the host first."""
+def test_flat_gemv_hook_rejects_bad_arguments_before_the_device():
+    """chpe_debug_gemv_flat checks its arguments on the host first.  (Tiles of any form, a mix of
+    forms, fewer tiles than the shape needs and widths that are not a multiple of 128 are legal:
+    the engine runs them tile by tile, tests/test_gpu_flat_poly.py.)"""
     w = (np.random.default_rng(1).standard_normal(32768) * 0.02).astype(np.float32)
     cells = np.stack([ca.pack_flat(w, bits=4), ca.pack_flat(w, bits=4)])
     x, g = np.ones(4096, np.float32), np.ones(4096, np.float32)
@@ -89,18 +91,10 @@ def test_flat_gemv_hook_rejects_bad_tiles_before_the_device():
         dict(mode="swiglu", rows=16, cols=4096, tiles=cells, x=x, gamma=g),       # no up tiles
         dict(mode="store", rows=16, cols=4096, tiles=cells, x=x, gamma=g),        # gamma outside 2/3
         dict(mode="logits", rows=16, cols=4096, tiles=cells, x=x),                # no gamma
-        dict(mode="store", rows=17, cols=4096, tiles=cells, x=x),                 # more rows than tiles
         dict(mode="store", rows=16, cols=2048, tiles=cells, x=x),                 # not a flat width
-        dict(mode="store", rows=8, cols=4160, tiles=cells, x=x),                  # width % 128
+        dict(mode="store", rows=0, cols=4096, tiles=cells, x=x),                  # no rows
+        dict(mode="store", rows=16, cols=4096, tiles=cells[:0], x=x),             # no tiles
     ]
     for kw in bad:
         with pytest.raises(ca.EngineError):
             ca.gpu_gemv_flat(**kw)
-    mixed = cells.copy()
-    mixed[1] = ca.pack_flat(w, bits=2)
-    with pytest.raises(ca.EngineError, match="uniformly"):
-        ca.gpu_gemv_flat("store", 16, 4096, mixed, x)
-    three = cells.copy()
-    three[0, 16448 + 20] = 3
-    with pytest.raises(ca.EngineError):
-        ca.gpu_gemv_flat("store", 16, 4096, three, x)

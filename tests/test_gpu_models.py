@@ -95,14 +95,16 @@ def run_model(path, arch, vocab, n_prompt, n_gen, seed):
             assert e.last()["hidden_norm"] == pytest.approx(r.hidden_norm, rel=1e-4)
             steps.append((lg.astype(np.float64), ol.astype(np.float64)))
         # the steps' dependence on their input: the change of the logits from one teacher-forced
-        # token to the next is the oracle's within the two steps' bars, and it is large against
-        # them -- a step that ignored its token (or the context) fails this even where the
-        # argmax does not move (the 2-bit model's greedy stream repeats one token)
+        # token to the next is at least 20 times the two steps' measured deviations from the
+        # oracle, so the comparisons above resolve it -- a step that ignored its token (or the
+        # context) would deviate by that change.  This holds where the argmax does not move:
+        # the 2-bit model's greedy stream repeats one token (its logits change by ~4e-3 between
+        # positions against deviations of ~7e-6)
         (g0, o0), (g1, o1) = steps
-        bar = 2 * 2e-4 * float(max(np.abs(o0).max(), np.abs(o1).max()))
+        err = float(np.abs(g0 - o0).max() + np.abs(g1 - o1).max())
         dd, dref = float(np.abs((g1 - g0) - (o1 - o0)).max()), float(np.abs(o1 - o0).max())
-        say(f"  logit change pos 0 -> 1: max {dref:.4f}, gpu vs oracle {dd:.2e} (bar {bar:.2e})")
-        assert dd <= bar and dref >= 20 * bar
+        say(f"  logit change pos 0 -> 1: max {dref:.4g}, gpu vs oracle {dd:.2e}, step deviations {err:.2e}")
+        assert dd <= err + 1e-12 and dref >= 20 * err
         say(f"stream (f32 KV): {n_prompt} prompt + {n_gen} generated")
         g = e.generate(prompt, n_gen)
         ref, gaps = o.generate(prompt, n_gen)
