@@ -168,6 +168,30 @@ def gemv_probe(workload):
     print(json.dumps({"gemv_probe": workload, "rows": I, "cols": D, "bits": bits, "launches": 4}), flush=True)
 
 
+def stage_probe(workload, iters):
+    """The decode step's launches of stages 0 (q/k/v), 1 (o) and 3 (down) alone, `iters` times
+    each on layers 0 and 1 of the workload's engine (chpe_time_stage, no context built), then the
+    attention kernels (stages 5 and 6) once at the workload's prompt length on synthetic fp16 rows
+    (chpe_debug_attention): the rocprofv3 --pmc traffic runs of the stages other than gate/up."""
+    import chpe_amd as ca
+    w = WORKLOADS[workload]
+    archive = ca.ensure_archive(w["kind"], seed=0)
+    e = ca.Engine(archive, arch=w["arch"], max_seq_len=64, kv_f16=True)
+    try:
+        for st in (0, 1, 3):
+            e.time_stage(st, 0, 2, iters)
+            log(f"stage {st}: {2 * iters} launches")
+    finally:
+        e.close()
+    P = w["prompt"]
+    rng = np.random.default_rng(0)
+    q = rng.standard_normal(w["H"] * w["hd"]).astype(np.float32)
+    k = rng.standard_normal((P + 1, w["KV"] * w["hd"])).astype(np.float32)
+    ca.gpu_attention(q, k, k, P, w["H"], w["KV"], w["hd"], 1)
+    print(json.dumps({"stage_probe": workload, "stages": [0, 1, 3], "launches_each": 2 * iters,
+                      "attention_position": P}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -181,6 +205,9 @@ def main():
     ap.add_argument("--copy-probe", action="store_true",
                     help="only copy 256 MiB device-to-device 4 times (calibrates rocprofv3 FETCH_SIZE / "
                          "WRITE_SIZE against known bytes)")
+    ap.add_argument("--stage-probe", action="store_true",
+                    help="only the q/k/v, o and down launches of layers 0-1 and one attention launch at the "
+                         "prompt length (the rocprofv3 --pmc traffic runs of the other stages)")
     ap.add_argument("--gemv-probe", action="store_true",
                     help="only the workload's gate/up GEMV on synthetic tiles of its shape, 4 launches "
                          "(the rocprofv3 --pmc traffic runs of the dominant kernel)")
@@ -190,6 +217,9 @@ def main():
         return
     if args.gemv_probe:
         gemv_probe(args.workload)
+        return
+    if args.stage_probe:
+        stage_probe(args.workload, 2)
         return
     if args.gpus != 1:
         print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported (the decode path runs "

@@ -728,6 +728,8 @@ struct oref_engine {
     size_t record_count, stride, wpt, max_seq_len;
     int kv_f16, threads;
     int no_break;  /* test only: skip forwardDecode's non-finite break (a planted deviation) */
+    int hybrid;    /* the true Qwen3.5-9B hybrid layers (oref_set_hybrid) */
+    float *conv_state, *rec_state, *hy_mix, *hy_conv, *hy_z, *hy_a, *hy_b, *hy_dn, *hy_qg;
     float *hidden, *norm_buf, *norm_gamma, *bias_buf, *q_buf, *k_buf, *v_buf, *attn_out, *gate_buf,
         *up_buf, *mlp_buf, *scores_buf, *logits_buf, *k_cache, *v_cache;
 };
@@ -868,6 +870,8 @@ void oref_close(oref_engine *e) {
     free(e->hidden); free(e->norm_buf); free(e->norm_gamma); free(e->bias_buf); free(e->q_buf);
     free(e->k_buf); free(e->v_buf); free(e->attn_out); free(e->gate_buf); free(e->up_buf);
     free(e->mlp_buf); free(e->scores_buf); free(e->logits_buf); free(e->k_cache); free(e->v_cache);
+    free(e->conv_state); free(e->rec_state); free(e->hy_mix); free(e->hy_conv); free(e->hy_z);
+    free(e->hy_a); free(e->hy_b); free(e->hy_dn); free(e->hy_qg);
     if (e->owns_map) munmap((void *)e->bytes, e->map_len);
     free(e);
 }
@@ -1188,8 +1192,11 @@ int oref_forward_layers(oref_engine *e, uint32_t token, size_t pos, size_t n_lay
     return forward_layers(e, token, pos, n_layers < e->arch.num_layers ? n_layers : e->arch.num_layers, res);
 }
 
+static int forward_hybrid(oref_engine *e, uint32_t token, size_t pos, size_t n_layers, oref_result *res);
+
 static int forward_layers(oref_engine *e, uint32_t token, size_t pos, size_t n_layers, oref_result *res) {
     /* forwardDecode: chpe_engine.zig:1663-1803 */
+    if (e->hybrid) return forward_hybrid(e, token, pos, n_layers, res);
     if (pos >= e->max_seq_len) return -2; /* the reference reads past its KV cache here */
     uint64_t t0 = now_ns();
     set_threads(e);
@@ -1265,5 +1272,188 @@ int oref_generate(oref_engine *e, const uint32_t *prompt, size_t n_prompt, size_
         }
         if (i + 1 < n_gen && oref_forward(e, r.argmax_token, n_prompt + i, &r)) return -2;
     }
+    return 0;
+}
+
+/* ---------------------------------------------------------------- the Qwen3.5-9B hybrid
+ * The true model of the 9B archive (no reference code: README.md:17,62 only name it; the 9B
+ * tensor map names its tensors, qwen35_tensor_map.zig:7-50).  The layer loop keeps
+ * forwardDecode's structure (embedding, per layer norm -> token mixer -> residual -> norm ->
+ * SwiGLU MLP -> residual, the non-finite break, final norm, LM head, argmax: chpe_engine.zig:
+ * 1663-1803); the token mixers follow the library that defines the layer, transformers 5.15.0
+ * models/qwen3_5/modeling_qwen3_5.py:
+ *   layer l is full attention when l % 4 == 3 (configuration_qwen3_5.py:113-116), else a gated
+ *   DeltaNet layer;
+ *   full attention (Qwen3_5Attention :629-701): q_proj rows are per head 256 query values then
+ *   256 output-gate values (:672-675); RMSNorm of each query and key head (q_norm / k_norm
+ *   gains, :677-678); rotary embedding on the first 64 of 256 dims (partial_rotary_factor
+ *   0.25, configuration :111; rotate_half pairs (i, i + 32), :546-591) with the reference's
+ *   frequency formula (applyRope chpe_engine.zig:195-216 over rot = 64 dims); the KV cache and
+ *   attention of forwardDecode (:1693-1734); the output times sigmoid(gate) (:696); o_proj;
+ *   gated DeltaNet (Qwen3_5GatedDeltaNet :387-543): in_proj_qkv, in_proj_z, in_proj_a,
+ *   in_proj_b; the causal conv1d update + SiLU over the 8192 channels; q, k, v split 2048 /
+ *   2048 / 4096; the gated delta rule over 32 value heads (deltanet_oracle.c); the gated
+ *   RMSNorm with z; out_proj.
+ * Norm tiles hold the effective gain (a converter stores 1 + w for the checkpoints' zero-centred
+ * Qwen3_5RMSNorm weights, :720-737).  The recurrent states (conv [24][8192][3], delta rule
+ * [24][32][128][128]) start from zero at position 0. */
+static int q35_full(size_t l) { return l % 4 == 3; }
+
+typedef struct {
+    size_t input_norm, post_norm, gate_proj, up_proj, down_proj;
+    size_t q_proj, k_proj, v_proj, o_proj, q_norm, k_norm;
+    size_t in_proj_qkv, in_proj_z, in_proj_a, in_proj_b, conv1d, a_log, dt_bias, linear_norm, out_proj;
+} q35_records;
+
+static q35_records q35_records_of(size_t l) {
+    /* record offsets inside each layer of qwen35_tensor_map.zig:62-1015 */
+    q35_records r;
+    memset(&r, 0, sizeof r);
+    size_t b = 62080;
+    for (size_t i = 0; i < l; i++) b += q35_full(i) ? 12804 : 13337;
+    r.input_norm = b;
+    if (q35_full(l)) {
+        r.q_proj = b + 1; r.k_proj = b + 2049; r.v_proj = b + 2305; r.o_proj = b + 2561;
+        r.q_norm = b + 3585; r.k_norm = b + 3586; r.post_norm = b + 3587;
+    } else {
+        r.in_proj_qkv = b + 1; r.in_proj_z = b + 2049; r.in_proj_a = b + 3073; r.in_proj_b = b + 3081;
+        r.conv1d = b + 3089; r.a_log = b + 3093; r.dt_bias = b + 3094; r.linear_norm = b + 3095;
+        r.out_proj = b + 3096; r.post_norm = b + 4120;
+    }
+    r.gate_proj = r.post_norm + 1;
+    r.up_proj = r.gate_proj + 3072;
+    r.down_proj = r.up_proj + 3072;
+    return r;
+}
+
+/* n bf16 values from consecutive records' code areas (8192 per record) */
+static void q35_bf16_vector(const oref_engine *e, size_t rec, float *out, size_t n) {
+    for (size_t i = 0; i < n; i++) {
+        const size_t r = rec + i / 8192;
+        out[i] = r < e->record_count ? oref_bf16_to_f32(rd16(tile_coded_ptr(e, r) + 2 * (i % 8192))) : 0.0f;
+    }
+}
+
+/* rotate_half over the first `rot` of hd dims of each head, the reference's angle formula */
+static void rope_partial(float *vec, size_t pos, size_t nh, size_t hd, size_t rot, float theta) {
+    float pos_f = (float)pos;
+    for (size_t h = 0; h < nh; h++) {
+        size_t base = h * hd;
+        for (size_t i = 0; i < rot / 2; i++) {
+            float freq = 1.0f / powf(theta, 2.0f * (float)i / (float)rot);
+            float ang = pos_f * freq;
+            float c = cosf(ang), s = sinf(ang);
+            float x0 = vec[base + i], x1 = vec[base + i + rot / 2];
+            vec[base + i] = x0 * c - x1 * s;
+            vec[base + i + rot / 2] = x0 * s + x1 * c;
+        }
+    }
+}
+
+int oref_set_hybrid(oref_engine *e, int on) {
+    if (!on) { e->hybrid = 0; return 0; }
+    if (e->map != 2 || e->is_raw) return -1;  /* the 9B cell archive only */
+    const size_t n_lin = 24;
+    if (!e->conv_state) {
+        e->conv_state = calloc(n_lin * 8192 * 3, 4);
+        e->rec_state = calloc(n_lin * 32 * 128 * 128, 4);
+        e->hy_mix = calloc(8192, 4); e->hy_conv = calloc(8192, 4); e->hy_z = calloc(4096, 4);
+        e->hy_a = calloc(32, 4); e->hy_b = calloc(32, 4); e->hy_dn = calloc(4096, 4); e->hy_qg = calloc(8192, 4);
+        if (!e->conv_state || !e->rec_state || !e->hy_qg) return -1;
+    }
+    e->hybrid = 1;
+    return 0;
+}
+
+static int forward_hybrid(oref_engine *e, uint32_t token, size_t pos, size_t n_layers, oref_result *res) {
+    if (pos >= e->max_seq_len) return -2;
+    uint64_t t0 = now_ns();
+    set_threads(e);
+    const oref_arch *a = &e->arch;
+    const size_t D = a->hidden_dim, I = a->intermediate_dim, H = 16, KV = 4, hd = 256, kvd = KV * hd;
+    if (pos == 0) {
+        memset(e->conv_state, 0, 24 * 8192 * 3 * 4);
+        memset(e->rec_state, 0, 24 * 32 * 128 * 128 * 4);
+    }
+    float gq[256], gk[256], conv_w[8192 * 4], a_log[32], dt_bias[32], lin_norm[128], tmp[256];
+    oref_unpack_embed_row(e, token, e->hidden);
+    size_t li = 0; /* linear-layer index */
+    for (size_t l = 0; l < n_layers; l++) {
+        const q35_records r = q35_records_of(l);
+        oref_unpack_norm(e, r.input_norm, e->norm_gamma, D);
+        oref_rmsnorm(e->hidden, e->norm_gamma, e->norm_buf, D, a->rms_eps);
+        if (q35_full(l)) {
+            oref_gemv_linear(e, r.q_proj, 2048, e->norm_buf, D, e->hy_qg, 8192, 8192, D, 0, -1);
+            oref_gemv_linear(e, r.k_proj, 256, e->norm_buf, D, e->k_buf, kvd, kvd, D, 0, -1);
+            oref_gemv_linear(e, r.v_proj, 256, e->norm_buf, D, e->v_buf, kvd, kvd, D, 0, -1);
+            q35_bf16_vector(e, r.q_norm, gq, 256);
+            q35_bf16_vector(e, r.k_norm, gk, 256);
+            for (size_t h = 0; h < H; h++) { /* the query half of each head, RMS-normed */
+                oref_rmsnorm(e->hy_qg + h * 512, gq, tmp, hd, a->rms_eps);
+                memcpy(e->q_buf + h * hd, tmp, hd * 4);
+            }
+            for (size_t h = 0; h < KV; h++) {
+                oref_rmsnorm(e->k_buf + h * hd, gk, tmp, hd, a->rms_eps);
+                memcpy(e->k_buf + h * hd, tmp, hd * 4);
+            }
+            rope_partial(e->q_buf, pos, H, hd, 64, a->rope_theta);
+            rope_partial(e->k_buf, pos, KV, hd, 64, a->rope_theta);
+            float *kc = e->k_cache + l * e->max_seq_len * kvd, *vc = e->v_cache + l * e->max_seq_len * kvd;
+            for (size_t i = 0; i < kvd; i++) {
+                float kk = e->k_buf[i], vv = e->v_buf[i];
+                if (e->kv_f16) { kk = oref_f16_to_f32(f32_to_f16(kk)); vv = oref_f16_to_f32(f32_to_f16(vv)); }
+                kc[pos * kvd + i] = kk;
+                vc[pos * kvd + i] = vv;
+            }
+            oref_attention(e->q_buf, kc, vc, pos, H, KV, hd, e->scores_buf, e->attn_out);
+            for (size_t h = 0; h < H; h++)
+                for (size_t d = 0; d < hd; d++) {
+                    const float g = e->hy_qg[h * 512 + 256 + d];
+                    e->attn_out[h * hd + d] = e->attn_out[h * hd + d] * (1.0f / (1.0f + expf(-g)));
+                }
+            oref_gemv_linear(e, r.o_proj, 1024, e->attn_out, H * hd, e->hidden, D, D, H * hd, 1, -1);
+        } else {
+            oref_gemv_linear(e, r.in_proj_qkv, 2048, e->norm_buf, D, e->hy_mix, 8192, 8192, D, 0, -1);
+            oref_gemv_linear(e, r.in_proj_z, 1024, e->norm_buf, D, e->hy_z, 4096, 4096, D, 0, -1);
+            oref_gemv_linear(e, r.in_proj_a, 8, e->norm_buf, D, e->hy_a, 32, 32, D, 0, -1);
+            oref_gemv_linear(e, r.in_proj_b, 8, e->norm_buf, D, e->hy_b, 32, 32, D, 0, -1);
+            q35_bf16_vector(e, r.conv1d, conv_w, 8192 * 4);
+            q35_bf16_vector(e, r.a_log, a_log, 32);
+            q35_bf16_vector(e, r.dt_bias, dt_bias, 32);
+            q35_bf16_vector(e, r.linear_norm, lin_norm, 128);
+            oref_conv1d_update(8192, 4, e->hy_mix, conv_w, e->conv_state + li * 8192 * 3, e->hy_conv);
+            oref_gated_delta_step(32, 16, 128, 128, e->hy_conv, e->hy_conv + 2048, e->hy_conv + 4096, e->hy_a,
+                                  e->hy_b, a_log, dt_bias, e->rec_state + li * 32 * 128 * 128, e->hy_dn);
+            oref_gated_rmsnorm(32, 128, e->hy_dn, e->hy_z, lin_norm, a->rms_eps, e->attn_out);
+            oref_gemv_linear(e, r.out_proj, 1024, e->attn_out, 4096, e->hidden, D, D, 4096, 1, -1);
+            li++;
+        }
+        oref_unpack_norm(e, r.post_norm, e->norm_gamma, D);
+        oref_rmsnorm(e->hidden, e->norm_gamma, e->norm_buf, D, a->rms_eps);
+        oref_gemv_linear(e, r.gate_proj, 3072, e->norm_buf, D, e->gate_buf, I, I, D, 0, -1);
+        oref_gemv_linear(e, r.up_proj, 3072, e->norm_buf, D, e->up_buf, I, I, D, 0, -1);
+        for (size_t i = 0; i < I; i++) e->mlp_buf[i] = oref_silu(e->gate_buf[i]) * e->up_buf[i];
+        oref_gemv_linear(e, r.down_proj, 3072, e->mlp_buf, I, e->hidden, D, D, I, 1, -1);
+        /* forwardDecode's non-finite break (:1753-1764) */
+        if (l < 3 || (l >= 8 && l <= 16) || !isfinite(e->hidden[0]))
+            if (!isfinite(sumsq_seq(e->hidden, D)) && !e->no_break) break;
+    }
+    oref_unpack_norm(e, oref_final_norm_for(e->map), e->norm_gamma, D);
+    oref_rmsnorm(e->hidden, e->norm_gamma, e->norm_buf, D, a->rms_eps);
+    compute_lm_head(e);
+    float max_logit = -1e30f;
+    uint32_t arg = 0;
+    int all_finite = 1;
+    for (size_t v = 0; v < a->vocab_size; v++) {
+        float val = e->logits_buf[v];
+        if (!isfinite(val)) all_finite = 0;
+        if (val > max_logit) { max_logit = val; arg = (uint32_t)v; }
+    }
+    res->argmax_token = arg;
+    res->max_logit = max_logit;
+    res->token0_logit = e->logits_buf[0];
+    res->elapsed_ns = now_ns() - t0;
+    res->hidden_norm = sqrtf(sumsq_seq(e->hidden, D));
+    res->all_finite = all_finite;
     return 0;
 }

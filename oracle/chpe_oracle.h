@@ -121,6 +121,10 @@ int oref_forward(oref_engine *e, uint32_t token, size_t pos, oref_result *res);
 /* worker threads of the row-parallel loops (results do not depend on it) */
 void oref_set_threads(oref_engine *e, int threads);
 void oref_set_break(oref_engine *e, int on);  /* test only: 0 removes the non-finite break */
+/* The true Qwen3.5-9B hybrid layers on the 9B cell archive (24 gated-DeltaNet layers, 8 gated
+ * full-attention layers with q/k norms and partial rotary embedding) instead of the
+ * reference's GQA aliasing; 0 ok, -1 not a 9B cell archive or out of memory. */
+int oref_set_hybrid(oref_engine *e, int on);
 /* the same step over the first n_layers layers only (a CPU timing sample) */
 int oref_forward_layers(oref_engine *e, uint32_t token, size_t pos, size_t n_layers, oref_result *res);
 /* Timing aid (no reference counterpart): fill K/V cache rows 0..n_pos-1 of every layer with

@@ -53,6 +53,8 @@ def lib():
         L.oref_forward_layers.argtypes = [V, ctypes.c_uint32, S, S, ctypes.POINTER(Result)]
         L.oref_set_threads.argtypes = [V, ctypes.c_int]
         L.oref_set_break.argtypes = [V, ctypes.c_int]
+        L.oref_set_hybrid.restype = ctypes.c_int
+        L.oref_set_hybrid.argtypes = [V, ctypes.c_int]
         L.oref_logits.restype = _fp
         L.oref_logits.argtypes = [V]
         L.oref_hidden.restype = _fp
@@ -157,6 +159,11 @@ class Oracle:
 
     def set_threads(self, n):
         self.L.oref_set_threads(self.e, n)
+
+    def set_hybrid(self, on=True):
+        """The true Qwen3.5-9B hybrid layers (DeltaNet + gated attention) on a 9B archive."""
+        if self.L.oref_set_hybrid(self.e, 1 if on else 0):
+            raise RuntimeError("oref_set_hybrid: not a 9B cell archive")
 
     def set_break(self, on):
         """Test only: set_break(False) removes forwardDecode's non-finite break (:1763), a
