@@ -78,7 +78,8 @@ Context* open_ctx(const char* path, int arch, size_t max_seq_len, bool kv_f16) {
     return nullptr;
   }
   EngineConfig cfg;
-  cfg.arch_id = arch < 0 ? arch_from_path(path) : arch;
+  cfg.arch_id = arch < 0 ? arch_from_path(path) : arch == 3 ? 1 : arch;
+  cfg.hybrid = arch == 3;
   cfg.max_seq_len = max_seq_len;
   cfg.kv_f16 = kv_f16;
   std::string err;
@@ -110,7 +111,7 @@ extern "C" {
 void* chpe_init(const char* archive_path) { return open_ctx(archive_path, -1, 2048, false); }
 
 void* chpe_init_ex(const char* archive_path, int arch, size_t max_seq_len, int kv_f16) {
-  if (arch > 2) { g_last_error = "unknown architecture"; return nullptr; }
+  if (arch > 3) { g_last_error = "unknown architecture"; return nullptr; }
   return open_ctx(archive_path, arch, max_seq_len, kv_f16 != 0);
 }
 
@@ -791,7 +792,7 @@ int chpe_debug_deltanet_conv(uint32_t channels, uint32_t taps, const float* x, c
       hipMemcpy(dx, x, nx * 4, hipMemcpyHostToDevice) == hipSuccess &&
       hipMemcpy(dw, w, nw * 4, hipMemcpyHostToDevice) == hipSuccess &&
       hipMemcpy(ds, state, ns * 4, hipMemcpyHostToDevice) == hipSuccess) {
-    DnConvArgs a{dx, dw, ds, dout, channels, taps};
+    DnConvArgs a{dx, dw, ds, dout, channels, taps, nullptr};
     launch_dn_conv(a, nullptr);
     if (hipDeviceSynchronize() == hipSuccess && hipMemcpy(out, dout, nx * 4, hipMemcpyDeviceToHost) == hipSuccess &&
         hipMemcpy(state, ds, ns * 4, hipMemcpyDeviceToHost) == hipSuccess)

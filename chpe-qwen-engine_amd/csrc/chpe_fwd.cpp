@@ -7,7 +7,9 @@
 // main.zig:86-104 does.  Each bench iteration runs the prompt from position 0
 // (chpe_forward_tokens, main.zig:169-184).  The receipt goes to stderr in the reference's
 // line format (main.zig:189-196), and the spoke JSON file is written when its directory
-// exists (main.zig:211-246).  One flag of its own: --kv-f16 keeps the KV cache in fp16.
+// exists (main.zig:211-246).  Two flags of its own: --kv-f16 keeps the KV cache in fp16;
+// --hybrid runs a Qwen3.5-9B archive through its true hybrid layers (chpe_init_ex arch 3)
+// instead of the reference's decode of the 9B map.
 #include <fcntl.h>
 #include <sys/stat.h>
 #include <unistd.h>
@@ -38,6 +40,7 @@ void usage() {
                "  --bench <iters>        Benchmark iterations (default: 1)\n"
                "  --max-seq-len <len>    Maximum sequence length (default: 2048)\n"
                "  --kv-f16               Keep the KV cache in fp16 (default: f32, as the reference)\n"
+               "  --hybrid               Qwen3.5-9B: gated DeltaNet + gated attention layers\n"
                "  -h, --help             Display this help message\n");
 }
 
@@ -48,7 +51,9 @@ int arch_of(const std::string& s, bool is_path) {
   return 0;
 }
 
-const char* arch_name(int a) { return a == 1 ? "Qwen3.5-9B" : (a == 2 ? "Qwen2.5-72B" : "Qwen2.5-3B"); }
+const char* arch_name(int a) {
+  return a == 3 ? "Qwen3.5-9B (hybrid)" : a == 1 ? "Qwen3.5-9B" : (a == 2 ? "Qwen2.5-72B" : "Qwen2.5-3B");
+}
 
 uint64_t now_ns() {
   return uint64_t(std::chrono::duration_cast<std::chrono::nanoseconds>(
@@ -61,7 +66,7 @@ uint64_t now_ns() {
 int main(int argc, char** argv) {
   std::string archive = "models/warc/Qwen2.5-3B-Instruct.bf16.raw.chpe", tokens_file, out_logits, arch_override;
   size_t bench_iters = 1, max_seq_len = 2048;
-  bool kv_f16 = false;
+  bool kv_f16 = false, hybrid = false;
   for (int i = 1; i < argc; ++i) {
     const std::string a = argv[i];
     auto next = [&](std::string* dst) {
@@ -84,12 +89,20 @@ int main(int argc, char** argv) {
       const unsigned long long n = std::strtoull(v.c_str(), &end, 10);
       max_seq_len = (!v.empty() && end && *end == 0) ? size_t(n) : 2048;
     } else if (a == "--kv-f16") kv_f16 = true;
+    else if (a == "--hybrid") hybrid = true;
     else if (a == "--help" || a == "-h") {
       usage();
       return 0;
     } else if (a.rfind("--", 0) != 0) archive = a;
   }
-  const int arch = arch_override.empty() ? arch_of(archive, true) : arch_of(arch_override, false);
+  int arch = arch_override.empty() ? arch_of(archive, true) : arch_of(arch_override, false);
+  if (hybrid) {
+    if (arch != 1) {
+      std::fprintf(stderr, "ERROR: --hybrid needs a Qwen3.5-9B archive\n");
+      return 1;
+    }
+    arch = 3;
+  }
 
   std::fprintf(stderr, "=== [UNIFIED POLYMORPHIC CHPE FORWARD ENGINE] ===\n");
   std::fprintf(stderr, "Archive Path   : %s\n", archive.c_str());

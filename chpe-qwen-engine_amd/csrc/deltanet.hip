@@ -35,12 +35,14 @@ __global__ void __launch_bounds__(256) k_dn_conv(DnConvArgs a) {
     sv[k] = k + 1 < T ? st[k] : 0.0f;
   }
   const float x = a.x[c], wl = w[T - 1];
+  const bool keep = a.step && a.step->broken;  // (after the step's break: the state stays)
   float acc = 0.0f;  // oldest tap first, the new input last
 #pragma unroll
   for (uint32_t k = 0; k < kDnMaxTaps; ++k)
     if (k + 1 < T) acc += wv[k] * sv[k];
   acc += wl * x;
   a.out[c] = silu_f(acc);
+  if (keep) return;
 #pragma unroll
   for (uint32_t k = 0; k + 1 < kDnMaxTaps; ++k)
     if (k + 2 < T) st[k] = sv[k + 1];
@@ -77,6 +79,7 @@ __global__ void __launch_bounds__(256) k_dn_step(DnStepArgs a) {
     kv[m] = a.k[size_t(kh) * D + lane + 64 * m];
   }
   const float vj = a.v[size_t(h) * D + c0 + j];
+  const bool keep = a.step && a.step->broken;  // (after the step's break: the state stays)
   const float beta = 1.0f / (1.0f + expf(-a.b[h]));
   const float decay = expf(-expf(a.A_log[h]) * softplus_f(a.a[h] + a.dt_bias[h]));
 
@@ -127,7 +130,7 @@ __global__ void __launch_bounds__(256) k_dn_step(DnStepArgs a) {
 #pragma unroll
   for (int r = 0; r < RPB; ++r) {
     sr[r] += s_kn[rb * RPB + r] * delta;
-    S[size_t(rb * RPB + r) * D] = sr[r];
+    if (!keep) S[size_t(rb * RPB + r) * D] = sr[r];
     o += sr[r] * s_qn[rb * RPB + r];
   }
   o = column_sum(o);

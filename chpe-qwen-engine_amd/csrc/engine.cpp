@@ -107,6 +107,8 @@ bool Engine::init(const uint8_t* b, size_t len, const EngineConfig& cfg, std::st
   host_bytes_ = b;
   len_ = len;
   if (!arch_preset(cfg.arch_id, &arch_)) { *err = "unknown architecture"; return false; }
+  if (cfg.hybrid && cfg.arch_id != 1) { *err = "the hybrid layers are Qwen3.5-9B's"; return false; }
+  rope_dim_ = uint32_t(cfg.hybrid ? 64 : arch_.head_dim);  // (partial_rotary_factor 0.25 of 256)
   // ---- format detection: CHPEEngine.init, src/chpe_engine.zig:869-918
   if (len >= 4096) {
     const uint32_t magic = rd<uint32_t>(b, len, 0);
@@ -261,15 +263,18 @@ bool Engine::init(const uint8_t* b, size_t len, const EngineConfig& cfg, std::st
   HIP_TRY(hipMemset(d_result_, 0, sizeof(StepResult)));
   HIP_TRY(hipMemset(d_state_, 0, sizeof(StepState)));
   // RoPE angles exactly as applyRope computes them (src/chpe_engine.zig:197-206), in f32
-  std::vector<float> cs(S * (hd / 2)), sn(S * (hd / 2));
+  // (the hybrid model rotates the first rope_dim_ = 64 dims of a head: the same formula over
+  // 64 dims)
+  const size_t rd = rope_dim_;
+  std::vector<float> cs(S * (rd / 2)), sn(S * (rd / 2));
   for (size_t p = 0; p < S; ++p) {
     const float pos_f = float(p);
-    for (size_t i = 0; i < hd / 2; ++i) {
-      const float freq_exponent = 2.0f * float(i) / float(hd);
+    for (size_t i = 0; i < rd / 2; ++i) {
+      const float freq_exponent = 2.0f * float(i) / float(rd);
       const float freq = 1.0f / std::pow(arch_.rope_theta, freq_exponent);
       const float theta = pos_f * freq;
-      cs[p * (hd / 2) + i] = std::cos(theta);
-      sn[p * (hd / 2) + i] = std::sin(theta);
+      cs[p * (rd / 2) + i] = std::cos(theta);
+      sn[p * (rd / 2) + i] = std::sin(theta);
     }
   }
   d_rope_cos_ = upload_vector(cs);
@@ -277,10 +282,12 @@ bool Engine::init(const uint8_t* b, size_t len, const EngineConfig& cfg, std::st
   d_rope_cur_ = static_cast<float*>(dev_alloc(hd * 4));
   HIP_TRY(hipHostMalloc(reinterpret_cast<void**>(&h_state_), sizeof(StepState), hipHostMallocDefault));
   HIP_TRY(hipHostMalloc(reinterpret_cast<void**>(&h_result_), sizeof(StepResult), hipHostMallocDefault));
-  {  // the block step for archives whose projections are all flat 4-bit tiles (CHPE_BLOCK=0: off)
+  if (cfg.hybrid && !plan_hybrid(err)) return false;
+  {  // the block step for archives whose projections are all flat 4-bit tiles (CHPE_BLOCK=0: off;
+     // the hybrid model: verify and prefill as decode steps, the recurrent state advances per token)
     const char* bk = std::getenv("CHPE_BLOCK");
     std::string why;
-    if (!(bk && bk[0] == '0') && !plan_block(&why) && !why.empty()) {
+    if (!cfg.hybrid && !(bk && bk[0] == '0') && !plan_block(&why) && !why.empty()) {
       *err = "block step: " + why;
       return false;
     }
@@ -731,7 +738,7 @@ RopeArgs Engine::rope_args(size_t l) const {
   RopeArgs r{};
   r.state = d_state_;
   r.cos = d_rope_cur_;
-  r.sin = d_rope_cur_ + arch_.head_dim / 2;
+  r.sin = d_rope_cur_ + rope_dim_ / 2;
   r.k_cache = static_cast<uint8_t*>(d_kcache_) + l * kvd * S * kv_elem;
   r.v_cache = static_cast<uint8_t*>(d_vcache_) + l * kvd * S * kv_elem;
   r.head_dim = uint32_t(arch_.head_dim);
@@ -781,7 +788,7 @@ EmbedArgs Engine::embed_args() const {
   e.rope_cos = d_rope_cos_;
   e.rope_sin = d_rope_sin_;
   e.rope_cur = d_rope_cur_;
-  e.rope_half = uint32_t(arch_.head_dim / 2);
+  e.rope_half = rope_dim_ / 2;
   e.rope_rows = uint32_t(cfg_.max_seq_len);
   return e;
 }
@@ -790,6 +797,7 @@ int Engine::set_state(const StepState& s) {
   *h_state_ = s;
   h_pos_ = s.pos;
   if (hipMemcpyAsync(d_state_, h_state_, sizeof(StepState), hipMemcpyHostToDevice, stream_) != hipSuccess) return -3;
+  if (cfg_.hybrid && s.pos == 0) reset_hybrid_state(stream_);  // a new sequence
   // the first step's input; with embed_fused_ every step's k_finish embeds the next token
   if (embed_fused_) launch_embed(embed_args(), stream_);
   return hipGetLastError() == hipSuccess ? 0 : -3;
@@ -798,6 +806,10 @@ int Engine::set_state(const StepState& s) {
 // One decode step (forwardDecode :1663-1803) on the device: its input hidden state is already in
 // place (set_state, or the previous step's k_finish).
 void Engine::record_step(hipStream_t st) {
+  if (cfg_.hybrid) {
+    record_step_hybrid(st);
+    return;
+  }
   const uint32_t D = uint32_t(arch_.hidden_dim), I = uint32_t(arch_.intermediate_dim);
   if (!embed_fused_) launch_embed(embed_args(), st);
   // begin/end events of every launch of one stage (time_stage_live; never during capture)
@@ -872,6 +884,7 @@ int Engine::launch_steps(size_t n) {
 
 int Engine::time_stage_live(int stage, size_t n_steps, double* avg_ms, size_t* launches) {
   if (stage < 0 || stage > 6 || n_steps == 0) return -1;
+  if (cfg_.hybrid && stage != 2 && stage != 3 && stage != 4) return -1;  // (the stages both layer kinds share)
   if (h_pos_ + n_steps > cfg_.max_seq_len) return -2;
   const size_t per_step = stage == 4 ? 1 : arch_.num_layers;
   const size_t n = per_step * n_steps;
@@ -1227,6 +1240,21 @@ double Engine::stage_bytes(int stage, size_t l) const {
 double Engine::step_bytes(size_t pos) const {
   double bytes = 0.0;
   const double D = double(arch_.hidden_dim);
+  if (cfg_.hybrid) {  // weights, norms, the 8 attention layers' KV rows, the DeltaNet states (r + w)
+    const double kv_row = double(arch_.num_kv_heads * arch_.head_dim) * (cfg_.kv_f16 ? 2 : 4);
+    for (size_t l = 0; l < hyb_.size(); ++l) {
+      const HybLayer& H = hyb_[l];
+      bytes += proj_bytes(H.in0) + proj_bytes(H.in1) + proj_bytes(H.in2) + proj_bytes(H.out) + 2 * D * 4;
+      bytes += stage_bytes(2, l) + stage_bytes(3, l);
+      if (H.full) {
+        bytes += 2 * 256 * 4 + 2 * kv_row * (double(pos) + 1) + 2 * kv_row;
+      } else {
+        bytes += proj_bytes(H.in3) + (8192.0 * 4 + 32 * 2 + 128) * 4;  // conv weights, A_log, dt_bias, norm
+        bytes += 2.0 * (8192.0 * 3 + 32.0 * 128 * 128) * 4;            // conv and delta-rule states
+      }
+    }
+    return bytes + stage_bytes(4, 0) + D * 4 + D * 0.5625;
+  }
   for (size_t l = 0; l < arch_.num_layers; ++l)
     bytes += stage_bytes(0, l) + stage_bytes(1, l) + stage_bytes(2, l) + stage_bytes(3, l) + 2 * D * 4;
   bytes += stage_bytes(4, 0) + D * 4;                        // LM head + final norm
@@ -1237,8 +1265,182 @@ double Engine::step_bytes(size_t pos) const {
   return bytes;
 }
 
+bool Engine::plan_hybrid(std::string* err) {
+  const size_t D = arch_.hidden_dim;
+  if (is_raw_ || D != 4096 || arch_.head_dim != 256 || arch_.num_attn_heads != 16 || arch_.num_kv_heads != 4) {
+    *err = "the hybrid layers need the 9B cell archive";
+    return false;
+  }
+  const uint8_t* b = host_bytes_;
+  const size_t cell_off = is_dense_ ? 0 : kPrefetchBytes;
+  // bf16 vectors: 8192 values per record's code area
+  auto bf16vec = [&](size_t rec, size_t n) {
+    std::vector<float> v(n, 0.0f);
+    for (size_t i = 0; i < n; ++i) {
+      const size_t r = rec + i / 8192;
+      if (r < record_count_)
+        v[i] = bf16_to_f32(rd<uint16_t>(b, len_, 4096 + r * stride_ + cell_off + kBytecodeHeader + 2 * (i % 8192)));
+    }
+    return upload_vector(v);
+  };
+  hyb_.resize(arch_.num_layers);
+  uint32_t n_lin = 0;
+  for (size_t l = 0; l < arch_.num_layers; ++l) {
+    const Qwen35Records r = qwen35_records(l);
+    HybLayer& H = hyb_[l];
+    H.full = r.full_attn;
+    std::string why;
+    auto plan = [&](const char* name, size_t ts, size_t nt, size_t rows, size_t cols, bool acc, ProjPlan* p) {
+      if (plan_projection(ts, nt, rows, cols, cols, rows, acc, -1, p, &why)) return true;
+      *err = "hybrid layer " + std::to_string(l) + " " + name + ": " + why;
+      return false;
+    };
+    if (H.full) {
+      if (!plan("q_proj", r.q_proj, 2048, 8192, D, false, &H.in0) || !plan("k_proj", r.k_proj, 256, 1024, D, false, &H.in1) ||
+          !plan("v_proj", r.v_proj, 256, 1024, D, false, &H.in2) || !plan("o_proj", r.o_proj, 1024, D, 4096, true, &H.out))
+        return false;
+      H.q_norm = bf16vec(r.q_norm, 256);
+      H.k_norm = bf16vec(r.k_norm, 256);
+    } else {
+      if (!plan("in_proj_qkv", r.in_proj_qkv, 2048, 8192, D, false, &H.in0) ||
+          !plan("in_proj_z", r.in_proj_z, 1024, 4096, D, false, &H.in1) ||
+          !plan("in_proj_a", r.in_proj_a, 8, 32, D, false, &H.in2) || !plan("in_proj_b", r.in_proj_b, 8, 32, D, false, &H.in3) ||
+          !plan("out_proj", r.out_proj, 1024, D, 4096, true, &H.out))
+        return false;
+      H.conv_w = bf16vec(r.conv1d, 8192 * 4);
+      H.A_log = bf16vec(r.a_log, 32);
+      H.dt_bias = bf16vec(r.dt_bias, 32);
+      H.lin_norm = bf16vec(r.linear_norm, 128);
+      H.lin = n_lin++;
+    }
+  }
+  auto fa = [&](size_t n) { return static_cast<float*>(dev_alloc(n * 4)); };
+  d_hx0_ = fa(8192);
+  d_hx1_ = fa(4096);
+  d_hx2_ = fa(1024);
+  d_hx3_ = fa(32);
+  d_hconv_ = fa(8192);
+  conv_state_floats_ = size_t(n_lin) * 8192 * 3;
+  rec_state_floats_ = size_t(n_lin) * 32 * 128 * 128;
+  d_conv_state_ = fa(conv_state_floats_);
+  d_rec_state_ = fa(rec_state_floats_);
+  if (!d_hx0_ || !d_hx1_ || !d_hx2_ || !d_hx3_ || !d_hconv_ || !d_conv_state_ || !d_rec_state_) {
+    *err = "allocation";
+    return false;
+  }
+  reset_hybrid_state(stream_);
+  return true;
+}
+
+void Engine::reset_hybrid_state(hipStream_t st) {
+  (void)hipMemsetAsync(d_conv_state_, 0, conv_state_floats_ * 4, st);
+  (void)hipMemsetAsync(d_rec_state_, 0, rec_state_floats_ * 4, st);
+}
+
+// One decode step of the Qwen3.5-9B hybrid (the layer loop of forwardDecode :1663-1803 with the
+// hybrid token mixers; see HybLayer).  Per layer: the normalised input projections (QkvRope
+// launches whose parts have role kRoleStore: rows stored as computed, the break test made),
+// then for a full-attention layer the q / k norms and partial rotary embedding with the KV
+// append (k_hyb_qk), the decode attention, the output gate, o_proj into the residual; for a
+// DeltaNet layer the conv update, the gated delta rule with the gated norm, out_proj into the
+// residual; then the MLP as in record_step.
+void Engine::record_step_hybrid(hipStream_t st) {
+  const uint32_t D = uint32_t(arch_.hidden_dim), I = uint32_t(arch_.intermediate_dim);
+  if (!embed_fused_) launch_embed(embed_args(), st);
+  // (stage timing: the MLP launches and the LM head, the stages both layer kinds share)
+  auto mark = [&](int stage) {
+    if (probe_stage_ != stage) return;
+    arm_launch_probe(probe_events_[probe_next_], probe_events_[probe_next_ + 1]);
+    probe_next_ += 2;
+  };
+  const uint32_t store[3] = {kRoleStore, kRoleStore, kRoleStore};
+  for (size_t l = 0; l < arch_.num_layers; ++l) {
+    const LayerPlan& L = layers_[l];
+    const HybLayer& H = hyb_[l];
+    RopeArgs ra = rope_args(l);
+    ra.head_dim = 32;  // (Store parts: rows pair within blocks of 32, a divisor of every part's rows)
+    float* hid[1] = {d_hidden_};
+    if (H.full) {
+      const ProjPlan* in[3] = {&H.in0, &H.in1, &H.in2};
+      float* outs[3] = {d_hx0_, d_hx1_, d_hx2_};
+      enqueue_gemv(in, outs, 3, GemvMode::QkvRope, d_hidden_, D, L.gamma_in, st, &ra, store);
+      const RopeArgs kv = rope_args(l);
+      HybQkArgs q{};
+      q.state = d_state_;
+      q.qg = d_hx0_;
+      q.k = d_hx1_;
+      q.v = d_hx2_;
+      q.q_norm = H.q_norm;
+      q.k_norm = H.k_norm;
+      q.rope_cos = d_rope_cos_;
+      q.rope_sin = d_rope_sin_;
+      q.q_out = d_q_;
+      q.k_cache = kv.k_cache;
+      q.v_cache = kv.v_cache;
+      q.H = uint32_t(arch_.num_attn_heads);
+      q.KV = uint32_t(arch_.num_kv_heads);
+      q.hd = uint32_t(arch_.head_dim);
+      q.rot = rope_dim_;
+      q.max_seq = kv.max_seq;
+      q.kv_f16 = kv.kv_f16;
+      q.rope_rows = uint32_t(cfg_.max_seq_len);
+      q.eps = arch_.rms_eps;
+      launch_hyb_qk(q, st);
+      const AttnArgs aa = attn_args(l);
+      launch_attention_partial(aa, st);
+      launch_attention_combine(aa, st);
+      launch_hyb_gate(d_attn_, d_hx0_, q.H, q.hd, st);
+      const ProjPlan* o[1] = {&H.out};
+      enqueue_gemv(o, hid, 1, GemvMode::Accum, d_attn_, uint32_t(q.H * q.hd), nullptr, st);
+    } else {
+      const ProjPlan* in[3] = {&H.in0, &H.in1, &H.in2};
+      float* outs[3] = {d_hx0_, d_hx1_, d_hx2_};
+      enqueue_gemv(in, outs, 3, GemvMode::QkvRope, d_hidden_, D, L.gamma_in, st, &ra, store);
+      const ProjPlan* inb[1] = {&H.in3};
+      float* outb[1] = {d_hx3_};
+      enqueue_gemv(inb, outb, 1, GemvMode::QkvRope, d_hidden_, D, L.gamma_in, st, &ra, store);
+      DnConvArgs c{d_hx0_, H.conv_w, d_conv_state_ + size_t(H.lin) * 8192 * 3, d_hconv_, 8192, 4, d_state_};
+      launch_dn_conv(c, st);
+      DnStepArgs dn{};
+      dn.q = d_hconv_;
+      dn.k = d_hconv_ + 2048;
+      dn.v = d_hconv_ + 4096;
+      dn.a = d_hx2_;
+      dn.b = d_hx3_;
+      dn.A_log = H.A_log;
+      dn.dt_bias = H.dt_bias;
+      dn.z = d_hx1_;
+      dn.norm_w = H.lin_norm;
+      dn.state = d_rec_state_ + size_t(H.lin) * 32 * 128 * 128;
+      dn.out = d_attn_;
+      dn.n_v_heads = 32;
+      dn.n_k_heads = 16;
+      dn.eps = arch_.rms_eps;
+      dn.step = d_state_;
+      launch_dn_step(dn, 128, st);
+      const ProjPlan* o[1] = {&H.out};
+      enqueue_gemv(o, hid, 1, GemvMode::Accum, d_attn_, 4096, nullptr, st);
+    }
+    const ProjPlan* gu[2] = {&L.gate, &L.up};
+    float* mlp[2] = {d_mlp_, d_mlp_};
+    mark(2);
+    enqueue_gemv(gu, mlp, 2, GemvMode::SwiGlu, d_hidden_, D, L.gamma_post, st);
+    const ProjPlan* dn[1] = {&L.down};
+    mark(3);
+    enqueue_gemv(dn, hid, 1, GemvMode::Accum, d_mlp_, I, nullptr, st);
+  }
+  const ProjPlan* lm[1] = {&lm_head_};
+  float* lg[1] = {d_logits_};
+  mark(4);
+  const uint32_t n_partials = enqueue_gemv(lm, lg, 1, GemvMode::Logits, d_hidden_, D, d_gamma_final_, st);
+  FinishArgs f{d_state_, d_prompt_, d_partials_, n_partials, d_logits_, d_result_, d_out_tokens_, embed_args(),
+               embed_fused_ ? 1u : 0u};
+  launch_finish(f, st);
+}
+
 int Engine::launch_stage(int stage, size_t l) {
   if (l >= layers_.size()) return -1;
+  if (cfg_.hybrid && stage != 2 && stage != 3 && stage != 4) return -1;  // (the MLP and LM head only)
   // q/k/v appends a KV row and attention reads rows up to the device position
   if ((stage == 0 || stage == 5 || stage == 6) && h_pos_ >= cfg_.max_seq_len) return -2;
   const LayerPlan& L = layers_[l];

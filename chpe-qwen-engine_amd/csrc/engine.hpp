@@ -42,6 +42,8 @@ struct EngineConfig {
   int arch_id = 0;
   size_t max_seq_len = 2048;
   bool kv_f16 = false;  // fp16 KV cache (the reference keeps f32)
+  bool hybrid = false;  // Qwen3.5-9B (arch 1): the true hybrid layers instead of the reference's
+                        //   GQA aliasing (HybLayer)
 };
 
 // One projection as the GPU computes it (a gemvLinear call of the reference).
@@ -100,6 +102,21 @@ struct LayerPlan {
   ProjPlan q, k, v, o, gate, up, down;
   float* gamma_in = nullptr;    // device, unpackNorm rules applied
   float* gamma_post = nullptr;
+};
+
+// A layer of the Qwen3.5-9B hybrid (EngineConfig::hybrid; no reference code, README.md:17,62):
+// layer l % 4 == 3 is gated full attention -- in0 = q_proj (per head 256 query rows, then 256
+// output-gate rows), in1 = k_proj, in2 = v_proj, out = o_proj, with q / k norm gains --, the
+// others gated DeltaNet -- in0 = in_proj_qkv, in1 = in_proj_z, in2 = in_proj_a, in3 = in_proj_b,
+// out = out_proj, with the conv weights [8192][4], A_log, dt_bias [32] and the gated norm's
+// gains [128]; `lin` indexes the DeltaNet layers' state buffers.  The MLP and the two norms are
+// the LayerPlan's.  Record offsets: qwen35_records (qwen35_tensor_map.zig:62-1015).
+struct HybLayer {
+  bool full = false;
+  ProjPlan in0, in1, in2, in3, out;
+  float *q_norm = nullptr, *k_norm = nullptr;
+  float *conv_w = nullptr, *A_log = nullptr, *dt_bias = nullptr, *lin_norm = nullptr;
+  uint32_t lin = 0;
 };
 
 class Engine {
@@ -175,6 +192,9 @@ class Engine {
   float* upload_vector(const std::vector<float>& v);
   void* dev_alloc(size_t bytes);
   void record_step(hipStream_t st);
+  void record_step_hybrid(hipStream_t st);    // (record_step's body for EngineConfig::hybrid)
+  bool plan_hybrid(std::string* err);          // the HybLayer plans, vectors and state buffers
+  void reset_hybrid_state(hipStream_t st);     // zero recurrent states (a step at position 0)
   EmbedArgs embed_args() const;
   int set_state(const StepState& s);  // host-set (token, pos, ...) and the embedding of its token
   void enqueue_qkv(size_t layer, hipStream_t st);
@@ -248,6 +268,13 @@ class Engine {
   PolyRaw poly_raw_{};               // polymorphic cells: raw row sums per part
   float* flat_part_ = nullptr;       // FlatPoly: row-segment sums per tile
   size_t flat_part_floats_ = 0;
+
+  // the hybrid model (EngineConfig::hybrid)
+  std::vector<HybLayer> hyb_;
+  float *d_hx0_ = nullptr, *d_hx1_ = nullptr, *d_hx2_ = nullptr, *d_hx3_ = nullptr, *d_hconv_ = nullptr;
+  float *d_conv_state_ = nullptr, *d_rec_state_ = nullptr;
+  size_t conv_state_floats_ = 0, rec_state_floats_ = 0;
+  uint32_t rope_dim_ = 0;   // dims of a head the rotary tables cover (head_dim; hybrid: 64)
 
   // the block step (plan_block): m <= kMaxBlock tokens' activations, operand tables, partials
   bool block_ok_ = false;

@@ -560,7 +560,7 @@ __device__ __forceinline__ void issue_unit(const GemvArgs& a, uint32_t unit, uin
     u->pre_ok = ok;
   }
   if constexpr (kRope) {  // cos / sin of the pair (j, j + half) served by lane S * i, i < RU/2
-    const bool ok = with_pre && active && (lane % S) == 0 && lane < 32 && P0.rope_role != kRoleV;
+    const bool ok = with_pre && active && (lane % S) == 0 && lane < 32 && P0.rope_role < kRoleV;
     const size_t at = ok ? (own % (2 * half)) : 0u;  // (the step's cos / sin row, staged)
     u->rc = a.rope.cos[at];
     u->rs = a.rope.sin[at];
@@ -613,11 +613,11 @@ __device__ __forceinline__ void rope_store(const GemvArgs& a, const GemvPart& P,
 #pragma clang fp contract(off)
   const uint32_t half = a.rope.head_dim / 2;
   float o0 = lo, o1 = hi;
-  if (P.rope_role != kRoleV) {
+  if (P.rope_role < kRoleV) {
     o0 = lo * c - hi * sn;
     o1 = lo * sn + hi * c;
   }
-  if (P.rope_role == kRoleQ) {
+  if (P.rope_role == kRoleQ || P.rope_role == kRoleStore) {
     P.y[r] = o0;
     P.y[r + half] = o1;
     return;
@@ -865,7 +865,7 @@ __global__ void __launch_bounds__(512, 2) k_gemv_split(GemvArgs a) {
       if (wave == 0 && (lane % S) == 0 && own < P0.rows) {
         pre = MODE == int(GemvMode::Accum) ? P0.y[own] : (P0.bias ? P0.bias[own] : 0.0f);
         if constexpr (kRope) {
-          if (lane < 32 && P0.rope_role != kRoleV) {
+          if (lane < 32 && P0.rope_role < kRoleV) {
             const size_t at = own % (2 * half);
             rc = a.rope.cos[at];
             rs = a.rope.sin[at];
@@ -1036,7 +1036,7 @@ __global__ void __launch_bounds__(kWave * kCellWaves) k_gemv_cells(GemvArgs a) {
     pre = (esrc ? esrc : a.x)[pre_ok ? orow : 0u];
   }
   if constexpr (kRope) {
-    rope_ok = elive && (lane % S) == 0 && lane < 32 && erole != kRoleV;
+    rope_ok = elive && (lane % S) == 0 && lane < 32 && erole < kRoleV;
     const size_t at = rope_ok ? (orow % (2 * half)) : 0u;
     rc = a.rope.cos[at];
     rs = a.rope.sin[at];
@@ -1378,7 +1378,7 @@ __global__ void __launch_bounds__(kWave * kMmaWaves) k_gemv_mma(GemvArgs a) {
     pre = (esrc ? esrc : a.x)[pre_ok ? orow : 0u];
   }
   if constexpr (kRope) {  // the pair's dimension: (first row of part A mod head_dim) + 4 eh + i < half
-    rope_ok = ovalid && (lane % S) == 0 && !oB && erole != kRoleV;
+    rope_ok = ovalid && (lane % S) == 0 && !oB && erole < kRoleV;
     const uint32_t fa = erA != 0xffffffffu ? erA : 0u, dA = fa - (fa / (2 * half)) * (2 * half);
     const size_t at = dA + 4 * eh + uint32_t(i8 & 3);
     rc = a.rope.cos[at];
@@ -1668,7 +1668,7 @@ __global__ void __launch_bounds__(kWave * W) k_gemv_flat(GemvArgs a) {
     pre = (src ? src : a.x)[pre_ok ? orow : 0u];
   }
   if constexpr (kRope) {
-    rope_ok = (lane % S) == 0 && lane < 32 && P0.rope_role != kRoleV;
+    rope_ok = (lane % S) == 0 && lane < 32 && P0.rope_role < kRoleV;
     const size_t at = rope_ok ? (orow % (2 * half)) : 0u;
     rc = a.rope.cos[at];
     rs = a.rope.sin[at];
@@ -1896,7 +1896,7 @@ __global__ void __launch_bounds__(kWave * NW) k_gemv_xs(GemvArgs a) {
         const bool ok2 = lane < NE && r2 < P0.rows && src != nullptr;
         L->pre2 = (src ? src : a.x)[ok2 ? r2 : 0u];
         L->pre2 = ok2 ? L->pre2 : 0.0f;
-        const bool rope = lane < NE && P0.rope_role != kRoleV;
+        const bool rope = lane < NE && P0.rope_role < kRoleV;
         const size_t at = rope ? (r % (2 * half)) : 0u;
         L->rc = rope ? a.rope.cos[at] : 1.0f;
         L->rs = rope ? a.rope.sin[at] : 0.0f;
@@ -2202,7 +2202,7 @@ __global__ void __launch_bounds__(kWave * NW) k_gemv_xm(GemvArgs a) {
         const bool ok2 = lane < NE && r2 < P0.rows && src != nullptr;
         L->pre2 = (src ? src : a.x)[ok2 ? r2 : 0u];
         L->pre2 = ok2 ? L->pre2 : 0.0f;
-        const bool rope = lane < NE && P0.rope_role != kRoleV;
+        const bool rope = lane < NE && P0.rope_role < kRoleV;
         const size_t at = rope ? (r % (2 * half)) : 0u;
         L->rc = rope ? a.rope.cos[at] : 1.0f;
         L->rs = rope ? a.rope.sin[at] : 0.0f;

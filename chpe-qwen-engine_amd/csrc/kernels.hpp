@@ -39,7 +39,9 @@ enum class GemvMode : int {
                // stored into the KV cache at the step's position (rounded to the cache type)
 };
 
-enum RopeRole : uint32_t { kRoleQ = 0, kRoleK = 1, kRoleV = 2 };
+// kRoleStore: the part's rows stored as computed (no rotation, no KV append) -- the normalised
+// input projections of the hybrid layers, whose per-head norms and rotary embedding come after
+enum RopeRole : uint32_t { kRoleQ = 0, kRoleK = 1, kRoleV = 2, kRoleStore = 3 };
 struct StepState;
 
 struct RopeArgs {            // QkvRope: applyRope (chpe_engine.zig:195-216) + KV append (:1693-1697)
@@ -336,6 +338,7 @@ struct DnConvArgs {         // depthwise causal conv update + SiLU
   float* state;             // [channels][taps-1], oldest first; shifted in place
   float* out;               // [channels]
   uint32_t channels, taps;
+  const StepState* step;    // or null: after the step's break (StepState::broken) the state stays
 };
 struct DnStepArgs {         // gated delta rule over the value heads (+ gated RMSNorm)
   const float *q, *k;       // [n_k_heads][head_dim], before the l2 norm
@@ -348,7 +351,32 @@ struct DnStepArgs {         // gated delta rule over the value heads (+ gated RM
   float* out;               // [n_v_heads][head_dim]
   uint32_t n_v_heads, n_k_heads;
   float eps;
+  const StepState* step;    // or null: after the step's break (StepState::broken) the state stays
 };
+
+// The hybrid model's gated full-attention layer around the decode attention kernels
+// (transformers' Qwen3_5Attention): per query head the RMS norm (q_norm gains) and the rotary
+// embedding of the first `rot` dims (pairs (i, i + rot/2)), into q_out; per kv head the same
+// for k (k_norm gains) and both appended to the KV cache at the step's position (as the QkvRope
+// epilogue appends them); then, after attention, the output times sigmoid(gate).
+struct HybQkArgs {
+  const StepState* state;   // position, StepState::broken (no KV append after a break)
+  const float* qg;          // [H][2 hd]: per head the query (hd values), then the output gate
+  const float* k;           // [KV][hd]
+  const float* v;           // [KV][hd]
+  const float* q_norm;      // [hd] gains
+  const float* k_norm;      // [hd]
+  const float* rope_cos;    // [rope_rows][rot/2]
+  const float* rope_sin;
+  float* q_out;             // [H][hd]
+  void* k_cache;            // this layer, as RopeArgs::k_cache / v_cache
+  void* v_cache;
+  uint32_t H, KV, hd, rot, max_seq, kv_f16, rope_rows;
+  float eps;
+};
+void launch_hyb_qk(const HybQkArgs& a, hipStream_t stream);
+// attn[h][d] *= sigmoid(qg[h][hd + d]) for H heads of hd
+void launch_hyb_gate(float* attn, const float* qg, uint32_t H, uint32_t hd, hipStream_t stream);
 bool deltanet_supported(uint32_t n_v_heads, uint32_t n_k_heads, uint32_t head_dim, uint32_t taps);
 void launch_dn_conv(const DnConvArgs& a, hipStream_t stream);
 void launch_dn_step(const DnStepArgs& a, uint32_t head_dim, hipStream_t stream);

@@ -51,8 +51,11 @@ void chpe_free(void *ctx);
 /* ---------------- additions (no counterpart in the reference) ---------------- */
 
 /* chpe_init with an explicit architecture (0 = Qwen2.5-3B, 1 = Qwen3.5-9B,
- * 2 = Qwen2.5-72B, -1 = guess from the path), max_seq_len and KV-cache type
- * (kv_f16 != 0: fp16 KV cache in HBM; 0: f32 as the reference). */
+ * 2 = Qwen2.5-72B, 3 = Qwen3.5-9B with its true hybrid layers -- gated DeltaNet and gated
+ * full attention with q / k norms and partial rotary embedding, recurrent states cleared at
+ * position 0; the 9B cell archive only --, -1 = guess from the path), max_seq_len and
+ * KV-cache type (kv_f16 != 0: fp16 KV cache in HBM; 0: f32 as the reference).  Arch 1 is the
+ * reference's decode of the 9B map (its GQA aliasing, chpe_engine.zig:1663-1803). */
 void *chpe_init_ex(const char *archive_path, int arch, size_t max_seq_len, int kv_f16);
 
 /* One forwardDecode(token, pos) (src/chpe_engine.zig:1663) on the context's current KV

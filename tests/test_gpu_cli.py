@@ -9,7 +9,8 @@ little-endian u32 (`--tokens-file`), runs `chpe_fwd --archive A --tokens-file P 
   * the receipt lines (main.zig:189-196) parse, and carry the C ABI's last-result values;
   * --bench N runs the prompt N times from position 0 (main.zig:169-184) with the same result;
   * the spoke JSON (main.zig:211-246) is written when run/spoke_outbox exists;
-  * error exits: a missing archive (FileNotFound), an empty tokens file (EmptyTokensFile).
+  * error exits: a missing archive (FileNotFound), an empty tokens file (EmptyTokensFile),
+    --hybrid on an archive that is not Qwen3.5-9B.
 """
 import json
 import re
@@ -119,5 +120,7 @@ def test_cli_error_exits(w4_archive, tmp_path):
     empty.write_bytes(b"")
     rc, err = run_cli(["--archive", w4_archive, "--tokens-file", empty], tmp_path)
     assert rc == 1 and "EmptyTokensFile" in err
+    rc, err = run_cli(["--archive", w4_archive, "--hybrid"], tmp_path)
+    assert rc == 1 and "--hybrid needs a Qwen3.5-9B archive" in err
     rc, err = run_cli(["-h"], tmp_path)
-    assert rc == 0 and "--tokens-file <path>" in err
+    assert rc == 0 and "--tokens-file <path>" in err and "--hybrid" in err
