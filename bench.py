@@ -7,7 +7,8 @@ seeded archive of libchpe_pack.so, 38.6 GB, resident in HBM), KV cache in fp16 i
 then `--steps` greedy decode steps timed (128 by default).  `--warmup` untimed steps run
 first, at positions 0..W-1 of the same prompt, before the context is built.  Other
 workloads: qwen72b-w2 (2-bit tiles), qwen3b-w4 (Qwen2.5-3B 4-bit cells, 4096-token prompt),
-qwen9b-w4 (Qwen3.5-9B 4-bit flat tiles, the reference's GQA-aliased decode, 2048 tokens).
+qwen9b-w4 (Qwen3.5-9B 4-bit flat tiles, the reference's GQA-aliased decode, 2048 tokens),
+qwen9b-hybrid (the same archive through the true hybrid layers: gated DeltaNet + gated attention).
 
 A step is one CHPEEngine.forwardDecode (src/chpe_engine.zig:1663-1803): embed, the layers,
 LM head, argmax, with the argmax fed back on the device.  Inputs are resident in HBM before
@@ -57,7 +58,13 @@ WORKLOADS = {
     "qwen9b-w4": dict(kind=7, arch=1, prompt=2048, V=248320, L=32, H=16, KV=4, hd=256, D=4096, I=12288,
                       desc="Qwen3.5-9B 4-bit GROUP128 flat tiles at the INT8 map's indices, "
                            "reference-compatible GQA decode"),
+    "qwen9b-hybrid": dict(kind=7, arch=3, oracle_arch=1, hybrid=True, prompt=2048, V=248320, L=32, H=16, KV=4,
+                          hd=256, D=4096, I=12288,
+                          desc="Qwen3.5-9B 4-bit GROUP128 flat tiles, the true hybrid layers (24 gated "
+                               "DeltaNet + 8 gated full attention)"),
 }
+# the stages both layer kinds of the hybrid model share (its token mixers are timed as the rest)
+HYBRID_STAGES = (2, 3, 4)
 
 
 def log(*a):
@@ -65,8 +72,10 @@ def log(*a):
 
 
 def attention_bytes(w, stage, pos):
-    """Algorithmic HBM bytes of one attention launch at position `pos` (fp16 KV)."""
-    chunk = 8192 // w["hd"]
+    """Algorithmic HBM bytes of one attention launch at position `pos` (fp16 KV); the chunk
+    length is the kernels' (attn_chunk_of: 128 positions at head dim 128 with >= 8 kv heads,
+    else 8192 / head dim)."""
+    chunk = 128 if w["hd"] == 128 and w["KV"] >= 8 else 8192 // w["hd"]
     chunks = math.ceil((pos + 1) / chunk)
     partials = w["H"] * chunks * (w["hd"] + 2) * 4
     if stage == 5:  # K and V rows 0..pos of one layer, the queries in, the partials out
@@ -100,8 +109,11 @@ def cpu_baseline(archive, w, prompt_len, budget_s):
     sys.path.insert(0, str(ROOT / "oracle"))
     import oracle as orc
     cores = len(os.sched_getaffinity(0))
-    o = orc.Oracle(archive, arch=w["arch"], max_seq_len=prompt_len + 64, kv_f16=True, threads=cores)
+    o = orc.Oracle(archive, arch=w.get("oracle_arch", w["arch"]), max_seq_len=prompt_len + 64, kv_f16=True,
+                   threads=cores)
     try:
+        if w.get("hybrid"):
+            o.set_hybrid(True)  # (the recurrent states as zero: their cost does not depend on them)
         o.prefill_synthetic(prompt_len, seed=1)
         tok, n, t0 = 151643, 0, time.perf_counter()
         while n < 32 and (n == 0 or time.perf_counter() - t0 < budget_s):
@@ -275,7 +287,7 @@ def main():
 
     # per-stage mean launch time inside real decode steps
     stages, pos = {}, P + K
-    for st in STAGE_DESC:
+    for st in (HYBRID_STAGES if w.get("hybrid") else STAGE_DESC):
         avg_ms = e.time_stage_live(st, args.live_steps)
         mid = pos + (args.live_steps - 1) / 2.0
         per_step = 1 if st == 4 else w["L"]
@@ -289,6 +301,10 @@ def main():
             f"{avg_ms * per_step:6.3f} ms/step ({stages[st]['share']:.1%}); {nbytes / 1e6:9.3f} MB/launch "
             f"-> {nbytes / avg_ms / 1e6:7.1f} GB/s")
         pos += args.live_steps
+    if w.get("hybrid"):
+        rest = 1.0 - sum(v["share"] for v in stages.values())
+        log(f"  the token mixers (DeltaNet and gated attention layers with their projections) and the "
+            f"rest: {rest * ms_per_step:.3f} ms/step ({rest:.1%})")
     # batch-M verify: 8 drafts at positions pos..pos+7 as one block step (or 8 decode steps)
     verify = None
     drafts = np.random.default_rng(2).integers(0, w["V"], 8).astype(np.uint32)
@@ -312,7 +328,8 @@ def main():
                 "kernel": kernel, "stage": d["desc"], "bytes_per_launch": round(d["bytes"]),
                 "us_per_launch": round(d["us"], 3), "share_of_step": round(d["share"], 4)}
     stage_table = {str(s): {"desc": v["desc"], "us_per_launch": round(v["us"], 3), "launches_per_step": v["per_step"],
-                            "bytes_per_launch": round(v["bytes"]), "GBps": round(v["bytes"] / v["us"] / 1e3, 1)}
+                            "bytes_per_launch": round(v["bytes"]), "GBps": round(v["bytes"] / v["us"] / 1e3, 1),
+                            "traffic": traffic_for(args.workload, s)}
                    for s, v in stages.items()}
     e.close()
 
