@@ -1,6 +1,6 @@
 // block.hip -- the block step's GEMV: m <= kMaxBlock tokens at consecutive positions through
-// flat 4-bit tiles (gemvCellFlat, chpe_engine.zig:584-729), every weight read once for all of
-// them.  Used by the batch-M verify and by the chunked prefill; each token's arithmetic is the
+// flat 4- or 2-bit tiles (gemvCellFlat, chpe_engine.zig:584-729), every weight read once for all
+// of them.  Used by the batch-M verify and by the chunked prefill; each token's arithmetic is the
 // batch-1 step's (forwardDecode :1663-1803).
 //
 // 1. k_block_limbs: per token the GEMV input (RMS-normalised, (x * inv) * gamma, rmsNorm
@@ -12,12 +12,16 @@
 //      A (16 x 64): row 4 t + L = limb L of token t of the quad (one half of the group),
 //      B (64 x 16): column n = weight row n of the unit (the same half, codes as bytes),
 //    so lane (n, q) holds D(4 q + j, n): token q, limb j, row n -- the exact integer sum of
-//    code * limb over the group, starting at -8 * (the limb's sum) for the codes' offset.  The
+//    code * limb over the group, starting at -8 * (the limb's sum) for the codes' offset.  2-bit
+//    tiles: the codebook {0, +1, -2, -1} (:220) is the 2-bit two's complement, so the operand
+//    is code ^ 2 (0..3) and the sum starts at -2 * (the limb's sum); the tables then hold the
+//    columns in the 2-bit fields' order.  The
 //    lane combines its 4 limbs (2^(8 j)), scales by 2^(e - 30) and by the row's group scale,
 //    and accumulates row n of token q over the range's groups; the raw row sums of each range
 //    go to a partial-sum buffer.  The B layout reads only 64 bytes of each of 16 rows per load
 //    instruction, which the memory system serves at about half the rate of long runs, so the
-//    codes are loaded 512 contiguous bytes of a row at a time (a stage of 16 rows x 8 groups),
+//    codes are loaded 512 contiguous bytes of a row at a time (a stage of 16 rows x 8 groups;
+//    2-bit: x 16 groups, the whole range),
 //    passed through a wave-private LDS slot and read back in the B layout; the next stage's
 //    loads are in flight meanwhile.
 // 3. k_block_epi: per output row the ranges' sums in a fixed order, the flat-tile outlier
@@ -41,7 +45,8 @@ using namespace dev;
 // sums (ssp), read together with the columns; chunk 0 keeps it (the LM head's hidden norm).
 // Token slots >= m get zero tables.  A q/k/v launch (chk, as RopeArgs::brk_check) also makes
 // forwardDecode's break test (StepState::broken) on each token's input and records it in brk[token].
-template <bool kNorm>
+// BITS: the tiles' code width, which fixes the tables' column order and the codes' offset.
+template <bool kNorm, int BITS>
 __global__ void __launch_bounds__(128) k_block_limbs(const float* X, const float* gamma, float eps, uint32_t C,
                                                       uint32_t m, const float* ssp, uint32_t n_ssp, BlockTables t,
                                                       uint32_t* brk, uint32_t chk) {
@@ -101,8 +106,24 @@ __global__ void __launch_bounds__(128) k_block_limbs(const float* X, const float
 #pragma unroll
   for (int i = 0; i < 8; ++i) z[i] = (uint32_t(int(xv[i] * up)) + 0x808080u) ^ 0x808080u;
   uint32_t lo[4], hi[4];
-  limb_words(z[0], z[2], z[4], z[6], lo);
-  limb_words(z[1], z[3], z[5], z[7], hi);
+  if constexpr (BITS == 2) {
+    // threads 2k, 2k + 1 hold columns 0..7 and 8..15 of a 16-column block; the 2-bit fields'
+    // order wants {0,4,8,12}, {1,5,9,13} in the even thread and {2,6,10,14}, {3,7,11,15} in the
+    // odd one: each sends the four its neighbour needs
+    const bool odd = (lane & 1) != 0;
+    const uint32_t r0 = pair_u(odd ? z[0] : z[2], 1), r1 = pair_u(odd ? z[1] : z[3], 1);
+    const uint32_t r2 = pair_u(odd ? z[4] : z[6], 1), r3 = pair_u(odd ? z[5] : z[7], 1);
+    if (odd) {
+      limb_words(r0, r2, z[2], z[6], lo);
+      limb_words(r1, r3, z[3], z[7], hi);
+    } else {
+      limb_words(z[0], z[4], r0, r2, lo);
+      limb_words(z[1], z[5], r1, r3, hi);
+    }
+  } else {  // the nibbles' order {0,2,4,6}, {1,3,5,7}, {8,10,12,14}, {9,11,13,15}
+    limb_words(z[0], z[2], z[4], z[6], lo);
+    limb_words(z[1], z[3], z[5], z[7], hi);
+  }
   const uint32_t g = cc >> 7, c = cc & 127u, kq = c >> 5, h = (c >> 4) & 1u, p = (c >> 3) & 1u;
   uint2* tb2 = reinterpret_cast<uint2*>(t.tb);
   int sums[4];
@@ -118,7 +139,8 @@ __global__ void __launch_bounds__(128) k_block_limbs(const float* X, const float
     sums[L] = sl;
   }
   if (in && c == 0) {
-    t.ci[(size_t(T) * ng + g) * 4 + tl] = make_int4(-8 * sums[0], -8 * sums[1], -8 * sums[2], -8 * sums[3]);
+    constexpr int kOff = BITS == 2 ? -2 : -8;
+    t.ci[(size_t(T) * ng + g) * 4 + tl] = make_int4(kOff * sums[0], kOff * sums[1], kOff * sums[2], kOff * sums[3]);
     t.ew[(size_t(T) * ng + g) * 4 + tl] = isfinite(mx) ? ldexpf(1.0f, e - 30) : __int_as_float(0x7fc00000);
   }
   if (in && live) {
@@ -127,24 +149,31 @@ __global__ void __launch_bounds__(128) k_block_limbs(const float* X, const float
   }
 }
 
-// A stage: 16 weight rows x 8 groups of the range (8 KB of codes), loaded 512 contiguous bytes
-// of two rows per instruction (lane l: row 2 i + (l >> 5), group (l & 31) >> 2, quarter l & 3),
-// then written to the wave's LDS slot so that the matrix-core layout (lane (n, q): row n,
-// quarter q of a group) reads it back; rows at kStageRow bytes (16 B of padding: the 16 rows of
-// one read fall on distinct banks).
+// A stage: 16 weight rows x 512 bytes of codes of the range (8 KB): 8 groups of 4-bit codes
+// (64 B each) or 16 groups of 2-bit codes (32 B each, the whole 2048-column range), loaded 512
+// contiguous bytes of two rows per instruction (lane l: row 2 i + (l >> 5), bytes 16 (l & 31)
+// of the row's 512), then written to the wave's LDS slot so that the matrix-core layout (lane
+// (n, q): row n, quarter q of a group) reads it back; rows at kStageRow bytes (16 B of padding:
+// the 16 rows of one read fall on distinct banks).
 constexpr uint32_t kStageRow = 528, kStageBytes = 16 * kStageRow;
+template <int BITS>
 struct MtStage {
-  uint4 v[8];      // codes, in the load layout above
-  uint32_t sc[2];  // group scales: lane l, row 8 i + (l >> 3), group l & 7
+  static constexpr int kScales = BITS == 2 ? 4 : 2;
+  uint4 v[8];            // codes, in the load layout above
+  uint32_t sc[kScales];  // group scales: 4-bit lane l, row 8 i + (l >> 3), group l & 7;
+                         //   2-bit lane l, row 4 i + (l >> 4), group l & 15
 };
 
-template <int NQ, int NW>
+template <int NQ, int NW, int BITS>
 __global__ void __launch_bounds__(kWave * NW) k_gemv_mt(BlockGemvArgs a) {
+  constexpr uint32_t GPS = BITS == 2 ? 16 : 8;   // groups per stage
+  constexpr uint32_t SPU = BITS == 2 ? 1 : 2;    // stages per unit
+  constexpr uint32_t GB = BITS == 2 ? 32 : 64;   // code bytes per group and row
   __shared__ __align__(16) uint4 s_tb[NQ][16][128];
   __shared__ __align__(16) int4 s_ci[NQ][16][4];
   __shared__ float s_ew[NQ][16][4];
   __shared__ __align__(16) uint8_t s_w[NW][kStageBytes];
-  __shared__ uint16_t s_sc[NW][16][8];
+  __shared__ uint16_t s_sc[NW][16][GPS];
   const int lane = threadIdx.x & 63, n = lane & 15, q = lane >> 4;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const uint32_t C = a.g.C, ng = C >> 7, range = blockIdx.x, g0 = range * 16;
@@ -152,7 +181,7 @@ __global__ void __launch_bounds__(kWave * NW) k_gemv_mt(BlockGemvArgs a) {
   const uint32_t n_units = a.n_units, waves_total = gridDim.y * NW;
   const uint32_t wid = blockIdx.y * NW + wave;
   const bool active = wid < n_units;
-  const uint32_t n_stages = active ? 2 * ((n_units - wid + waves_total - 1) / waves_total) : 0u;
+  const uint32_t n_stages = active ? SPU * ((n_units - wid + waves_total - 1) / waves_total) : 0u;
   uint8_t* slot = s_w[wave];
   // the unit's part: parts hold consecutive unit ranges from part[p].unit_begin
   auto part_index = [&](uint32_t u) {
@@ -161,54 +190,68 @@ __global__ void __launch_bounds__(kWave * NW) k_gemv_mt(BlockGemvArgs a) {
     for (int k = 1; k < kMaxParts; ++k) p += (k < a.g.n_parts && u >= a.g.part[k].unit_begin) ? 1 : 0;
     return p;
   };
-  // stage j of this wave: unit wid + (j >> 1) * waves_total, groups 8 (j & 1) .. + 7 of the range
-  // (a stage past the last repeats the last: its lines are cached)
-  auto issue = [&](uint32_t j, MtStage* st) {
+  // stage j of this wave: unit wid + (j / SPU) * waves_total, groups GPS (j % SPU) .. + GPS - 1
+  // of the range (a stage past the last repeats the last: its lines are cached)
+  auto issue = [&](uint32_t j, MtStage<BITS>* st) {
     j = j < n_stages ? j : n_stages - 1;
-    const uint32_t u = wid + (j >> 1) * waves_total, h = j & 1u;
+    const uint32_t u = wid + (j / SPU) * waves_total, h = j % SPU;
     const int p = int(__builtin_amdgcn_readfirstlane(part_index(u)));
     const GemvPart& P = a.g.part[p];
     const uint8_t* base = P.base;
     const uint32_t stride = P.stride, wr = P.wrows, r0 = (u - P.unit_begin) * kBlockUnit;
-    const uint32_t gl = 8 * h + ((uint32_t(lane) & 31u) >> 2), gc = gl < ngr ? gl : 0u;
+    const uint32_t lb = 16 * (uint32_t(lane) & 31u);  // the lane's bytes in the row's 512
+    const uint32_t gl = GPS * h + lb / GB, gc = gl < ngr ? gl : 0u;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const uint32_t r = r0 + 2 * uint32_t(i) + (uint32_t(lane) >> 5), rr = r < wr ? r : 0u;
       const uint32_t G = rr * ng + g0 + gc;
-      st->v[i] = ld_u128(base + ((G >> 8) * stride + 64 + (G & 255u) * 64 + 16 * (uint32_t(lane) & 3u)));
+      st->v[i] = ld_u128(base + ((G >> 8) * stride + 64 + (G & 255u) * GB + lb % GB));
     }
+    constexpr int kRowsPer = 64 / int(GPS);  // rows per scale load: 8 (4-bit), 4 (2-bit)
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const uint32_t r = r0 + 8 * uint32_t(i) + (uint32_t(lane) >> 3), rr = r < wr ? r : 0u;
-      const uint32_t g = 8 * h + (uint32_t(lane) & 7u), G = rr * ng + g0 + (g < ngr ? g : 0u);
+    for (int i = 0; i < MtStage<BITS>::kScales; ++i) {
+      const uint32_t r = r0 + uint32_t(kRowsPer * i) + uint32_t(lane) / GPS, rr = r < wr ? r : 0u;
+      const uint32_t g = GPS * h + (uint32_t(lane) % GPS), G = rr * ng + g0 + (g < ngr ? g : 0u);
       st->sc[i] = ld_u16(base + ((G >> 8) * stride + 16448 + 48 + 2 * (G & 255u)));
     }
   };
   // into the wave's slot (LDS operations of one wave complete in order: the previous stage's
   // reads are done before these writes land)
-  auto stage = [&](const MtStage& st) {
+  auto stage = [&](const MtStage<BITS>& st) {
 #pragma unroll
     for (int i = 0; i < 8; ++i)
       *reinterpret_cast<uint4*>(slot + (2 * i + (lane >> 5)) * kStageRow + 16 * (lane & 31)) = st.v[i];
+    constexpr int kRowsPer = 64 / int(GPS);
 #pragma unroll
-    for (int i = 0; i < 2; ++i) s_sc[wave][8 * i + (lane >> 3)][lane & 7] = uint16_t(st.sc[i]);
+    for (int i = 0; i < MtStage<BITS>::kScales; ++i)
+      s_sc[wave][kRowsPer * i + lane / int(GPS)][lane % int(GPS)] = uint16_t(st.sc[i]);
   };
   float acc[NQ];
 #pragma unroll
   for (int T = 0; T < NQ; ++T) acc[T] = 0.0f;
   auto compute = [&](uint32_t j) {
-    const uint32_t h = j & 1u;
+    const uint32_t h = j % SPU;
 #pragma unroll 4
-    for (int k = 0; k < 8; ++k) {
-      const uint32_t gl = 8 * h + uint32_t(k);
+    for (int k = 0; k < int(GPS); ++k) {
+      const uint32_t gl = GPS * h + uint32_t(k);
       const bool gv = gl < ngr;
       const uint32_t gk = gv ? gl : 0u;
-      const uint4 w = *reinterpret_cast<const uint4*>(slot + n * kStageRow + 64 * k + 16 * q);
       const float sc = gv ? h2f(s_sc[wave][n][k]) : 0.0f;
-      const i32x4_t B0 = {int(w.x & 0x0f0f0f0fu), int((w.x >> 4) & 0x0f0f0f0fu), int(w.y & 0x0f0f0f0fu),
-                          int((w.y >> 4) & 0x0f0f0f0fu)};
-      const i32x4_t B1 = {int(w.z & 0x0f0f0f0fu), int((w.z >> 4) & 0x0f0f0f0fu), int(w.w & 0x0f0f0f0fu),
-                          int((w.w >> 4) & 0x0f0f0f0fu)};
+      i32x4_t B0, B1;
+      if constexpr (BITS == 2) {  // 16 codes in 4 bytes: field f of each byte, code ^ 2
+        const uint2 w2 = *reinterpret_cast<const uint2*>(slot + n * kStageRow + 32 * k + 8 * q);
+        const uint32_t x = w2.x ^ 0xAAAAAAAAu, y = w2.y ^ 0xAAAAAAAAu;
+        B0 = i32x4_t{int(x & 0x03030303u), int((x >> 2) & 0x03030303u), int((x >> 4) & 0x03030303u),
+                     int((x >> 6) & 0x03030303u)};
+        B1 = i32x4_t{int(y & 0x03030303u), int((y >> 2) & 0x03030303u), int((y >> 4) & 0x03030303u),
+                     int((y >> 6) & 0x03030303u)};
+      } else {
+        const uint4 w = *reinterpret_cast<const uint4*>(slot + n * kStageRow + 64 * k + 16 * q);
+        B0 = i32x4_t{int(w.x & 0x0f0f0f0fu), int((w.x >> 4) & 0x0f0f0f0fu), int(w.y & 0x0f0f0f0fu),
+                     int((w.y >> 4) & 0x0f0f0f0fu)};
+        B1 = i32x4_t{int(w.z & 0x0f0f0f0fu), int((w.z >> 4) & 0x0f0f0f0fu), int(w.w & 0x0f0f0f0fu),
+                     int((w.w >> 4) & 0x0f0f0f0fu)};
+      }
 #pragma unroll
       for (int T = 0; T < NQ; ++T) {
         const uint4 t0 = s_tb[T][gk][(uint32_t(q) * 2) * 16 + uint32_t(n)];
@@ -223,8 +266,8 @@ __global__ void __launch_bounds__(kWave * NW) k_gemv_mt(BlockGemvArgs a) {
         acc[T] += gv ? f * s_ew[T][gk][q] * sc : 0.0f;
       }
     }
-    if (h == 1u) {  // the unit's second stage: row n of tokens 4 T + q
-      const uint32_t u = wid + (j >> 1) * waves_total;
+    if (h == SPU - 1) {  // the unit's last stage: row n of tokens 4 T + q
+      const uint32_t u = wid + (j / SPU) * waves_total;
       const int p = int(__builtin_amdgcn_readfirstlane(part_index(u)));
       const GemvPart& P = a.g.part[p];
       const uint32_t r = (u - P.unit_begin) * kBlockUnit + uint32_t(n), at = P.unit_begin * kBlockUnit + r;
@@ -238,7 +281,7 @@ __global__ void __launch_bounds__(kWave * NW) k_gemv_mt(BlockGemvArgs a) {
   };
   // the first stage's loads are in flight while the range's operand tables are staged, the next
   // stage's while the current stage is staged and multiplied
-  MtStage SA, SB;
+  MtStage<BITS> SA, SB;
   if (active) issue(0, &SA);
   for (uint32_t i = threadIdx.x; i < uint32_t(NQ) * 16 * 128; i += kWave * NW) {
     const uint32_t T = i >> 11, gl = (i >> 7) & 15u, e = i & 127u;
@@ -532,12 +575,11 @@ __global__ void __launch_bounds__(256) k_block_finish(BlockFinishArgs a) {
 void launch_block_limbs(const BlockGemvArgs& a, hipStream_t st) {
   const dim3 grid((a.g.C + 1023) / 1024, 4 * a.nq);
   const uint32_t chk = GemvMode(a.g.mode) == GemvMode::QkvRope ? a.g.rope.brk_check : 0u;
-  if (a.g.gamma)
-    launch_kernel(&k_block_limbs<true>, grid, dim3(128), st, a.g.x, a.g.gamma, a.g.eps, a.g.C, a.m, a.ssp, a.n_ssp, a.t,
-                  a.brk, chk);
-  else
-    launch_kernel(&k_block_limbs<false>, grid, dim3(128), st, a.g.x, a.g.gamma, a.g.eps, a.g.C, a.m, a.ssp, a.n_ssp, a.t,
-                  a.brk, 0u);
+  auto go = [&](auto kern, uint32_t c) {
+    launch_kernel(kern, grid, dim3(128), st, a.g.x, a.g.gamma, a.g.eps, a.g.C, a.m, a.ssp, a.n_ssp, a.t, a.brk, c);
+  };
+  if (a.bits == 2) a.g.gamma ? go(&k_block_limbs<true, 2>, chk) : go(&k_block_limbs<false, 2>, 0u);
+  else a.g.gamma ? go(&k_block_limbs<true, 4>, chk) : go(&k_block_limbs<false, 4>, 0u);
 }
 
 uint32_t launch_block_gemv(BlockGemvArgs& a, hipStream_t st) {
@@ -549,8 +591,13 @@ uint32_t launch_block_gemv(BlockGemvArgs& a, hipStream_t st) {
   const uint32_t need = (a.n_units + 7) / 8;  // (a wave per unit at least)
   if (per > need) per = need;
   const dim3 grid(ranges, per);
-  if (a.nq <= 1) launch_kernel(&k_gemv_mt<1, 8>, grid, dim3(512), st, a);
-  else launch_kernel(&k_gemv_mt<2, 8>, grid, dim3(512), st, a);
+  if (a.bits == 2) {
+    if (a.nq <= 1) launch_kernel(&k_gemv_mt<1, 8, 2>, grid, dim3(512), st, a);
+    else launch_kernel(&k_gemv_mt<2, 8, 2>, grid, dim3(512), st, a);
+  } else {
+    if (a.nq <= 1) launch_kernel(&k_gemv_mt<1, 8, 4>, grid, dim3(512), st, a);
+    else launch_kernel(&k_gemv_mt<2, 8, 4>, grid, dim3(512), st, a);
+  }
   uint32_t outs = 0;
   if (GemvMode(a.g.mode) == GemvMode::QkvRope) {
     for (int p = 0; p < a.g.n_parts; ++p) outs += a.g.part[p].rows / 2;

@@ -283,7 +283,7 @@ bool Engine::init(const uint8_t* b, size_t len, const EngineConfig& cfg, std::st
   HIP_TRY(hipHostMalloc(reinterpret_cast<void**>(&h_state_), sizeof(StepState), hipHostMallocDefault));
   HIP_TRY(hipHostMalloc(reinterpret_cast<void**>(&h_result_), sizeof(StepResult), hipHostMallocDefault));
   if (cfg.hybrid && !plan_hybrid(err)) return false;
-  {  // the block step for archives whose projections are all flat 4-bit tiles (CHPE_BLOCK=0: off;
+  {  // the block step for archives whose projections are all flat 4-/2-bit tiles (CHPE_BLOCK=0: off;
      // the hybrid model: verify and prefill as decode steps, the recurrent state advances per token)
     const char* bk = std::getenv("CHPE_BLOCK");
     std::string why;
@@ -984,14 +984,16 @@ int Engine::verify(const uint32_t* drafts, size_t m, size_t pos, uint32_t* out_a
 
 // ---- the block step ---------------------------------------------------------------------------
 // Returns false with *err empty when the archive has no block step (a projection that is not
-// flat 4-bit tiles), false with *err set on an allocation failure.
+// flat 4- or 2-bit tiles), false with *err set on an allocation failure.
 bool Engine::plan_block(std::string* err) {
   block_ok_ = false;
   const size_t D = arch_.hidden_dim, I = arch_.intermediate_dim, V = arch_.vocab_size;
   const size_t qd = arch_.num_attn_heads * arch_.head_dim, kvd = arch_.num_kv_heads * arch_.head_dim;
-  auto flat = [](const ProjPlan& p) { return p.kind == WeightKind::FlatW4; };
+  // flat 4- or 2-bit tiles, one code width per launch (the q/k/v parts, gate and up alike)
+  auto flat = [](const ProjPlan& p) { return p.kind == WeightKind::FlatW4 || p.kind == WeightKind::FlatW2; };
   for (const LayerPlan& L : layers_)
-    if (!flat(L.q) || !flat(L.k) || !flat(L.v) || !flat(L.o) || !flat(L.gate) || !flat(L.up) || !flat(L.down))
+    if (!flat(L.q) || !flat(L.k) || !flat(L.v) || !flat(L.o) || !flat(L.gate) || !flat(L.up) || !flat(L.down) ||
+        L.k.kind != L.q.kind || L.v.kind != L.q.kind || L.up.kind != L.gate.kind)
       return false;
   // (the o projection reads the attention output of qd columns as hidden_dim columns, as the
   // reference's gemvLinear call does, :1737: the two must agree)
@@ -1071,6 +1073,7 @@ uint32_t Engine::enqueue_block_gemv(const ProjPlan* const* parts, float* const* 
     units += (p.rows + kBlockUnit - 1) / kBlockUnit;
   }
   b.t = btab_;
+  b.bits = parts[0]->kind == WeightKind::FlatW2 ? 2u : 4u;
   b.m = m;
   b.nq = (m + 3) / 4;
   b.n_units = units;

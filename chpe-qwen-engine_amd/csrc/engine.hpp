@@ -140,7 +140,7 @@ class Engine {
   // positions are overwritten); out_argmax[i] = argmax after draft i
   int verify(const uint32_t* drafts, size_t m, size_t pos, uint32_t* out_argmax, ForwardResult* last);
   // the block step: tokens[0..m), m <= kMaxBlock, at positions pos..pos+m-1 through every layer
-  // with each weight read once for all m tokens (flat 4-bit archives: block_ready()), each
+  // with each weight read once for all m tokens (flat 4-/2-bit archives: block_ready()), each
   // token's arithmetic that of forwardDecode; KV rows pos..pos+m-1 are written;
   // out_argmax[i] = argmax after token i; the last token's logits become copy_logits()'s and
   // its result *last.  The decode state is not touched.  0, -1 bad arguments or no block step

@@ -261,7 +261,7 @@ size_t flat_poly_part_floats(uint32_t n_tiles, uint32_t C);
 uint32_t launch_gemv_flat_poly(const GemvArgs& a, const uint32_t* n_tiles, float* xn, const PolyRaw& raw,
                                float* part, hipStream_t stream);
 
-// ---- the block step: m <= kMaxBlock tokens at consecutive positions through flat 4-bit tiles,
+// ---- the block step: m <= kMaxBlock tokens at consecutive positions through flat 4- or 2-bit tiles,
 // every weight read once for all m tokens (batch-M verify, chunked prefill) ----------------------
 constexpr uint32_t kMaxBlock = 8;
 constexpr uint32_t kBlockRange = 2048;  // input columns per workgroup of the block GEMV
@@ -275,7 +275,7 @@ constexpr uint32_t kMaxSsPartials = 4096;  // Σx² partials a block kernel may 
 struct BlockTables {
   uint4* tb;   // [nq][ng][4 kq][2 h][16]: entry lane 4t + L = limb L of token 4T + t, the 16
                //   columns 32 kq + 16 h .. of the group in the operand byte order
-  int4* ci;    // [nq][ng][4]: -8 * the group's limb sums (limbs 0..3) of token 4T + t
+  int4* ci;    // [nq][ng][4]: -8 (4-bit) / -2 (2-bit) * the group's limb sums (limbs 0..3) of token 4T + t
   float* ew;   // [nq][ng][4]: 2^(e - 30) of token 4T + t in the group
   float* xt;   // [C][kMaxBlock]: the (normalised) input, token-minor (for the outlier corrections)
   float* ss;   // [kMaxBlock]: each token's sum of squares of the raw input (norm GEMVs)
@@ -300,6 +300,7 @@ struct BlockGemvArgs {
   ArgmaxPartial* partials;  // Logits: [kMaxBlock][epi_blocks]
   uint32_t epi_blocks;      // set by launch_block_gemv
   uint32_t* brk;            // [kMaxBlock]: token t broke (StepState::broken), cleared by the block's embedding
+  uint32_t bits;            // the parts' code width: 4 or 2 (flat tiles)
 };
 
 struct BlockFinishArgs {

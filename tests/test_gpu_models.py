@@ -143,7 +143,7 @@ def top2_gap(lg):
     return float(t[-1] - t[-2])
 
 
-def run_block(path, arch, vocab, seed, oracle_check):
+def run_block(path, arch, vocab, seed, oracle_check, block=True):
     """The block step (every weight read once for up to 8 tokens; no reference code, defined as
     the decode steps it replaces) against the decode step on the same engine: chpe_prefill vs
     chpe_forward_tokens (the last position's logits, then one decode step on each cache, so the
@@ -153,7 +153,8 @@ def run_block(path, arch, vocab, seed, oracle_check):
     so k / v elements near an fp16 rounding boundary round differently, and here 19 cached
     positions (not 3) carry such flips through 80 layers.  An argmax may differ only where the
     decode step's top-2 gap is below twice the bar.  oracle_check: the prefill's logits against
-    the oracle's forward as well."""
+    the oracle's forward as well; block: whether the archive runs the block step (flat 4- and
+    2-bit tiles do)."""
     rng = np.random.default_rng(seed)
     prompt = rng.integers(0, vocab, 11).astype(np.uint32)
     drafts = rng.integers(0, vocab, 8).astype(np.uint32)
@@ -161,7 +162,8 @@ def run_block(path, arch, vocab, seed, oracle_check):
     for kv16, rel in ((False, 2e-4), (True, 3e-3)):
         e = ca.Engine(path, arch=arch, max_seq_len=64, kv_f16=kv16)
         try:
-            if not e.block_ready():  # 2-bit tiles: prefill and verify are the decode steps, bit for bit
+            assert e.block_ready() == block
+            if not e.block_ready():  # no block step: prefill and verify are the decode steps, bit for bit
                 _, lseq = e.forward_tokens(prompt, want_logits=True)
                 _, lblk = e.prefill(prompt, want_logits=True)
                 assert np.array_equal(lseq.view(np.uint32), lblk.view(np.uint32))
