@@ -305,20 +305,22 @@ def main():
         rest = 1.0 - sum(v["share"] for v in stages.values())
         log(f"  the token mixers (DeltaNet and gated attention layers with their projections) and the "
             f"rest: {rest * ms_per_step:.3f} ms/step ({rest:.1%})")
-    # batch-M verify: 8 drafts at positions pos..pos+7 as one block step (or 8 decode steps)
-    verify = None
+    # batch-M verify: 8 (then 4) drafts at positions pos.. as one block step (or M decode steps)
     drafts = np.random.default_rng(2).integers(0, w["V"], 8).astype(np.uint32)
-    e.verify(drafts, pos)
-    device_sync()
-    reps = 5
-    t = time.perf_counter()
-    for _ in range(reps):
-        e.verify(drafts, pos)
-    vt = (time.perf_counter() - t) / reps
-    verify = {"m": 8, "ms_per_call": round(vt * 1e3, 3), "positions_per_s": round(8 / vt, 2),
-              "vs_batch1_tok_s": round(8 / vt / value, 3), "block_step": bool(block), "position": int(pos)}
-    log(f"verify: 8 drafts at positions {pos}..{pos + 7} in {vt * 1e3:.2f} ms -> {8 / vt:.1f} positions/s "
-        f"({8 / vt / value:.2f}x the batch-1 decode rate; {'one block step' if block else '8 decode steps'})")
+    verify, by_m = None, {}
+    for m in (8, 4):
+        e.verify(drafts[:m], pos)
+        device_sync()
+        reps = 5
+        t = time.perf_counter()
+        for _ in range(reps):
+            e.verify(drafts[:m], pos)
+        vt = (time.perf_counter() - t) / reps
+        by_m[m] = {"m": m, "ms_per_call": round(vt * 1e3, 3), "positions_per_s": round(m / vt, 2),
+                   "vs_batch1_tok_s": round(m / vt / value, 3), "block_step": bool(block), "position": int(pos)}
+        log(f"verify: {m} drafts at positions {pos}..{pos + m - 1} in {vt * 1e3:.2f} ms -> {m / vt:.1f} positions/s "
+            f"({m / vt / value:.2f}x the batch-1 decode rate; {'one block step' if block else f'{m} decode steps'})")
+    verify = dict(by_m[8], m4=by_m[4])
     dom = max(stages, key=lambda s: stages[s]["us"] * stages[s]["per_step"])
     d = stages[dom]
     kernel = e.stage_kernel(dom)

@@ -432,12 +432,12 @@ __global__ void __launch_bounds__(256) k_block_epi(BlockGemvArgs a) {
       const float hi = v[1] + (P0.bias ? P0.bias[r + half] : 0.0f);
       const uint32_t pos = pos0 + t, d = r % (2 * half);
       float o0 = lo, o1 = hi;
-      if (P0.rope_role != kRoleV && pos < a.rope_rows) {  // applyRope :195-216
+      if (P0.rope_role < kRoleV && pos < a.rope_rows) {  // applyRope :195-216
         const float c = a.rope_cos[size_t(pos) * half + d], sn = a.rope_sin[size_t(pos) * half + d];
         o0 = lo * c - hi * sn;
         o1 = lo * sn + hi * c;
       }
-      if (P0.rope_role == kRoleQ) {
+      if (P0.rope_role == kRoleQ || P0.rope_role == kRoleStore) {  // (Store: as computed)
         y[r] = o0;
         y[r + half] = o1;
       } else if (!brk) {

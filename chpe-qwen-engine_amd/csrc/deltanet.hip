@@ -12,6 +12,11 @@
 // of the head's 128x128 f32 state is read once and written once (the columns of the update are
 // independent; 32 heads x 8 blocks = 256 workgroups at the 9B shape); k_dn_gnorm: the gated
 // RMSNorm of each head's output.  Memory-bound: 2 x 64 KiB of state per head and step.
+//
+// The block step (m <= kMaxBlock tokens in order, the speculative verify and the prefill):
+// k_dn_conv_block, k_dn_step_block and k_dn_gnorm_block run the same arithmetic token after
+// token inside one launch, each state read once and written once for the m tokens (the conv
+// state in registers per channel, a head's state slab in registers per workgroup).
 #include "device_common.hpp"
 #include "kernels.hpp"
 
@@ -155,7 +160,159 @@ __global__ void __launch_bounds__(D) k_dn_gnorm(DnStepArgs a) {
   a.out[size_t(h) * D + j] = w * (o * rr) * silu_f(z);
 }
 
+// ---- the block step: m tokens in order, each state read and written once ----------------------
+__global__ void __launch_bounds__(256) k_dn_conv_block(DnBlockArgs a) {
+  const uint32_t c = blockIdx.x * 256 + threadIdx.x;
+  if (c >= a.channels) return;
+  const uint32_t T = a.taps;
+  const float* w = a.w + size_t(c) * T;
+  float* st = a.conv_state + size_t(c) * (T - 1);
+  float wv[kDnMaxTaps], sv[kDnMaxTaps];
+#pragma unroll
+  for (uint32_t k = 0; k < kDnMaxTaps; ++k) {
+    wv[k] = k + 1 < T ? w[k] : 0.0f;
+    sv[k] = k + 1 < T ? st[k] : 0.0f;
+  }
+  const float wl = w[T - 1];
+  for (uint32_t t = 0; t < a.m; ++t) {
+    const float x = a.x[size_t(t) * a.x_stride + c];
+    float acc = 0.0f;  // oldest tap first, the new input last (k_dn_conv)
+#pragma unroll
+    for (uint32_t k = 0; k < kDnMaxTaps; ++k)
+      if (k + 1 < T) acc += wv[k] * sv[k];
+    acc += wl * x;
+    a.conv_out[size_t(t) * a.channels + c] = silu_f(acc);
+    if (a.brk[t]) continue;  // (token t broke before this layer: its shift is skipped)
+#pragma unroll
+    for (uint32_t k = 0; k + 1 < kDnMaxTaps; ++k)
+      if (k + 2 < T) sv[k] = sv[k + 1];
+    sv[T - 2] = x;
+  }
+#pragma unroll
+  for (uint32_t k = 0; k + 1 < kDnMaxTaps; ++k)
+    if (k + 1 < T) st[k] = sv[k];
+}
+
+// k_dn_step's workgroup (value head, 16-column block) over the m tokens: the slab stays in
+// registers from the first token's read to the last token's write; per token the same steps as
+// k_dn_step (l2-normalised q and k, decay, kv_mem, delta, the update, o), a token that broke
+// before this layer leaving the slab as it is.
+template <int D, int CW>
+__global__ void __launch_bounds__(256) k_dn_step_block(DnBlockArgs a) {
+  constexpr int NT = 256, RB = NT / CW, RPB = D / RB, NWV = NT / 64;
+  static_assert(CW == 16 && NT % CW == 0 && D % RB == 0 && D % 64 == 0, "lanes 16 / 32 apart share a column");
+  const uint32_t h = blockIdx.x, c0 = blockIdx.y * CW, kh = h / (a.n_v_heads / a.n_k_heads);
+  const int t = threadIdx.x, j = t % CW, rb = t / CW, lane = t & 63, wave = t >> 6;
+  __shared__ float s_qn[D], s_kn[D];
+  __shared__ float s_part[NWV][CW];
+  float* S = a.state + size_t(h) * D * D + c0 + j;
+  float sr[RPB];
+#pragma unroll
+  for (int r = 0; r < RPB; ++r) sr[r] = S[size_t(rb * RPB + r) * D];
+  constexpr int PL = D / 64;
+  const float scale = 1.0f / sqrtf(float(D));
+  const uint32_t nk = a.n_k_heads * D;  // q: [0, nk), k: [nk, 2 nk), v: [2 nk, ..) of a token's channels
+  const float A = expf(a.A_log[h]), dtb = a.dt_bias[h];
+
+  auto column_sum = [&](float p) {
+    p = pair_sum(p, 16);
+    p = pair_sum(p, 32);
+    if (lane < CW) s_part[wave][lane] = p;
+    __syncthreads();
+    float v = 0.0f;
+#pragma unroll
+    for (int w = 0; w < NWV; ++w) v += s_part[w][j];
+    __syncthreads();
+    return v;
+  };
+
+  for (uint32_t tk = 0; tk < a.m; ++tk) {
+    const float* xc = a.conv_out + size_t(tk) * a.channels;
+    float qv[PL], kv[PL];
+#pragma unroll
+    for (int m = 0; m < PL; ++m) {
+      qv[m] = xc[size_t(kh) * D + lane + 64 * m];
+      kv[m] = xc[nk + size_t(kh) * D + lane + 64 * m];
+    }
+    const float vj = xc[2 * nk + size_t(h) * D + c0 + j];
+    const float bt = a.b[size_t(tk) * a.ab_stride + h], at = a.a[size_t(tk) * a.ab_stride + h];
+    const float beta = 1.0f / (1.0f + expf(-bt));
+    const float decay = expf(-A * softplus_f(at + dtb));
+    float q2 = 0.0f, k2 = 0.0f;
+#pragma unroll
+    for (int m = 0; m < PL; ++m) {
+      q2 += qv[m] * qv[m];
+      k2 += kv[m] * kv[m];
+    }
+    q2 = wave_sum(q2);
+    k2 = wave_sum(k2);
+    const float qi = 1.0f / sqrtf(q2 + 1e-6f), ki = 1.0f / sqrtf(k2 + 1e-6f);
+    __syncthreads();  // the previous token's reads of s_qn / s_kn are done
+    if (wave == 0) {
+#pragma unroll
+      for (int m = 0; m < PL; ++m) {
+        s_qn[lane + 64 * m] = qv[m] * qi * scale;
+        s_kn[lane + 64 * m] = kv[m] * ki;
+      }
+    }
+    __syncthreads();
+    if (a.brk[tk]) {  // (uniform: the token's slab update is skipped, its output is not used)
+      if (t < CW) a.out[size_t(tk) * a.out_stride + size_t(h) * D + c0 + j] = 0.0f;
+      continue;
+    }
+    float p = 0.0f;
+#pragma unroll
+    for (int r = 0; r < RPB; ++r) {
+      sr[r] *= decay;
+      p += sr[r] * s_kn[rb * RPB + r];
+    }
+    const float kvm = column_sum(p);
+    const float delta = (vj - kvm) * beta;
+    float o = 0.0f;
+#pragma unroll
+    for (int r = 0; r < RPB; ++r) {
+      sr[r] += s_kn[rb * RPB + r] * delta;
+      o += sr[r] * s_qn[rb * RPB + r];
+    }
+    o = column_sum(o);
+    if (t < CW) a.out[size_t(tk) * a.out_stride + size_t(h) * D + c0 + j] = o;
+  }
+#pragma unroll
+  for (int r = 0; r < RPB; ++r) S[size_t(rb * RPB + r) * D] = sr[r];
+}
+
+// k_dn_gnorm for token blockIdx.y
+template <int D>
+__global__ void __launch_bounds__(D) k_dn_gnorm_block(DnBlockArgs a) {
+  const uint32_t h = blockIdx.x, tk = blockIdx.y;
+  const int j = threadIdx.x, lane = j & 63, wave = j >> 6;
+  __shared__ float s_red[D / 64];
+  float* out = a.out + size_t(tk) * a.out_stride;
+  const float* zt = a.z + size_t(tk) * a.z_stride;
+  const float o = out[size_t(h) * D + j], z = zt[size_t(h) * D + j], w = a.norm_w[j];
+  const float s2 = wave_sum(o * o);
+  if (lane == 0) s_red[wave] = s2;
+  __syncthreads();
+  float tot = 0.0f;
+#pragma unroll
+  for (int k = 0; k < D / 64; ++k) tot += s_red[k];
+  const float rr = 1.0f / sqrtf(tot / float(D) + a.eps);
+  out[size_t(h) * D + j] = w * (o * rr) * silu_f(z);
+}
+
 }  // namespace
+
+void launch_dn_block(const DnBlockArgs& a, hipStream_t st) {
+  constexpr uint32_t CW = 16;
+  launch_kernel(&k_dn_conv_block, dim3((a.channels + 255) / 256), dim3(256), st, a);
+  if (a.head_dim == 128) {
+    launch_kernel(&k_dn_step_block<128, CW>, dim3(a.n_v_heads, 128 / CW), dim3(256), st, a);
+    launch_kernel(&k_dn_gnorm_block<128>, dim3(a.n_v_heads, a.m), dim3(128), st, a);
+  } else {
+    launch_kernel(&k_dn_step_block<64, CW>, dim3(a.n_v_heads, 64 / CW), dim3(256), st, a);
+    launch_kernel(&k_dn_gnorm_block<64>, dim3(a.n_v_heads, a.m), dim3(64), st, a);
+  }
+}
 
 bool deltanet_supported(uint32_t n_v_heads, uint32_t n_k_heads, uint32_t head_dim, uint32_t taps) {
   return n_k_heads > 0 && n_v_heads % n_k_heads == 0 && (head_dim == 64 || head_dim == 128) && taps >= 2 &&

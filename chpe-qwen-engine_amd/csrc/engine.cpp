@@ -283,11 +283,10 @@ bool Engine::init(const uint8_t* b, size_t len, const EngineConfig& cfg, std::st
   HIP_TRY(hipHostMalloc(reinterpret_cast<void**>(&h_state_), sizeof(StepState), hipHostMallocDefault));
   HIP_TRY(hipHostMalloc(reinterpret_cast<void**>(&h_result_), sizeof(StepResult), hipHostMallocDefault));
   if (cfg.hybrid && !plan_hybrid(err)) return false;
-  {  // the block step for archives whose projections are all flat 4-/2-bit tiles (CHPE_BLOCK=0: off;
-     // the hybrid model: verify and prefill as decode steps, the recurrent state advances per token)
+  {  // the block step for archives whose projections are all flat 4-/2-bit tiles (CHPE_BLOCK=0: off)
     const char* bk = std::getenv("CHPE_BLOCK");
     std::string why;
-    if (!cfg.hybrid && !(bk && bk[0] == '0') && !plan_block(&why) && !why.empty()) {
+    if (!(bk && bk[0] == '0') && !plan_block(&why) && !why.empty()) {
       *err = "block step: " + why;
       return false;
     }
@@ -991,10 +990,19 @@ bool Engine::plan_block(std::string* err) {
   const size_t qd = arch_.num_attn_heads * arch_.head_dim, kvd = arch_.num_kv_heads * arch_.head_dim;
   // flat 4- or 2-bit tiles, one code width per launch (the q/k/v parts, gate and up alike)
   auto flat = [](const ProjPlan& p) { return p.kind == WeightKind::FlatW4 || p.kind == WeightKind::FlatW2; };
-  for (const LayerPlan& L : layers_)
-    if (!flat(L.q) || !flat(L.k) || !flat(L.v) || !flat(L.o) || !flat(L.gate) || !flat(L.up) || !flat(L.down) ||
-        L.k.kind != L.q.kind || L.v.kind != L.q.kind || L.up.kind != L.gate.kind)
+  for (size_t l = 0; l < layers_.size(); ++l) {
+    const LayerPlan& L = layers_[l];
+    if (!flat(L.gate) || !flat(L.up) || !flat(L.down) || L.up.kind != L.gate.kind) return false;
+    if (cfg_.hybrid) {  // the hybrid's mixers (HybLayer) instead of the q/k/v/o plans
+      const HybLayer& H = hyb_[l];
+      if (!flat(H.in0) || !flat(H.in1) || !flat(H.in2) || !flat(H.out) || H.in1.kind != H.in0.kind ||
+          H.in2.kind != H.in0.kind || (!H.full && !flat(H.in3)))
+        return false;
+      continue;
+    }
+    if (!flat(L.q) || !flat(L.k) || !flat(L.v) || !flat(L.o) || L.k.kind != L.q.kind || L.v.kind != L.q.kind)
       return false;
+  }
   // (the o projection reads the attention output of qd columns as hidden_dim columns, as the
   // reference's gemvLinear call does, :1737: the two must agree)
   if (!flat(lm_head_) || D % 128 || I % 128 || qd % 128 || qd != D) return false;
@@ -1006,6 +1014,8 @@ bool Engine::plan_block(std::string* err) {
   part_floats = std::max(part_floats, ranges(D) * kBlockUnit * 2 * units(I));
   part_floats = std::max(part_floats, ranges(I) * kBlockUnit * units(D));
   part_floats = std::max(part_floats, ranges(D) * kBlockUnit * units(V));
+  if (cfg_.hybrid)  // in_proj_qkv + z + a (8192 + 4096 + 32 rows), q + k + v (8192 + 2 x 1024), out_proj
+    part_floats = std::max(part_floats, ranges(D) * kBlockUnit * (units(8192) + units(4096) + units(32)));
   part_floats *= kMaxBlock;
   const size_t Cmax = std::max({D, I, qd}), ngm = Cmax / 128, nq = (kMaxBlock + 3) / 4;
   const size_t hd = arch_.head_dim, H = arch_.num_attn_heads;
@@ -1029,6 +1039,17 @@ bool Engine::plan_block(std::string* err) {
   btab_.xt = fa(Cmax * kMaxBlock);
   btab_.ss = fa(kMaxBlock);
   d_bpartials_ = static_cast<ArgmaxPartial*>(dev_alloc(kMaxBlock * 512 * sizeof(ArgmaxPartial)));
+  if (cfg_.hybrid) {
+    d_bhx0_ = fa(kMaxBlock * 8192);
+    d_bhx1_ = fa(kMaxBlock * 4096);
+    d_bhx2_ = fa(kMaxBlock * 1024);
+    d_bhx3_ = fa(kMaxBlock * 32);
+    d_bhconv_ = fa(kMaxBlock * 8192);
+    if (!d_bhx0_ || !d_bhx1_ || !d_bhx2_ || !d_bhx3_ || !d_bhconv_) {
+      *err = "allocation";
+      return false;
+    }
+  }
   if (!d_btok_ || !d_bout_ || !d_bstate_ || !d_bbrk_ || !d_bx_ || !d_bq_ || !d_battn_ || !d_bmlp_ || !d_blog_ || !d_bpartial_ ||
       !d_bpml_ || !d_bpacc_ || !d_bss_ || !btab_.tb || !btab_.ci || !btab_.ew || !btab_.xt || !btab_.ss ||
       !d_bpartials_) {
@@ -1047,7 +1068,7 @@ bool Engine::plan_block(std::string* err) {
 
 uint32_t Engine::enqueue_block_gemv(const ProjPlan* const* parts, float* const* outs, int n, GemvMode mode,
                                     const float* x, uint32_t C, const float* gamma, uint32_t n_ss, uint32_t m,
-                                    size_t layer, hipStream_t st) {
+                                    size_t layer, hipStream_t st, const uint32_t* roles_in, uint32_t pair_dim) {
   BlockGemvArgs b{};
   b.g.n_parts = n;
   b.g.mode = int(mode);
@@ -1069,7 +1090,7 @@ uint32_t Engine::enqueue_block_gemv(const ProjPlan* const* parts, float* const* 
     gp.bias = p.bias;
     gp.corr = p.corr;
     gp.corr_kmax = p.corr_kmax;
-    gp.rope_role = mode == GemvMode::QkvRope ? roles[i] : 0u;
+    gp.rope_role = mode == GemvMode::QkvRope ? (roles_in ? roles_in[i] : roles[i]) : 0u;
     units += (p.rows + kBlockUnit - 1) / kBlockUnit;
   }
   b.t = btab_;
@@ -1082,6 +1103,7 @@ uint32_t Engine::enqueue_block_gemv(const ProjPlan* const* parts, float* const* 
   b.brk = d_bbrk_;
   if (mode == GemvMode::QkvRope) {
     b.g.rope = rope_args(layer);
+    if (pair_dim) b.g.rope.head_dim = pair_dim;
     b.state = d_bstate_;
     b.rope_cos = d_rope_cos_;
     b.rope_sin = d_rope_sin_;
@@ -1106,6 +1128,7 @@ int Engine::block_forward(const uint32_t* tokens, size_t m, size_t pos, uint32_t
   if (hipMemcpyAsync(d_btok_, h_btok_, m * 4, hipMemcpyHostToDevice, st) != hipSuccess ||
       hipMemcpyAsync(d_bstate_, h_bstate_, sizeof(StepState), hipMemcpyHostToDevice, st) != hipSuccess)
     return -3;
+  if (cfg_.hybrid && pos == 0) reset_hybrid_state(st);  // a new sequence (outside the graph)
   if (use_graph_) {  // one captured graph per token count, captured on first use
     if (!bgraph_exec_[m]) {
       if (hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal) != hipSuccess) return -3;
@@ -1135,6 +1158,10 @@ int Engine::block_forward(const uint32_t* tokens, size_t m, size_t pos, uint32_t
 }
 
 void Engine::record_block(uint32_t mm, hipStream_t st) {
+  if (cfg_.hybrid) {
+    record_block_hybrid(mm, st);
+    return;
+  }
   const uint32_t D = uint32_t(arch_.hidden_dim), I = uint32_t(arch_.intermediate_dim), V = uint32_t(arch_.vocab_size);
   const uint32_t qd = uint32_t(arch_.num_attn_heads * arch_.head_dim);
   launch_block_embed(embed_args(), d_btok_, mm, d_bx_, d_bss_, d_bbrk_, st);
@@ -1160,6 +1187,106 @@ void Engine::record_block(uint32_t mm, hipStream_t st) {
     enqueue_block_gemv(gu, mlp, 2, GemvMode::SwiGlu, d_bx_, D, L.gamma_post, n_ss, mm, l, st);
     const ProjPlan* dn[1] = {&L.down};
     n_ss = enqueue_block_gemv(dn, hid, 1, GemvMode::Accum, d_bmlp_, I, nullptr, 0, mm, l, st);
+  }
+  const ProjPlan* lm[1] = {&lm_head_};
+  float* lg[1] = {d_blog_};
+  const uint32_t eb = enqueue_block_gemv(lm, lg, 1, GemvMode::Logits, d_bx_, D, d_gamma_final_, n_ss, mm, 0, st);
+  launch_block_finish(BlockFinishArgs{d_bpartials_, eb, mm, d_blog_, V, btab_.ss, d_bout_, d_result_}, st);
+  (void)hipMemcpyAsync(d_logits_, d_blog_ + size_t(mm - 1) * V, size_t(V) * 4, hipMemcpyDeviceToDevice, st);
+}
+
+// The hybrid model's block step: record_step_hybrid's layers for m tokens, every weight read once
+// (k_gemv_mt), the DeltaNet states rolled over the m tokens in order inside one launch each
+// (launch_dn_block), the gated attention layers' q / k norms, rotary embedding and KV append per
+// token (k_hyb_qk over the tokens) and the multi-query decode attention.
+void Engine::record_block_hybrid(uint32_t mm, hipStream_t st) {
+  const uint32_t D = uint32_t(arch_.hidden_dim), I = uint32_t(arch_.intermediate_dim), V = uint32_t(arch_.vocab_size);
+  const uint32_t H = uint32_t(arch_.num_attn_heads), KV = uint32_t(arch_.num_kv_heads), hd = uint32_t(arch_.head_dim);
+  const uint32_t store[3] = {kRoleStore, kRoleStore, kRoleStore};
+  launch_block_embed(embed_args(), d_btok_, mm, d_bx_, d_bss_, d_bbrk_, st);
+  uint32_t n_ss = 1;
+  for (size_t l = 0; l < arch_.num_layers; ++l) {
+    const LayerPlan& L = layers_[l];
+    const HybLayer& Hy = hyb_[l];
+    float* hid[1] = {d_bx_};
+    const ProjPlan* in[3] = {&Hy.in0, &Hy.in1, &Hy.in2};
+    float* outs[3] = {d_bhx0_, d_bhx1_, d_bhx2_};
+    enqueue_block_gemv(in, outs, 3, GemvMode::QkvRope, d_bx_, D, L.gamma_in, n_ss, mm, l, st, store, 32);
+    if (Hy.full) {
+      const RopeArgs kv = rope_args(l);
+      HybQkArgs q{};
+      q.state = d_bstate_;
+      q.qg = d_bhx0_;
+      q.k = d_bhx1_;
+      q.v = d_bhx2_;
+      q.q_norm = Hy.q_norm;
+      q.k_norm = Hy.k_norm;
+      q.rope_cos = d_rope_cos_;
+      q.rope_sin = d_rope_sin_;
+      q.q_out = d_bq_;
+      q.k_cache = kv.k_cache;
+      q.v_cache = kv.v_cache;
+      q.H = H;
+      q.KV = KV;
+      q.hd = hd;
+      q.rot = rope_dim_;
+      q.max_seq = kv.max_seq;
+      q.kv_f16 = kv.kv_f16;
+      q.rope_rows = uint32_t(cfg_.max_seq_len);
+      q.eps = arch_.rms_eps;
+      q.m = mm;
+      q.qg_stride = 8192;
+      q.kv_stride = 1024;
+      q.q_stride = H * hd;
+      q.brk = d_bbrk_;
+      launch_hyb_qk(q, st);
+      AttnArgs at = attn_args(l);
+      at.state = d_bstate_;
+      at.q = d_bq_;
+      at.out = d_battn_;
+      at.part_ml = d_bpml_;
+      at.part_acc = d_bpacc_;
+      at.nq = mm;
+      launch_attention(at, st);
+      launch_hyb_gate(d_battn_, d_bhx0_, H, hd, mm, st);
+    } else {
+      const ProjPlan* inb[1] = {&Hy.in3};
+      float* outb[1] = {d_bhx3_};
+      enqueue_block_gemv(inb, outb, 1, GemvMode::QkvRope, d_bx_, D, L.gamma_in, n_ss, mm, l, st, store, 32);
+      DnBlockArgs dn{};
+      dn.x = d_bhx0_;
+      dn.w = Hy.conv_w;
+      dn.conv_state = d_conv_state_ + size_t(Hy.lin) * 8192 * 3;
+      dn.conv_out = d_bhconv_;
+      dn.channels = 8192;
+      dn.taps = 4;
+      dn.x_stride = 8192;
+      dn.a = d_bhx2_;
+      dn.b = d_bhx3_;
+      dn.ab_stride = 32;
+      dn.A_log = Hy.A_log;
+      dn.dt_bias = Hy.dt_bias;
+      dn.z = d_bhx1_;
+      dn.z_stride = 4096;
+      dn.norm_w = Hy.lin_norm;
+      dn.state = d_rec_state_ + size_t(Hy.lin) * 32 * 128 * 128;
+      dn.out = d_battn_;
+      dn.out_stride = 4096;
+      dn.n_v_heads = 32;
+      dn.n_k_heads = 16;
+      dn.head_dim = 128;
+      dn.m = mm;
+      dn.eps = arch_.rms_eps;
+      dn.brk = d_bbrk_;
+      launch_dn_block(dn, st);
+    }
+    const ProjPlan* o[1] = {&Hy.out};
+    n_ss = enqueue_block_gemv(o, hid, 1, GemvMode::Accum, d_battn_, 4096, nullptr, 0, mm, l, st);
+    const ProjPlan* gu[2] = {&L.gate, &L.up};
+    float* mlp[2] = {d_bmlp_, d_bmlp_};
+    enqueue_block_gemv(gu, mlp, 2, GemvMode::SwiGlu, d_bx_, D, L.gamma_post, n_ss, mm, l, st);
+    const ProjPlan* dnp[1] = {&L.down};
+    n_ss = enqueue_block_gemv(dnp, hid, 1, GemvMode::Accum, d_bmlp_, I, nullptr, 0, mm, l, st);
   }
   const ProjPlan* lm[1] = {&lm_head_};
   float* lg[1] = {d_blog_};
@@ -1392,7 +1519,7 @@ void Engine::record_step_hybrid(hipStream_t st) {
       const AttnArgs aa = attn_args(l);
       launch_attention_partial(aa, st);
       launch_attention_combine(aa, st);
-      launch_hyb_gate(d_attn_, d_hx0_, q.H, q.hd, st);
+      launch_hyb_gate(d_attn_, d_hx0_, q.H, q.hd, 1, st);
       const ProjPlan* o[1] = {&H.out};
       enqueue_gemv(o, hid, 1, GemvMode::Accum, d_attn_, uint32_t(q.H * q.hd), nullptr, st);
     } else {

@@ -216,9 +216,12 @@ class Engine {
   void record_block(uint32_t m, hipStream_t st);  // the block step of m tokens after its inputs
   // gamma set: the input's Σx² comes as n_ss partials in d_bss_; Accum leaves the updated rows'
   // partials there and returns their count (as it returns the Logits partials' count)
+  // roles (QkvRope): the parts' RopeRole (null: q, k, v); pair_dim: the row pairing of the
+  // QkvRope epilogue when not the head dim (the hybrid's Store launches: 32)
   uint32_t enqueue_block_gemv(const ProjPlan* const* parts, float* const* outs, int n, GemvMode mode,
                               const float* x, uint32_t C, const float* gamma, uint32_t n_ss, uint32_t m,
-                              size_t layer, hipStream_t st);
+                              size_t layer, hipStream_t st, const uint32_t* roles = nullptr, uint32_t pair_dim = 0);
+  void record_block_hybrid(uint32_t m, hipStream_t st);  // record_block of the hybrid model
 
  public:
   // run one projection's GEMV on a caller vector (Store mode, bias included): parity hooks
@@ -284,6 +287,9 @@ class Engine {
   float *d_bx_ = nullptr, *d_bq_ = nullptr, *d_battn_ = nullptr, *d_bmlp_ = nullptr, *d_blog_ = nullptr;
   float *d_bpartial_ = nullptr, *d_bpml_ = nullptr, *d_bpacc_ = nullptr;
   float* d_bss_ = nullptr;  // [kMaxSsPartials][kMaxBlock]: Σx² partials of the hidden rows for the next norm
+  // the hybrid's block activations, [kMaxBlock][rows]: the in-projections' outputs (as d_hx0_ ..
+  // d_hx3_) and the conv outputs
+  float *d_bhx0_ = nullptr, *d_bhx1_ = nullptr, *d_bhx2_ = nullptr, *d_bhx3_ = nullptr, *d_bhconv_ = nullptr;
   BlockTables btab_{};
   ArgmaxPartial* d_bpartials_ = nullptr;
   hipGraph_t bgraph_[kMaxBlock + 1] = {};          // captured block steps, by token count

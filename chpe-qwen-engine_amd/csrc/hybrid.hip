@@ -14,18 +14,24 @@ namespace chpe {
 namespace {
 using namespace dev;
 
-// one workgroup per head: blocks 0..H-1 the query heads, H..H+KV-1 the key heads, then the
-// value heads; thread d holds dimension d
+// one workgroup per head and token (blockIdx.y: token t at position pos + t of a block step, 0
+// in the decode step): blocks 0..H-1 the query heads, H..H+KV-1 the key heads, then the value
+// heads; thread d holds dimension d
 template <int HD>
 __global__ void __launch_bounds__(HD) k_hyb_qk(HybQkArgs a) {
 #pragma clang fp contract(off)
-  const uint32_t b = blockIdx.x, d = threadIdx.x;
+  const uint32_t b = blockIdx.x, d = threadIdx.x, tk = blockIdx.y;
   const bool is_q = b < a.H, is_k = !is_q && b < a.H + a.KV;
   const uint32_t h = is_q ? b : (is_k ? b - a.H : b - a.H - a.KV);
-  const StepState st = *a.state;
+  StepState st = *a.state;
+  st.pos += tk;
+  if (a.brk) st.broken = a.brk[tk];
+  const float* qg = a.qg + size_t(tk) * a.qg_stride;
+  const float* kk = a.k + size_t(tk) * a.kv_stride;
+  const float* vv = a.v + size_t(tk) * a.kv_stride;
   __shared__ float s_x[HD];
   __shared__ float s_red[HD / 64];
-  float x = is_q ? a.qg[size_t(h) * 2 * HD + d] : (is_k ? a.k[size_t(h) * HD + d] : a.v[size_t(h) * HD + d]);
+  float x = is_q ? qg[size_t(h) * 2 * HD + d] : (is_k ? kk[size_t(h) * HD + d] : vv[size_t(h) * HD + d]);
   if (is_q || is_k) {  // (uniform per workgroup)
     const float g = is_q ? a.q_norm[d] : a.k_norm[d];
     const float s2 = wave_sum(x * x);
@@ -47,7 +53,7 @@ __global__ void __launch_bounds__(HD) k_hyb_qk(HybQkArgs a) {
     }
   }
   if (is_q) {
-    a.q_out[size_t(h) * HD + d] = x;
+    a.q_out[size_t(tk) * a.q_stride + size_t(h) * HD + d] = x;
     return;
   }
   if (st.broken) return;  // forwardDecode's break: no KV append
@@ -63,12 +69,13 @@ __global__ void __launch_bounds__(HD) k_hyb_qk(HybQkArgs a) {
   }
 }
 
-__global__ void __launch_bounds__(256) k_hyb_gate(float* attn, const float* qg, uint32_t H, uint32_t hd) {
+// m tokens: attn [m][H hd], qg [m][2 H hd]
+__global__ void __launch_bounds__(256) k_hyb_gate(float* attn, const float* qg, uint32_t H, uint32_t hd, uint32_t m) {
 #pragma clang fp contract(off)
   const uint32_t i = blockIdx.x * 256 + threadIdx.x;
-  if (i >= H * hd) return;
-  const uint32_t h = i / hd, d = i % hd;
-  const float g = qg[size_t(h) * 2 * hd + hd + d];
+  if (i >= m * H * hd) return;
+  const uint32_t tk = i / (H * hd), e = i % (H * hd), h = e / hd, d = e % hd;
+  const float g = qg[size_t(tk) * 2 * H * hd + size_t(h) * 2 * hd + hd + d];
   attn[i] = attn[i] * (1.0f / (1.0f + expf(-g)));
 }
 
@@ -76,11 +83,11 @@ __global__ void __launch_bounds__(256) k_hyb_gate(float* attn, const float* qg, 
 
 void launch_hyb_qk(const HybQkArgs& a, hipStream_t st) {
   if (a.hd != 256) return;  // (the 9B head dim; the engine checks the shape at init)
-  launch_kernel(&k_hyb_qk<256>, dim3(a.H + 2 * a.KV), dim3(256), st, a);
+  launch_kernel(&k_hyb_qk<256>, dim3(a.H + 2 * a.KV, a.m ? a.m : 1), dim3(256), st, a);
 }
 
-void launch_hyb_gate(float* attn, const float* qg, uint32_t H, uint32_t hd, hipStream_t st) {
-  launch_kernel(&k_hyb_gate, dim3((H * hd + 255) / 256), dim3(256), st, attn, qg, H, hd);
+void launch_hyb_gate(float* attn, const float* qg, uint32_t H, uint32_t hd, uint32_t m, hipStream_t st) {
+  launch_kernel(&k_hyb_gate, dim3((m * H * hd + 255) / 256), dim3(256), st, attn, qg, H, hd, m);
 }
 
 }  // namespace chpe

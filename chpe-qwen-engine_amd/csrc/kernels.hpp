@@ -355,6 +355,29 @@ struct DnStepArgs {         // gated delta rule over the value heads (+ gated RM
   const StepState* step;    // or null: after the step's break (StepState::broken) the state stays
 };
 
+// A DeltaNet layer's m tokens in order (the block step): conv update + SiLU, the gated delta
+// rule and the gated norm per token, each state read once and written once (launch_dn_block).
+struct DnBlockArgs {
+  const float* x;           // conv input [m][x_stride] (channels used)
+  const float* w;           // [channels][taps]
+  float* conv_state;        // [channels][taps-1]
+  float* conv_out;          // [m][channels]: q [n_k_heads][hd], k, v [n_v_heads][hd] per token
+  uint32_t channels, taps, x_stride;
+  const float *a, *b;       // [m][ab_stride]
+  uint32_t ab_stride;
+  const float *A_log, *dt_bias;
+  const float* z;           // [m][z_stride]
+  uint32_t z_stride;
+  const float* norm_w;      // [head_dim]
+  float* state;             // [n_v_heads][hd][hd]
+  float* out;               // [m][out_stride]
+  uint32_t out_stride;
+  uint32_t n_v_heads, n_k_heads, head_dim, m;
+  float eps;
+  const uint32_t* brk;      // [m]: token t broke before this layer (its state updates are skipped)
+};
+void launch_dn_block(const DnBlockArgs& a, hipStream_t stream);
+
 // The hybrid model's gated full-attention layer around the decode attention kernels
 // (transformers' Qwen3_5Attention): per query head the RMS norm (q_norm gains) and the rotary
 // embedding of the first `rot` dims (pairs (i, i + rot/2)), into q_out; per kv head the same
@@ -374,10 +397,14 @@ struct HybQkArgs {
   void* v_cache;
   uint32_t H, KV, hd, rot, max_seq, kv_f16, rope_rows;
   float eps;
+  // the block step: m tokens at positions pos .. pos + m - 1 (0 or 1: the decode step), the
+  // per-token strides of qg, k / v and q_out, and each token's break flag (null: StepState::broken)
+  uint32_t m, qg_stride, kv_stride, q_stride;
+  const uint32_t* brk;
 };
 void launch_hyb_qk(const HybQkArgs& a, hipStream_t stream);
-// attn[h][d] *= sigmoid(qg[h][hd + d]) for H heads of hd
-void launch_hyb_gate(float* attn, const float* qg, uint32_t H, uint32_t hd, hipStream_t stream);
+// attn[t][h][d] *= sigmoid(qg[t][h][hd + d]) for m tokens of H heads of hd
+void launch_hyb_gate(float* attn, const float* qg, uint32_t H, uint32_t hd, uint32_t m, hipStream_t stream);
 bool deltanet_supported(uint32_t n_v_heads, uint32_t n_k_heads, uint32_t head_dim, uint32_t taps);
 void launch_dn_conv(const DnConvArgs& a, hipStream_t stream);
 void launch_dn_step(const DnStepArgs& a, uint32_t head_dim, hipStream_t stream);

@@ -8,9 +8,11 @@ Bars as for the other whole-model tests: single-step logits within 2e-4 * max|lo
 >= 0.9999 with the f32 KV cache, 1.5e-3 with the fp16 cache; greedy streams identical, a
 difference allowed only after an oracle step whose top-2 gap is below 1e-3.  Then the state
 machinery: the recurrent states restart at position 0 (a prompt run twice gives the same
-logits bit for bit), verify and prefill are the decode steps (the same kernels, bit for bit),
-and the hybrid decode is not the reference's decode of the same archive (arch 1); the command
-line's --hybrid writes chpe_forward_tokens' logits of arch 3, bit for bit."""
+logits bit for bit); the block step (speculative verify of 4 and 8 drafts, the chunked
+prefill: every weight read once, the DeltaNet states rolled over the tokens in order) against
+the decode steps and against the oracle; the hybrid decode is not the reference's decode of the
+same archive (arch 1); the command line's --hybrid writes chpe_forward_tokens' logits of arch
+3, bit for bit."""
 import numpy as np
 import pytest
 
@@ -83,33 +85,54 @@ def test_hybrid_steps_and_stream_match_oracle(a9h):
         o.close()
 
 
+def top2_gap(lg):
+    t = np.sort(lg.astype(np.float64))
+    return float(t[-1] - t[-2])
+
+
 @pytest.mark.timeout(600)
-def test_hybrid_restart_verify_prefill(a9h):
-    prompt, drafts = prompt_of(11, 6), prompt_of(12, 4)
+def test_hybrid_restart_and_block_step(a9h):
+    """Position 0 restarts the recurrent states; the block step (every weight read once for the
+    m tokens, the DeltaNet states rolled over them in order inside one launch per kernel)
+    against the decode steps on the same engine, with the block-step bars of the other models
+    (2e-4 * max|logit| with the f32 cache, 3e-3 with the fp16 cache; an argmax may differ only
+    where the decode step's top-2 gap is below twice the bar)."""
+    prompt, drafts = prompt_of(11, 6), prompt_of(12, 8)
     n = len(prompt)
-    e = ca.Engine(a9h, arch=3, max_seq_len=64, kv_f16=True)
-    try:
-        assert not e.block_ready()  # the recurrent state advances token by token
-        say("hybrid: the prompt twice from position 0")
-        _, l1 = e.forward_tokens(prompt, want_logits=True)
-        seq = [e.decode_step(int(d), n + i) for i, d in enumerate(drafts)]
-        _, l2 = e.forward_tokens(prompt, want_logits=True)
-        assert np.array_equal(l1.view(np.uint32), l2.view(np.uint32))
-        say("hybrid: verify 4 drafts = 4 decode steps")
-        got = e.verify(drafts, n)
-        assert list(map(int, got)) == [int(s[0]) for s in seq]
-        assert np.array_equal(e.logits().view(np.uint32), seq[-1][1].view(np.uint32))
-        say("hybrid: prefill = forward_tokens")
-        _, lp = e.prefill(prompt, want_logits=True)
-        assert np.array_equal(lp.view(np.uint32), l1.view(np.uint32))
-        # a step at position 1 continues from the state position 0 left
-        a = e.decode_step(int(prompt[0]), 0)[1]
-        b = e.decode_step(int(prompt[1]), 1)[1]
-        e.decode_step(int(prompt[2]), 0)
-        c = e.decode_step(int(prompt[1]), 1)[1]
-        assert not np.array_equal(b, c) and not np.array_equal(a, b)
-    finally:
-        e.close()
+    for kv16, rel in ((True, 3e-3), (False, 2e-4)):
+        e = ca.Engine(a9h, arch=3, max_seq_len=64, kv_f16=kv16)
+        try:
+            assert e.block_ready()
+            say(f"hybrid kv_f16={kv16}: the prompt twice from position 0")
+            _, l1 = e.forward_tokens(prompt, want_logits=True)
+            seq = [e.decode_step(int(d), n + i) for i, d in enumerate(drafts)]
+            _, l2 = e.forward_tokens(prompt, want_logits=True)
+            assert np.array_equal(l1.view(np.uint32), l2.view(np.uint32))
+            for m in (4, 8):
+                say(f"hybrid: verify {m} drafts vs {m} decode steps")
+                e.forward_tokens(prompt)
+                got = e.verify(drafts[:m], n)
+                for i in range(m):
+                    if int(got[i]) != int(seq[i][0]):
+                        assert top2_gap(seq[i][1]) < 2 * rel * float(np.abs(seq[i][1]).max()), (m, i)
+                compare_logits(e.logits(), seq[m - 1][1], f"verify {m}: last draft", rel)
+                if m == 4:  # the decode state continues after the block: the next draft's step
+                    am, lg = e.decode_step(int(drafts[4]), n + 4)
+                    compare_logits(lg, seq[4][1], "decode step after verify 4", rel)
+            say("hybrid: prefill (block steps of 6) vs forward_tokens")
+            _, lp = e.prefill(prompt, want_logits=True)
+            compare_logits(lp, l1, "prefill vs forward_tokens", rel)
+            am, lg = e.decode_step(int(drafts[0]), n)
+            compare_logits(lg, seq[0][1], "decode step after prefill", rel)
+            if kv16:
+                # a step at position 1 continues from the state position 0 left
+                a = e.decode_step(int(prompt[0]), 0)[1]
+                b = e.decode_step(int(prompt[1]), 1)[1]
+                e.decode_step(int(prompt[2]), 0)
+                c = e.decode_step(int(prompt[1]), 1)[1]
+                assert not np.array_equal(b, c) and not np.array_equal(a, b)
+        finally:
+            e.close()
     # the reference's decode of the 9B map (arch 1) is another computation
     e = ca.Engine(a9h, arch=1, max_seq_len=64, kv_f16=True)
     try:
@@ -117,6 +140,40 @@ def test_hybrid_restart_verify_prefill(a9h):
         assert not np.allclose(lc, l1, rtol=1e-2, atol=1e-2)
     finally:
         e.close()
+
+
+@pytest.mark.timeout(900)
+def test_hybrid_block_step_matches_oracle(a9h):
+    """The speculative verify of the hybrid (4 and 8 drafts over an 11-token context, the
+    block step) and the block prefill against the oracle's sequential hybrid steps (f32 cache):
+    every argmax (up to a near-tie) and the last draft's logits within 2e-4 * max|logit|."""
+    prompt, drafts = prompt_of(21, 11), prompt_of(22, 8)
+    n = len(prompt)
+    e = ca.Engine(a9h, arch=3, max_seq_len=64, kv_f16=False)
+    o = orc.Oracle(a9h, arch=1, max_seq_len=64, kv_f16=False, threads=threads())
+    o.set_hybrid(True)
+    try:
+        say("hybrid: prefill of 11 positions (blocks of 8 + 3) vs the oracle")
+        _, lp = e.prefill(prompt, want_logits=True)
+        for pos, t in enumerate(prompt):
+            o.forward(int(t), pos)
+        compare_logits(lp, o.logits(), "prefill vs oracle", 2e-4)
+        for m in (4, 8):
+            say(f"hybrid: verify {m} drafts vs the oracle")
+            e.prefill(prompt)
+            got = e.verify(drafts[:m], n)
+            lv = e.logits()
+            for pos, t in enumerate(prompt):  # the oracle's context again (its states restart at 0)
+                o.forward(int(t), pos)
+            for i in range(m):
+                r = o.forward(int(drafts[i]), n + i)
+                if int(got[i]) != r.argmax_token:
+                    ol = o.logits()
+                    assert top2_gap(ol) < 4e-4 * float(np.abs(ol).max()), (m, i, int(got[i]), r.argmax_token)
+            compare_logits(lv, o.logits(), f"verify {m}: last draft vs oracle", 2e-4)
+    finally:
+        e.close()
+        o.close()
 
 
 def test_hybrid_needs_the_9b_archive(w4_archive):
