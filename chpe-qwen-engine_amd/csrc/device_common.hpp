@@ -17,7 +17,10 @@ inline void launch_kernel_lds(K kernel, dim3 grid, dim3 block, size_t lds, hipSt
   if (lds > 65536)
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
                               int(lds));
-  if (detail::g_record_names) detail::g_last_kernel = hipKernelNameRefByPtr(reinterpret_cast<const void*>(kernel), st);
+  if (detail::g_record_names) {  // (name lookup only: nothing is launched)
+    detail::g_last_kernel = hipKernelNameRefByPtr(reinterpret_cast<const void*>(kernel), st);
+    return;
+  }
   const LaunchProbe p = take_launch_probe();
   if (p.start)
     hipExtLaunchKernelGGL(kernel, grid, block, uint32_t(lds), st, p.start, p.stop, 0, args...);

@@ -1579,10 +1579,10 @@ int Engine::launch_stage(int stage, size_t l) {
     case 0:
       enqueue_qkv(l, stream_);
       return 0;
-    case 1: {  // writes a scratch vector, not the residual stream
+    case 1: {  // the step's Accum launch into a scratch vector, not the residual stream
       const ProjPlan* o[1] = {&L.o};
       float* y[1] = {d_q_};
-      enqueue_gemv(o, y, 1, GemvMode::Store, d_attn_, D, nullptr, stream_);
+      enqueue_gemv(o, y, 1, GemvMode::Accum, d_attn_, D, nullptr, stream_);
       return 0;
     }
     case 2: {
@@ -1591,10 +1591,10 @@ int Engine::launch_stage(int stage, size_t l) {
       enqueue_gemv(gu, y, 2, GemvMode::SwiGlu, d_hidden_, D, L.gamma_post, stream_);
       return 0;
     }
-    case 3: {
+    case 3: {  // (as stage 1)
       const ProjPlan* dn[1] = {&L.down};
       float* y[1] = {d_attn_};
-      enqueue_gemv(dn, y, 1, GemvMode::Store, d_mlp_, I, nullptr, stream_);
+      enqueue_gemv(dn, y, 1, GemvMode::Accum, d_mlp_, I, nullptr, stream_);
       return 0;
     }
     case 4: {

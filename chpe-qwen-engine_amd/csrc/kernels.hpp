@@ -435,7 +435,7 @@ void arm_launch_probe(hipEvent_t start, hipEvent_t stop);
 LaunchProbe take_launch_probe();
 
 // Measurement: while on, every launcher on this host thread records the (mangled) name of the
-// kernel it launches; last_kernel_name() returns the latest one.
+// kernel it would launch, and launches nothing; last_kernel_name() returns the latest one.
 void record_kernel_names(bool on);
 const char* last_kernel_name();
 namespace detail {

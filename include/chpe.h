@@ -104,7 +104,10 @@ int chpe_get_hidden(void *ctx, float *out);
 int chpe_time_steps(void *ctx, size_t n, float *ms);
 /* Launch one stage alone (0 q/k/v, 1 o, 2 gate+up, 3 down, 4 LM head, 5 attention over the
  * context chunks, 6 merge of the chunks) for each layer in [layer0, layer1), `iters` times,
- * between HIP events; *ms = total. */
+ * between HIP events; *ms = total.  The step's own kernels and arguments, except that o and
+ * down add into scratch vectors (not the residual stream) and the LM head's logits replace the
+ * last step's; stage 0 writes the KV row at the device position, which the next step
+ * overwrites.  The hybrid model (arch 3): stages 2-4 only. */
 int chpe_time_stage(void *ctx, int stage, size_t layer0, size_t layer1, size_t iters, float *ms);
 /* Run n_steps real decode steps (greedy feedback, continuing from the device state), launched
  * without the graph and with a HIP event pair around every launch of `stage` (numbering as
@@ -115,7 +118,8 @@ int chpe_time_stage_live(void *ctx, int stage, size_t n_steps, float *avg_ms);
 double chpe_stage_bytes(void *ctx, int stage, size_t layer);
 double chpe_step_bytes(void *ctx, size_t pos);
 /* The (mangled) name of the kernel that runs `stage` of layer 0 (numbering as above; the last
- * launch of the stage), found by launching it once; "" on error. */
+ * launch of the stage), looked up without launching anything (the decode state is untouched);
+ * "" on error. */
 const char *chpe_stage_kernel(void *ctx, int stage);
 
 /* Parity hooks: one projection's GEMV on a caller vector (which: 0 q, 1 k, 2 v, 3 o,

@@ -20,7 +20,9 @@ Each archive is written into $CHPE_ARCHIVE_DIR when first needed and removed aft
 (a 72B archive is 38.6 GB).
 """
 import os
+import subprocess
 import sys
+import tempfile
 
 import numpy as np
 import pytest
@@ -217,6 +219,44 @@ def run_block(path, arch, vocab, seed, oracle_check, block=True):
 @pytest.mark.timeout(1200)
 def test_72b_block_step_matches_decode_steps(a72):
     run_block(a72, 2, 152064, seed=5, oracle_check=True)
+
+
+STEPS_CHILD = r"""
+import sys
+import numpy as np
+sys.path.insert(0, sys.argv[1])
+import chpe_amd as ca
+e = ca.Engine(sys.argv[2], arch=2, max_seq_len=16, kv_f16=True)
+out = [e.decode_step(int(t), p)[1] for p, t in enumerate(np.load(sys.argv[3]))]
+e.close()
+np.save(sys.argv[4], np.stack(out))
+"""
+
+
+@pytest.mark.timeout(900)
+def test_72b_w2_permuted_copies_bit_identical(a72):
+    """A 2-bit archive's decode launches all read a permuted copy of their codes (the 3-part
+    q/k/v launch, o, gate/up, down, the LM head): decode steps with the copies (here) and
+    without them (a child process started with CHPE_XM_LAYOUT=0, the codes read from the
+    records) give the same logits bit for bit -- the copies hold the same bytes for the same
+    lanes, whatever the launch's parts and modes."""
+    if "-w2-" not in a72.name:
+        pytest.skip("4-bit archives copy gate/up and the LM head only (test_gpu_xm_layout.py)")
+    toks = np.array([151643, 9707, 11], np.uint32)
+    say("72B 2-bit: decode steps with the permuted copies")
+    e = ca.Engine(a72, arch=2, max_seq_len=16, kv_f16=True)
+    try:
+        got = np.stack([e.decode_step(int(t), p)[1] for p, t in enumerate(toks)])
+    finally:
+        e.close()
+    with tempfile.TemporaryDirectory() as td:
+        tf, out = os.path.join(td, "t.npy"), os.path.join(td, "l.npy")
+        np.save(tf, toks)
+        say("  the same steps from the records (CHPE_XM_LAYOUT=0, child process)")
+        subprocess.run([sys.executable, "-c", STEPS_CHILD, str(ca.PKG_DIR), str(a72), tf, out],
+                       env=dict(os.environ, CHPE_XM_LAYOUT="0"), check=True, timeout=600)
+        want = np.load(out)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
 
 
 @pytest.mark.timeout(900)

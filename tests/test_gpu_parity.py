@@ -272,6 +272,26 @@ def test_c_abi_semantics(w4_archive):
         e.close()
 
 
+def test_stage_kernel_lookup_launches_nothing(w4_archive):
+    """chpe_stage_kernel names each stage's kernel without launching it: decode steps with the
+    lookups between them give the logits of the same steps without, bit for bit."""
+    toks = [151643, 9707, 11]
+    runs = []
+    for lookups in (False, True):
+        e = ca.Engine(w4_archive, arch=0, max_seq_len=16)
+        try:
+            out = []
+            for pos, t in enumerate(toks):
+                if lookups:
+                    names = [e.stage_kernel(st) for st in range(7)]
+                    assert all(names), names
+                out.append(e.decode_step(t, pos)[1])
+            runs.append(np.stack(out))
+        finally:
+            e.close()
+    assert np.array_equal(runs[0].view(np.uint32), runs[1].view(np.uint32))
+
+
 def test_kv_f16_matches_oracle_kv_f16(w4_archive):
     """fp16 KV cache against the oracle's fp16-cache mode.  Every k / v element is rounded to
     fp16, and an element whose f32 value differs from the oracle's in the last bits (another
