@@ -204,6 +204,39 @@ def stage_probe(workload, iters):
                       "attention_position": P}), flush=True)
 
 
+def trace_summary(path, out):
+    """Per-kernel statistics of a `rocprofv3 --kernel-trace` CSV (run_kernel_trace.csv) of a
+    bench run, split into the decode phase -- the longest run of dispatches without a block-step
+    GEMV (k_gemv_mt), i.e. the timed decode steps and the stage-timing steps -- and the rest
+    (context build, verify, load); writes a Markdown table to `out`."""
+    import csv
+    import collections
+    rows = []
+    with open(path) as f:
+        for r in csv.DictReader(f):
+            rows.append((int(r["Start_Timestamp"]), r["Kernel_Name"], int(r["Start_Timestamp"]), int(r["End_Timestamp"])))
+    rows.sort()  # (in start order)
+    blk = [i for i, r in enumerate(rows) if "k_gemv_mt" in r[1]]
+    cuts = [-1] + blk + [len(rows)]
+    a, b = max(zip(cuts, cuts[1:]), key=lambda ab: ab[1] - ab[0])
+    phases = {"decode": rows[a + 1:b], "other (context build, verify, load)": rows[:a + 1] + rows[b:]}
+    lines = [f"Source: `{path}` ({len(rows)} dispatches; decode phase = dispatches {a + 2}..{b} of the run)", ""]
+    for name, rs in phases.items():
+        st = collections.defaultdict(list)
+        for _, k, t0, t1 in rs:
+            st[k].append((t1 - t0) / 1e3)
+        total = sum(sum(v) for v in st.values()) or 1.0
+        lines += [f"### {name}: {len(rs)} dispatches, {total / 1e3:.2f} ms of kernel time", "",
+                  "| kernel | calls | avg µs | min µs | max µs | % of phase |", "|---|---|---|---|---|---|"]
+        for k, v in sorted(st.items(), key=lambda kv: -sum(kv[1])):
+            short = k.replace("chpe::(anonymous namespace)::", "").split("(")[0].replace("void ", "")
+            lines.append(f"| `{short}` | {len(v)} | {sum(v) / len(v):.2f} | {min(v):.2f} | {max(v):.2f} | "
+                         f"{100 * sum(v) / total:.2f} |")
+        lines.append("")
+    Path(out).write_text("\n".join(lines))
+    print(json.dumps({"trace_summary": str(out), "dispatches": len(rows), "decode": len(phases["decode"])}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -220,10 +253,15 @@ def main():
     ap.add_argument("--stage-probe", action="store_true",
                     help="only the q/k/v, o and down launches of layers 0-1 and one attention launch at the "
                          "prompt length (the rocprofv3 --pmc traffic runs of the other stages)")
+    ap.add_argument("--trace-summary", nargs=2, metavar=("KERNEL_TRACE_CSV", "OUT_MD"),
+                    help="summarise a rocprofv3 kernel-trace CSV of a bench run (decode phase vs the rest) and exit")
     ap.add_argument("--gemv-probe", action="store_true",
                     help="only the workload's gate/up GEMV on synthetic tiles of its shape, 4 launches "
                          "(the rocprofv3 --pmc traffic runs of the dominant kernel)")
     args = ap.parse_args()
+    if args.trace_summary:
+        trace_summary(*args.trace_summary)
+        return
     if args.copy_probe:
         copy_probe()
         return
