@@ -586,6 +586,7 @@ bool Engine::plan_lm_head(std::string* err) {
         if (!live) R.col[k] = 0;
       }
     }
+    lm_repl_host_ = repl;
     lm_head_.repl = static_cast<CellReplace*>(dev_alloc(n_cells * sizeof(CellReplace)));
     if (!lm_head_.repl) { *err = "allocation"; return false; }
     (void)hipMemcpy(lm_head_.repl, repl.data(), n_cells * sizeof(CellReplace), hipMemcpyHostToDevice);
@@ -988,24 +989,35 @@ bool Engine::plan_block(std::string* err) {
   block_ok_ = false;
   const size_t D = arch_.hidden_dim, I = arch_.intermediate_dim, V = arch_.vocab_size;
   const size_t qd = arch_.num_attn_heads * arch_.head_dim, kvd = arch_.num_kv_heads * arch_.head_dim;
-  // flat 4- or 2-bit tiles, one code width per launch (the q/k/v parts, gate and up alike)
-  auto flat = [](const ProjPlan& p) { return p.kind == WeightKind::FlatW4 || p.kind == WeightKind::FlatW2; };
+  // flat 4- or 2-bit tiles, one code width per launch (the q/k/v parts, gate and up alike); 16-row
+  // 4-bit group-128 cells at 2048 columns hold their codes and scales exactly as 2048-column flat
+  // tiles do (16 rows x 1024 B, f16[16][16]), so the block GEMV reads them as such, their outliers
+  // as per-row corrections (plan_cell_corrections)
+  auto flat = [](const ProjPlan& p) {
+    return p.kind == WeightKind::FlatW4 || p.kind == WeightKind::FlatW2 || (p.kind == WeightKind::Cell16W4 && p.cols == 2048);
+  };
+  auto bits_of = [](const ProjPlan& p) { return p.kind == WeightKind::FlatW2 ? 2 : 4; };
   for (size_t l = 0; l < layers_.size(); ++l) {
     const LayerPlan& L = layers_[l];
-    if (!flat(L.gate) || !flat(L.up) || !flat(L.down) || L.up.kind != L.gate.kind) return false;
+    if (!flat(L.gate) || !flat(L.up) || !flat(L.down) || bits_of(L.up) != bits_of(L.gate)) return false;
     if (cfg_.hybrid) {  // the hybrid's mixers (HybLayer) instead of the q/k/v/o plans
       const HybLayer& H = hyb_[l];
-      if (!flat(H.in0) || !flat(H.in1) || !flat(H.in2) || !flat(H.out) || H.in1.kind != H.in0.kind ||
-          H.in2.kind != H.in0.kind || (!H.full && !flat(H.in3)))
+      if (!flat(H.in0) || !flat(H.in1) || !flat(H.in2) || !flat(H.out) || bits_of(H.in1) != bits_of(H.in0) ||
+          bits_of(H.in2) != bits_of(H.in0) || (!H.full && !flat(H.in3)))
         return false;
       continue;
     }
-    if (!flat(L.q) || !flat(L.k) || !flat(L.v) || !flat(L.o) || L.k.kind != L.q.kind || L.v.kind != L.q.kind)
+    if (!flat(L.q) || !flat(L.k) || !flat(L.v) || !flat(L.o) || bits_of(L.k) != bits_of(L.q) ||
+        bits_of(L.v) != bits_of(L.q))
       return false;
   }
   // (the o projection reads the attention output of qd columns as hidden_dim columns, as the
   // reference's gemvLinear call does, :1737: the two must agree)
   if (!flat(lm_head_) || D % 128 || I % 128 || qd % 128 || qd != D) return false;
+  for (LayerPlan& L : layers_)
+    for (ProjPlan* p : {&L.q, &L.k, &L.v, &L.o, &L.gate, &L.up, &L.down})
+      if (p->kind == WeightKind::Cell16W4 && !plan_cell_corrections(p, p->cols, err)) return false;
+  if (lm_head_.kind == WeightKind::Cell16W4 && !plan_cell_corrections(&lm_head_, D, err)) return false;
   auto units = [](size_t rows) { return (rows + kBlockUnit - 1) / kBlockUnit; };
   auto ranges = [](size_t C) { return (C + kBlockRange - 1) / kBlockRange; };
   size_t part_floats = 0;  // ranges x kMaxBlock x rows_all, the largest GEMV
@@ -1066,6 +1078,45 @@ bool Engine::plan_block(std::string* err) {
   return true;
 }
 
+// A 16-row cell tensor's outliers for the block step, [rows][8] (column bits, weight): added
+// outliers (gemvTileW4 :404-410: the cell's 8 columns, each row's 8 f16 weights times the input
+// there, columns past the input giving 0), or for the tied LM head the replace tables' additive
+// deltas (w_out - dequantised code, prepared at load).
+bool Engine::plan_cell_corrections(ProjPlan* p, size_t C, std::string* err) {
+  const size_t rows = p->rows, n_cells = (rows + 15) / 16;
+  std::vector<float2> corr(rows * 8, make_float2(0.0f, 0.0f));
+  const size_t off0 = size_t(p->base - d_image_);  // (the archive offset of the first cell)
+  for (size_t t = 0; t < n_cells; ++t) {
+    const size_t pl = off0 + t * p->stride + kPayloadOff;
+    for (size_t n = 0; n < 16 && 16 * t + n < rows; ++n)
+      for (int k = 0; k < 8; ++k) {
+        uint32_t col = 0;
+        float w = 0.0f;
+        if (p->replace_outliers) {
+          const CellReplace& R = lm_repl_host_[t];
+          col = R.col[k];
+          w = R.delta[n][k];
+        } else {
+          col = rd<uint16_t>(host_bytes_, len_, pl + kRowOutlierCols + 2 * k);
+          w = f16_to_f32(rd<uint16_t>(host_bytes_, len_, pl + kRowOutlierW + 2 * (n * 8 + k)));
+        }
+        if (col >= C) w = 0.0f;  // (its input is 0: no term)
+        const uint32_t cb = w == 0.0f ? 0u : col;  // (the column's bits, as the flat tables hold it)
+        float cf;
+        std::memcpy(&cf, &cb, 4);
+        corr[(16 * t + n) * 8 + k] = make_float2(cf, w);
+      }
+  }
+  p->bcorr = static_cast<float2*>(dev_alloc(corr.size() * sizeof(float2)));
+  if (!p->bcorr) {
+    *err = "allocation";
+    return false;
+  }
+  (void)hipMemcpy(p->bcorr, corr.data(), corr.size() * sizeof(float2), hipMemcpyHostToDevice);
+  p->bcorr_kmax = 8;
+  return true;
+}
+
 uint32_t Engine::enqueue_block_gemv(const ProjPlan* const* parts, float* const* outs, int n, GemvMode mode,
                                     const float* x, uint32_t C, const float* gamma, uint32_t n_ss, uint32_t m,
                                     size_t layer, hipStream_t st, const uint32_t* roles_in, uint32_t pair_dim) {
@@ -1088,13 +1139,13 @@ uint32_t Engine::enqueue_block_gemv(const ProjPlan* const* parts, float* const* 
     gp.unit_begin = units;
     gp.y = outs[i];
     gp.bias = p.bias;
-    gp.corr = p.corr;
-    gp.corr_kmax = p.corr_kmax;
+    gp.corr = p.bcorr ? p.bcorr : p.corr;
+    gp.corr_kmax = p.bcorr ? p.bcorr_kmax : p.corr_kmax;
     gp.rope_role = mode == GemvMode::QkvRope ? (roles_in ? roles_in[i] : roles[i]) : 0u;
     units += (p.rows + kBlockUnit - 1) / kBlockUnit;
   }
   b.t = btab_;
-  b.bits = parts[0]->kind == WeightKind::FlatW2 ? 2u : 4u;
+  b.bits = parts[0]->kind == WeightKind::FlatW2 ? 2u : 4u;  // (16-row cells: 4, read as flat tiles)
   b.m = m;
   b.nq = (m + 3) / 4;
   b.n_units = units;

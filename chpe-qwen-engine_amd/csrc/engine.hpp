@@ -59,6 +59,8 @@ struct ProjPlan {
   float2* corr = nullptr;              // device [rows][corr_kmax] flat-tile outlier corrections
   uint32_t corr_kmax = 0;
   CellReplace* repl = nullptr;         // device, replace-mode outliers of 16-row cells
+  float2* bcorr = nullptr;             // device [rows][bcorr_kmax]: a 16-row cell tensor's outliers as
+  uint32_t bcorr_kmax = 0;             //   the block step's per-row corrections (plan_block)
   uint8_t* xcodes = nullptr;           // device, the decode launch's codes in the persistent
                                        //   matrix-core kernel's load order (see xm_layout_bytes);
                                        //   set on the launch's first part, and passed only to
@@ -278,6 +280,8 @@ class Engine {
   float *d_conv_state_ = nullptr, *d_rec_state_ = nullptr;
   size_t conv_state_floats_ = 0, rec_state_floats_ = 0;
   uint32_t rope_dim_ = 0;   // dims of a head the rotary tables cover (head_dim; hybrid: 64)
+  std::vector<CellReplace> lm_repl_host_;  // the tied cell LM head's replace tables (for plan_block)
+  bool plan_cell_corrections(ProjPlan* p, size_t C, std::string* err);
 
   // the block step (plan_block): m <= kMaxBlock tokens' activations, operand tables, partials
   bool block_ok_ = false;

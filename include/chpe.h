@@ -72,21 +72,23 @@ int chpe_generate(void *ctx, const uint32_t *prompt, size_t n_prompt, size_t n_g
  * earlier calls, out_argmax[i] = the argmax after draft i.  Equal to m sequential
  * chpe_decode_step(ctx, drafts[i], pos + i) calls (the reference has no verify code; its
  * equivalent is m forwardDecode calls, src/chpe_engine.zig:1663-1803, whose KV write at pos
- * overwrites the row, :1693-1697): on archives of flat 4- or 2-bit tiles (chpe_block_ready) and
+ * overwrites the row, :1693-1697): on archives of flat 4- or 2-bit tiles or 4-bit 16-row cells
+ * (chpe_block_ready) and
  * 2 <= m <= 8 as one block step that reads every weight once for the m drafts, with each draft's
  * arithmetic that of the decode step up to the order of the float sums; otherwise m replays of
  * the decode step, bit-identical.  last_* report the final step; chpe_get_last_logits gives
  * its logits.  Returns 0, -1 bad args, -2 pos + m > max_seq_len, -3 device error. */
 int chpe_verify(void *ctx, const uint32_t *drafts, size_t m, size_t pos, uint32_t *out_argmax);
 /* Prefill: positions 0..num_tokens-1 teacher-forced as chpe_forward_tokens, in block steps of
- * up to 8 tokens that read every weight once per block (archives of flat 4- or 2-bit tiles; others:
+ * up to 8 tokens that read every weight once per block (archives of flat 4- or 2-bit tiles or
+ * 4-bit 16-row cells; others:
  * the sequential steps).  Each token's arithmetic is the decode step's up to the order of the
  * float sums; the KV cache holds the same rows.  Leaves the decode state at (the last argmax,
  * num_tokens).  Returns the last argmax, -1 bad args, -2 too long, -3 device error;
  * out_logits (optional) receives the last position's logits. */
 int chpe_prefill(void *ctx, const uint32_t *tokens, size_t num_tokens, float *out_logits);
-/* 1 when the archive runs the block step (every projection flat 4- or 2-bit tiles, one width per
- * launch: q/k/v alike, gate/up alike; not the hybrid model), else 0. */
+/* 1 when the archive runs the block step (every projection flat 4- or 2-bit tiles or 4-bit 16-row
+ * cells at 2048 columns, one width per launch: q/k/v alike, gate/up alike), else 0. */
 int chpe_block_ready(void *ctx);
 
 /* Message of the last failed chpe_init / chpe_init_ex on this thread ("" if none). */

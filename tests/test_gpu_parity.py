@@ -9,6 +9,7 @@ Bars:
     a step's logits max-abs <= 2e-3 and cosine >= 0.9999;
   * greedy token streams: identical.
 """
+import os
 import sys
 
 import numpy as np
@@ -219,12 +220,27 @@ def test_token_stream_w4(w4):
     assert check_stream(g, r, gaps, "w4") == 32
 
 
+@pytest.fixture(scope="module")
+def w4_replay(w4_archive):
+    """An engine without the block step (CHPE_BLOCK=0, read at init): verify and prefill replay
+    the decode step."""
+    os.environ["CHPE_BLOCK"] = "0"
+    try:
+        e = ca.Engine(w4_archive, arch=0, max_seq_len=128, kv_f16=False)
+    finally:
+        del os.environ["CHPE_BLOCK"]
+    yield e
+    e.close()
+
+
 @pytest.mark.parametrize("m", [1, 4, 8])
-def test_verify_equals_sequential_steps(w4, m):
+def test_verify_equals_sequential_steps(w4_replay, w4, m):
     """chpe_verify (batch-M verify, no reference code) is defined as m sequential
-    forwardDecode(draft_i, pos + i): same argmaxes and, for the last draft, the same logits
-    bit for bit; for m = 4 the argmaxes also match the oracle's sequential steps."""
-    e, o = w4
+    forwardDecode(draft_i, pos + i); without the block step it replays them: same argmaxes and,
+    for the last draft, the same logits bit for bit; for m = 4 the argmaxes also match the
+    oracle's sequential steps.  (The block step: test_cell_block_step_matches_decode_steps.)"""
+    e, o = w4_replay, w4[1]
+    assert not e.block_ready()
     rng = np.random.default_rng(100 + m)
     prompt = rng.integers(0, V, 6).astype(np.uint32)
     drafts = rng.integers(0, V, m).astype(np.uint32)
@@ -244,6 +260,17 @@ def test_verify_equals_sequential_steps(w4, m):
             r = o.forward(int(d), p + i)
             compare_step(seq[i][1], o.logits(), f"verify {i}")
             assert int(got[i]) == r.argmax_token
+
+
+@pytest.mark.timeout(900)
+def test_cell_block_step_matches_decode_steps(w4_archive):
+    """The block step on 16-row 4-bit cells (the 3B archive: q/k/v/o/gate/up and the tied LM
+    head read as 2048-column flat tiles, their outliers as per-row corrections -- added, or the
+    LM head's replace deltas -- and the flat down projection): prefill and verify-8 against the
+    decode steps on the same engine, verify-4 and the prefill against the oracle, with the f32
+    and fp16 caches (run_block's bars)."""
+    from test_gpu_models import run_block
+    run_block(w4_archive, 0, V, seed=7, oracle_check=True)
 
 
 def test_c_abi_semantics(w4_archive):
