@@ -1669,8 +1669,10 @@ int Engine::launch_stage(int stage, size_t l) {
 namespace chpe {
 
 int Engine::debug_gemv(size_t layer, int which, const float* x, float* y) {
-  // which: 0 q, 1 k, 2 v, 3 o, 4 gate, 5 up, 6 down, 7 LM head (logits only)
+  // which: 0 q, 1 k, 2 v, 3 o, 4 gate, 5 up, 6 down, 7 LM head (logits only); the hybrid model
+  // has no q/k/v/o plans of the reference's map
   if (which < 7 && layer >= layers_.size()) return -1;
+  if (cfg_.hybrid && which >= 0 && which < 4) return -1;
   const ProjPlan* p = nullptr;
   if (which == 7) {
     p = &lm_head_;

@@ -125,7 +125,8 @@ double chpe_step_bytes(void *ctx, size_t pos);
 const char *chpe_stage_kernel(void *ctx, int stage);
 
 /* Parity hooks: one projection's GEMV on a caller vector (which: 0 q, 1 k, 2 v, 3 o,
- * 4 gate, 5 up, 6 down, 7 LM head), bias included, no norm; y gets the output rows. */
+ * 4 gate, 5 up, 6 down, 7 LM head), bias included, no norm; y gets the output rows.  -1 for
+ * which 0-3 on the hybrid model (arch 3), whose mixers are not the reference map's q/k/v/o. */
 int chpe_debug_gemv(void *ctx, size_t layer, int which, const float *x, float *y);
 /* Materialised weights of one flat 32768-weight tile (gemvCellFlat's dequantisation),
  * computed by the GPU from the 17408-byte cell. */
