@@ -1003,7 +1003,7 @@ bool Engine::plan_block(std::string* err) {
     if (cfg_.hybrid) {  // the hybrid's mixers (HybLayer) instead of the q/k/v/o plans
       const HybLayer& H = hyb_[l];
       if (!flat(H.in0) || !flat(H.in1) || !flat(H.in2) || !flat(H.out) || bits_of(H.in1) != bits_of(H.in0) ||
-          bits_of(H.in2) != bits_of(H.in0) || (!H.full && !flat(H.in3)))
+          bits_of(H.in2) != bits_of(H.in0) || (!H.full && !flat(H.in3)) || (H.has_ab && !flat(H.ab)))
         return false;
       continue;
     }
@@ -1027,7 +1027,7 @@ bool Engine::plan_block(std::string* err) {
   part_floats = std::max(part_floats, ranges(I) * kBlockUnit * units(D));
   part_floats = std::max(part_floats, ranges(D) * kBlockUnit * units(V));
   if (cfg_.hybrid)  // in_proj_qkv + z + a (8192 + 4096 + 32 rows), q + k + v (8192 + 2 x 1024), out_proj
-    part_floats = std::max(part_floats, ranges(D) * kBlockUnit * (units(8192) + units(4096) + units(32)));
+    part_floats = std::max(part_floats, ranges(D) * kBlockUnit * (units(8192) + units(4096) + units(64)));
   part_floats *= kMaxBlock;
   const size_t Cmax = std::max({D, I, qd}), ngm = Cmax / 128, nq = (kMaxBlock + 3) / 4;
   const size_t hd = arch_.head_dim, H = arch_.num_attn_heads;
@@ -1260,7 +1260,7 @@ void Engine::record_block_hybrid(uint32_t mm, hipStream_t st) {
     const LayerPlan& L = layers_[l];
     const HybLayer& Hy = hyb_[l];
     float* hid[1] = {d_bx_};
-    const ProjPlan* in[3] = {&Hy.in0, &Hy.in1, &Hy.in2};
+    const ProjPlan* in[3] = {&Hy.in0, &Hy.in1, (!Hy.full && Hy.has_ab) ? &Hy.ab : &Hy.in2};
     float* outs[3] = {d_bhx0_, d_bhx1_, d_bhx2_};
     enqueue_block_gemv(in, outs, 3, GemvMode::QkvRope, d_bx_, D, L.gamma_in, n_ss, mm, l, st, store, 32);
     if (Hy.full) {
@@ -1301,9 +1301,11 @@ void Engine::record_block_hybrid(uint32_t mm, hipStream_t st) {
       launch_attention(at, st);
       launch_hyb_gate(d_battn_, d_bhx0_, H, hd, mm, st);
     } else {
-      const ProjPlan* inb[1] = {&Hy.in3};
-      float* outb[1] = {d_bhx3_};
-      enqueue_block_gemv(inb, outb, 1, GemvMode::QkvRope, d_bx_, D, L.gamma_in, n_ss, mm, l, st, store, 32);
+      if (!Hy.has_ab) {
+        const ProjPlan* inb[1] = {&Hy.in3};
+        float* outb[1] = {d_bhx3_};
+        enqueue_block_gemv(inb, outb, 1, GemvMode::QkvRope, d_bx_, D, L.gamma_in, n_ss, mm, l, st, store, 32);
+      }
       DnBlockArgs dn{};
       dn.x = d_bhx0_;
       dn.w = Hy.conv_w;
@@ -1313,8 +1315,8 @@ void Engine::record_block_hybrid(uint32_t mm, hipStream_t st) {
       dn.taps = 4;
       dn.x_stride = 8192;
       dn.a = d_bhx2_;
-      dn.b = d_bhx3_;
-      dn.ab_stride = 32;
+      dn.b = Hy.has_ab ? d_bhx2_ + 32 : d_bhx3_;
+      dn.ab_stride = Hy.has_ab ? 64 : 32;
       dn.A_log = Hy.A_log;
       dn.dt_bias = Hy.dt_bias;
       dn.z = d_bhx1_;
@@ -1488,6 +1490,36 @@ bool Engine::plan_hybrid(std::string* err) {
           !plan("in_proj_a", r.in_proj_a, 8, 32, D, false, &H.in2) || !plan("in_proj_b", r.in_proj_b, 8, 32, D, false, &H.in3) ||
           !plan("out_proj", r.out_proj, 1024, D, 4096, true, &H.out))
         return false;
+      {  // a and b side by side: 4 + 4 whole tiles of 8 rows each, copied record for record
+        const size_t na = 4, rec_bytes = stride_;
+        if (r.in_proj_a + na <= record_count_ && r.in_proj_b + na <= record_count_ &&
+            H.in2.kind == WeightKind::FlatW4 && H.in3.kind == WeightKind::FlatW4 && H.in2.wrows == 32 &&
+            H.in3.wrows == 32) {
+          std::vector<uint8_t> ab(2 * na * rec_bytes);
+          std::memcpy(ab.data(), b + 4096 + r.in_proj_a * rec_bytes, na * rec_bytes);
+          std::memcpy(ab.data() + na * rec_bytes, b + 4096 + r.in_proj_b * rec_bytes, na * rec_bytes);
+          FlatPlan fp;
+          plan_flat(ab.data() + cell_off, ab.size() - cell_off, rec_bytes, 2 * na, 64, D, &fp);
+          if (fp.kind == WeightKind::FlatW4 && fp.wrows == 64) {
+            uint8_t* d = static_cast<uint8_t*>(dev_alloc(ab.size()));
+            float2* dc = fp.corr.empty() ? nullptr : static_cast<float2*>(dev_alloc(fp.corr.size() * sizeof(float2)));
+            if (!d || (!fp.corr.empty() && !dc)) {
+              *err = "allocation";
+              return false;
+            }
+            (void)hipMemcpy(d, ab.data(), ab.size(), hipMemcpyHostToDevice);
+            if (dc) (void)hipMemcpy(dc, fp.corr.data(), fp.corr.size() * sizeof(float2), hipMemcpyHostToDevice);
+            H.ab = H.in2;
+            H.ab.base = d + cell_off;
+            H.ab.stride = uint32_t(rec_bytes);
+            H.ab.rows = H.ab.wrows = 64;
+            H.ab.corr = dc;
+            H.ab.corr_kmax = fp.corr_kmax;
+            H.ab.xcodes = nullptr;
+            H.has_ab = true;
+          }
+        }
+      }
       H.conv_w = bf16vec(r.conv1d, 8192 * 4);
       H.A_log = bf16vec(r.a_log, 32);
       H.dt_bias = bf16vec(r.dt_bias, 32);
@@ -1574,12 +1606,14 @@ void Engine::record_step_hybrid(hipStream_t st) {
       const ProjPlan* o[1] = {&H.out};
       enqueue_gemv(o, hid, 1, GemvMode::Accum, d_attn_, uint32_t(q.H * q.hd), nullptr, st);
     } else {
-      const ProjPlan* in[3] = {&H.in0, &H.in1, &H.in2};
+      const ProjPlan* in[3] = {&H.in0, &H.in1, H.has_ab ? &H.ab : &H.in2};
       float* outs[3] = {d_hx0_, d_hx1_, d_hx2_};
       enqueue_gemv(in, outs, 3, GemvMode::QkvRope, d_hidden_, D, L.gamma_in, st, &ra, store);
-      const ProjPlan* inb[1] = {&H.in3};
-      float* outb[1] = {d_hx3_};
-      enqueue_gemv(inb, outb, 1, GemvMode::QkvRope, d_hidden_, D, L.gamma_in, st, &ra, store);
+      if (!H.has_ab) {
+        const ProjPlan* inb[1] = {&H.in3};
+        float* outb[1] = {d_hx3_};
+        enqueue_gemv(inb, outb, 1, GemvMode::QkvRope, d_hidden_, D, L.gamma_in, st, &ra, store);
+      }
       DnConvArgs c{d_hx0_, H.conv_w, d_conv_state_ + size_t(H.lin) * 8192 * 3, d_hconv_, 8192, 4, d_state_};
       launch_dn_conv(c, st);
       DnStepArgs dn{};
@@ -1587,7 +1621,7 @@ void Engine::record_step_hybrid(hipStream_t st) {
       dn.k = d_hconv_ + 2048;
       dn.v = d_hconv_ + 4096;
       dn.a = d_hx2_;
-      dn.b = d_hx3_;
+      dn.b = H.has_ab ? d_hx2_ + 32 : d_hx3_;
       dn.A_log = H.A_log;
       dn.dt_bias = H.dt_bias;
       dn.z = d_hx1_;

@@ -119,6 +119,10 @@ struct HybLayer {
   float *q_norm = nullptr, *k_norm = nullptr;
   float *conv_w = nullptr, *A_log = nullptr, *dt_bias = nullptr, *lin_norm = nullptr;
   uint32_t lin = 0;
+  // in_proj_a and in_proj_b as one 64-row part (rows 0-31 a, 32-63 b): their tiles copied next
+  // to each other at load, so that the in-projections run as one launch (has_ab)
+  ProjPlan ab;
+  bool has_ab = false;
 };
 
 class Engine {
