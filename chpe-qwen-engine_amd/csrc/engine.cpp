@@ -1484,6 +1484,10 @@ bool Engine::plan_hybrid(std::string* err) {
         return false;
       H.q_norm = bf16vec(r.q_norm, 256);
       H.k_norm = bf16vec(r.k_norm, 256);
+      if (!H.q_norm || !H.k_norm) {
+        *err = "allocation";
+        return false;
+      }
     } else {
       if (!plan("in_proj_qkv", r.in_proj_qkv, 2048, 8192, D, false, &H.in0) ||
           !plan("in_proj_z", r.in_proj_z, 1024, 4096, D, false, &H.in1) ||
@@ -1524,6 +1528,10 @@ bool Engine::plan_hybrid(std::string* err) {
       H.A_log = bf16vec(r.a_log, 32);
       H.dt_bias = bf16vec(r.dt_bias, 32);
       H.lin_norm = bf16vec(r.linear_norm, 128);
+      if (!H.conv_w || !H.A_log || !H.dt_bias || !H.lin_norm) {
+        *err = "allocation";
+        return false;
+      }
       H.lin = n_lin++;
     }
   }
@@ -1573,10 +1581,21 @@ void Engine::record_step_hybrid(hipStream_t st) {
     RopeArgs ra = rope_args(l);
     ra.head_dim = 32;  // (Store parts: rows pair within blocks of 32, a divisor of every part's rows)
     float* hid[1] = {d_hidden_};
+    // the normalised in-projections: one launch when the parts share a weight layout, else one
+    // launch per part (as enqueue_qkv)
+    auto in_proj = [&](const ProjPlan* const* ps, float* const* os, int n) {
+      bool same = true;
+      for (int i = 1; i < n; ++i) same = same && ps[i]->kind == ps[0]->kind;
+      if (same) {
+        enqueue_gemv(ps, os, n, GemvMode::QkvRope, d_hidden_, D, L.gamma_in, st, &ra, store);
+        return;
+      }
+      for (int i = 0; i < n; ++i) enqueue_gemv(&ps[i], &os[i], 1, GemvMode::QkvRope, d_hidden_, D, L.gamma_in, st, &ra, store);
+    };
     if (H.full) {
       const ProjPlan* in[3] = {&H.in0, &H.in1, &H.in2};
       float* outs[3] = {d_hx0_, d_hx1_, d_hx2_};
-      enqueue_gemv(in, outs, 3, GemvMode::QkvRope, d_hidden_, D, L.gamma_in, st, &ra, store);
+      in_proj(in, outs, 3);
       const RopeArgs kv = rope_args(l);
       HybQkArgs q{};
       q.state = d_state_;
@@ -1608,11 +1627,11 @@ void Engine::record_step_hybrid(hipStream_t st) {
     } else {
       const ProjPlan* in[3] = {&H.in0, &H.in1, H.has_ab ? &H.ab : &H.in2};
       float* outs[3] = {d_hx0_, d_hx1_, d_hx2_};
-      enqueue_gemv(in, outs, 3, GemvMode::QkvRope, d_hidden_, D, L.gamma_in, st, &ra, store);
+      in_proj(in, outs, 3);
       if (!H.has_ab) {
         const ProjPlan* inb[1] = {&H.in3};
         float* outb[1] = {d_hx3_};
-        enqueue_gemv(inb, outb, 1, GemvMode::QkvRope, d_hidden_, D, L.gamma_in, st, &ra, store);
+        in_proj(inb, outb, 1);
       }
       DnConvArgs c{d_hx0_, H.conv_w, d_conv_state_ + size_t(H.lin) * 8192 * 3, d_hconv_, 8192, 4, d_state_};
       launch_dn_conv(c, st);
