@@ -207,16 +207,20 @@ def stage_probe(workload, iters):
 def trace_summary(path, out):
     """Per-kernel statistics of a `rocprofv3 --kernel-trace` CSV (run_kernel_trace.csv) of a
     bench run, split into the decode phase -- the longest run of dispatches without a block-step
-    GEMV (k_gemv_mt), i.e. the timed decode steps and the stage-timing steps -- and the rest
-    (context build, verify, load); writes a Markdown table to `out`."""
+    GEMV (k_gemv_mt, k_block_gemm), i.e. the timed decode steps and the stage-timing steps -- and
+    the rest (context build, verify, load); block-step kernels are listed per grid shape (one
+    shape per projection); writes a Markdown table to `out`."""
     import csv
     import collections
     rows = []
     with open(path) as f:
         for r in csv.DictReader(f):
-            rows.append((int(r["Start_Timestamp"]), r["Kernel_Name"], int(r["Start_Timestamp"]), int(r["End_Timestamp"])))
+            name = r["Kernel_Name"]
+            if "k_block_" in name or "k_gemv_mt" in name:  # block-step launches: by shape (one per projection)
+                name += f" grid {r.get('Grid_Size_X', r.get('Grid_Size', '?'))}x{r.get('Grid_Size_Y', '')}"
+            rows.append((int(r["Start_Timestamp"]), name, int(r["Start_Timestamp"]), int(r["End_Timestamp"])))
     rows.sort()  # (in start order)
-    blk = [i for i, r in enumerate(rows) if "k_gemv_mt" in r[1]]
+    blk = [i for i, r in enumerate(rows) if "k_gemv_mt" in r[1] or "k_block_gemm" in r[1]]
     cuts = [-1] + blk + [len(rows)]
     a, b = max(zip(cuts, cuts[1:]), key=lambda ab: ab[1] - ab[0])
     phases = {"decode": rows[a + 1:b], "other (context build, verify, load)": rows[:a + 1] + rows[b:]}
@@ -230,6 +234,8 @@ def trace_summary(path, out):
                   "| kernel | calls | avg µs | min µs | max µs | % of phase |", "|---|---|---|---|---|---|"]
         for k, v in sorted(st.items(), key=lambda kv: -sum(kv[1])):
             short = k.replace("chpe::(anonymous namespace)::", "").split("(")[0].replace("void ", "")
+            if " grid " in k:
+                short += " grid " + k.split(" grid ")[-1]
             lines.append(f"| `{short}` | {len(v)} | {sum(v) / len(v):.2f} | {min(v):.2f} | {max(v):.2f} | "
                          f"{100 * sum(v) / total:.2f} |")
         lines.append("")
@@ -302,9 +308,9 @@ def main():
         e.generate(prompt[:W], 1)  # W steps at positions 0..W-1
     block = e.block_ready()
     log(f"building the context: {P} teacher-forced positions "
-        f"({'block steps of 8 tokens' if block else 'decode steps'})")
+        f"({'block steps of 32 tokens' if block else 'decode steps'})")
     t = time.perf_counter()
-    if block:  # positions 0..P-1, every weight read once per 8 tokens; decode continues from P
+    if block:  # positions 0..P-1, every weight read once per 32 tokens; decode continues from P
         first = [e.prefill(prompt)]
     else:
         first = e.generate(prompt, 1)  # teacher-forced context: positions 0..P-1
@@ -395,7 +401,7 @@ def main():
         "cpu_baseline": cpu,
         "context_build_s": round(prefill_s, 3),
         "prefill": {"positions": P, "s": round(prefill_s, 3), "tok_s": round(P / prefill_s, 1),
-                    "mode": "block steps of 8 tokens" if block else "decode steps"},
+                    "mode": "block steps of 32 tokens" if block else "decode steps"},
         "verify": verify,
     }
     print(json.dumps(out), flush=True)

@@ -156,28 +156,40 @@ __global__ void __launch_bounds__(128) k_block_limbs(const float* X, const float
 // (n, q): row n, quarter q of a group) reads it back; rows at kStageRow bytes (16 B of padding:
 // the 16 rows of one read fall on distinct banks).
 constexpr uint32_t kStageRow = 528, kStageBytes = 16 * kStageRow;
-template <int BITS>
+// The stage geometry of a range of RG groups: GPS groups per stage (at most 512 bytes of a row),
+// SPU stages per unit, RB bytes of a row per stage, LPR lanes per row and RPI rows per load
+// instruction, NLD 16-byte loads per lane and stage.
+template <int BITS, int RG>
+struct MtGeom {
+  static constexpr uint32_t GB = BITS == 2 ? 32 : 64;  // code bytes per group and row
+  static constexpr uint32_t GPS = RG * GB <= 512 ? RG : 512 / GB;
+  static constexpr uint32_t SPU = RG / GPS;
+  static constexpr uint32_t RB = GPS * GB, LPR = RB / 16, RPI = 64 / LPR, NLD = 16 / RPI;
+  static constexpr uint32_t kScales = 16 * GPS / 64, kRowsPer = 64 / GPS;  // scales per lane; rows per scale load
+  static_assert(RG % GPS == 0 && LPR * RPI == 64 && NLD * RPI == 16 && kScales >= 1, "");
+};
+template <int BITS, int RG>
 struct MtStage {
-  static constexpr int kScales = BITS == 2 ? 4 : 2;
-  uint4 v[8];            // codes, in the load layout above
-  uint32_t sc[kScales];  // group scales: 4-bit lane l, row 8 i + (l >> 3), group l & 7;
-                         //   2-bit lane l, row 4 i + (l >> 4), group l & 15
+  using G = MtGeom<BITS, RG>;
+  uint4 v[G::NLD];           // codes: lane l, row RPI i + l / LPR, bytes 16 (l % LPR) of the row's RB
+  uint32_t sc[G::kScales];   // group scales: lane l, row kRowsPer i + l / GPS, group l % GPS
 };
 
-template <int NQ, int NW, int BITS>
+// NQ token quads (tables in LDS: NQ x RG groups x 2 KB), RG groups of 128 columns per range
+template <int NQ, int NW, int BITS, int RG>
 __global__ void __launch_bounds__(kWave * NW) k_gemv_mt(BlockGemvArgs a) {
-  constexpr uint32_t GPS = BITS == 2 ? 16 : 8;   // groups per stage
-  constexpr uint32_t SPU = BITS == 2 ? 1 : 2;    // stages per unit
-  constexpr uint32_t GB = BITS == 2 ? 32 : 64;   // code bytes per group and row
-  __shared__ __align__(16) uint4 s_tb[NQ][16][128];
-  __shared__ __align__(16) int4 s_ci[NQ][16][4];
-  __shared__ float s_ew[NQ][16][4];
+  using G = MtGeom<BITS, RG>;
+  constexpr uint32_t GPS = G::GPS, SPU = G::SPU, GB = G::GB;
+  __shared__ __align__(16) uint4 s_tb[NQ][RG][128];
+  __shared__ __align__(16) int4 s_ci[NQ][RG][4];
+  __shared__ float s_ew[NQ][RG][4];
   __shared__ __align__(16) uint8_t s_w[NW][kStageBytes];
   __shared__ uint16_t s_sc[NW][16][GPS];
   const int lane = threadIdx.x & 63, n = lane & 15, q = lane >> 4;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const uint32_t C = a.g.C, ng = C >> 7, range = blockIdx.x, g0 = range * 16;
-  const uint32_t ngr = ng - g0 < 16u ? ng - g0 : 16u;
+  const uint32_t C = a.g.C, ng = C >> 7, range = blockIdx.x, g0 = range * RG;
+  const uint32_t ngr = ng - g0 < uint32_t(RG) ? ng - g0 : uint32_t(RG);
+  const uint32_t nq = a.nq;  // (quads past it hold no tokens: skipped)
   const uint32_t n_units = a.n_units, waves_total = gridDim.y * NW;
   const uint32_t wid = blockIdx.y * NW + wave;
   const bool active = wid < n_units;
@@ -192,39 +204,37 @@ __global__ void __launch_bounds__(kWave * NW) k_gemv_mt(BlockGemvArgs a) {
   };
   // stage j of this wave: unit wid + (j / SPU) * waves_total, groups GPS (j % SPU) .. + GPS - 1
   // of the range (a stage past the last repeats the last: its lines are cached)
-  auto issue = [&](uint32_t j, MtStage<BITS>* st) {
+  auto issue = [&](uint32_t j, MtStage<BITS, RG>* st) {
     j = j < n_stages ? j : n_stages - 1;
     const uint32_t u = wid + (j / SPU) * waves_total, h = j % SPU;
     const int p = int(__builtin_amdgcn_readfirstlane(part_index(u)));
     const GemvPart& P = a.g.part[p];
     const uint8_t* base = P.base;
     const uint32_t stride = P.stride, wr = P.wrows, r0 = (u - P.unit_begin) * kBlockUnit;
-    const uint32_t lb = 16 * (uint32_t(lane) & 31u);  // the lane's bytes in the row's 512
+    const uint32_t lb = 16 * (uint32_t(lane) % G::LPR);  // the lane's bytes in the row's RB
     const uint32_t gl = GPS * h + lb / GB, gc = gl < ngr ? gl : 0u;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const uint32_t r = r0 + 2 * uint32_t(i) + (uint32_t(lane) >> 5), rr = r < wr ? r : 0u;
-      const uint32_t G = rr * ng + g0 + gc;
-      st->v[i] = ld_u128(base + ((G >> 8) * stride + 64 + (G & 255u) * GB + lb % GB));
+    for (int i = 0; i < int(G::NLD); ++i) {
+      const uint32_t r = r0 + G::RPI * uint32_t(i) + uint32_t(lane) / G::LPR, rr = r < wr ? r : 0u;
+      const uint32_t Gi = rr * ng + g0 + gc;
+      st->v[i] = ld_u128(base + ((Gi >> 8) * stride + 64 + (Gi & 255u) * GB + lb % GB));
     }
-    constexpr int kRowsPer = 64 / int(GPS);  // rows per scale load: 8 (4-bit), 4 (2-bit)
 #pragma unroll
-    for (int i = 0; i < MtStage<BITS>::kScales; ++i) {
-      const uint32_t r = r0 + uint32_t(kRowsPer * i) + uint32_t(lane) / GPS, rr = r < wr ? r : 0u;
-      const uint32_t g = GPS * h + (uint32_t(lane) % GPS), G = rr * ng + g0 + (g < ngr ? g : 0u);
-      st->sc[i] = ld_u16(base + ((G >> 8) * stride + 16448 + 48 + 2 * (G & 255u)));
+    for (int i = 0; i < int(G::kScales); ++i) {
+      const uint32_t r = r0 + G::kRowsPer * uint32_t(i) + uint32_t(lane) / GPS, rr = r < wr ? r : 0u;
+      const uint32_t g = GPS * h + (uint32_t(lane) % GPS), Gi = rr * ng + g0 + (g < ngr ? g : 0u);
+      st->sc[i] = ld_u16(base + ((Gi >> 8) * stride + 16448 + 48 + 2 * (Gi & 255u)));
     }
   };
   // into the wave's slot (LDS operations of one wave complete in order: the previous stage's
   // reads are done before these writes land)
-  auto stage = [&](const MtStage<BITS>& st) {
+  auto stage = [&](const MtStage<BITS, RG>& st) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
-      *reinterpret_cast<uint4*>(slot + (2 * i + (lane >> 5)) * kStageRow + 16 * (lane & 31)) = st.v[i];
-    constexpr int kRowsPer = 64 / int(GPS);
+    for (int i = 0; i < int(G::NLD); ++i)
+      *reinterpret_cast<uint4*>(slot + (G::RPI * i + lane / G::LPR) * kStageRow + 16 * (lane % G::LPR)) = st.v[i];
 #pragma unroll
-    for (int i = 0; i < MtStage<BITS>::kScales; ++i)
-      s_sc[wave][kRowsPer * i + lane / int(GPS)][lane % int(GPS)] = uint16_t(st.sc[i]);
+    for (int i = 0; i < int(G::kScales); ++i)
+      s_sc[wave][G::kRowsPer * i + lane / int(GPS)][lane % int(GPS)] = uint16_t(st.sc[i]);
   };
   float acc[NQ];
 #pragma unroll
@@ -254,6 +264,7 @@ __global__ void __launch_bounds__(kWave * NW) k_gemv_mt(BlockGemvArgs a) {
       }
 #pragma unroll
       for (int T = 0; T < NQ; ++T) {
+        if (NQ > 2 && uint32_t(T) >= nq) break;  // (uniform)
         const uint4 t0 = s_tb[T][gk][(uint32_t(q) * 2) * 16 + uint32_t(n)];
         const uint4 t1 = s_tb[T][gk][(uint32_t(q) * 2 + 1) * 16 + uint32_t(n)];
         const i32x4_t A0 = {int(t0.x), int(t0.y), int(t0.z), int(t0.w)};
@@ -281,14 +292,15 @@ __global__ void __launch_bounds__(kWave * NW) k_gemv_mt(BlockGemvArgs a) {
   };
   // the first stage's loads are in flight while the range's operand tables are staged, the next
   // stage's while the current stage is staged and multiplied
-  MtStage<BITS> SA, SB;
+  MtStage<BITS, RG> SA, SB;
   if (active) issue(0, &SA);
-  for (uint32_t i = threadIdx.x; i < uint32_t(NQ) * 16 * 128; i += kWave * NW) {
-    const uint32_t T = i >> 11, gl = (i >> 7) & 15u, e = i & 127u;
+  const uint32_t nqt = NQ > 2 ? (nq < uint32_t(NQ) ? nq : uint32_t(NQ)) : uint32_t(NQ);  // quads with tables
+  for (uint32_t i = threadIdx.x; i < nqt * RG * 128; i += kWave * NW) {
+    const uint32_t T = i / (RG * 128), gl = (i / 128) % RG, e = i % 128;
     s_tb[T][gl][e] = gl < ngr ? a.t.tb[(size_t(T) * ng + g0 + gl) * 128 + e] : make_uint4(0, 0, 0, 0);
   }
-  for (uint32_t i = threadIdx.x; i < uint32_t(NQ) * 16 * 4; i += kWave * NW) {
-    const uint32_t T = i >> 6, gl = (i >> 2) & 15u, k = i & 3u;
+  for (uint32_t i = threadIdx.x; i < nqt * RG * 4; i += kWave * NW) {
+    const uint32_t T = i / (RG * 4), gl = (i / 4) % RG, k = i % 4;
     const bool ok = gl < ngr;
     s_ci[T][gl][k] = ok ? a.t.ci[(size_t(T) * ng + g0 + gl) * 4 + k] : make_int4(0, 0, 0, 0);
     s_ew[T][gl][k] = ok ? a.t.ew[(size_t(T) * ng + g0 + gl) * 4 + k] : 0.0f;
@@ -307,39 +319,268 @@ __global__ void __launch_bounds__(kWave * NW) k_gemv_mt(BlockGemvArgs a) {
   }
 }
 
-// Epilogue: a wave serves 4 outputs (16 lanes each: lane (i, e) = output i, correction entries
-// e, e + 16, ..; after the 16-lane reduction lane (i, t) finishes token t of output i).
-// Outputs: rows of part 0 (Store / Accum / Logits), gate row = up row (SwiGlu), RoPE pairs of
-// every part (QkvRope).
-template <int MODE>
+// Blocks of 9 .. kMaxBlock tokens (the prefill): output-stationary.  A workgroup of kGmWaves
+// waves owns a row block of kGmWaves * U units (wave w: units U w .. U w + U - 1 of the block)
+// and one range of column chunks (GC groups each: 128 code bytes of a row for 4-bit GC = 2).
+// Per chunk:
+//   * the token quads' operand tables of the chunk are in one of two LDS buffers; the workgroup
+//     loads the next chunk's tables into registers meanwhile and writes them to the other
+//     buffer after its multiplies (one barrier per chunk);
+//   * each wave loads the chunk's codes of its 16 U rows (RPI whole rows of RB bytes per
+//     instruction), passes them through its LDS slot into the B layout, with the next chunk's
+//     loads in flight;
+//   * per group and token quad the wave reads the quad's operand once and runs it against its
+//     U units (k_gemv_mt reads it once per unit: U times the LDS reads per weight byte, the
+//     bound of that loop at 32 tokens).
+// The codes enter the matrix cores as signed bytes, code - 8 (4-bit) or the 2-bit two's
+// complement value, so no offset term is needed.  A range's raw row sums go to the partial-sum
+// buffer as k_gemv_mt's; the ranges are few (block_gemv_ranges: enough workgroups to fill the
+// CUs).
+constexpr int kGmWaves = 8;
+constexpr uint32_t kGmUnits = 4, kGmChunk = 2;  // U, GC of the launches
+template <int BITS, int U, int GC>
+struct GmGeom {
+  static constexpr uint32_t GB = BITS == 2 ? 32 : 64;      // code bytes per group and row
+  static constexpr uint32_t RB = GC * GB;                    // code bytes per row and chunk
+  static constexpr uint32_t LPR = RB / 16, RPI = 64 / LPR;   // lanes per row; rows per load
+  static constexpr uint32_t ROWS = 16 * U, NLD = ROWS / RPI;  // the wave's rows; loads per lane
+  static constexpr uint32_t SROW = RB + 16, SLOT = ROWS * SROW;  // slot rows (16 B of padding)
+  static_assert(LPR * RPI == 64 && 16 % RPI == 0 && 16 * GC <= 64, "a load within one unit");
+};
+template <int BITS, int U, int GC>
+struct GmStage {
+  uint4 v[GmGeom<BITS, U, GC>::NLD];  // codes: lane l, row RPI i + l / LPR, bytes 16 (l % LPR)
+  uint32_t sc[U];                     // scales of unit u: lane l < 16 GC, row l / GC, group l % GC
+};
+// bytes b (0..15 each) as signed bytes b - 8, and (0..3 each) as b - 2: + (128 - off), then the
+// sign bit flipped (no carry leaves a byte)
+__device__ __forceinline__ int sbytes4(uint32_t b) { return int((b + 0x78787878u) ^ 0x80808080u); }
+__device__ __forceinline__ int sbytes2(uint32_t b) { return int((b + 0x7e7e7e7eu) ^ 0x80808080u); }
+
+template <int BITS, int U, int GC>
+__global__ void __launch_bounds__(kWave * kGmWaves) k_block_gemm(BlockGemvArgs a) {
+  using G = GmGeom<BITS, U, GC>;
+  constexpr int NQ = int(kMaxBlock / 4);
+  constexpr int kThreads = kWave * kGmWaves;
+  constexpr int kTabPer = NQ * GC * 128 / kThreads;  // table entries per thread and chunk
+  static_assert(NQ * GC * 128 % kThreads == 0 && NQ * GC * 4 <= kThreads, "");
+  __shared__ __align__(16) uint4 s_tb[2][NQ][GC][128];
+  __shared__ float s_ew[2][NQ][GC][4];
+  __shared__ __align__(16) uint8_t s_w[kGmWaves][G::SLOT];
+  __shared__ uint16_t s_sc[kGmWaves][G::ROWS][GC];
+  const int tid = threadIdx.x, lane = tid & 63, n = lane & 15, q = lane >> 4;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(uint32_t(tid) >> 6);
+  const uint32_t ng = a.g.C >> 7, nch = (ng + GC - 1) / GC, range = blockIdx.x;
+  const uint32_t c_begin = uint32_t(uint64_t(range) * nch / gridDim.x);
+  const uint32_t c_end = uint32_t(uint64_t(range + 1) * nch / gridDim.x);
+  const uint32_t nq = a.nq, nqt = nq < uint32_t(NQ) ? nq : uint32_t(NQ);
+  const uint32_t u0 = (blockIdx.y * kGmWaves + wave) * U;  // the wave's first unit
+  uint8_t* slot = s_w[wave];
+  // each unit's part (parts hold consecutive unit ranges from part[p].unit_begin); a unit past
+  // the last reads unit 0's rows and writes nothing
+  const uint8_t* ubase[U];
+  uint32_t ustride[U], uwr[U], ur0[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const uint32_t uu = u0 + uint32_t(u) < a.n_units ? u0 + uint32_t(u) : 0u;
+    int p = 0;
+#pragma unroll
+    for (int k = 1; k < kMaxParts; ++k) p += (k < a.g.n_parts && uu >= a.g.part[k].unit_begin) ? 1 : 0;
+    p = int(__builtin_amdgcn_readfirstlane(p));
+    ubase[u] = a.g.part[p].base;
+    ustride[u] = a.g.part[p].stride;
+    uwr[u] = a.g.part[p].wrows;
+    ur0[u] = (uu - a.g.part[p].unit_begin) * kBlockUnit;
+  }
+  const bool active = u0 < a.n_units;
+  // the chunk's codes and scales of the wave's rows (groups past the last repeat the chunk's first)
+  auto issue = [&](uint32_t c, GmStage<BITS, U, GC>* st) {
+    const uint32_t cg = c * GC;
+    const uint32_t lb = 16 * (uint32_t(lane) % G::LPR), gk = cg + lb / G::GB, gg = gk < ng ? gk : cg;
+#pragma unroll
+    for (int i = 0; i < int(G::NLD); ++i) {
+      const int u = int(G::RPI) * i / 16;
+      const uint32_t r = ur0[u] + (G::RPI * uint32_t(i)) % 16 + uint32_t(lane) / G::LPR, rr = r < uwr[u] ? r : 0u;
+      const uint32_t Gi = rr * ng + gg;
+      st->v[i] = ld_u128(ubase[u] + ((Gi >> 8) * ustride[u] + 64 + (Gi & 255u) * G::GB + lb % G::GB));
+    }
+    const uint32_t sk = uint32_t(lane) % GC, sg = cg + sk < ng ? cg + sk : cg;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const uint32_t r = ur0[u] + uint32_t(lane) / GC, rr = r < uwr[u] ? r : 0u;
+      const uint32_t Gi = rr * ng + sg;
+      st->sc[u] = lane < 16 * GC ? ld_u16(ubase[u] + ((Gi >> 8) * ustride[u] + 16448 + 48 + 2 * (Gi & 255u))) : 0u;
+    }
+  };
+  // into the wave's slot (LDS operations of one wave complete in order: the previous chunk's
+  // reads are done before these writes land)
+  auto stage = [&](const GmStage<BITS, U, GC>& st) {
+#pragma unroll
+    for (int i = 0; i < int(G::NLD); ++i)
+      *reinterpret_cast<uint4*>(slot + (G::RPI * i + lane / G::LPR) * G::SROW + 16 * (lane % G::LPR)) = st.v[i];
+    if (lane < 16 * GC) {
+#pragma unroll
+      for (int u = 0; u < U; ++u) s_sc[wave][16 * u + lane / GC][lane % GC] = uint16_t(st.sc[u]);
+    }
+  };
+  // the operand tables of chunk c: registers, then LDS buffer b (quads past nq and groups past
+  // the last: zero)
+  uint4 pa[kTabPer];
+  float pe = 0.0f;
+  auto fetch_tables = [&](uint32_t c) {
+    const uint32_t cg = c * GC;
+#pragma unroll
+    for (int j = 0; j < kTabPer; ++j) {
+      const uint32_t i = uint32_t(tid + kThreads * j), T = i / (GC * 128), k = (i / 128) % GC, e = i % 128;
+      const bool ok = T < nqt && cg + k < ng;
+      pa[j] = ok ? a.t.tb[(size_t(T) * ng + cg + k) * 128 + e] : make_uint4(0, 0, 0, 0);
+    }
+    if (tid < NQ * GC * 4) {
+      const uint32_t T = uint32_t(tid) / (GC * 4), k = (uint32_t(tid) / 4) % GC, qq = uint32_t(tid) % 4;
+      const bool ok = T < nqt && cg + k < ng;
+      pe = ok ? a.t.ew[(size_t(T) * ng + cg + k) * 4 + qq] : 0.0f;
+    }
+  };
+  auto store_tables = [&](int b) {
+#pragma unroll
+    for (int j = 0; j < kTabPer; ++j) (&s_tb[b][0][0][0])[tid + kThreads * j] = pa[j];
+    if (tid < NQ * GC * 4) (&s_ew[b][0][0][0])[tid] = pe;
+  };
+  float acc[U][NQ];
+#pragma unroll
+  for (int u = 0; u < U; ++u)
+#pragma unroll
+    for (int T = 0; T < NQ; ++T) acc[u][T] = 0.0f;
+  // per group (a group past the last: skipped, uniformly) the U units' operands; per token quad
+  // the 2 U matrix-core products first, then the conversions: lane (n, q) holds token q's limb
+  // sums D0..D3 of row n, combined exactly in pairs (|D| < 2^18: D0 + 2^8 D1 fits), then
+  // lo + 2^16 hi in float, scaled by 2^(e - 30) * the row's group scale
+  auto compute = [&](uint32_t c, int b) {
+    const uint32_t cg = c * GC;
+#pragma unroll
+    for (int k = 0; k < GC; ++k) {
+      if (cg + uint32_t(k) >= ng) break;  // (uniform: only in the last chunk of an odd group count)
+      i32x4_t B0[U], B1[U];
+      float scv[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const uint8_t* row = slot + (16 * u + n) * G::SROW + G::GB * k;
+        if constexpr (BITS == 2) {  // 16 codes in 4 bytes: field f of each byte, as (code ^ 2) - 2
+          const uint2 w2 = *reinterpret_cast<const uint2*>(row + 8 * q);
+          const uint32_t x = w2.x ^ 0xAAAAAAAAu, y = w2.y ^ 0xAAAAAAAAu;
+          B0[u] = i32x4_t{sbytes2(x & 0x03030303u), sbytes2((x >> 2) & 0x03030303u), sbytes2((x >> 4) & 0x03030303u),
+                          sbytes2((x >> 6) & 0x03030303u)};
+          B1[u] = i32x4_t{sbytes2(y & 0x03030303u), sbytes2((y >> 2) & 0x03030303u), sbytes2((y >> 4) & 0x03030303u),
+                          sbytes2((y >> 6) & 0x03030303u)};
+        } else {
+          const uint4 w = *reinterpret_cast<const uint4*>(row + 16 * q);
+          B0[u] = i32x4_t{sbytes4(w.x & 0x0f0f0f0fu), sbytes4((w.x >> 4) & 0x0f0f0f0fu), sbytes4(w.y & 0x0f0f0f0fu),
+                          sbytes4((w.y >> 4) & 0x0f0f0f0fu)};
+          B1[u] = i32x4_t{sbytes4(w.z & 0x0f0f0f0fu), sbytes4((w.z >> 4) & 0x0f0f0f0fu), sbytes4(w.w & 0x0f0f0f0fu),
+                          sbytes4((w.w >> 4) & 0x0f0f0f0fu)};
+        }
+        scv[u] = h2f(s_sc[wave][16 * u + n][k]);
+      }
+#pragma unroll
+      for (int T = 0; T < NQ; ++T) {  // (quads past nq: zero tables, no stores)
+        const uint4 t0 = s_tb[b][T][k][(uint32_t(q) * 2) * 16 + uint32_t(n)];
+        const uint4 t1 = s_tb[b][T][k][(uint32_t(q) * 2 + 1) * 16 + uint32_t(n)];
+        const i32x4_t A0 = {int(t0.x), int(t0.y), int(t0.z), int(t0.w)};
+        const i32x4_t A1 = {int(t1.x), int(t1.y), int(t1.z), int(t1.w)};
+        const float ew = s_ew[b][T][k][q];
+        i32x4_t D[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) D[u] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A0, B0[u], i32x4_t{0, 0, 0, 0}, 0, 0, 0);
+#pragma unroll
+        for (int u = 0; u < U; ++u) D[u] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A1, B1[u], D[u], 0, 0, 0);
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const int lo = D[u][0] + int(uint32_t(D[u][1]) << 8), hi = D[u][2] + int(uint32_t(D[u][3]) << 8);
+          const float f = fmaf(float(hi), 65536.0f, float(lo));
+          acc[u][T] = fmaf(f, ew * scv[u], acc[u][T]);
+        }
+      }
+    }
+  };
+  GmStage<BITS, U, GC> SA, SB;
+  fetch_tables(c_begin);
+  if (active) issue(c_begin, &SA);
+  store_tables(0);
+  __syncthreads();
+  // chunk c (tables in buffer b): its codes in `cur`; the next chunk's codes into `nxt` and its
+  // tables into registers while c is multiplied, then into buffer b ^ 1 (last read by chunk
+  // c - 1, before the previous barrier); the barrier is uniform (c_end is the workgroup's)
+  auto body = [&](uint32_t c, int b, GmStage<BITS, U, GC>& cur, GmStage<BITS, U, GC>& nxt) {
+    const bool more = c + 1 < c_end;
+    if (more) fetch_tables(c + 1);
+    if (active) {
+      stage(cur);
+      if (more) issue(c + 1, &nxt);
+      compute(c, b);
+    }
+    if (more) store_tables(b ^ 1);
+    __syncthreads();
+  };
+  for (uint32_t c = c_begin;; c += 2) {
+    body(c, 0, SA, SB);
+    if (c + 1 >= c_end) break;
+    body(c + 1, 1, SB, SA);
+    if (c + 2 >= c_end) break;
+  }
+  if (!active) return;
+  // row n of unit u, tokens 4 T + q
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const uint32_t uu = u0 + uint32_t(u);
+    if (uu >= a.n_units) break;
+    const bool row_ok = ur0[u] + uint32_t(n) < uwr[u];
+    float* dst = a.partial + (size_t(range) * a.rows_all + uu * kBlockUnit + uint32_t(n)) * kMaxBlock;
+#pragma unroll
+    for (int T = 0; T < NQ; ++T) {
+      const uint32_t tk = 4 * uint32_t(T) + uint32_t(q);
+      if (tk < a.m) dst[tk] = row_ok ? acc[u][T] : 0.0f;
+    }
+  }
+}
+
+// Epilogue: a wave serves 64 / TW outputs, TW lanes each (TW >= m): lane (i, t) = output i,
+// token t.  Per token: the ranges' raw sums in range order, the outlier corrections of the row
+// in entry order (w * x[col] of the token: the flat tiles' replace deltas, the cells' added
+// outliers), then the batch-1 step's epilogue.  Outputs: rows of part 0 (Store / Accum /
+// Logits), gate row = up row (SwiGlu), RoPE pairs of every part (QkvRope).
+template <int MODE, int TW>
 __global__ void __launch_bounds__(256) k_block_epi(BlockGemvArgs a) {
   constexpr bool kSwi = MODE == int(GemvMode::SwiGlu);
   constexpr bool kRope = MODE == int(GemvMode::QkvRope);
   constexpr bool kLogits = MODE == int(GemvMode::Logits);
+  constexpr bool kAcc = MODE == int(GemvMode::Accum);
   constexpr int NR = (kSwi || kRope) ? 2 : 1;  // rows per output
-  const int lane = threadIdx.x & 63, e0 = lane & 15, i = lane >> 4, wave = threadIdx.x >> 6;
-  const uint32_t m = a.m, ranges = (a.g.C + kBlockRange - 1) / kBlockRange;
+  constexpr int OPW = 64 / TW;                 // outputs per wave
+  static_assert(TW <= int(kMaxBlock) && 64 % TW == 0, "");
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const uint32_t t = uint32_t(lane % TW), i = uint32_t(lane / TW);
+  const uint32_t m = a.m, ranges = a.ranges;
+  const bool live = t < m;
   const uint32_t half = a.g.rope.head_dim / 2;
+  const size_t rstride = size_t(a.rows_all) * kMaxBlock;  // one range of the partial sums
   uint32_t total = 0;
   if constexpr (kRope) {
     for (int p = 0; p < a.g.n_parts; ++p) total += a.g.part[p].rows / 2;
   } else {
     total = a.g.part[0].rows;
   }
-  float bv = -1e30f;
+  float bv = -1e30f, sq = 0.0f;  // Logits: the lane's best value / index; Accum: Σy² of the token
   uint32_t bi = 0xffffffffu, nf = 0;
-  float sq = 0.0f;  // Accum: this lane's sum of y^2 over its token's updated rows
+  const bool brk = (kRope || kAcc) && live && a.brk[t] != 0u;  // (k_block_limbs): no KV append, the residual stays
   const uint32_t pos0 = kRope ? a.state->pos : 0u;
-  // token e0's break (k_block_limbs): no KV append, the residual stays
-  const bool brk = (kRope || MODE == int(GemvMode::Accum)) && uint32_t(e0) < m && a.brk[e0] != 0u;
-  for (uint32_t q4 = blockIdx.x * 4 + uint32_t(wave); q4 * 4 < total; q4 += gridDim.x * 4) {
-    const uint32_t o = q4 * 4 + uint32_t(i);
-    const bool ok = o < total;
+  for (uint32_t ob = (blockIdx.x * 4 + uint32_t(wave)) * OPW; ob < total; ob += gridDim.x * 4 * OPW) {
+    const uint32_t o = ob + i;
+    if (o >= total || !live) continue;
     // the output's part and rows
     int p = 0;
     uint32_t rows_k[NR];
     if constexpr (kRope) {
-      uint32_t oo = ok ? o : 0u;
+      uint32_t oo = o;
       while (p + 1 < a.g.n_parts && oo >= a.g.part[p].rows / 2) {
         oo -= a.g.part[p].rows / 2;
         ++p;
@@ -348,78 +589,57 @@ __global__ void __launch_bounds__(256) k_block_epi(BlockGemvArgs a) {
       rows_k[0] = lo;
       rows_k[1] = lo + half;
     } else {
-      rows_k[0] = ok ? o : 0u;
-      if constexpr (kSwi) rows_k[1] = rows_k[0];
+      rows_k[0] = o;
+      if constexpr (kSwi) rows_k[1] = o;
     }
-    // the ranges' raw sums of token t = e0 of each row (requested before the corrections)
-    const uint32_t t = uint32_t(e0);
-    float sum_k[NR];
-#pragma unroll
-    for (int k = 0; k < NR; ++k) {
-      const GemvPart& P = a.g.part[kSwi ? k : p];
-      const uint32_t at = P.unit_begin * kBlockUnit + rows_k[k];
-      float acc_s = 0.0f;
-      if (ok && t < m)
-        for (uint32_t rg = 0; rg < ranges; ++rg) acc_s += a.partial[(size_t(rg) * a.rows_all + at) * kMaxBlock + t];
-      sum_k[k] = acc_s;
-    }
-    // corrections of each row, all tokens
-    float cor[NR][kMaxBlock];
+    float v[NR];
 #pragma unroll
     for (int k = 0; k < NR; ++k) {
       const GemvPart& P = a.g.part[kSwi ? k : p];
       const uint32_t r = rows_k[k];
+      const float* ps = a.partial + size_t(P.unit_begin * kBlockUnit + r) * kMaxBlock + t;
+      float acc_s = 0.0f;  // (four loads in flight, added in range order)
+      uint32_t rg = 0;
+      for (; rg + 4 <= ranges; rg += 4) {
+        const float p0 = ps[rg * rstride], p1 = ps[(rg + 1) * rstride];
+        const float p2 = ps[(rg + 2) * rstride], p3 = ps[(rg + 3) * rstride];
+        acc_s += p0;
+        acc_s += p1;
+        acc_s += p2;
+        acc_s += p3;
+      }
+      for (; rg < ranges; ++rg) acc_s += ps[rg * rstride];
+      float c = 0.0f;
       const float2* corr = P.corr;
       const uint32_t kmax = P.corr_kmax;
+      if (corr != nullptr && r < P.wrows) {
+        // eight entries' loads, then their eight columns' loads, in flight together
+        const float2* ce = corr + size_t(r) * kmax;
+        uint32_t e = 0;
+        for (; e + 8 <= kmax; e += 8) {
+          float2 cv[8];
+          float xc[8];
 #pragma unroll
-      for (int t = 0; t < int(kMaxBlock); ++t) cor[k][t] = 0.0f;
-      if (corr != nullptr && ok && r < P.wrows) {
-        // two entries per trip, their loads together (unused slots read entry 0, masked)
-        for (uint32_t e = uint32_t(e0); e < kmax; e += 32) {
-          const bool u1 = e + 16 < kmax;
-          const float2 c0 = corr[size_t(r) * kmax + e];
-          const float2 c1 = corr[size_t(r) * kmax + (u1 ? e + 16 : e)];
-          const float w0 = c0.y, w1 = u1 ? c1.y : 0.0f;
-          const float4* x0 = reinterpret_cast<const float4*>(a.t.xt + size_t(__float_as_uint(c0.x)) * kMaxBlock);
-          const float4* x1 = reinterpret_cast<const float4*>(a.t.xt + size_t(__float_as_uint(c1.x)) * kMaxBlock);
-          const float4 xa = x0[0], xb = x0[1], ya = x1[0], yb = x1[1];
-          const float xs0[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
-          const float xs1[8] = {ya.x, ya.y, ya.z, ya.w, yb.x, yb.y, yb.z, yb.w};
+          for (int j = 0; j < 8; ++j) cv[j] = ce[e + uint32_t(j)];
 #pragma unroll
-          for (int tt = 0; tt < int(kMaxBlock); ++tt) {  // padding entries (w = 0) are skipped
-            float c = cor[k][tt];
-            c = w0 != 0.0f ? fmaf(w0, xs0[tt], c) : c;
-            c = w1 != 0.0f ? fmaf(w1, xs1[tt], c) : c;
-            cor[k][tt] = c;
-          }
+          for (int j = 0; j < 8; ++j) xc[j] = a.t.xt[size_t(__float_as_uint(cv[j].x)) * kMaxBlock + t];
+#pragma unroll
+          for (int j = 0; j < 8; ++j) c = cv[j].y != 0.0f ? fmaf(cv[j].y, xc[j], c) : c;  // (padding: w = 0)
+        }
+        for (; e < kmax; ++e) {
+          const float2 cv = ce[e];
+          const float xc = a.t.xt[size_t(__float_as_uint(cv.x)) * kMaxBlock + t];
+          c = cv.y != 0.0f ? fmaf(cv.y, xc, c) : c;
         }
       }
-#pragma unroll
-      for (int t = 0; t < int(kMaxBlock); ++t) {
-        float v = cor[k][t];
-        v = pair_sum(v, 1);
-        v = pair_sum(v, 2);
-        v = pair_sum(v, 4);
-        v = pair_sum(v, 8);
-        cor[k][t] = v;
-      }
-    }
-    // lane (i, t): token t of the output
-    if (!ok || t >= m) continue;
-    float v[NR];
-#pragma unroll
-    for (int k = 0; k < NR; ++k) {
-      float c = cor[k][0];
-#pragma unroll
-      for (int tt = 1; tt < int(kMaxBlock); ++tt) c = t == uint32_t(tt) ? cor[k][tt] : c;
-      v[k] = sum_k[k] + c;
+      v[k] = acc_s + c;
     }
     const GemvPart& P0 = a.g.part[kSwi ? 0 : p];
     const uint32_t r = rows_k[0];
     float* y = P0.y + size_t(t) * P0.rows;
     if constexpr (MODE == int(GemvMode::Store)) {
       y[r] = v[0] + (P0.bias ? P0.bias[r] : 0.0f);
-    } else if constexpr (MODE == int(GemvMode::Accum)) {
+    } else if constexpr (kAcc) {
       const bool upd = r < P0.wrows && !brk;  // rows past the tiles stay
       const float yo = y[r], yn = upd ? yo + v[0] : yo;
       if (upd) y[r] = yn;
@@ -433,9 +653,9 @@ __global__ void __launch_bounds__(256) k_block_epi(BlockGemvArgs a) {
       const uint32_t pos = pos0 + t, d = r % (2 * half);
       float o0 = lo, o1 = hi;
       if (P0.rope_role < kRoleV && pos < a.rope_rows) {  // applyRope :195-216
-        const float c = a.rope_cos[size_t(pos) * half + d], sn = a.rope_sin[size_t(pos) * half + d];
-        o0 = lo * c - hi * sn;
-        o1 = lo * sn + hi * c;
+        const float cc = a.rope_cos[size_t(pos) * half + d], sn = a.rope_sin[size_t(pos) * half + d];
+        o0 = lo * cc - hi * sn;
+        o1 = lo * sn + hi * cc;
       }
       if (P0.rope_role == kRoleQ || P0.rope_role == kRoleStore) {  // (Store: as computed)
         y[r] = o0;
@@ -468,20 +688,20 @@ __global__ void __launch_bounds__(256) k_block_epi(BlockGemvArgs a) {
     }
   }
   if constexpr (kLogits) {
-    // per token (lanes e0 = t of the 4 outputs), then over the waves
+    // per token over the wave's outputs (lanes t + TW i), then over the waves
+    __shared__ float s_bv[4][TW];
+    __shared__ uint32_t s_bi[4][TW], s_nf[4][TW];
 #pragma unroll
-    for (int o = 16; o <= 32; o <<= 1) {
-      const float ov = pair_val(bv, o);
-      const uint32_t oi = pair_u(bi, o);
-      nf |= pair_u(nf, o);
+    for (int off = TW; off < 64; off <<= 1) {
+      const float ov = pair_val(bv, off);
+      const uint32_t oi = pair_u(bi, off);
+      nf |= pair_u(nf, off);
       if (better(ov, oi, bv, bi)) {
         bv = ov;
         bi = oi;
       }
     }
-    __shared__ float s_bv[4][16];
-    __shared__ uint32_t s_bi[4][16], s_nf[4][16];
-    if (lane < 16) {
+    if (lane < TW) {
       s_bv[wave][lane] = bv;
       s_bi[wave][lane] = bi;
       s_nf[wave][lane] = nf;
@@ -501,16 +721,16 @@ __global__ void __launch_bounds__(256) k_block_epi(BlockGemvArgs a) {
       a.partials[size_t(tk) * a.epi_blocks + blockIdx.x] = ArgmaxPartial{b, bx, f, 0u};
     }
   }
-  if constexpr (MODE == int(GemvMode::Accum)) {
-    // the workgroup's sums of y^2 per token for the next GEMV's RMS norm (lanes e0 = t of the 4
+  if constexpr (kAcc) {
+    // the workgroup's sums of y^2 per token for the next GEMV's RMS norm (over the wave's
     // outputs, then over the waves, in a fixed order)
     if (a.ssp_out) {
-      float v = pair_sum(sq, 16);
-      v = pair_sum(v, 32);
-      __shared__ float s_sq[4][16];
-      if (lane < 16) s_sq[wave][lane] = v;
+      __shared__ float s_sq[4][TW];
+#pragma unroll
+      for (int off = TW; off < 64; off <<= 1) sq = pair_sum(sq, off);
+      if (lane < TW) s_sq[wave][lane] = sq;
       __syncthreads();
-      if (threadIdx.x < kMaxBlock) {
+      if (threadIdx.x < m) {
         const uint32_t tk = threadIdx.x;
         a.ssp_out[size_t(blockIdx.x) * kMaxBlock + tk] = (s_sq[0][tk] + s_sq[1][tk]) + (s_sq[2][tk] + s_sq[3][tk]);
       }
@@ -582,21 +802,47 @@ void launch_block_limbs(const BlockGemvArgs& a, hipStream_t st) {
   else a.g.gamma ? go(&k_block_limbs<true, 4>, chk) : go(&k_block_limbs<false, 4>, 0u);
 }
 
+uint32_t block_gemv_ranges(uint32_t n_units, uint32_t C, uint32_t m) {
+  if (m <= 8) return (C + kBlockRange - 1) / kBlockRange;
+  // k_block_gemm: the fewest ranges for the least time in rounds of one workgroup per CU, a
+  // range costing about two chunks more (its partial sums written and read back)
+  const uint32_t rb = (n_units + kGmWaves * kGmUnits - 1) / (kGmWaves * kGmUnits);
+  const uint32_t nch = (C / 128 + kGmChunk - 1) / kGmChunk;
+  constexpr uint32_t kSlots = 256;
+  uint32_t best = 1, best_cost = 0xffffffffu;
+  for (uint32_t R = 1; R <= nch; ++R) {
+    const uint32_t rounds = (rb * R + kSlots - 1) / kSlots, cost = rounds * ((nch + R - 1) / R + 2);
+    if (cost < best_cost) {
+      best_cost = cost;
+      best = R;
+    }
+  }
+  return best;
+}
+
 uint32_t launch_block_gemv(BlockGemvArgs& a, hipStream_t st) {
-  const uint32_t ranges = (a.g.C + kBlockRange - 1) / kBlockRange;
-  // workgroups per range: at most 256 workgroups of 8 waves in all, one round on the 256 CUs (one
-  // workgroup per CU: the LDS tables and stage slots; a 257th workgroup would double the launch)
-  uint32_t per = 256 / ranges;
-  if (per == 0) per = 1;
-  const uint32_t need = (a.n_units + 7) / 8;  // (a wave per unit at least)
-  if (per > need) per = need;
-  const dim3 grid(ranges, per);
-  if (a.bits == 2) {
-    if (a.nq <= 1) launch_kernel(&k_gemv_mt<1, 8, 2>, grid, dim3(512), st, a);
-    else launch_kernel(&k_gemv_mt<2, 8, 2>, grid, dim3(512), st, a);
+  const uint32_t ranges = block_gemv_ranges(a.n_units, a.g.C, a.m);
+  a.ranges = ranges;
+  if (a.m > 8) {  // output-stationary: row blocks of kGmWaves waves x kGmUnits units, few ranges
+    const dim3 grid(ranges, (a.n_units + kGmWaves * kGmUnits - 1) / (kGmWaves * kGmUnits));
+    if (a.bits == 2) launch_kernel(&k_block_gemm<2, kGmUnits, kGmChunk>, grid, dim3(kWave * kGmWaves), st, a);
+    else launch_kernel(&k_block_gemm<4, kGmUnits, kGmChunk>, grid, dim3(kWave * kGmWaves), st, a);
   } else {
-    if (a.nq <= 1) launch_kernel(&k_gemv_mt<1, 8, 4>, grid, dim3(512), st, a);
-    else launch_kernel(&k_gemv_mt<2, 8, 4>, grid, dim3(512), st, a);
+    // up to 8 tokens: ranges of 2048 columns (the tables of 2 quads in LDS), workgroups per
+    // range: at most 256 workgroups of 8 waves in all, one round on the 256 CUs (one workgroup
+    // per CU: the LDS tables and stage slots; a 257th workgroup would double the launch)
+    uint32_t per = 256 / ranges;
+    if (per == 0) per = 1;
+    const uint32_t need = (a.n_units + 7) / 8;  // (a wave per unit at least)
+    if (per > need) per = need;
+    const dim3 grid(ranges, per);
+    if (a.bits == 2) {
+      if (a.nq <= 1) launch_kernel(&k_gemv_mt<1, 8, 2, 16>, grid, dim3(512), st, a);
+      else launch_kernel(&k_gemv_mt<2, 8, 2, 16>, grid, dim3(512), st, a);
+    } else {
+      if (a.nq <= 1) launch_kernel(&k_gemv_mt<1, 8, 4, 16>, grid, dim3(512), st, a);
+      else launch_kernel(&k_gemv_mt<2, 8, 4, 16>, grid, dim3(512), st, a);
+    }
   }
   uint32_t outs = 0;
   if (GemvMode(a.g.mode) == GemvMode::QkvRope) {
@@ -604,17 +850,26 @@ uint32_t launch_block_gemv(BlockGemvArgs& a, hipStream_t st) {
   } else {
     outs = a.g.part[0].rows;
   }
-  uint32_t eb = (outs + 15) / 16;  // one pass: 16 outputs per workgroup
-  if (eb > kMaxSsPartials) eb = kMaxSsPartials;  // (Accum leaves a Σy² partial per workgroup)
-  if (GemvMode(a.g.mode) == GemvMode::Logits && eb > 512) eb = 512;
+  // lanes per output: the token count rounded up to 8, 16 or 32; one pass of 4 waves
+  const uint32_t tw = a.m <= 8 ? 8u : a.m <= 16 ? 16u : 32u, per_wg = 4 * (64 / tw);
+  uint32_t eb = (outs + per_wg - 1) / per_wg;  // (one pass: the most latency chains in flight)
+  if (GemvMode(a.g.mode) == GemvMode::Accum && eb > 1024) eb = 1024;  // (a Σy² partial per workgroup)
+  if (GemvMode(a.g.mode) == GemvMode::Logits && eb > 512) eb = 512;   // (an argmax partial per workgroup)
   a.epi_blocks = eb;
+  auto epi = [&](auto k8, auto k16, auto k32) {
+    if (tw == 8) launch_kernel(k8, dim3(eb), dim3(256), st, a);
+    else if (tw == 16) launch_kernel(k16, dim3(eb), dim3(256), st, a);
+    else launch_kernel(k32, dim3(eb), dim3(256), st, a);
+  };
+#define CHPE_EPI(M) epi(&k_block_epi<int(M), 8>, &k_block_epi<int(M), 16>, &k_block_epi<int(M), 32>)
   switch (GemvMode(a.g.mode)) {
-    case GemvMode::Store: launch_kernel(&k_block_epi<int(GemvMode::Store)>, dim3(eb), dim3(256), st, a); break;
-    case GemvMode::Accum: launch_kernel(&k_block_epi<int(GemvMode::Accum)>, dim3(eb), dim3(256), st, a); break;
-    case GemvMode::SwiGlu: launch_kernel(&k_block_epi<int(GemvMode::SwiGlu)>, dim3(eb), dim3(256), st, a); break;
-    case GemvMode::Logits: launch_kernel(&k_block_epi<int(GemvMode::Logits)>, dim3(eb), dim3(256), st, a); break;
-    case GemvMode::QkvRope: launch_kernel(&k_block_epi<int(GemvMode::QkvRope)>, dim3(eb), dim3(256), st, a); break;
+    case GemvMode::Store: CHPE_EPI(GemvMode::Store); break;
+    case GemvMode::Accum: CHPE_EPI(GemvMode::Accum); break;
+    case GemvMode::SwiGlu: CHPE_EPI(GemvMode::SwiGlu); break;
+    case GemvMode::Logits: CHPE_EPI(GemvMode::Logits); break;
+    case GemvMode::QkvRope: CHPE_EPI(GemvMode::QkvRope); break;
   }
+#undef CHPE_EPI
   return eb;
 }
 

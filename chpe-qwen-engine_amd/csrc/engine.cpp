@@ -1019,15 +1019,22 @@ bool Engine::plan_block(std::string* err) {
       if (p->kind == WeightKind::Cell16W4 && !plan_cell_corrections(p, p->cols, err)) return false;
   if (lm_head_.kind == WeightKind::Cell16W4 && !plan_cell_corrections(&lm_head_, D, err)) return false;
   auto units = [](size_t rows) { return (rows + kBlockUnit - 1) / kBlockUnit; };
-  auto ranges = [](size_t C) { return (C + kBlockRange - 1) / kBlockRange; };
-  size_t part_floats = 0;  // ranges x kMaxBlock x rows_all, the largest GEMV
-  part_floats = std::max(part_floats, ranges(D) * kBlockUnit * (units(qd) + 2 * units(kvd)));
-  part_floats = std::max(part_floats, ranges(qd) * kBlockUnit * units(D));
-  part_floats = std::max(part_floats, ranges(D) * kBlockUnit * 2 * units(I));
-  part_floats = std::max(part_floats, ranges(I) * kBlockUnit * units(D));
-  part_floats = std::max(part_floats, ranges(D) * kBlockUnit * units(V));
-  if (cfg_.hybrid)  // in_proj_qkv + z + a (8192 + 4096 + 32 rows), q + k + v (8192 + 2 x 1024), out_proj
-    part_floats = std::max(part_floats, ranges(D) * kBlockUnit * (units(8192) + units(4096) + units(64)));
+  size_t part_floats = 0;  // ranges x kMaxBlock x rows_all, the largest GEMV at any token count
+  auto need = [&](size_t n_units, size_t C) {
+    const size_t r = std::max(block_gemv_ranges(uint32_t(n_units), uint32_t(C), 8),
+                              block_gemv_ranges(uint32_t(n_units), uint32_t(C), kMaxBlock));
+    part_floats = std::max(part_floats, r * kBlockUnit * n_units);
+  };
+  need(units(qd) + 2 * units(kvd), D);
+  need(units(D), qd);
+  need(2 * units(I), D);
+  need(units(D), I);
+  need(units(V), D);
+  if (cfg_.hybrid) {  // in_proj_qkv + z + a/b (8192 + 4096 + 64 rows), q + k + v (8192 + 2 x 1024), out_proj
+    need(units(8192) + units(4096) + units(64), D);
+    need(units(8192) + 2 * units(1024), D);
+    need(units(D), 4096);
+  }
   part_floats *= kMaxBlock;
   const size_t Cmax = std::max({D, I, qd}), ngm = Cmax / 128, nq = (kMaxBlock + 3) / 4;
   const size_t hd = arch_.head_dim, H = arch_.num_attn_heads;
@@ -1042,6 +1049,7 @@ bool Engine::plan_block(std::string* err) {
   d_bmlp_ = fa(kMaxBlock * I);
   d_blog_ = fa(kMaxBlock * V);
   d_bpartial_ = fa(part_floats);
+  bpart_floats_ = part_floats;
   d_bpml_ = fa(kMaxBlock * H * n_chunks_ * 2);
   d_bpacc_ = fa(kMaxBlock * H * n_chunks_ * hd);
   d_bss_ = fa(size_t(kMaxSsPartials) * kMaxBlock);
@@ -1152,6 +1160,10 @@ uint32_t Engine::enqueue_block_gemv(const ProjPlan* const* parts, float* const* 
   b.rows_all = kBlockUnit * units;
   b.partial = d_bpartial_;
   b.brk = d_bbrk_;
+  if (size_t(block_gemv_ranges(units, C, m)) * b.rows_all * kMaxBlock > bpart_floats_) {  // (the plan's sizes)
+    bpart_short_ = true;
+    return 1;
+  }
   if (mode == GemvMode::QkvRope) {
     b.g.rope = rope_args(layer);
     if (pair_dim) b.g.rope.head_dim = pair_dim;
@@ -1184,13 +1196,21 @@ int Engine::block_forward(const uint32_t* tokens, size_t m, size_t pos, uint32_t
     if (!bgraph_exec_[m]) {
       if (hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal) != hipSuccess) return -3;
       record_block(mm, st);
-      if (hipStreamEndCapture(st, &bgraph_[m]) != hipSuccess ||
-          hipGraphInstantiate(&bgraph_exec_[m], bgraph_[m], nullptr, nullptr, 0) != hipSuccess)
+      if (hipStreamEndCapture(st, &bgraph_[m]) != hipSuccess) return -3;
+      if (bpart_short_) {
+        (void)hipGraphDestroy(bgraph_[m]);
+        bgraph_[m] = nullptr;
         return -3;
+      }
+      if (hipGraphInstantiate(&bgraph_exec_[m], bgraph_[m], nullptr, nullptr, 0) != hipSuccess) return -3;
     }
     if (hipGraphLaunch(bgraph_exec_[m], st) != hipSuccess) return -3;
   } else {
     record_block(mm, st);
+    if (bpart_short_) {
+      (void)hipStreamSynchronize(st);
+      return -3;
+    }
   }
   if (hipMemcpyAsync(h_bout_, d_bout_, m * 4, hipMemcpyDeviceToHost, st) != hipSuccess ||
       hipMemcpyAsync(h_result_, d_result_, sizeof(StepResult), hipMemcpyDeviceToHost, st) != hipSuccess)

@@ -294,6 +294,8 @@ class Engine {
   uint32_t* d_bbrk_ = nullptr;  // [kMaxBlock] per-token break flags of the block step
   float *d_bx_ = nullptr, *d_bq_ = nullptr, *d_battn_ = nullptr, *d_bmlp_ = nullptr, *d_blog_ = nullptr;
   float *d_bpartial_ = nullptr, *d_bpml_ = nullptr, *d_bpacc_ = nullptr;
+  size_t bpart_floats_ = 0;   // d_bpartial_'s capacity
+  bool bpart_short_ = false;  // a block GEMV's partial sums did not fit (not launched; the block step fails)
   float* d_bss_ = nullptr;  // [kMaxSsPartials][kMaxBlock]: Σx² partials of the hidden rows for the next norm
   // the hybrid's block activations, [kMaxBlock][rows]: the in-projections' outputs (as d_hx0_ ..
   // d_hx3_) and the conv outputs

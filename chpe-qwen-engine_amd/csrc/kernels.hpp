@@ -263,8 +263,8 @@ uint32_t launch_gemv_flat_poly(const GemvArgs& a, const uint32_t* n_tiles, float
 
 // ---- the block step: m <= kMaxBlock tokens at consecutive positions through flat 4- or 2-bit tiles,
 // every weight read once for all m tokens (batch-M verify, chunked prefill) ----------------------
-constexpr uint32_t kMaxBlock = 8;
-constexpr uint32_t kBlockRange = 2048;  // input columns per workgroup of the block GEMV
+constexpr uint32_t kMaxBlock = 32;
+constexpr uint32_t kBlockRange = 2048;  // input columns per workgroup of the block GEMV (<= 8 tokens)
 constexpr uint32_t kBlockUnit = 16;     // weight rows per unit of the block GEMV
 
 constexpr uint32_t kMaxSsPartials = 4096;  // Σx² partials a block kernel may leave for the next GEMV
@@ -301,6 +301,7 @@ struct BlockGemvArgs {
   uint32_t epi_blocks;      // set by launch_block_gemv
   uint32_t* brk;            // [kMaxBlock]: token t broke (StepState::broken), cleared by the block's embedding
   uint32_t bits;            // the parts' code width: 4 or 2 (flat tiles)
+  uint32_t ranges;          // column ranges of the partial sums (set by launch_block_gemv)
 };
 
 struct BlockFinishArgs {
@@ -320,6 +321,9 @@ void launch_block_embed(const EmbedArgs& e, const uint32_t* tokens, uint32_t m, 
 // launch_block_gemv returns the epilogue's workgroups (Logits / Σy² partials)
 void launch_block_limbs(const BlockGemvArgs& a, hipStream_t stream);
 uint32_t launch_block_gemv(BlockGemvArgs& a, hipStream_t stream);
+// the column ranges (partial sums per output row and token) launch_block_gemv uses for m tokens
+// through n_units units of C columns
+uint32_t block_gemv_ranges(uint32_t n_units, uint32_t C, uint32_t m);
 void launch_block_finish(const BlockFinishArgs& a, hipStream_t stream);
 
 // launchers; all enqueue on `stream` and never synchronise

@@ -74,13 +74,13 @@ int chpe_generate(void *ctx, const uint32_t *prompt, size_t n_prompt, size_t n_g
  * equivalent is m forwardDecode calls, src/chpe_engine.zig:1663-1803, whose KV write at pos
  * overwrites the row, :1693-1697): on archives of flat 4- or 2-bit tiles or 4-bit 16-row cells
  * (chpe_block_ready) and
- * 2 <= m <= 8 as one block step that reads every weight once for the m drafts, with each draft's
+ * 2 <= m <= 32 as one block step that reads every weight once for the m drafts, with each draft's
  * arithmetic that of the decode step up to the order of the float sums; otherwise m replays of
  * the decode step, bit-identical.  last_* report the final step; chpe_get_last_logits gives
  * its logits.  Returns 0, -1 bad args, -2 pos + m > max_seq_len, -3 device error. */
 int chpe_verify(void *ctx, const uint32_t *drafts, size_t m, size_t pos, uint32_t *out_argmax);
 /* Prefill: positions 0..num_tokens-1 teacher-forced as chpe_forward_tokens, in block steps of
- * up to 8 tokens that read every weight once per block (archives of flat 4- or 2-bit tiles or
+ * up to 32 tokens that read every weight once per block (archives of flat 4- or 2-bit tiles or
  * 4-bit 16-row cells; others:
  * the sequential steps).  Each token's arithmetic is the decode step's up to the order of the
  * float sums; the KV cache holds the same rows.  Leaves the decode state at (the last argmax,

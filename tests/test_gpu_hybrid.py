@@ -119,11 +119,16 @@ def test_hybrid_restart_and_block_step(a9h):
                 if m == 4:  # the decode state continues after the block: the next draft's step
                     am, lg = e.decode_step(int(drafts[4]), n + 4)
                     compare_logits(lg, seq[4][1], "decode step after verify 4", rel)
-            say("hybrid: prefill (block steps of 6) vs forward_tokens")
+            say("hybrid: prefill (a block step of 6) vs forward_tokens")
             _, lp = e.prefill(prompt, want_logits=True)
             compare_logits(lp, l1, "prefill vs forward_tokens", rel)
             am, lg = e.decode_step(int(drafts[0]), n)
             compare_logits(lg, seq[0][1], "decode step after prefill", rel)
+            say("hybrid: prefill of 40 positions (blocks of 32 + 8) vs forward_tokens")
+            long = prompt_of(13, 40)
+            _, ls = e.forward_tokens(long, want_logits=True)
+            _, lb = e.prefill(long, want_logits=True)
+            compare_logits(lb, ls, "prefill 40 vs forward_tokens", rel)
             if kv16:
                 # a step at position 1 continues from the state position 0 left
                 a = e.decode_step(int(prompt[0]), 0)[1]
@@ -153,7 +158,7 @@ def test_hybrid_block_step_matches_oracle(a9h):
     o = orc.Oracle(a9h, arch=1, max_seq_len=64, kv_f16=False, threads=threads())
     o.set_hybrid(True)
     try:
-        say("hybrid: prefill of 11 positions (blocks of 8 + 3) vs the oracle")
+        say("hybrid: prefill of 11 positions (one block) vs the oracle")
         _, lp = e.prefill(prompt, want_logits=True)
         for pos, t in enumerate(prompt):
             o.forward(int(t), pos)

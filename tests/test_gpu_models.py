@@ -146,10 +146,12 @@ def top2_gap(lg):
 
 
 def run_block(path, arch, vocab, seed, oracle_check, block=True):
-    """The block step (every weight read once for up to 8 tokens; no reference code, defined as
+    """The block step (every weight read once for up to 32 tokens; no reference code, defined as
     the decode steps it replaces) against the decode step on the same engine: chpe_prefill vs
     chpe_forward_tokens (the last position's logits, then one decode step on each cache, so the
-    KV rows agree), chpe_verify of 8 drafts vs 8 decode steps (every argmax, the last logits).
+    KV rows agree; 11 tokens: one block of the 512-column ranges with 3 token quads; 43 tokens:
+    a full block of 32 and one of 11), chpe_verify of 8 drafts vs 8 decode steps (every argmax,
+    the last logits; the 2048-column ranges).
     Bars: 2e-4 * max|logit| with the f32 cache, as for the decode step against the oracle;
     3e-3 with the fp16 cache, twice the single-step bar: the two paths sum in different orders,
     so k / v elements near an fp16 rounding boundary round differently, and here 19 cached
@@ -175,11 +177,17 @@ def run_block(path, arch, vocab, seed, oracle_check, block=True):
             say(f"block step arch {arch} kv_f16={kv16}: sequential reference")
             _, lseq = e.forward_tokens(prompt, want_logits=True)
             seq = [e.decode_step(int(d), n + i) for i, d in enumerate(drafts)]
-            say("  prefill (blocks of 8 + 3)")
+            say("  prefill of 11 positions (one block)")
             _, lblk = e.prefill(prompt, want_logits=True)
             compare_logits(lblk, lseq, "prefill vs forward_tokens", rel)
             am, lg = e.decode_step(int(drafts[0]), n)
             compare_logits(lg, seq[0][1], "decode step after prefill", rel)
+            say("  prefill of 43 positions (a block of 32 + 11) vs forward_tokens")
+            long = rng.integers(0, vocab, 43).astype(np.uint32)
+            _, lseq2 = e.forward_tokens(long, want_logits=True)
+            _, lblk2 = e.prefill(long, want_logits=True)
+            compare_logits(lblk2, lseq2, "prefill 43 vs forward_tokens", rel)
+            e.forward_tokens(prompt)  # (the context of the verify below)
             say("  verify 8 drafts")
             got = e.verify(drafts, n)
             for i in range(8):
@@ -289,7 +297,7 @@ def test_9b_break_in_block_and_decode_steps(a9):
         nb.set_break(False)
         try:
             assert e.block_ready()
-            say("9B break: prefill of 11 positions (blocks of 8 + 3)")
+            say("9B break: prefill of 11 positions (one block)")
             am, lg = e.prefill(prompt, want_logits=True)
             for pos, tok in enumerate(prompt):
                 r = o.forward(int(tok), pos)
