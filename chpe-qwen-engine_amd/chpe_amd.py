@@ -29,7 +29,7 @@ ENGINE_SYMBOLS = [
     "chpe_generate", "chpe_verify", "chpe_prefill", "chpe_block_ready", "chpe_last_error", "chpe_build_id", "chpe_get_max_seq_len", "chpe_get_hidden",
     "chpe_time_steps", "chpe_time_stage", "chpe_time_stage_live", "chpe_stage_bytes", "chpe_step_bytes", "chpe_stage_kernel",
     "chpe_debug_gemv", "chpe_debug_flat_tile_weights", "chpe_debug_gemv_flat", "chpe_debug_gemv_cells", "chpe_debug_gemv_poly", "chpe_debug_gemv_raw", "chpe_debug_embed_row_cell",
-    "chpe_debug_attention", "chpe_attention_noalloc", "chpe_debug_deltanet_conv", "chpe_debug_deltanet_step",
+    "chpe_debug_attention", "chpe_debug_attention_block", "chpe_attention_noalloc", "chpe_debug_deltanet_conv", "chpe_debug_deltanet_step",
 ]
 
 _c_float_p = ctypes.POINTER(ctypes.c_float)
@@ -113,6 +113,8 @@ def load_engine_lib():
             "chpe_debug_embed_row_cell": (I, [_c_u8_p, S, ctypes.c_uint32, ctypes.c_uint32, _c_float_p]),
             "chpe_debug_attention": (I, [ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32, I, ctypes.c_uint32,
                                          _c_float_p, _c_float_p, _c_float_p, _c_float_p]),
+            "chpe_debug_attention_block": (I, [ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32, I, ctypes.c_uint32,
+                                               ctypes.c_uint32, _c_float_p, _c_float_p, _c_float_p, _c_float_p]),
             "chpe_attention_noalloc": (I, [ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32, I, ctypes.c_uint32,
                                            ctypes.c_uint32, V, V, V, V, V]),
             "chpe_debug_deltanet_conv": (I, [ctypes.c_uint32, ctypes.c_uint32, _c_float_p, _c_float_p, _c_float_p,
@@ -459,6 +461,23 @@ def gpu_attention(q, k_rows, v_rows, pos, heads, kv_heads, head_dim, kv_f16):
                                                 _fp(v), _fp(out))
     if rc:
         raise EngineError(f"chpe_debug_attention failed: {rc}")
+    return out
+
+
+def gpu_attention_block(q, k_rows, v_rows, pos, heads, kv_heads, head_dim, kv_f16):
+    """The block step's attention kernels on caller rows: q [nq][heads*hd] at positions pos ..
+    pos+nq-1, k_rows / v_rows [pos+nq][kv*hd] f32; returns [nq][heads*hd]."""
+    q = np.ascontiguousarray(q, dtype=np.float32)
+    k = np.ascontiguousarray(k_rows, dtype=np.float32)
+    v = np.ascontiguousarray(v_rows, dtype=np.float32)
+    nq = q.shape[0]
+    if q.ndim != 2 or q.shape[1] != heads * head_dim or k.size != (pos + nq) * kv_heads * head_dim or v.size != k.size:
+        raise ValueError("attention operand sizes do not match the shape")
+    out = np.empty_like(q)
+    rc = load_engine_lib().chpe_debug_attention_block(head_dim, heads, kv_heads, int(kv_f16), pos, nq, _fp(q),
+                                                      _fp(k), _fp(v), _fp(out))
+    if rc:
+        raise EngineError(f"chpe_debug_attention_block failed: {rc}")
     return out
 
 

@@ -214,6 +214,10 @@ __global__ void __launch_bounds__(NW * 64) k_attn_chunk(AttnArgs a0) {
 // lane group G takes dims [G*HD/4, (G+1)*HD/4) of a K row (one contiguous read), and output
 // column n of N-tile j is dim n*HD/16 + j, so a lane's V operand over all N-tiles is one
 // contiguous read of the 4-position-blocked V cache.  Exact fp16 products, f32 accumulation.
+// QZ > 1 (a block step): the workgroup serves queries QZ blockIdx.z .. + QZ - 1 in turn over the
+// K and V rows it loaded once (each query's arithmetic as alone), the next query's rows loaded
+// while one is processed.
+constexpr int kAttnQz = 8;  // queries per workgroup of a block step's attention
 typedef _Float16 h4_t __attribute__((ext_vector_type(4)));
 typedef float f4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u2_t __attribute__((ext_vector_type(2)));
@@ -230,17 +234,20 @@ __device__ __forceinline__ h4_t f16_part(float a, float b, float c, float d, boo
   return rem ? r : h;
 }
 
-template <int HD, int GQ, int NW, int T>
-__global__ void __launch_bounds__(NW * 64) k_attn_mfma(AttnArgs a0) {
-  const AttnArgs a = attn_query(a0);
+template <int HD, int GQ, int NW, int T, int QZ>
+__global__ void __launch_bounds__(NW * 64) k_attn_mfma(AttnArgs a) {
   constexpr int KD = HD / 4;   // K dims per lane
   constexpr int KS = HD / 16;  // k-steps of the score product
   constexpr int VD = HD / 16;  // V dims per lane = N-tiles of the output product
   constexpr int CH = NW * T * 16, NT = NW * 64;
   static_assert(GQ <= 8 && NW * GQ <= 64 && (NW & (NW - 1)) == 0, "");
   const uint32_t c = blockIdx.x, kvh = blockIdx.y;
-  // the position is requested first and waited for only after the loads below are issued
-  const uint32_t pos = a.state->pos + blockIdx.z, ctx = pos + 1;
+  // the queries z0 .. z1 - 1 (positions pos + z); the position is requested first and waited
+  // for only after the loads below are issued
+  const uint32_t nz = a.nq > 1 ? a.nq : 1u, z0 = blockIdx.z * QZ;
+  const uint32_t z1 = QZ == 1 ? z0 + 1 : (z0 + QZ < nz ? z0 + QZ : nz);  // (QZ = 1: grid.z = nz)
+  const uint32_t pos0 = a.state->pos;
+  const size_t qrows = size_t(a.H) * HD;  // one query's rows of q / out
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int G = lane >> 4, n = lane & 15, h = n & 7;  // h: the query head of column / row n
   const bool rem = n >= 8;
@@ -260,8 +267,11 @@ __global__ void __launch_bounds__(NW * 64) k_attn_mfma(AttnArgs a0) {
   constexpr int QN4 = GQ * HD / 4, QF4 = (QN4 + NT - 1) / NT;
   __shared__ __align__(16) float s_q[GQ * HD];
   float4 qld[QF4];
+  auto load_q = [&](uint32_t z) {
 #pragma unroll
-  for (int k = 0; k < QF4; ++k) qld[k] = ld_f4(a.q + size_t(kvh * GQ) * HD + min(tid + NT * k, QN4 - 1) * 4);
+    for (int k = 0; k < QF4; ++k) qld[k] = ld_f4(a.q + z * qrows + size_t(kvh * GQ) * HD + min(tid + NT * k, QN4 - 1) * 4);
+  };
+  load_q(z0);
   const uint8_t* kc = reinterpret_cast<const uint8_t*>(a.k_cache) + size_t(kvh) * a.max_seq * HD * 2;
   const uint8_t* vc = reinterpret_cast<const uint8_t*>(a.v_cache) + size_t(kvh) * a.max_seq * HD * 2;
   uint4 kf[T][KD / 8], vf[T][VD / 2];
@@ -279,17 +289,26 @@ __global__ void __launch_bounds__(NW * 64) k_attn_mfma(AttnArgs a0) {
   // keep every load above this point: the scheduler would otherwise sink the V loads next to
   // the P.V products, after the softmax
   __builtin_amdgcn_sched_barrier(0);
+  for (uint32_t z = z0; z < z1; ++z) {
+  const uint32_t pos = pos0 + z, ctx = pos + 1;
+  if (z != z0) __syncthreads();  // (the previous query's LDS reads are done)
 #pragma unroll
   for (int k = 0; k < QF4; ++k)
     if (tid + NT * k < QN4) *reinterpret_cast<float4*>(&s_q[(tid + NT * k) * 4]) = qld[k];
   __syncthreads();
-  if (c * CH >= ctx) return;  // the whole workgroup; its loads are dropped
+  if (c * CH >= ctx) {  // the whole workgroup (a later query may reach the chunk)
+    if (QZ > 1 && z + 1 < z1) load_q(z + 1);
+    continue;
+  }
+  float* const part_ml = a.part_ml + size_t(z) * a.H * a.n_chunks * 2;
+  float* const part_acc = a.part_acc + size_t(z) * a.H * a.n_chunks * HD;
 
-  // 2. the query operand (zero for heads past the group)
+  // 2. the query operand (zero for heads past the group); the next query's rows are loaded
   const float* qsrc = s_q + (qok ? h : 0) * HD + G * KD;
   float4 qv[KD / 4];
 #pragma unroll
   for (int i = 0; i < KD / 4; ++i) qv[i] = *reinterpret_cast<const float4*>(qsrc + 4 * i);
+  if (QZ > 1 && z + 1 < z1) load_q(z + 1);
   h4_t qb[KS];
 #pragma unroll
   for (int st = 0; st < KS; ++st) {
@@ -377,8 +396,8 @@ __global__ void __launch_bounds__(NW * 64) k_attn_mfma(AttnArgs a0) {
     s_f[g][w] = f;
     if (w == 0) {
       const size_t hc = size_t(kvh * GQ + g) * nch + c;
-      a.part_ml[hc * 2] = M;
-      a.part_ml[hc * 2 + 1] = L;
+      part_ml[hc * 2] = M;
+      part_ml[hc * 2 + 1] = L;
     }
   }
   __syncthreads();
@@ -389,8 +408,9 @@ __global__ void __launch_bounds__(NW * 64) k_attn_mfma(AttnArgs a0) {
     float A = 0.0f;
 #pragma unroll
     for (int w = 0; w < NW; ++w) A = fmaf(s_acc[w][g][d] + s_acc[w][g + 8][d], s_f[g][w], A);
-    a.part_acc[(size_t(kvh * GQ + g) * nch + c) * HD + d] = A;
+    part_acc[(size_t(kvh * GQ + g) * nch + c) * HD + d] = A;
   }
+  }  // (query z)
 }
 
 // out[h][d] = sum_c A_c[d] w_c / sum_c L_c w_c, w_c = exp(M_c - M), over the active chunks.  One
@@ -469,18 +489,26 @@ __global__ void __launch_bounds__(64 * kMergeWaves) k_attn_merge(AttnArgs a0) {
 }  // namespace
 
 void launch_attention_partial(const AttnArgs& a, hipStream_t st) {
-  const dim3 grid(a.n_chunks, a.KV, a.nq > 1 ? a.nq : 1);
+  const uint32_t nq = a.nq > 1 ? a.nq : 1;
+  const dim3 grid(a.n_chunks, a.KV, nq);
+  // fp16 cache, more than 4 queries: kAttnQz queries per workgroup over one load of its K / V rows
+  const bool mq = a.kv_f16 && nq > 4;
+  const dim3 grid_mq(a.n_chunks, a.KV, (nq + kAttnQz - 1) / kAttnQz);
   const uint32_t gq = a.H / a.KV;
   // (the chunk size a.chunk = attn_chunk(hd, KV) picks the instance: CH = waves x positions)
-  if (a.hd == 128 && gq == 8 && a.chunk == 128)  // fp16: 4 waves x 2 tiles; f32: 8 waves x 16 positions
-    a.kv_f16 ? launch_kernel(&k_attn_mfma<128, 8, 4, 2>, grid, dim3(256), st, a)
-             : launch_kernel(&k_attn_chunk<128, 8, float, 4, 8>, grid, dim3(512), st, a);
-  else if (a.hd == 128 && gq == 8)  // 64: fp16 4 waves x 1 tile; f32 4 waves x 16 positions, 4 lanes per K row
-    a.kv_f16 ? launch_kernel(&k_attn_mfma<128, 8, 4, 1>, grid, dim3(256), st, a)
-             : launch_kernel(&k_attn_chunk<128, 8, float, 4, 4>, grid, dim3(256), st, a);
-  else if (a.hd == 256 && gq == 4)  // fp16: 2 waves x 1 tile; f32: 2 waves x 16 positions
-    a.kv_f16 ? launch_kernel(&k_attn_mfma<256, 4, 2, 1>, grid, dim3(128), st, a)
-             : launch_kernel(&k_attn_chunk<256, 4, float, 4, 2>, grid, dim3(128), st, a);
+  if (a.hd == 128 && gq == 8 && a.chunk == 128) {  // fp16: 4 waves x 2 tiles; f32: 8 waves x 16 positions
+    if (mq) launch_kernel(&k_attn_mfma<128, 8, 4, 2, kAttnQz>, grid_mq, dim3(256), st, a);
+    else if (a.kv_f16) launch_kernel(&k_attn_mfma<128, 8, 4, 2, 1>, grid, dim3(256), st, a);
+    else launch_kernel(&k_attn_chunk<128, 8, float, 4, 8>, grid, dim3(512), st, a);
+  } else if (a.hd == 128 && gq == 8) {  // 64: fp16 4 waves x 1 tile; f32 4 waves x 16 positions, 4 lanes per K row
+    if (mq) launch_kernel(&k_attn_mfma<128, 8, 4, 1, kAttnQz>, grid_mq, dim3(256), st, a);
+    else if (a.kv_f16) launch_kernel(&k_attn_mfma<128, 8, 4, 1, 1>, grid, dim3(256), st, a);
+    else launch_kernel(&k_attn_chunk<128, 8, float, 4, 4>, grid, dim3(256), st, a);
+  } else if (a.hd == 256 && gq == 4) {  // fp16: 2 waves x 1 tile; f32: 2 waves x 16 positions
+    if (mq) launch_kernel(&k_attn_mfma<256, 4, 2, 1, kAttnQz>, grid_mq, dim3(128), st, a);
+    else if (a.kv_f16) launch_kernel(&k_attn_mfma<256, 4, 2, 1, 1>, grid, dim3(128), st, a);
+    else launch_kernel(&k_attn_chunk<256, 4, float, 4, 2>, grid, dim3(128), st, a);
+  }
 }
 
 void launch_attention_combine(const AttnArgs& a, hipStream_t st) {

@@ -336,8 +336,8 @@ __global__ void __launch_bounds__(kWave * NW) k_gemv_mt(BlockGemvArgs a) {
 // complement value, so no offset term is needed.  A range's raw row sums go to the partial-sum
 // buffer as k_gemv_mt's; the ranges are few (block_gemv_ranges: enough workgroups to fill the
 // CUs).
-constexpr int kGmWaves = 8;
-constexpr uint32_t kGmUnits = 4, kGmChunk = 2;  // U, GC of the launches
+constexpr int kGmWaves = 16;
+constexpr uint32_t kGmUnits = 2, kGmChunk = 2;  // U, GC of the launches
 template <int BITS, int U, int GC>
 struct GmGeom {
   static constexpr uint32_t GB = BITS == 2 ? 32 : 64;      // code bytes per group and row
@@ -362,10 +362,10 @@ __global__ void __launch_bounds__(kWave * kGmWaves) k_block_gemm(BlockGemvArgs a
   using G = GmGeom<BITS, U, GC>;
   constexpr int NQ = int(kMaxBlock / 4);
   constexpr int kThreads = kWave * kGmWaves;
-  constexpr int kTabPer = NQ * GC * 128 / kThreads;  // table entries per thread and chunk
-  static_assert(NQ * GC * 128 % kThreads == 0 && NQ * GC * 4 <= kThreads, "");
-  __shared__ __align__(16) uint4 s_tb[2][NQ][GC][128];
-  __shared__ float s_ew[2][NQ][GC][4];
+  // (the two table buffers are separate objects, so that the compiler sees the loads into one
+  // and the reads of the other as independent)
+  __shared__ __align__(16) uint4 s_tb0[NQ][GC][128], s_tb1[NQ][GC][128];
+  __shared__ float s_ew0[NQ][GC][4], s_ew1[NQ][GC][4];
   __shared__ __align__(16) uint8_t s_w[kGmWaves][G::SLOT];
   __shared__ uint16_t s_sc[kGmWaves][G::ROWS][GC];
   const int tid = threadIdx.x, lane = tid & 63, n = lane & 15, q = lane >> 4;
@@ -373,7 +373,6 @@ __global__ void __launch_bounds__(kWave * kGmWaves) k_block_gemm(BlockGemvArgs a
   const uint32_t ng = a.g.C >> 7, nch = (ng + GC - 1) / GC, range = blockIdx.x;
   const uint32_t c_begin = uint32_t(uint64_t(range) * nch / gridDim.x);
   const uint32_t c_end = uint32_t(uint64_t(range + 1) * nch / gridDim.x);
-  const uint32_t nq = a.nq, nqt = nq < uint32_t(NQ) ? nq : uint32_t(NQ);
   const uint32_t u0 = (blockIdx.y * kGmWaves + wave) * U;  // the wave's first unit
   uint8_t* slot = s_w[wave];
   // each unit's part (parts hold consecutive unit ranges from part[p].unit_begin); a unit past
@@ -404,67 +403,68 @@ __global__ void __launch_bounds__(kWave * kGmWaves) k_block_gemm(BlockGemvArgs a
       const uint32_t Gi = rr * ng + gg;
       st->v[i] = ld_u128(ubase[u] + ((Gi >> 8) * ustride[u] + 64 + (Gi & 255u) * G::GB + lb % G::GB));
     }
+    // (every lane loads; lanes past 16 GC read a row of the part or row 0 and are not staged)
     const uint32_t sk = uint32_t(lane) % GC, sg = cg + sk < ng ? cg + sk : cg;
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const uint32_t r = ur0[u] + uint32_t(lane) / GC, rr = r < uwr[u] ? r : 0u;
       const uint32_t Gi = rr * ng + sg;
-      st->sc[u] = lane < 16 * GC ? ld_u16(ubase[u] + ((Gi >> 8) * ustride[u] + 16448 + 48 + 2 * (Gi & 255u))) : 0u;
+      st->sc[u] = ld_u16(ubase[u] + ((Gi >> 8) * ustride[u] + 16448 + 48 + 2 * (Gi & 255u)));
     }
   };
   // into the wave's slot (LDS operations of one wave complete in order: the previous chunk's
   // reads are done before these writes land)
-  auto stage = [&](const GmStage<BITS, U, GC>& st) {
+  // (the scale of a group past the last, chunk c's, is staged as 0)
+  auto stage = [&](const GmStage<BITS, U, GC>& st, uint32_t c, uint8_t* sl, uint16_t* sc) {
 #pragma unroll
     for (int i = 0; i < int(G::NLD); ++i)
-      *reinterpret_cast<uint4*>(slot + (G::RPI * i + lane / G::LPR) * G::SROW + 16 * (lane % G::LPR)) = st.v[i];
+      *reinterpret_cast<uint4*>(sl + (G::RPI * i + lane / G::LPR) * G::SROW + 16 * (lane % G::LPR)) = st.v[i];
+    const bool gv = c * GC + uint32_t(lane) % GC < ng;
     if (lane < 16 * GC) {
 #pragma unroll
-      for (int u = 0; u < U; ++u) s_sc[wave][16 * u + lane / GC][lane % GC] = uint16_t(st.sc[u]);
+      for (int u = 0; u < U; ++u) sc[(16 * u + lane / GC) * GC + lane % GC] = gv ? uint16_t(st.sc[u]) : uint16_t(0);
     }
   };
-  // the operand tables of chunk c: registers, then LDS buffer b (quads past nq and groups past
-  // the last: zero)
-  uint4 pa[kTabPer];
-  float pe = 0.0f;
-  auto fetch_tables = [&](uint32_t c) {
+  // the operand tables of chunk c straight into LDS buffer b (global_load_lds: 64 lanes x 16 B
+  // to consecutive LDS per instruction, no registers), each wave kTabInst instructions, wave 0
+  // also the 64 group exponents.  Nothing is zeroed: the tables of quads past nq -- allocated
+  // for kMaxBlock tokens, stale -- feed only results that are not stored, and a group past the
+  // last reads the last group's and is skipped in compute.
+  constexpr int kTabInst = NQ * GC * 128 / kThreads;
+  auto fetch_tables = [&](uint32_t c, uint4* tdst, float* edst) {
     const uint32_t cg = c * GC;
 #pragma unroll
-    for (int j = 0; j < kTabPer; ++j) {
-      const uint32_t i = uint32_t(tid + kThreads * j), T = i / (GC * 128), k = (i / 128) % GC, e = i % 128;
-      const bool ok = T < nqt && cg + k < ng;
-      pa[j] = ok ? a.t.tb[(size_t(T) * ng + cg + k) * 128 + e] : make_uint4(0, 0, 0, 0);
+    for (int j = 0; j < kTabInst; ++j) {
+      const uint32_t i0 = (wave * kTabInst + uint32_t(j)) * kWave, i = i0 + uint32_t(lane);
+      const uint32_t T = i / (GC * 128), k = (i / 128) % GC, e = i % 128, g = cg + k < ng ? cg + k : ng - 1;
+      __builtin_amdgcn_global_load_lds(a.t.tb + (size_t(T) * ng + g) * 128 + e, tdst + i0, 16, 0, 0);
     }
-    if (tid < NQ * GC * 4) {
-      const uint32_t T = uint32_t(tid) / (GC * 4), k = (uint32_t(tid) / 4) % GC, qq = uint32_t(tid) % 4;
-      const bool ok = T < nqt && cg + k < ng;
-      pe = ok ? a.t.ew[(size_t(T) * ng + cg + k) * 4 + qq] : 0.0f;
+    if (wave == 0) {
+      const uint32_t T = uint32_t(lane) / (GC * 4) % NQ, k = (uint32_t(lane) / 4) % GC, qq = uint32_t(lane) % 4;
+      const uint32_t g = cg + k < ng ? cg + k : ng - 1;
+      __builtin_amdgcn_global_load_lds(a.t.ew + (size_t(T) * ng + g) * 4 + qq, edst, 4, 0, 0);
     }
   };
-  auto store_tables = [&](int b) {
-#pragma unroll
-    for (int j = 0; j < kTabPer; ++j) (&s_tb[b][0][0][0])[tid + kThreads * j] = pa[j];
-    if (tid < NQ * GC * 4) (&s_ew[b][0][0][0])[tid] = pe;
-  };
+  static_assert(NQ * GC * 128 % kThreads == 0 && NQ * GC * 4 == kWave, "table loads: whole instructions");
   float acc[U][NQ];
 #pragma unroll
   for (int u = 0; u < U; ++u)
 #pragma unroll
     for (int T = 0; T < NQ; ++T) acc[u][T] = 0.0f;
-  // per group (a group past the last: skipped, uniformly) the U units' operands; per token quad
+  // per group the U units' operands (a group past the last -- only in the last chunk of an odd
+  // group count -- runs on the clamped, finite data with the scale 0 stage() gave it: no
+  // branch); per token quad
   // the 2 U matrix-core products first, then the conversions: lane (n, q) holds token q's limb
   // sums D0..D3 of row n, combined exactly in pairs (|D| < 2^18: D0 + 2^8 D1 fits), then
   // lo + 2^16 hi in float, scaled by 2^(e - 30) * the row's group scale
-  auto compute = [&](uint32_t c, int b) {
-    const uint32_t cg = c * GC;
+  auto compute = [&](const uint4* tsrc, const float* esrc, const uint8_t* sl, const uint16_t* scs) {
 #pragma unroll
     for (int k = 0; k < GC; ++k) {
-      if (cg + uint32_t(k) >= ng) break;  // (uniform: only in the last chunk of an odd group count)
       i32x4_t B0[U], B1[U];
       float scv[U];
 #pragma unroll
       for (int u = 0; u < U; ++u) {
-        const uint8_t* row = slot + (16 * u + n) * G::SROW + G::GB * k;
+        const uint8_t* row = sl + (16 * u + n) * G::SROW + G::GB * k;
         if constexpr (BITS == 2) {  // 16 codes in 4 bytes: field f of each byte, as (code ^ 2) - 2
           const uint2 w2 = *reinterpret_cast<const uint2*>(row + 8 * q);
           const uint32_t x = w2.x ^ 0xAAAAAAAAu, y = w2.y ^ 0xAAAAAAAAu;
@@ -479,15 +479,16 @@ __global__ void __launch_bounds__(kWave * kGmWaves) k_block_gemm(BlockGemvArgs a
           B1[u] = i32x4_t{sbytes4(w.z & 0x0f0f0f0fu), sbytes4((w.z >> 4) & 0x0f0f0f0fu), sbytes4(w.w & 0x0f0f0f0fu),
                           sbytes4((w.w >> 4) & 0x0f0f0f0fu)};
         }
-        scv[u] = h2f(s_sc[wave][16 * u + n][k]);
+        scv[u] = h2f(scs[(16 * u + n) * GC + k]);
       }
 #pragma unroll
       for (int T = 0; T < NQ; ++T) {  // (quads past nq: zero tables, no stores)
-        const uint4 t0 = s_tb[b][T][k][(uint32_t(q) * 2) * 16 + uint32_t(n)];
-        const uint4 t1 = s_tb[b][T][k][(uint32_t(q) * 2 + 1) * 16 + uint32_t(n)];
+        const uint4* tb = tsrc + (T * GC + k) * 128;
+        const uint4 t0 = tb[(uint32_t(q) * 2) * 16 + uint32_t(n)];
+        const uint4 t1 = tb[(uint32_t(q) * 2 + 1) * 16 + uint32_t(n)];
         const i32x4_t A0 = {int(t0.x), int(t0.y), int(t0.z), int(t0.w)};
         const i32x4_t A1 = {int(t1.x), int(t1.y), int(t1.z), int(t1.w)};
-        const float ew = s_ew[b][T][k][q];
+        const float ew = esrc[(T * GC + k) * 4 + q];
         i32x4_t D[U];
 #pragma unroll
         for (int u = 0; u < U; ++u) D[u] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A0, B0[u], i32x4_t{0, 0, 0, 0}, 0, 0, 0);
@@ -503,28 +504,47 @@ __global__ void __launch_bounds__(kWave * kGmWaves) k_block_gemm(BlockGemvArgs a
     }
   };
   GmStage<BITS, U, GC> SA, SB;
-  fetch_tables(c_begin);
-  if (active) issue(c_begin, &SA);
-  store_tables(0);
+  fetch_tables(c_begin, &s_tb0[0][0][0], &s_ew0[0][0][0]);
+  issue(c_begin, &SA);
+  __builtin_amdgcn_s_waitcnt(0);  // (the first tables; vmcnt, expcnt and lgkmcnt all 0)
   __syncthreads();
-  // chunk c (tables in buffer b): its codes in `cur`; the next chunk's codes into `nxt` and its
-  // tables into registers while c is multiplied, then into buffer b ^ 1 (last read by chunk
-  // c - 1, before the previous barrier); the barrier is uniform (c_end is the workgroup's)
-  auto body = [&](uint32_t c, int b, GmStage<BITS, U, GC>& cur, GmStage<BITS, U, GC>& nxt) {
-    const bool more = c + 1 < c_end;
-    if (more) fetch_tables(c + 1);
-    if (active) {
-      stage(cur);
-      if (more) issue(c + 1, &nxt);
-      compute(c, b);
-    }
-    if (more) store_tables(b ^ 1);
-    __syncthreads();
+  // chunk c (tables in buffer b): its codes in `cur`, staged first (the wait is for them alone);
+  // then the next chunk's tables into registers and its codes into `nxt` while c is
+  // multiplied, then the tables into buffer b ^ 1 (last read by chunk c - 1, before the
+  // previous barrier); the barrier is uniform (c_end is the workgroup's)
+  // (s_waitcnt immediates: vmcnt in bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8; expcnt and
+  // lgkmcnt left at their maxima)
+  constexpr int kCodeLoads = int(G::NLD) + U;  // the loads of one issue()
+  static_assert(kCodeLoads < 16, "");
+  // The body has no branch (a branch around loads makes the compiler wait for every load in
+  // flight where the paths join): a wave past the last unit works on unit 0's rows and stores
+  // nothing, and the last chunk's "next" chunk is itself again (loads of data that exist, not
+  // used).  The buffers come in as restrict pointers: the compiler then knows that the reads of
+  // one do not wait for the loads into the other.  The barrier is a bare s_barrier: the only LDS
+  // data other waves read are the tables, whose loads each wave has waited for (a fenced
+  // __syncthreads would also wait for the code loads in flight); no table load is in flight
+  // when the workgroup ends.
+  auto body = [&](uint32_t c, const uint4* __restrict__ tcur, const float* __restrict__ ecur, uint4* __restrict__ tnxt,
+                  float* __restrict__ enxt, uint8_t* __restrict__ sl, uint16_t* __restrict__ scs,
+                  GmStage<BITS, U, GC>& cur, GmStage<BITS, U, GC>& nxt) {
+    const uint32_t cn = c + 1 < c_end ? c + 1 : c;
+    stage(cur, c, sl, scs);
+    fetch_tables(cn, tnxt, enxt);
+    __builtin_amdgcn_sched_barrier(0);  // (the table loads are issued before the code loads)
+    issue(cn, &nxt);
+    compute(tcur, ecur, sl, scs);
+    __builtin_amdgcn_s_waitcnt(0x0F70 | kCodeLoads);  // the next tables have landed
+    __builtin_amdgcn_s_barrier();
   };
+  uint4* const tb0 = &s_tb0[0][0][0];
+  uint4* const tb1 = &s_tb1[0][0][0];
+  float* const ew0 = &s_ew0[0][0][0];
+  float* const ew1 = &s_ew1[0][0][0];
+  uint16_t* const scw = &s_sc[wave][0][0];
   for (uint32_t c = c_begin;; c += 2) {
-    body(c, 0, SA, SB);
+    body(c, tb0, ew0, tb1, ew1, slot, scw, SA, SB);
     if (c + 1 >= c_end) break;
-    body(c + 1, 1, SB, SA);
+    body(c + 1, tb1, ew1, tb0, ew0, slot, scw, SB, SA);
     if (c + 2 >= c_end) break;
   }
   if (!active) return;

@@ -715,10 +715,13 @@ int chpe_debug_embed_row_cell(const uint8_t* bytes, size_t len, uint32_t row, ui
 // The decode step's attention kernels on caller data: the caller's f32 rows are laid out as
 // the engine's cache holds them (fp16 rounded to nearest even when kv_f16; V in 4-position
 // blocks for fp16), and the chunk + merge kernels run once.
-int chpe_debug_attention(uint32_t head_dim, uint32_t heads, uint32_t kv_heads, int kv_f16, uint32_t pos,
-                         const float* q, const float* k_rows, const float* v_rows, float* out) {
-  if (!q || !k_rows || !v_rows || !out || !attention_supported(heads, kv_heads, head_dim)) return -1;
-  const uint32_t chunk = attn_chunk(head_dim, kv_heads), ctx = pos + 1;
+// nq queries at positions pos .. pos + nq - 1 (nq 1: the decode step's launch; more: the block
+// step's), each over the rows up to its own position
+static int debug_attention(uint32_t head_dim, uint32_t heads, uint32_t kv_heads, int kv_f16, uint32_t pos,
+                           uint32_t nq, const float* q, const float* k_rows, const float* v_rows, float* out) {
+  if (!q || !k_rows || !v_rows || !out || nq == 0 || nq > kMaxBlock || !attention_supported(heads, kv_heads, head_dim))
+    return -1;
+  const uint32_t chunk = attn_chunk(head_dim, kv_heads), ctx = pos + nq;
   const uint32_t n_chunks = (ctx + chunk - 1) / chunk, rows = n_chunks * chunk;  // a multiple of 16
   if (n_chunks > kAttnMaxChunks) return -1;
   const size_t hd = head_dim, kvd = size_t(kv_heads) * hd, el = kv_f16 ? 2 : 4;
@@ -737,7 +740,7 @@ int chpe_debug_attention(uint32_t head_dim, uint32_t heads, uint32_t kv_heads, i
           reinterpret_cast<float*>(vc.data())[ka] = vv;
         }
       }
-  const size_t qn = size_t(heads) * hd;
+  const size_t qn = size_t(nq) * heads * hd;
   void *dk = nullptr, *dv = nullptr;
   float *dq = nullptr, *dout = nullptr, *dml = nullptr, *dacc = nullptr;
   StepState* dst = nullptr;
@@ -746,8 +749,8 @@ int chpe_debug_attention(uint32_t head_dim, uint32_t heads, uint32_t kv_heads, i
   int rc = -3;
   if (hipMalloc(&dk, kc.size()) == hipSuccess && hipMalloc(&dv, vc.size()) == hipSuccess &&
       hipMalloc(&dq, qn * 4) == hipSuccess && hipMalloc(&dout, qn * 4) == hipSuccess &&
-      hipMalloc(&dml, size_t(heads) * n_chunks * 2 * 4) == hipSuccess &&
-      hipMalloc(&dacc, size_t(heads) * n_chunks * hd * 4) == hipSuccess &&
+      hipMalloc(&dml, size_t(nq) * heads * n_chunks * 2 * 4) == hipSuccess &&
+      hipMalloc(&dacc, size_t(nq) * heads * n_chunks * hd * 4) == hipSuccess &&
       hipMalloc(&dst, sizeof(StepState)) == hipSuccess &&
       hipMemcpy(dk, kc.data(), kc.size(), hipMemcpyHostToDevice) == hipSuccess &&
       hipMemcpy(dv, vc.data(), vc.size(), hipMemcpyHostToDevice) == hipSuccess &&
@@ -769,6 +772,7 @@ int chpe_debug_attention(uint32_t head_dim, uint32_t heads, uint32_t kv_heads, i
     a.chunk = chunk;
     a.kv_f16 = kv_f16 ? 1 : 0;
     a.scale = 1.0f / std::sqrt(float(head_dim));
+    a.nq = nq;
     launch_attention(a, nullptr);
     if (hipDeviceSynchronize() == hipSuccess && hipMemcpy(out, dout, qn * 4, hipMemcpyDeviceToHost) == hipSuccess)
       rc = 0;
@@ -777,6 +781,16 @@ int chpe_debug_attention(uint32_t head_dim, uint32_t heads, uint32_t kv_heads, i
                   static_cast<void*>(dacc), static_cast<void*>(dst)})
     if (p) (void)hipFree(p);
   return rc;
+}
+
+int chpe_debug_attention(uint32_t head_dim, uint32_t heads, uint32_t kv_heads, int kv_f16, uint32_t pos,
+                         const float* q, const float* k_rows, const float* v_rows, float* out) {
+  return debug_attention(head_dim, heads, kv_heads, kv_f16, pos, 1, q, k_rows, v_rows, out);
+}
+
+int chpe_debug_attention_block(uint32_t head_dim, uint32_t heads, uint32_t kv_heads, int kv_f16, uint32_t pos,
+                               uint32_t nq, const float* q, const float* k_rows, const float* v_rows, float* out) {
+  return debug_attention(head_dim, heads, kv_heads, kv_f16, pos, nq, q, k_rows, v_rows, out);
 }
 
 // One decode step of a gated-DeltaNet layer's recurrent core on caller data (the layers have no

@@ -181,6 +181,13 @@ int chpe_debug_embed_row_cell(const uint8_t *bytes, size_t len, uint32_t row, ui
  * 0 on success, -1 bad arguments or unsupported shape, -3 device error. */
 int chpe_debug_attention(uint32_t head_dim, uint32_t heads, uint32_t kv_heads, int kv_f16, uint32_t pos,
                          const float *q, const float *k_rows, const float *v_rows, float *out);
+/* No counterpart in the reference (it attends one position per forwardDecode call).  The block
+ * step's attention on caller data: nq <= 32 queries q [nq][heads][head_dim] at positions
+ * pos .. pos+nq-1, query z over rows 0..pos+z of k_rows / v_rows [pos+nq][kv_heads*head_dim]
+ * (the fp16 cache and more than 4 queries: the multi-query launch); out [nq][heads][head_dim].
+ * 0 on success, -1 bad arguments or unsupported shape, -3 device error. */
+int chpe_debug_attention_block(uint32_t head_dim, uint32_t heads, uint32_t kv_heads, int kv_f16, uint32_t pos,
+                               uint32_t nq, const float *q, const float *k_rows, const float *v_rows, float *out);
 /* No counterpart in the reference.  The decode step's attention (chunk + merge kernels) on
  * caller device buffers, allocating nothing: for callers that cannot allocate (code under HIP
  * graph capture, serving loops, harnesses that forbid hipMalloc).  q [heads][head_dim] f32

@@ -178,6 +178,31 @@ def test_attention_kernels_match_oracle(hd, H, KV, kv_f16):
         assert err <= 2e-5 * float(np.max(np.abs(vr))), (pos, err)
 
 
+@pytest.mark.parametrize("kv_f16", [1, 0])
+@pytest.mark.parametrize("hd,H,KV", ATTN_SHAPES)
+def test_block_attention_matches_oracle(hd, H, KV, kv_f16):
+    """The block step's attention (nq queries at consecutive positions, query z over the rows up
+    to its own position; the fp16 cache with more than 4 queries runs the multi-query launch,
+    8 queries per workgroup over one load of its K / V rows) against the oracle's attention of
+    each query alone, at the bar of the single-query test: block starts at 0, inside a chunk,
+    a block crossing a chunk boundary (queries whose first chunks differ), a ragged last
+    workgroup (11, 13 queries) and a long context."""
+    rng = np.random.default_rng(hd * 7 + H + kv_f16)
+    chunk = 16384 // hd
+    for pos, nq in ((0, 32), (5, 11), (chunk - 6, 13), (chunk - 1, 8), (3 * chunk + 2, 32), (4000, 6), (8160, 32)):
+        say(f"block attention hd={hd} H={H} KV={KV} kv_f16={kv_f16} pos={pos} nq={nq}")
+        q = (rng.standard_normal((nq, H * hd)) * 2.0).astype(np.float32)
+        k = rng.standard_normal((pos + nq, KV * hd)).astype(np.float32)
+        v = rng.standard_normal((pos + nq, KV * hd)).astype(np.float32)
+        kr, vr = (k.astype(np.float16).astype(np.float32), v.astype(np.float16).astype(np.float32)) \
+            if kv_f16 else (k, v)
+        got = ca.gpu_attention_block(q, k, v, pos, H, KV, hd, kv_f16)
+        for z in range(nq):
+            ref = orc.attention(q[z], kr[:pos + z + 1], vr[:pos + z + 1], pos + z, H, KV, hd)
+            err = float(np.max(np.abs(got[z] - ref)))
+            assert err <= 2e-5 * float(np.max(np.abs(vr[:pos + z + 1]))), (pos, nq, z, err)
+
+
 def compare_step(e_logits, o_logits, tag):
     d = np.abs(e_logits.astype(np.float64) - o_logits)
     cos = float(e_logits.astype(np.float64) @ o_logits / np.linalg.norm(e_logits) / np.linalg.norm(o_logits))
