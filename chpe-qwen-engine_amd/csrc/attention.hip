@@ -491,8 +491,9 @@ __global__ void __launch_bounds__(64 * kMergeWaves) k_attn_merge(AttnArgs a0) {
 void launch_attention_partial(const AttnArgs& a, hipStream_t st) {
   const uint32_t nq = a.nq > 1 ? a.nq : 1;
   const dim3 grid(a.n_chunks, a.KV, nq);
-  // fp16 cache, more than 4 queries: kAttnQz queries per workgroup over one load of its K / V rows
-  const bool mq = a.kv_f16 && nq > 4;
+  // fp16 cache, a block of more than 8 queries (the prefill): kAttnQz queries per workgroup over
+  // one load of its K / V rows (the verify's few queries run in parallel workgroups)
+  const bool mq = a.kv_f16 && nq > kSmallBlock;
   const dim3 grid_mq(a.n_chunks, a.KV, (nq + kAttnQz - 1) / kAttnQz);
   const uint32_t gq = a.H / a.KV;
   // (the chunk size a.chunk = attn_chunk(hd, KV) picks the instance: CH = waves x positions)

@@ -49,7 +49,7 @@ using namespace dev;
 template <bool kNorm, int BITS>
 __global__ void __launch_bounds__(128) k_block_limbs(const float* X, const float* gamma, float eps, uint32_t C,
                                                       uint32_t m, const float* ssp, uint32_t n_ssp, BlockTables t,
-                                                      uint32_t* brk, uint32_t chk) {
+                                                      uint32_t* brk, uint32_t chk, uint32_t ts) {
   const uint32_t tok = blockIdx.y, T = tok >> 2, tl = tok & 3u, ng = C >> 7;
   const bool live = tok < m;
   const float* x = X + size_t(live ? tok : 0u) * C;
@@ -145,7 +145,7 @@ __global__ void __launch_bounds__(128) k_block_limbs(const float* X, const float
   }
   if (in && live) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) t.xt[size_t(cc + uint32_t(i)) * kMaxBlock + tok] = xv[i];
+    for (int i = 0; i < 8; ++i) t.xt[size_t(cc + uint32_t(i)) * ts + tok] = xv[i];
   }
 }
 
@@ -285,7 +285,7 @@ __global__ void __launch_bounds__(kWave * NW) k_gemv_mt(BlockGemvArgs a) {
 #pragma unroll
       for (int T = 0; T < NQ; ++T) {
         const uint32_t tk = 4 * uint32_t(T) + uint32_t(q);
-        if (tk < a.m) a.partial[(size_t(range) * a.rows_all + at) * kMaxBlock + tk] = r < P.wrows ? acc[T] : 0.0f;
+        if (tk < a.m) a.partial[(size_t(range) * a.rows_all + at) * a.ts + tk] = r < P.wrows ? acc[T] : 0.0f;
         acc[T] = 0.0f;
       }
     }
@@ -563,8 +563,220 @@ __global__ void __launch_bounds__(kWave * kGmWaves) k_block_gemm(BlockGemvArgs a
   }
 }
 
-// Epilogue: a wave serves 64 / TW outputs, TW lanes each (TW >= m): lane (i, t) = output i,
-// token t.  Per token: the ranges' raw sums in range order, the outlier corrections of the row
+// Epilogue of blocks of up to kSmallBlock tokens (the partial sums and the input token-minor
+// with stride kSmallBlock): a wave serves 4 outputs (16 lanes each: lane (i, e) = output i, correction entries
+// e, e + 16, ..; after the 16-lane reduction lane (i, t) finishes token t of output i).
+// Outputs: rows of part 0 (Store / Accum / Logits), gate row = up row (SwiGlu), RoPE pairs of
+// every part (QkvRope).
+template <int MODE>
+__global__ void __launch_bounds__(256) k_block_epi8(BlockGemvArgs a) {
+  constexpr bool kSwi = MODE == int(GemvMode::SwiGlu);
+  constexpr bool kRope = MODE == int(GemvMode::QkvRope);
+  constexpr bool kLogits = MODE == int(GemvMode::Logits);
+  constexpr int NR = (kSwi || kRope) ? 2 : 1;  // rows per output
+  const int lane = threadIdx.x & 63, e0 = lane & 15, i = lane >> 4, wave = threadIdx.x >> 6;
+  const uint32_t m = a.m, ranges = a.ranges;
+  const uint32_t half = a.g.rope.head_dim / 2;
+  uint32_t total = 0;
+  if constexpr (kRope) {
+    for (int p = 0; p < a.g.n_parts; ++p) total += a.g.part[p].rows / 2;
+  } else {
+    total = a.g.part[0].rows;
+  }
+  float bv = -1e30f;
+  uint32_t bi = 0xffffffffu, nf = 0;
+  float sq = 0.0f;  // Accum: this lane's sum of y^2 over its token's updated rows
+  const uint32_t pos0 = kRope ? a.state->pos : 0u;
+  // token e0's break (k_block_limbs): no KV append, the residual stays
+  const bool brk = (kRope || MODE == int(GemvMode::Accum)) && uint32_t(e0) < m && a.brk[e0] != 0u;
+  for (uint32_t q4 = blockIdx.x * 4 + uint32_t(wave); q4 * 4 < total; q4 += gridDim.x * 4) {
+    const uint32_t o = q4 * 4 + uint32_t(i);
+    const bool ok = o < total;
+    // the output's part and rows
+    int p = 0;
+    uint32_t rows_k[NR];
+    if constexpr (kRope) {
+      uint32_t oo = ok ? o : 0u;
+      while (p + 1 < a.g.n_parts && oo >= a.g.part[p].rows / 2) {
+        oo -= a.g.part[p].rows / 2;
+        ++p;
+      }
+      const uint32_t lo = (oo / half) * (2 * half) + oo % half;
+      rows_k[0] = lo;
+      rows_k[1] = lo + half;
+    } else {
+      rows_k[0] = ok ? o : 0u;
+      if constexpr (kSwi) rows_k[1] = rows_k[0];
+    }
+    // the ranges' raw sums of token t = e0 of each row (requested before the corrections)
+    const uint32_t t = uint32_t(e0);
+    float sum_k[NR];
+#pragma unroll
+    for (int k = 0; k < NR; ++k) {
+      const GemvPart& P = a.g.part[kSwi ? k : p];
+      const uint32_t at = P.unit_begin * kBlockUnit + rows_k[k];
+      float acc_s = 0.0f;
+      if (ok && t < m)
+        for (uint32_t rg = 0; rg < ranges; ++rg) acc_s += a.partial[(size_t(rg) * a.rows_all + at) * kSmallBlock + t];
+      sum_k[k] = acc_s;
+    }
+    // corrections of each row, all tokens
+    float cor[NR][kSmallBlock];
+#pragma unroll
+    for (int k = 0; k < NR; ++k) {
+      const GemvPart& P = a.g.part[kSwi ? k : p];
+      const uint32_t r = rows_k[k];
+      const float2* corr = P.corr;
+      const uint32_t kmax = P.corr_kmax;
+#pragma unroll
+      for (int t = 0; t < int(kSmallBlock); ++t) cor[k][t] = 0.0f;
+      if (corr != nullptr && ok && r < P.wrows) {
+        // two entries per trip, their loads together (unused slots read entry 0, masked)
+        for (uint32_t e = uint32_t(e0); e < kmax; e += 32) {
+          const bool u1 = e + 16 < kmax;
+          const float2 c0 = corr[size_t(r) * kmax + e];
+          const float2 c1 = corr[size_t(r) * kmax + (u1 ? e + 16 : e)];
+          const float w0 = c0.y, w1 = u1 ? c1.y : 0.0f;
+          const float4* x0 = reinterpret_cast<const float4*>(a.t.xt + size_t(__float_as_uint(c0.x)) * kSmallBlock);
+          const float4* x1 = reinterpret_cast<const float4*>(a.t.xt + size_t(__float_as_uint(c1.x)) * kSmallBlock);
+          const float4 xa = x0[0], xb = x0[1], ya = x1[0], yb = x1[1];
+          const float xs0[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+          const float xs1[8] = {ya.x, ya.y, ya.z, ya.w, yb.x, yb.y, yb.z, yb.w};
+#pragma unroll
+          for (int tt = 0; tt < int(kSmallBlock); ++tt) {  // padding entries (w = 0) are skipped
+            float c = cor[k][tt];
+            c = w0 != 0.0f ? fmaf(w0, xs0[tt], c) : c;
+            c = w1 != 0.0f ? fmaf(w1, xs1[tt], c) : c;
+            cor[k][tt] = c;
+          }
+        }
+      }
+#pragma unroll
+      for (int t = 0; t < int(kSmallBlock); ++t) {
+        float v = cor[k][t];
+        v = pair_sum(v, 1);
+        v = pair_sum(v, 2);
+        v = pair_sum(v, 4);
+        v = pair_sum(v, 8);
+        cor[k][t] = v;
+      }
+    }
+    // lane (i, t): token t of the output
+    if (!ok || t >= m) continue;
+    float v[NR];
+#pragma unroll
+    for (int k = 0; k < NR; ++k) {
+      float c = cor[k][0];
+#pragma unroll
+      for (int tt = 1; tt < int(kSmallBlock); ++tt) c = t == uint32_t(tt) ? cor[k][tt] : c;
+      v[k] = sum_k[k] + c;
+    }
+    const GemvPart& P0 = a.g.part[kSwi ? 0 : p];
+    const uint32_t r = rows_k[0];
+    float* y = P0.y + size_t(t) * P0.rows;
+    if constexpr (MODE == int(GemvMode::Store)) {
+      y[r] = v[0] + (P0.bias ? P0.bias[r] : 0.0f);
+    } else if constexpr (MODE == int(GemvMode::Accum)) {
+      const bool upd = r < P0.wrows && !brk;  // rows past the tiles stay
+      const float yo = y[r], yn = upd ? yo + v[0] : yo;
+      if (upd) y[r] = yn;
+      sq = fmaf(yn, yn, sq);
+    } else if constexpr (kSwi) {
+      y[r] = v[0] / (1.0f + expf(-v[0])) * v[1];  // silu(g)*u: :159-161, :1746-1748
+    } else if constexpr (kRope) {
+#pragma clang fp contract(off)
+      const float lo = v[0] + (P0.bias ? P0.bias[r] : 0.0f);
+      const float hi = v[1] + (P0.bias ? P0.bias[r + half] : 0.0f);
+      const uint32_t pos = pos0 + t, d = r % (2 * half);
+      float o0 = lo, o1 = hi;
+      if (P0.rope_role < kRoleV && pos < a.rope_rows) {  // applyRope :195-216
+        const float c = a.rope_cos[size_t(pos) * half + d], sn = a.rope_sin[size_t(pos) * half + d];
+        o0 = lo * c - hi * sn;
+        o1 = lo * sn + hi * c;
+      }
+      if (P0.rope_role == kRoleQ || P0.rope_role == kRoleStore) {  // (Store: as computed)
+        y[r] = o0;
+        y[r + half] = o1;
+      } else if (!brk) {
+        const uint32_t hd = a.g.rope.head_dim, head = r / hd;
+        void* cache = P0.rope_role == kRoleK ? a.g.rope.k_cache : a.g.rope.v_cache;
+        if (a.g.rope.kv_f16 && P0.rope_role == kRoleV) {  // 4-position blocks: [pos/4][dim][pos%4]
+          const size_t blk = (size_t(head) * a.g.rope.max_seq + (pos & ~3u)) * hd + (pos & 3u);
+          reinterpret_cast<__half*>(cache)[blk + size_t(d) * 4] = __float2half_rn(o0);
+          reinterpret_cast<__half*>(cache)[blk + size_t(d + half) * 4] = __float2half_rn(o1);
+        } else {
+          const size_t at = (size_t(head) * a.g.rope.max_seq + pos) * hd + d;
+          if (a.g.rope.kv_f16) {
+            reinterpret_cast<__half*>(cache)[at] = __float2half_rn(o0);
+            reinterpret_cast<__half*>(cache)[at + half] = __float2half_rn(o1);
+          } else {
+            reinterpret_cast<float*>(cache)[at] = o0;
+            reinterpret_cast<float*>(cache)[at + half] = o1;
+          }
+        }
+      }
+    } else {
+      y[r] = v[0];
+      if (!isfinite(v[0])) nf = 1;
+      if (v[0] > -1e30f && better(v[0], r, bv, bi)) {
+        bv = v[0];
+        bi = r;
+      }
+    }
+  }
+  if constexpr (kLogits) {
+    // per token (lanes e0 = t of the 4 outputs), then over the waves
+#pragma unroll
+    for (int o = 16; o <= 32; o <<= 1) {
+      const float ov = pair_val(bv, o);
+      const uint32_t oi = pair_u(bi, o);
+      nf |= pair_u(nf, o);
+      if (better(ov, oi, bv, bi)) {
+        bv = ov;
+        bi = oi;
+      }
+    }
+    __shared__ float s_bv[4][16];
+    __shared__ uint32_t s_bi[4][16], s_nf[4][16];
+    if (lane < 16) {
+      s_bv[wave][lane] = bv;
+      s_bi[wave][lane] = bi;
+      s_nf[wave][lane] = nf;
+    }
+    __syncthreads();
+    if (threadIdx.x < m) {
+      const uint32_t tk = threadIdx.x;
+      float b = s_bv[0][tk];
+      uint32_t bx = s_bi[0][tk], f = s_nf[0][tk];
+      for (int w = 1; w < 4; ++w) {
+        f |= s_nf[w][tk];
+        if (better(s_bv[w][tk], s_bi[w][tk], b, bx)) {
+          b = s_bv[w][tk];
+          bx = s_bi[w][tk];
+        }
+      }
+      a.partials[size_t(tk) * a.epi_blocks + blockIdx.x] = ArgmaxPartial{b, bx, f, 0u};
+    }
+  }
+  if constexpr (MODE == int(GemvMode::Accum)) {
+    // the workgroup's sums of y^2 per token for the next GEMV's RMS norm (lanes e0 = t of the 4
+    // outputs, then over the waves, in a fixed order)
+    if (a.ssp_out) {
+      float v = pair_sum(sq, 16);
+      v = pair_sum(v, 32);
+      __shared__ float s_sq[4][16];
+      if (lane < 16) s_sq[wave][lane] = v;
+      __syncthreads();
+      if (threadIdx.x < kSmallBlock) {
+        const uint32_t tk = threadIdx.x;
+        a.ssp_out[size_t(blockIdx.x) * kMaxBlock + tk] = (s_sq[0][tk] + s_sq[1][tk]) + (s_sq[2][tk] + s_sq[3][tk]);
+      }
+    }
+  }
+}
+
+// Epilogue of blocks of more than kSmallBlock tokens (token stride kMaxBlock): a wave serves
+// 64 / TW outputs, TW lanes each (TW >= m): lane (i, t) = output i, token t.  Per token: the ranges' raw sums in range order, the outlier corrections of the row
 // in entry order (w * x[col] of the token: the flat tiles' replace deltas, the cells' added
 // outliers), then the batch-1 step's epilogue.  Outputs: rows of part 0 (Store / Accum /
 // Logits), gate row = up row (SwiGlu), RoPE pairs of every part (QkvRope).
@@ -576,7 +788,7 @@ __global__ void __launch_bounds__(256) k_block_epi(BlockGemvArgs a) {
   constexpr bool kAcc = MODE == int(GemvMode::Accum);
   constexpr int NR = (kSwi || kRope) ? 2 : 1;  // rows per output
   constexpr int OPW = 64 / TW;                 // outputs per wave
-  static_assert(TW <= int(kMaxBlock) && 64 % TW == 0, "");
+  static_assert(TW <= int(kMaxBlock) && TW > int(kSmallBlock) && 64 % TW == 0, "");
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const uint32_t t = uint32_t(lane % TW), i = uint32_t(lane / TW);
   const uint32_t m = a.m, ranges = a.ranges;
@@ -816,14 +1028,14 @@ void launch_block_limbs(const BlockGemvArgs& a, hipStream_t st) {
   const dim3 grid((a.g.C + 1023) / 1024, 4 * a.nq);
   const uint32_t chk = GemvMode(a.g.mode) == GemvMode::QkvRope ? a.g.rope.brk_check : 0u;
   auto go = [&](auto kern, uint32_t c) {
-    launch_kernel(kern, grid, dim3(128), st, a.g.x, a.g.gamma, a.g.eps, a.g.C, a.m, a.ssp, a.n_ssp, a.t, a.brk, c);
+    launch_kernel(kern, grid, dim3(128), st, a.g.x, a.g.gamma, a.g.eps, a.g.C, a.m, a.ssp, a.n_ssp, a.t, a.brk, c, a.ts);
   };
   if (a.bits == 2) a.g.gamma ? go(&k_block_limbs<true, 2>, chk) : go(&k_block_limbs<false, 2>, 0u);
   else a.g.gamma ? go(&k_block_limbs<true, 4>, chk) : go(&k_block_limbs<false, 4>, 0u);
 }
 
 uint32_t block_gemv_ranges(uint32_t n_units, uint32_t C, uint32_t m) {
-  if (m <= 8) return (C + kBlockRange - 1) / kBlockRange;
+  if (m <= kSmallBlock) return (C + kBlockRange - 1) / kBlockRange;
   // k_block_gemm: the fewest ranges for the least time in rounds of one workgroup per CU, a
   // range costing about two chunks more (its partial sums written and read back)
   const uint32_t rb = (n_units + kGmWaves * kGmUnits - 1) / (kGmWaves * kGmUnits);
@@ -843,7 +1055,7 @@ uint32_t block_gemv_ranges(uint32_t n_units, uint32_t C, uint32_t m) {
 uint32_t launch_block_gemv(BlockGemvArgs& a, hipStream_t st) {
   const uint32_t ranges = block_gemv_ranges(a.n_units, a.g.C, a.m);
   a.ranges = ranges;
-  if (a.m > 8) {  // output-stationary: row blocks of kGmWaves waves x kGmUnits units, few ranges
+  if (a.m > kSmallBlock) {  // output-stationary: row blocks of kGmWaves waves x kGmUnits units, few ranges
     const dim3 grid(ranges, (a.n_units + kGmWaves * kGmUnits - 1) / (kGmWaves * kGmUnits));
     if (a.bits == 2) launch_kernel(&k_block_gemm<2, kGmUnits, kGmChunk>, grid, dim3(kWave * kGmWaves), st, a);
     else launch_kernel(&k_block_gemm<4, kGmUnits, kGmChunk>, grid, dim3(kWave * kGmWaves), st, a);
@@ -870,18 +1082,20 @@ uint32_t launch_block_gemv(BlockGemvArgs& a, hipStream_t st) {
   } else {
     outs = a.g.part[0].rows;
   }
-  // lanes per output: the token count rounded up to 8, 16 or 32; one pass of 4 waves
-  const uint32_t tw = a.m <= 8 ? 8u : a.m <= 16 ? 16u : 32u, per_wg = 4 * (64 / tw);
+  // up to kSmallBlock tokens: 16 outputs per workgroup (4 per wave, the correction entries over
+  // 16 lanes); more: lanes per output = the token count rounded up to 16 or 32, one pass of 4 waves
+  const bool small = a.m <= kSmallBlock;
+  const uint32_t tw = a.m <= 16 ? 16u : 32u, per_wg = small ? 16u : 4 * (64 / tw);
   uint32_t eb = (outs + per_wg - 1) / per_wg;  // (one pass: the most latency chains in flight)
   if (GemvMode(a.g.mode) == GemvMode::Accum && eb > 1024) eb = 1024;  // (a Σy² partial per workgroup)
   if (GemvMode(a.g.mode) == GemvMode::Logits && eb > 512) eb = 512;   // (an argmax partial per workgroup)
   a.epi_blocks = eb;
   auto epi = [&](auto k8, auto k16, auto k32) {
-    if (tw == 8) launch_kernel(k8, dim3(eb), dim3(256), st, a);
+    if (small) launch_kernel(k8, dim3(eb), dim3(256), st, a);
     else if (tw == 16) launch_kernel(k16, dim3(eb), dim3(256), st, a);
     else launch_kernel(k32, dim3(eb), dim3(256), st, a);
   };
-#define CHPE_EPI(M) epi(&k_block_epi<int(M), 8>, &k_block_epi<int(M), 16>, &k_block_epi<int(M), 32>)
+#define CHPE_EPI(M) epi(&k_block_epi8<int(M)>, &k_block_epi<int(M), 16>, &k_block_epi<int(M), 32>)
   switch (GemvMode(a.g.mode)) {
     case GemvMode::Store: CHPE_EPI(GemvMode::Store); break;
     case GemvMode::Accum: CHPE_EPI(GemvMode::Accum); break;

@@ -1021,7 +1021,7 @@ bool Engine::plan_block(std::string* err) {
   auto units = [](size_t rows) { return (rows + kBlockUnit - 1) / kBlockUnit; };
   size_t part_floats = 0;  // ranges x kMaxBlock x rows_all, the largest GEMV at any token count
   auto need = [&](size_t n_units, size_t C) {
-    const size_t r = std::max(block_gemv_ranges(uint32_t(n_units), uint32_t(C), 8),
+    const size_t r = std::max(block_gemv_ranges(uint32_t(n_units), uint32_t(C), kSmallBlock),
                               block_gemv_ranges(uint32_t(n_units), uint32_t(C), kMaxBlock));
     part_floats = std::max(part_floats, r * kBlockUnit * n_units);
   };
@@ -1156,6 +1156,7 @@ uint32_t Engine::enqueue_block_gemv(const ProjPlan* const* parts, float* const* 
   b.bits = parts[0]->kind == WeightKind::FlatW2 ? 2u : 4u;  // (16-row cells: 4, read as flat tiles)
   b.m = m;
   b.nq = (m + 3) / 4;
+  b.ts = m <= kSmallBlock ? kSmallBlock : kMaxBlock;
   b.n_units = units;
   b.rows_all = kBlockUnit * units;
   b.partial = d_bpartial_;

@@ -264,6 +264,7 @@ uint32_t launch_gemv_flat_poly(const GemvArgs& a, const uint32_t* n_tiles, float
 // ---- the block step: m <= kMaxBlock tokens at consecutive positions through flat 4- or 2-bit tiles,
 // every weight read once for all m tokens (batch-M verify, chunked prefill) ----------------------
 constexpr uint32_t kMaxBlock = 32;
+constexpr uint32_t kSmallBlock = 8;     // blocks up to this size: k_gemv_mt, token stride 8
 constexpr uint32_t kBlockRange = 2048;  // input columns per workgroup of the block GEMV (<= 8 tokens)
 constexpr uint32_t kBlockUnit = 16;     // weight rows per unit of the block GEMV
 
@@ -277,7 +278,7 @@ struct BlockTables {
                //   columns 32 kq + 16 h .. of the group in the operand byte order
   int4* ci;    // [nq][ng][4]: -8 (4-bit) / -2 (2-bit) * the group's limb sums (limbs 0..3) of token 4T + t
   float* ew;   // [nq][ng][4]: 2^(e - 30) of token 4T + t in the group
-  float* xt;   // [C][kMaxBlock]: the (normalised) input, token-minor (for the outlier corrections)
+  float* xt;   // [C][ts]: the (normalised) input, token-minor (for the outlier corrections)
   float* ss;   // [kMaxBlock]: each token's sum of squares of the raw input (norm GEMVs)
 };
 
@@ -289,7 +290,7 @@ struct BlockGemvArgs {
   uint32_t m, nq;
   uint32_t n_units;    // kBlockUnit-row units over the parts (unit_begin of part p in units)
   uint32_t rows_all;   // kBlockUnit * n_units: rows of the partial-sum buffer
-  float* partial;      // [ranges][rows_all][kMaxBlock]: raw row sums per column range, token-minor
+  float* partial;      // [ranges][rows_all][ts]: raw row sums per column range, token-minor
   const float* ssp;    // [n_ssp][kMaxBlock]: partial sums of x^2 of the input rows (with g.gamma)
   uint32_t n_ssp;
   float* ssp_out;      // Accum: [epi_blocks][kMaxBlock] partial sums of y^2 of the updated rows
@@ -302,6 +303,8 @@ struct BlockGemvArgs {
   uint32_t* brk;            // [kMaxBlock]: token t broke (StepState::broken), cleared by the block's embedding
   uint32_t bits;            // the parts' code width: 4 or 2 (flat tiles)
   uint32_t ranges;          // column ranges of the partial sums (set by launch_block_gemv)
+  uint32_t ts;              // token stride of partial and t.xt: kSmallBlock for m <= kSmallBlock
+                            // (the verify's few tokens on few cache lines), else kMaxBlock
 };
 
 struct BlockFinishArgs {
