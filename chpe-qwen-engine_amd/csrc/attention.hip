@@ -217,7 +217,8 @@ __global__ void __launch_bounds__(NW * 64) k_attn_chunk(AttnArgs a0) {
 // QZ > 1 (a block step): the workgroup serves queries QZ blockIdx.z .. + QZ - 1 in turn over the
 // K and V rows it loaded once (each query's arithmetic as alone), the next query's rows loaded
 // while one is processed.
-constexpr int kAttnQz = 8;  // queries per workgroup of a block step's attention
+constexpr int kAttnQz = 8;    // queries per workgroup of a block step's attention (k_attn_mfma)
+constexpr int kAttnMqQz = 8;  // the same for k_attn_mq
 typedef _Float16 h4_t __attribute__((ext_vector_type(4)));
 typedef float f4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u2_t __attribute__((ext_vector_type(2)));
@@ -413,6 +414,140 @@ __global__ void __launch_bounds__(NW * 64) k_attn_mfma(AttnArgs a) {
   }  // (query z)
 }
 
+// A block step of more than 8 queries (the prefill), fp16 cache, head dim 128, 8 query heads per
+// kv head: workgroup (chunk c of 128 positions, kv head, QZ queries).  The chunk's K rows and V
+// blocks are staged in LDS once; wave w then takes queries w, w + 4, ... of the QZ, each over all
+// 128 positions with k_attn_mfma's arithmetic and operand layouts (the operands read from LDS:
+// eight 16-position tiles per wave), and writes that query's chunk partial (max, sum, weighted V
+// sum) itself: the wave covers the chunk, so there is no merge over waves and no barrier per
+// query.  Rows h and h + 8 of the output product (the f16 weights and their remainders of head h)
+// sit in lanes G and G + 2: one lane exchange adds them.
+template <int QZ>
+__global__ void __launch_bounds__(256) k_attn_mq(AttnArgs a) {
+  constexpr int HD = 128, GQ = 8, CH = 128, NT = CH / 16;
+  constexpr int KD = HD / 4, KS = HD / 16, VD = HD / 16;
+  constexpr int KROW = HD * 2 + 16;  // LDS bytes per K row (16 B of padding: a read's 16 rows on distinct banks)
+  static_assert(QZ % 4 == 0, "");
+  __shared__ __align__(16) uint8_t s_k[CH * KROW];
+  __shared__ __align__(16) uint8_t s_v[CH * HD * 2];  // [CH/4][HD][4] f16, as the cache holds it
+  const uint32_t c = blockIdx.x, kvh = blockIdx.y, p0 = c * CH;
+  const uint32_t nz = a.nq > 1 ? a.nq : 1u, z0 = blockIdx.z * QZ;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int G = lane >> 4, n = lane & 15, h = n & 7;
+  const bool rem = n >= 8;
+  const uint8_t* kc = reinterpret_cast<const uint8_t*>(a.k_cache) + size_t(kvh) * a.max_seq * HD * 2;
+  const uint8_t* vc = reinterpret_cast<const uint8_t*>(a.v_cache) + size_t(kvh) * a.max_seq * HD * 2;
+  // 1. the chunk: K rows (16 threads per 256-byte row) and V blocks (64 threads per 1 KB block of
+  // 4 positions); rows past the cache repeat its last row / block and are masked at use
+  {
+    uint4 kv[8], vv[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const uint32_t e = uint32_t(tid) + 256u * uint32_t(i), row = e / 16, col = e % 16;
+      const uint32_t pk = p0 + row < a.max_seq ? p0 + row : a.max_seq - 1;
+      kv[i] = ld_u128(kc + size_t(pk) * HD * 2 + col * 16);
+      const uint32_t blk = e / 64, piece = e % 64;
+      const uint32_t pb = p0 + 4 * blk < a.max_seq - 3 ? p0 + 4 * blk : a.max_seq - 4;
+      vv[i] = ld_u128(vc + size_t(pb) * HD * 2 + piece * 16);
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const uint32_t e = uint32_t(tid) + 256u * uint32_t(i);
+      *reinterpret_cast<uint4*>(s_k + (e / 16) * KROW + (e % 16) * 16) = kv[i];
+      *reinterpret_cast<uint4*>(s_v + e * 16) = vv[i];
+    }
+  }
+  const uint32_t pos0 = a.state->pos;
+  __syncthreads();
+  // 2. the wave's queries (no barrier below: a wave leaves on its own)
+  for (int k = 0; k < QZ / 4; ++k) {
+    const uint32_t z = z0 + uint32_t(wave) + 4u * uint32_t(k);
+    if (z >= nz) break;
+    const uint32_t ctx = pos0 + z + 1;
+    if (p0 >= ctx) continue;  // (a later query may reach the chunk)
+    const float* qsrc = a.q + size_t(z) * a.H * HD + size_t(kvh * GQ + h) * HD + G * KD;
+    float4 qv[KD / 4];
+#pragma unroll
+    for (int i = 0; i < KD / 4; ++i) qv[i] = ld_f4(qsrc + 4 * i);
+    h4_t qb[KS];
+#pragma unroll
+    for (int st = 0; st < KS; ++st) qb[st] = f16_part(qv[st].x, qv[st].y, qv[st].z, qv[st].w, rem);
+    // scores: lane (G, n) gets head h at positions 4G + i of each tile
+    float sc[NT][4];
+    float m = -INFINITY;
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      f4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+      const uint8_t* kr = s_k + (t * 16 + n) * KROW + G * KD * 2;
+#pragma unroll
+      for (int st = 0; st < KS; ++st) {
+        const uint4 w = *reinterpret_cast<const uint4*>(kr + 16 * (st / 2));
+        const h4_t kk = (st & 1) ? as_h4(w.z, w.w) : as_h4(w.x, w.y);
+        acc = __builtin_amdgcn_mfma_f32_16x16x16f16(kk, qb[st], acc, 0, 0, 0);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float sv = pair_sum(acc[i], 8);
+        const bool ok = p0 + t * 16 + 4 * G + i < ctx;
+        sc[t][i] = ok ? sv * a.scale : -INFINITY;
+        m = fmaxf(m, sc[t][i]);
+      }
+    }
+    m = pair_max(pair_max(m, 16), 32);
+    // exp-weights, their sum per head; O = P . V
+    float l = 0.0f;
+    f4_t o[VD];
+#pragma unroll
+    for (int j = 0; j < VD; ++j) o[j] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      float e[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        e[i] = sc[t][i] > -INFINITY ? expf(sc[t][i] - m) : 0.0f;
+        l += e[i];
+      }
+      const h4_t pa = f16_part(e[0], e[1], e[2], e[3], rem);
+      // V rows past the context hold stale or zero rows: zeroed, so that 0 * (non-finite) cannot
+      // reach the sums (e = 0 there already)
+      const uint32_t pb = p0 + t * 16 + 4 * G;
+      const uint32_t mlo = (pb < ctx ? 0xffffu : 0u) | (pb + 1 < ctx ? 0xffff0000u : 0u);
+      const uint32_t mhi = (pb + 2 < ctx ? 0xffffu : 0u) | (pb + 3 < ctx ? 0xffff0000u : 0u);
+      const uint8_t* vr = s_v + size_t(t * 4 + G) * HD * 8 + n * VD * 8;
+#pragma unroll
+      for (int j = 0; j < VD; ++j) {
+        const uint4 w0 = *reinterpret_cast<const uint4*>(vr + 16 * (j / 2));
+        const uint4 w = make_uint4(w0.x & mlo, w0.y & mhi, w0.z & mlo, w0.w & mhi);
+        const h4_t vv = (j & 1) ? as_h4(w.z, w.w) : as_h4(w.x, w.y);
+        o[j] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa, vv, o[j], 0, 0, 0);
+      }
+    }
+    l = pair_sum(pair_sum(l, 16), 32);
+    // 3. the chunk partial of query z: (max, sum) per head, and the weighted V sums of rows h and
+    // h + 8 added (lanes G and G + 2: lanes G < 2 hold heads 4 G + i, dims n VD + j)
+    const uint32_t nch = a.n_chunks;
+    float* const part_ml = a.part_ml + size_t(z) * a.H * nch * 2;
+    float* const part_acc = a.part_acc + size_t(z) * a.H * nch * HD;
+    if (G == 0 && n < GQ) {
+      const size_t hc = size_t(kvh * GQ + n) * nch + c;
+      part_ml[hc * 2] = m;
+      part_ml[hc * 2 + 1] = l;
+    }
+#pragma unroll
+    for (int j = 0; j < VD; ++j)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) o[j][i] = pair_sum(o[j][i], 32);
+    if (G < 2) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float* dst = part_acc + (size_t(kvh * GQ + 4 * G + i) * nch + c) * HD + n * VD;
+        *reinterpret_cast<float4*>(dst) = make_float4(o[0][i], o[1][i], o[2][i], o[3][i]);
+        *reinterpret_cast<float4*>(dst + 4) = make_float4(o[4][i], o[5][i], o[6][i], o[7][i]);
+      }
+    }
+  }
+}
+
 // out[h][d] = sum_c A_c[d] w_c / sum_c L_c w_c, w_c = exp(M_c - M), over the active chunks.  One
 // wave per (head, 64 dims): lane d of dims block y.  The chunk statistics are spread over the
 // lanes (chunk lane + 64 k), the weights go through LDS (w_c = 0 past the active chunks, whose
@@ -498,7 +633,7 @@ void launch_attention_partial(const AttnArgs& a, hipStream_t st) {
   const uint32_t gq = a.H / a.KV;
   // (the chunk size a.chunk = attn_chunk(hd, KV) picks the instance: CH = waves x positions)
   if (a.hd == 128 && gq == 8 && a.chunk == 128) {  // fp16: 4 waves x 2 tiles; f32: 8 waves x 16 positions
-    if (mq) launch_kernel(&k_attn_mfma<128, 8, 4, 2, kAttnQz>, grid_mq, dim3(256), st, a);
+    if (mq) launch_kernel(&k_attn_mq<kAttnMqQz>, dim3(a.n_chunks, a.KV, (nq + kAttnMqQz - 1) / kAttnMqQz), dim3(256), st, a);
     else if (a.kv_f16) launch_kernel(&k_attn_mfma<128, 8, 4, 2, 1>, grid, dim3(256), st, a);
     else launch_kernel(&k_attn_chunk<128, 8, float, 4, 8>, grid, dim3(512), st, a);
   } else if (a.hd == 128 && gq == 8) {  // 64: fp16 4 waves x 1 tile; f32 4 waves x 16 positions, 4 lanes per K row
