@@ -74,10 +74,11 @@ std::unique_ptr<Engine> Engine::create(const uint8_t* bytes, size_t len, const E
 
 Engine::~Engine() {
   if (stream_) (void)hipStreamSynchronize(stream_);
-  for (uint32_t m = 0; m <= kMaxBlock; ++m) {
-    if (bgraph_exec_[m]) (void)hipGraphExecDestroy(bgraph_exec_[m]);
-    if (bgraph_[m]) (void)hipGraphDestroy(bgraph_[m]);
-  }
+  for (int hd = 0; hd < 2; ++hd)
+    for (uint32_t m = 0; m <= kMaxBlock; ++m) {
+      if (bgraph_exec_[hd][m]) (void)hipGraphExecDestroy(bgraph_exec_[hd][m]);
+      if (bgraph_[hd][m]) (void)hipGraphDestroy(bgraph_[hd][m]);
+    }
   if (graph_exec_) (void)hipGraphExecDestroy(graph_exec_);
   if (graph_) (void)hipGraphDestroy(graph_);
   for (void* p : allocs_) (void)hipFree(p);
@@ -1181,8 +1182,9 @@ uint32_t Engine::enqueue_block_gemv(const ProjPlan* const* parts, float* const* 
   return launch_block_gemv(b, st);
 }
 
-int Engine::block_forward(const uint32_t* tokens, size_t m, size_t pos, uint32_t* out_argmax, ForwardResult* last) {
-  if (!block_ok_ || !tokens || m == 0 || m > kMaxBlock) return -1;
+int Engine::block_forward(const uint32_t* tokens, size_t m, size_t pos, uint32_t* out_argmax, ForwardResult* last,
+                          bool head) {
+  if (!block_ok_ || !tokens || m == 0 || m > kMaxBlock || (!head && (out_argmax || last))) return -1;
   if (pos + m > cfg_.max_seq_len) return -2;
   const uint64_t t0 = now_ns();
   const uint32_t mm = uint32_t(m);
@@ -1193,19 +1195,22 @@ int Engine::block_forward(const uint32_t* tokens, size_t m, size_t pos, uint32_t
       hipMemcpyAsync(d_bstate_, h_bstate_, sizeof(StepState), hipMemcpyHostToDevice, st) != hipSuccess)
     return -3;
   if (cfg_.hybrid && pos == 0) reset_hybrid_state(st);  // a new sequence (outside the graph)
-  if (use_graph_) {  // one captured graph per token count, captured on first use
-    if (!bgraph_exec_[m]) {
+  bhead_ = head;
+  if (use_graph_) {  // one captured graph per (head, token count), captured on first use
+    hipGraph_t& g = bgraph_[head ? 1 : 0][m];
+    hipGraphExec_t& ge = bgraph_exec_[head ? 1 : 0][m];
+    if (!ge) {
       if (hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal) != hipSuccess) return -3;
       record_block(mm, st);
-      if (hipStreamEndCapture(st, &bgraph_[m]) != hipSuccess) return -3;
+      if (hipStreamEndCapture(st, &g) != hipSuccess) return -3;
       if (bpart_short_) {
-        (void)hipGraphDestroy(bgraph_[m]);
-        bgraph_[m] = nullptr;
+        (void)hipGraphDestroy(g);
+        g = nullptr;
         return -3;
       }
-      if (hipGraphInstantiate(&bgraph_exec_[m], bgraph_[m], nullptr, nullptr, 0) != hipSuccess) return -3;
+      if (hipGraphInstantiate(&ge, g, nullptr, nullptr, 0) != hipSuccess) return -3;
     }
-    if (hipGraphLaunch(bgraph_exec_[m], st) != hipSuccess) return -3;
+    if (hipGraphLaunch(ge, st) != hipSuccess) return -3;
   } else {
     record_block(mm, st);
     if (bpart_short_) {
@@ -1213,6 +1218,7 @@ int Engine::block_forward(const uint32_t* tokens, size_t m, size_t pos, uint32_t
       return -3;
     }
   }
+  if (!head) return hipStreamSynchronize(st) == hipSuccess ? 0 : -3;
   if (hipMemcpyAsync(h_bout_, d_bout_, m * 4, hipMemcpyDeviceToHost, st) != hipSuccess ||
       hipMemcpyAsync(h_result_, d_result_, sizeof(StepResult), hipMemcpyDeviceToHost, st) != hipSuccess)
     return -3;
@@ -1260,6 +1266,7 @@ void Engine::record_block(uint32_t mm, hipStream_t st) {
     const ProjPlan* dn[1] = {&L.down};
     n_ss = enqueue_block_gemv(dn, hid, 1, GemvMode::Accum, d_bmlp_, I, nullptr, 0, mm, l, st);
   }
+  if (!bhead_) return;  // (a prefill block before the last: its logits are not read)
   const ProjPlan* lm[1] = {&lm_head_};
   float* lg[1] = {d_blog_};
   const uint32_t eb = enqueue_block_gemv(lm, lg, 1, GemvMode::Logits, d_bx_, D, d_gamma_final_, n_ss, mm, 0, st);
@@ -1362,6 +1369,7 @@ void Engine::record_block_hybrid(uint32_t mm, hipStream_t st) {
     const ProjPlan* dnp[1] = {&L.down};
     n_ss = enqueue_block_gemv(dnp, hid, 1, GemvMode::Accum, d_bmlp_, I, nullptr, 0, mm, l, st);
   }
+  if (!bhead_) return;  // (a prefill block before the last: its logits are not read)
   const ProjPlan* lm[1] = {&lm_head_};
   float* lg[1] = {d_blog_};
   const uint32_t eb = enqueue_block_gemv(lm, lg, 1, GemvMode::Logits, d_bx_, D, d_gamma_final_, n_ss, mm, 0, st);
@@ -1381,7 +1389,8 @@ int Engine::prefill(const uint32_t* tokens, size_t n, ForwardResult* out) {
   uint32_t am[kMaxBlock];
   for (size_t i = 0; i < n; i += kMaxBlock) {
     const size_t m = std::min<size_t>(kMaxBlock, n - i);
-    const int rc = block_forward(tokens + i, m, i, am, out);
+    const bool head = i + m == n;  // (only the last block's logits are read)
+    const int rc = block_forward(tokens + i, m, i, head ? am : nullptr, head ? out : nullptr, head);
     if (rc) return rc;
   }
   // continue greedy decoding from here: the last argmax at position n

@@ -152,7 +152,9 @@ class Engine {
   // its result *last.  The decode state is not touched.  0, -1 bad arguments or no block step
   // for this archive, -2 past max_seq_len, -3 device error.  (verify() and prefill() then leave
   // the decode state where the sequential steps would: the last argmax at pos + m.)
-  int block_forward(const uint32_t* tokens, size_t m, size_t pos, uint32_t* out_argmax, ForwardResult* last);
+  // head false: no LM head (out_argmax and last must be null; the prefill's blocks before its last)
+  int block_forward(const uint32_t* tokens, size_t m, size_t pos, uint32_t* out_argmax, ForwardResult* last,
+                    bool head = true);
   bool block_ready() const { return block_ok_; }
   // positions 0..n-1 teacher-forced in blocks of kMaxBlock (prefill); result and logits of
   // the last position; the decode state is left at (argmax of the last, n)
@@ -302,8 +304,11 @@ class Engine {
   float *d_bhx0_ = nullptr, *d_bhx1_ = nullptr, *d_bhx2_ = nullptr, *d_bhx3_ = nullptr, *d_bhconv_ = nullptr;
   BlockTables btab_{};
   ArgmaxPartial* d_bpartials_ = nullptr;
-  hipGraph_t bgraph_[kMaxBlock + 1] = {};          // captured block steps, by token count
-  hipGraphExec_t bgraph_exec_[kMaxBlock + 1] = {};
+  // captured block steps, by [with the LM head][token count]; bhead_: the one being recorded has
+  // the LM head (the prefill's blocks before its last have none: their logits are not read)
+  hipGraph_t bgraph_[2][kMaxBlock + 1] = {};
+  hipGraphExec_t bgraph_exec_[2][kMaxBlock + 1] = {};
+  bool bhead_ = true;
   int probe_stage_ = -1;                 // stage bracketed by events in record_step
   hipEvent_t* probe_events_ = nullptr;
   size_t probe_next_ = 0;
