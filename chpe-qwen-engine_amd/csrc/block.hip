@@ -776,9 +776,10 @@ __global__ void __launch_bounds__(256) k_block_epi8(BlockGemvArgs a) {
 }
 
 // Epilogue of blocks of more than kSmallBlock tokens (token stride kMaxBlock): a wave serves
-// 64 / TW outputs, TW lanes each (TW >= m): lane (i, t) = output i, token t.  Per token: the ranges' raw sums in range order, the outlier corrections of the row
-// in entry order (w * x[col] of the token: the flat tiles' replace deltas, the cells' added
-// outliers), then the batch-1 step's epilogue.  Outputs: rows of part 0 (Store / Accum /
+// 64 / TW outputs, TW lanes each (TW >= m): lane (i, t) = output i, token t.  Per token: the
+// ranges' raw sums in range order, the outlier corrections of the row in entry order (w * x[col]
+// of the token: the flat tiles' replace deltas, the cells' added outliers; the row's non-zero
+// entries only, BlockGemvArgs::cpack), then the batch-1 step's epilogue.  Outputs: rows of part 0 (Store / Accum /
 // Logits), gate row = up row (SwiGlu), RoPE pairs of every part (QkvRope).
 template <int MODE, int TW>
 __global__ void __launch_bounds__(256) k_block_epi(BlockGemvArgs a) {
@@ -842,26 +843,22 @@ __global__ void __launch_bounds__(256) k_block_epi(BlockGemvArgs a) {
       }
       for (; rg < ranges; ++rg) acc_s += ps[rg * rstride];
       float c = 0.0f;
-      const float2* corr = P.corr;
-      const uint32_t kmax = P.corr_kmax;
-      if (corr != nullptr && r < P.wrows) {
-        // eight entries' loads, then their eight columns' loads, in flight together
-        const float2* ce = corr + size_t(r) * kmax;
-        uint32_t e = 0;
-        for (; e + 8 <= kmax; e += 8) {
+      const uint32_t* coff = a.coff[kSwi ? k : p];
+      if (coff != nullptr && r < P.wrows) {
+        // the row's non-zero entries (the padded table's terms in its order), eight entries'
+        // loads, then their eight columns' loads, in flight together (a trip past the row's
+        // last entry repeats it and adds nothing)
+        const float2* ce = a.cpack[kSwi ? k : p];
+        const uint32_t e1 = coff[r + 1];
+        for (uint32_t e = coff[r]; e < e1; e += 8) {
           float2 cv[8];
           float xc[8];
 #pragma unroll
-          for (int j = 0; j < 8; ++j) cv[j] = ce[e + uint32_t(j)];
+          for (int j = 0; j < 8; ++j) cv[j] = ce[e + uint32_t(j) < e1 ? e + uint32_t(j) : e1 - 1];
 #pragma unroll
           for (int j = 0; j < 8; ++j) xc[j] = a.t.xt[size_t(__float_as_uint(cv[j].x)) * kMaxBlock + t];
 #pragma unroll
-          for (int j = 0; j < 8; ++j) c = cv[j].y != 0.0f ? fmaf(cv[j].y, xc[j], c) : c;  // (padding: w = 0)
-        }
-        for (; e < kmax; ++e) {
-          const float2 cv = ce[e];
-          const float xc = a.t.xt[size_t(__float_as_uint(cv.x)) * kMaxBlock + t];
-          c = cv.y != 0.0f ? fmaf(cv.y, xc, c) : c;
+          for (int j = 0; j < 8; ++j) c = e + uint32_t(j) < e1 ? fmaf(cv[j].y, xc[j], c) : c;
         }
       }
       v[k] = acc_s + c;

@@ -470,6 +470,11 @@ bool Engine::plan_projection(size_t tile_start, size_t num_tiles, size_t r_total
         p->corr = static_cast<float2*>(dev_alloc(fp.corr.size() * sizeof(float2)));
         if (!p->corr) { *err = "allocation"; return false; }
         (void)hipMemcpy(p->corr, fp.corr.data(), fp.corr.size() * sizeof(float2), hipMemcpyHostToDevice);
+        if ((fp.kind == WeightKind::FlatW4 || fp.kind == WeightKind::FlatW2) &&
+            !plan_packed_corrections(fp.corr, r_total, fp.corr_kmax, p)) {
+          *err = "allocation";
+          return false;
+        }
       }
       p->poly.n_cells = fp.n_tiles;
       if (fp.kind == WeightKind::FlatPoly && !ensure_poly_buffers(fp.n_tiles, uint32_t(c_total))) {
@@ -1123,6 +1128,36 @@ bool Engine::plan_cell_corrections(ProjPlan* p, size_t C, std::string* err) {
   }
   (void)hipMemcpy(p->bcorr, corr.data(), corr.size() * sizeof(float2), hipMemcpyHostToDevice);
   p->bcorr_kmax = 8;
+  if (!plan_packed_corrections(corr, rows, 8, p)) {
+    *err = "allocation";
+    return false;
+  }
+  return true;
+}
+
+// The block epilogue's form of a [rows][kmax] correction table: only the entries with a
+// non-zero weight (a zero-weight entry -- padding, or an outlier equal to its code's value --
+// adds no term), row after row in entry order, and each row's first entry, so that a row's
+// loop runs over its own entries instead of the table's widest row.  The terms and their order
+// are those of the padded table.
+bool Engine::plan_packed_corrections(const std::vector<float2>& padded, size_t rows, uint32_t kmax, ProjPlan* p) {
+  std::vector<uint32_t> off(rows + 1);
+  std::vector<float2> pk;
+  pk.reserve(padded.size());
+  for (size_t r = 0; r < rows; ++r) {
+    off[r] = uint32_t(pk.size());
+    for (uint32_t k = 0; k < kmax; ++k) {
+      const float2 e = padded[r * kmax + k];
+      if (e.y != 0.0f) pk.push_back(e);  // (a NaN weight stays: it makes the row NaN)
+    }
+  }
+  off[rows] = uint32_t(pk.size());
+  if (pk.empty()) pk.push_back(make_float2(0.0f, 0.0f));  // (an allocation; no row reads it)
+  p->boff = static_cast<uint32_t*>(dev_alloc(off.size() * sizeof(uint32_t)));
+  p->bpack = static_cast<float2*>(dev_alloc(pk.size() * sizeof(float2)));
+  if (!p->boff || !p->bpack) return false;
+  (void)hipMemcpy(p->boff, off.data(), off.size() * sizeof(uint32_t), hipMemcpyHostToDevice);
+  (void)hipMemcpy(p->bpack, pk.data(), pk.size() * sizeof(float2), hipMemcpyHostToDevice);
   return true;
 }
 
@@ -1150,6 +1185,12 @@ uint32_t Engine::enqueue_block_gemv(const ProjPlan* const* parts, float* const* 
     gp.bias = p.bias;
     gp.corr = p.bcorr ? p.bcorr : p.corr;
     gp.corr_kmax = p.bcorr ? p.bcorr_kmax : p.corr_kmax;
+    b.cpack[i] = gp.corr ? p.bpack : nullptr;
+    b.coff[i] = gp.corr ? p.boff : nullptr;
+    if (gp.corr && !p.boff) {  // (every block-step part's table has its packed form: plan_projection, plan_block)
+      bpart_short_ = true;
+      return 1;
+    }
     gp.rope_role = mode == GemvMode::QkvRope ? (roles_in ? roles_in[i] : roles[i]) : 0u;
     units += (p.rows + kBlockUnit - 1) / kBlockUnit;
   }
@@ -1549,6 +1590,12 @@ bool Engine::plan_hybrid(std::string* err) {
             H.ab.rows = H.ab.wrows = 64;
             H.ab.corr = dc;
             H.ab.corr_kmax = fp.corr_kmax;
+            H.ab.bpack = nullptr;
+            H.ab.boff = nullptr;
+            if (dc && !plan_packed_corrections(fp.corr, 64, fp.corr_kmax, &H.ab)) {
+              *err = "allocation";
+              return false;
+            }
             H.ab.xcodes = nullptr;
             H.has_ab = true;
           }

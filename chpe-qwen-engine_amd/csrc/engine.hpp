@@ -61,6 +61,9 @@ struct ProjPlan {
   CellReplace* repl = nullptr;         // device, replace-mode outliers of 16-row cells
   float2* bcorr = nullptr;             // device [rows][bcorr_kmax]: a 16-row cell tensor's outliers as
   uint32_t bcorr_kmax = 0;             //   the block step's per-row corrections (plan_block)
+  float2* bpack = nullptr;             // device: the non-zero entries of the block step's corrections
+  uint32_t* boff = nullptr;            //   (bcorr, else corr) row after row, and each row's first entry
+                                       //   [rows + 1] (plan_packed_corrections)
   uint8_t* xcodes = nullptr;           // device, the decode launch's codes in the persistent
                                        //   matrix-core kernel's load order (see xm_layout_bytes);
                                        //   set on the launch's first part, and passed only to
@@ -288,6 +291,7 @@ class Engine {
   uint32_t rope_dim_ = 0;   // dims of a head the rotary tables cover (head_dim; hybrid: 64)
   std::vector<CellReplace> lm_repl_host_;  // the tied cell LM head's replace tables (for plan_block)
   bool plan_cell_corrections(ProjPlan* p, size_t C, std::string* err);
+  bool plan_packed_corrections(const std::vector<float2>& padded, size_t rows, uint32_t kmax, ProjPlan* p);
 
   // the block step (plan_block): m <= kMaxBlock tokens' activations, operand tables, partials
   bool block_ok_ = false;

@@ -305,6 +305,11 @@ struct BlockGemvArgs {
   uint32_t ranges;          // column ranges of the partial sums (set by launch_block_gemv)
   uint32_t ts;              // token stride of partial and t.xt: kSmallBlock for m <= kSmallBlock
                             // (the verify's few tokens on few cache lines), else kMaxBlock
+  // per part, the outlier corrections of the epilogue of more than kSmallBlock tokens: the
+  // non-zero entries of g.part[p].corr row after row in entry order, and each row's first entry
+  // ([rows + 1]); null when the part has none
+  const float2* cpack[kMaxParts];
+  const uint32_t* coff[kMaxParts];
 };
 
 struct BlockFinishArgs {
