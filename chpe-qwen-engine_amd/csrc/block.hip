@@ -808,7 +808,9 @@ __global__ void __launch_bounds__(256) k_block_epi(BlockGemvArgs a) {
   const uint32_t pos0 = kRope ? a.state->pos : 0u;
   for (uint32_t ob = (blockIdx.x * 4 + uint32_t(wave)) * OPW; ob < total; ob += gridDim.x * 4 * OPW) {
     const uint32_t o = ob + i;
-    if (o >= total || !live) continue;
+    // (every lane of an output's TW runs the sums: the correction entries are loaded one per
+    // lane; lanes of tokens past m read stale partial sums and inputs and store nothing)
+    if (o >= total) continue;
     // the output's part and rows
     int p = 0;
     uint32_t rows_k[NR];
@@ -824,6 +826,15 @@ __global__ void __launch_bounds__(256) k_block_epi(BlockGemvArgs a) {
     } else {
       rows_k[0] = o;
       if constexpr (kSwi) rows_k[1] = o;
+    }
+    // the rows' correction ranges, requested before the partial sums
+    uint32_t e0[NR], e1[NR];
+#pragma unroll
+    for (int k = 0; k < NR; ++k) {
+      const uint32_t* coff = a.coff[kSwi ? k : p];
+      const bool has = coff != nullptr && rows_k[k] < a.g.part[kSwi ? k : p].wrows;
+      e0[k] = has ? coff[rows_k[k]] : 0u;
+      e1[k] = has ? coff[rows_k[k] + 1] : 0u;
     }
     float v[NR];
 #pragma unroll
@@ -843,26 +854,35 @@ __global__ void __launch_bounds__(256) k_block_epi(BlockGemvArgs a) {
       }
       for (; rg < ranges; ++rg) acc_s += ps[rg * rstride];
       float c = 0.0f;
-      const uint32_t* coff = a.coff[kSwi ? k : p];
-      if (coff != nullptr && r < P.wrows) {
-        // the row's non-zero entries (the padded table's terms in its order), eight entries'
-        // loads, then their eight columns' loads, in flight together (a trip past the row's
-        // last entry repeats it and adds nothing)
+      {
+        // the row's non-zero entries (the padded table's terms in its order): TW entries in one
+        // load, one per lane of the output, then each entry's column and weight from its lane
+        // and 16 columns' loads in flight together (entries past the row's last repeat it and
+        // add nothing)
         const float2* ce = a.cpack[kSwi ? k : p];
-        const uint32_t e1 = coff[r + 1];
-        for (uint32_t e = coff[r]; e < e1; e += 8) {
-          float2 cv[8];
-          float xc[8];
+        const uint32_t ee = e1[k];
+        const int g0 = lane & ~(TW - 1);  // the output's first lane
+        for (uint32_t e = e0[k]; e < ee; e += TW) {
+          const float2 mine = ce[e + t < ee ? e + t : ee - 1];
+          const uint32_t n = ee - e < uint32_t(TW) ? ee - e : uint32_t(TW);
+          for (uint32_t j = 0; j < n; j += 16) {  // (j + 15 < TW)
+            float xc[16];
 #pragma unroll
-          for (int j = 0; j < 8; ++j) cv[j] = ce[e + uint32_t(j) < e1 ? e + uint32_t(j) : e1 - 1];
+            for (int jj = 0; jj < 16; ++jj) {
+              const uint32_t col = __shfl(__float_as_uint(mine.x), g0 + int(j) + jj);
+              xc[jj] = a.t.xt[size_t(col) * kMaxBlock + t];
+            }
 #pragma unroll
-          for (int j = 0; j < 8; ++j) xc[j] = a.t.xt[size_t(__float_as_uint(cv[j].x)) * kMaxBlock + t];
-#pragma unroll
-          for (int j = 0; j < 8; ++j) c = e + uint32_t(j) < e1 ? fmaf(cv[j].y, xc[j], c) : c;
+            for (int jj = 0; jj < 16; ++jj) {
+              const float w = __shfl(mine.y, g0 + int(j) + jj);
+              c = j + uint32_t(jj) < n ? fmaf(w, xc[jj], c) : c;
+            }
+          }
         }
       }
       v[k] = acc_s + c;
     }
+    if (!live) continue;
     const GemvPart& P0 = a.g.part[kSwi ? 0 : p];
     const uint32_t r = rows_k[0];
     float* y = P0.y + size_t(t) * P0.rows;
