@@ -1660,19 +1660,19 @@ void Engine::record_step_hybrid(hipStream_t st) {
     float* hid[1] = {d_hidden_};
     // the normalised in-projections: one launch when the parts share a weight layout, else one
     // launch per part (as enqueue_qkv)
-    auto in_proj = [&](const ProjPlan* const* ps, float* const* os, int n) {
+    auto in_proj = [&](const ProjPlan* const* ps, float* const* os, int n, const uint32_t* roles) {
       bool same = true;
       for (int i = 1; i < n; ++i) same = same && ps[i]->kind == ps[0]->kind;
       if (same) {
-        enqueue_gemv(ps, os, n, GemvMode::QkvRope, d_hidden_, D, L.gamma_in, st, &ra, store);
+        enqueue_gemv(ps, os, n, GemvMode::QkvRope, d_hidden_, D, L.gamma_in, st, &ra, roles);
         return;
       }
-      for (int i = 0; i < n; ++i) enqueue_gemv(&ps[i], &os[i], 1, GemvMode::QkvRope, d_hidden_, D, L.gamma_in, st, &ra, store);
+      for (int i = 0; i < n; ++i) enqueue_gemv(&ps[i], &os[i], 1, GemvMode::QkvRope, d_hidden_, D, L.gamma_in, st, &ra, roles + i);
     };
     if (H.full) {
       const ProjPlan* in[3] = {&H.in0, &H.in1, &H.in2};
       float* outs[3] = {d_hx0_, d_hx1_, d_hx2_};
-      in_proj(in, outs, 3);
+      in_proj(in, outs, 3, store);
       const RopeArgs kv = rope_args(l);
       HybQkArgs q{};
       q.state = d_state_;
@@ -1702,16 +1702,19 @@ void Engine::record_step_hybrid(hipStream_t st) {
       const ProjPlan* o[1] = {&H.out};
       enqueue_gemv(o, hid, 1, GemvMode::Accum, d_attn_, uint32_t(q.H * q.hd), nullptr, st);
     } else {
+      // in_proj_qkv's rows go through the causal conv in the launch's epilogue (kRoleConv):
+      // d_hconv_ receives silu(conv), the conv state is shifted there
       const ProjPlan* in[3] = {&H.in0, &H.in1, H.has_ab ? &H.ab : &H.in2};
-      float* outs[3] = {d_hx0_, d_hx1_, d_hx2_};
-      in_proj(in, outs, 3);
+      float* outs[3] = {d_hconv_, d_hx1_, d_hx2_};
+      const uint32_t conv_roles[3] = {kRoleConv, kRoleStore, kRoleStore};
+      ra.conv_w = H.conv_w;  // (in place of the KV cache pointers: no part appends a KV row)
+      ra.conv_state = d_conv_state_ + size_t(H.lin) * 8192 * (kDnConvTaps - 1);
+      in_proj(in, outs, 3, conv_roles);
       if (!H.has_ab) {
         const ProjPlan* inb[1] = {&H.in3};
         float* outb[1] = {d_hx3_};
-        in_proj(inb, outb, 1);
+        in_proj(inb, outb, 1, store);
       }
-      DnConvArgs c{d_hx0_, H.conv_w, d_conv_state_ + size_t(H.lin) * 8192 * 3, d_hconv_, 8192, 4, d_state_};
-      launch_dn_conv(c, st);
       DnStepArgs dn{};
       dn.q = d_hconv_;
       dn.k = d_hconv_ + 2048;

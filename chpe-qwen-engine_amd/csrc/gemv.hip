@@ -605,13 +605,41 @@ __device__ __forceinline__ bool break_now(const GemvArgs& a, const BreakIn& b, b
   }
 }
 
+// kRoleConv: channel c of the hybrid's depthwise causal conv with input x (k_dn_conv's
+// arithmetic: the oldest tap first, the new input last, then SiLU); the state is shifted unless
+// the step broke
+__device__ __forceinline__ void conv_store(const RopeArgs& ra, const GemvPart& P, uint32_t c, float x, bool brk) {
+#pragma clang fp contract(off)
+  constexpr uint32_t T = kDnConvTaps;
+  const float* w = ra.conv_w + size_t(c) * T;
+  float* st = ra.conv_state + size_t(c) * (T - 1);
+  float sv[T - 1];
+#pragma unroll
+  for (uint32_t k = 0; k + 1 < T; ++k) sv[k] = st[k];
+  float acc = 0.0f;
+#pragma unroll
+  for (uint32_t k = 0; k + 1 < T; ++k) acc += w[k] * sv[k];
+  acc += w[T - 1] * x;
+  P.y[c] = acc / (1.0f + expf(-acc));
+  if (brk) return;
+#pragma unroll
+  for (uint32_t k = 0; k + 2 < T; ++k) st[k] = sv[k + 1];
+  st[T - 2] = x;
+}
+
 // QkvRope epilogue for the pair (r, r + half) of part P: bias added, then RoPE (q, k) with the
 // reference's arithmetic (x0*cos - x1*sin, x0*sin + x1*cos, :212-213); q into y, k and v into
-// the KV cache at `pos`, rounded to the cache type (not after a break: brk).
+// the KV cache at `pos`, rounded to the cache type (not after a break: brk).  kRoleConv: both
+// rows through the hybrid's conv (conv_store).
 __device__ __forceinline__ void rope_store(const GemvArgs& a, const GemvPart& P, uint32_t r, float lo, float hi,
                                            float c, float sn, bool brk) {
 #pragma clang fp contract(off)
   const uint32_t half = a.rope.head_dim / 2;
+  if (P.rope_role == kRoleConv) {
+    conv_store(a.rope, P, r, lo, brk);
+    conv_store(a.rope, P, r + half, hi, brk);
+    return;
+  }
   float o0 = lo, o1 = hi;
   if (P.rope_role < kRoleV) {
     o0 = lo * c - hi * sn;

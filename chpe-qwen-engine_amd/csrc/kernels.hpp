@@ -40,16 +40,32 @@ enum class GemvMode : int {
 };
 
 // kRoleStore: the part's rows stored as computed (no rotation, no KV append) -- the normalised
-// input projections of the hybrid layers, whose per-head norms and rotary embedding come after
-enum RopeRole : uint32_t { kRoleQ = 0, kRoleK = 1, kRoleV = 2, kRoleStore = 3 };
+// input projections of the hybrid layers, whose per-head norms and rotary embedding come after.
+// kRoleConv: row c is channel c of the hybrid's depthwise causal conv (RopeArgs::conv_w,
+// conv_state): silu(conv over [state, row]) stored, the state shifted (not after a break) -- the
+// decode step's in_proj_qkv, with k_dn_conv's arithmetic
+enum RopeRole : uint32_t { kRoleQ = 0, kRoleK = 1, kRoleV = 2, kRoleStore = 3, kRoleConv = 4 };
+constexpr uint32_t kDnConvTaps = 4;  // the hybrid's conv kernel size (kRoleConv)
+// (the conv's weights and state travel in RopeArgs' cache pointers: a launch with a conv part
+// has no part that appends a KV row)
 struct StepState;
 
 struct RopeArgs {            // QkvRope: applyRope (chpe_engine.zig:195-216) + KV append (:1693-1697)
   StepState* state;          // (also set for the residual launches: StepState::broken)
   const float* cos;          // [head_dim/2]: the step's row of the cos table (staged by k_embed /
   const float* sin;          //   k_finish from the [max_seq][head_dim/2] tables), and of sin
-  void* k_cache;             // this layer: [KV][max_seq][head_dim], f16 or f32
-  void* v_cache;             // f32: as k_cache; f16: [KV][max_seq/4][head_dim][4] (4-position blocks)
+  // this layer: [KV][max_seq][head_dim], f16 or f32; a launch with a kRoleConv part (whose parts
+  // append no KV row) holds the conv's [channels][kDnConvTaps] weights here instead
+  union {
+    void* k_cache;
+    const float* conv_w;
+  };
+  // f32: as k_cache; f16: [KV][max_seq/4][head_dim][4] (4-position blocks); with a kRoleConv
+  // part: the conv state [channels][kDnConvTaps - 1], oldest first, shifted in place
+  union {
+    void* v_cache;
+    float* conv_state;
+  };
   uint32_t head_dim, max_seq, kv_f16;  // max_seq: cache rows per kv head, a multiple of 16
   uint32_t brk_check;        // the break test this launch makes on its input (see StepState::broken):
                              //   0 none (layer 0), 1 the sum of squares (after layers 0-2 and 8-16),
