@@ -8,10 +8,12 @@
 // RMSNormGated :168-184).
 //
 // k_dn_conv: the depthwise causal conv over [state, x] + SiLU, one thread per channel, the
-// state shifted in place.  k_dn_step: a workgroup per (value head, 16-column block): its slab
-// of the head's 128x128 f32 state is read once and written once (the columns of the update are
-// independent; 32 heads x 8 blocks = 256 workgroups at the 9B shape); k_dn_gnorm: the gated
-// RMSNorm of each head's output.  Memory-bound: 2 x 64 KiB of state per head and step.
+// state shifted in place (the decode step applies it in its in-projection's epilogue instead).
+// k_dn_step_head: the gated delta rule and the gated RMSNorm of one value head per workgroup
+// (the decode step's form); k_dn_step: a workgroup per (value head, 16-column block), its slab
+// of the head's 128x128 f32 state read once and written once (the columns of the update are
+// independent), with k_dn_gnorm for the gated RMSNorm of each head's output.  2 x 64 KiB of
+// state per head and step.
 //
 // The block step (m <= kMaxBlock tokens in order, the speculative verify and the prefill):
 // k_dn_conv_block, k_dn_step_block and k_dn_gnorm_block run the same arithmetic token after
@@ -140,6 +142,103 @@ __global__ void __launch_bounds__(256) k_dn_step(DnStepArgs a) {
   }
   o = column_sum(o);
   if (t < CW) a.out[size_t(h) * D + c0 + j] = o;
+}
+
+// The gated delta rule and the gated RMSNorm of one value head in one workgroup of kDnRb * D
+// threads (thread (row block rb, column j): rows rb * D / kDnRb .. of column j; the column sums
+// meet in LDS over the row blocks in order), so that the norm, a reduction over the head's D
+// outputs, needs no second launch.  The same arithmetic as k_dn_step + k_dn_gnorm up to the
+// order of the float sums.
+constexpr int kDnRb = 8;
+template <int D>
+__global__ void __launch_bounds__(kDnRb * D) k_dn_step_head(DnStepArgs a) {
+  constexpr int NT = kDnRb * D, RPB = D / kDnRb, NWV = NT / 64;
+  static_assert(D % 64 == 0 && D % kDnRb == 0, "");
+  const uint32_t h = blockIdx.x, kh = h / (a.n_v_heads / a.n_k_heads);
+  const int t = threadIdx.x, j = t % D, rb = t / D, lane = t & 63, wave = t >> 6;
+  __shared__ float s_qn[D], s_kn[D];
+  __shared__ float s_part[kDnRb][D];
+  __shared__ float s_red[NWV];
+
+  // 1. loads: the thread's state rows, then the head's inputs (all before any use)
+  float* S = a.state + size_t(h) * D * D + j;
+  float sr[RPB];
+#pragma unroll
+  for (int r = 0; r < RPB; ++r) sr[r] = S[size_t(rb * RPB + r) * D];
+  constexpr int PL = D / 64;
+  float qv[PL], kv[PL];
+#pragma unroll
+  for (int m = 0; m < PL; ++m) {
+    qv[m] = a.q[size_t(kh) * D + lane + 64 * m];
+    kv[m] = a.k[size_t(kh) * D + lane + 64 * m];
+  }
+  const float vj = a.v[size_t(h) * D + j], zj = a.z[size_t(h) * D + j], wj = a.norm_w[j];
+  const bool keep = a.step && a.step->broken;  // (after the step's break: the state stays)
+  const float beta = 1.0f / (1.0f + expf(-a.b[h]));
+  const float decay = expf(-expf(a.A_log[h]) * softplus_f(a.a[h] + a.dt_bias[h]));
+
+  // 2. l2-normalised q (scaled by 1/sqrt(D)) and k, into LDS
+  float q2 = 0.0f, k2 = 0.0f;
+#pragma unroll
+  for (int m = 0; m < PL; ++m) {
+    q2 += qv[m] * qv[m];
+    k2 += kv[m] * kv[m];
+  }
+  q2 = wave_sum(q2);
+  k2 = wave_sum(k2);
+  const float qi = 1.0f / sqrtf(q2 + 1e-6f), ki = 1.0f / sqrtf(k2 + 1e-6f), scale = 1.0f / sqrtf(float(D));
+  if (wave == 0) {
+#pragma unroll
+    for (int m = 0; m < PL; ++m) {
+      s_qn[lane + 64 * m] = qv[m] * qi * scale;
+      s_kn[lane + 64 * m] = kv[m] * ki;
+    }
+  }
+  __syncthreads();
+
+  // the column sum of a per-thread partial over the row blocks, in order (every thread gets it)
+  auto column_sum = [&](float p) {
+    s_part[rb][j] = p;
+    __syncthreads();
+    float v = 0.0f;
+#pragma unroll
+    for (int b = 0; b < kDnRb; ++b) v += s_part[b][j];
+    __syncthreads();  // s_part is reused by the next sum
+    return v;
+  };
+
+  // 3. decayed state; kv_mem[j] = sum_i S[i][j] k[i]
+  float p = 0.0f;
+#pragma unroll
+  for (int r = 0; r < RPB; ++r) {
+    sr[r] *= decay;
+    p += sr[r] * s_kn[rb * RPB + r];
+  }
+  const float kvm = column_sum(p);
+  const float delta = (vj - kvm) * beta;
+
+  // 4. S += k delta^T, written back; o[j] = sum_i S[i][j] q[i]
+  float o = 0.0f;
+#pragma unroll
+  for (int r = 0; r < RPB; ++r) {
+    sr[r] += s_kn[rb * RPB + r] * delta;
+    if (!keep) S[size_t(rb * RPB + r) * D] = sr[r];
+    o += sr[r] * s_qn[rb * RPB + r];
+  }
+  o = column_sum(o);
+
+  // 5. the gated RMSNorm over the head's D outputs (row block 0's threads): w * (o * rr) * silu(z)
+  if (rb == 0) {
+    const float s2 = wave_sum(o * o);
+    if (lane == 0) s_red[wave] = s2;
+  }
+  __syncthreads();
+  if (rb != 0) return;
+  float tot = 0.0f;
+#pragma unroll
+  for (int w = 0; w < D / 64; ++w) tot += s_red[w];
+  const float rr = 1.0f / sqrtf(tot / float(D) + a.eps);
+  a.out[size_t(h) * D + j] = wj * (o * rr) * silu_f(zj);
 }
 
 // the gated RMSNorm of each value head's output (one workgroup of D threads per head):
@@ -325,6 +424,10 @@ void launch_dn_conv(const DnConvArgs& a, hipStream_t st) {
 
 void launch_dn_step(const DnStepArgs& a, uint32_t head_dim, hipStream_t st) {
   constexpr uint32_t CW = 16;
+  if (a.norm_w && head_dim == 128) {  // the gated form: a workgroup per head, the norm included
+    launch_kernel(&k_dn_step_head<128>, dim3(a.n_v_heads), dim3(kDnRb * 128), st, a);
+    return;
+  }
   if (head_dim == 128) {
     launch_kernel(&k_dn_step<128, CW>, dim3(a.n_v_heads, 128 / CW), dim3(256), st, a);
     if (a.norm_w) launch_kernel(&k_dn_gnorm<128>, dim3(a.n_v_heads), dim3(128), st, a);
