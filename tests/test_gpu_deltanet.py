@@ -36,8 +36,10 @@ def test_conv1d_update_matches_oracle():
 @pytest.mark.parametrize("hd,nv,nk", [(128, 32, 16), (64, 8, 8)])
 @pytest.mark.parametrize("gated", [False, True])
 def test_gated_delta_steps_match_oracle(hd, nv, nk, gated):
-    """Tolerance 2e-5 relative to the largest output: the column sums run over 16 row blocks
-    (GPU: a workgroup per head and 16-column block) against one sequential sum (oracle)."""
+    """Tolerance 2e-5 relative to the largest output: the GPU's column sums run over row blocks
+    (ungated: a workgroup per head and 16-column block, 16 row blocks; gated at head dim 128:
+    k_dn_step_head, a workgroup per head, 8 row blocks, the norm in the same workgroup) against
+    one sequential sum (oracle)."""
     rng = np.random.default_rng(hd + nv + int(gated))
     A_log = np.log(rng.uniform(0.1, 16, nv)).astype(np.float32)
     dt_bias = rng.standard_normal(nv).astype(np.float32)
