@@ -7,6 +7,7 @@ libchpe.so raises, it is never replaced by a fallback.
 """
 import ctypes
 import os
+import shutil
 from pathlib import Path
 
 import numpy as np
@@ -548,6 +549,14 @@ def ensure_archive(kind, seed=0, directory=None, threads=0):
     path = d / f"{ARCHIVE_NAMES[kind]}-s{seed}-{_generator_tag()}.chpe"
     if not path.exists() or path.stat().st_size != archive_size(kind):
         tmp = path.with_suffix(".tmp")
+        # the writer fills a memory-mapped file: on a file system without room for it the
+        # process would die of SIGBUS mid-write, so the room is checked first
+        d.mkdir(parents=True, exist_ok=True)
+        tmp.unlink(missing_ok=True)  # (a write that did not finish)
+        have = shutil.disk_usage(d).free
+        if have < archive_size(kind):
+            raise OSError(f"{d}: {have / 1e9:.1f} GB free, {ARCHIVE_NAMES[kind]} needs {archive_size(kind) / 1e9:.1f} GB "
+                          "(remove older archives there or set CHPE_ARCHIVE_DIR)")
         write_archive(tmp, kind, seed, threads)
         os.replace(tmp, path)
     return path

@@ -120,3 +120,16 @@ def test_9b_layout():
     r3 = 62080 + 3 * 13337
     q = ca.pack_records(ca.PACK_9B_W4, r3 + 1 + 1023, 2)
     assert q[0, PAYLOAD + 20] == 4 and not q[1].any()
+
+
+def test_archive_needs_room(tmp_path, monkeypatch):
+    # the writer fills a memory-mapped file: without room it would die of SIGBUS mid-write, so
+    # ensure_archive checks the free space first and writes nothing
+    class Usage:
+        free = ca.archive_size(ca.PACK_72B_W4) - 1
+
+    monkeypatch.setattr(ca.shutil, "disk_usage", lambda d: Usage)
+    (tmp_path / "stale.tmp").write_bytes(b"x")
+    with pytest.raises(OSError, match="GB free"):
+        ca.ensure_archive(ca.PACK_72B_W4, 0, directory=tmp_path)
+    assert [p.name for p in tmp_path.iterdir()] == ["stale.tmp"]
