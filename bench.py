@@ -7,6 +7,7 @@ seeded archive of libchpe_pack.so, 38.6 GB, resident in HBM), KV cache in fp16 i
 then `--steps` greedy decode steps timed (128 by default).  `--warmup` untimed steps run
 first, at positions 0..W-1 of the same prompt, before the context is built.  Other
 workloads: qwen72b-w2 (2-bit tiles), qwen3b-w4 (Qwen2.5-3B 4-bit cells, 4096-token prompt),
+qwen3b-fp16 (Qwen2.5-3B fp16 raw tiles, 32-token prompt: the reference's own CPU-runnable case),
 qwen9b-w4 (Qwen3.5-9B 4-bit flat tiles, the reference's GQA-aliased decode, 2048 tokens),
 qwen9b-hybrid (the same archive through the true hybrid layers: gated DeltaNet + gated attention).
 
@@ -55,6 +56,8 @@ WORKLOADS = {
                        desc="Qwen2.5-72B 2-bit GROUP128 flat tiles (dense 17408 B records)"),
     "qwen3b-w4": dict(kind=2, arch=0, prompt=4096, V=151936, L=36, H=16, KV=2, hd=128, D=2048, I=11008,
                       desc="Qwen2.5-3B 4-bit GROUP128 cells (dense 17408 B records)"),
+    "qwen3b-fp16": dict(kind=0, arch=0, prompt=32, V=151936, L=36, H=16, KV=2, hd=128, D=2048, I=11008,
+                        desc="Qwen2.5-3B fp16 raw tiles (the reference's own CPU-runnable case)"),
     "qwen9b-w4": dict(kind=7, arch=1, prompt=2048, V=248320, L=32, H=16, KV=4, hd=256, D=4096, I=12288,
                       desc="Qwen3.5-9B 4-bit GROUP128 flat tiles at the INT8 map's indices, "
                            "reference-compatible GQA decode"),
