@@ -618,7 +618,15 @@ __global__ void __launch_bounds__(64 * kMergeWaves) k_attn_merge(AttnArgs a0) {
   }
   s_o[wave][lane] = o;
   __syncthreads();
-  if (wave == 0) a.out[size_t(h) * HD + d] = ((s_o[0][lane] + s_o[1][lane]) + (s_o[2][lane] + s_o[3][lane])) / L;
+  if (wave == 0) {
+#pragma clang fp contract(off)
+    float v = ((s_o[0][lane] + s_o[1][lane]) + (s_o[2][lane] + s_o[3][lane])) / L;
+    if (a.gate) {  // the hybrid's output gate: the merged value times sigmoid(g)
+      const float g = a.gate[size_t(blockIdx.z) * 2 * a.H * HD + size_t(h) * 2 * HD + HD + d];
+      v = v * (1.0f / (1.0f + expf(-g)));
+    }
+    a.out[size_t(h) * HD + d] = v;
+  }
 }
 
 }  // namespace

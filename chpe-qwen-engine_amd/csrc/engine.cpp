@@ -1367,8 +1367,8 @@ void Engine::record_block_hybrid(uint32_t mm, hipStream_t st) {
       at.part_ml = d_bpml_;
       at.part_acc = d_bpacc_;
       at.nq = mm;
+      at.gate = d_bhx0_;  // (the output gate applied by the merge)
       launch_attention(at, st);
-      launch_hyb_gate(d_battn_, d_bhx0_, H, hd, mm, st);
     } else {
       if (!Hy.has_ab) {
         const ProjPlan* inb[1] = {&Hy.in3};
@@ -1695,10 +1695,10 @@ void Engine::record_step_hybrid(hipStream_t st) {
       q.rope_rows = uint32_t(cfg_.max_seq_len);
       q.eps = arch_.rms_eps;
       launch_hyb_qk(q, st);
-      const AttnArgs aa = attn_args(l);
+      AttnArgs aa = attn_args(l);
+      aa.gate = d_hx0_;  // (the output gate applied by the merge)
       launch_attention_partial(aa, st);
       launch_attention_combine(aa, st);
-      launch_hyb_gate(d_attn_, d_hx0_, q.H, q.hd, 1, st);
       const ProjPlan* o[1] = {&H.out};
       enqueue_gemv(o, hid, 1, GemvMode::Accum, d_attn_, uint32_t(q.H * q.hd), nullptr, st);
     } else {

@@ -5,8 +5,9 @@
 // query then the output gate (:672-675); RMSNorm of each query and key head (:677-678, the
 // gains as stored: the engine's norm tiles hold the effective gain); the rotary embedding of
 // the first rot dims, rotate_half pairs (i, i + rot/2) (:546-591), angles from the engine's
-// tables (the reference's applyRope formula over rot dims, chpe_engine.zig:195-216); the
-// attention output times sigmoid(gate) (:696).
+// tables (the reference's applyRope formula over rot dims, chpe_engine.zig:195-216).  The
+// attention output times sigmoid(gate) (:696) is applied by the attention merge
+// (AttnArgs::gate).
 #include "device_common.hpp"
 #include "kernels.hpp"
 
@@ -69,25 +70,11 @@ __global__ void __launch_bounds__(HD) k_hyb_qk(HybQkArgs a) {
   }
 }
 
-// m tokens: attn [m][H hd], qg [m][2 H hd]
-__global__ void __launch_bounds__(256) k_hyb_gate(float* attn, const float* qg, uint32_t H, uint32_t hd, uint32_t m) {
-#pragma clang fp contract(off)
-  const uint32_t i = blockIdx.x * 256 + threadIdx.x;
-  if (i >= m * H * hd) return;
-  const uint32_t tk = i / (H * hd), e = i % (H * hd), h = e / hd, d = e % hd;
-  const float g = qg[size_t(tk) * 2 * H * hd + size_t(h) * 2 * hd + hd + d];
-  attn[i] = attn[i] * (1.0f / (1.0f + expf(-g)));
-}
-
 }  // namespace
 
 void launch_hyb_qk(const HybQkArgs& a, hipStream_t st) {
   if (a.hd != 256) return;  // (the 9B head dim; the engine checks the shape at init)
   launch_kernel(&k_hyb_qk<256>, dim3(a.H + 2 * a.KV, a.m ? a.m : 1), dim3(256), st, a);
-}
-
-void launch_hyb_gate(float* attn, const float* qg, uint32_t H, uint32_t hd, uint32_t m, hipStream_t st) {
-  launch_kernel(&k_hyb_gate, dim3((m * H * hd + 255) / 256), dim3(256), st, attn, qg, H, hd, m);
 }
 
 }  // namespace chpe

@@ -196,6 +196,8 @@ struct AttnArgs {
   float scale;              // 1/sqrt(hd)
   uint32_t nq;              // queries of a block step at positions pos .. pos + nq - 1 (rows of q,
                             // out and the partials follow each other); 0 or 1: one query
+  const float* gate;        // or null: the merge writes out * sigmoid(g), g the hybrid's output gate
+                            //   (query z, head h: gate[z][h][hd + d] of rows [H][2 hd] per query)
 };
 
 struct FinishArgs {
@@ -431,8 +433,6 @@ struct HybQkArgs {
   const uint32_t* brk;
 };
 void launch_hyb_qk(const HybQkArgs& a, hipStream_t stream);
-// attn[t][h][d] *= sigmoid(qg[t][h][hd + d]) for m tokens of H heads of hd
-void launch_hyb_gate(float* attn, const float* qg, uint32_t H, uint32_t hd, uint32_t m, hipStream_t stream);
 bool deltanet_supported(uint32_t n_v_heads, uint32_t n_k_heads, uint32_t head_dim, uint32_t taps);
 void launch_dn_conv(const DnConvArgs& a, hipStream_t stream);
 void launch_dn_step(const DnStepArgs& a, uint32_t head_dim, hipStream_t stream);
