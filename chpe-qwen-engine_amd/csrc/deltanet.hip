@@ -19,6 +19,8 @@
 // k_dn_conv_block, k_dn_step_block and k_dn_gnorm_block run the same arithmetic token after
 // token inside one launch, each state read once and written once for the m tokens (the conv
 // state in registers per channel, a head's state slab in registers per workgroup).
+#include <cstdio>
+
 #include "device_common.hpp"
 #include "kernels.hpp"
 
@@ -260,10 +262,11 @@ __global__ void __launch_bounds__(D) k_dn_gnorm(DnStepArgs a) {
 }
 
 // ---- the block step: m tokens in order, each state read and written once ----------------------
+// (the conv's taps fixed at compile time: the token loop unrolls, the inputs stay in registers)
 __global__ void __launch_bounds__(256) k_dn_conv_block(DnBlockArgs a) {
   const uint32_t c = blockIdx.x * 256 + threadIdx.x;
   if (c >= a.channels) return;
-  const uint32_t T = a.taps;
+  constexpr uint32_t T = kDnConvTaps;
   const float* w = a.w + size_t(c) * T;
   float* st = a.conv_state + size_t(c) * (T - 1);
   float wv[kDnMaxTaps], sv[kDnMaxTaps];
@@ -273,15 +276,26 @@ __global__ void __launch_bounds__(256) k_dn_conv_block(DnBlockArgs a) {
     sv[k] = k + 1 < T ? st[k] : 0.0f;
   }
   const float wl = w[T - 1];
-  for (uint32_t t = 0; t < a.m; ++t) {
-    const float x = a.x[size_t(t) * a.x_stride + c];
+  // every token's input and break flag requested before the first is used (the tokens' chain
+  // through the state is short; their loads are not)
+  float xs[kMaxBlock];
+  uint32_t bm = 0;
+#pragma unroll
+  for (uint32_t t = 0; t < kMaxBlock; ++t) {
+    xs[t] = t < a.m ? a.x[size_t(t) * a.x_stride + c] : 0.0f;
+    bm |= (t < a.m && a.brk[t] != 0u ? 1u : 0u) << t;
+  }
+#pragma unroll
+  for (uint32_t t = 0; t < kMaxBlock; ++t) {
+    if (t >= a.m) break;
+    const float x = xs[t];
     float acc = 0.0f;  // oldest tap first, the new input last (k_dn_conv)
 #pragma unroll
     for (uint32_t k = 0; k < kDnMaxTaps; ++k)
       if (k + 1 < T) acc += wv[k] * sv[k];
     acc += wl * x;
     a.conv_out[size_t(t) * a.channels + c] = silu_f(acc);
-    if (a.brk[t]) continue;  // (token t broke before this layer: its shift is skipped)
+    if ((bm >> t) & 1u) continue;  // (token t broke before this layer: its shift is skipped)
 #pragma unroll
     for (uint32_t k = 0; k + 1 < kDnMaxTaps; ++k)
       if (k + 2 < T) sv[k] = sv[k + 1];
@@ -324,6 +338,9 @@ __global__ void __launch_bounds__(256) k_dn_step_block(DnBlockArgs a) {
     __syncthreads();
     return v;
   };
+  uint32_t bm = 0;  // the tokens' break flags, read once (not one dependent load per token)
+#pragma unroll
+  for (uint32_t u = 0; u < kMaxBlock; ++u) bm |= (u < a.m && a.brk[u] != 0u ? 1u : 0u) << u;
 
   for (uint32_t tk = 0; tk < a.m; ++tk) {
     const float* xc = a.conv_out + size_t(tk) * a.channels;
@@ -355,7 +372,7 @@ __global__ void __launch_bounds__(256) k_dn_step_block(DnBlockArgs a) {
       }
     }
     __syncthreads();
-    if (a.brk[tk]) {  // (uniform: the token's slab update is skipped, its output is not used)
+    if ((bm >> tk) & 1u) {  // (uniform: the token's slab update is skipped, its output is not used)
       if (t < CW) a.out[size_t(tk) * a.out_stride + size_t(h) * D + c0 + j] = 0.0f;
       continue;
     }
@@ -403,6 +420,10 @@ __global__ void __launch_bounds__(D) k_dn_gnorm_block(DnBlockArgs a) {
 
 void launch_dn_block(const DnBlockArgs& a, hipStream_t st) {
   constexpr uint32_t CW = 16;
+  if (a.taps != kDnConvTaps) {  // (the engine plans the 9B layers: 4 taps)
+    std::fprintf(stderr, "chpe: the block step's conv is built for %u taps\n", kDnConvTaps);
+    return;
+  }
   launch_kernel(&k_dn_conv_block, dim3((a.channels + 255) / 256), dim3(256), st, a);
   if (a.head_dim == 128) {
     launch_kernel(&k_dn_step_block<128, CW>, dim3(a.n_v_heads, 128 / CW), dim3(256), st, a);
