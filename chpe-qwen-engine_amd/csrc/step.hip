@@ -68,14 +68,27 @@ __device__ bool unpack_embed_row_cell_fast(const Image& im, uint64_t cell, uint3
   return true;
 }
 
+// gi, gn: this thread's index and the thread count of the launch.  The per-tile scale form (the
+// 72B and 9B embeddings) is split over all of them; the other forms, whose outliers are stored
+// after the row under a workgroup barrier, run in the lead workgroup alone.
 __device__ bool unpack_embed_row_cell(const Image& im, uint64_t cell, uint32_t row, uint32_t D,
-                                      float* out) {
-  bool handled = false;
-  const bool ok = unpack_embed_row_cell_fast(im, cell, row, D, out, &handled);
-  if (handled) return ok;
+                                      float* out, uint32_t gi, uint32_t gn, bool lead) {
   const uint64_t codes = cell + 64, pl = cell + 16448;
   const uint8_t qb = im.u8(pl + 20);
   const bool g128 = (im.u64(pl + 24) & 1u) != 0;
+  if (qb != 8 && qb != 2 && !g128 && qb != 4) {  // (nibble - 8) * scale + bias (:1384-1394)
+    const float scale = im.f32(pl + 32), bias = im.f32(pl + 36);
+    for (uint32_t i = gi; i < (D / 2) * 2; i += gn) {
+      const uint32_t b = im.u8(codes + uint64_t(row) * (D / 2) + i / 2);
+      const float q = float((b >> (4 * (i & 1))) & 15u);
+      out[i] = __fadd_rn(__fmul_rn(q - 8.0f, scale), bias);
+    }
+    return true;
+  }
+  if (!lead) return true;
+  bool handled = false;
+  const bool ok = unpack_embed_row_cell_fast(im, cell, row, D, out, &handled);
+  if (handled) return ok;
   const uint32_t ng = D / 128;
   const int tid = threadIdx.x, nt = blockDim.x;
   if (qb == 8) {
@@ -100,14 +113,6 @@ __device__ bool unpack_embed_row_cell(const Image& im, uint64_t cell, uint32_t r
       const uint32_t b = im.u8(codes + uint64_t(row) * (D / 2) + i / 2);
       out[i] = (float((b >> (4 * (i & 1))) & 15u) - 8.0f) * s;
     }
-  } else {
-    const float scale = im.f32(pl + 32), bias = im.f32(pl + 36);
-    for (uint32_t i = tid; i < (D / 2) * 2; i += nt) {
-      const uint32_t b = im.u8(codes + uint64_t(row) * (D / 2) + i / 2);
-      const float q = float((b >> (4 * (i & 1))) & 15u);
-      out[i] = __fadd_rn(__fmul_rn(q - 8.0f, scale), bias);
-    }
-    return true;
   }
   if (g128) {  // outliers replace, in entry order (the last entry for a column wins)
     __syncthreads();
@@ -130,10 +135,11 @@ __device__ void stage_rope_row(const EmbedArgs& a, uint32_t pos) {
                                       : a.rope_sin[size_t(pos) * a.rope_half + (i - a.rope_half)];
 }
 
-__device__ void embed_token(const EmbedArgs& a, uint32_t tok) {
+// gi, gn, lead: as unpack_embed_row_cell (one workgroup: threadIdx.x, blockDim.x, true)
+__device__ void embed_token(const EmbedArgs& a, uint32_t tok, uint32_t gi, uint32_t gn, bool lead) {
   const uint32_t D = a.D;
   const Image im{a.image, a.image_len};
-  const int tid = threadIdx.x, nt = blockDim.x;
+  const uint32_t tid = gi, nt = gn;
   bool done = false;
   if (a.kind == 1 || a.kind == 2 || a.kind == 3) {
     const uint32_t rpt = (a.kind == 3 ? 16384u : 8192u) / D;
@@ -153,7 +159,7 @@ __device__ void embed_token(const EmbedArgs& a, uint32_t tok) {
   } else if (a.kind == 4) {
     const uint32_t tile = tok / 16, row = tok % 16;
     if (tile < a.record_count) {
-      unpack_embed_row_cell(im, 4096 + uint64_t(tile) * a.stride + a.cell_off, row, D, a.hidden);
+      unpack_embed_row_cell(im, 4096 + uint64_t(tile) * a.stride + a.cell_off, row, D, a.hidden, gi, gn, lead);
       done = true;  // an out-of-range row keeps the previous hidden state, as on the CPU
     }
   }
@@ -161,9 +167,11 @@ __device__ void embed_token(const EmbedArgs& a, uint32_t tok) {
     for (uint32_t i = tid; i < D; i += nt) a.hidden[i] = 0.05f * float(int((i + tok) % 17u) - 8);
 }
 
+// the step's input row over D / 256 workgroups (the 72B and 9B rows are decoded
+// byte by byte); workgroup 0 also stages the RoPE row
 __global__ void __launch_bounds__(256) k_embed(EmbedArgs a) {
-  stage_rope_row(a, a.state->pos);
-  embed_token(a, a.state->token);
+  if (blockIdx.x == 0) stage_rope_row(a, a.state->pos);
+  embed_token(a, a.state->token, blockIdx.x * blockDim.x + threadIdx.x, gridDim.x * blockDim.x, blockIdx.x == 0);
 }
 
 // the block step's inputs: token blockIdx.x's embedding row into X[blockIdx.x]
@@ -174,7 +182,7 @@ __global__ void __launch_bounds__(256) k_block_embed(EmbedArgs a, const uint32_t
   if (threadIdx.x == 0) brk[blockIdx.x] = 0u;
   float* row = X + size_t(blockIdx.x) * a.D;
   e.hidden = row;
-  embed_token(e, tokens[blockIdx.x]);
+  embed_token(e, tokens[blockIdx.x], threadIdx.x, blockDim.x, true);
   __syncthreads();  // the workgroup's row writes are visible to it
   float ss = 0.0f;
   for (uint32_t c = threadIdx.x; c < a.D; c += blockDim.x) ss = fmaf(row[c], row[c], ss);
@@ -246,7 +254,7 @@ __global__ void __launch_bounds__(256) k_finish(FinishArgs a) {
   // the next step's input: the embedding row of the next token (one launch less per step)
   if (a.embed_next) {
     __syncthreads();
-    embed_token(a.embed, s_next);
+    embed_token(a.embed, s_next, threadIdx.x, blockDim.x, true);
   }
 }
 
@@ -281,7 +289,7 @@ __global__ void k_flat_tile_weights(const uint8_t* cell, float* out) {
 __global__ void k_embed_row_cell(const uint8_t* cell, uint64_t len, uint32_t row, uint32_t D,
                                  float* out, int* written) {
   const Image im{cell, len};
-  const bool w = unpack_embed_row_cell(im, 0, row, D, out);
+  const bool w = unpack_embed_row_cell(im, 0, row, D, out, threadIdx.x, blockDim.x, true);
   if (threadIdx.x == 0) *written = w ? 1 : 0;
 }
 
@@ -312,7 +320,7 @@ void record_kernel_names(bool on) {
 const char* last_kernel_name() { return detail::g_last_kernel ? detail::g_last_kernel : ""; }
 
 void launch_embed(const EmbedArgs& a, hipStream_t st) {
-  launch_kernel(k_embed, dim3(1), dim3(256), st, a);
+  launch_kernel(k_embed, dim3(a.D > 256 ? (a.D + 255) / 256 : 1), dim3(256), st, a);
 }
 
 void launch_block_embed(const EmbedArgs& e, const uint32_t* tokens, uint32_t m, float* X, float* ssp, uint32_t* brk,
